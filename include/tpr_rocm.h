@@ -1,0 +1,142 @@
+/*
+ * tpr_rocm.h -- C-ABI launch layer of the MI355X (gfx950) reduction + top-k
+ * backend.  Plain pointers, sizes and int status codes; no C++ or torch types;
+ * no exceptions cross this boundary.  Every call is asynchronous on the given
+ * HIP stream (passed as void*, NULL = the default stream) and never allocates
+ * user-visible memory: outputs and the workspace are owned by the caller.
+ *
+ * It replaces the CUDA backend's reduction registrations in TensorPlay
+ * (/root/reference/p10/src/backend/cuda/ReductionKernels.cu:385-418), which are
+ * reached through the P10 dispatcher
+ * (/root/reference/p10/include/Dispatcher.h:46-59, DispatchStub::call).
+ * The host adapters in tensorplay_amd/csrc/core/ROCmReductionKernels.cpp
+ * register under DispatchKey::ROCm with the dispatcher's exact argument types
+ * (tools/codegen/gen.py:38-53, STUB_TYPE_MAP) and call into this layer.
+ */
+#ifndef TPR_ROCM_H
+#define TPR_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TPR_MAX_DIMS 8
+
+/* Status codes.  tpr_last_error() holds a message for the calling thread. */
+enum tpr_status {
+    TPR_OK = 0,
+    TPR_ERR_INVALID_ARG = 1,       /* bad shape, dim, k, pointer, descriptor   */
+    TPR_ERR_UNSUPPORTED_DTYPE = 2, /* dtype not implemented on this backend    */
+    TPR_ERR_HIP = 3,               /* a HIP runtime call or launch failed      */
+    TPR_ERR_WORKSPACE = 4,         /* workspace smaller than *_workspace_bytes */
+    TPR_ERR_NOT_IMPLEMENTED = 5
+};
+
+/* Element types.  Numbering follows P10's ScalarType
+ * (/root/reference/p10/include/DType.h:63-79) so adapters pass it through. */
+enum tpr_dtype {
+    TPR_UINT8 = 0, TPR_INT8 = 1, TPR_INT16 = 2, TPR_INT32 = 3, TPR_INT64 = 4,
+    TPR_UINT16 = 5, TPR_UINT32 = 6, TPR_UINT64 = 7,
+    TPR_FLOAT32 = 8, TPR_FLOAT64 = 9, TPR_BOOL = 10
+};
+
+/* Reduction operators.  Each maps to the reference kernels named beside it
+ * (/root/reference/p10/src/backend/cpu/ReductionKernels.cpp). */
+enum tpr_reduce_op {
+    TPR_SUM = 0,    /* sum_kernel :72-106, sum_dim_kernel :108-189            */
+    TPR_MEAN = 1,   /* mean_kernel :191-196, mean_dim_kernel :198-211         */
+    TPR_AMAX = 2,   /* max_kernel :231-254, max_dim_kernel :256-315            */
+    TPR_AMIN = 3,   /* min_kernel :317-340, min_dim_kernel :342-401            */
+    TPR_ARGMAX = 4, /* argmax_kernel :682-746                                  */
+    TPR_ARGMIN = 5, /* argmin_kernel :748-812                                  */
+    TPR_VAR = 6,    /* var_kernel :817-827, var_dim_kernel :829-847            */
+    TPR_STD = 7     /* std_kernel :849-851, std_dim_kernel :853-855            */
+};
+
+/* One reduction over an arbitrary strided view.
+ *  - sizes/strides are in elements; strides may be any value (including 0).
+ *  - reduce_mask bit d set => dim d is reduced.  reduce_mask == all dims (or
+ *    ndim == 0) is a full reduction to one value.
+ *  - The output is written densely (row-major over the kept dims, in their
+ *    original order); keepdim only changes the shape the caller reports.
+ *  - out_dtype: SUM/MEAN: FLOAT32 or FLOAT64.  AMAX/AMIN: the input dtype.
+ *    ARGMAX/ARGMIN: INT64 (index along the reduced dims, row-major; first
+ *    index wins ties; NaN never wins, as the reference's strict compare).
+ *    VAR/STD: FLOAT32.
+ *  - count_override > 0 replaces the element count used by MEAN/VAR/STD (the
+ *    reference multiplies the size of every listed dim, duplicates included,
+ *    ReductionKernels.cpp:203-208 and :840-845); 0 = product of reduced sizes.
+ *  - correction: VAR/STD divisor is max(0, count - correction).
+ * An empty reduced extent writes: SUM 0, MEAN NaN, AMAX -inf, AMIN +inf,
+ * ARGMAX/ARGMIN 0, VAR/STD NaN (the reference's full max/min raise instead;
+ * the adapters check that before calling). */
+typedef struct tpr_reduce_desc {
+    int32_t op;          /* enum tpr_reduce_op */
+    int32_t in_dtype;    /* enum tpr_dtype     */
+    int32_t out_dtype;   /* enum tpr_dtype     */
+    int32_t ndim;        /* 0..TPR_MAX_DIMS    */
+    int64_t sizes[TPR_MAX_DIMS];
+    int64_t strides[TPR_MAX_DIMS];
+    uint32_t reduce_mask;
+    int32_t reserved0;
+    int64_t correction;
+    int64_t count_override;
+} tpr_reduce_desc;
+
+/* Bytes of device workspace tpr_reduce needs for this descriptor (0 is
+ * common).  Deterministic in the descriptor. */
+size_t tpr_reduce_workspace_bytes(const tpr_reduce_desc* desc);
+
+/* Launch the reduction.  `in` points at element [0,...,0] of the view.
+ * Replaces: DispatchStub<...>::call("sum" | "sum.dim_IntList" | "mean" |
+ * "mean.dim" | "max" | "max.dim" | "min" | "min.dim" | "argmax" | "argmin" |
+ * "var" | "var.dim" | "std" | "std.dim", DispatchKey::CUDA, ...)
+ * (/root/reference/p10/src/backend/cuda/ReductionKernels.cu:385-418). */
+int tpr_reduce(const tpr_reduce_desc* desc, const void* in, void* out,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* Top-k along the last dim of a [rows, cols] view whose rows start
+ * row_stride elements apart (elements within a row are contiguous).
+ * Outputs are dense [rows, k]: values in the input dtype, indices int64.
+ * Order: value descending for largest=1 (ascending for largest=0), equal
+ * values by lowest index; -0.0 == +0.0; NaN ranks above every number.
+ * sorted=0 is accepted and returns the same (sorted) order.
+ * k must satisfy 0 <= k <= cols.  No reference counterpart: TensorPlay has no
+ * topk; this adds the schema row
+ *   topk(Tensor self, int64_t k, int64_t dim=-1, bool largest=true,
+ *        bool sorted=true) -> (Tensor values, Tensor indices)
+ * next to the reduction rows of config/native_functions.yaml:695-809. */
+size_t tpr_topk_workspace_bytes(int32_t dtype, int64_t rows, int64_t cols, int64_t k);
+int tpr_topk(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t row_stride,
+             int64_t k, int32_t largest, int32_t sorted, void* out_values, void* out_indices,
+             void* workspace, size_t workspace_bytes, void* stream);
+
+/* Strided -> dense copy (row-major over sizes).  Counterpart of the CUDA
+ * backend's copy_cast_kernel_impl / copy_kernel
+ * (/root/reference/p10/src/backend/cuda/CopyKernels.cu:42-157) for the layout
+ * normalisation the reduction path needs (Tensor::contiguous, topk on a
+ * non-last dim).  elem_size in {1,2,4,8}. */
+int tpr_copy_strided(const void* in, int32_t elem_size, int32_t ndim, const int64_t* sizes,
+                     const int64_t* in_strides, void* out, void* stream);
+
+/* Thread-local message for the last non-OK status on this thread. */
+const char* tpr_last_error(void);
+
+/* ABI version (major << 16 | minor). */
+int32_t tpr_abi_version(void);
+
+/* Tuning / test hook: force plan choices.  Keys: "splits" (row/full/column
+ * split count, 0 = automatic), "lanes" (threads per row in the row kernel,
+ * 0 = automatic), "general" (1 = always use the generic strided kernel),
+ * "topk_fallback" (1 = always take top-k's exact multi-pass path).
+ * Process-wide; not synchronised with concurrent launches.  Returns
+ * TPR_ERR_INVALID_ARG for an unknown key.  No reference counterpart. */
+int tpr_debug_set(const char* key, int64_t value);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TPR_ROCM_H */

@@ -1,0 +1,63 @@
+/*
+ * TEST INFRASTRUCTURE ONLY.  CPU restatement of TensorPlay's P10 CPU reduction
+ * path (p10/src/backend/cpu/ReductionKernels.cpp) plus this build's topk
+ * definition.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load this library, and only as the checker / the timed CPU baseline.
+ * The product path (libtpr_rocm.so, tensorplay_amd._C) never links it.
+ *
+ * All tensors are float32; shapes/strides are in elements (int64).
+ */
+#ifndef TP_CPU_REDUCE_H
+#define TP_CPU_REDUCE_H
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* a1: sum_kernel (ReductionKernels.cpp:72-106): double accumulation in memory
+ * order of the contiguous copy, then one rounding to float. */
+float or_sum_all(const float* x, int ndim, const int64_t* sizes, const int64_t* strides);
+/* a2: sum_dim_kernel (ReductionKernels.cpp:108-189): fp32 accumulation in the
+ * output buffer, visiting input elements in row-major logical order.
+ * reduce_mask bit d set = dim d reduced.  out is contiguous over kept dims. */
+void or_sum_dim(const float* x, int ndim, const int64_t* sizes, const int64_t* strides,
+                uint32_t reduce_mask, float* out);
+/* a3: mean_kernel / mean_dim_kernel (ReductionKernels.cpp:191-211) followed by
+ * div_scalar_kernel (ArithmeticKernels.cpp:1502-1532). */
+float or_mean_all(const float* x, int ndim, const int64_t* sizes, const int64_t* strides);
+void or_mean_dim(const float* x, int ndim, const int64_t* sizes, const int64_t* strides,
+                 uint32_t reduce_mask, const int64_t* dims_list, int n_dims_list, float* out);
+/* a4: max_kernel/min_kernel (:231-254, :317-340); max_dim/min_dim (:256-315, :342-401).
+ * is_max = 1 for max.  Returns 0 on success, -1 for an empty full reduction. */
+int or_minmax_all(const float* x, int ndim, const int64_t* sizes, const int64_t* strides,
+                  int is_max, float* out);
+void or_minmax_dim(const float* x, int ndim, const int64_t* sizes, const int64_t* strides,
+                   uint32_t reduce_mask, int is_max, float* out);
+/* a5: argmax_kernel/argmin_kernel (:682-812).  dim < 0 after wrapping means flat.
+ * quirk = 1 reproduces the CPU path's transpose(d,-1) row layout (:714-735);
+ * quirk = 0 gives the permute (CUDA path, ReductionKernels.cu:67-75) layout. */
+int64_t or_argminmax_all(const float* x, int ndim, const int64_t* sizes, const int64_t* strides,
+                         int is_max);
+void or_argminmax_dim(const float* x, int ndim, const int64_t* sizes, const int64_t* strides,
+                      int dim, int is_max, int quirk, int64_t* out);
+/* a6: var_kernel/var_dim_kernel/std_* (:817-855). */
+float or_var_all(const float* x, int ndim, const int64_t* sizes, const int64_t* strides,
+                 int64_t correction, int take_sqrt);
+void or_var_dim(const float* x, int ndim, const int64_t* sizes, const int64_t* strides,
+                uint32_t reduce_mask, const int64_t* dims_list, int n_dims_list,
+                int64_t correction, int take_sqrt, float* out);
+/* a11: topk (absent from the reference; this build's definition).  Rows of a
+ * [rows, cols] view with row_stride.  Order: key descending, index ascending,
+ * where key canonicalises -0.0 to +0.0 and treats NaN as the largest value.
+ * largest = 0 reverses the key order (NaN then the smallest).  Values are the
+ * input elements at the selected indices (original bits). */
+void or_topk(const float* x, int64_t rows, int64_t cols, int64_t row_stride, int64_t k,
+             int largest, float* out_vals, int64_t* out_idx);
+/* Same selection, rows split over n_threads pthreads (CPU baseline at all cores). */
+void or_topk_mt(const float* x, int64_t rows, int64_t cols, int64_t row_stride, int64_t k,
+                int largest, float* out_vals, int64_t* out_idx, int n_threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,173 @@
+"""ctypes binding of the C-ABI launch layer (include/tpr_rocm.h).
+
+This is the same stub a TensorPlay maintainer would add on the reference side
+to reach the backend from Python; the C++ host core (tensorplay_amd._C) calls
+the same entry points directly.  Device memory and streams come from PyTorch
+(plumbing only): tensors are passed as raw device pointers + element strides.
+
+The library must have been built (python -m tensorplay_amd.build); loading
+fails loudly otherwise -- there is no CPU fallback.
+"""
+import ctypes
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libtpr_rocm.so")
+
+MAX_DIMS = 8
+
+# enum tpr_status
+OK, ERR_INVALID_ARG, ERR_UNSUPPORTED_DTYPE, ERR_HIP, ERR_WORKSPACE, ERR_NOT_IMPLEMENTED = range(6)
+# enum tpr_dtype (P10 ScalarType numbering)
+UINT8, INT8, INT16, INT32, INT64, UINT16, UINT32, UINT64, FLOAT32, FLOAT64, BOOL = range(11)
+# enum tpr_reduce_op
+SUM, MEAN, AMAX, AMIN, ARGMAX, ARGMIN, VAR, STD = range(8)
+OP_NAMES = {"sum": SUM, "mean": MEAN, "amax": AMAX, "amin": AMIN, "argmax": ARGMAX,
+            "argmin": ARGMIN, "var": VAR, "std": STD}
+
+EXPORTED = ["tpr_reduce_workspace_bytes", "tpr_reduce", "tpr_topk_workspace_bytes", "tpr_topk",
+            "tpr_copy_strided", "tpr_last_error", "tpr_abi_version", "tpr_debug_set"]
+
+
+class TprError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__(f"tpr status {status}: {msg}")
+        self.status = status
+
+
+class ReduceDesc(ctypes.Structure):
+    _fields_ = [
+        ("op", ctypes.c_int32),
+        ("in_dtype", ctypes.c_int32),
+        ("out_dtype", ctypes.c_int32),
+        ("ndim", ctypes.c_int32),
+        ("sizes", ctypes.c_int64 * MAX_DIMS),
+        ("strides", ctypes.c_int64 * MAX_DIMS),
+        ("reduce_mask", ctypes.c_uint32),
+        ("reserved0", ctypes.c_int32),
+        ("correction", ctypes.c_int64),
+        ("count_override", ctypes.c_int64),
+    ]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built; run `python -m tensorplay_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, sz, i32, i64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_int64
+        dp = ctypes.POINTER(ReduceDesc)
+        i64p = ctypes.POINTER(ctypes.c_int64)
+        L.tpr_reduce_workspace_bytes.argtypes = [dp]
+        L.tpr_reduce_workspace_bytes.restype = sz
+        L.tpr_reduce.argtypes = [dp, vp, vp, vp, sz, vp]
+        L.tpr_reduce.restype = ctypes.c_int
+        L.tpr_topk_workspace_bytes.argtypes = [i32, i64, i64, i64]
+        L.tpr_topk_workspace_bytes.restype = sz
+        L.tpr_topk.argtypes = [vp, i32, i64, i64, i64, i64, i32, i32, vp, vp, vp, sz, vp]
+        L.tpr_topk.restype = ctypes.c_int
+        L.tpr_copy_strided.argtypes = [vp, i32, i32, i64p, i64p, vp, vp]
+        L.tpr_copy_strided.restype = ctypes.c_int
+        L.tpr_last_error.argtypes = []
+        L.tpr_last_error.restype = ctypes.c_char_p
+        L.tpr_abi_version.argtypes = []
+        L.tpr_abi_version.restype = i32
+        L.tpr_debug_set.argtypes = [ctypes.c_char_p, i64]
+        L.tpr_debug_set.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _check(rc):
+    if rc != OK:
+        raise TprError(rc, lib().tpr_last_error().decode())
+
+
+def debug_set(key, value):
+    _check(lib().tpr_debug_set(key.encode(), int(value)))
+
+
+def make_desc(op, shape, strides, reduce_dims, out_dtype, correction=1, count_override=0,
+              in_dtype=FLOAT32):
+    d = ReduceDesc()
+    d.op = OP_NAMES[op] if isinstance(op, str) else op
+    d.in_dtype = in_dtype
+    d.out_dtype = out_dtype
+    d.ndim = len(shape)
+    if d.ndim > MAX_DIMS:
+        raise ValueError("at most 8 dims")
+    for i, (n, s) in enumerate(zip(shape, strides)):
+        d.sizes[i] = n
+        d.strides[i] = s
+    m = 0
+    for r in reduce_dims:
+        m |= 1 << r
+    d.reduce_mask = m
+    d.correction = correction
+    d.count_override = count_override
+    return d
+
+
+def _stream(torch, device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def default_out_dtype(op):
+    op = OP_NAMES[op] if isinstance(op, str) else op
+    return INT64 if op in (ARGMAX, ARGMIN) else FLOAT32
+
+
+def reduce(x, op, dims=None, correction=1, out_dtype=None, count_override=0):
+    """Reduce a float32 CUDA(ROCm) torch tensor over `dims` (None = all).
+
+    Returns a dense torch tensor of the kept dims' shape (keepdim=False)."""
+    import torch
+    nd = x.dim()
+    if dims is None:
+        rd = list(range(nd))
+    else:
+        rd = sorted(set((d + nd) if d < 0 else d for d in dims))
+    kept = [x.shape[i] for i in range(nd) if i not in rd]
+    od = default_out_dtype(op) if out_dtype is None else out_dtype
+    tdt = {FLOAT32: torch.float32, FLOAT64: torch.float64, INT64: torch.int64}[od]
+    out = torch.empty(kept, dtype=tdt, device=x.device)
+    desc = make_desc(op, list(x.shape), list(x.stride()), rd, od, correction, count_override)
+    L = lib()
+    wsb = L.tpr_reduce_workspace_bytes(ctypes.byref(desc))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
+    _check(L.tpr_reduce(ctypes.byref(desc), ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                        ctypes.c_void_p(ws.data_ptr()), wsb, _stream(torch, x.device)))
+    return out
+
+
+def topk(x2d, k, largest=True, sorted=True):
+    """Top-k along the last dim of a 2-D float32 device tensor (unit inner stride)."""
+    import torch
+    assert x2d.dim() == 2 and (x2d.stride(1) == 1 or x2d.shape[1] <= 1)
+    rows, cols = x2d.shape
+    vals = torch.empty((rows, k), dtype=torch.float32, device=x2d.device)
+    idx = torch.empty((rows, k), dtype=torch.int64, device=x2d.device)
+    L = lib()
+    wsb = L.tpr_topk_workspace_bytes(FLOAT32, rows, cols, k)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x2d.device)
+    _check(L.tpr_topk(ctypes.c_void_p(x2d.data_ptr()), FLOAT32, rows, cols, x2d.stride(0), k,
+                      int(largest), int(sorted), ctypes.c_void_p(vals.data_ptr()),
+                      ctypes.c_void_p(idx.data_ptr()), ctypes.c_void_p(ws.data_ptr()), wsb,
+                      _stream(torch, x2d.device)))
+    return vals, idx
+
+
+def copy_strided(x):
+    """Dense copy of any strided device tensor through tpr_copy_strided."""
+    import torch
+    out = torch.empty(list(x.shape), dtype=x.dtype, device=x.device)
+    nd = x.dim()
+    sizes = (ctypes.c_int64 * max(1, nd))(*x.shape)
+    strides = (ctypes.c_int64 * max(1, nd))(*x.stride())
+    _check(lib().tpr_copy_strided(ctypes.c_void_p(x.data_ptr()), x.element_size(), nd, sizes, strides,
+                                  ctypes.c_void_p(out.data_ptr()), _stream(torch, x.device)))
+    return out

@@ -1,0 +1,62 @@
+"""Build the native parts of tensorplay_amd in-tree for gfx950.
+
+  libtpr_rocm.so   HIP kernels + the C-ABI launch layer (include/tpr_rocm.h)
+
+Usage: python -m tensorplay_amd.build  (or tensorplay_amd.build.build_all()).
+"""
+import os
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+BUILD = os.path.join(PKG, "_build")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+# -packed-fp32-ops: never emit packed fp32 (v_pk_*_f32) instructions.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-result",
+]
+
+ROCM_SOURCES = ["rocm/capi.cpp", "rocm/reduce.hip", "rocm/topk.hip", "rocm/copy.hip"]
+LIB_TPR = os.path.join(PKG, "libtpr_rocm.so")
+
+
+def _run(cmd):
+    print("+", " ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+
+
+def _newer(target, deps):
+    if not os.path.exists(target):
+        return True
+    t = os.path.getmtime(target)
+    return any(os.path.getmtime(d) > t for d in deps)
+
+
+def build_tpr(force=True):
+    os.makedirs(BUILD, exist_ok=True)
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", os.path.join(CSRC, "rocm")]
+    headers = [os.path.join(ROOT, "include", "tpr_rocm.h"), os.path.join(CSRC, "rocm", "common.h")]
+    objs = []
+    for src in ROCM_SOURCES:
+        s = os.path.join(CSRC, src)
+        o = os.path.join(BUILD, os.path.basename(src) + ".o")
+        if force or _newer(o, [s] + headers):
+            lang = ["-x", "hip"] if src.endswith(".cpp") else []
+            _run([HIPCC] + HIP_FLAGS + inc + lang + ["-c", s, "-o", o])
+        objs.append(o)
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", LIB_TPR] + objs)
+    return LIB_TPR
+
+
+def build_all(force=True):
+    build_tpr(force)
+
+
+if __name__ == "__main__":
+    build_all(force="--incremental" not in sys.argv)

@@ -1,0 +1,72 @@
+// C-ABI plumbing shared by every entry point: thread-local last error,
+// device facts, ABI version and the tuning hook.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstring>
+#include <string>
+
+#include "common.h"
+
+namespace tpr {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int status, const std::string& msg) {
+    g_last_error = msg;
+    return status;
+}
+
+int check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        return fail(TPR_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+    }
+    return TPR_OK;
+}
+
+const DeviceInfo& device_info() {
+    static constexpr int kMaxDev = 64;
+    static DeviceInfo infos[kMaxDev];
+    static std::atomic<int> ready[kMaxDev];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) dev = 0;
+    if (!ready[dev].load(std::memory_order_acquire)) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0) {
+            cus = 256;
+        }
+        infos[dev].cus = cus;  // every racing writer stores the same value
+        ready[dev].store(1, std::memory_order_release);
+    }
+    return infos[dev];
+}
+
+DebugKnobs& knobs() {
+    static DebugKnobs k;
+    return k;
+}
+
+}  // namespace tpr
+
+extern "C" {
+
+const char* tpr_last_error(void) { return tpr::g_last_error.c_str(); }
+
+int32_t tpr_abi_version(void) { return (1 << 16) | 0; }
+
+int tpr_debug_set(const char* key, int64_t value) {
+    if (!key) return tpr::fail(TPR_ERR_INVALID_ARG, "tpr_debug_set: null key");
+    auto& k = tpr::knobs();
+    if (!std::strcmp(key, "splits")) k.splits = value;
+    else if (!std::strcmp(key, "lanes")) k.lanes = value;
+    else if (!std::strcmp(key, "general")) k.general = value;
+    else if (!std::strcmp(key, "topk_fallback")) k.topk_fallback = value;
+    else return tpr::fail(TPR_ERR_INVALID_ARG, std::string("tpr_debug_set: unknown key ") + key);
+    return TPR_OK;
+}
+
+}  // extern "C"

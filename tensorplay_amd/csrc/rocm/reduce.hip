@@ -1,0 +1,740 @@
+// gfx950 reduction kernels (sum / mean / amax / amin / argmax / argmin / var /
+// std) over arbitrary strided float32 views, and the host planner behind
+// tpr_reduce().
+//
+// Semantics follow TensorPlay's CPU path
+// (/root/reference/p10/src/backend/cpu/ReductionKernels.cpp):
+//  * max/min keep the first occurrence under a strict compare, so NaN never
+//    wins and ties go to the lowest index (:242, :294, :694, :732);
+//  * sums accumulate in fp64 (the reference's full sum does, :30/:94; its dim
+//    sum accumulates in fp32, :168, which is less accurate -- the result here is
+//    closer to the exact sum than the reference's);
+//  * var/std use a Welford/Chan merge of per-thread shifted sums instead of the
+//    reference's five-pass mean/sub/mul/sum/div composite (:817-855).
+//
+// Layout classes after the host canonicalises the view (drop size-1 dims, merge
+// adjacent dims that are contiguous with each other and share reduce status):
+//   rows    [K, R]     R contiguous          -> k_rows   (128-bit loads along rows)
+//   cols    [K1, R, K2] K2 contiguous         -> k_cols   (128-bit loads along K2)
+//   general anything else                    -> k_general (index arithmetic)
+// Any of them may split the reduced extent over S workgroups; the S partial
+// states then go through k_finalize (no atomics; fixed combine order, so results
+// are deterministic run to run).
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "common.h"
+
+namespace tpr {
+namespace {
+
+constexpr long long kSentinel = 0x7fffffffffffffffLL;
+constexpr int kBlock = 256;
+
+// ---------------------------------------------------------------------------
+// Operator policies.  Acc = per-thread running state, State = mergeable state.
+// ---------------------------------------------------------------------------
+struct SumS { double s; };
+
+struct SumOp {
+    using Acc = double;
+    using State = SumS;
+    __device__ static Acc init() { return 0.0; }
+    __device__ static void acc(Acc& a, float x, long long) { a += (double)x; }
+    __device__ static State state(Acc a) { return {a}; }
+    __device__ static State identity() { return {0.0}; }
+    __device__ static State comb(State a, State b) { return {a.s + b.s}; }
+    __device__ static State shfl(State s, int m) { return {__shfl_xor(s.s, m, kWave)}; }
+};
+
+struct ArgS { float v; long long i; };
+
+// Strict compare in index order; lowest index wins equal values (-0.0 == +0.0).
+template <bool IS_MAX>
+struct ArgOp {
+    using Acc = ArgS;
+    using State = ArgS;
+    __device__ static Acc init() { return {IS_MAX ? -INFINITY : INFINITY, kSentinel}; }
+    __device__ static void acc(Acc& a, float x, long long i) {
+        bool t = IS_MAX ? (x > a.v) : (x < a.v);
+        a.v = t ? x : a.v;
+        a.i = t ? i : a.i;
+    }
+    __device__ static State state(Acc a) { return a; }
+    __device__ static State identity() { return init(); }
+    __device__ static State comb(State a, State b) {
+        bool t = IS_MAX ? (b.v > a.v) : (b.v < a.v);
+        t = t || (b.v == a.v && b.i < a.i);
+        return t ? b : a;
+    }
+    __device__ static State shfl(State s, int m) {
+        return {__shfl_xor(s.v, m, kWave), __shfl_xor(s.i, m, kWave)};
+    }
+};
+
+struct WelS { double n, mean, m2; };
+// Per-thread shifted sums: d = x - K with K the thread's first element, so the
+// running sums stay small and M2 = S2 - S1^2/n loses nothing to cancellation.
+struct WelAcc { float k; int n; double s1, s2; };
+
+struct WelfordOp {
+    using Acc = WelAcc;
+    using State = WelS;
+    __device__ static Acc init() { return {0.0f, 0, 0.0, 0.0}; }
+    __device__ static void acc(Acc& a, float x, long long) {
+        a.k = (a.n == 0) ? x : a.k;
+        double d = (double)x - (double)a.k;
+        a.s1 += d;
+        a.s2 = fma(d, d, a.s2);
+        a.n += 1;
+    }
+    __device__ static State state(Acc a) {
+        if (a.n == 0) return {0.0, 0.0, 0.0};
+        double n = (double)a.n;
+        double m = a.s1 / n;
+        return {n, (double)a.k + m, fmax(0.0, a.s2 - a.s1 * m)};
+    }
+    __device__ static State identity() { return {0.0, 0.0, 0.0}; }
+    // Chan et al. pairwise merge.
+    __device__ static State comb(State a, State b) {
+        if (a.n == 0.0) return b;
+        if (b.n == 0.0) return a;
+        double n = a.n + b.n;
+        double d = b.mean - a.mean;
+        double f = b.n / n;
+        return {n, a.mean + d * f, a.m2 + b.m2 + d * d * a.n * f};
+    }
+    __device__ static State shfl(State s, int m) {
+        return {__shfl_xor(s.n, m, kWave), __shfl_xor(s.mean, m, kWave),
+                __shfl_xor(s.m2, m, kWave)};
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Finalisation: state -> output element.
+// ---------------------------------------------------------------------------
+struct Fin {
+    int op;         // tpr_reduce_op
+    int out_f64;    // SUM/MEAN write double
+    double count;   // divisor count (reference semantics, duplicates included)
+    double corr;    // VAR/STD correction
+};
+
+__device__ __forceinline__ void fin_write(const SumS& s, const Fin& f, void* out, long long o) {
+    double v = s.s;
+    if (f.op == TPR_MEAN) v = v / f.count;
+    if (f.out_f64) ((double*)out)[o] = v;
+    else ((float*)out)[o] = (float)v;
+}
+
+__device__ __forceinline__ void fin_write(const ArgS& s, const Fin& f, void* out, long long o) {
+    if (f.op == TPR_AMAX || f.op == TPR_AMIN) ((float*)out)[o] = s.v;
+    else ((long long*)out)[o] = (s.i == kSentinel) ? 0 : s.i;
+}
+
+__device__ __forceinline__ void fin_write(const WelS& s, const Fin& f, void* out, long long o) {
+    // The reference centres on sum/count where count multiplies every listed dim
+    // (duplicates included); with count == n this is the plain mean.  Expanding
+    // sum((x - m')^2) = M2 + n (mean - m')^2 reproduces that centring exactly.
+    double mp = s.mean * (s.n / f.count);
+    double dm = s.mean - mp;
+    double m2 = s.m2 + s.n * dm * dm;
+    double div = fmax(0.0, f.count - f.corr);
+    float var = (float)(m2 / div);
+    ((float*)out)[o] = (f.op == TPR_STD) ? sqrtf(var) : var;
+}
+
+// ---------------------------------------------------------------------------
+// Workgroup combine helpers.
+// ---------------------------------------------------------------------------
+template <class Op, int WIDTH>
+__device__ __forceinline__ typename Op::State group_reduce_sub_wave(typename Op::State st) {
+#pragma unroll
+    for (int m = 1; m < WIDTH; m <<= 1) st = Op::comb(st, Op::shfl(st, m));
+    return st;
+}
+
+template <class Op>
+__device__ __forceinline__ typename Op::State block_reduce(typename Op::State st) {
+    using State = typename Op::State;
+    __shared__ State sh[kBlock / kWave];
+    st = group_reduce_sub_wave<Op, kWave>(st);
+    const int w = threadIdx.x / kWave;
+    if (__lane_id() == 0) sh[w] = st;
+    __syncthreads();
+    State r = sh[0];
+#pragma unroll
+    for (int i = 1; i < kBlock / kWave; ++i) r = Op::comb(r, sh[i]);
+    return r;  // valid in every thread
+}
+
+template <class Op>
+__device__ __forceinline__ void acc4(typename Op::Acc& a, float4 t, long long e) {
+    Op::acc(a, t.x, e);
+    Op::acc(a, t.y, e + 1);
+    Op::acc(a, t.z, e + 2);
+    Op::acc(a, t.w, e + 3);
+}
+
+// ---------------------------------------------------------------------------
+// Row kernel: [rows, R] with R contiguous.  LANES threads per row segment.
+// blockIdx.x = row_block * S + split.
+// ---------------------------------------------------------------------------
+struct RowArgs {
+    const float* in;
+    long long rows, R, row_stride, seg;
+    int S;
+    void* out;
+    void* part;
+    Fin fin;
+};
+
+template <class Op, int VEC, int LANES>
+__global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
+    using Acc = typename Op::Acc;
+    using State = typename Op::State;
+    constexpr int GROUPS = (LANES >= kBlock) ? 1 : kBlock / LANES;
+    const int tid = threadIdx.x;
+    const int g = tid / LANES;
+    const int l = tid % LANES;
+    const long long rb = blockIdx.x / a.S;
+    const int s = blockIdx.x % a.S;
+    const long long row = rb * GROUPS + g;
+
+    Acc acc = Op::init();
+    if (row < a.rows) {
+        const float* p = a.in + row * a.row_stride;
+        const long long beg = (long long)s * a.seg;
+        const long long end = min(a.R, beg + a.seg);
+        if (VEC == 4) {
+            const long long nv = (end - beg) >> 2;
+            const float4* pv = reinterpret_cast<const float4*>(p + beg);
+            long long v = l;
+            for (; v + 3 * LANES < nv; v += 4 * LANES) {
+                float4 t0 = pv[v];
+                float4 t1 = pv[v + LANES];
+                float4 t2 = pv[v + 2 * LANES];
+                float4 t3 = pv[v + 3 * LANES];
+                acc4<Op>(acc, t0, beg + 4 * v);
+                acc4<Op>(acc, t1, beg + 4 * (v + LANES));
+                acc4<Op>(acc, t2, beg + 4 * (v + 2 * LANES));
+                acc4<Op>(acc, t3, beg + 4 * (v + 3 * LANES));
+            }
+            for (; v < nv; v += LANES) acc4<Op>(acc, pv[v], beg + 4 * v);
+            for (long long e = beg + 4 * nv + l; e < end; e += LANES) Op::acc(acc, p[e], e);
+        } else {
+            long long e = beg + l;
+            for (; e + 3 * LANES < end; e += 4 * LANES) {
+                float x0 = p[e], x1 = p[e + LANES], x2 = p[e + 2 * LANES], x3 = p[e + 3 * LANES];
+                Op::acc(acc, x0, e);
+                Op::acc(acc, x1, e + LANES);
+                Op::acc(acc, x2, e + 2 * LANES);
+                Op::acc(acc, x3, e + 3 * LANES);
+            }
+            for (; e < end; e += LANES) Op::acc(acc, p[e], e);
+        }
+    }
+
+    State st = Op::state(acc);
+    constexpr int SUBW = LANES < kWave ? LANES : kWave;
+    st = group_reduce_sub_wave<Op, SUBW>(st);
+    if (LANES > kWave) {
+        constexpr int WPG = LANES / kWave;  // waves per group
+        __shared__ State sh[kBlock / kWave];
+        const int w = tid / kWave;
+        if (__lane_id() == 0) sh[w] = st;
+        __syncthreads();
+        if (l == 0) {
+            State r = sh[g * WPG];
+#pragma unroll
+            for (int i = 1; i < WPG; ++i) r = Op::comb(r, sh[g * WPG + i]);
+            st = r;
+        }
+    }
+    if (l == 0 && row < a.rows) {
+        if (a.S == 1) fin_write(st, a.fin, a.out, row);
+        else reinterpret_cast<State*>(a.part)[(long long)s * a.rows + row] = st;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Column kernel: [outer, R, inner], inner contiguous.  TX threads across the
+// inner dim (VEC elements each), TY = 256/TX threads across R.
+// blockIdx.x = (o * ncb + cb) * S + split.
+// ---------------------------------------------------------------------------
+struct ColArgs {
+    const float* in;
+    long long outer, os, R, rs, inner, segR;
+    int S;
+    long long ncb;
+    void* out;
+    void* part;
+    Fin fin;
+};
+
+template <class Op, int VEC, int TX>
+__global__ __launch_bounds__(kBlock) void k_cols(ColArgs a) {
+    using Acc = typename Op::Acc;
+    using State = typename Op::State;
+    constexpr int TY = kBlock / TX;
+    const int tid = threadIdx.x;
+    const int tx = tid % TX;
+    const int ty = tid / TX;
+    const int s = blockIdx.x % a.S;
+    const long long ob = blockIdx.x / a.S;
+    const long long cb = ob % a.ncb;
+    const long long o = ob / a.ncb;
+    const long long col0 = (cb * TX + tx) * VEC;
+
+    Acc acc[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) acc[j] = Op::init();
+
+    if (col0 < a.inner) {
+        const float* base = a.in + o * a.os + col0;
+        const long long rbeg = (long long)s * a.segR;
+        const long long rend = min(a.R, rbeg + a.segR);
+        if (VEC == 4 && col0 + 3 < a.inner) {
+            long long r = rbeg + ty;
+            for (; r + 3 * TY < rend; r += 4 * TY) {
+                float4 t0 = *reinterpret_cast<const float4*>(base + r * a.rs);
+                float4 t1 = *reinterpret_cast<const float4*>(base + (r + TY) * a.rs);
+                float4 t2 = *reinterpret_cast<const float4*>(base + (r + 2 * TY) * a.rs);
+                float4 t3 = *reinterpret_cast<const float4*>(base + (r + 3 * TY) * a.rs);
+                Op::acc(acc[0], t0.x, r); Op::acc(acc[1], t0.y, r);
+                Op::acc(acc[2], t0.z, r); Op::acc(acc[3], t0.w, r);
+                Op::acc(acc[0], t1.x, r + TY); Op::acc(acc[1], t1.y, r + TY);
+                Op::acc(acc[2], t1.z, r + TY); Op::acc(acc[3], t1.w, r + TY);
+                Op::acc(acc[0], t2.x, r + 2 * TY); Op::acc(acc[1], t2.y, r + 2 * TY);
+                Op::acc(acc[2], t2.z, r + 2 * TY); Op::acc(acc[3], t2.w, r + 2 * TY);
+                Op::acc(acc[0], t3.x, r + 3 * TY); Op::acc(acc[1], t3.y, r + 3 * TY);
+                Op::acc(acc[2], t3.z, r + 3 * TY); Op::acc(acc[3], t3.w, r + 3 * TY);
+            }
+            for (; r < rend; r += TY) {
+                float4 t = *reinterpret_cast<const float4*>(base + r * a.rs);
+                Op::acc(acc[0], t.x, r); Op::acc(acc[1], t.y, r);
+                Op::acc(acc[2], t.z, r); Op::acc(acc[3], t.w, r);
+            }
+        } else {
+            const int nj = (int)min((long long)VEC, a.inner - col0);
+            for (long long r = rbeg + ty; r < rend; r += TY) {
+                const float* q = base + r * a.rs;
+#pragma unroll
+                for (int j = 0; j < VEC; ++j)
+                    if (j < nj) Op::acc(acc[j], q[j], r);
+            }
+        }
+    }
+
+    State st[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) st[j] = Op::state(acc[j]);
+
+    if (TY > 1) {
+        __shared__ State sh[TY][TX * VEC];
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) sh[ty][tx * VEC + j] = st[j];
+        __syncthreads();
+        if (ty == 0) {
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) {
+                State r = sh[0][tx * VEC + j];
+#pragma unroll
+                for (int y = 1; y < TY; ++y) r = Op::comb(r, sh[y][tx * VEC + j]);
+                st[j] = r;
+            }
+        }
+    }
+    if (ty == 0) {
+        const long long nout = a.outer * a.inner;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+            const long long c = col0 + j;
+            if (c < a.inner) {
+                const long long oi = o * a.inner + c;
+                if (a.S == 1) fin_write(st[j], a.fin, a.out, oi);
+                else reinterpret_cast<State*>(a.part)[(long long)s * nout + oi] = st[j];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// General kernel: any strides.  One workgroup per (output, split); threads walk
+// the reduced index space with div/mod.  Also serves empty reduced extents.
+// ---------------------------------------------------------------------------
+struct GenArgs {
+    const float* in;
+    int nk, nr;
+    long long ksz[TPR_MAX_DIMS], kst[TPR_MAX_DIMS];
+    long long rsz[TPR_MAX_DIMS], rst[TPR_MAX_DIMS];
+    long long nout, count, seg;
+    int S;
+    void* out;
+    void* part;
+    Fin fin;
+};
+
+template <class Op>
+__global__ __launch_bounds__(kBlock) void k_general(GenArgs a) {
+    using Acc = typename Op::Acc;
+    using State = typename Op::State;
+    const long long o = blockIdx.x / a.S;
+    const int s = blockIdx.x % a.S;
+    long long base = 0;
+    {
+        long long rem = o;
+        for (int d = a.nk - 1; d >= 0; --d) {
+            base += (rem % a.ksz[d]) * a.kst[d];
+            rem /= a.ksz[d];
+        }
+    }
+    Acc acc = Op::init();
+    const long long beg = (long long)s * a.seg;
+    const long long end = min(a.count, beg + a.seg);
+    for (long long j = beg + threadIdx.x; j < end; j += kBlock) {
+        long long rem = j, off = 0;
+        for (int d = a.nr - 1; d >= 0; --d) {
+            off += (rem % a.rsz[d]) * a.rst[d];
+            rem /= a.rsz[d];
+        }
+        Op::acc(acc, a.in[base + off], j);
+    }
+    State st = block_reduce<Op>(Op::state(acc));
+    if (threadIdx.x == 0) {
+        if (a.S == 1) fin_write(st, a.fin, a.out, o);
+        else reinterpret_cast<State*>(a.part)[(long long)s * a.nout + o] = st;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Finalize: combine S partial states per output in split order.
+// ---------------------------------------------------------------------------
+struct FinArgs {
+    const void* part;
+    long long nout;
+    int S;
+    void* out;
+    Fin fin;
+};
+
+template <class Op>
+__global__ __launch_bounds__(kBlock) void k_finalize_thread(FinArgs a) {
+    using State = typename Op::State;
+    const long long o = (long long)blockIdx.x * kBlock + threadIdx.x;
+    if (o >= a.nout) return;
+    const State* p = reinterpret_cast<const State*>(a.part);
+    State st = p[o];
+    for (int s = 1; s < a.S; ++s) st = Op::comb(st, p[(long long)s * a.nout + o]);
+    fin_write(st, a.fin, a.out, o);
+}
+
+template <class Op>
+__global__ __launch_bounds__(kBlock) void k_finalize_block(FinArgs a) {
+    using State = typename Op::State;
+    const long long o = blockIdx.x;
+    const State* p = reinterpret_cast<const State*>(a.part);
+    State st = Op::identity();
+    for (int s = threadIdx.x; s < a.S; s += kBlock) st = Op::comb(st, p[(long long)s * a.nout + o]);
+    st = block_reduce<Op>(st);
+    if (threadIdx.x == 0) fin_write(st, a.fin, a.out, o);
+}
+
+// ---------------------------------------------------------------------------
+// Host planner.
+// ---------------------------------------------------------------------------
+enum PlanKind { P_ROWS = 1, P_COLS = 2, P_GENERAL = 3 };
+
+struct Plan {
+    int kind = P_GENERAL;
+    int vec = 1;
+    int lanes = 64;  // rows
+    int tx = 64;     // cols
+    long long S = 1;
+    size_t state_bytes = 8;
+    size_t ws = 0;
+    // geometry
+    long long rows = 1, R = 1, row_stride = 0, seg = 1;       // rows
+    long long outer = 1, os = 0, rs = 0, inner = 1, ncb = 1;  // cols
+    int nk = 0, nr = 0;
+    long long ksz[TPR_MAX_DIMS], kst[TPR_MAX_DIMS], rsz[TPR_MAX_DIMS], rst[TPR_MAX_DIMS];
+    long long nout = 1, count = 1;
+};
+
+size_t state_size(int op) {
+    switch (op) {
+        case TPR_SUM: case TPR_MEAN: return sizeof(SumS);
+        case TPR_AMAX: case TPR_AMIN: case TPR_ARGMAX: case TPR_ARGMIN: return sizeof(ArgS);
+        default: return sizeof(WelS);
+    }
+}
+
+long long ceil_div(long long a, long long b) { return (a + b - 1) / b; }
+long long round_up(long long a, long long b) { return ceil_div(a, b) * b; }
+long long pow2_ceil(long long v) {
+    long long p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+int validate(const tpr_reduce_desc* d) {
+    if (!d) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: null descriptor");
+    if (d->ndim < 0 || d->ndim > TPR_MAX_DIMS)
+        return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: ndim out of range [0, 8]");
+    if (d->op < TPR_SUM || d->op > TPR_STD) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: bad op");
+    for (int i = 0; i < d->ndim; ++i)
+        if (d->sizes[i] < 0) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: negative size");
+    if (d->ndim < 32 && (d->reduce_mask >> d->ndim) != 0)
+        return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: reduce_mask names a dim >= ndim");
+    if (d->in_dtype != TPR_FLOAT32)
+        return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: only float32 input is implemented");
+    switch (d->op) {
+        case TPR_SUM: case TPR_MEAN:
+            if (d->out_dtype != TPR_FLOAT32 && d->out_dtype != TPR_FLOAT64)
+                return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: sum/mean output must be float32 or float64");
+            break;
+        case TPR_AMAX: case TPR_AMIN:
+            if (d->out_dtype != d->in_dtype)
+                return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: amax/amin output dtype must equal input dtype");
+            break;
+        case TPR_ARGMAX: case TPR_ARGMIN:
+            if (d->out_dtype != TPR_INT64)
+                return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: argmax/argmin output must be int64");
+            break;
+        default:
+            if (d->out_dtype != TPR_FLOAT32)
+                return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: var/std output must be float32");
+    }
+    return TPR_OK;
+}
+
+Plan make_plan(const tpr_reduce_desc* d, const void* in) {
+    Plan p;
+    p.state_bytes = state_size(d->op);
+    const int nd = d->ndim;
+    uint32_t mask = (nd == 0) ? 0u : d->reduce_mask;
+    // counts (before dropping size-1 dims)
+    p.nout = 1;
+    p.count = 1;
+    for (int i = 0; i < nd; ++i) {
+        if (mask & (1u << i)) p.count *= d->sizes[i];
+        else p.nout *= d->sizes[i];
+    }
+    // canonicalise: drop size-1 dims, merge contiguous neighbours of equal kind
+    struct Dim { long long size, stride; bool red; };
+    std::vector<Dim> dims;
+    for (int i = 0; i < nd; ++i) {
+        if (d->sizes[i] == 1) continue;
+        Dim x{d->sizes[i], d->strides[i], (mask & (1u << i)) != 0};
+        if (!dims.empty() && dims.back().red == x.red && dims.back().stride == x.stride * x.size) {
+            dims.back().size *= x.size;
+            dims.back().stride = x.stride;
+        } else {
+            dims.push_back(x);
+        }
+    }
+    std::vector<Dim> K, Rd;
+    for (auto& x : dims) (x.red ? Rd : K).push_back(x);
+
+    const auto& dev = device_info();
+    const long long target = (long long)dev.cus * 2048;  // threads for a full chip
+    const bool aligned16 = (reinterpret_cast<uintptr_t>(in) & 15u) == 0;
+    const bool force_general = knobs().general != 0;
+    const bool empty = (p.count == 0 || p.nout == 0);
+
+    auto fill_general = [&]() {
+        p.kind = P_GENERAL;
+        p.nk = (int)K.size();
+        p.nr = (int)Rd.size();
+        for (int i = 0; i < p.nk; ++i) { p.ksz[i] = K[i].size; p.kst[i] = K[i].stride; }
+        for (int i = 0; i < p.nr; ++i) { p.rsz[i] = Rd[i].size; p.rst[i] = Rd[i].stride; }
+        p.S = 1;
+        if (!empty) {
+            long long blocks = p.nout;
+            long long want = (long long)dev.cus * 8;
+            if (blocks < want) p.S = std::min(ceil_div(want, blocks), std::max(1LL, p.count / (kBlock * 16)));
+            if (knobs().splits > 0) p.S = knobs().splits;
+            p.S = std::max(1LL, std::min(p.S, p.count));
+        }
+        p.seg = ceil_div(std::max(1LL, p.count), p.S);
+        p.S = ceil_div(std::max(1LL, p.count), p.seg);
+    };
+
+    if (empty || force_general) {
+        fill_general();
+    } else if (K.size() <= 1 && (Rd.empty() || (Rd.size() == 1 && Rd[0].stride == 1))) {
+        // rows: [K?, R] with R contiguous (R may be absent: each output is one element)
+        p.kind = P_ROWS;
+        p.rows = K.empty() ? 1 : K[0].size;
+        p.row_stride = K.empty() ? 0 : K[0].stride;
+        p.R = Rd.empty() ? 1 : Rd[0].size;
+        p.vec = (aligned16 && (p.rows == 1 || p.row_stride % 4 == 0) && p.R >= 4) ? 4 : 1;
+        const long long E = 64;  // elements per thread before splitting the row
+        long long lanes = std::min(256LL, std::max(16LL, pow2_ceil(ceil_div(p.R, E))));
+        if (knobs().lanes > 0) lanes = knobs().lanes;
+        p.lanes = (int)lanes;
+        long long threads = p.rows * lanes;
+        long long S = 1;
+        if (threads < target) S = std::min(ceil_div(target, threads), std::max(1LL, p.R / (lanes * 16)));
+        if (knobs().splits > 0) S = knobs().splits;
+        S = std::max(1LL, S);
+        p.seg = round_up(ceil_div(p.R, S), 4 * lanes);
+        p.S = ceil_div(p.R, p.seg);
+    } else if (!K.empty() && K.back().stride == 1 && Rd.size() == 1 &&
+               (K.size() == 1 ? true : (K.size() == 2)) &&
+               (K.size() == 1 ? (dims.front().red) : (dims.size() == 3 && dims[1].red))) {
+        // cols: [K1?, R, K2] with K2 contiguous
+        p.kind = P_COLS;
+        p.inner = K.back().size;
+        p.outer = (K.size() == 2) ? K[0].size : 1;
+        p.os = (K.size() == 2) ? K[0].stride : 0;
+        p.R = Rd[0].size;
+        p.rs = Rd[0].stride;
+        p.vec = (aligned16 && p.rs % 4 == 0 && (p.outer == 1 || p.os % 4 == 0) && p.inner >= 4) ? 4 : 1;
+        const long long cols_v = ceil_div(p.inner, p.vec);
+        // TX=256 (no cross-row combine) if that alone fills the chip
+        long long ncb256 = ceil_div(cols_v, 256);
+        if (p.outer * ncb256 * kBlock >= target || p.R < 16) p.tx = 256;
+        else p.tx = 64;
+        p.ncb = ceil_div(cols_v, p.tx);
+        const long long ty = kBlock / p.tx;
+        long long threads = p.outer * p.ncb * kBlock;
+        long long S = 1;
+        if (threads < target) S = std::min(ceil_div(target, threads), std::max(1LL, p.R / (ty * 16)));
+        if (knobs().splits > 0) S = knobs().splits;
+        S = std::max(1LL, std::min(S, p.R));
+        p.seg = ceil_div(p.R, S);
+        p.S = ceil_div(p.R, p.seg);
+    } else {
+        fill_general();
+    }
+    p.ws = (p.S > 1) ? (size_t)p.S * (size_t)p.nout * p.state_bytes : 0;
+    return p;
+}
+
+template <class Op>
+int launch_rows(const Plan& p, const float* in, void* out, void* ws, Fin fin, hipStream_t st) {
+    RowArgs a{in, p.rows, p.R, p.row_stride, p.seg, (int)p.S, out, ws, fin};
+    const long long groups = (p.lanes >= kBlock) ? 1 : kBlock / p.lanes;
+    const long long grid = ceil_div(p.rows, groups) * p.S;
+#define TPR_ROWS_CASE(L)                                                                  \
+    case L:                                                                               \
+        if (p.vec == 4) hipLaunchKernelGGL((k_rows<Op, 4, L>), dim3(grid), dim3(kBlock), 0, st, a); \
+        else hipLaunchKernelGGL((k_rows<Op, 1, L>), dim3(grid), dim3(kBlock), 0, st, a);            \
+        break;
+    switch (p.lanes) {
+        TPR_ROWS_CASE(16)
+        TPR_ROWS_CASE(32)
+        TPR_ROWS_CASE(64)
+        TPR_ROWS_CASE(128)
+        TPR_ROWS_CASE(256)
+        default: return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: lanes must be 16/32/64/128/256");
+    }
+#undef TPR_ROWS_CASE
+    return check_launch("k_rows");
+}
+
+template <class Op>
+int launch_cols(const Plan& p, const float* in, void* out, void* ws, Fin fin, hipStream_t st) {
+    ColArgs a{in, p.outer, p.os, p.R, p.rs, p.inner, p.seg, (int)p.S, p.ncb, out, ws, fin};
+    const long long grid = p.outer * p.ncb * p.S;
+    if (p.tx == 256) {
+        if (p.vec == 4) hipLaunchKernelGGL((k_cols<Op, 4, 256>), dim3(grid), dim3(kBlock), 0, st, a);
+        else hipLaunchKernelGGL((k_cols<Op, 1, 256>), dim3(grid), dim3(kBlock), 0, st, a);
+    } else {
+        if (p.vec == 4) hipLaunchKernelGGL((k_cols<Op, 4, 64>), dim3(grid), dim3(kBlock), 0, st, a);
+        else hipLaunchKernelGGL((k_cols<Op, 1, 64>), dim3(grid), dim3(kBlock), 0, st, a);
+    }
+    return check_launch("k_cols");
+}
+
+template <class Op>
+int launch_general(const Plan& p, const float* in, void* out, void* ws, Fin fin, hipStream_t st) {
+    GenArgs a;
+    a.in = in;
+    a.nk = p.nk;
+    a.nr = p.nr;
+    for (int i = 0; i < TPR_MAX_DIMS; ++i) {
+        a.ksz[i] = i < p.nk ? p.ksz[i] : 1;
+        a.kst[i] = i < p.nk ? p.kst[i] : 0;
+        a.rsz[i] = i < p.nr ? p.rsz[i] : 1;
+        a.rst[i] = i < p.nr ? p.rst[i] : 0;
+    }
+    a.nout = p.nout;
+    a.count = p.count;
+    a.seg = p.seg;
+    a.S = (int)p.S;
+    a.out = out;
+    a.part = ws;
+    a.fin = fin;
+    hipLaunchKernelGGL((k_general<Op>), dim3(p.nout * p.S), dim3(kBlock), 0, st, a);
+    return check_launch("k_general");
+}
+
+template <class Op>
+int launch_finalize(const Plan& p, void* out, const void* ws, Fin fin, hipStream_t st) {
+    FinArgs a{ws, p.nout, (int)p.S, out, fin};
+    if (p.S >= 64 && p.nout <= 4096) {
+        hipLaunchKernelGGL((k_finalize_block<Op>), dim3(p.nout), dim3(kBlock), 0, st, a);
+    } else {
+        hipLaunchKernelGGL((k_finalize_thread<Op>), dim3(ceil_div(p.nout, kBlock)), dim3(kBlock), 0, st, a);
+    }
+    return check_launch("k_finalize");
+}
+
+template <class Op>
+int run(const Plan& p, const float* in, void* out, void* ws, Fin fin, hipStream_t st) {
+    int rc = TPR_OK;
+    if (p.kind == P_ROWS) rc = launch_rows<Op>(p, in, out, ws, fin, st);
+    else if (p.kind == P_COLS) rc = launch_cols<Op>(p, in, out, ws, fin, st);
+    else rc = launch_general<Op>(p, in, out, ws, fin, st);
+    if (rc != TPR_OK) return rc;
+    if (p.S > 1) rc = launch_finalize<Op>(p, out, ws, fin, st);
+    return rc;
+}
+
+}  // namespace
+}  // namespace tpr
+
+extern "C" {
+
+size_t tpr_reduce_workspace_bytes(const tpr_reduce_desc* desc) {
+    if (tpr::validate(desc) != TPR_OK) return 0;
+    // alignment does not change the workspace size; plan with an aligned pointer
+    return tpr::make_plan(desc, nullptr).ws;
+}
+
+int tpr_reduce(const tpr_reduce_desc* desc, const void* in, void* out, void* workspace,
+               size_t workspace_bytes, void* stream) {
+    using namespace tpr;
+    int rc = validate(desc);
+    if (rc != TPR_OK) return rc;
+    Plan p = make_plan(desc, in);
+    if (p.nout == 0) return TPR_OK;
+    if (!out) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: null output");
+    if (!in && p.count > 0) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: null input");
+    if (p.ws > 0 && (workspace == nullptr || workspace_bytes < p.ws))
+        return fail(TPR_ERR_WORKSPACE, "tpr_reduce: workspace too small (need " +
+                                           std::to_string(p.ws) + " bytes)");
+    Fin fin;
+    fin.op = desc->op;
+    fin.out_f64 = desc->out_dtype == TPR_FLOAT64;
+    fin.count = (double)(desc->count_override > 0 ? desc->count_override : p.count);
+    fin.corr = (double)desc->correction;
+    const float* x = static_cast<const float*>(in);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    switch (desc->op) {
+        case TPR_SUM: case TPR_MEAN: return run<SumOp>(p, x, out, workspace, fin, st);
+        case TPR_AMAX: case TPR_ARGMAX: return run<ArgOp<true>>(p, x, out, workspace, fin, st);
+        case TPR_AMIN: case TPR_ARGMIN: return run<ArgOp<false>>(p, x, out, workspace, fin, st);
+        default: return run<WelfordOp>(p, x, out, workspace, fin, st);
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,66 @@
+"""CPU-side checks of the C-ABI library: it loads, exports every function
+declared in include/*.h, and validates arguments on the host without a GPU."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+from tensorplay_amd import _capi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        txt = open(h).read()
+        txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+        for m in re.finditer(r"\b(tpr_[a-z_0-9]+)\s*\(", txt):
+            names.add(m.group(1))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    L = _capi.lib()
+    declared = _declared_functions()
+    assert declared == set(_capi.EXPORTED)
+    for name in declared:
+        assert hasattr(L, name), name
+
+
+def test_abi_version():
+    assert _capi.lib().tpr_abi_version() >> 16 == 1
+
+
+def test_descriptor_layout_matches_header():
+    # int32 x4, int64[8] x2, uint32, int32, int64 x2
+    assert ctypes.sizeof(_capi.ReduceDesc) == 16 + 128 + 8 + 16
+
+
+def test_argument_validation_without_gpu():
+    L = _capi.lib()
+    d = _capi.make_desc("sum", [4, 4], [4, 1], [1], _capi.FLOAT32)
+    d.in_dtype = _capi.INT32
+    rc = L.tpr_reduce(ctypes.byref(d), None, None, None, 0, None)
+    assert rc == _capi.ERR_UNSUPPORTED_DTYPE
+    assert b"float32" in L.tpr_last_error()
+    d = _capi.make_desc("argmax", [4, 4], [4, 1], [1], _capi.FLOAT32)
+    assert L.tpr_reduce(ctypes.byref(d), None, None, None, 0, None) == _capi.ERR_INVALID_ARG
+    rc = L.tpr_topk(None, _capi.FLOAT32, 2, 5, 5, 6, 1, 1, None, None, None, 0, None)
+    assert rc == _capi.ERR_INVALID_ARG and b"k out of range" in L.tpr_last_error()
+    rc = L.tpr_topk(None, _capi.FLOAT64, 2, 5, 5, 1, 1, 1, None, None, None, 0, None)
+    assert rc == _capi.ERR_UNSUPPORTED_DTYPE
+    with pytest.raises(_capi.TprError):
+        _capi.debug_set("no_such_knob", 1)
+    d = _capi.make_desc("sum", [4], [1], [0], _capi.FLOAT32)
+    d.ndim = 9
+    assert L.tpr_reduce(ctypes.byref(d), None, None, None, 0, None) == _capi.ERR_INVALID_ARG
+
+
+def test_empty_output_is_a_no_op_without_gpu():
+    L = _capi.lib()
+    d = _capi.make_desc("sum", [0, 4], [4, 1], [1], _capi.FLOAT32)
+    assert L.tpr_reduce(ctypes.byref(d), None, None, None, 0, None) == _capi.OK
+    assert L.tpr_topk(None, _capi.FLOAT32, 3, 5, 5, 0, 1, 1, None, None, None, 0, None) == _capi.OK

@@ -1,0 +1,239 @@
+"""GPU parity of tpr_reduce (via the C-ABI) against the CPU oracle.
+
+  * amax/amin/argmax/argmin: bit-exact against the oracle (the reference CPU
+    semantics: strict compare, first index wins, NaN ignored).  argmax over a
+    non-last dim follows the permute layout (CUDA path, ReductionKernels.cu:67-75),
+    i.e. oracle quirk=0.
+  * sum/mean/var/std: max relative error <= 1e-5 against an fp64 host reference
+    (numpy float64); the CPU oracle's own error is measured beside it.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tensorplay_amd import _capi
+from tests.gpu_util import assert_bits_equal, assert_close_rel, device_view, fp64_reference, rel_err
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+@pytest.fixture(autouse=True)
+def _reset_knobs():
+    yield
+    for k in ("splits", "lanes", "general"):
+        _capi.debug_set(k, 0)
+
+
+def gpu(t, op, dims, correction=1):
+    out = _capi.reduce(t, op, dims, correction=correction)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def check(v, t, op, dims, correction=1):
+    """Compare one reduction of the numpy view v / torch view t."""
+    print(f"case op={op} shape={v.shape} strides={v.strides} dims={dims}", flush=True)
+    got = gpu(t, op, dims, correction)
+    if op in ("amax", "amin"):
+        f = O.amax if op == "amax" else O.amin
+        if dims is None or len(dims) == v.ndim:
+            if v.size == 0:
+                return
+            exp = np.float32(f(v))
+        else:
+            exp = f(v, list(dims))
+        assert_bits_equal(got.reshape(np.shape(exp)), exp)
+    elif op in ("argmax", "argmin"):
+        f = O.argmax if op == "argmax" else O.argmin
+        if dims is None:
+            exp = np.int64(f(v))
+            assert int(got.reshape(())) == int(exp)
+        else:
+            assert_bits_equal(got, f(v, dims[0]))
+    else:
+        ref = fp64_reference(v, op, dims, correction)
+        assert_close_rel(got.reshape(np.shape(ref)), ref)
+
+
+KNOWN = json.load(open(os.path.join(HERE, "golden", "reference_known_answers.json")))
+
+
+@pytest.mark.parametrize("case", KNOWN, ids=[c["src"] + ":" + c["op"] for c in KNOWN])
+def test_reference_known_answers_on_device(case):
+    # test_cuda_reductions.py / test_reduction.py known answers, on the ROCm device
+    x = np.array(case["x"], np.float32).reshape(case["shape"])
+    t = torch.from_numpy(x).cuda()
+    got = gpu(t, case["op"], case.get("dims"))
+    exp = case["expect"]
+    if isinstance(exp, list):
+        np.testing.assert_array_equal(got.ravel(), np.array(exp))
+    elif "places" in case:
+        assert round(float(got) - exp, case["places"]) == 0
+    else:
+        assert float(got) == exp
+
+
+OPS = ["sum", "mean", "amax", "amin", "argmax", "argmin", "var", "std"]
+
+
+def _views(rng):
+    """(base, view) pairs covering the layout classes: rows, cols, general, full."""
+    out = []
+    for shape in [(7,), (33, 5), (5, 1000), (16, 4096), (3, 17, 129), (4, 8, 6, 5), (2, 3, 1, 64)]:
+        b = rng.standard_normal(shape).astype(np.float32)
+        out.append((b, b))
+    b = rng.standard_normal((40, 64)).astype(np.float32)
+    out.append((b, b.T))                 # transposed
+    out.append((b, b[:, ::3]))           # stepped inner dim
+    out.append((b, b[1:, 1:]))           # misaligned start (not 16B aligned)
+    b = rng.standard_normal((6, 10, 12)).astype(np.float32)
+    out.append((b, b.transpose(2, 0, 1)))
+    out.append((b, b[:, 2:7, :]))
+    b = rng.standard_normal(1 << 16).astype(np.float32)
+    out.append((b, b[1:]))               # misaligned, odd length
+    out.append((b, b[::2]))              # strided full
+    return out
+
+
+def _dim_sets(nd):
+    sets = [None]
+    for d in range(nd):
+        sets.append([d])
+    if nd >= 2:
+        sets.append([0, nd - 1])
+    if nd >= 3:
+        sets.append([1, 2])
+    return sets
+
+
+@pytest.mark.parametrize("op", OPS)
+def test_random_layouts(op):
+    rng = np.random.default_rng(11)
+    for base, v in _views(rng):
+        t = device_view(torch, base, v)
+        for dims in _dim_sets(v.ndim):
+            if op in ("argmax", "argmin") and dims is not None and len(dims) > 1:
+                continue
+            check(v, t, op, dims)
+
+
+@pytest.mark.parametrize("knob,values", [("general", [1]), ("splits", [1, 2, 3, 7, 64]),
+                                         ("lanes", [16, 32, 64, 128, 256])])
+def test_forced_plans(knob, values):
+    rng = np.random.default_rng(12)
+    b = rng.standard_normal((37, 1029)).astype(np.float32)
+    c = rng.standard_normal((5, 300, 36)).astype(np.float32)
+    for val in values:
+        _capi.debug_set(knob, val)
+        for op in OPS:
+            check(b, torch.from_numpy(b).cuda(), op, [1])
+            check(b, torch.from_numpy(b).cuda(), op, None)
+            if knob != "lanes":
+                check(c, torch.from_numpy(c).cuda(), op, [1])
+                check(c, torch.from_numpy(c).cuda(), op, [0])
+
+
+def test_special_values():
+    x = np.array([[np.nan, -0.0, 0.0, 1.0, 1.0],
+                  [np.nan, np.nan, np.nan, np.nan, np.nan],
+                  [-np.inf, -np.inf, -np.inf, -np.inf, -np.inf],
+                  [0.0, -0.0, 0.0, -0.0, 0.0],
+                  [3.0, np.inf, 2.0, np.inf, 1.0]], np.float32)
+    t = torch.from_numpy(x).cuda()
+    for op in ("amax", "amin", "argmax", "argmin"):
+        for dims in ([1], [0], None):
+            check(x, t, op, dims)
+    # ties across threads: the lowest index wins wherever the equal values sit
+    y = np.zeros((3, 5000), np.float32)
+    y[0, [17, 4000, 4001]] = 7.0
+    y[1, [4999, 256, 1024]] = -7.0
+    for op in ("argmax", "argmin", "amax", "amin"):
+        check(y, torch.from_numpy(y).cuda(), op, [1])
+        check(y, torch.from_numpy(y).cuda(), op, None)
+
+
+def test_empty_and_degenerate():
+    e = np.zeros((0, 4), np.float32)
+    t = torch.from_numpy(e).cuda()
+    assert gpu(t, "sum", [1]).shape == (0,)
+    s = gpu(t, "sum", [0])
+    np.testing.assert_array_equal(s, np.zeros(4, np.float32))
+    assert np.isnan(gpu(t, "mean", [0])).all()
+    assert np.isnan(gpu(t, "var", [0])).all()
+    assert (gpu(t, "amax", [0]) == -np.inf).all()
+    assert (gpu(t, "argmax", [0]) == 0).all()
+    one = np.array([2.5], np.float32)
+    to = torch.from_numpy(one).cuda()
+    assert np.isnan(gpu(to, "var", None))           # 0/0 as the reference
+    assert gpu(to, "var", None, correction=0) == 0.0
+    assert gpu(to, "sum", None) == 2.5
+
+
+def test_mean_var_count_override_duplicates():
+    # reference divides by the product over the listed dims, duplicates included
+    x = np.random.default_rng(13).standard_normal((6, 9)).astype(np.float32)
+    t = torch.from_numpy(x).cuda()
+    m = _capi.reduce(t, "mean", [1], count_override=81).cpu().numpy()
+    np.testing.assert_allclose(m, x.astype(np.float64).sum(1) / 81, rtol=1e-5)
+    v = _capi.reduce(t, "var", [1], count_override=81).cpu().numpy()
+    np.testing.assert_allclose(v, O.var(x, [1, 1]), rtol=1e-4)
+
+
+# ---- BASELINE configurations at full size ---------------------------------------
+def test_config1_sum_lastdim():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((4096, 4096), dtype=np.float32)
+    t = torch.from_numpy(x).cuda()
+    got = gpu(t, "sum", [-1])
+    ref = x.astype(np.float64).sum(1)
+    e_gpu = assert_close_rel(got, ref)
+    e_cpu = rel_err(O.sum(x, [-1]), ref)
+    print(f"C1 sum dim=-1: gpu rel err {e_gpu:.2e}, reference-CPU-path rel err {e_cpu:.2e}")
+
+
+def test_config2_strided():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((64, 1024, 1024), dtype=np.float32)
+    t = torch.from_numpy(x).cuda()
+    got = gpu(t, "mean", [1])
+    ref = x.astype(np.float64).mean(1)
+    assert_close_rel(got, ref)
+    print(f"C2 mean dim=1 cpu-path err {rel_err(O.mean(x, [1]), ref):.2e}")
+    assert_bits_equal(gpu(t, "amax", [0]), O.amax(x, [0]))
+    assert_bits_equal(gpu(t, "argmax", [0]), O.argmax(x, 0))
+    for op in ("var", "std"):
+        got = gpu(t, op, [-1])
+        ref = fp64_reference(x, op, [2])
+        assert_close_rel(got, ref)
+        f = O.var if op == "var" else O.std
+        print(f"C2 {op} dim=-1 cpu-path err {rel_err(f(x, [-1]), ref):.2e}")
+
+
+def test_config4_full_tensor():
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal(1 << 28, dtype=np.float32) * np.float32(2.0) + np.float32(0.5))
+    t = torch.from_numpy(x).cuda()
+    x64 = x.astype(np.float64)
+    s64 = x64.sum()
+    assert_close_rel(gpu(t, "sum", None), s64)
+    assert_close_rel(gpu(t, "mean", None), s64 / x.size)
+    assert_bits_equal(gpu(t, "amax", None).reshape(()), np.float32(O.amax(x)))
+    assert int(gpu(t, "argmax", None)) == int(O.argmax(x))
+    v64 = x64.var(ddof=1)
+    del x64
+    assert_close_rel(gpu(t, "var", None), v64)
+    assert_close_rel(gpu(t, "std", None), np.sqrt(v64))
+
+
+def test_config5_argmax_logits():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((256, 151936), dtype=np.float32) * np.float32(3.0)
+    for r in range(256):
+        x[r, rng.choice(151936, 8, replace=False)] += np.float32(15.0)
+    t = torch.from_numpy(x).cuda()
+    assert_bits_equal(gpu(t, "argmax", [-1]), O.argmax(x, -1))

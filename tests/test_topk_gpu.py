@@ -1,0 +1,82 @@
+"""GPU parity of tpr_topk (via the C-ABI) against the CPU oracle: values and
+indices bit-exact (ties to the lowest index, -0.0 == +0.0, NaN largest)."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tensorplay_amd import _capi
+from tests.gpu_util import assert_bits_equal, device_view
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(autouse=True)
+def _reset_knobs():
+    yield
+    _capi.debug_set("topk_fallback", 0)
+
+
+def check(base, v, k, largest=True):
+    print(f"case topk shape={v.shape} strides={v.strides} k={k} largest={largest}", flush=True)
+    t = device_view(torch, base, v)
+    gv, gi = _capi.topk(t, k, largest)
+    torch.cuda.synchronize()
+    ev, ei = O.topk(np.ascontiguousarray(v) if v.strides[1] != 4 else v, k, largest)
+    assert_bits_equal(gi.cpu().numpy(), ei)
+    assert_bits_equal(gv.cpu().numpy(), ev)
+
+
+@pytest.mark.parametrize("fallback", [0, 1])
+def test_random_shapes(fallback):
+    _capi.debug_set("topk_fallback", fallback)
+    rng = np.random.default_rng(21)
+    for rows, cols in [(1, 1), (3, 7), (5, 64), (4, 1000), (2, 4097), (9, 16384), (3, 40000)]:
+        x = rng.uniform(-1, 1, (rows, cols)).astype(np.float32)
+        for k in sorted({1, min(cols, 7), min(cols, 64), min(cols, 1024), cols if cols <= 1024 else 1024}):
+            for largest in (True, False):
+                check(x, x, k, largest)
+
+
+def test_adversarial_rows():
+    rng = np.random.default_rng(22)
+    n = 20000
+    rows = [np.full(n, 0.25, np.float32),                        # all equal
+            np.arange(n, dtype=np.float32),                      # ascending
+            np.arange(n, dtype=np.float32)[::-1].copy(),         # descending
+            rng.integers(0, 3, n).astype(np.float32),            # heavy duplicates
+            np.where(rng.random(n) < 0.5, -0.0, 0.0).astype(np.float32),
+            rng.standard_normal(n).astype(np.float32)]
+    r = rng.standard_normal(n).astype(np.float32)
+    r[rng.choice(n, 100, replace=False)] = np.nan
+    r[rng.choice(n, 10, replace=False)] = np.inf
+    r[rng.choice(n, 10, replace=False)] = -np.inf
+    rows.append(r)
+    x = np.stack(rows)
+    for k in (1, 50, 64, 1024):
+        for largest in (True, False):
+            check(x, x, k, largest)
+
+
+def test_strided_and_misaligned_rows():
+    rng = np.random.default_rng(23)
+    b = rng.uniform(-1, 1, (6, 5003)).astype(np.float32)
+    check(b, b[:, 1:], 33)            # misaligned rows, odd stride
+    check(b, b[::2, :4096], 64)       # row stride 2*5003
+    check(b, b[:, 3:3 + 1031], 100)
+
+
+def test_config3_uniform():
+    rng = np.random.default_rng(3)
+    x = rng.uniform(-1, 1, (1024, 32768)).astype(np.float32)
+    # U(-1,1) fp32 rows of 32768 contain duplicate values: ties are exercised
+    assert any(len(np.unique(x[r])) < x.shape[1] for r in range(64))
+    check(x, x, 64)
+
+
+def test_config5_peaked_logits():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((256, 151936), dtype=np.float32) * np.float32(3.0)
+    for r in range(256):
+        x[r, rng.choice(151936, 8, replace=False)] += np.float32(15.0)
+    check(x, x, 50)
