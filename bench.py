@@ -1,0 +1,287 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X reduction + top-k path (one GPU).
+
+A "step" is one pass of the hot path over one batch of the headline workload,
+a contiguous fp32 [64, 1024, 1024] N(0,1) tensor reduced
+five ways -- mean over dim=1, amax and argmax over dim=0, var and std
+(unbiased) over dim=-1.  `value` is the step's algorithmic HBM bytes (input read
+once + output written once, per op) divided by the step time: GB/s.
+
+Inputs are resident in HBM before the timed region; consecutive steps rotate
+over 3 input buffers (768 MiB > the 256 MB Infinity Cache) so every step reads
+from HBM.  Times come from HIP events on the stream the kernels run on.
+The other BASELINE configs (C1 sum, C3 topk, C4 full-tensor, C5 logits topk /
+argmax) are measured the same way and reported under "configs".
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+METRIC = "achieved HBM GB/s (% of MI355X peak) for sum/argmax/topk; rows/s topk"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="headline workload only")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 256 MiB copy (PMC calibration for FETCH/WRITE_SIZE)")
+    ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "pmc_traffic.json"))
+    return ap.parse_args()
+
+
+class Call:
+    """A pre-bound C-ABI launch (all argument marshalling done up front)."""
+
+    def __init__(self, fn, args):
+        self.fn, self.args = fn, args
+
+    def __call__(self):
+        rc = self.fn(*self.args)
+        if rc != 0:
+            from tensorplay_amd import _capi
+            raise RuntimeError(_capi.lib().tpr_last_error().decode())
+
+
+def reduce_call(torch, capi, x, op, dims, stream, correction=1):
+    nd = x.dim()
+    rd = sorted(set((d + nd) % nd for d in dims)) if dims is not None else list(range(nd))
+    kept = [x.shape[i] for i in range(nd) if i not in rd]
+    od = capi.default_out_dtype(op)
+    tdt = torch.int64 if od == capi.INT64 else torch.float32
+    out = torch.empty(kept, dtype=tdt, device=x.device)
+    desc = capi.make_desc(op, list(x.shape), list(x.stride()), rd, od, correction)
+    L = capi.lib()
+    wsb = L.tpr_reduce_workspace_bytes(ctypes.byref(desc))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
+    keep = (desc, out, ws)
+    c = Call(L.tpr_reduce, (ctypes.byref(desc), ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                            ctypes.c_void_p(ws.data_ptr()), wsb, stream))
+    c.keep = keep
+    c.out_bytes = out.numel() * out.element_size()
+    return c
+
+
+def topk_call(torch, capi, x, k, stream):
+    rows, cols = x.shape
+    vals = torch.empty((rows, k), dtype=torch.float32, device=x.device)
+    idx = torch.empty((rows, k), dtype=torch.int64, device=x.device)
+    L = capi.lib()
+    wsb = L.tpr_topk_workspace_bytes(capi.FLOAT32, rows, cols, k)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
+    c = Call(L.tpr_topk, (ctypes.c_void_p(x.data_ptr()), capi.FLOAT32, rows, cols, x.stride(0), k, 1, 1,
+                          ctypes.c_void_p(vals.data_ptr()), ctypes.c_void_p(idx.data_ptr()),
+                          ctypes.c_void_p(ws.data_ptr()), wsb, stream))
+    c.keep = (vals, idx, ws)
+    c.out_bytes = rows * k * (4 + 8)
+    return c
+
+
+def time_calls(torch, step_fns, steps, warmup):
+    """Run warmup, then time `steps` iterations of step_fns[i % len] with HIP events."""
+    for i in range(warmup):
+        step_fns[i % len(step_fns)]()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(steps):
+        step_fns[i % len(step_fns)]()
+    ev1.record()
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) / steps  # ms per iteration
+
+
+def gen(torch, shape, kind, seed, dev):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    if kind == "normal":
+        return torch.randn(shape, generator=g, device=dev, dtype=torch.float32)
+    if kind == "uniform":
+        return torch.rand(shape, generator=g, device=dev, dtype=torch.float32) * 2 - 1
+    raise ValueError(kind)
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one GPU only (the reduction/top-k path has no "
+              "multi-GPU exchange); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from tensorplay_amd import _capi as capi
+
+    capi.lib()  # fails loudly if the HIP library is not built
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    steps, warmup = args.steps, args.warmup
+
+    # ---------------- headline: configs[1] --------------------------------------
+    shape2 = (64, 1024, 1024)
+    nbuf = 3
+    bufs = [gen(torch, shape2, "normal", 1000 + i, dev) for i in range(nbuf)]
+    in_bytes = 64 * 1024 * 1024 * 4
+    ops2 = [("mean", [1]), ("amax", [0]), ("argmax", [0]), ("var", [-1]), ("std", [-1])]
+    calls = [[reduce_call(torch, capi, b, op, dims, stream) for (op, dims) in ops2] for b in bufs]
+    op_bytes = [in_bytes + c.out_bytes for c in calls[0]]
+    step_bytes = sum(op_bytes)
+
+    def make_step(i):
+        def f():
+            for c in calls[i]:
+                c()
+        return f
+
+    step_fns = [make_step(i) for i in range(nbuf)]
+    ms_step = time_calls(torch, step_fns, steps, warmup)
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+
+    breakdown = {}
+    for j, (op, dims) in enumerate(ops2):
+        fns = [calls[i][j] for i in range(nbuf)]
+        ms = time_calls(torch, fns, steps, warmup)
+        gbs = op_bytes[j] / (ms * 1e-3) / 1e9
+        breakdown[f"{op}_dim{dims[0]}"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1),
+                                           "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+                                           "alg_bytes": op_bytes[j]}
+    dom_name, dom = max(breakdown.items(), key=lambda kv: kv[1]["ms"])
+
+    traffic = None
+    if os.path.exists(args.traffic_file):
+        try:
+            tf = json.load(open(args.traffic_file))
+            traffic = tf.get(dom_name, {}).get("hbm_bytes_per_launch")
+        except Exception:
+            traffic = None
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: torch.randn N(0,1) seeded on device, 3 rotating 256 MiB buffers",
+        "config": {"workload": "configs[1]: fp32 [64,1024,1024]; mean dim=1, amax+argmax dim=0, "
+                               "var+std dim=-1 (unbiased)",
+                   "frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+                   "step_alg_bytes": step_bytes},
+        "roofline": {"bound": "hbm", "kernel_op": dom_name, "achieved": dom["GB/s"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(dom["GB/s"] / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "breakdown": breakdown,
+    }
+
+    # ---------------- other BASELINE configs --------------------------------------
+    extras = {}
+    if not args.no_extras:
+        # C1: sum dim=-1 of [4096,4096]
+        b1 = [gen(torch, (4096, 4096), "normal", 2000 + i, dev) for i in range(12)]
+        c1 = [reduce_call(torch, capi, b, "sum", [-1], stream) for b in b1]
+        ms = time_calls(torch, c1, max(steps, 24), warmup)
+        by = 4096 * 4096 * 4 + c1[0].out_bytes
+        extras["C1_sum_dim-1_4096x4096"] = {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
+                                            "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        del b1, c1
+        # C3: topk k=64 of [1024,32768] U(-1,1)
+        b3 = [gen(torch, (1024, 32768), "uniform", 3000 + i, dev) for i in range(6)]
+        c3 = [topk_call(torch, capi, b, 64, stream) for b in b3]
+        ms = time_calls(torch, c3, max(steps, 12), warmup)
+        by = 1024 * 32768 * 4 + c3[0].out_bytes
+        extras["C3_topk64_1024x32768"] = {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
+                                          "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4),
+                                          "rows_per_s": round(1024 / (ms * 1e-3), 1)}
+        del b3, c3
+        # C4: full-tensor reductions of 2^28 N(0.5, 2)
+        x4 = gen(torch, (1 << 28,), "normal", 4000, dev) * 2.0 + 0.5
+        c4 = {}
+        for op in ("sum", "mean", "amax", "argmax", "var", "std"):
+            c = reduce_call(torch, capi, x4, op, None, stream)
+            ms = time_calls(torch, [c], max(steps // 2, 5), 2)
+            by = (1 << 28) * 4 + c.out_bytes
+            c4[op] = {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
+                      "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        extras["C4_full_2^28"] = c4
+        del x4
+        # C5: topk k=50 + argmax dim=-1 of [256,151936] N(0,3) + 8 boosted positions per row
+        b5 = []
+        for i in range(5):
+            x = gen(torch, (256, 151936), "normal", 5000 + i, dev) * 3.0
+            g = torch.Generator(device="cpu")
+            g.manual_seed(5100 + i)
+            pos = torch.stack([torch.randperm(151936, generator=g)[:8] for _ in range(256)]).to(dev)
+            x.scatter_add_(1, pos, torch.full((256, 8), 15.0, device=dev))
+            b5.append(x)
+        c5 = [topk_call(torch, capi, b, 50, stream) for b in b5]
+        ms = time_calls(torch, c5, max(steps, 10), warmup)
+        by = 256 * 151936 * 4 + c5[0].out_bytes
+        e5 = {"topk50": {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
+                         "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4),
+                         "rows_per_s": round(256 / (ms * 1e-3), 1)}}
+        c5a = [reduce_call(torch, capi, b, "argmax", [-1], stream) for b in b5]
+        ms = time_calls(torch, c5a, max(steps, 10), warmup)
+        by = 256 * 151936 * 4 + c5a[0].out_bytes
+        e5["argmax_dim-1"] = {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
+                              "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        extras["C5_logits_256x151936"] = e5
+        del b5, c5, c5a
+    if args.calibrate_copy:
+        xc = gen(torch, (64 << 20,), "normal", 6000, dev)
+        for _ in range(3):
+            capi.copy_strided(xc)
+        torch.cuda.synchronize()
+    result["configs"] = extras
+
+    # ---------------- CPU baseline (oracle restatement, 1 core) -------------------
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(bufs[0], ops2, op_bytes)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline(x_dev, ops2, op_bytes):
+    """Time the C restatement of TensorPlay's CPU reduction path (single-threaded,
+    as ReductionKernels.cpp is) on one full headline step: the same five
+    reductions of one [64,1024,1024] buffer copied to host memory."""
+    import numpy as np
+    from oracle import oracle as O
+
+    x = x_dev.cpu().numpy()
+    fns = {"mean": lambda d: O.mean(x, d), "amax": lambda d: O.amax(x, d),
+           "argmax": lambda d: O.argmax(x, d[0]), "var": lambda d: O.var(x, d), "std": lambda d: O.std(x, d)}
+    t0 = time.perf_counter()
+    per = {}
+    for (op, dims) in ops2:
+        t = time.perf_counter()
+        fns[op](dims)
+        per[f"{op}_dim{dims[0]}"] = round(time.perf_counter() - t, 3)
+    dt = time.perf_counter() - t0
+    total = float(sum(op_bytes))
+    return {"value": round(total / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": "one full headline step (mean dim1, amax+argmax dim0, var+std dim-1 of one "
+                      "[64,1024,1024] buffer) through oracle/tp_cpu_reduce.c, 1 thread",
+            "seconds": round(dt, 3), "per_op_s": per, "host_cpus": os.cpu_count()}
+
+
+if __name__ == "__main__":
+    main()
