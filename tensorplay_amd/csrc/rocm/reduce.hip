@@ -188,7 +188,7 @@ __device__ __forceinline__ void acc4(typename Op::Acc& a, float4 t, long long e)
 // ---------------------------------------------------------------------------
 struct RowArgs {
     const float* in;
-    long long rows, R, row_stride, seg;
+    long long rows, R, row_stride;
     int S;
     void* out;
     void* part;
@@ -200,6 +200,8 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
     using Acc = typename Op::Acc;
     using State = typename Op::State;
     constexpr int GROUPS = (LANES >= kBlock) ? 1 : kBlock / LANES;
+    constexpr int U = 4;                  // vectors in flight per lane
+    constexpr long long TILE = U * LANES; // vectors per tile (contiguous in memory)
     const int tid = threadIdx.x;
     const int g = tid / LANES;
     const int l = tid % LANES;
@@ -207,37 +209,48 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
     const int s = blockIdx.x % a.S;
     const long long row = rb * GROUPS + g;
 
+    // The row is cut into tiles of U*LANES vectors; split s takes tiles s, s+S,
+    // s+2S, ... so the S workgroups of a row sweep it front to back together.
     Acc acc = Op::init();
     if (row < a.rows) {
         const float* p = a.in + row * a.row_stride;
-        const long long beg = (long long)s * a.seg;
-        const long long end = min(a.R, beg + a.seg);
+        const long long step = (long long)a.S * TILE;
         if (VEC == 4) {
-            const long long nv = (end - beg) >> 2;
-            const float4* pv = reinterpret_cast<const float4*>(p + beg);
-            long long v = l;
-            for (; v + 3 * LANES < nv; v += 4 * LANES) {
-                float4 t0 = pv[v];
-                float4 t1 = pv[v + LANES];
-                float4 t2 = pv[v + 2 * LANES];
-                float4 t3 = pv[v + 3 * LANES];
-                acc4<Op>(acc, t0, beg + 4 * v);
-                acc4<Op>(acc, t1, beg + 4 * (v + LANES));
-                acc4<Op>(acc, t2, beg + 4 * (v + 2 * LANES));
-                acc4<Op>(acc, t3, beg + 4 * (v + 3 * LANES));
+            const long long nv = a.R >> 2;
+            const float4* pv = reinterpret_cast<const float4*>(p);
+            long long t0 = (long long)s * TILE;
+            for (; t0 + TILE <= nv; t0 += step) {
+                float4 t[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) t[u] = pv[t0 + l + u * LANES];
+#pragma unroll
+                for (int u = 0; u < U; ++u) acc4<Op>(acc, t[u], 4 * (t0 + l + u * LANES));
             }
-            for (; v < nv; v += LANES) acc4<Op>(acc, pv[v], beg + 4 * v);
-            for (long long e = beg + 4 * nv + l; e < end; e += LANES) Op::acc(acc, p[e], e);
+            if (t0 < nv) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const long long v = t0 + l + u * LANES;
+                    if (v < nv) acc4<Op>(acc, pv[v], 4 * v);
+                }
+            }
+            for (long long e = 4 * nv + (long long)s * LANES + l; e < a.R; e += (long long)a.S * LANES)
+                Op::acc(acc, p[e], e);
         } else {
-            long long e = beg + l;
-            for (; e + 3 * LANES < end; e += 4 * LANES) {
-                float x0 = p[e], x1 = p[e + LANES], x2 = p[e + 2 * LANES], x3 = p[e + 3 * LANES];
-                Op::acc(acc, x0, e);
-                Op::acc(acc, x1, e + LANES);
-                Op::acc(acc, x2, e + 2 * LANES);
-                Op::acc(acc, x3, e + 3 * LANES);
+            long long t0 = (long long)s * TILE;
+            for (; t0 + TILE <= a.R; t0 += step) {
+                float x[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) x[u] = p[t0 + l + u * LANES];
+#pragma unroll
+                for (int u = 0; u < U; ++u) Op::acc(acc, x[u], t0 + l + u * LANES);
             }
-            for (; e < end; e += LANES) Op::acc(acc, p[e], e);
+            if (t0 < a.R) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const long long e = t0 + l + u * LANES;
+                    if (e < a.R) Op::acc(acc, p[e], e);
+                }
+            }
         }
     }
 
@@ -270,7 +283,7 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
 // ---------------------------------------------------------------------------
 struct ColArgs {
     const float* in;
-    long long outer, os, R, rs, inner, segR;
+    long long outer, os, R, rs, inner;
     int S;
     long long ncb;
     void* out;
@@ -296,34 +309,37 @@ __global__ __launch_bounds__(kBlock) void k_cols(ColArgs a) {
 #pragma unroll
     for (int j = 0; j < VEC; ++j) acc[j] = Op::init();
 
+    // rows of the reduced dim are interleaved over the TY thread rows and the S
+    // splits (row r goes to split (r / TY) % S), so concurrently running
+    // workgroups read neighbouring rows
     if (col0 < a.inner) {
         const float* base = a.in + o * a.os + col0;
-        const long long rbeg = (long long)s * a.segR;
-        const long long rend = min(a.R, rbeg + a.segR);
+        const long long rstep = (long long)TY * a.S;
+        const long long r0 = (long long)s * TY + ty;
         if (VEC == 4 && col0 + 3 < a.inner) {
-            long long r = rbeg + ty;
-            for (; r + 3 * TY < rend; r += 4 * TY) {
+            long long r = r0;
+            for (; r + 3 * rstep < a.R; r += 4 * rstep) {
                 float4 t0 = *reinterpret_cast<const float4*>(base + r * a.rs);
-                float4 t1 = *reinterpret_cast<const float4*>(base + (r + TY) * a.rs);
-                float4 t2 = *reinterpret_cast<const float4*>(base + (r + 2 * TY) * a.rs);
-                float4 t3 = *reinterpret_cast<const float4*>(base + (r + 3 * TY) * a.rs);
+                float4 t1 = *reinterpret_cast<const float4*>(base + (r + rstep) * a.rs);
+                float4 t2 = *reinterpret_cast<const float4*>(base + (r + 2 * rstep) * a.rs);
+                float4 t3 = *reinterpret_cast<const float4*>(base + (r + 3 * rstep) * a.rs);
                 Op::acc(acc[0], t0.x, r); Op::acc(acc[1], t0.y, r);
                 Op::acc(acc[2], t0.z, r); Op::acc(acc[3], t0.w, r);
-                Op::acc(acc[0], t1.x, r + TY); Op::acc(acc[1], t1.y, r + TY);
-                Op::acc(acc[2], t1.z, r + TY); Op::acc(acc[3], t1.w, r + TY);
-                Op::acc(acc[0], t2.x, r + 2 * TY); Op::acc(acc[1], t2.y, r + 2 * TY);
-                Op::acc(acc[2], t2.z, r + 2 * TY); Op::acc(acc[3], t2.w, r + 2 * TY);
-                Op::acc(acc[0], t3.x, r + 3 * TY); Op::acc(acc[1], t3.y, r + 3 * TY);
-                Op::acc(acc[2], t3.z, r + 3 * TY); Op::acc(acc[3], t3.w, r + 3 * TY);
+                Op::acc(acc[0], t1.x, r + rstep); Op::acc(acc[1], t1.y, r + rstep);
+                Op::acc(acc[2], t1.z, r + rstep); Op::acc(acc[3], t1.w, r + rstep);
+                Op::acc(acc[0], t2.x, r + 2 * rstep); Op::acc(acc[1], t2.y, r + 2 * rstep);
+                Op::acc(acc[2], t2.z, r + 2 * rstep); Op::acc(acc[3], t2.w, r + 2 * rstep);
+                Op::acc(acc[0], t3.x, r + 3 * rstep); Op::acc(acc[1], t3.y, r + 3 * rstep);
+                Op::acc(acc[2], t3.z, r + 3 * rstep); Op::acc(acc[3], t3.w, r + 3 * rstep);
             }
-            for (; r < rend; r += TY) {
+            for (; r < a.R; r += rstep) {
                 float4 t = *reinterpret_cast<const float4*>(base + r * a.rs);
                 Op::acc(acc[0], t.x, r); Op::acc(acc[1], t.y, r);
                 Op::acc(acc[2], t.z, r); Op::acc(acc[3], t.w, r);
             }
         } else {
             const int nj = (int)min((long long)VEC, a.inner - col0);
-            for (long long r = rbeg + ty; r < rend; r += TY) {
+            for (long long r = r0; r < a.R; r += rstep) {
                 const float* q = base + r * a.rs;
 #pragma unroll
                 for (int j = 0; j < VEC; ++j)
@@ -543,7 +559,6 @@ Plan make_plan(const tpr_reduce_desc* d, const void* in) {
     for (auto& x : dims) (x.red ? Rd : K).push_back(x);
 
     const auto& dev = device_info();
-    const long long target = (long long)dev.cus * 2048;  // threads for a full chip
     const bool aligned16 = (reinterpret_cast<uintptr_t>(in) & 15u) == 0;
     const bool force_general = knobs().general != 0;
     const bool empty = (p.count == 0 || p.nout == 0);
@@ -575,17 +590,22 @@ Plan make_plan(const tpr_reduce_desc* d, const void* in) {
         p.row_stride = K.empty() ? 0 : K[0].stride;
         p.R = Rd.empty() ? 1 : Rd[0].size;
         p.vec = (aligned16 && (p.rows == 1 || p.row_stride % 4 == 0) && p.R >= 4) ? 4 : 1;
-        const long long E = 64;  // elements per thread before splitting the row
-        long long lanes = std::min(256LL, std::max(16LL, pow2_ceil(ceil_div(p.R, E))));
+        // lanes per row: >= ~32 elements per thread, and enough lanes that the
+        // grid holds ~4096 threads per CU; rows are split over workgroups only
+        // when even 256 lanes per row leave fewer than ~512 threads per CU
+        const long long E = 32;
+        long long lanes = std::max(pow2_ceil(ceil_div(p.R, E)),
+                                   pow2_ceil(ceil_div((long long)dev.cus * 4096, p.rows)));
+        lanes = std::min(256LL, std::max(16LL, std::min(lanes, pow2_ceil(ceil_div(p.R, 4)))));
         if (knobs().lanes > 0) lanes = knobs().lanes;
         p.lanes = (int)lanes;
+        const long long target = (long long)dev.cus * 512;
+        const long long tiles = std::max(1LL, ceil_div(p.R, 16 * lanes));  // 4 vectors x 4 floats per lane
         long long threads = p.rows * lanes;
         long long S = 1;
-        if (threads < target) S = std::min(ceil_div(target, threads), std::max(1LL, p.R / (lanes * 16)));
+        if (threads < target) S = std::min(ceil_div(target, threads), tiles);
         if (knobs().splits > 0) S = knobs().splits;
-        S = std::max(1LL, S);
-        p.seg = round_up(ceil_div(p.R, S), 4 * lanes);
-        p.S = ceil_div(p.R, p.seg);
+        p.S = std::max(1LL, S);
     } else if (!K.empty() && K.back().stride == 1 && Rd.size() == 1 &&
                (K.size() == 1 ? true : (K.size() == 2)) &&
                (K.size() == 1 ? (dims.front().red) : (dims.size() == 3 && dims[1].red))) {
@@ -597,20 +617,20 @@ Plan make_plan(const tpr_reduce_desc* d, const void* in) {
         p.R = Rd[0].size;
         p.rs = Rd[0].stride;
         p.vec = (aligned16 && p.rs % 4 == 0 && (p.outer == 1 || p.os % 4 == 0) && p.inner >= 4) ? 4 : 1;
-        const long long cols_v = ceil_div(p.inner, p.vec);
-        // TX=256 (no cross-row combine) if that alone fills the chip
-        long long ncb256 = ceil_div(cols_v, 256);
-        if (p.outer * ncb256 * kBlock >= target || p.R < 16) p.tx = 256;
+        // plan on float4 columns whatever the alignment, so the workspace size
+        // does not depend on the pointer
+        const long long cols4 = ceil_div(p.inner, 4);
+        const long long target = (long long)dev.cus * 512;
+        if (p.outer * ceil_div(cols4, 256) * kBlock >= target || p.R < 16) p.tx = 256;
         else p.tx = 64;
-        p.ncb = ceil_div(cols_v, p.tx);
+        if (knobs().tx == 64 || knobs().tx == 256) p.tx = (int)knobs().tx;
+        p.ncb = ceil_div(ceil_div(p.inner, p.vec), p.tx);
         const long long ty = kBlock / p.tx;
-        long long threads = p.outer * p.ncb * kBlock;
+        const long long threads = p.outer * ceil_div(cols4, p.tx) * kBlock;
         long long S = 1;
-        if (threads < target) S = std::min(ceil_div(target, threads), std::max(1LL, p.R / (ty * 16)));
+        if (threads < target) S = std::min(ceil_div(target, threads), std::max(1LL, p.R / (ty * 8)));
         if (knobs().splits > 0) S = knobs().splits;
-        S = std::max(1LL, std::min(S, p.R));
-        p.seg = ceil_div(p.R, S);
-        p.S = ceil_div(p.R, p.seg);
+        p.S = std::max(1LL, std::min(S, ceil_div(p.R, ty)));
     } else {
         fill_general();
     }
@@ -620,7 +640,7 @@ Plan make_plan(const tpr_reduce_desc* d, const void* in) {
 
 template <class Op>
 int launch_rows(const Plan& p, const float* in, void* out, void* ws, Fin fin, hipStream_t st) {
-    RowArgs a{in, p.rows, p.R, p.row_stride, p.seg, (int)p.S, out, ws, fin};
+    RowArgs a{in, p.rows, p.R, p.row_stride, (int)p.S, out, ws, fin};
     const long long groups = (p.lanes >= kBlock) ? 1 : kBlock / p.lanes;
     const long long grid = ceil_div(p.rows, groups) * p.S;
 #define TPR_ROWS_CASE(L)                                                                  \
@@ -642,7 +662,7 @@ int launch_rows(const Plan& p, const float* in, void* out, void* ws, Fin fin, hi
 
 template <class Op>
 int launch_cols(const Plan& p, const float* in, void* out, void* ws, Fin fin, hipStream_t st) {
-    ColArgs a{in, p.outer, p.os, p.R, p.rs, p.inner, p.seg, (int)p.S, p.ncb, out, ws, fin};
+    ColArgs a{in, p.outer, p.os, p.R, p.rs, p.inner, (int)p.S, p.ncb, out, ws, fin};
     const long long grid = p.outer * p.ncb * p.S;
     if (p.tx == 256) {
         if (p.vec == 4) hipLaunchKernelGGL((k_cols<Op, 4, 256>), dim3(grid), dim3(kBlock), 0, st, a);
