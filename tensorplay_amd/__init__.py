@@ -1,2 +1,124 @@
-"""tensorplay_amd: MI355X (gfx950) backend for TensorPlay's P10 reduction + top-k path."""
+"""tensorplay_amd: MI355X (gfx950) backend for TensorPlay's P10 reduction + top-k path.
+
+The Python surface mirrors the parts of TensorPlay this path touches:
+``Tensor`` methods sum/mean/max/min/argmax/argmin/var/std (the overload set of
+/root/reference/src/bindings/python/Tensor.cpp:1099-1224) plus ``topk``, and the
+module functions of /root/reference/tensorplay/functional.py:401-432.  Tensors
+live on ``"cpu"`` or ``"rocm[:N]"``; reductions run on ROCm devices only (the
+CPU key has no kernels here -- that path stays TensorPlay's own).
+
+The native library must be built (``python -m tensorplay_amd.build``); there is
+no fallback.
+"""
+try:
+    # One HIP runtime per process: torch ships its own libamdhip64 (same soname)
+    # and its libraries load it by file name, so if this package's runtime were
+    # loaded first the process would hold two.  Loading torch first makes both
+    # resolve to torch's copy.
+    import torch as _torch  # noqa: F401
+except ImportError:
+    pass
+from . import _C  # noqa: E402
+
 __version__ = "0.1.0"
+
+Tensor = _C.TensorBase
+DType = _C.DType
+Device = _C.Device
+
+uint8 = DType.uint8
+int8 = DType.int8
+int16 = DType.int16
+int32 = DType.int32
+int64 = DType.int64
+float32 = DType.float32
+float64 = DType.float64
+bool_ = DType.bool
+undefined = DType.undefined
+
+
+def device(spec):
+    return Device(spec)
+
+
+def tensor(data, dtype=None, device="cpu"):
+    """Copy array-like `data` into a new tensor on `device` ("cpu" / "rocm[:N]")."""
+    import numpy as np
+    arr = np.asarray(data)
+    if dtype is None and arr.dtype == np.float64 and not isinstance(data, np.ndarray):
+        arr = arr.astype(np.float32)  # Python floats default to float32, as TensorPlay's tensor()
+    return _C.tensor(arr, dtype, str(device))
+
+
+def from_numpy(arr, device="cpu"):
+    return _C.tensor(arr, None, str(device))
+
+
+def empty(shape, dtype=float32, device="cpu"):
+    return _C.empty(list(shape), dtype, str(device))
+
+
+def from_torch(t):
+    """Zero-copy view of a torch tensor that lives on an AMD GPU (keeps `t` alive)."""
+    import torch
+    if not t.is_cuda:
+        return _C.tensor(t.detach().numpy(), None, "cpu")
+    dt = {torch.float32: float32, torch.float64: float64, torch.int64: int64, torch.int32: int32}[t.dtype]
+    return _C._from_device_ptr(t.data_ptr(), list(t.shape), list(t.stride()), dt, t.device.index or 0, t)
+
+
+# ---- functional forms (tensorplay/functional.py:401-432 + topk) ----
+def sum(input, dim=None, keepdim=False, dtype=None):
+    return input.sum(dtype=dtype) if dim is None else input.sum(dim, keepdim, dtype=dtype)
+
+
+def mean(input, dim=None, keepdim=False, dtype=None):
+    return input.mean(dtype=dtype) if dim is None else input.mean(dim, keepdim, dtype=dtype)
+
+
+def max(input, dim=None, keepdim=False):
+    return input.max() if dim is None else input.max(dim, keepdim)
+
+
+def min(input, dim=None, keepdim=False):
+    return input.min() if dim is None else input.min(dim, keepdim)
+
+
+def amax(input, dim=None, keepdim=False):
+    return max(input, dim, keepdim)
+
+
+def amin(input, dim=None, keepdim=False):
+    return min(input, dim, keepdim)
+
+
+def argmax(input, dim=None, keepdim=False):
+    return input.argmax(dim, keepdim)
+
+
+def argmin(input, dim=None, keepdim=False):
+    return input.argmin(dim, keepdim)
+
+
+def var(input, dim=None, correction=1, keepdim=False):
+    return input.var(correction) if dim is None else input.var(dim, correction, keepdim)
+
+
+def std(input, dim=None, correction=1, keepdim=False):
+    return input.std(correction) if dim is None else input.std(dim, correction, keepdim)
+
+
+def topk(input, k, dim=-1, largest=True, sorted=True):
+    return input.topk(k, dim, largest, sorted)
+
+
+class rocm:
+    """ROCm runtime helpers (the counterpart of tensorplay.cuda for this backend)."""
+
+    is_available = staticmethod(_C._rocm.is_available)
+    device_count = staticmethod(_C._rocm.device_count)
+    synchronize = staticmethod(_C._rocm.synchronize)
+    set_stream = staticmethod(_C._rocm.set_stream)
+    current_stream = staticmethod(_C._rocm.current_stream)
+    empty_cache = staticmethod(_C._rocm.empty_cache)
+    memory_stats = staticmethod(_C._rocm.memory_stats)

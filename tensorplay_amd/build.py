@@ -1,6 +1,9 @@
 """Build the native parts of tensorplay_amd in-tree for gfx950.
 
   libtpr_rocm.so   HIP kernels + the C-ABI launch layer (include/tpr_rocm.h)
+  _C<ext>          host core (tensor, dispatcher with the ROCm key, caching
+                   allocator, reduction adapters) + Python bindings; links
+                   libtpr_rocm.so
 
 Usage: python -m tensorplay_amd.build  (or tensorplay_amd.build.build_all()).
 """
@@ -54,8 +57,39 @@ def build_tpr(force=True):
     return LIB_TPR
 
 
+CORE_SOURCES = ["core/Dispatcher.cpp", "core/Allocator.cpp", "core/Tensor.cpp",
+                "core/ROCmReductionKernels.cpp", "core/bindings.cpp"]
+CXX = os.environ.get("CXX", "g++")
+
+
+def build_core(force=True):
+    import sysconfig
+    import pybind11
+    os.makedirs(BUILD, exist_ok=True)
+    ext = sysconfig.get_config_var("EXT_SUFFIX")
+    out = os.path.join(PKG, "_C" + ext)
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", os.path.join(CSRC, "core"),
+           "-I", "/opt/rocm/include", "-I", pybind11.get_include(),
+           "-I", sysconfig.get_paths()["include"]]
+    flags = ["-O2", "-std=c++17", "-fPIC", "-D__HIP_PLATFORM_AMD__", "-fvisibility=hidden", "-Wall"]
+    headers = [os.path.join(CSRC, "core", h) for h in os.listdir(os.path.join(CSRC, "core")) if h.endswith(".h")]
+    headers.append(os.path.join(ROOT, "include", "tpr_rocm.h"))
+    objs = []
+    for src in CORE_SOURCES:
+        s = os.path.join(CSRC, src)
+        o = os.path.join(BUILD, os.path.basename(src) + ".o")
+        if force or _newer(o, [s] + headers):
+            _run([CXX] + flags + inc + ["-c", s, "-o", o])
+        objs.append(o)
+    _run([CXX, "-shared", "-o", out] + objs +
+         ["-L", PKG, "-ltpr_rocm", "-L", "/opt/rocm/lib", "-lamdhip64",
+          "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,/opt/rocm/lib"])
+    return out
+
+
 def build_all(force=True):
     build_tpr(force)
+    build_core(force)
 
 
 if __name__ == "__main__":

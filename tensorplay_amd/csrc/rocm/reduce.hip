@@ -492,7 +492,6 @@ size_t state_size(int op) {
 }
 
 long long ceil_div(long long a, long long b) { return (a + b - 1) / b; }
-long long round_up(long long a, long long b) { return ceil_div(a, b) * b; }
 long long pow2_ceil(long long v) {
     long long p = 1;
     while (p < v) p <<= 1;

@@ -1,0 +1,62 @@
+"""Host-core checks that need no GPU: dispatcher registry, schema set, error
+mapping, reduction-shape rules, views and host copies."""
+import numpy as np
+import pytest
+
+import tensorplay_amd as tp
+from tensorplay_amd import _C
+
+SCHEMAS = ["argmax", "argmin", "max", "max.dim", "mean", "mean.dim", "min", "min.dim", "std", "std.dim",
+           "sum", "sum.dim_IntList", "topk", "var", "var.dim"]
+
+
+def test_rocm_key_registers_every_schema():
+    # config/native_functions.yaml:695-809 reduction rows (+ topk), registered by name
+    assert _C._registered_ops("ROCm") == SCHEMAS
+    assert _C._registered_ops("CPU") == []
+
+
+def test_missing_kernel_is_not_implemented_error():
+    t = tp.tensor([[1.0, 2.0], [3.0, 4.0]])
+    with pytest.raises(NotImplementedError, match="Kernel not found for op: sum on backend: CPU"):
+        t.sum()
+    with pytest.raises(NotImplementedError, match="sum.dim_IntList"):
+        t.sum(0)
+    with pytest.raises(NotImplementedError, match="topk"):
+        t.topk(1)
+
+
+def test_reduction_shape_rules():
+    # ReductionKernels.cpp:48-70: negative dims wrap, keepdim keeps 1s, out of range raises
+    assert _C._reduction_shape([2, 3, 4], [-1], False) == [2, 3]
+    assert _C._reduction_shape([2, 3, 4], [0, 2], True) == [1, 3, 1]
+    assert _C._reduction_shape([2, 3, 4], [1, 1], False) == [2, 4]
+    with pytest.raises(RuntimeError, match="Dimension out of range"):
+        _C._reduction_shape([2, 3], [2], False)
+    with pytest.raises(RuntimeError, match="Dimension out of range"):
+        _C._reduction_shape([2, 3], [-3], False)
+
+
+def test_views_and_host_copies():
+    a = np.arange(24, dtype=np.float32).reshape(2, 3, 4)
+    t = tp.from_numpy(a)
+    assert t.shape == [2, 3, 4] and t.stride() == [12, 4, 1] and t.is_contiguous()
+    p = t.permute([2, 0, 1])
+    assert p.shape == [4, 2, 3] and not p.is_contiguous()
+    np.testing.assert_array_equal(p.numpy(), a.transpose(2, 0, 1))
+    np.testing.assert_array_equal(p.contiguous().numpy(), a.transpose(2, 0, 1))
+    np.testing.assert_array_equal(t.transpose(0, -1).numpy(), a.swapaxes(0, 2))
+    np.testing.assert_array_equal(t[1].numpy(), a[1])
+    with pytest.raises(IndexError):
+        t.transpose(0, 5)
+    assert tp.tensor(np.array([7], np.int64)).item() == 7
+    assert tp.tensor([2.5]).item() == 2.5
+    assert tp.tensor([1.0, 2.0]).dtype == tp.float32
+
+
+def test_device_parsing():
+    assert str(tp.device("rocm:1")) == "rocm:1"
+    assert tp.device("cpu").type == "cpu"
+    with pytest.raises(ValueError):
+        tp.device("cuda")
+    assert isinstance(tp.rocm.is_available(), bool)

@@ -1,0 +1,159 @@
+"""The reference's own reduction tests, re-expressed on the ROCm device through
+the drop-in Tensor API (dispatcher -> ROCm adapters -> C-ABI -> HIP):
+  test/test_cuda_reductions.py:19-98, test/test_reduction.py:35-57,
+  test/test_statistical.py:19-88 (vs torch at rtol 1e-5, atol 1e-8)."""
+import math
+
+import numpy as np
+import pytest
+
+import tensorplay_amd as tp
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+DEV = "rocm"
+
+
+def close(tpt, tt, rtol=1e-5, atol=1e-8):
+    assert tpt.shape == list(tt.shape)
+    np.testing.assert_allclose(tpt.numpy(), tt.numpy(), rtol=rtol, atol=atol)
+
+
+# ---- test_cuda_reductions.py equivalents --------------------------------------------------
+def test_sum():
+    t = tp.tensor(np.ones(10, np.float32), device=DEV)
+    assert t.sum().item() == 10.0
+    t = tp.tensor(np.ones((3, 4), np.float32), device=DEV)
+    s0 = t.sum(dim=[0])
+    assert s0.shape == [4] and s0.sum().item() == 12.0
+    s1 = t.sum(dim=[1], keepdim=True)
+    assert s1.shape == [3, 1] and s1.sum().item() == 12.0
+
+
+def test_mean():
+    t = tp.tensor(np.ones((3, 4), np.float32), device=DEV)
+    assert t.mean().item() == 1.0
+    t2 = tp.tensor(np.full((3, 4), 2.0, np.float32), device=DEV)
+    assert t2.mean(dim=[0]).sum().item() == 8.0
+
+
+def test_max_min():
+    t = tp.tensor(np.array([1.0, 2.0, 3.0, 4.0], np.float32).reshape(2, 2), device=DEV)
+    assert t.max().item() == 4.0 and t.min().item() == 1.0
+    m0 = t.max(dim=[0])
+    assert m0.shape == [2] and m0.sum().item() == 7.0
+
+
+def test_var_std():
+    t = tp.tensor([1.0, 2.0, 3.0, 4.0], device=DEV)
+    assert round(t.var().item() - 5.0 / 3.0, 7) == 0
+    assert round(t.std().item() - math.sqrt(5.0 / 3.0), 7) == 0
+
+
+def test_argmax_argmin():
+    t = tp.tensor([1.0, 5.0, 2.0, 8.0], device=DEV)
+    assert t.argmax().item() == 3 and t.argmin().item() == 0
+
+
+# ---- test_reduction.py equivalents -----------------------------------------------------------
+def test_reduction_known_answers():
+    x = tp.tensor([[1.0, 5.0, 2.0], [4.0, 3.0, 6.0]], device=DEV)
+    assert x.argmax().item() == 5 and x.argmin().item() == 0
+    am0 = x.argmax(dim=0)
+    assert [am0[i].item() for i in range(3)] == [1, 0, 1]
+    am1 = x.argmax(dim=1)
+    assert [am1[i].item() for i in range(2)] == [1, 2]
+    y = tp.tensor([[1.0, 2.0], [3.0, 4.0]], device=DEV)
+    assert y.sum().item() == 10.0 and y.mean().item() == 2.5
+
+
+# ---- test_statistical.py equivalents ---------------------------------------------------------
+@pytest.mark.parametrize("shape", [(10,), (5, 5), (2, 3, 4)])
+def test_var_std_vs_torch(shape):
+    g = torch.Generator().manual_seed(31)
+    data = torch.randn(shape, dtype=torch.float32, generator=g)
+    t = tp.tensor(data.numpy(), device=DEV)
+    close(t.var(), data.var())
+    close(t.var(correction=0), data.var(correction=0))
+    close(t.std(), data.std())
+    close(t.std(correction=0), data.std(correction=0))
+    if len(shape) > 1:
+        close(t.var(dim=0), data.var(dim=0))
+        close(t.var(dim=1, keepdim=True), data.var(dim=1, keepdim=True))
+        close(t.std(dim=0), data.std(dim=0))
+        close(t.std(dim=1, keepdim=True), data.std(dim=1, keepdim=True))
+
+
+@pytest.mark.parametrize("shape", [(10,), (5, 5), (2, 3, 4)])
+def test_max_min_vs_torch(shape):
+    g = torch.Generator().manual_seed(32)
+    data = torch.randn(shape, dtype=torch.float32, generator=g)
+    t = tp.tensor(data.numpy(), device=DEV)
+    close(t.max(), data.max())
+    close(t.min(), data.min())
+    if len(shape) > 1:
+        close(t.max(dim=[0]), data.amax(dim=0))
+        close(t.min(dim=[0], keepdim=True), data.amin(dim=0, keepdim=True))
+
+
+# ---- drop-in semantics through the dispatcher ----------------------------------------------
+def test_dims_dtypes_and_errors():
+    a = np.random.default_rng(33).standard_normal((4, 5, 6)).astype(np.float32)
+    t = tp.tensor(a, device=DEV)
+    s = t.sum([0, 2], keepdim=True)
+    assert s.shape == [1, 5, 1]
+    np.testing.assert_allclose(s.numpy().ravel(), a.astype(np.float64).sum((0, 2)), rtol=1e-5)
+    d = t.sum(dtype=tp.float64)
+    assert d.dtype == tp.float64 and abs(d.item() - a.astype(np.float64).sum()) < 1e-9
+    assert t.argmax(1, keepdim=True).shape == [4, 1, 6]
+    assert t.argmax(keepdim=True).shape == []          # flat argmax ignores keepdim
+    np.testing.assert_array_equal(t.argmax(0).numpy(), O.argmax(a, 0))
+    np.testing.assert_array_equal(t.max(-1).numpy(), O.amax(a, [-1]))
+    with pytest.raises(RuntimeError, match="Dimension out of range"):
+        t.sum(3)
+    with pytest.raises(IndexError):
+        t.argmax(3)
+    with pytest.raises(RuntimeError, match="non-empty"):
+        tp.empty([0], device=DEV).max()
+    assert math.isnan(tp.empty([0], device=DEV).var().item())
+    with pytest.raises(NotImplementedError):
+        tp.tensor(np.ones(3, np.int64), device=DEV).sum()
+    # strided (non-contiguous) inputs reduce without a copy
+    p = t.permute([2, 0, 1])
+    np.testing.assert_allclose(p.mean(1).numpy(), a.transpose(2, 0, 1).astype(np.float64).mean(1), rtol=1e-5)
+
+
+def test_topk_api():
+    a = np.random.default_rng(34).uniform(-1, 1, (3, 40, 7)).astype(np.float32)
+    t = tp.tensor(a, device=DEV)
+    for dim, k in ((-1, 5), (1, 5), (0, 3), (2, 7)):
+        v, i = t.topk(k, dim=dim)
+        tv, ti = torch.topk(torch.from_numpy(a), k, dim=dim)
+        assert v.shape == list(tv.shape) and i.shape == list(ti.shape)
+        np.testing.assert_array_equal(v.numpy(), tv.numpy())
+        np.testing.assert_array_equal(i.numpy(), ti.numpy())
+    v, i = tp.topk(t, 3, dim=1, largest=False)
+    tv, ti = torch.topk(torch.from_numpy(a), 3, dim=1, largest=False)
+    np.testing.assert_array_equal(v.numpy(), tv.numpy())
+    with pytest.raises(RuntimeError, match="k out of range"):
+        t.topk(8)
+
+
+def test_torch_interop_zero_copy():
+    x = torch.randn(64, 1000, device="cuda")
+    t = tp.from_torch(x)
+    tp.rocm.set_stream(torch.cuda.current_stream().cuda_stream)
+    try:
+        np.testing.assert_allclose(t.sum(1).numpy(), x.double().sum(1).cpu().numpy(), rtol=1e-5)
+    finally:
+        tp.rocm.set_stream(0)
+
+
+def test_caching_allocator_reuses_blocks():
+    t = tp.tensor(np.ones((256, 256), np.float32), device=DEV)
+    t.sum(1)
+    before = tp.rocm.memory_stats()["device_allocs"]
+    for _ in range(20):
+        t.sum(1).numpy()
+    assert tp.rocm.memory_stats()["device_allocs"] == before
