@@ -132,7 +132,9 @@ int32_t tpr_abi_version(void);
  * split count, 0 = automatic), "lanes" (threads per row in the row kernel,
  * 0 = automatic), "general" (1 = always use the generic strided kernel),
  * "topk_fallback" (1 = always take top-k's exact multi-pass path), "tx" (64 or 256:
- * threads across the contiguous dim in the column kernel, 0 = automatic).
+ * threads across the contiguous dim in the column kernel, 0 = automatic),
+ * "topk_variant" (1 = 8 waves/SIMD without prefetch, 2 = 7 waves/SIMD with a
+ * one-slice prefetch, 0 = automatic).
  * Process-wide; not synchronised with concurrent launches.  Returns
  * TPR_ERR_INVALID_ARG for an unknown key.  No reference counterpart. */
 int tpr_debug_set(const char* key, int64_t value);

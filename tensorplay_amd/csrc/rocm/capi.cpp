@@ -66,6 +66,7 @@ int tpr_debug_set(const char* key, int64_t value) {
     else if (!std::strcmp(key, "general")) k.general = value;
     else if (!std::strcmp(key, "topk_fallback")) k.topk_fallback = value;
     else if (!std::strcmp(key, "tx")) k.tx = value;
+    else if (!std::strcmp(key, "topk_variant")) k.topk_variant = value;
     else return tpr::fail(TPR_ERR_INVALID_ARG, std::string("tpr_debug_set: unknown key ") + key);
     return TPR_OK;
 }

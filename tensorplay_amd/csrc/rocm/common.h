@@ -29,6 +29,7 @@ struct DebugKnobs {
     int64_t general = 0;
     int64_t topk_fallback = 0;
     int64_t tx = 0;
+    int64_t topk_variant = 0;
 };
 DebugKnobs& knobs();
 

@@ -7,34 +7,38 @@
 // 64-bit "composite" key  (key << 32) | (0xffffffff - index)  so every element
 // of a row has a distinct composite and larger composite == ranks earlier.
 //
-// Pass 1 (k_topk_seg): one 512-thread workgroup per (row, segment); rows are
-// cut into segments so that the grid holds several workgroups per CU (memory
-// latency is hidden by occupancy, not by register double-buffering).  Each
-// workgroup streams its segment once from HBM in chunks of 512 x 16 floats
-// (four 128-bit loads per thread) and keeps the exact top k of the segment:
-//  1. The first chunk gives a lower bound T on the segment's k-th key: each
-//     wave takes the r-th largest of its 64 per-lane maxima (r = ceil(k/8)); the
-//     minimum over the 8 waves has >= 8*r >= k distinct elements at or above it.
-//  2. Every element with key >= T is appended to an LDS candidate list
-//     (wave-aggregated slot reservation: one LDS atomic per wave per chunk).
-//  3. When the list grows past max(2k, 256) it is compacted to its exact top k
-//     (rank selection below) and T rises past the k-th key kept.
-//  4. The exact top k of the list is ranked; with one segment per row it is the
-//     answer, otherwise its k composites go to the workspace.
-// Pass 2 (k_topk_merge, only when rows are split): per row, rank the
-// segments' candidates and write the final top k.
-// Rank selection: rank(c) = #{candidates with a larger composite}; composites
-// are distinct, so the ranks 0..k-1 are a permutation and give the sorted
-// output directly.  The work is split over all threads (partial counts summed
-// in LDS).
-// If the list would overflow (adversarial rows: all-equal values, long runs of
-// the threshold value), the workgroup switches to an exact multi-pass path over
-// its segment: 4-pass 8-bit radix select in global memory finds the k-th key,
-// then an index-ordered gather takes every larger key plus the lowest-index
-// elements equal to it.
+// A row is cut into segments so the grid holds several workgroups per CU; each
+// 512-thread workgroup keeps the exact top k of its segment.  With one segment
+// per row it writes the answer, otherwise k_topk_merge ranks the segments'
+// winners.  The segment kernel is a threshold filter over one HBM pass:
+//   * Bound.  In a first slice every wave takes the r-th largest of its 64
+//     per-lane maxima (r = ceil(k/8)); the minimum T0 over the 8 waves has
+//     >= 8r >= k distinct elements at or above it, so no element below T0 can
+//     be in the top k.
+//   * Filter.  Elements with key >= T are appended to an LDS candidate list.
+//   * Compaction.  A long list is cut with a 256-bin histogram of
+//     (key - T) >> shift spanning [T, max key]: the lower edge of the bin where
+//     the count from the top reaches k has >= k candidates at or above it and
+//     becomes the new T.  Cost O(list), no sorting.
+//   * Ranking.  rank(c) = #{candidates with a larger composite}; composites are
+//     distinct, so ranks 0..k-1 are a permutation and give the sorted output.
+//   * Exact path.  If a list would overflow (adversarial rows: all-equal values,
+//     long runs of one value) the workgroup switches to a 4-pass 8-bit radix
+//     select over its segment in global memory, then an index-ordered gather
+//     takes every larger key plus the lowest-index elements equal to the k-th.
+// Two variants of the segment kernel:
+//   k_topk_wave  (k <= 128, segments >= 8192): every wave streams its own
+//     1024-element slices (w, w+8, ...) into a wave-private list with no
+//     workgroup barrier in the loop, so one wave's filtering overlaps the other
+//     waves' loads.  Waves share a monotone threshold through an LDS atomicMax;
+//     a published value always has >= k candidates at or above it in the
+//     publishing wave's list, so it bounds every wave.
+//   k_topk_block (any k <= 1024, any segment): workgroup-wide chunks with one
+//     shared list; used for large k and short rows.
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <string>
 
 #include "common.h"
@@ -44,12 +48,18 @@ namespace {
 
 constexpr int kT = 512;          // threads per segment workgroup
 constexpr int kW = kT / 64;      // waves per workgroup
-constexpr int kV = 4;            // float4 loads per thread per chunk
-constexpr int kCH = kT * 4 * kV; // elements per chunk (8192)
-constexpr int kB = 2048;         // candidate list capacity
+constexpr int kV = 4;            // float4 loads per thread per chunk (block kernel)
+constexpr int kCH = kT * 4 * kV; // elements per block-kernel chunk (8192)
+constexpr int kB = 2048;         // block candidate list capacity
 constexpr int kKMax = 1024;      // largest k
 constexpr int kMergeT = 256;     // merge workgroup
 constexpr int kMergeMax = 4096;  // candidates a merge workgroup ranks (nseg * k)
+
+constexpr int kWaveK = 128;                   // largest k of the wave kernel
+constexpr int kWB = 256;                      // per-wave list capacity
+constexpr int kWaveCompact = 192;             // per-wave list size that triggers compaction
+constexpr int kSlice = 64 * 16;               // elements per wave slice (4 float4 per lane)
+constexpr int kWaveMinSeg = kW * kSlice;      // every wave has a full first slice (8192)
 
 __device__ __forceinline__ uint32_t f2key(float f, int largest) {
     uint32_t u = __float_as_uint(f);
@@ -57,6 +67,20 @@ __device__ __forceinline__ uint32_t f2key(float f, int largest) {
     u = (u == 0x80000000u) ? 0u : u;                          // -0 -> +0
     uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return largest ? k : ~k;  // valid keys are never 0: 0 marks "no element"
+}
+
+// Inverse of f2key.  Exact except for the two canonicalised cases (-0.0 comes
+// back as +0.0, any NaN as 0x7fc00000); callers re-read the input for those.
+__device__ __forceinline__ uint32_t key2bits(uint32_t key, int largest) {
+    const uint32_t k = largest ? key : ~key;
+    return (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+}
+
+// Output value of a selected element: from its key, or from the input row when
+// the key cannot tell (+-0.0, NaN payloads).
+__device__ __forceinline__ float selected_value(const float* p, uint32_t key, uint32_t idx, int largest) {
+    const uint32_t u = key2bits(key, largest);
+    return (u == 0u || u == 0x7fc00000u) ? p[idx] : __uint_as_float(u);
 }
 
 __device__ __forceinline__ unsigned long long comp_key(uint32_t key, uint32_t idx) {
@@ -67,12 +91,10 @@ __device__ __forceinline__ uint32_t comp_index(unsigned long long c) {
     return 0xffffffffu - (uint32_t)(c & 0xffffffffull);
 }
 
-// DPP wave reductions from the device library (no LDS round trips).
+// DPP wave reduction from the device library (no LDS round trips).
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) { return __ockl_wfred_max_u32(v); }
 
-__device__ __forceinline__ unsigned long long lanemask_lt() {
-    return (1ull << __lane_id()) - 1ull;
-}
+__device__ __forceinline__ unsigned long long lanemask_lt() { return (1ull << __lane_id()) - 1ull; }
 
 struct TopkArgs {
     const float* in;
@@ -83,16 +105,14 @@ struct TopkArgs {
     int largest;
     int force_fallback;
     int nseg;
-    int seg_len;                 // multiple of kCH
-    unsigned long long* part;    // [rows][nseg][k] composites when nseg > 1
+    int seg_len;
+    unsigned long long* part;  // [rows][nseg][k] composites when nseg > 1
     float* out_v;
     long long* out_i;
 };
 
-// Two candidate lists (ping-pong for compaction).  The final ranking reuses the
-// idle list for its rank counters and sorted output.
-struct TopkShared {
-    unsigned long long list[2][kB];
+// Small shared state of the workgroup-level helpers.
+struct BlockScratch {
     uint32_t wave_val[kW];
     int wave_cnt[kW];
     uint32_t hist[256];
@@ -100,13 +120,28 @@ struct TopkShared {
     int count2;
     int over;
     uint32_t thresh;
-    uint32_t hi;
+    uint32_t tshared;
     int digit;
     int kk;
     int eq_taken;
 };
-static_assert(sizeof(int) * kB + sizeof(unsigned long long) * kKMax <= sizeof(unsigned long long) * kB,
-              "rank + sel must fit in one idle list");
+
+// r-th largest of the wave's per-lane maxima of `key` (0 if fewer than r lanes
+// hold valid keys).
+__device__ __forceinline__ uint32_t wave_rth_of_lane_max(const uint32_t* key, int nkeys, int r) {
+    const int lane = __lane_id();
+    uint32_t m = 0;
+    for (int q = 0; q < nkeys; ++q) m = max(m, key[q]);
+    uint32_t rth = 0;
+    for (int i = 0; i < r; ++i) {
+        const uint32_t wm = wave_max_u32(m);
+        rth = wm;
+        if (wm == 0) break;
+        const unsigned long long bal = __ballot(m == wm);
+        if (lane == __ffsll((long long)bal) - 1) m = 0;
+    }
+    return rth;
+}
 
 // Exact top-k of cand[0..m) into sel[0..k) (sorted).  m >= k.  Candidate i is
 // counted by `groups` threads, each over a slice of the list; partial counts
@@ -147,17 +182,383 @@ __device__ void rank_select(const unsigned long long* cand, int* rank, unsigned 
     __syncthreads();
 }
 
+// Threshold from a 256-bin histogram whose bins span [T, T + 256 << shift):
+// lane l of one wave owns bins 4l..4l+3.  Returns the lower edge of the bin
+// where the count from the top first reaches k (valid in every lane).
+__device__ __forceinline__ uint32_t hist_threshold(const uint32_t* hist, int k, uint32_t T, int shift) {
+    const int lane = __lane_id();
+    const uint32_t h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2], h3 = hist[4 * lane + 3];
+    const int own = (int)(h0 + h1 + h2 + h3);
+    int suf = own;  // inclusive suffix sum over lanes >= lane
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int t = __shfl_down(suf, d, 64);
+        if (lane + d < 64) suf += t;
+    }
+    const unsigned long long ok = __ballot(suf >= k);
+    const int L = 63 - __clzll((long long)ok);  // highest lane whose suffix reaches k
+    uint32_t tn = 0;
+    if (lane == L) {
+        int cum = suf - own;
+        const uint32_t hs[4] = {h0, h1, h2, h3};
+        int b = 3;
+        for (; b > 0; --b) {
+            if (cum + (int)hs[b] >= k) break;
+            cum += (int)hs[b];
+        }
+        tn = T + ((uint32_t)(4 * lane + b) << shift);
+    }
+    return __shfl(tn, L, 64);
+}
+
+__device__ __forceinline__ int hist_shift(uint32_t hi, uint32_t T) {
+    const uint32_t range = hi - T;
+    return (range < 256u) ? 0 : (32 - __clz((int)range)) - 8;
+}
+
+// Workgroup-level compaction: raises T using src[0..m) (all keys >= T) and moves
+// the survivors to dst.  Returns the new T; bs.count2 = survivors.
+template <int NT>
+__device__ uint32_t block_compact(BlockScratch& bs, const unsigned long long* src, unsigned long long* dst, int m,
+                                  int k, uint32_t T) {
+    const int tid = threadIdx.x;
+    const int lane = __lane_id();
+    const int w = tid / 64;
+    uint32_t mx = 0;
+    for (int i = tid; i < m; i += NT) mx = max(mx, (uint32_t)(src[i] >> 32));
+    mx = wave_max_u32(mx);
+    if (lane == 0) bs.wave_val[w] = mx;
+    if (tid < 256) bs.hist[tid] = 0;
+    if (tid == 0) bs.count2 = 0;
+    __syncthreads();
+    uint32_t hi = 0;
+    for (int i = 0; i < NT / 64; ++i) hi = max(hi, bs.wave_val[i]);
+    const int shift = hist_shift(hi, T);
+    for (int i = tid; i < m; i += NT) atomicAdd(&bs.hist[((uint32_t)(src[i] >> 32) - T) >> shift], 1u);
+    __syncthreads();
+    if (w == 0) {
+        const uint32_t tn = hist_threshold(bs.hist, k, T, shift);
+        if (lane == 0) bs.thresh = tn;
+    }
+    __syncthreads();
+    const uint32_t Tn = bs.thresh;
+    for (int i0 = 0; i0 < m; i0 += NT) {
+        const int i = i0 + tid;
+        const unsigned long long c = (i < m) ? src[i] : 0ull;
+        const bool keep = (i < m) && (uint32_t)(c >> 32) >= Tn;
+        const unsigned long long bal = __ballot(keep);
+        int base = 0;
+        if (lane == 0 && bal) base = atomicAdd(&bs.count2, __popcll(bal));
+        base = __shfl(base, 0, 64);
+        if (keep) dst[base + __popcll(bal & lanemask_lt())] = c;
+    }
+    __syncthreads();
+    return Tn;
+}
+
+// Wave-level compaction of list[0..m) in place (all keys >= T); m is updated.
+__device__ uint32_t wave_compact(unsigned long long* list, uint32_t* hist, int& m, int k, uint32_t T) {
+    const int lane = __lane_id();
+    uint32_t mx = 0;
+    for (int i = lane; i < m; i += 64) mx = max(mx, (uint32_t)(list[i] >> 32));
+    mx = wave_max_u32(mx);
+    const int shift = hist_shift(mx, T);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) hist[4 * lane + b] = 0;
+    __builtin_amdgcn_wave_barrier();
+    for (int i = lane; i < m; i += 64) atomicAdd(&hist[((uint32_t)(list[i] >> 32) - T) >> shift], 1u);
+    __builtin_amdgcn_wave_barrier();
+    const uint32_t tn = hist_threshold(hist, k, T, shift);
+    // a write position never passes the read position, so in place is safe
+    int out = 0;
+    for (int i0 = 0; i0 < m; i0 += 64) {
+        const int i = i0 + lane;
+        const unsigned long long c = (i < m) ? list[i] : 0ull;
+        const bool keep = (i < m) && (uint32_t)(c >> 32) >= tn;
+        const unsigned long long b = __ballot(keep);
+        __builtin_amdgcn_wave_barrier();
+        if (keep) list[out + __popcll(b & lanemask_lt())] = c;
+        out += __popcll(b);
+        __builtin_amdgcn_wave_barrier();
+    }
+    m = out;
+    return tn;
+}
+
+// Exact multi-pass path over p[lo, hi) (any data): leaves the k selected
+// composites in cand[0..k) (unordered).  hi - lo >= k.
+template <int NT>
+__device__ void exact_select(BlockScratch& bs, unsigned long long* cand, const float* p, int lo, int hi, int k,
+                             int largest) {
+    constexpr int NW = NT / 64;
+    const int tid = threadIdx.x;
+    const int lane = __lane_id();
+    const int w = tid / 64;
+    uint32_t prefix = 0, pmask = 0;
+    int kk = k;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        if (tid < 256) bs.hist[tid] = 0;
+        __syncthreads();
+        for (int e = lo + tid; e < hi; e += NT) {
+            const uint32_t key = f2key(p[e], largest);
+            if ((key & pmask) == prefix) atomicAdd(&bs.hist[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int cum = 0, d = 0;
+            for (int b = 255; b >= 0; --b) {
+                const int h = (int)bs.hist[b];
+                if (cum + h >= kk) { d = b; break; }
+                cum += h;
+            }
+            bs.digit = d;
+            bs.kk = kk - cum;
+        }
+        __syncthreads();
+        prefix |= (uint32_t)bs.digit << shift;
+        pmask |= 0xffu << shift;
+        kk = bs.kk;
+        __syncthreads();
+    }
+    const uint32_t T = prefix;  // exact k-th key; kk = how many keys == T to take
+    if (tid == 0) { bs.count = 0; bs.eq_taken = 0; }
+    __syncthreads();
+    for (int base = lo; base < hi; base += NT) {
+        const int e = base + tid;
+        const uint32_t key = (e < hi) ? f2key(p[e], largest) : 0u;
+        const bool gt = (e < hi) && key > T;
+        const bool eq = (e < hi) && key == T;
+        if (gt) cand[atomicAdd(&bs.count, 1)] = comp_key(key, (uint32_t)e);
+        const unsigned long long bal = __ballot(eq);
+        const int before = __popcll(bal & lanemask_lt());
+        if (lane == 0) bs.wave_cnt[w] = __popcll(bal);
+        __syncthreads();
+        int wbase = bs.eq_taken;
+        int total = 0;
+        for (int i = 0; i < NW; ++i) {
+            if (i < w) wbase += bs.wave_cnt[i];
+            total += bs.wave_cnt[i];
+        }
+        if (eq && wbase + before < kk) cand[atomicAdd(&bs.count, 1)] = comp_key(key, (uint32_t)e);
+        __syncthreads();
+        if (tid == 0) bs.eq_taken += total;
+        __syncthreads();
+    }
+    __syncthreads();
+}
+
+// Writes the ranked top k of one segment: the final values/indices when the row
+// is not split, else the k composites for the merge pass.
+__device__ __forceinline__ void write_segment(const TopkArgs& a, long long row, int seg, const float* p,
+                                              const unsigned long long* sel, int k) {
+    if (a.nseg == 1) {
+        for (int i = threadIdx.x; i < k; i += blockDim.x) {
+            const uint32_t idx = comp_index(sel[i]);
+            a.out_v[row * k + i] = selected_value(p, (uint32_t)(sel[i] >> 32), idx, a.largest);
+            a.out_i[row * k + i] = (long long)idx;
+        }
+    } else {
+        unsigned long long* dst = a.part + ((long long)row * a.nseg + seg) * k;
+        for (int i = threadIdx.x; i < k; i += blockDim.x) dst[i] = sel[i];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Wave-independent segment kernel.
+// ---------------------------------------------------------------------------
+struct WaveShared {
+    unsigned long long wl[kW][kWB];    // per-wave candidate lists (16 KiB)
+    union {
+        uint32_t hist[kW][256];        // per-wave histograms while streaming (8 KiB)
+        unsigned long long un[kB];     // gathered list afterwards (16 KiB)
+    };
+    BlockScratch bs;
+};
+static_assert(kW * kWB == kB, "the per-wave lists double as a block-sized scratch list");
+static_assert(sizeof(int) * kB + sizeof(unsigned long long) * kKMax <= sizeof(unsigned long long) * kB,
+              "rank + sel must fit in one idle list");
+
+template <bool VEC, int SV>
+__device__ __forceinline__ void load_slice(float4 (&cur)[SV], const float* p, int base, int hi) {
+    const int lane = __lane_id();
+    if (VEC && base + 256 * SV <= hi) {
+#pragma unroll
+        for (int j = 0; j < SV; ++j) cur[j] = *reinterpret_cast<const float4*>(p + base + 4 * (j * 64 + lane));
+    } else {
+#pragma unroll
+        for (int j = 0; j < SV; ++j) {
+            const int e = base + 4 * (j * 64 + lane);
+            float v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int eq = e + q;
+                const float x = p[eq < hi ? eq : hi - 1];
+                v[q] = (eq < hi) ? x : 0.0f;
+            }
+            cur[j] = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+}
+
+template <int SV>
+__device__ __forceinline__ void slice_keys(const float4 (&cur)[SV], int base, int hi, int largest,
+                                           uint32_t (&key)[4 * SV]) {
+    const int lane = __lane_id();
+#pragma unroll
+    for (int j = 0; j < SV; ++j) {
+        const int e = base + 4 * (j * 64 + lane);
+        key[4 * j + 0] = (e + 0 < hi) ? f2key(cur[j].x, largest) : 0u;
+        key[4 * j + 1] = (e + 1 < hi) ? f2key(cur[j].y, largest) : 0u;
+        key[4 * j + 2] = (e + 2 < hi) ? f2key(cur[j].z, largest) : 0u;
+        key[4 * j + 3] = (e + 3 < hi) ? f2key(cur[j].w, largest) : 0u;
+    }
+}
+
+template <bool VEC, int SV, int OCC, bool PF>
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(OCC, 8))) void k_topk_wave(TopkArgs a) {
+    constexpr int kSl = 256 * SV;  // elements per wave slice
+    __shared__ WaveShared sh;
+    BlockScratch& bs = sh.bs;
+    const int tid = threadIdx.x;
+    const int lane = __lane_id();
+    const int w = tid / 64;
+    const long long row = blockIdx.x / a.nseg;
+    const int seg = blockIdx.x % a.nseg;
+    const float* p = a.in + row * a.row_stride;
+    const int k = a.k;
+    const int largest = a.largest;
+    const int lo = seg * a.seg_len;
+    const int hi = min(a.cols, lo + a.seg_len);
+    const int nsl = (hi - lo + kSl - 1) / kSl;
+    const int r = (k + kW - 1) / kW;
+    unsigned long long* list = sh.wl[w];
+    uint32_t* hist = sh.hist[w];
+
+    if (tid == 0) {
+        bs.tshared = 1;
+        bs.count = 0;
+        bs.over = a.force_fallback;
+    }
+
+    // first slice of every wave gives the workgroup bound T0
+    float4 cur[SV];
+    uint32_t key[4 * SV];
+    load_slice<VEC, SV>(cur, p, lo + w * kSl, hi);
+    slice_keys(cur, lo + w * kSl, hi, largest, key);
+    // prefetch: the next slice is loaded into `cur` as soon as the current one
+    // has become keys, so its latency overlaps the work on the current slice
+    if (PF && w + kW < nsl) load_slice<VEC, SV>(cur, p, lo + (w + kW) * kSl, hi);
+    const uint32_t rth = wave_rth_of_lane_max(key, 4 * SV, r);
+    if (lane == 0) bs.wave_val[w] = rth;
+    __syncthreads();
+    uint32_t T = 0xffffffffu;
+#pragma unroll
+    for (int i = 0; i < kW; ++i) T = min(T, bs.wave_val[i]);
+    T = max(T, 1u);
+    bool over = bs.over != 0;
+    int cnt = 0;  // this wave's list length (wave-uniform)
+
+    // streaming loop: no workgroup barriers
+    for (int c = w; c < nsl && !over; c += kW) {
+        const int base = lo + c * kSl;
+        if (c != w) {
+            if (!PF) load_slice<VEC, SV>(cur, p, base, hi);
+            slice_keys(cur, base, hi, largest, key);
+            if (PF && c + kW < nsl) load_slice<VEC, SV>(cur, p, lo + (c + kW) * kSl, hi);
+        }
+        T = max(T, __atomic_load_n(&bs.tshared, __ATOMIC_RELAXED));
+        int total = 0;
+#pragma unroll
+        for (int q = 0; q < 4 * SV; ++q) total += __popcll(__ballot(key[q] >= T));
+        while (total > 0 && cnt + total > kWB) {  // no room: raise T from the list first
+            const uint32_t tn = (cnt > k) ? wave_compact(list, hist, cnt, k, T) : T;
+            if (tn <= T) { over = true; break; }
+            if (lane == 0) atomicMax(&bs.tshared, tn);
+            T = tn;
+            total = 0;
+#pragma unroll
+            for (int q = 0; q < 4 * SV; ++q) total += __popcll(__ballot(key[q] >= T));
+        }
+        if (over) break;
+        if (total) {
+            const unsigned long long lt = lanemask_lt();
+            int pos = cnt;
+#pragma unroll
+            for (int q = 0; q < 4 * SV; ++q) {
+                const bool pass = key[q] >= T;
+                const unsigned long long b = __ballot(pass);
+                if (pass)
+                    list[pos + __popcll(b & lt)] =
+                        comp_key(key[q], (uint32_t)(base + 4 * ((q >> 2) * 64 + lane) + (q & 3)));
+                pos += __popcll(b);
+            }
+            cnt = pos;
+        }
+        if (cnt > kWaveCompact) {
+            const uint32_t tn = wave_compact(list, hist, cnt, k, T);
+            if (tn > T) {
+                if (lane == 0) atomicMax(&bs.tshared, tn);
+                T = tn;
+            }
+        }
+        if (__atomic_load_n(&bs.over, __ATOMIC_RELAXED)) over = true;
+    }
+    if (over && lane == 0) __atomic_store_n(&bs.over, 1, __ATOMIC_RELAXED);
+    __syncthreads();
+
+    // gather: each wave keeps the entries at or above the final shared threshold
+    const bool any_over = bs.over != 0;
+    const uint32_t Tf = max(T, bs.tshared);
+    __syncthreads();  // the histogram area is reused as the gathered list below
+    if (!any_over) {
+        for (int i0 = 0; i0 < cnt; i0 += 64) {
+            const int i = i0 + lane;
+            const unsigned long long c = (i < cnt) ? list[i] : 0ull;
+            const bool keep = (i < cnt) && (uint32_t)(c >> 32) >= Tf;
+            const unsigned long long b = __ballot(keep);
+            int gbase = 0;
+            if (lane == 0 && b) gbase = atomicAdd(&bs.count, __popcll(b));
+            gbase = __shfl(gbase, 0, 64);
+            if (keep) sh.un[gbase + __popcll(b & lanemask_lt())] = c;  // sum of lists <= kW * kWB == kB
+        }
+    }
+    __syncthreads();
+    unsigned long long* cand = sh.un;
+    unsigned long long* other = &sh.wl[0][0];
+    int m = bs.count;
+    if (any_over) {
+        exact_select<kT>(bs, cand, p, lo, hi, k, largest);
+        m = k;
+    } else if (m > max(2 * k, 256)) {
+        block_compact<kT>(bs, cand, other, m, k, Tf);
+        m = bs.count2;
+        unsigned long long* t = cand;
+        cand = other;
+        other = t;
+    }
+    int* rank = reinterpret_cast<int*>(other);
+    unsigned long long* sel = other + kB / 2;
+    rank_select<kT>(cand, rank, sel, m, k);
+    write_segment(a, row, seg, p, sel, k);
+}
+
+// ---------------------------------------------------------------------------
+// Workgroup-level segment kernel (large k, short rows).
+// ---------------------------------------------------------------------------
+struct BlockShared {
+    unsigned long long list[2][kB];
+    BlockScratch bs;
+};
+
 // Loads one chunk (kV float4 per thread).  The bounds test is uniform across the
 // workgroup, so a full chunk is kV unconditional 128-bit loads; the tail chunk
-// uses clamped (always valid) scalar addresses and a select, so no divergent
-// branch sits between a load and its use.
+// uses clamped (always valid) scalar addresses and a select.
 template <bool VEC>
 __device__ __forceinline__ void load_chunk(float4 (&dst)[kV], const float* p, int cbase, int n) {
     const int tid = threadIdx.x;
     if (VEC && cbase + kCH <= n) {
 #pragma unroll
-        for (int j = 0; j < kV; ++j)
-            dst[j] = *reinterpret_cast<const float4*>(p + cbase + 4 * (j * kT + tid));
+        for (int j = 0; j < kV; ++j) dst[j] = *reinterpret_cast<const float4*>(p + cbase + 4 * (j * kT + tid));
     } else {
 #pragma unroll
         for (int j = 0; j < kV; ++j) {
@@ -174,134 +575,10 @@ __device__ __forceinline__ void load_chunk(float4 (&dst)[kV], const float* p, in
     }
 }
 
-// Exact multi-pass path over p[lo, hi) (any data).  Leaves the k selected
-// composites in sh.list[0][0..k) (unordered).  hi - lo >= k.
-__device__ void exact_select(TopkShared& sh, const float* p, int lo, int hi, int k, int largest) {
-    const int tid = threadIdx.x;
-    const int lane = __lane_id();
-    const int w = tid / 64;
-    unsigned long long* cand = sh.list[0];
-    uint32_t prefix = 0, pmask = 0;
-    int kk = k;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        if (tid < 256) sh.hist[tid] = 0;
-        __syncthreads();
-        for (int e = lo + tid; e < hi; e += kT) {
-            const uint32_t key = f2key(p[e], largest);
-            if ((key & pmask) == prefix) atomicAdd(&sh.hist[(key >> shift) & 255u], 1u);
-        }
-        __syncthreads();
-        if (tid == 0) {
-            int cum = 0, d = 0;
-            for (int b = 255; b >= 0; --b) {
-                const int h = (int)sh.hist[b];
-                if (cum + h >= kk) { d = b; break; }
-                cum += h;
-            }
-            sh.digit = d;
-            sh.kk = kk - cum;
-        }
-        __syncthreads();
-        prefix |= (uint32_t)sh.digit << shift;
-        pmask |= 0xffu << shift;
-        kk = sh.kk;
-        __syncthreads();
-    }
-    const uint32_t T = prefix;  // exact k-th key; kk = how many keys == T to take
-    if (tid == 0) { sh.count = 0; sh.eq_taken = 0; }
-    __syncthreads();
-    for (int base = lo; base < hi; base += kT) {
-        const int e = base + tid;
-        const uint32_t key = (e < hi) ? f2key(p[e], largest) : 0u;
-        const bool gt = (e < hi) && key > T;
-        const bool eq = (e < hi) && key == T;
-        if (gt) cand[atomicAdd(&sh.count, 1)] = comp_key(key, (uint32_t)e);
-        const unsigned long long bal = __ballot(eq);
-        const int before = __popcll(bal & lanemask_lt());
-        if (lane == 0) sh.wave_cnt[w] = __popcll(bal);
-        __syncthreads();
-        int wbase = sh.eq_taken;
-        int total = 0;
-        for (int i = 0; i < kW; ++i) {
-            if (i < w) wbase += sh.wave_cnt[i];
-            total += sh.wave_cnt[i];
-        }
-        if (eq && wbase + before < kk) cand[atomicAdd(&sh.count, 1)] = comp_key(key, (uint32_t)e);
-        __syncthreads();
-        if (tid == 0) sh.eq_taken += total;
-        __syncthreads();
-    }
-    __syncthreads();
-}
-
-// Raises the bound T using the candidate list src[0..m) (all keys >= T) and
-// moves the survivors to dst.  A 256-bin histogram of (key - T) >> shift, with
-// shift chosen so the bins span [T, max key], locates the bin where the count
-// from the top first reaches k; its lower edge T' has >= k candidates at or
-// above it, so it is a valid bound.  Returns T'; sh.count2 = survivors.
-__device__ uint32_t compact(TopkShared& sh, const unsigned long long* src, unsigned long long* dst, int m,
-                            int k, uint32_t T) {
-    const int tid = threadIdx.x;
-    const int lane = __lane_id();
-    const int w = tid / 64;
-    uint32_t mx = 0;
-    for (int i = tid; i < m; i += kT) mx = max(mx, (uint32_t)(src[i] >> 32));
-    mx = wave_max_u32(mx);
-    if (lane == 0) sh.wave_val[w] = mx;
-    if (tid < 256) sh.hist[tid] = 0;
-    if (tid == 0) sh.count2 = 0;
-    __syncthreads();
-    uint32_t hi = 0;
-#pragma unroll
-    for (int i = 0; i < kW; ++i) hi = max(hi, sh.wave_val[i]);
-    const uint32_t range = hi - T;
-    const int shift = (range < 256u) ? 0 : (32 - __clz((int)range)) - 8;
-    for (int i = tid; i < m; i += kT) atomicAdd(&sh.hist[((uint32_t)(src[i] >> 32) - T) >> shift], 1u);
-    __syncthreads();
-    if (w == 0) {
-        // lane l owns bins 4l..4l+3; suffix sums from the top bin downwards
-        const uint32_t h0 = sh.hist[4 * lane], h1 = sh.hist[4 * lane + 1];
-        const uint32_t h2 = sh.hist[4 * lane + 2], h3 = sh.hist[4 * lane + 3];
-        const int own = (int)(h0 + h1 + h2 + h3);
-        // inclusive suffix sum over lanes >= lane
-        int suf = own;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int t = __shfl_down(suf, d, 64);
-            if (lane + d < 64) suf += t;
-        }
-        const unsigned long long ok = __ballot(suf >= k);
-        const int L = 63 - __clzll((long long)ok);  // highest lane whose suffix reaches k
-        if (lane == L) {
-            int cum = suf - own;  // count strictly above this lane's bins
-            int b = 3;
-            const uint32_t hs[4] = {h0, h1, h2, h3};
-            for (; b > 0; --b) {
-                if (cum + (int)hs[b] >= k) break;
-                cum += (int)hs[b];
-            }
-            sh.thresh = T + ((uint32_t)(4 * lane + b) << shift);
-        }
-    }
-    __syncthreads();
-    const uint32_t Tn = sh.thresh;
-    for (int i0 = 0; i0 < m; i0 += kT) {
-        const int i = i0 + tid;
-        const unsigned long long c = (i < m) ? src[i] : 0ull;
-        const bool keep = (i < m) && (uint32_t)(c >> 32) >= Tn;
-        const unsigned long long bal = __ballot(keep);
-        int base = 0;
-        if (lane == 0 && bal) base = atomicAdd(&sh.count2, __popcll(bal));
-        base = __shfl(base, 0, 64);
-        if (keep) dst[base + __popcll(bal & lanemask_lt())] = c;
-    }
-    __syncthreads();
-    return Tn;
-}
-
 template <bool VEC>
-__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_topk_seg(TopkArgs a) {
-    __shared__ TopkShared sh;
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_topk_block(TopkArgs a) {
+    __shared__ BlockShared sh;
+    BlockScratch& bs = sh.bs;
     const int tid = threadIdx.x;
     const int lane = __lane_id();
     const int w = tid / 64;
@@ -312,12 +589,11 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     const int largest = a.largest;
     const int lo = seg * a.seg_len;
     const int hi = min(a.cols, lo + a.seg_len);
-    const int n = hi;  // loads are bounded by the segment end
     const int nchunks = (hi - lo + kCH - 1) / kCH;
-    const int r = (k + kW - 1) / kW;                 // per-wave rank for the bound
-    const int compact_at = max(2 * k, 256);          // list size that triggers compaction
+    const int r = (k + kW - 1) / kW;
+    const int compact_at = max(2 * k, 256);
 
-    if (tid == 0) { sh.count = 0; sh.over = 0; }
+    if (tid == 0) { bs.count = 0; bs.over = 0; }
     __syncthreads();
 
     int cur_list = 0;
@@ -326,78 +602,66 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     for (int c = 0; c < nchunks && !over; ++c) {
         const int cbase = lo + c * kCH;
         float4 cur[kV];
-        load_chunk<VEC>(cur, p, cbase, n);
+        load_chunk<VEC>(cur, p, cbase, hi);
         uint32_t key[4 * kV];
 #pragma unroll
         for (int j = 0; j < kV; ++j) {
             const int e = cbase + 4 * (j * kT + tid);
-            key[4 * j + 0] = (e + 0 < n) ? f2key(cur[j].x, largest) : 0u;
-            key[4 * j + 1] = (e + 1 < n) ? f2key(cur[j].y, largest) : 0u;
-            key[4 * j + 2] = (e + 2 < n) ? f2key(cur[j].z, largest) : 0u;
-            key[4 * j + 3] = (e + 3 < n) ? f2key(cur[j].w, largest) : 0u;
+            key[4 * j + 0] = (e + 0 < hi) ? f2key(cur[j].x, largest) : 0u;
+            key[4 * j + 1] = (e + 1 < hi) ? f2key(cur[j].y, largest) : 0u;
+            key[4 * j + 2] = (e + 2 < hi) ? f2key(cur[j].z, largest) : 0u;
+            key[4 * j + 3] = (e + 3 < hi) ? f2key(cur[j].w, largest) : 0u;
         }
         if (c == 0) {
-            uint32_t m = 0;
-#pragma unroll
-            for (int q = 0; q < 4 * kV; ++q) m = max(m, key[q]);
-            uint32_t rth = 0;
-            for (int i = 0; i < r; ++i) {
-                const uint32_t wm = wave_max_u32(m);
-                rth = wm;
-                if (wm == 0) break;
-                const unsigned long long bal = __ballot(m == wm);
-                if (lane == __ffsll((long long)bal) - 1) m = 0;
-            }
-            if (lane == 0) sh.wave_val[w] = rth;
+            const uint32_t rth = wave_rth_of_lane_max(key, 4 * kV, r);
+            if (lane == 0) bs.wave_val[w] = rth;
             __syncthreads();
             uint32_t tb = 0xffffffffu;
 #pragma unroll
-            for (int i = 0; i < kW; ++i) tb = min(tb, sh.wave_val[i]);
+            for (int i = 0; i < kW; ++i) tb = min(tb, bs.wave_val[i]);
             T = max(T, tb);
         }
         // filter: per-slot ballots give each passing element its wave offset
         unsigned long long* cand = sh.list[cur_list];
-        unsigned long long bal[4 * kV];
         int total = 0;
 #pragma unroll
-        for (int q = 0; q < 4 * kV; ++q) {
-            bal[q] = __ballot(key[q] >= T);
-            total += __popcll(bal[q]);
-        }
+        for (int q = 0; q < 4 * kV; ++q) total += __popcll(__ballot(key[q] >= T));
         if (total) {
             int base = 0;
-            if (lane == 0) base = atomicAdd(&sh.count, total);
+            if (lane == 0) base = atomicAdd(&bs.count, total);
             base = __shfl(base, 0, 64);
             const unsigned long long lt = lanemask_lt();
 #pragma unroll
             for (int q = 0; q < 4 * kV; ++q) {
-                if (bal[q] & (1ull << lane)) {
-                    const int pos = base + __popcll(bal[q] & lt);
+                const bool pass = key[q] >= T;
+                const unsigned long long b = __ballot(pass);
+                if (pass) {
+                    const int pos = base + __popcll(b & lt);
                     const int e = cbase + 4 * ((q >> 2) * kT + tid) + (q & 3);
                     if (pos < kB) cand[pos] = comp_key(key[q], (uint32_t)e);
-                    else sh.over = 1;
+                    else bs.over = 1;
                 }
-                base += __popcll(bal[q]);
+                base += __popcll(b);
             }
         }
         __syncthreads();
         // read the shared verdicts, then fence them off from the next chunk's atomics
-        over = sh.over != 0;
-        const int m = sh.count;
+        over = bs.over != 0;
+        const int m = bs.count;
         __syncthreads();
         if (over) break;
         if (m > compact_at) {
-            T = compact(sh, sh.list[cur_list], sh.list[cur_list ^ 1], m, k, T);
+            T = block_compact<kT>(bs, sh.list[cur_list], sh.list[cur_list ^ 1], m, k, T);
             cur_list ^= 1;
-            if (tid == 0) sh.count = sh.count2;
+            if (tid == 0) bs.count = bs.count2;
             __syncthreads();
         }
     }
     __syncthreads();
 
-    int m = sh.count;
+    int m = bs.count;
     if (over) {
-        exact_select(sh, p, lo, hi, k, largest);
+        exact_select<kT>(bs, sh.list[0], p, lo, hi, k, largest);
         m = k;
         cur_list = 0;
     }
@@ -405,16 +669,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     int* rank = reinterpret_cast<int*>(sh.list[cur_list ^ 1]);
     unsigned long long* sel = sh.list[cur_list ^ 1] + kB / 2;
     rank_select<kT>(cand, rank, sel, m, k);
-    if (a.nseg == 1) {
-        for (int i = tid; i < k; i += kT) {
-            const uint32_t idx = comp_index(sel[i]);
-            a.out_v[row * k + i] = p[idx];
-            a.out_i[row * k + i] = (long long)idx;
-        }
-    } else {
-        unsigned long long* dst = a.part + ((long long)row * a.nseg + seg) * k;
-        for (int i = tid; i < k; i += kT) dst[i] = sel[i];
-    }
+    write_segment(a, row, seg, p, sel, k);
 }
 
 struct MergeShared {
@@ -436,7 +691,7 @@ __global__ __launch_bounds__(kMergeT) void k_topk_merge(TopkArgs a) {
     const float* p = a.in + row * a.row_stride;
     for (int i = threadIdx.x; i < k; i += kMergeT) {
         const uint32_t idx = comp_index(sh.sel[i]);
-        a.out_v[row * k + i] = p[idx];
+        a.out_v[row * k + i] = selected_value(p, (uint32_t)(sh.sel[i] >> 32), idx, a.largest);
         a.out_i[row * k + i] = (long long)idx;
     }
 }
@@ -444,29 +699,38 @@ __global__ __launch_bounds__(kMergeT) void k_topk_merge(TopkArgs a) {
 struct TopkPlan {
     int nseg;
     int seg_len;
+    bool wave;
     size_t ws;
 };
 
+// Segments: >= 2 segment workgroups per CU when rows are few, >= 2 units per
+// segment, every segment holding >= k elements (and, for the wave kernel, a full
+// first slice per wave), and a merge list that fits one merge workgroup.
 TopkPlan plan_topk(long long rows, long long cols, long long k) {
-    TopkPlan pl{1, 0, 0};
-    const long long chunks = (cols + kCH - 1) / kCH;
-    // aim for >= 4 segment workgroups per CU, >= 2 chunks per segment, and a
-    // merge list that fits one merge workgroup
-    const long long want = 4LL * device_info().cus;
+    TopkPlan pl{1, (int)cols, false, 0};
+    const bool wave_ok = k <= kWaveK && cols >= kWaveMinSeg;
+    const long long unit = wave_ok ? kWaveMinSeg : kCH;
+    const long long units = (cols + unit - 1) / unit;
+    const long long want = 2LL * device_info().cus;
+    const long long merge_cap = std::max(1LL, (long long)kMergeMax / std::max(1LL, k));
     long long nseg = 1;
     if (rows < want) nseg = (want + rows - 1) / rows;
-    nseg = std::min(nseg, std::max(1LL, chunks / 2));
-    nseg = std::min(nseg, std::max(1LL, (long long)kMergeMax / std::max(1LL, k)));
-    if (knobs().splits > 0) nseg = std::min<long long>(knobs().splits, std::max(1LL, (long long)kMergeMax / std::max(1LL, k)));
-    const long long seg_chunks = (chunks + nseg - 1) / nseg;
-    pl.seg_len = (int)std::max<long long>(kCH, seg_chunks * kCH);
-    pl.nseg = (int)((cols + pl.seg_len - 1) / pl.seg_len);
-    if (pl.nseg < 1) pl.nseg = 1;
-    // a segment shorter than k cannot hold k winners: do not split such rows
-    if (pl.nseg > 1 && (cols - (long long)(pl.nseg - 1) * pl.seg_len) < k) {
-        pl.nseg = 1;
-        pl.seg_len = (int)std::max<long long>(kCH, chunks * kCH);
+    nseg = std::min(nseg, std::max(1LL, units / 2));
+    if (knobs().splits > 0) nseg = knobs().splits;
+    nseg = std::max(1LL, std::min(nseg, merge_cap));
+    const long long min_last = wave_ok ? std::max<long long>(k, kWaveMinSeg) : k;
+    for (; nseg > 1; --nseg) {
+        const long long seg_len = (units + nseg - 1) / nseg * unit;
+        const long long n = (cols + seg_len - 1) / seg_len;
+        const long long last = cols - (n - 1) * seg_len;
+        if (n > 1 && last >= min_last) {
+            pl.nseg = (int)n;
+            pl.seg_len = (int)seg_len;
+            break;
+        }
+        if (n == 1) break;
     }
+    pl.wave = wave_ok;
     pl.ws = pl.nseg > 1 ? (size_t)rows * pl.nseg * k * sizeof(unsigned long long) : 0;
     return pl;
 }
@@ -514,8 +778,19 @@ int tpr_topk(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t 
     const bool vec = ((reinterpret_cast<uintptr_t>(in) & 15u) == 0) && (rows == 1 || row_stride % 4 == 0);
     hipStream_t st = static_cast<hipStream_t>(stream);
     const long long grid = rows * pl.nseg;
-    if (vec) hipLaunchKernelGGL((k_topk_seg<true>), dim3(grid), dim3(kT), 0, st, a);
-    else hipLaunchKernelGGL((k_topk_seg<false>), dim3(grid), dim3(kT), 0, st, a);
+    if (pl.wave) {
+        // Many rows: 8 waves/SIMD (4 workgroups per CU) without prefetch.
+        // Few, split rows: 7 waves/SIMD with a one-slice prefetch per wave.
+        // (Measured on MI355X at [1024, 32768] k=64 and [256, 151936] k=50.)
+        long long var = knobs().topk_variant;
+        if (var == 0) var = pl.nseg == 1 ? 1 : 2;
+        if (!vec) hipLaunchKernelGGL((k_topk_wave<false, 4, 6, true>), dim3(grid), dim3(kT), 0, st, a);
+        else if (var == 1) hipLaunchKernelGGL((k_topk_wave<true, 4, 8, false>), dim3(grid), dim3(kT), 0, st, a);
+        else hipLaunchKernelGGL((k_topk_wave<true, 4, 7, true>), dim3(grid), dim3(kT), 0, st, a);
+    } else {
+        if (vec) hipLaunchKernelGGL((k_topk_block<true>), dim3(grid), dim3(kT), 0, st, a);
+        else hipLaunchKernelGGL((k_topk_block<false>), dim3(grid), dim3(kT), 0, st, a);
+    }
     int rc = check_launch("k_topk_seg");
     if (rc != TPR_OK || pl.nseg == 1) return rc;
     hipLaunchKernelGGL(k_topk_merge, dim3(rows), dim3(kMergeT), 0, st, a);

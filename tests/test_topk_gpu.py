@@ -14,7 +14,8 @@ torch = pytest.importorskip("torch")
 @pytest.fixture(autouse=True)
 def _reset_knobs():
     yield
-    _capi.debug_set("topk_fallback", 0)
+    for k in ("topk_fallback", "topk_variant", "splits"):
+        _capi.debug_set(k, 0)
 
 
 def check(base, v, k, largest=True):
@@ -80,3 +81,18 @@ def test_config5_peaked_logits():
     for r in range(256):
         x[r, rng.choice(151936, 8, replace=False)] += np.float32(15.0)
     check(x, x, 50)
+
+
+@pytest.mark.parametrize("variant", [1, 2])
+@pytest.mark.parametrize("splits", [0, 1, 2, 3, 5])
+def test_wave_kernel_variants_and_segments(variant, splits):
+    # both wave-kernel variants, rows cut into 1..5 segments (merge pass)
+    _capi.debug_set("topk_variant", variant)
+    _capi.debug_set("splits", splits)
+    rng = np.random.default_rng(24 + splits)
+    x = rng.standard_normal((6, 50000)).astype(np.float32)
+    x[1, :] = np.round(x[1, :] * 4) / 4   # many duplicate values
+    x[2, 123] = np.nan
+    for k in (1, 50, 128):
+        for largest in (True, False):
+            check(x, x, k, largest)
