@@ -210,6 +210,7 @@ def main():
         extras["C3_topk64_1024x32768"] = {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
                                           "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4),
                                           "rows_per_s": round(1024 / (ms * 1e-3), 1)}
+        keep_c3 = b3[0]
         del b3, c3
         # C4: full-tensor reductions of 2^28 N(0.5, 2)
         x4 = gen(torch, (1 << 28,), "normal", 4000, dev) * 2.0 + 0.5
@@ -243,6 +244,7 @@ def main():
         e5["argmax_dim-1"] = {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
                               "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4)}
         extras["C5_logits_256x151936"] = e5
+        keep_c5 = b5[0]
         del b5, c5, c5a
     if args.calibrate_copy:
         xc = gen(torch, (64 << 20,), "normal", 6000, dev)
@@ -254,33 +256,74 @@ def main():
     # ---------------- CPU baseline (oracle restatement, 1 core) -------------------
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(bufs[0], ops2, op_bytes)
+        if not args.no_extras:
+            result["cpu_baseline"]["configs"] = cpu_extras(keep_c3, keep_c5)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
 
 
-def cpu_baseline(x_dev, ops2, op_bytes):
+def cpu_baseline(x_dev, ops2, op_bytes, budget_s=10.0):
     """Time the C restatement of TensorPlay's CPU reduction path (single-threaded,
-    as ReductionKernels.cpp is) on one full headline step: the same five
-    reductions of one [64,1024,1024] buffer copied to host memory."""
-    import numpy as np
+    as ReductionKernels.cpp is) on the headline step: the same five reductions of
+    one [64,1024,1024] buffer copied to host memory, repeated until ~budget_s."""
     from oracle import oracle as O
 
     x = x_dev.cpu().numpy()
     fns = {"mean": lambda d: O.mean(x, d), "amax": lambda d: O.amax(x, d),
            "argmax": lambda d: O.argmax(x, d[0]), "var": lambda d: O.var(x, d), "std": lambda d: O.std(x, d)}
+    per = {f"{op}_dim{dims[0]}": 0.0 for (op, dims) in ops2}
+    reps = 0
     t0 = time.perf_counter()
-    per = {}
-    for (op, dims) in ops2:
-        t = time.perf_counter()
-        fns[op](dims)
-        per[f"{op}_dim{dims[0]}"] = round(time.perf_counter() - t, 3)
-    dt = time.perf_counter() - t0
+    while reps == 0 or time.perf_counter() - t0 < budget_s:
+        for (op, dims) in ops2:
+            t = time.perf_counter()
+            fns[op](dims)
+            per[f"{op}_dim{dims[0]}"] += time.perf_counter() - t
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
     total = float(sum(op_bytes))
     return {"value": round(total / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": "one full headline step (mean dim1, amax+argmax dim0, var+std dim-1 of one "
+            "sample": f"{reps} full headline steps (mean dim1, amax+argmax dim0, var+std dim-1 of one "
                       "[64,1024,1024] buffer) through oracle/tp_cpu_reduce.c, 1 thread",
-            "seconds": round(dt, 3), "per_op_s": per, "host_cpus": os.cpu_count()}
+            "seconds_per_step": round(dt, 4),
+            "per_op_s": {k: round(v / reps, 4) for k, v in per.items()}, "host_cpus": os.cpu_count()}
+
+
+def cpu_extras(c3_dev, c5_dev):
+    """CPU figures for the other configs on bounded samples (1 thread unless noted)."""
+    import numpy as np
+    from oracle import oracle as O
+
+    out = {}
+    x1 = np.random.default_rng(1).standard_normal((4096, 4096), dtype=np.float32)
+    t = time.perf_counter()
+    O.sum(x1, [-1])
+    dt = time.perf_counter() - t
+    out["C1_sum_dim-1_4096x4096"] = {"GB/s": round(x1.nbytes / dt / 1e9, 3), "sample": "full config", "cores": 1}
+    x3 = c3_dev[:256].cpu().numpy()
+    t = time.perf_counter()
+    O.topk(x3, 64)
+    dt = time.perf_counter() - t
+    out["C3_topk64_1024x32768"] = {"GB/s": round(x3.nbytes / dt / 1e9, 3), "rows_per_s": round(256 / dt, 1),
+                                   "sample": "256 of 1024 rows, heap selection + sort (no TensorPlay topk exists)",
+                                   "cores": 1}
+    nt = min(16, os.cpu_count() or 1)
+    t = time.perf_counter()
+    O.topk(x3, 64, threads=nt)
+    dt = time.perf_counter() - t
+    out["C3_topk64_1024x32768"]["all_cores"] = {"GB/s": round(x3.nbytes / dt / 1e9, 3), "cores": nt}
+    x5 = c5_dev[:64].cpu().numpy()
+    t = time.perf_counter()
+    O.topk(x5, 50)
+    dt = time.perf_counter() - t
+    out["C5_topk50_256x151936"] = {"GB/s": round(x5.nbytes / dt / 1e9, 3), "rows_per_s": round(64 / dt, 1),
+                                   "sample": "64 of 256 rows", "cores": 1}
+    t = time.perf_counter()
+    O.argmax(x5, -1)
+    dt = time.perf_counter() - t
+    out["C5_argmax_dim-1"] = {"GB/s": round(x5.nbytes / dt / 1e9, 3), "sample": "64 of 256 rows", "cores": 1}
+    return out
 
 
 if __name__ == "__main__":

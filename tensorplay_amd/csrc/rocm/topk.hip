@@ -57,7 +57,7 @@ constexpr int kMergeMax = 4096;  // candidates a merge workgroup ranks (nseg * k
 
 constexpr int kWaveK = 128;                   // largest k of the wave kernel
 constexpr int kWB = 256;                      // per-wave list capacity
-constexpr int kWaveCompact = 192;             // per-wave list size that triggers compaction
+constexpr int kWaveCompact = 192;             // per-wave list size that always triggers compaction
 constexpr int kSlice = 64 * 16;               // elements per wave slice (4 float4 per lane)
 constexpr int kWaveMinSeg = kW * kSlice;      // every wave has a full first slice (8192)
 
@@ -196,6 +196,7 @@ __device__ __forceinline__ uint32_t hist_threshold(const uint32_t* hist, int k, 
         if (lane + d < 64) suf += t;
     }
     const unsigned long long ok = __ballot(suf >= k);
+    if (ok == 0) return T;                      // fewer than k entries: no raise
     const int L = 63 - __clzll((long long)ok);  // highest lane whose suffix reaches k
     uint32_t tn = 0;
     if (lane == L) {
@@ -256,19 +257,37 @@ __device__ uint32_t block_compact(BlockScratch& bs, const unsigned long long* sr
     return Tn;
 }
 
-// Wave-level compaction of list[0..m) in place (all keys >= T); m is updated.
+// Wave-level compaction of list[0..m) in place; m is updated.  Entries below T
+// (admitted before another wave raised the shared bound) are dropped.  If more
+// than k entries are >= T, the threshold is raised by the histogram rule and
+// the survivors are those >= the new threshold (>= k of them); otherwise T is
+// returned unchanged.
 __device__ uint32_t wave_compact(unsigned long long* list, uint32_t* hist, int& m, int k, uint32_t T) {
     const int lane = __lane_id();
     uint32_t mx = 0;
-    for (int i = lane; i < m; i += 64) mx = max(mx, (uint32_t)(list[i] >> 32));
+    int ge = 0;
+    for (int i = lane; i < m; i += 64) {
+        const uint32_t key = (uint32_t)(list[i] >> 32);
+        if (key >= T) {
+            mx = max(mx, key);
+            ++ge;
+        }
+    }
     mx = wave_max_u32(mx);
-    const int shift = hist_shift(mx, T);
+    ge = (int)__ockl_wfred_add_u32((uint32_t)ge);
+    uint32_t tn = T;
+    if (ge > k) {
+        const int shift = hist_shift(mx, T);
 #pragma unroll
-    for (int b = 0; b < 4; ++b) hist[4 * lane + b] = 0;
-    __builtin_amdgcn_wave_barrier();
-    for (int i = lane; i < m; i += 64) atomicAdd(&hist[((uint32_t)(list[i] >> 32) - T) >> shift], 1u);
-    __builtin_amdgcn_wave_barrier();
-    const uint32_t tn = hist_threshold(hist, k, T, shift);
+        for (int b = 0; b < 4; ++b) hist[4 * lane + b] = 0;
+        __builtin_amdgcn_wave_barrier();
+        for (int i = lane; i < m; i += 64) {
+            const uint32_t key = (uint32_t)(list[i] >> 32);
+            if (key >= T) atomicAdd(&hist[(key - T) >> shift], 1u);
+        }
+        __builtin_amdgcn_wave_barrier();
+        tn = hist_threshold(hist, k, T, shift);
+    }
     // a write position never passes the read position, so in place is safe
     int out = 0;
     for (int i0 = 0; i0 < m; i0 += 64) {
@@ -431,6 +450,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(OCC, 8))) vo
     const int hi = min(a.cols, lo + a.seg_len);
     const int nsl = (hi - lo + kSl - 1) / kSl;
     const int r = (k + kW - 1) / kW;
+    const int compact_at = min(kWaveCompact, max(2 * k, 64));  // per-wave list length that triggers compaction
     unsigned long long* list = sh.wl[w];
     uint32_t* hist = sh.hist[w];
 
@@ -470,14 +490,19 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(OCC, 8))) vo
         int total = 0;
 #pragma unroll
         for (int q = 0; q < 4 * SV; ++q) total += __popcll(__ballot(key[q] >= T));
-        while (total > 0 && cnt + total > kWB) {  // no room: raise T from the list first
-            const uint32_t tn = (cnt > k) ? wave_compact(list, hist, cnt, k, T) : T;
-            if (tn <= T) { over = true; break; }
-            if (lane == 0) atomicMax(&bs.tshared, tn);
-            T = tn;
-            total = 0;
+        while (total > 0 && cnt + total > kWB) {  // no room: drop stale entries / raise T first
+            const int before = cnt;
+            const uint32_t tn = wave_compact(list, hist, cnt, k, T);
+            if (tn > T) {
+                if (lane == 0) atomicMax(&bs.tshared, tn);
+                T = tn;
+                total = 0;
 #pragma unroll
-            for (int q = 0; q < 4 * SV; ++q) total += __popcll(__ballot(key[q] >= T));
+                for (int q = 0; q < 4 * SV; ++q) total += __popcll(__ballot(key[q] >= T));
+            } else if (cnt == before) {
+                over = true;  // nothing could be dropped: take the exact path
+                break;
+            }
         }
         if (over) break;
         if (total) {
@@ -494,7 +519,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(OCC, 8))) vo
             }
             cnt = pos;
         }
-        if (cnt > kWaveCompact) {
+        if (cnt > compact_at) {
             const uint32_t tn = wave_compact(list, hist, cnt, k, T);
             if (tn > T) {
                 if (lane == 0) atomicMax(&bs.tshared, tn);
@@ -786,7 +811,7 @@ int tpr_topk(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t 
         if (var == 0) var = pl.nseg == 1 ? 1 : 2;
         if (!vec) hipLaunchKernelGGL((k_topk_wave<false, 4, 6, true>), dim3(grid), dim3(kT), 0, st, a);
         else if (var == 1) hipLaunchKernelGGL((k_topk_wave<true, 4, 8, false>), dim3(grid), dim3(kT), 0, st, a);
-        else hipLaunchKernelGGL((k_topk_wave<true, 4, 7, true>), dim3(grid), dim3(kT), 0, st, a);
+        else hipLaunchKernelGGL((k_topk_wave<true, 4, 6, true>), dim3(grid), dim3(kT), 0, st, a);
     } else {
         if (vec) hipLaunchKernelGGL((k_topk_block<true>), dim3(grid), dim3(kT), 0, st, a);
         else hipLaunchKernelGGL((k_topk_block<false>), dim3(grid), dim3(kT), 0, st, a);

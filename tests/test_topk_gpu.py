@@ -96,3 +96,19 @@ def test_wave_kernel_variants_and_segments(variant, splits):
     for k in (1, 50, 128):
         for largest in (True, False):
             check(x, x, k, largest)
+
+
+@pytest.mark.parametrize("variant", [1, 2])
+def test_rising_rows_stale_candidates(variant):
+    # Values trend upwards along the row, so every wave keeps finding better
+    # elements, compacts repeatedly and raises the shared bound while other
+    # waves still hold entries admitted under older, lower bounds.
+    _capi.debug_set("topk_variant", variant)
+    rng = np.random.default_rng(25)
+    n = 65536
+    trend = np.linspace(0, 50, n, dtype=np.float32)
+    x = np.stack([trend + rng.standard_normal(n).astype(np.float32) * s for s in (0.5, 2.0, 8.0)]
+                 + [trend[::-1].copy() + rng.standard_normal(n).astype(np.float32)])
+    for k in (1, 17, 64, 128):
+        check(x, x, k, True)
+        check(x, x, k, False)
