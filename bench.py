@@ -26,6 +26,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+# kernel each headline op launches (single-kernel plans at this shape)
+DOMINANT_KERNEL = {"mean_dim1": "k_cols<SumOp,4,64> + k_finalize_thread<SumOp>",
+                   "amax_dim0": "k_cols<ArgOp<true>,4,256>", "argmax_dim0": "k_cols<ArgOp<true>,4,256>",
+                   "var_dim-1": "k_rows<WelfordOp,4,32>", "std_dim-1": "k_rows<WelfordOp,4,32>"}
 METRIC = "achieved HBM GB/s (% of MI355X peak) for sum/argmax/topk; rows/s topk"
 
 
@@ -104,6 +108,21 @@ def time_calls(torch, step_fns, steps, warmup):
     return ev0.elapsed_time(ev1) / steps  # ms per iteration
 
 
+def time_each_launch(torch, fns, launches):
+    """Average duration of single launches, each bracketed by its own pair of
+    HIP events on the launch stream (comparable to rocprof's per-kernel time)."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(launches)]
+    for i in range(3):
+        fns[i % len(fns)]()
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(evs):
+        a.record()
+        fns[i % len(fns)]()
+        b.record()
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / launches
+
+
 def gen(torch, shape, kind, seed, dev):
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
@@ -160,6 +179,9 @@ def main():
                                            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
                                            "alg_bytes": op_bytes[j]}
     dom_name, dom = max(breakdown.items(), key=lambda kv: kv[1]["ms"])
+    dom_j = [f"{op}_dim{dims[0]}" for (op, dims) in ops2].index(dom_name)
+    dom_ms = time_each_launch(torch, [calls[i][dom_j] for i in range(nbuf)], max(steps, 10))
+    dom_gbs = op_bytes[dom_j] / (dom_ms * 1e-3) / 1e9
 
     traffic = None
     if os.path.exists(args.traffic_file):
@@ -186,8 +208,10 @@ def main():
                                "var+std dim=-1 (unbiased)",
                    "frac_of_peak": round(value / HBM_PEAK_GBS, 4),
                    "step_alg_bytes": step_bytes},
-        "roofline": {"bound": "hbm", "kernel_op": dom_name, "achieved": dom["GB/s"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(dom["GB/s"] / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "op": dom_name, "kernel": DOMINANT_KERNEL.get(dom_name, "?"),
+                     "avg_launch_ms": round(dom_ms, 5), "alg_bytes_per_launch": op_bytes[dom_j]},
         "breakdown": breakdown,
     }
 

@@ -16,6 +16,20 @@ def test_rocm_key_registers_every_schema():
     assert _C._registered_ops("CPU") == []
 
 
+def test_schema_file_matches_registry():
+    import os
+    import yaml
+    path = os.path.join(os.path.dirname(tp.__file__), "native_functions.yaml")
+    rows = yaml.safe_load(open(path))
+    names = sorted(r["func"].split("(")[0] for r in rows)
+    assert names == SCHEMAS
+    adapters = open(os.path.join(os.path.dirname(tp.__file__), "csrc", "core", "ROCmReductionKernels.cpp")).read()
+    for r in rows:
+        name = r["func"].split("(")[0]
+        assert f'("{name}", rocm::{r["adapter"]})' in adapters
+        assert f'm.impl<{r["stub"].replace("const std::vector<int64_t>&", "V")}>("{name}"' in adapters
+
+
 def test_missing_kernel_is_not_implemented_error():
     t = tp.tensor([[1.0, 2.0], [3.0, 4.0]])
     with pytest.raises(NotImplementedError, match="Kernel not found for op: sum on backend: CPU"):
