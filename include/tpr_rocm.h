@@ -131,8 +131,11 @@ int32_t tpr_abi_version(void);
 /* Tuning / test hook: force plan choices.  Keys: "splits" (row/full/column
  * split count, 0 = automatic), "lanes" (threads per row in the row kernel,
  * 0 = automatic), "general" (1 = always use the generic strided kernel),
- * "topk_fallback" (1 = always take top-k's exact multi-pass path), "tx" (64 or 256:
- * threads across the contiguous dim in the column kernel, 0 = automatic),
+ * "topk_fallback" (1 = always take top-k's exact multi-pass path), "tx" (64, 128
+ * or 256: threads across the contiguous dim in the column kernel, 0 = automatic),
+ * "unroll" (1, 2 or 4 vectors in flight per thread in the row/column kernels,
+ * 0 = automatic), "colblock" (256, 512 or 1024 threads per column-kernel
+ * workgroup, 0 = automatic),
  * "topk_variant" (1 = 8 waves/SIMD without prefetch, 2 = 7 waves/SIMD with a
  * one-slice prefetch, 0 = automatic).
  * Process-wide; not synchronised with concurrent launches.  Returns

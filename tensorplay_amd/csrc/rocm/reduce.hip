@@ -43,10 +43,13 @@ constexpr int kBlock = 256;
 struct SumS { double s; };
 
 struct SumOp {
+    static constexpr bool kIndexed = false;
     using Acc = double;
     using State = SumS;
+    using Wide = SumOp;
     __device__ static Acc init() { return 0.0; }
-    __device__ static void acc(Acc& a, float x, long long) { a += (double)x; }
+    template <class I>
+    __device__ static void acc(Acc& a, float x, I) { a += (double)x; }
     __device__ static State state(Acc a) { return {a}; }
     __device__ static State identity() { return {0.0}; }
     __device__ static State comb(State a, State b) { return {a.s + b.s}; }
@@ -56,18 +59,30 @@ struct SumOp {
 struct ArgS { float v; long long i; };
 
 // Strict compare in index order; lowest index wins equal values (-0.0 == +0.0).
-template <bool IS_MAX>
+// IdxT is the index type of the per-thread accumulator: int inside the row and
+// column kernels (extent < 2^31, checked by the planner; 32-bit selects are
+// cheaper per element), long long in the general kernel.  States always carry
+// a 64-bit index.
+template <bool IS_MAX, class IdxT = int>
 struct ArgOp {
-    using Acc = ArgS;
+    static constexpr bool kIndexed = true;
+    static constexpr IdxT kNone = (IdxT)(sizeof(IdxT) == 4 ? 0x7fffffff : kSentinel);
+    struct Acc { float v; IdxT i; };
     using State = ArgS;
-    __device__ static Acc init() { return {IS_MAX ? -INFINITY : INFINITY, kSentinel}; }
-    __device__ static void acc(Acc& a, float x, long long i) {
+    using Wide = ArgOp<IS_MAX, long long>;
+    __device__ static Acc init() { return {IS_MAX ? -INFINITY : INFINITY, kNone}; }
+    template <class I>
+    __device__ static void acc(Acc& a, float x, I i) {
         bool t = IS_MAX ? (x > a.v) : (x < a.v);
         a.v = t ? x : a.v;
-        a.i = t ? i : a.i;
+        a.i = t ? (IdxT)i : a.i;
     }
-    __device__ static State state(Acc a) { return a; }
-    __device__ static State identity() { return init(); }
+    // state of an accumulator whose stored index is idx: element index = idx * mul + add
+    __device__ static State state_scaled(Acc a, long long mul, long long add) {
+        return {a.v, a.i == kNone ? kSentinel : (long long)a.i * mul + add};
+    }
+    __device__ static State state(Acc a) { return state_scaled(a, 1, 0); }
+    __device__ static State identity() { return {IS_MAX ? -INFINITY : INFINITY, kSentinel}; }
     __device__ static State comb(State a, State b) {
         bool t = IS_MAX ? (b.v > a.v) : (b.v < a.v);
         t = t || (b.v == a.v && b.i < a.i);
@@ -84,10 +99,13 @@ struct WelS { double n, mean, m2; };
 struct WelAcc { float k; int n; double s1, s2; };
 
 struct WelfordOp {
+    static constexpr bool kIndexed = false;
     using Acc = WelAcc;
     using State = WelS;
+    using Wide = WelfordOp;
     __device__ static Acc init() { return {0.0f, 0, 0.0, 0.0}; }
-    __device__ static void acc(Acc& a, float x, long long) {
+    template <class I>
+    __device__ static void acc(Acc& a, float x, I) {
         a.k = (a.n == 0) ? x : a.k;
         double d = (double)x - (double)a.k;
         a.s1 += d;
@@ -105,9 +123,10 @@ struct WelfordOp {
     __device__ static State comb(State a, State b) {
         if (a.n == 0.0) return b;
         if (b.n == 0.0) return a;
-        double n = a.n + b.n;
-        double d = b.mean - a.mean;
-        double f = b.n / n;
+        const double n = a.n + b.n;
+        const double d = b.mean - a.mean;
+        // equal counts (every lane of a full row) need no divide: b.n / n == 1/2
+        const double f = (a.n == b.n) ? 0.5 : b.n / n;
         return {n, a.mean + d * f, a.m2 + b.m2 + d * d * a.n * f};
     }
     __device__ static State shfl(State s, int m) {
@@ -174,8 +193,8 @@ __device__ __forceinline__ typename Op::State block_reduce(typename Op::State st
     return r;  // valid in every thread
 }
 
-template <class Op>
-__device__ __forceinline__ void acc4(typename Op::Acc& a, float4 t, long long e) {
+template <class Op, class I>
+__device__ __forceinline__ void acc4(typename Op::Acc& a, float4 t, I e) {
     Op::acc(a, t.x, e);
     Op::acc(a, t.y, e + 1);
     Op::acc(a, t.z, e + 2);
@@ -195,13 +214,13 @@ struct RowArgs {
     Fin fin;
 };
 
-template <class Op, int VEC, int LANES>
+template <class Op, int VEC, int LANES, int U>
 __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
     using Acc = typename Op::Acc;
     using State = typename Op::State;
     constexpr int GROUPS = (LANES >= kBlock) ? 1 : kBlock / LANES;
-    constexpr int U = 4;                  // vectors in flight per lane
-    constexpr long long TILE = U * LANES; // vectors per tile (contiguous in memory)
+    // U = vectors in flight per lane
+    constexpr int TILE = U * LANES;       // vectors per tile (contiguous in memory)
     const int tid = threadIdx.x;
     const int g = tid / LANES;
     const int l = tid % LANES;
@@ -211,32 +230,56 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
 
     // The row is cut into tiles of U*LANES vectors; split s takes tiles s, s+S,
     // s+2S, ... so the S workgroups of a row sweep it front to back together.
+    // Indexed ops (argmax/amax) keep one accumulator per float4 component with
+    // a 32-bit vector index, so each element costs one compare and two selects.
     Acc acc = Op::init();
+    Acc accq[Op::kIndexed ? 4 : 1];
+#pragma unroll
+    for (int q = 0; q < (Op::kIndexed ? 4 : 1); ++q) accq[q] = Op::init();
     if (row < a.rows) {
         const float* p = a.in + row * a.row_stride;
-        const long long step = (long long)a.S * TILE;
+        const int step = a.S * TILE;
         if (VEC == 4) {
-            const long long nv = a.R >> 2;
+            const int nv = (int)(a.R >> 2);
             const float4* pv = reinterpret_cast<const float4*>(p);
-            long long t0 = (long long)s * TILE;
+            int t0 = s * TILE;
             for (; t0 + TILE <= nv; t0 += step) {
                 float4 t[U];
 #pragma unroll
                 for (int u = 0; u < U; ++u) t[u] = pv[t0 + l + u * LANES];
 #pragma unroll
-                for (int u = 0; u < U; ++u) acc4<Op>(acc, t[u], 4 * (t0 + l + u * LANES));
+                for (int u = 0; u < U; ++u) {
+                    const int v = t0 + l + u * LANES;
+                    if constexpr (Op::kIndexed) {
+                        Op::acc(accq[0], t[u].x, v);
+                        Op::acc(accq[1 % (Op::kIndexed ? 4 : 1)], t[u].y, v);
+                        Op::acc(accq[2 % (Op::kIndexed ? 4 : 1)], t[u].z, v);
+                        Op::acc(accq[3 % (Op::kIndexed ? 4 : 1)], t[u].w, v);
+                    } else {
+                        acc4<Op>(acc, t[u], 4 * v);
+                    }
+                }
             }
             if (t0 < nv) {
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
-                    const long long v = t0 + l + u * LANES;
-                    if (v < nv) acc4<Op>(acc, pv[v], 4 * v);
+                    const int v = t0 + l + u * LANES;
+                    if (v < nv) {
+                        const float4 t = pv[v];
+                        if constexpr (Op::kIndexed) {
+                            Op::acc(accq[0], t.x, v);
+                            Op::acc(accq[1 % (Op::kIndexed ? 4 : 1)], t.y, v);
+                            Op::acc(accq[2 % (Op::kIndexed ? 4 : 1)], t.z, v);
+                            Op::acc(accq[3 % (Op::kIndexed ? 4 : 1)], t.w, v);
+                        } else {
+                            acc4<Op>(acc, t, 4 * v);
+                        }
+                    }
                 }
             }
-            for (long long e = 4 * nv + (long long)s * LANES + l; e < a.R; e += (long long)a.S * LANES)
-                Op::acc(acc, p[e], e);
+            for (int e = 4 * nv + s * LANES + l; e < a.R; e += a.S * LANES) Op::acc(acc, p[e], e);
         } else {
-            long long t0 = (long long)s * TILE;
+            int t0 = s * TILE;
             for (; t0 + TILE <= a.R; t0 += step) {
                 float x[U];
 #pragma unroll
@@ -247,7 +290,7 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
             if (t0 < a.R) {
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
-                    const long long e = t0 + l + u * LANES;
+                    const int e = t0 + l + u * LANES;
                     if (e < a.R) Op::acc(acc, p[e], e);
                 }
             }
@@ -255,6 +298,10 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
     }
 
     State st = Op::state(acc);
+    if constexpr (Op::kIndexed) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) st = Op::comb(st, Op::state_scaled(accq[q % (Op::kIndexed ? 4 : 1)], 4, q));
+    }
     constexpr int SUBW = LANES < kWave ? LANES : kWave;
     st = group_reduce_sub_wave<Op, SUBW>(st);
     if (LANES > kWave) {
@@ -291,11 +338,11 @@ struct ColArgs {
     Fin fin;
 };
 
-template <class Op, int VEC, int TX>
-__global__ __launch_bounds__(kBlock) void k_cols(ColArgs a) {
+template <class Op, int VEC, int TX, int U, int BLK>
+__global__ __launch_bounds__(BLK) void k_cols(ColArgs a) {
     using Acc = typename Op::Acc;
     using State = typename Op::State;
-    constexpr int TY = kBlock / TX;
+    constexpr int TY = BLK / TX;
     const int tid = threadIdx.x;
     const int tx = tid % TX;
     const int ty = tid / TX;
@@ -311,36 +358,38 @@ __global__ __launch_bounds__(kBlock) void k_cols(ColArgs a) {
 
     // rows of the reduced dim are interleaved over the TY thread rows and the S
     // splits (row r goes to split (r / TY) % S), so concurrently running
-    // workgroups read neighbouring rows
+    // workgroups read neighbouring rows; U rows are in flight per thread
     if (col0 < a.inner) {
         const float* base = a.in + o * a.os + col0;
-        const long long rstep = (long long)TY * a.S;
-        const long long r0 = (long long)s * TY + ty;
+        const int R = (int)a.R;
+        const int rstep = TY * a.S;
+        const int r0 = s * TY + ty;
         if (VEC == 4 && col0 + 3 < a.inner) {
-            long long r = r0;
-            for (; r + 3 * rstep < a.R; r += 4 * rstep) {
-                float4 t0 = *reinterpret_cast<const float4*>(base + r * a.rs);
-                float4 t1 = *reinterpret_cast<const float4*>(base + (r + rstep) * a.rs);
-                float4 t2 = *reinterpret_cast<const float4*>(base + (r + 2 * rstep) * a.rs);
-                float4 t3 = *reinterpret_cast<const float4*>(base + (r + 3 * rstep) * a.rs);
-                Op::acc(acc[0], t0.x, r); Op::acc(acc[1], t0.y, r);
-                Op::acc(acc[2], t0.z, r); Op::acc(acc[3], t0.w, r);
-                Op::acc(acc[0], t1.x, r + rstep); Op::acc(acc[1], t1.y, r + rstep);
-                Op::acc(acc[2], t1.z, r + rstep); Op::acc(acc[3], t1.w, r + rstep);
-                Op::acc(acc[0], t2.x, r + 2 * rstep); Op::acc(acc[1], t2.y, r + 2 * rstep);
-                Op::acc(acc[2], t2.z, r + 2 * rstep); Op::acc(acc[3], t2.w, r + 2 * rstep);
-                Op::acc(acc[0], t3.x, r + 3 * rstep); Op::acc(acc[1], t3.y, r + 3 * rstep);
-                Op::acc(acc[2], t3.z, r + 3 * rstep); Op::acc(acc[3], t3.w, r + 3 * rstep);
+            int r = r0;
+            for (; r + (U - 1) * rstep < R; r += U * rstep) {
+                float4 t[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) t[u] = *reinterpret_cast<const float4*>(base + (long long)(r + u * rstep) * a.rs);
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int ru = r + u * rstep;
+                    Op::acc(acc[0], t[u].x, ru);
+                    Op::acc(acc[1 % VEC], t[u].y, ru);
+                    Op::acc(acc[2 % VEC], t[u].z, ru);
+                    Op::acc(acc[3 % VEC], t[u].w, ru);
+                }
             }
-            for (; r < a.R; r += rstep) {
-                float4 t = *reinterpret_cast<const float4*>(base + r * a.rs);
-                Op::acc(acc[0], t.x, r); Op::acc(acc[1], t.y, r);
-                Op::acc(acc[2], t.z, r); Op::acc(acc[3], t.w, r);
+            for (; r < R; r += rstep) {
+                float4 t = *reinterpret_cast<const float4*>(base + (long long)r * a.rs);
+                Op::acc(acc[0], t.x, r);
+                Op::acc(acc[1 % VEC], t.y, r);
+                Op::acc(acc[2 % VEC], t.z, r);
+                Op::acc(acc[3 % VEC], t.w, r);
             }
         } else {
             const int nj = (int)min((long long)VEC, a.inner - col0);
-            for (long long r = r0; r < a.R; r += rstep) {
-                const float* q = base + r * a.rs;
+            for (int r = r0; r < R; r += rstep) {
+                const float* q = base + (long long)r * a.rs;
 #pragma unroll
                 for (int j = 0; j < VEC; ++j)
                     if (j < nj) Op::acc(acc[j], q[j], r);
@@ -352,19 +401,21 @@ __global__ __launch_bounds__(kBlock) void k_cols(ColArgs a) {
 #pragma unroll
     for (int j = 0; j < VEC; ++j) st[j] = Op::state(acc[j]);
 
-    if (TY > 1) {
-        __shared__ State sh[TY][TX * VEC];
+    // combine the TY thread rows with a halving tree in LDS (fixed order)
+    if constexpr (TY > 1) {
+        __shared__ State sh[(TY > 1 ? TY / 2 : 1) * TX * VEC];
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) sh[ty][tx * VEC + j] = st[j];
-        __syncthreads();
-        if (ty == 0) {
+        for (int half = TY / 2; half >= 1; half /= 2) {
+            if (ty >= half && ty < 2 * half) {
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) {
-                State r = sh[0][tx * VEC + j];
-#pragma unroll
-                for (int y = 1; y < TY; ++y) r = Op::comb(r, sh[y][tx * VEC + j]);
-                st[j] = r;
+                for (int j = 0; j < VEC; ++j) sh[((ty - half) * TX + tx) * VEC + j] = st[j];
             }
+            __syncthreads();
+            if (ty < half) {
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) st[j] = Op::comb(st[j], sh[(ty * TX + tx) * VEC + j]);
+            }
+            __syncthreads();
         }
     }
     if (ty == 0) {
@@ -472,6 +523,8 @@ struct Plan {
     int vec = 1;
     int lanes = 64;  // rows
     int tx = 64;     // cols
+    int unroll = 4;  // rows/cols: vectors in flight per thread
+    int colblock = 256;  // cols: threads per workgroup
     long long S = 1;
     size_t state_bytes = 8;
     size_t ws = 0;
@@ -580,7 +633,9 @@ Plan make_plan(const tpr_reduce_desc* d, const void* in) {
         p.S = ceil_div(std::max(1LL, p.count), p.seg);
     };
 
-    if (empty || force_general) {
+    const long long kIntMax = 0x7fffffffLL;
+    const bool int_ok = Rd.empty() || (Rd.size() == 1 && Rd[0].size < kIntMax);
+    if (empty || force_general || !int_ok) {
         fill_general();
     } else if (K.size() <= 1 && (Rd.empty() || (Rd.size() == 1 && Rd[0].stride == 1))) {
         // rows: [K?, R] with R contiguous (R may be absent: each output is one element)
@@ -622,10 +677,18 @@ Plan make_plan(const tpr_reduce_desc* d, const void* in) {
         const long long target = (long long)dev.cus * 512;
         if (p.outer * ceil_div(cols4, 256) * kBlock >= target || p.R < 16) p.tx = 256;
         else p.tx = 64;
-        if (knobs().tx == 64 || knobs().tx == 256) p.tx = (int)knobs().tx;
+        if (knobs().tx == 64 || knobs().tx == 128 || knobs().tx == 256) p.tx = (int)knobs().tx;
+        p.unroll = (p.tx == 256) ? 2 : 4;  // measured: 2 rows in flight per thread at TX=256, 4 at TX=64
+        // grow the workgroup (more thread rows over R) before splitting R over
+        // workgroups: a split costs a finalize launch (~4-5 us on MI355X)
+        const long long base_threads = p.outer * ceil_div(cols4, p.tx);
+        while (p.colblock < 1024 && base_threads * p.colblock < target && p.R >= 8 * (2 * p.colblock / p.tx))
+            p.colblock *= 2;
+        if (knobs().colblock == 256 || knobs().colblock == 512 || knobs().colblock == 1024)
+            p.colblock = (int)knobs().colblock;
         p.ncb = ceil_div(ceil_div(p.inner, p.vec), p.tx);
-        const long long ty = kBlock / p.tx;
-        const long long threads = p.outer * ceil_div(cols4, p.tx) * kBlock;
+        const long long ty = p.colblock / p.tx;
+        const long long threads = p.outer * ceil_div(cols4, p.tx) * p.colblock;
         long long S = 1;
         if (threads < target) S = std::min(ceil_div(target, threads), std::max(1LL, p.R / (ty * 8)));
         if (knobs().splits > 0) S = knobs().splits;
@@ -633,6 +696,7 @@ Plan make_plan(const tpr_reduce_desc* d, const void* in) {
     } else {
         fill_general();
     }
+    if (knobs().unroll == 1 || knobs().unroll == 2 || knobs().unroll == 4) p.unroll = (int)knobs().unroll;
     p.ws = (p.S > 1) ? (size_t)p.S * (size_t)p.nout * p.state_bytes : 0;
     return p;
 }
@@ -642,10 +706,12 @@ int launch_rows(const Plan& p, const float* in, void* out, void* ws, Fin fin, hi
     RowArgs a{in, p.rows, p.R, p.row_stride, (int)p.S, out, ws, fin};
     const long long groups = (p.lanes >= kBlock) ? 1 : kBlock / p.lanes;
     const long long grid = ceil_div(p.rows, groups) * p.S;
-#define TPR_ROWS_CASE(L)                                                                  \
-    case L:                                                                               \
-        if (p.vec == 4) hipLaunchKernelGGL((k_rows<Op, 4, L>), dim3(grid), dim3(kBlock), 0, st, a); \
-        else hipLaunchKernelGGL((k_rows<Op, 1, L>), dim3(grid), dim3(kBlock), 0, st, a);            \
+#define TPR_ROWS_CASE(L)                                                                             \
+    case L:                                                                                          \
+        if (p.vec == 4 && p.unroll == 1) hipLaunchKernelGGL((k_rows<Op, 4, L, 1>), dim3(grid), dim3(kBlock), 0, st, a); \
+        else if (p.vec == 4 && p.unroll == 2) hipLaunchKernelGGL((k_rows<Op, 4, L, 2>), dim3(grid), dim3(kBlock), 0, st, a); \
+        else if (p.vec == 4) hipLaunchKernelGGL((k_rows<Op, 4, L, 4>), dim3(grid), dim3(kBlock), 0, st, a); \
+        else hipLaunchKernelGGL((k_rows<Op, 1, L, 4>), dim3(grid), dim3(kBlock), 0, st, a);        \
         break;
     switch (p.lanes) {
         TPR_ROWS_CASE(16)
@@ -663,13 +729,25 @@ template <class Op>
 int launch_cols(const Plan& p, const float* in, void* out, void* ws, Fin fin, hipStream_t st) {
     ColArgs a{in, p.outer, p.os, p.R, p.rs, p.inner, (int)p.S, p.ncb, out, ws, fin};
     const long long grid = p.outer * p.ncb * p.S;
-    if (p.tx == 256) {
-        if (p.vec == 4) hipLaunchKernelGGL((k_cols<Op, 4, 256>), dim3(grid), dim3(kBlock), 0, st, a);
-        else hipLaunchKernelGGL((k_cols<Op, 1, 256>), dim3(grid), dim3(kBlock), 0, st, a);
-    } else {
-        if (p.vec == 4) hipLaunchKernelGGL((k_cols<Op, 4, 64>), dim3(grid), dim3(kBlock), 0, st, a);
-        else hipLaunchKernelGGL((k_cols<Op, 1, 64>), dim3(grid), dim3(kBlock), 0, st, a);
+#define TPR_COLS_LAUNCH(TXV, BLK)                                                                          \
+    {                                                                                                     \
+        if (p.vec != 4) hipLaunchKernelGGL((k_cols<Op, 1, TXV, 4, BLK>), dim3(grid), dim3(BLK), 0, st, a); \
+        else if (p.unroll == 1) hipLaunchKernelGGL((k_cols<Op, 4, TXV, 1, BLK>), dim3(grid), dim3(BLK), 0, st, a); \
+        else if (p.unroll == 2) hipLaunchKernelGGL((k_cols<Op, 4, TXV, 2, BLK>), dim3(grid), dim3(BLK), 0, st, a); \
+        else hipLaunchKernelGGL((k_cols<Op, 4, TXV, 4, BLK>), dim3(grid), dim3(BLK), 0, st, a);            \
     }
+#define TPR_COLS_CASE(TXV)                      \
+    if (p.tx == TXV) {                          \
+        if (p.colblock == 1024) TPR_COLS_LAUNCH(TXV, 1024)     \
+        else if (p.colblock == 512) TPR_COLS_LAUNCH(TXV, 512)  \
+        else TPR_COLS_LAUNCH(TXV, 256)                         \
+    }
+    TPR_COLS_CASE(256)
+    else TPR_COLS_CASE(128)
+    else TPR_COLS_CASE(64)
+    else return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: tx must be 64, 128 or 256");
+#undef TPR_COLS_LAUNCH
+#undef TPR_COLS_CASE
     return check_launch("k_cols");
 }
 
@@ -692,7 +770,7 @@ int launch_general(const Plan& p, const float* in, void* out, void* ws, Fin fin,
     a.out = out;
     a.part = ws;
     a.fin = fin;
-    hipLaunchKernelGGL((k_general<Op>), dim3(p.nout * p.S), dim3(kBlock), 0, st, a);
+    hipLaunchKernelGGL((k_general<typename Op::Wide>), dim3(p.nout * p.S), dim3(kBlock), 0, st, a);
     return check_launch("k_general");
 }
 

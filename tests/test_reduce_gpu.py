@@ -25,7 +25,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 @pytest.fixture(autouse=True)
 def _reset_knobs():
     yield
-    for k in ("splits", "lanes", "general", "tx"):
+    for k in ("splits", "lanes", "general", "tx", "unroll", "colblock"):
         _capi.debug_set(k, 0)
 
 
@@ -123,7 +123,8 @@ def test_random_layouts(op):
 
 
 @pytest.mark.parametrize("knob,values", [("general", [1]), ("splits", [1, 2, 3, 7, 64]),
-                                         ("lanes", [16, 32, 64, 128, 256]), ("tx", [64, 256])])
+                                         ("lanes", [16, 32, 64, 128, 256]), ("tx", [64, 128, 256]),
+                                         ("unroll", [1, 2, 4]), ("colblock", [256, 512, 1024])])
 def test_forced_plans(knob, values):
     rng = np.random.default_rng(12)
     b = rng.standard_normal((37, 1029)).astype(np.float32)
@@ -133,7 +134,7 @@ def test_forced_plans(knob, values):
         for op in OPS:
             check(b, torch.from_numpy(b).cuda(), op, [1])
             check(b, torch.from_numpy(b).cuda(), op, None)
-            if knob in ("tx", "splits"):
+            if knob in ("tx", "splits", "unroll", "colblock"):
                 d = rng.standard_normal((3, 9, 1030)).astype(np.float32)  # inner not a multiple of 4
                 check(d, torch.from_numpy(d).cuda(), op, [1])
                 check(d[:, :, 1:], device_view(torch, d, d[:, :, 1:]), op, [0])
