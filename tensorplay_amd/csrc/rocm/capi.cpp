@@ -69,6 +69,7 @@ int tpr_debug_set(const char* key, int64_t value) {
     else if (!std::strcmp(key, "topk_variant")) k.topk_variant = value;
     else if (!std::strcmp(key, "unroll")) k.unroll = value;
     else if (!std::strcmp(key, "colblock")) k.colblock = value;
+    else if (!std::strcmp(key, "nt")) k.nt = value;
     else return tpr::fail(TPR_ERR_INVALID_ARG, std::string("tpr_debug_set: unknown key ") + key);
     return TPR_OK;
 }

@@ -32,6 +32,7 @@ struct DebugKnobs {
     int64_t topk_variant = 0;
     int64_t unroll = 0;
     int64_t colblock = 0;
+    int64_t nt = 0;
 };
 DebugKnobs& knobs();
 

@@ -193,6 +193,16 @@ __device__ __forceinline__ typename Op::State block_reduce(typename Op::State st
     return r;  // valid in every thread
 }
 
+// Streaming 128-bit load; `nt` marks it nontemporal (read once, do not keep in cache).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld4(const float4* p, int nt) {
+    if (nt) {
+        const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+        return make_float4(v.x, v.y, v.z, v.w);
+    }
+    return *p;
+}
+
 template <class Op, class I>
 __device__ __forceinline__ void acc4(typename Op::Acc& a, float4 t, I e) {
     Op::acc(a, t.x, e);
@@ -209,6 +219,7 @@ struct RowArgs {
     const float* in;
     long long rows, R, row_stride;
     int S;
+    int nt;
     void* out;
     void* part;
     Fin fin;
@@ -246,7 +257,7 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
             for (; t0 + TILE <= nv; t0 += step) {
                 float4 t[U];
 #pragma unroll
-                for (int u = 0; u < U; ++u) t[u] = pv[t0 + l + u * LANES];
+                for (int u = 0; u < U; ++u) t[u] = ld4(pv + t0 + l + u * LANES, a.nt);
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const int v = t0 + l + u * LANES;
@@ -332,6 +343,7 @@ struct ColArgs {
     const float* in;
     long long outer, os, R, rs, inner;
     int S;
+    int nt;
     long long ncb;
     void* out;
     void* part;
@@ -369,7 +381,7 @@ __global__ __launch_bounds__(BLK) void k_cols(ColArgs a) {
             for (; r + (U - 1) * rstep < R; r += U * rstep) {
                 float4 t[U];
 #pragma unroll
-                for (int u = 0; u < U; ++u) t[u] = *reinterpret_cast<const float4*>(base + (long long)(r + u * rstep) * a.rs);
+                for (int u = 0; u < U; ++u) t[u] = ld4(reinterpret_cast<const float4*>(base + (long long)(r + u * rstep) * a.rs), a.nt);
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const int ru = r + u * rstep;
@@ -524,6 +536,7 @@ struct Plan {
     int lanes = 64;  // rows
     int tx = 64;     // cols
     int unroll = 4;  // rows/cols: vectors in flight per thread
+    int nt = 0;      // rows/cols: nontemporal input loads
     int colblock = 256;  // cols: threads per workgroup
     long long S = 1;
     size_t state_bytes = 8;
@@ -697,13 +710,18 @@ Plan make_plan(const tpr_reduce_desc* d, const void* in) {
         fill_general();
     }
     if (knobs().unroll == 1 || knobs().unroll == 2 || knobs().unroll == 4) p.unroll = (int)knobs().unroll;
+    // Inputs are read exactly once: mark the loads nontemporal for large
+    // reductions (measured on MI355X: +8..13% at 256 MiB and 1 GiB; no gain at
+    // 64 MiB).
+    p.nt = (p.count * p.nout >= (32LL << 20)) ? 1 : 0;  // >= 128 MiB of float32
+    if (knobs().nt != 0) p.nt = knobs().nt > 0 ? 1 : 0;
     p.ws = (p.S > 1) ? (size_t)p.S * (size_t)p.nout * p.state_bytes : 0;
     return p;
 }
 
 template <class Op>
 int launch_rows(const Plan& p, const float* in, void* out, void* ws, Fin fin, hipStream_t st) {
-    RowArgs a{in, p.rows, p.R, p.row_stride, (int)p.S, out, ws, fin};
+    RowArgs a{in, p.rows, p.R, p.row_stride, (int)p.S, p.nt, out, ws, fin};
     const long long groups = (p.lanes >= kBlock) ? 1 : kBlock / p.lanes;
     const long long grid = ceil_div(p.rows, groups) * p.S;
 #define TPR_ROWS_CASE(L)                                                                             \
@@ -727,7 +745,7 @@ int launch_rows(const Plan& p, const float* in, void* out, void* ws, Fin fin, hi
 
 template <class Op>
 int launch_cols(const Plan& p, const float* in, void* out, void* ws, Fin fin, hipStream_t st) {
-    ColArgs a{in, p.outer, p.os, p.R, p.rs, p.inner, (int)p.S, p.ncb, out, ws, fin};
+    ColArgs a{in, p.outer, p.os, p.R, p.rs, p.inner, (int)p.S, p.nt, p.ncb, out, ws, fin};
     const long long grid = p.outer * p.ncb * p.S;
 #define TPR_COLS_LAUNCH(TXV, BLK)                                                                          \
     {                                                                                                     \

@@ -397,12 +397,20 @@ static_assert(kW * kWB == kB, "the per-wave lists double as a block-sized scratc
 static_assert(sizeof(int) * kB + sizeof(unsigned long long) * kKMax <= sizeof(unsigned long long) * kB,
               "rank + sel must fit in one idle list");
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 128-bit load marked nontemporal: the row is read once.
+__device__ __forceinline__ float4 ld4_nt(const float* p) {
+    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 template <bool VEC, int SV>
 __device__ __forceinline__ void load_slice(float4 (&cur)[SV], const float* p, int base, int hi) {
     const int lane = __lane_id();
     if (VEC && base + 256 * SV <= hi) {
 #pragma unroll
-        for (int j = 0; j < SV; ++j) cur[j] = *reinterpret_cast<const float4*>(p + base + 4 * (j * 64 + lane));
+        for (int j = 0; j < SV; ++j) cur[j] = ld4_nt(p + base + 4 * (j * 64 + lane));
     } else {
 #pragma unroll
         for (int j = 0; j < SV; ++j) {

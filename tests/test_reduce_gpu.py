@@ -25,7 +25,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 @pytest.fixture(autouse=True)
 def _reset_knobs():
     yield
-    for k in ("splits", "lanes", "general", "tx", "unroll", "colblock"):
+    for k in ("splits", "lanes", "general", "tx", "unroll", "colblock", "nt"):
         _capi.debug_set(k, 0)
 
 
@@ -124,7 +124,8 @@ def test_random_layouts(op):
 
 @pytest.mark.parametrize("knob,values", [("general", [1]), ("splits", [1, 2, 3, 7, 64]),
                                          ("lanes", [16, 32, 64, 128, 256]), ("tx", [64, 128, 256]),
-                                         ("unroll", [1, 2, 4]), ("colblock", [256, 512, 1024])])
+                                         ("unroll", [1, 2, 4]), ("colblock", [256, 512, 1024]),
+                                         ("nt", [1, -1])])
 def test_forced_plans(knob, values):
     rng = np.random.default_rng(12)
     b = rng.standard_normal((37, 1029)).astype(np.float32)
