@@ -129,7 +129,7 @@ const char* tpr_last_error(void);
 int32_t tpr_abi_version(void);
 
 /* Tuning / test hook: force plan choices.  Keys: "splits" (row/full/column
- * split count, 0 = automatic), "lanes" (threads per row in the row kernel,
+ * split count, 0 = automatic), "lanes" (threads per row in the row kernel, 16..1024,
  * 0 = automatic), "general" (1 = always use the generic strided kernel),
  * "topk_fallback" (1 = always take top-k's exact multi-pass path), "tx" (64, 128
  * or 256: threads across the contiguous dim in the column kernel, 0 = automatic),

@@ -226,10 +226,11 @@ struct RowArgs {
 };
 
 template <class Op, int VEC, int LANES, int U>
-__global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
+__global__ __launch_bounds__(LANES > kBlock ? LANES : kBlock) void k_rows(RowArgs a) {
     using Acc = typename Op::Acc;
     using State = typename Op::State;
-    constexpr int GROUPS = (LANES >= kBlock) ? 1 : kBlock / LANES;
+    constexpr int BLK = LANES > kBlock ? LANES : kBlock;  // one long row per 512/1024-thread block
+    constexpr int GROUPS = (LANES >= BLK) ? 1 : BLK / LANES;
     // U = vectors in flight per lane
     constexpr int TILE = U * LANES;       // vectors per tile (contiguous in memory)
     const int tid = threadIdx.x;
@@ -317,7 +318,7 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
     st = group_reduce_sub_wave<Op, SUBW>(st);
     if (LANES > kWave) {
         constexpr int WPG = LANES / kWave;  // waves per group
-        __shared__ State sh[kBlock / kWave];
+        __shared__ State sh[BLK / kWave];
         const int w = tid / kWave;
         if (__lane_id() == 0) sh[w] = st;
         __syncthreads();
@@ -664,9 +665,12 @@ Plan make_plan(const tpr_reduce_desc* d, const void* in) {
         long long lanes = std::max(pow2_ceil(ceil_div(p.R, E)),
                                    pow2_ceil(ceil_div((long long)dev.cus * 4096, p.rows)));
         lanes = std::min(256LL, std::max(16LL, std::min(lanes, pow2_ceil(ceil_div(p.R, 4)))));
+        const long long target = (long long)dev.cus * 512;
+        // few long rows: give one row a 512- or 1024-thread workgroup before
+        // splitting it over workgroups (a split costs a finalize launch)
+        while (p.rows * lanes < 2 * target && lanes < 1024 && 16 * 2 * lanes <= p.R) lanes *= 2;
         if (knobs().lanes > 0) lanes = knobs().lanes;
         p.lanes = (int)lanes;
-        const long long target = (long long)dev.cus * 512;
         const long long tiles = std::max(1LL, ceil_div(p.R, 16 * lanes));  // 4 vectors x 4 floats per lane
         long long threads = p.rows * lanes;
         long long S = 1;
@@ -725,19 +729,23 @@ int launch_rows(const Plan& p, const float* in, void* out, void* ws, Fin fin, hi
     const long long groups = (p.lanes >= kBlock) ? 1 : kBlock / p.lanes;
     const long long grid = ceil_div(p.rows, groups) * p.S;
 #define TPR_ROWS_CASE(L)                                                                             \
-    case L:                                                                                          \
-        if (p.vec == 4 && p.unroll == 1) hipLaunchKernelGGL((k_rows<Op, 4, L, 1>), dim3(grid), dim3(kBlock), 0, st, a); \
-        else if (p.vec == 4 && p.unroll == 2) hipLaunchKernelGGL((k_rows<Op, 4, L, 2>), dim3(grid), dim3(kBlock), 0, st, a); \
-        else if (p.vec == 4) hipLaunchKernelGGL((k_rows<Op, 4, L, 4>), dim3(grid), dim3(kBlock), 0, st, a); \
-        else hipLaunchKernelGGL((k_rows<Op, 1, L, 4>), dim3(grid), dim3(kBlock), 0, st, a);        \
-        break;
+    case L: {                                                                                        \
+        constexpr int B = L > kBlock ? L : kBlock;                                                   \
+        if (p.vec == 4 && p.unroll == 1) hipLaunchKernelGGL((k_rows<Op, 4, L, 1>), dim3(grid), dim3(B), 0, st, a); \
+        else if (p.vec == 4 && p.unroll == 2) hipLaunchKernelGGL((k_rows<Op, 4, L, 2>), dim3(grid), dim3(B), 0, st, a); \
+        else if (p.vec == 4) hipLaunchKernelGGL((k_rows<Op, 4, L, 4>), dim3(grid), dim3(B), 0, st, a); \
+        else hipLaunchKernelGGL((k_rows<Op, 1, L, 4>), dim3(grid), dim3(B), 0, st, a);             \
+        break;                                                                                       \
+    }
     switch (p.lanes) {
         TPR_ROWS_CASE(16)
         TPR_ROWS_CASE(32)
         TPR_ROWS_CASE(64)
         TPR_ROWS_CASE(128)
         TPR_ROWS_CASE(256)
-        default: return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: lanes must be 16/32/64/128/256");
+        TPR_ROWS_CASE(512)
+        TPR_ROWS_CASE(1024)
+        default: return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: lanes must be 16/32/64/128/256/512/1024");
     }
 #undef TPR_ROWS_CASE
     return check_launch("k_rows");

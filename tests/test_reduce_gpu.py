@@ -123,7 +123,7 @@ def test_random_layouts(op):
 
 
 @pytest.mark.parametrize("knob,values", [("general", [1]), ("splits", [1, 2, 3, 7, 64]),
-                                         ("lanes", [16, 32, 64, 128, 256]), ("tx", [64, 128, 256]),
+                                         ("lanes", [16, 32, 64, 128, 256, 512, 1024]), ("tx", [64, 128, 256]),
                                          ("unroll", [1, 2, 4]), ("colblock", [256, 512, 1024]),
                                          ("nt", [1, -1])])
 def test_forced_plans(knob, values):
@@ -243,3 +243,14 @@ def test_config5_argmax_logits():
         x[r, rng.choice(151936, 8, replace=False)] += np.float32(15.0)
     t = torch.from_numpy(x).cuda()
     assert_bits_equal(gpu(t, "argmax", [-1]), O.argmax(x, -1))
+
+
+def test_few_long_rows():
+    """Few long rows run one row per 512/1024-thread workgroup (no split)."""
+    rng = np.random.default_rng(13)
+    for rows, cols in ((3, 70001), (64, 151936), (1, 1 << 20)):
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        x[0, [5, cols - 1]] = 9.0  # tie far apart: lowest index wins
+        t = torch.from_numpy(x).cuda()
+        for op in OPS:
+            check(x, t, op, [1])
