@@ -136,8 +136,9 @@ int32_t tpr_abi_version(void);
  * "unroll" (1, 2 or 4 vectors in flight per thread in the row/column kernels,
  * 0 = automatic), "colblock" (256, 512 or 1024 threads per column-kernel
  * workgroup, 0 = automatic),
- * "topk_variant" (1 = 8 waves/SIMD without prefetch, 2 = 7 waves/SIMD with a
- * one-slice prefetch, 0 = automatic).
+ * "topk_variant" (wave kernel prefetch depth: 1 = none, 2 = one slice, 3 = two
+ * slices; 0 = automatic), "topk_waves" (8 or 16 waves per wave-kernel
+ * workgroup, 0 = automatic).
  * Process-wide; not synchronised with concurrent launches.  Returns
  * TPR_ERR_INVALID_ARG for an unknown key.  No reference counterpart. */
 int tpr_debug_set(const char* key, int64_t value);

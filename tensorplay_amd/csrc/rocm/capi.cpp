@@ -67,6 +67,7 @@ int tpr_debug_set(const char* key, int64_t value) {
     else if (!std::strcmp(key, "topk_fallback")) k.topk_fallback = value;
     else if (!std::strcmp(key, "tx")) k.tx = value;
     else if (!std::strcmp(key, "topk_variant")) k.topk_variant = value;
+    else if (!std::strcmp(key, "topk_waves")) k.topk_waves = value;
     else if (!std::strcmp(key, "unroll")) k.unroll = value;
     else if (!std::strcmp(key, "colblock")) k.colblock = value;
     else if (!std::strcmp(key, "nt")) k.nt = value;

@@ -30,6 +30,7 @@ struct DebugKnobs {
     int64_t topk_fallback = 0;
     int64_t tx = 0;
     int64_t topk_variant = 0;
+    int64_t topk_waves = 0;
     int64_t unroll = 0;
     int64_t colblock = 0;
     int64_t nt = 0;

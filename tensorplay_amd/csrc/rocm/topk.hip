@@ -48,6 +48,7 @@ namespace {
 
 constexpr int kT = 512;          // threads per segment workgroup
 constexpr int kW = kT / 64;      // waves per workgroup
+constexpr int kMaxW = 16;        // most waves of any top-k workgroup (1024 threads)
 constexpr int kV = 4;            // float4 loads per thread per chunk (block kernel)
 constexpr int kCH = kT * 4 * kV; // elements per block-kernel chunk (8192)
 constexpr int kB = 2048;         // block candidate list capacity
@@ -60,6 +61,7 @@ constexpr int kWB = 256;                      // per-wave list capacity
 constexpr int kWaveCompact = 192;             // per-wave list size that always triggers compaction
 constexpr int kSlice = 64 * 16;               // elements per wave slice (4 float4 per lane)
 constexpr int kWaveMinSeg = kW * kSlice;      // every wave has a full first slice (8192)
+constexpr long long kWaveMaxSeg = 1LL << 28;  // longest wave-kernel segment (32-bit byte offsets)
 
 __device__ __forceinline__ uint32_t f2key(float f, int largest) {
     uint32_t u = __float_as_uint(f);
@@ -113,8 +115,8 @@ struct TopkArgs {
 
 // Small shared state of the workgroup-level helpers.
 struct BlockScratch {
-    uint32_t wave_val[kW];
-    int wave_cnt[kW];
+    uint32_t wave_val[kMaxW];
+    int wave_cnt[kMaxW];
     uint32_t hist[256];
     int count;
     int count2;
@@ -385,19 +387,22 @@ __device__ __forceinline__ void write_segment(const TopkArgs& a, long long row, 
 // ---------------------------------------------------------------------------
 // Wave-independent segment kernel.
 // ---------------------------------------------------------------------------
+template <int NW>
 struct WaveShared {
-    unsigned long long wl[kW][kWB];    // per-wave candidate lists (16 KiB)
+    unsigned long long wl[NW][kWB];    // per-wave candidate lists (2 KiB per wave)
     union {
-        uint32_t hist[kW][256];        // per-wave histograms while streaming (8 KiB)
-        unsigned long long un[kB];     // gathered list afterwards (16 KiB)
+        uint32_t hist[NW][256];        // per-wave histograms while streaming
+        unsigned long long un[NW * kWB];  // gathered list afterwards
     };
     BlockScratch bs;
 };
-static_assert(kW * kWB == kB, "the per-wave lists double as a block-sized scratch list");
-static_assert(sizeof(int) * kB + sizeof(unsigned long long) * kKMax <= sizeof(unsigned long long) * kB,
-              "rank + sel must fit in one idle list");
+// After the gather the per-wave list area (NW * kWB composites) is idle: rank
+// (m <= NW * kWB ints) takes its first half and sel (k composites) its second.
+static_assert(kWaveK <= 8 * kWB / 2, "sel fits in the second half of the list area");
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kBufWord3 = 0x00020000;  // raw buffer resource, 32-bit data (gfx9 family)
+constexpr int kNT = 2;                 // cache policy bit: nontemporal (the row is read once)
 
 // 128-bit load marked nontemporal: the row is read once.
 __device__ __forceinline__ float4 ld4_nt(const float* p) {
@@ -405,50 +410,61 @@ __device__ __forceinline__ float4 ld4_nt(const float* p) {
     return make_float4(v.x, v.y, v.z, v.w);
 }
 
+// Segment loads go through a buffer resource whose range is the segment: the
+// hardware range check is per dword, so a load past the segment end returns 0
+// and moves no data.  Slice loads are therefore unconditional (a prefetch past
+// the last slice is free), which keeps the compiler's wait counts exact.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t segment_rsrc(const float* seg, int n) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(seg), (short)0, n * 4, kBufWord3);
+}
+
+// Loads slice elements [rel, rel + 256*SV) of the segment: lane l, vector j
+// gets elements rel + 4*(j*64 + l) .. +3.  VEC: 128-bit loads (16-byte aligned
+// segment); otherwise four 32-bit loads per vector.
 template <bool VEC, int SV>
-__device__ __forceinline__ void load_slice(float4 (&cur)[SV], const float* p, int base, int hi) {
+__device__ __forceinline__ void load_slice(float4 (&cur)[SV], __amdgpu_buffer_rsrc_t r, int rel) {
     const int lane = __lane_id();
-    if (VEC && base + 256 * SV <= hi) {
 #pragma unroll
-        for (int j = 0; j < SV; ++j) cur[j] = ld4_nt(p + base + 4 * (j * 64 + lane));
-    } else {
-#pragma unroll
-        for (int j = 0; j < SV; ++j) {
-            const int e = base + 4 * (j * 64 + lane);
-            float v[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int eq = e + q;
-                const float x = p[eq < hi ? eq : hi - 1];
-                v[q] = (eq < hi) ? x : 0.0f;
-            }
-            cur[j] = make_float4(v[0], v[1], v[2], v[3]);
+    for (int j = 0; j < SV; ++j) {
+        const int off = 4 * (rel + 4 * (j * 64 + lane));
+        if constexpr (VEC) {
+            const f32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kNT);
+            cur[j] = make_float4(v.x, v.y, v.z, v.w);
+        } else {
+            cur[j] = make_float4(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kNT),
+                                 __builtin_amdgcn_raw_buffer_load_b32(r, off + 4, 0, kNT),
+                                 __builtin_amdgcn_raw_buffer_load_b32(r, off + 8, 0, kNT),
+                                 __builtin_amdgcn_raw_buffer_load_b32(r, off + 12, 0, kNT));
         }
     }
 }
 
+// Sortable keys of one slice; elements at or past `hi` get key 0 (below every
+// threshold).  Branch-free: a select per element.
 template <int SV>
 __device__ __forceinline__ void slice_keys(const float4 (&cur)[SV], int base, int hi, int largest,
                                            uint32_t (&key)[4 * SV]) {
-    const int lane = __lane_id();
+    const int lim = hi - base - 4 * (int)__lane_id();  // element e = base + 4*lane + 256*j + q is valid iff 256*j + q < lim
 #pragma unroll
     for (int j = 0; j < SV; ++j) {
-        const int e = base + 4 * (j * 64 + lane);
-        key[4 * j + 0] = (e + 0 < hi) ? f2key(cur[j].x, largest) : 0u;
-        key[4 * j + 1] = (e + 1 < hi) ? f2key(cur[j].y, largest) : 0u;
-        key[4 * j + 2] = (e + 2 < hi) ? f2key(cur[j].z, largest) : 0u;
-        key[4 * j + 3] = (e + 3 < hi) ? f2key(cur[j].w, largest) : 0u;
+        key[4 * j + 0] = (256 * j + 0 < lim) ? f2key(cur[j].x, largest) : 0u;
+        key[4 * j + 1] = (256 * j + 1 < lim) ? f2key(cur[j].y, largest) : 0u;
+        key[4 * j + 2] = (256 * j + 2 < lim) ? f2key(cur[j].z, largest) : 0u;
+        key[4 * j + 3] = (256 * j + 3 < lim) ? f2key(cur[j].w, largest) : 0u;
     }
 }
 
-template <bool VEC, int SV, int OCC, bool PF>
-__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(OCC, 8))) void k_topk_wave(TopkArgs a) {
+template <bool VEC, int SV, int OCC, int PD, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8))) void k_topk_wave(TopkArgs a) {
     constexpr int kSl = 256 * SV;  // elements per wave slice
-    __shared__ WaveShared sh;
+    constexpr int kW = NW;         // waves of this workgroup
+    constexpr int kT = NW * 64;
+    constexpr int kB = NW * kWB;   // gathered-list capacity
+    __shared__ WaveShared<NW> sh;
     BlockScratch& bs = sh.bs;
     const int tid = threadIdx.x;
     const int lane = __lane_id();
-    const int w = tid / 64;
+    const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave-uniform: scalar loop control
     const long long row = blockIdx.x / a.nseg;
     const int seg = blockIdx.x % a.nseg;
     const float* p = a.in + row * a.row_stride;
@@ -468,14 +484,20 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(OCC, 8))) vo
         bs.over = a.force_fallback;
     }
 
-    // first slice of every wave gives the workgroup bound T0
-    float4 cur[SV];
+    // Wave slices are w, w+8, w+16, ...  PD = slices whose loads are in flight
+    // while the current one is filtered (0: load, wait, filter; 1: the next
+    // slice's load is issued as soon as the current one has become keys; 2: two
+    // register buffers alternate, so two slices are in flight).
+    float4 bufA[SV];
+    float4 bufB[PD == 2 ? SV : 1];
     uint32_t key[4 * SV];
-    load_slice<VEC, SV>(cur, p, lo + w * kSl, hi);
-    slice_keys(cur, lo + w * kSl, hi, largest, key);
-    // prefetch: the next slice is loaded into `cur` as soon as the current one
-    // has become keys, so its latency overlaps the work on the current slice
-    if (PF && w + kW < nsl) load_slice<VEC, SV>(cur, p, lo + (w + kW) * kSl, hi);
+    const __amdgpu_buffer_rsrc_t rs = segment_rsrc(p + lo, hi - lo);
+    load_slice<VEC, SV>(bufA, rs, w * kSl);
+    if constexpr (PD == 2) load_slice<VEC, SV>(bufB, rs, (w + kW) * kSl);
+    slice_keys(bufA, lo + w * kSl, hi, largest, key);
+    if constexpr (PD == 1) load_slice<VEC, SV>(bufA, rs, (w + kW) * kSl);
+    if constexpr (PD == 2) load_slice<VEC, SV>(bufA, rs, (w + 2 * kW) * kSl);
+    // the first slice of every wave gives the workgroup bound T0
     const uint32_t rth = wave_rth_of_lane_max(key, 4 * SV, r);
     if (lane == 0) bs.wave_val[w] = rth;
     __syncthreads();
@@ -486,14 +508,9 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(OCC, 8))) vo
     bool over = bs.over != 0;
     int cnt = 0;  // this wave's list length (wave-uniform)
 
-    // streaming loop: no workgroup barriers
-    for (int c = w; c < nsl && !over; c += kW) {
-        const int base = lo + c * kSl;
-        if (c != w) {
-            if (!PF) load_slice<VEC, SV>(cur, p, base, hi);
-            slice_keys(cur, base, hi, largest, key);
-            if (PF && c + kW < nsl) load_slice<VEC, SV>(cur, p, lo + (c + kW) * kSl, hi);
-        }
+    // Appends the slice's keys >= T to the wave list; false when the list
+    // cannot take them (the workgroup then takes the exact path).
+    auto filter = [&](int base) -> bool {
         T = max(T, __atomic_load_n(&bs.tshared, __ATOMIC_RELAXED));
         int total = 0;
 #pragma unroll
@@ -508,11 +525,9 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(OCC, 8))) vo
 #pragma unroll
                 for (int q = 0; q < 4 * SV; ++q) total += __popcll(__ballot(key[q] >= T));
             } else if (cnt == before) {
-                over = true;  // nothing could be dropped: take the exact path
-                break;
+                return false;  // nothing could be dropped
             }
         }
-        if (over) break;
         if (total) {
             const unsigned long long lt = lanemask_lt();
             int pos = cnt;
@@ -534,7 +549,38 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(OCC, 8))) vo
                 T = tn;
             }
         }
-        if (__atomic_load_n(&bs.over, __ATOMIC_RELAXED)) over = true;
+        return __atomic_load_n(&bs.over, __ATOMIC_RELAXED) == 0;
+    };
+
+    // streaming loop: no workgroup barriers
+    if (!over) {
+        int c = w;
+        if constexpr (PD == 2) {
+            for (;;) {
+                if (!filter(lo + c * kSl)) { over = true; break; }
+                c += kW;
+                if (c >= nsl) break;
+                slice_keys(bufB, lo + c * kSl, hi, largest, key);
+                load_slice<VEC, SV>(bufB, rs, (c + 2 * kW) * kSl);
+                if (!filter(lo + c * kSl)) { over = true; break; }
+                c += kW;
+                if (c >= nsl) break;
+                slice_keys(bufA, lo + c * kSl, hi, largest, key);
+                load_slice<VEC, SV>(bufA, rs, (c + 2 * kW) * kSl);
+            }
+        } else {
+            for (; c < nsl; c += kW) {
+                const int base = lo + c * kSl;
+                if (c != w) {
+                    if constexpr (PD == 0) load_slice<VEC, SV>(bufA, rs, c * kSl);
+                    slice_keys(bufA, base, hi, largest, key);
+                    if constexpr (PD == 1) {
+                        load_slice<VEC, SV>(bufA, rs, (c + kW) * kSl);
+                    }
+                }
+                if (!filter(base)) { over = true; break; }
+            }
+        }
     }
     if (over && lane == 0) __atomic_store_n(&bs.over, 1, __ATOMIC_RELAXED);
     __syncthreads();
@@ -733,25 +779,32 @@ struct TopkPlan {
     int nseg;
     int seg_len;
     bool wave;
+    int nw;  // waves per wave-kernel workgroup (8 or 16)
     size_t ws;
 };
 
-// Segments: >= 2 segment workgroups per CU when rows are few, >= 2 units per
-// segment, every segment holding >= k elements (and, for the wave kernel, a full
-// first slice per wave), and a merge list that fits one merge workgroup.
+// Grid: about 2 * CUs 512-thread workgroups (or CUs 1024-thread ones).  Many
+// rows: one 512-thread workgroup per row.  Fewer rows than that: the wave
+// kernel gives each row a 1024-thread workgroup and cuts rows into segments
+// only when rows < CUs.  Every segment holds >= k elements (and, for the wave
+// kernel, a full first slice per wave), and the merge list fits one merge
+// workgroup.
 TopkPlan plan_topk(long long rows, long long cols, long long k) {
-    TopkPlan pl{1, (int)cols, false, 0};
+    TopkPlan pl{1, (int)cols, false, 8, 0};
+    const int cus = device_info().cus;
     const bool wave_ok = k <= kWaveK && cols >= kWaveMinSeg;
-    const long long unit = wave_ok ? kWaveMinSeg : kCH;
+    const int nw = (wave_ok && rows < 2LL * cus && cols >= 2 * kWaveMinSeg) ? 16 : 8;
+    const long long unit = wave_ok ? (long long)nw * kSlice : kCH;
     const long long units = (cols + unit - 1) / unit;
-    const long long want = 2LL * device_info().cus;
+    const long long want = (nw == 16) ? cus : 2LL * cus;
     const long long merge_cap = std::max(1LL, (long long)kMergeMax / std::max(1LL, k));
     long long nseg = 1;
     if (rows < want) nseg = (want + rows - 1) / rows;
     nseg = std::min(nseg, std::max(1LL, units / 2));
+    if (wave_ok) nseg = std::max(nseg, (cols + kWaveMaxSeg - 1) / kWaveMaxSeg);
     if (knobs().splits > 0) nseg = knobs().splits;
     nseg = std::max(1LL, std::min(nseg, merge_cap));
-    const long long min_last = wave_ok ? std::max<long long>(k, kWaveMinSeg) : k;
+    const long long min_last = wave_ok ? std::max<long long>(k, unit) : k;
     for (; nseg > 1; --nseg) {
         const long long seg_len = (units + nseg - 1) / nseg * unit;
         const long long n = (cols + seg_len - 1) / seg_len;
@@ -763,7 +816,10 @@ TopkPlan plan_topk(long long rows, long long cols, long long k) {
         }
         if (n == 1) break;
     }
-    pl.wave = wave_ok;
+    // wave-kernel byte offsets are 32-bit: segments stay below 2^28 elements
+    pl.wave = wave_ok && pl.seg_len <= kWaveMaxSeg;
+    pl.nw = nw;
+    if (knobs().topk_waves == 8 || knobs().topk_waves == 16) pl.nw = (int)knobs().topk_waves;
     pl.ws = pl.nseg > 1 ? (size_t)rows * pl.nseg * k * sizeof(unsigned long long) : 0;
     return pl;
 }
@@ -812,14 +868,23 @@ int tpr_topk(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t 
     hipStream_t st = static_cast<hipStream_t>(stream);
     const long long grid = rows * pl.nseg;
     if (pl.wave) {
-        // Many rows: 8 waves/SIMD (4 workgroups per CU) without prefetch.
-        // Few, split rows: 7 waves/SIMD with a one-slice prefetch per wave.
+        // 512-thread workgroups (many rows): 8 waves/SIMD without prefetch.
+        // 1024-thread workgroups (few rows): one slice prefetched per wave.
         // (Measured on MI355X at [1024, 32768] k=64 and [256, 151936] k=50.)
         long long var = knobs().topk_variant;
-        if (var == 0) var = pl.nseg == 1 ? 1 : 2;
-        if (!vec) hipLaunchKernelGGL((k_topk_wave<false, 4, 6, true>), dim3(grid), dim3(kT), 0, st, a);
-        else if (var == 1) hipLaunchKernelGGL((k_topk_wave<true, 4, 8, false>), dim3(grid), dim3(kT), 0, st, a);
-        else hipLaunchKernelGGL((k_topk_wave<true, 4, 6, true>), dim3(grid), dim3(kT), 0, st, a);
+        if (var == 0) var = pl.nw == 16 ? 2 : (pl.nseg == 1 ? 1 : 2);
+        const dim3 blk(pl.nw * 64);
+        if (pl.nw == 16) {
+            if (!vec) hipLaunchKernelGGL((k_topk_wave<false, 4, 4, 1, 16>), dim3(grid), blk, 0, st, a);
+            else if (var == 1) hipLaunchKernelGGL((k_topk_wave<true, 4, 4, 0, 16>), dim3(grid), blk, 0, st, a);
+            else if (var == 3) hipLaunchKernelGGL((k_topk_wave<true, 4, 4, 2, 16>), dim3(grid), blk, 0, st, a);
+            else hipLaunchKernelGGL((k_topk_wave<true, 4, 4, 1, 16>), dim3(grid), blk, 0, st, a);
+        } else {
+            if (!vec) hipLaunchKernelGGL((k_topk_wave<false, 4, 6, 1, 8>), dim3(grid), blk, 0, st, a);
+            else if (var == 1) hipLaunchKernelGGL((k_topk_wave<true, 4, 8, 0, 8>), dim3(grid), blk, 0, st, a);
+            else if (var == 3) hipLaunchKernelGGL((k_topk_wave<true, 4, 4, 2, 8>), dim3(grid), blk, 0, st, a);
+            else hipLaunchKernelGGL((k_topk_wave<true, 4, 6, 1, 8>), dim3(grid), blk, 0, st, a);
+        }
     } else {
         if (vec) hipLaunchKernelGGL((k_topk_block<true>), dim3(grid), dim3(kT), 0, st, a);
         else hipLaunchKernelGGL((k_topk_block<false>), dim3(grid), dim3(kT), 0, st, a);

@@ -14,7 +14,7 @@ torch = pytest.importorskip("torch")
 @pytest.fixture(autouse=True)
 def _reset_knobs():
     yield
-    for k in ("topk_fallback", "topk_variant", "splits"):
+    for k in ("topk_fallback", "topk_variant", "topk_waves", "splits"):
         _capi.debug_set(k, 0)
 
 
@@ -83,11 +83,14 @@ def test_config5_peaked_logits():
     check(x, x, 50)
 
 
-@pytest.mark.parametrize("variant", [1, 2])
+@pytest.mark.parametrize("waves", [8, 16])
+@pytest.mark.parametrize("variant", [1, 2, 3])
 @pytest.mark.parametrize("splits", [0, 1, 2, 3, 5])
-def test_wave_kernel_variants_and_segments(variant, splits):
-    # both wave-kernel variants, rows cut into 1..5 segments (merge pass)
+def test_wave_kernel_variants_and_segments(variant, splits, waves):
+    # wave-kernel prefetch depths and workgroup sizes, rows cut into 1..5
+    # segments (merge pass)
     _capi.debug_set("topk_variant", variant)
+    _capi.debug_set("topk_waves", waves)
     _capi.debug_set("splits", splits)
     rng = np.random.default_rng(24 + splits)
     x = rng.standard_normal((6, 50000)).astype(np.float32)
@@ -98,12 +101,14 @@ def test_wave_kernel_variants_and_segments(variant, splits):
             check(x, x, k, largest)
 
 
-@pytest.mark.parametrize("variant", [1, 2])
-def test_rising_rows_stale_candidates(variant):
+@pytest.mark.parametrize("waves", [8, 16])
+@pytest.mark.parametrize("variant", [1, 2, 3])
+def test_rising_rows_stale_candidates(variant, waves):
     # Values trend upwards along the row, so every wave keeps finding better
     # elements, compacts repeatedly and raises the shared bound while other
     # waves still hold entries admitted under older, lower bounds.
     _capi.debug_set("topk_variant", variant)
+    _capi.debug_set("topk_waves", waves)
     rng = np.random.default_rng(25)
     n = 65536
     trend = np.linspace(0, 50, n, dtype=np.float32)
@@ -112,3 +117,20 @@ def test_rising_rows_stale_candidates(variant):
     for k in (1, 17, 64, 128):
         check(x, x, k, True)
         check(x, x, k, False)
+
+
+@pytest.mark.parametrize("waves", [8, 16])
+@pytest.mark.parametrize("variant", [1, 2, 3])
+def test_single_row_ragged_end(variant, waves):
+    # one aligned row whose length is not a multiple of 4: the last 128-bit
+    # load straddles the row end (the segment range check zeroes the rest)
+    _capi.debug_set("topk_variant", variant)
+    _capi.debug_set("topk_waves", waves)
+    rng = np.random.default_rng(26)
+    for n in (50003, 65537, 16387):
+        x = rng.standard_normal((1, n)).astype(np.float32)
+        x[0, n - 1] = 100.0  # the last element is the maximum
+        x[0, n - 3] = 99.0
+        for k in (1, 3, 64):
+            check(x, x, k, True)
+            check(x, x, k, False)
