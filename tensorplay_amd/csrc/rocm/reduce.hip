@@ -666,9 +666,11 @@ Plan make_plan(const tpr_reduce_desc* d, const void* in) {
                                    pow2_ceil(ceil_div((long long)dev.cus * 4096, p.rows)));
         lanes = std::min(256LL, std::max(16LL, std::min(lanes, pow2_ceil(ceil_div(p.R, 4)))));
         const long long target = (long long)dev.cus * 512;
-        // few long rows: give one row a 512- or 1024-thread workgroup before
-        // splitting it over workgroups (a split costs a finalize launch)
-        while (p.rows * lanes < 2 * target && lanes < 1024 && 16 * 2 * lanes <= p.R) lanes *= 2;
+        // few long rows: give one row a 512- or 1024-thread workgroup when that
+        // avoids splitting rows over workgroups (a split costs a finalize
+        // launch); rows that need a split anyway keep 256-thread workgroups
+        if (p.rows * 1024 >= target)
+            while (p.rows * lanes < 2 * target && lanes < 1024 && 16 * 2 * lanes <= p.R) lanes *= 2;
         if (knobs().lanes > 0) lanes = knobs().lanes;
         p.lanes = (int)lanes;
         const long long tiles = std::max(1LL, ceil_div(p.R, 16 * lanes));  // 4 vectors x 4 floats per lane

@@ -134,3 +134,23 @@ def test_single_row_ragged_end(variant, waves):
         for k in (1, 3, 64):
             check(x, x, k, True)
             check(x, x, k, False)
+
+
+@pytest.mark.parametrize("waves", [8, 16])
+def test_denormals_signed_zeros_and_infinities(waves):
+    # Thresholds that land on +-0, denormals and +-inf: the float-domain filter
+    # must agree with the key order (denormals kept, -0.0 == +0.0).
+    _capi.debug_set("topk_waves", waves)
+    rng = np.random.default_rng(27)
+    n = 40000
+    tiny = np.float32(1e-45)  # smallest denormal
+    pool = np.array([0.0, -0.0, tiny, -tiny, 3 * tiny, -3 * tiny, 1e-39, -1e-39,
+                     np.inf, -np.inf, 1.0, -1.0], np.float32)
+    x = pool[rng.integers(0, len(pool), size=(4, n))]
+    x[1] = np.where(rng.random(n) < 0.5, np.float32(0.0), np.float32(-0.0))
+    x[2, ::7] = np.nan
+    x[3] = -np.inf
+    x[3, 17] = -1e-39
+    for k in (1, 5, 64, 128):
+        check(x, x, k, True)
+        check(x, x, k, False)
