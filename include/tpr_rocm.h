@@ -53,7 +53,12 @@ enum tpr_reduce_op {
     TPR_ARGMAX = 4, /* argmax_kernel :682-746                                  */
     TPR_ARGMIN = 5, /* argmin_kernel :748-812                                  */
     TPR_VAR = 6,    /* var_kernel :817-827, var_dim_kernel :829-847            */
-    TPR_STD = 7     /* std_kernel :849-851, std_dim_kernel :853-855            */
+    TPR_STD = 7,    /* std_kernel :849-851, std_dim_kernel :853-855            */
+    TPR_PROD = 8,   /* prod_kernel :406-439, prod_dim_kernel :441-514          */
+    TPR_NORM = 9,   /* norm_kernel :858-864, norm_dim_kernel :866-872 (p = desc.p) */
+    TPR_ALL = 10,   /* all_kernel :517-539, all_dim_kernel :565-620            */
+    TPR_ANY = 11,   /* any_kernel :541-563, any_dim_kernel :622-677            */
+    TPR_MEDIAN = 12 /* median_kernel :874-901 (full reductions only)           */
 };
 
 /* One reduction over an arbitrary strided view.
@@ -62,16 +67,23 @@ enum tpr_reduce_op {
  *    ndim == 0) is a full reduction to one value.
  *  - The output is written densely (row-major over the kept dims, in their
  *    original order); keepdim only changes the shape the caller reports.
- *  - out_dtype: SUM/MEAN: FLOAT32 or FLOAT64.  AMAX/AMIN: the input dtype.
- *    ARGMAX/ARGMIN: INT64 (index along the reduced dims, row-major; first
- *    index wins ties; NaN never wins, as the reference's strict compare).
- *    VAR/STD: FLOAT32.
+ *  - out_dtype: SUM/MEAN/PROD: FLOAT32 or FLOAT64.  AMAX/AMIN: the input
+ *    dtype.  ARGMAX/ARGMIN: INT64 (index along the reduced dims, row-major;
+ *    first index wins ties; NaN never wins, as the reference's strict
+ *    compare).  VAR/STD/NORM/MEDIAN: FLOAT32.  ALL/ANY: BOOL (one byte, 0/1;
+ *    an element counts as true when it is != 0, so NaN is true).
+ *  - NORM: (sum |x|^p)^(1/p); p = +inf / -inf: max / min of |x| (NaN ignored,
+ *    as AMAX/AMIN); p = 0 gives the reference's n^(1/0).
+ *  - MEDIAN: lower median ((n-1)/2-th smallest) of all elements; -0.0 == +0.0
+ *    (a zero median is returned as +0.0); NaN ranks above every number.  Only
+ *    full reductions of a contiguous view (TPR_ERR_NOT_IMPLEMENTED otherwise).
  *  - count_override > 0 replaces the element count used by MEAN/VAR/STD (the
  *    reference multiplies the size of every listed dim, duplicates included,
  *    ReductionKernels.cpp:203-208 and :840-845); 0 = product of reduced sizes.
  *  - correction: VAR/STD divisor is max(0, count - correction).
  * An empty reduced extent writes: SUM 0, MEAN NaN, AMAX -inf, AMIN +inf,
- * ARGMAX/ARGMIN 0, VAR/STD NaN (the reference's full max/min raise instead;
+ * ARGMAX/ARGMIN 0, VAR/STD NaN, PROD 1, ALL 1, ANY 0, NORM 0^(1/p) (-inf / +inf
+ * for p = +inf / -inf), MEDIAN NaN (the reference's full max/min raise instead;
  * the adapters check that before calling). */
 typedef struct tpr_reduce_desc {
     int32_t op;          /* enum tpr_reduce_op */
@@ -84,6 +96,7 @@ typedef struct tpr_reduce_desc {
     int32_t reserved0;
     int64_t correction;
     int64_t count_override;
+    double p;            /* NORM exponent (ignored by the other ops) */
 } tpr_reduce_desc;
 
 /* Bytes of device workspace tpr_reduce needs for this descriptor (0 is

@@ -47,6 +47,13 @@ def lib():
         L.or_argminmax_dim.argtypes = [vp, i32, _i64p, _i64p, i32, i32, i32, vp]
         L.or_var_all.argtypes = [vp, i32, _i64p, _i64p, i64, i32]; L.or_var_all.restype = ctypes.c_float
         L.or_var_dim.argtypes = [vp, i32, _i64p, _i64p, u32, _i64p, i32, i64, i32, vp]
+        L.or_prod_all.argtypes = [vp, i32, _i64p, _i64p]; L.or_prod_all.restype = ctypes.c_float
+        L.or_prod_dim.argtypes = [vp, i32, _i64p, _i64p, u32, vp]
+        L.or_allany_all.argtypes = [vp, i32, _i64p, _i64p, i32]; L.or_allany_all.restype = i32
+        L.or_allany_dim.argtypes = [vp, i32, _i64p, _i64p, u32, i32, vp]
+        L.or_norm_all.argtypes = [vp, i32, _i64p, _i64p, ctypes.c_double, _f32p]; L.or_norm_all.restype = i32
+        L.or_norm_dim.argtypes = [vp, i32, _i64p, _i64p, u32, ctypes.c_double, vp]
+        L.or_median.argtypes = [vp, i32, _i64p, _i64p]; L.or_median.restype = ctypes.c_float
         L.or_topk.argtypes = [vp, i64, i64, i64, i64, i32, vp, vp]
         L.or_topk_mt.argtypes = [vp, i64, i64, i64, i64, i32, vp, vp, i32]
         _lib = L
@@ -160,6 +167,52 @@ def var(x, dims=None, correction=1, keepdim=False, take_sqrt=False):
 
 def std(x, dims=None, correction=1, keepdim=False):
     return var(x, dims, correction, keepdim, take_sqrt=True)
+
+
+def prod(x, dims=None, keepdim=False):
+    L = lib()
+    p, nd, sz, st = _geom(x)
+    if not dims:
+        return np.float32(L.or_prod_all(p, nd, sz, st))
+    dd = _wrap_dims(nd, dims)
+    out = np.empty(_reduced_shape(x.shape, dd, keepdim), np.float32)
+    L.or_prod_dim(p, nd, sz, st, _mask(dd), ctypes.c_void_p(out.ctypes.data))
+    return out
+
+
+def all_(x, dims=None, keepdim=False, is_any=False):
+    L = lib()
+    p, nd, sz, st = _geom(x)
+    if not dims:
+        return np.bool_(L.or_allany_all(p, nd, sz, st, int(is_any)))
+    dd = _wrap_dims(nd, dims)
+    out = np.empty(_reduced_shape(x.shape, dd, keepdim), np.uint8)
+    L.or_allany_dim(p, nd, sz, st, _mask(dd), int(is_any), ctypes.c_void_p(out.ctypes.data))
+    return out.astype(np.bool_)
+
+
+def any_(x, dims=None, keepdim=False):
+    return all_(x, dims, keepdim, is_any=True)
+
+
+def norm(x, p=2.0, dims=None, keepdim=False):
+    L = lib()
+    ptr, nd, sz, st = _geom(x)
+    if not dims:
+        v = ctypes.c_float()
+        if L.or_norm_all(ptr, nd, sz, st, float(p), ctypes.byref(v)) != 0:
+            raise RuntimeError("max(): Expected reduction dim to be non-empty")
+        return np.float32(v.value)
+    dd = _wrap_dims(nd, dims)
+    out = np.empty(_reduced_shape(x.shape, dd, keepdim), np.float32)
+    L.or_norm_dim(ptr, nd, sz, st, _mask(dd), float(p), ctypes.c_void_p(out.ctypes.data))
+    return out
+
+
+def median(x):
+    L = lib()
+    p, nd, sz, st = _geom(x)
+    return np.float32(L.or_median(p, nd, sz, st))
 
 
 def topk(x2d, k, largest=True, threads=1):

@@ -340,3 +340,130 @@ void or_topk_mt(const float* x, int64_t rows, int64_t cols, int64_t row_stride, 
     }
     for (int t = 0; t < used; ++t) pthread_join(th[t], NULL);
 }
+
+/* ---- prod / all / any / norm / median (ReductionKernels.cpp:406-677, :858-901) ---- */
+
+/* prod_kernel (:406-439): out dtype float32 for float input, `ctype prod_val = 1`
+ * multiplied sequentially in float over the contiguous copy. */
+float or_prod_all(const float* x, int ndim, const int64_t* sizes, const int64_t* strides) {
+    int64_t n = numel_of(ndim, sizes);
+    float acc = 1.0f;
+    for (int64_t i = 0; i < n; ++i) acc = acc * x[logical_offset(ndim, sizes, strides, i)];
+    return acc;
+}
+
+/* prod_dim_kernel (:441-514): out = ones, out[o] *= x (float) in walk order. */
+void or_prod_dim(const float* x, int ndim, const int64_t* sizes, const int64_t* strides,
+                 uint32_t reduce_mask, float* out) {
+    walk_t w; walk_init(&w, ndim, sizes, strides, reduce_mask);
+    int64_t no = kept_numel(ndim, sizes, reduce_mask);
+    for (int64_t i = 0; i < no; ++i) out[i] = 1.0f;
+    WALK_BEGIN(&w)
+        out[out_off] = out[out_off] * x[in_off];
+    WALK_END(&w)
+}
+
+/* all_kernel / any_kernel (:517-563): static_cast<bool>(x), i.e. x != 0 (NaN is
+ * true); empty all = true, empty any = false. */
+int or_allany_all(const float* x, int ndim, const int64_t* sizes, const int64_t* strides, int is_any) {
+    int64_t n = numel_of(ndim, sizes);
+    for (int64_t i = 0; i < n; ++i) {
+        int b = x[logical_offset(ndim, sizes, strides, i)] != 0.0f;
+        if (is_any && b) return 1;
+        if (!is_any && !b) return 0;
+    }
+    return is_any ? 0 : 1;
+}
+
+/* all_dim_kernel / any_dim_kernel (:565-677): out initialised to 1 / 0. */
+void or_allany_dim(const float* x, int ndim, const int64_t* sizes, const int64_t* strides,
+                   uint32_t reduce_mask, int is_any, uint8_t* out) {
+    walk_t w; walk_init(&w, ndim, sizes, strides, reduce_mask);
+    int64_t no = kept_numel(ndim, sizes, reduce_mask);
+    for (int64_t i = 0; i < no; ++i) out[i] = is_any ? 0 : 1;
+    WALK_BEGIN(&w)
+        int b = x[in_off] != 0.0f;
+        if (is_any && b) out[out_off] = 1;
+        if (!is_any && !b) out[out_off] = 0;
+    WALK_END(&w)
+}
+
+/* abs().pow(Scalar(p)) (PointwiseKernels.cpp:392-395): std::pow(float, double)
+ * in double, stored as float. */
+static float abs_pow(float v, double p) { return (float)pow((double)fabsf(v), p); }
+
+/* norm_kernel (:858-864).  p = +-inf: abs().max() / abs().min() (max_kernel's
+ * strict compare; returns -1 for an empty tensor, which raises there).
+ * Otherwise abs().pow(p).sum() (double accumulation, :94) then .pow(1/p) on the
+ * float result. */
+int or_norm_all(const float* x, int ndim, const int64_t* sizes, const int64_t* strides, double p,
+                float* out) {
+    int64_t n = numel_of(ndim, sizes);
+    if (isinf(p)) {
+        if (n == 0) return -1;
+        int is_max = p > 0;
+        float best = is_max ? -INFINITY : INFINITY;
+        for (int64_t i = 0; i < n; ++i) {
+            float v = fabsf(x[logical_offset(ndim, sizes, strides, i)]);
+            if (is_max ? (v > best) : (v < best)) best = v;
+        }
+        *out = best;
+        return 0;
+    }
+    double acc = 0.0;
+    for (int64_t i = 0; i < n; ++i) acc += (double)abs_pow(x[logical_offset(ndim, sizes, strides, i)], p);
+    *out = (float)pow((double)(float)acc, 1.0 / p);
+    return 0;
+}
+
+/* norm_dim_kernel (:866-872): abs().pow(p).sum(dim) (fp32 accumulation in walk
+ * order, :157-178) then .pow(1/p); p = +-inf: abs().max(dim) / min(dim). */
+void or_norm_dim(const float* x, int ndim, const int64_t* sizes, const int64_t* strides,
+                 uint32_t reduce_mask, double p, float* out) {
+    walk_t w; walk_init(&w, ndim, sizes, strides, reduce_mask);
+    int64_t no = kept_numel(ndim, sizes, reduce_mask);
+    if (isinf(p)) {
+        int is_max = p > 0;
+        for (int64_t i = 0; i < no; ++i) out[i] = is_max ? -INFINITY : INFINITY;
+        WALK_BEGIN(&w)
+            float v = fabsf(x[in_off]);
+            if (is_max ? (v > out[out_off]) : (v < out[out_off])) out[out_off] = v;
+        WALK_END(&w)
+        return;
+    }
+    for (int64_t i = 0; i < no; ++i) out[i] = 0.0f;
+    WALK_BEGIN(&w)
+        out[out_off] = out[out_off] + abs_pow(x[in_off], p);
+    WALK_END(&w)
+    for (int64_t i = 0; i < no; ++i) out[i] = (float)pow((double)out[i], 1.0 / p);
+}
+
+/* median_kernel (:874-901): the (n-1)/2-th smallest element of the flattened
+ * tensor; NaN for an empty one.  std::nth_element leaves the order of NaN and of
+ * -0.0 vs +0.0 unspecified; this restatement fixes it as the build's median does:
+ * ascending sortable keys, -0.0 == +0.0 (returned as +0.0), NaN above +inf. */
+static inline uint32_t asc_key(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) u = 0x7fc00000u;
+    if (u == 0x80000000u) u = 0u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+static int cmp_u32(const void* a, const void* b) {
+    uint32_t x = *(const uint32_t*)a, y = *(const uint32_t*)b;
+    return (x > y) - (x < y);
+}
+float or_median(const float* x, int ndim, const int64_t* sizes, const int64_t* strides) {
+    int64_t n = numel_of(ndim, sizes);
+    if (n == 0) return NAN;
+    uint32_t* k = (uint32_t*)malloc((size_t)n * sizeof(uint32_t));
+    for (int64_t i = 0; i < n; ++i) k[i] = asc_key(x[logical_offset(ndim, sizes, strides, i)]);
+    qsort(k, (size_t)n, sizeof(uint32_t), cmp_u32);
+    uint32_t key = k[(n - 1) / 2];
+    free(k);
+    uint32_t bits = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
+    float v;
+    memcpy(&v, &bits, 4);
+    return v;
+}
+

@@ -46,6 +46,22 @@ float or_var_all(const float* x, int ndim, const int64_t* sizes, const int64_t* 
 void or_var_dim(const float* x, int ndim, const int64_t* sizes, const int64_t* strides,
                 uint32_t reduce_mask, const int64_t* dims_list, int n_dims_list,
                 int64_t correction, int take_sqrt, float* out);
+/* prod_kernel / prod_dim_kernel (:406-514): float multiplies, sequential. */
+float or_prod_all(const float* x, int ndim, const int64_t* sizes, const int64_t* strides);
+void or_prod_dim(const float* x, int ndim, const int64_t* sizes, const int64_t* strides,
+                 uint32_t reduce_mask, float* out);
+/* all/any (:517-677): x != 0 is true (NaN true).  out is one byte per output. */
+int or_allany_all(const float* x, int ndim, const int64_t* sizes, const int64_t* strides, int is_any);
+void or_allany_dim(const float* x, int ndim, const int64_t* sizes, const int64_t* strides,
+                   uint32_t reduce_mask, int is_any, uint8_t* out);
+/* norm_kernel / norm_dim_kernel (:858-872).  or_norm_all returns -1 for p = +-inf
+ * on an empty tensor (the reference raises there). */
+int or_norm_all(const float* x, int ndim, const int64_t* sizes, const int64_t* strides, double p,
+                float* out);
+void or_norm_dim(const float* x, int ndim, const int64_t* sizes, const int64_t* strides,
+                 uint32_t reduce_mask, double p, float* out);
+/* median_kernel (:874-901): lower median; NaN for an empty tensor. */
+float or_median(const float* x, int ndim, const int64_t* sizes, const int64_t* strides);
 /* a11: topk (absent from the reference; this build's definition).  Rows of a
  * [rows, cols] view with row_stride.  Order: key descending, index ascending,
  * where key canonicalises -0.0 to +0.0 and treats NaN as the largest value.

@@ -108,6 +108,26 @@ def std(input, dim=None, correction=1, keepdim=False):
     return input.std(correction) if dim is None else input.std(dim, correction, keepdim)
 
 
+def prod(input, dim=None, keepdim=False, dtype=None):
+    return input.prod(dtype=dtype) if dim is None else input.prod(dim, keepdim, dtype=dtype)
+
+
+def all(input, dim=None, keepdim=False):
+    return input.all() if dim is None else input.all(dim, keepdim)
+
+
+def any(input, dim=None, keepdim=False):
+    return input.any() if dim is None else input.any(dim, keepdim)
+
+
+def median(input):
+    return input.median()
+
+
+def norm(input, p=2.0, dim=None, keepdim=False):
+    return input.norm(p) if dim is None else input.norm(dim, p, keepdim)
+
+
 def topk(input, k, dim=-1, largest=True, sorted=True):
     return input.topk(k, dim, largest, sorted)
 

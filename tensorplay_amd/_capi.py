@@ -21,9 +21,10 @@ OK, ERR_INVALID_ARG, ERR_UNSUPPORTED_DTYPE, ERR_HIP, ERR_WORKSPACE, ERR_NOT_IMPL
 # enum tpr_dtype (P10 ScalarType numbering)
 UINT8, INT8, INT16, INT32, INT64, UINT16, UINT32, UINT64, FLOAT32, FLOAT64, BOOL = range(11)
 # enum tpr_reduce_op
-SUM, MEAN, AMAX, AMIN, ARGMAX, ARGMIN, VAR, STD = range(8)
+SUM, MEAN, AMAX, AMIN, ARGMAX, ARGMIN, VAR, STD, PROD, NORM, ALL, ANY, MEDIAN = range(13)
 OP_NAMES = {"sum": SUM, "mean": MEAN, "amax": AMAX, "amin": AMIN, "argmax": ARGMAX,
-            "argmin": ARGMIN, "var": VAR, "std": STD}
+            "argmin": ARGMIN, "var": VAR, "std": STD, "prod": PROD, "norm": NORM, "all": ALL,
+            "any": ANY, "median": MEDIAN}
 
 EXPORTED = ["tpr_reduce_workspace_bytes", "tpr_reduce", "tpr_topk_workspace_bytes", "tpr_topk",
             "tpr_copy_strided", "tpr_last_error", "tpr_abi_version", "tpr_debug_set"]
@@ -47,6 +48,7 @@ class ReduceDesc(ctypes.Structure):
         ("reserved0", ctypes.c_int32),
         ("correction", ctypes.c_int64),
         ("count_override", ctypes.c_int64),
+        ("p", ctypes.c_double),
     ]
 
 
@@ -92,7 +94,7 @@ def debug_set(key, value):
 
 
 def make_desc(op, shape, strides, reduce_dims, out_dtype, correction=1, count_override=0,
-              in_dtype=FLOAT32):
+              in_dtype=FLOAT32, p=2.0):
     d = ReduceDesc()
     d.op = OP_NAMES[op] if isinstance(op, str) else op
     d.in_dtype = in_dtype
@@ -109,6 +111,7 @@ def make_desc(op, shape, strides, reduce_dims, out_dtype, correction=1, count_ov
     d.reduce_mask = m
     d.correction = correction
     d.count_override = count_override
+    d.p = p
     return d
 
 
@@ -118,10 +121,14 @@ def _stream(torch, device):
 
 def default_out_dtype(op):
     op = OP_NAMES[op] if isinstance(op, str) else op
-    return INT64 if op in (ARGMAX, ARGMIN) else FLOAT32
+    if op in (ARGMAX, ARGMIN):
+        return INT64
+    if op in (ALL, ANY):
+        return BOOL
+    return FLOAT32
 
 
-def reduce(x, op, dims=None, correction=1, out_dtype=None, count_override=0):
+def reduce(x, op, dims=None, correction=1, out_dtype=None, count_override=0, p=2.0):
     """Reduce a float32 CUDA(ROCm) torch tensor over `dims` (None = all).
 
     Returns a dense torch tensor of the kept dims' shape (keepdim=False)."""
@@ -133,9 +140,9 @@ def reduce(x, op, dims=None, correction=1, out_dtype=None, count_override=0):
         rd = sorted(set((d + nd) if d < 0 else d for d in dims))
     kept = [x.shape[i] for i in range(nd) if i not in rd]
     od = default_out_dtype(op) if out_dtype is None else out_dtype
-    tdt = {FLOAT32: torch.float32, FLOAT64: torch.float64, INT64: torch.int64}[od]
+    tdt = {FLOAT32: torch.float32, FLOAT64: torch.float64, INT64: torch.int64, BOOL: torch.bool}[od]
     out = torch.empty(kept, dtype=tdt, device=x.device)
-    desc = make_desc(op, list(x.shape), list(x.stride()), rd, od, correction, count_override)
+    desc = make_desc(op, list(x.shape), list(x.stride()), rd, od, correction, count_override, p=p)
     L = lib()
     wsb = L.tpr_reduce_workspace_bytes(ctypes.byref(desc))
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)

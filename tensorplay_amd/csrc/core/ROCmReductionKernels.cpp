@@ -8,6 +8,7 @@
 // (include/tpr_rocm.h).  The CUDA registrations these replace are
 // /root/reference/p10/src/backend/cuda/ReductionKernels.cu:385-418.
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <numeric>
 
@@ -58,7 +59,7 @@ void require_float32_input(const Tensor& self, const char* op) {
 }
 
 Tensor launch(const Tensor& self, int op, uint32_t mask, DType out_dtype, const std::vector<int64_t>& out_shape,
-              int64_t correction, int64_t count_override, const char* name) {
+              int64_t correction, int64_t count_override, const char* name, double p = 2.0) {
     Tensor out = Tensor::empty(out_shape, out_dtype, self.device());
     tpr_reduce_desc d;
     std::memset(&d, 0, sizeof(d));
@@ -73,6 +74,7 @@ Tensor launch(const Tensor& self, int op, uint32_t mask, DType out_dtype, const 
     d.reduce_mask = mask;
     d.correction = correction;
     d.count_override = count_override;
+    d.p = p;
     const size_t wsb = tpr_reduce_workspace_bytes(&d);
     std::shared_ptr<void> ws;
     if (wsb) ws = allocate(wsb, self.device());
@@ -202,6 +204,69 @@ Tensor std_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, int6
     return var_dims(self, dims, correction, keepdim, true);
 }
 
+// prod_kernel / prod_dim_kernel (ReductionKernels.cpp:406-514).  Output dtype as
+// sum (integral -> Int64); float inputs multiply in fp64 here (the reference
+// multiplies in the output dtype).  Empty dims -> full product.
+Tensor prod_kernel(const Tensor& self, DType dtype) {
+    require_float32_input(self, "prod");
+    return launch(self, TPR_PROD, all_dims(self), sum_out_dtype(self, dtype), {}, 0, 0, "prod");
+}
+Tensor prod_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, bool keepdim, DType dtype) {
+    if (dims.empty()) return prod_kernel(self, dtype);
+    require_float32_input(self, "prod");
+    const auto shape = reductionShape(self.shape(), dims, keepdim);
+    return launch(self, TPR_PROD, mask_of(self, dims), sum_out_dtype(self, dtype), shape, 0, 0, "prod");
+}
+
+// all_kernel / any_kernel / all_dim_kernel / any_dim_kernel
+// (ReductionKernels.cpp:517-677): Bool output, x != 0 is true (NaN is true).
+static Tensor bool_reduce(const Tensor& self, const std::vector<int64_t>* dims, bool keepdim, bool is_any) {
+    const char* name = is_any ? "any" : "all";
+    require_float32_input(self, name);
+    const int op = is_any ? TPR_ANY : TPR_ALL;
+    if (!dims || dims->empty()) return launch(self, op, all_dims(self), DType::Bool, {}, 0, 0, name);
+    return launch(self, op, mask_of(self, *dims), DType::Bool, reductionShape(self.shape(), *dims, keepdim), 0, 0,
+                  name);
+}
+Tensor all_kernel(const Tensor& self) { return bool_reduce(self, nullptr, false, false); }
+Tensor any_kernel(const Tensor& self) { return bool_reduce(self, nullptr, false, true); }
+Tensor all_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, bool keepdim) {
+    return bool_reduce(self, &dims, keepdim, false);
+}
+Tensor any_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, bool keepdim) {
+    return bool_reduce(self, &dims, keepdim, true);
+}
+
+// norm_kernel / norm_dim_kernel (ReductionKernels.cpp:858-872): (sum |x|^p)^(1/p);
+// p = +-inf: max / min of |x| (an empty full reduction raises, as max()/min()).
+// Every p is served on ROCm (the CUDA path serves p = 2 only,
+// ReductionKernels.cu:295-321).
+Tensor norm_kernel(const Tensor& self, double p) {
+    require_float32_input(self, "norm");
+    if (std::isinf(p) && self.numel() == 0)
+        TP_THROW(RuntimeError, std::string(p > 0 ? "max" : "min") + "(): Expected reduction dim to be non-empty");
+    return launch(self, TPR_NORM, all_dims(self), self.dtype(), {}, 0, 0, "norm", p);
+}
+Tensor norm_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, double p, bool keepdim) {
+    require_float32_input(self, "norm");
+    if (dims.empty()) return norm_kernel(self, p);
+    const auto shape = reductionShape(self.shape(), dims, keepdim);
+    return launch(self, TPR_NORM, mask_of(self, dims), self.dtype(), shape, 0, 0, "norm", p);
+}
+
+// median_kernel (ReductionKernels.cpp:874-901): lower median of all elements,
+// a 0-dim tensor of the input dtype; an empty input gives a one-element NaN
+// tensor (shape [1]), as the reference's Tensor::tensor({NaN}).
+Tensor median_kernel(const Tensor& self) {
+    require_float32_input(self, "median");
+    if (self.numel() == 0) {
+        const Tensor flat = self.contiguous().reshape({0});
+        return launch(flat, TPR_MEDIAN, 1u, DType::Float32, {}, 0, 0, "median").reshape({1});
+    }
+    const Tensor x = self.contiguous();
+    return launch(x, TPR_MEDIAN, all_dims(x), DType::Float32, {}, 0, 0, "median");
+}
+
 // topk(Tensor self, int64_t k, int64_t dim=-1, bool largest=true, bool sorted=true)
 //   -> (Tensor values, Tensor indices)
 // New schema (TensorPlay has no topk).  The selected dim is moved last and made
@@ -293,6 +358,15 @@ TENSORPLAY_LIBRARY_IMPL(ROCm, ReductionKernels) {
     m.impl<Tensor(const Tensor&, V, int64_t, bool)>("var.dim", rocm::var_dim_kernel);
     m.impl<Tensor(const Tensor&, int64_t)>("std", rocm::std_kernel);
     m.impl<Tensor(const Tensor&, V, int64_t, bool)>("std.dim", rocm::std_dim_kernel);
+    m.impl<Tensor(const Tensor&, DType)>("prod", rocm::prod_kernel);
+    m.impl<Tensor(const Tensor&, V, bool, DType)>("prod.dim_IntList", rocm::prod_dim_kernel);
+    m.impl<Tensor(const Tensor&)>("all", rocm::all_kernel);
+    m.impl<Tensor(const Tensor&, V, bool)>("all.dim", rocm::all_dim_kernel);
+    m.impl<Tensor(const Tensor&)>("any", rocm::any_kernel);
+    m.impl<Tensor(const Tensor&, V, bool)>("any.dim", rocm::any_dim_kernel);
+    m.impl<Tensor(const Tensor&)>("median", rocm::median_kernel);
+    m.impl<Tensor(const Tensor&, double)>("norm", rocm::norm_kernel);
+    m.impl<Tensor(const Tensor&, V, double, bool)>("norm.dim", rocm::norm_dim_kernel);
     m.impl<std::tuple<Tensor, Tensor>(const Tensor&, int64_t, int64_t, bool, bool)>("topk", rocm::topk_kernel);
 }
 

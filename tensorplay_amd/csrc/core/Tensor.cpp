@@ -333,6 +333,31 @@ Tensor Tensor::std(const std::vector<int64_t>& dim, int64_t correction, bool kee
     return DispatchStub<Tensor, const Tensor&, const std::vector<int64_t>&, int64_t, bool>::call(
         "std.dim", TP_KEY, *this, dim, correction, keepdim);
 }
+Tensor Tensor::prod(DType dtype) const {
+    return DispatchStub<Tensor, const Tensor&, DType>::call("prod", TP_KEY, *this, dtype);
+}
+Tensor Tensor::prod(const std::vector<int64_t>& dim, bool keepdim, DType dtype) const {
+    return DispatchStub<Tensor, const Tensor&, const std::vector<int64_t>&, bool, DType>::call(
+        "prod.dim_IntList", TP_KEY, *this, dim, keepdim, dtype);
+}
+Tensor Tensor::all() const { return DispatchStub<Tensor, const Tensor&>::call("all", TP_KEY, *this); }
+Tensor Tensor::all(const std::vector<int64_t>& dim, bool keepdim) const {
+    return DispatchStub<Tensor, const Tensor&, const std::vector<int64_t>&, bool>::call("all.dim", TP_KEY, *this, dim,
+                                                                                       keepdim);
+}
+Tensor Tensor::any() const { return DispatchStub<Tensor, const Tensor&>::call("any", TP_KEY, *this); }
+Tensor Tensor::any(const std::vector<int64_t>& dim, bool keepdim) const {
+    return DispatchStub<Tensor, const Tensor&, const std::vector<int64_t>&, bool>::call("any.dim", TP_KEY, *this, dim,
+                                                                                       keepdim);
+}
+Tensor Tensor::median() const { return DispatchStub<Tensor, const Tensor&>::call("median", TP_KEY, *this); }
+Tensor Tensor::norm(double p) const {
+    return DispatchStub<Tensor, const Tensor&, double>::call("norm", TP_KEY, *this, p);
+}
+Tensor Tensor::norm(const std::vector<int64_t>& dim, double p, bool keepdim) const {
+    return DispatchStub<Tensor, const Tensor&, const std::vector<int64_t>&, double, bool>::call(
+        "norm.dim", TP_KEY, *this, dim, p, keepdim);
+}
 std::tuple<Tensor, Tensor> Tensor::topk(int64_t k, int64_t dim, bool largest, bool sorted) const {
     return DispatchStub<std::tuple<Tensor, Tensor>, const Tensor&, int64_t, int64_t, bool, bool>::call(
         "topk", TP_KEY, *this, k, dim, largest, sorted);

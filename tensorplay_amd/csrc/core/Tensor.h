@@ -89,6 +89,15 @@ public:
     Tensor var(const std::vector<int64_t>& dim, int64_t correction = 1, bool keepdim = false) const;  // var.dim
     Tensor std(int64_t correction = 1) const;                                                      // std
     Tensor std(const std::vector<int64_t>& dim, int64_t correction = 1, bool keepdim = false) const;  // std.dim
+    Tensor prod(DType dtype = DType::Undefined) const;                                             // prod
+    Tensor prod(const std::vector<int64_t>& dim, bool keepdim = false, DType dtype = DType::Undefined) const;  // prod.dim_IntList
+    Tensor all() const;                                                                            // all
+    Tensor all(const std::vector<int64_t>& dim, bool keepdim = false) const;                       // all.dim
+    Tensor any() const;                                                                            // any
+    Tensor any(const std::vector<int64_t>& dim, bool keepdim = false) const;                       // any.dim
+    Tensor median() const;                                                                         // median
+    Tensor norm(double p = 2.0) const;                                                             // norm
+    Tensor norm(const std::vector<int64_t>& dim, double p = 2.0, bool keepdim = false) const;      // norm.dim
     // topk (schema added by this backend; TensorPlay has none)
     std::tuple<Tensor, Tensor> topk(int64_t k, int64_t dim = -1, bool largest = true, bool sorted = true) const;
 

@@ -198,6 +198,28 @@ PYBIND11_MODULE(_C, m) {
              py::arg("correction") = 1, py::arg("keepdim") = false)
         .def("std", [](const Tensor& s, int64_t d, int64_t c, bool k) { return s.std(V{d}, c, k); }, py::arg("dim"),
              py::arg("correction") = 1, py::arg("keepdim") = false)
+        .def("prod", [](const Tensor& s, std::optional<DType> dt) { return s.prod(opt_dtype(dt)); },
+             py::kw_only(), py::arg("dtype") = py::none())
+        .def("prod", [](const Tensor& s, const V& d, bool k, std::optional<DType> dt) { return s.prod(d, k, opt_dtype(dt)); },
+             py::arg("dim"), py::arg("keepdim") = false, py::kw_only(), py::arg("dtype") = py::none())
+        .def("prod", [](const Tensor& s, int64_t d, bool k, std::optional<DType> dt) { return s.prod(V{d}, k, opt_dtype(dt)); },
+             py::arg("dim"), py::arg("keepdim") = false, py::kw_only(), py::arg("dtype") = py::none())
+        .def("all", [](const Tensor& s) { return s.all(); })
+        .def("all", [](const Tensor& s, const V& d, bool k) { return s.all(d, k); }, py::arg("dim"),
+             py::arg("keepdim") = false)
+        .def("all", [](const Tensor& s, int64_t d, bool k) { return s.all(V{d}, k); }, py::arg("dim"),
+             py::arg("keepdim") = false)
+        .def("any", [](const Tensor& s) { return s.any(); })
+        .def("any", [](const Tensor& s, const V& d, bool k) { return s.any(d, k); }, py::arg("dim"),
+             py::arg("keepdim") = false)
+        .def("any", [](const Tensor& s, int64_t d, bool k) { return s.any(V{d}, k); }, py::arg("dim"),
+             py::arg("keepdim") = false)
+        .def("median", [](const Tensor& s) { return s.median(); })
+        .def("norm", [](const Tensor& s, double p) { return s.norm(p); }, py::arg("p") = 2.0)
+        .def("norm", [](const Tensor& s, const V& d, double p, bool k) { return s.norm(d, p, k); }, py::arg("dim"),
+             py::arg("p") = 2.0, py::arg("keepdim") = false)
+        .def("norm", [](const Tensor& s, int64_t d, double p, bool k) { return s.norm(V{d}, p, k); }, py::arg("dim"),
+             py::arg("p") = 2.0, py::arg("keepdim") = false)
         .def("topk", [](const Tensor& s, int64_t k, int64_t d, bool largest, bool sorted) {
             return s.topk(k, d, largest, sorted);
         }, py::arg("k"), py::arg("dim") = -1, py::arg("largest") = true, py::arg("sorted") = true);

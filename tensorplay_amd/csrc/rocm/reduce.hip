@@ -49,11 +49,68 @@ struct SumOp {
     using Wide = SumOp;
     __device__ static Acc init() { return 0.0; }
     template <class I>
-    __device__ static void acc(Acc& a, float x, I) { a += (double)x; }
+    __device__ static void acc(Acc& a, float x, I, float) { a += (double)x; }
     __device__ static State state(Acc a) { return {a}; }
     __device__ static State identity() { return {0.0}; }
     __device__ static State comb(State a, State b) { return {a.s + b.s}; }
     __device__ static State shfl(State s, int m) { return {__shfl_xor(s.s, m, kWave)}; }
+};
+
+// Product in fp64 (the reference multiplies in the output dtype, :424-427).
+struct ProdOp {
+    static constexpr bool kIndexed = false;
+    using Acc = double;
+    using State = SumS;
+    using Wide = ProdOp;
+    __device__ static Acc init() { return 1.0; }
+    template <class I>
+    __device__ static void acc(Acc& a, float x, I, float) { a *= (double)x; }
+    __device__ static State state(Acc a) { return {a}; }
+    __device__ static State identity() { return {1.0}; }
+    __device__ static State comb(State a, State b) { return {a.s * b.s}; }
+    __device__ static State shfl(State s, int m) { return {__shfl_xor(s.s, m, kWave)}; }
+};
+
+// Sum of |x|^p in fp64 (norm_kernel's abs().pow(p).sum(), :858-872).  KIND 1:
+// |x|, KIND 2: x*x (exact in fp64), KIND 0: powf(|x|, p) for any other p.
+template <int KIND>
+struct NormOp {
+    static constexpr bool kIndexed = false;
+    using Acc = double;
+    using State = SumS;
+    using Wide = NormOp;
+    __device__ static Acc init() { return 0.0; }
+    template <class I>
+    __device__ static void acc(Acc& a, float x, I, float p) {
+        if constexpr (KIND == 1) a += (double)fabsf(x);
+        else if constexpr (KIND == 2) a = fma((double)x, (double)x, a);
+        else a += (double)powf(fabsf(x), p);
+    }
+    __device__ static State state(Acc a) { return {a}; }
+    __device__ static State identity() { return {0.0}; }
+    __device__ static State comb(State a, State b) { return {a.s + b.s}; }
+    __device__ static State shfl(State s, int m) { return {__shfl_xor(s.s, m, kWave)}; }
+};
+
+// all / any: an element is true when x != 0 (NaN is true, -0.0 is false), as
+// static_cast<bool> in all_kernel/any_kernel (:517-563).
+struct BoolS { int b; };
+template <bool ANY>
+struct BoolOp {
+    static constexpr bool kIndexed = false;
+    using Acc = int;
+    using State = BoolS;
+    using Wide = BoolOp;
+    __device__ static Acc init() { return ANY ? 0 : 1; }
+    template <class I>
+    __device__ static void acc(Acc& a, float x, I, float) {
+        if constexpr (ANY) a |= (x != 0.0f) ? 1 : 0;
+        else a &= (x != 0.0f) ? 1 : 0;
+    }
+    __device__ static State state(Acc a) { return {a}; }
+    __device__ static State identity() { return {ANY ? 0 : 1}; }
+    __device__ static State comb(State a, State b) { return {ANY ? (a.b | b.b) : (a.b & b.b)}; }
+    __device__ static State shfl(State s, int m) { return {__shfl_xor(s.b, m, kWave)}; }
 };
 
 struct ArgS { float v; long long i; };
@@ -63,16 +120,18 @@ struct ArgS { float v; long long i; };
 // column kernels (extent < 2^31, checked by the planner; 32-bit selects are
 // cheaper per element), long long in the general kernel.  States always carry
 // a 64-bit index.
-template <bool IS_MAX, class IdxT = int>
+// ABS compares |x| (norm with p = +-inf: max/min of |x|).
+template <bool IS_MAX, class IdxT = int, bool ABS = false>
 struct ArgOp {
     static constexpr bool kIndexed = true;
     static constexpr IdxT kNone = (IdxT)(sizeof(IdxT) == 4 ? 0x7fffffff : kSentinel);
     struct Acc { float v; IdxT i; };
     using State = ArgS;
-    using Wide = ArgOp<IS_MAX, long long>;
+    using Wide = ArgOp<IS_MAX, long long, ABS>;
     __device__ static Acc init() { return {IS_MAX ? -INFINITY : INFINITY, kNone}; }
     template <class I>
-    __device__ static void acc(Acc& a, float x, I i) {
+    __device__ static void acc(Acc& a, float x, I i, float) {
+        if constexpr (ABS) x = fabsf(x);
         bool t = IS_MAX ? (x > a.v) : (x < a.v);
         a.v = t ? x : a.v;
         a.i = t ? (IdxT)i : a.i;
@@ -105,7 +164,7 @@ struct WelfordOp {
     using Wide = WelfordOp;
     __device__ static Acc init() { return {0.0f, 0, 0.0, 0.0}; }
     template <class I>
-    __device__ static void acc(Acc& a, float x, I) {
+    __device__ static void acc(Acc& a, float x, I, float) {
         a.k = (a.n == 0) ? x : a.k;
         double d = (double)x - (double)a.k;
         a.s1 += d;
@@ -143,18 +202,25 @@ struct Fin {
     int out_f64;    // SUM/MEAN write double
     double count;   // divisor count (reference semantics, duplicates included)
     double corr;    // VAR/STD correction
+    float p;        // NORM exponent (passed to every op's acc; only NormOp reads it)
+    double inv_p;   // NORM: 1/p
 };
 
 __device__ __forceinline__ void fin_write(const SumS& s, const Fin& f, void* out, long long o) {
     double v = s.s;
     if (f.op == TPR_MEAN) v = v / f.count;
+    if (f.op == TPR_NORM) v = (f.inv_p == 0.5) ? sqrt(v) : (f.inv_p == 1.0 ? v : pow(v, f.inv_p));
     if (f.out_f64) ((double*)out)[o] = v;
     else ((float*)out)[o] = (float)v;
 }
 
 __device__ __forceinline__ void fin_write(const ArgS& s, const Fin& f, void* out, long long o) {
-    if (f.op == TPR_AMAX || f.op == TPR_AMIN) ((float*)out)[o] = s.v;
+    if (f.op == TPR_AMAX || f.op == TPR_AMIN || f.op == TPR_NORM) ((float*)out)[o] = s.v;
     else ((long long*)out)[o] = (s.i == kSentinel) ? 0 : s.i;
+}
+
+__device__ __forceinline__ void fin_write(const BoolS& s, const Fin&, void* out, long long o) {
+    ((unsigned char*)out)[o] = (unsigned char)s.b;
 }
 
 __device__ __forceinline__ void fin_write(const WelS& s, const Fin& f, void* out, long long o) {
@@ -204,11 +270,11 @@ __device__ __forceinline__ float4 ld4(const float4* p, int nt) {
 }
 
 template <class Op, class I>
-__device__ __forceinline__ void acc4(typename Op::Acc& a, float4 t, I e) {
-    Op::acc(a, t.x, e);
-    Op::acc(a, t.y, e + 1);
-    Op::acc(a, t.z, e + 2);
-    Op::acc(a, t.w, e + 3);
+__device__ __forceinline__ void acc4(typename Op::Acc& a, float4 t, I e, float prm) {
+    Op::acc(a, t.x, e, prm);
+    Op::acc(a, t.y, e + 1, prm);
+    Op::acc(a, t.z, e + 2, prm);
+    Op::acc(a, t.w, e + 3, prm);
 }
 
 // ---------------------------------------------------------------------------
@@ -233,6 +299,7 @@ __global__ __launch_bounds__(LANES > kBlock ? LANES : kBlock) void k_rows(RowArg
     constexpr int GROUPS = (LANES >= BLK) ? 1 : BLK / LANES;
     // U = vectors in flight per lane
     constexpr int TILE = U * LANES;       // vectors per tile (contiguous in memory)
+    const float prm = a.fin.p;            // op parameter (NORM exponent)
     const int tid = threadIdx.x;
     const int g = tid / LANES;
     const int l = tid % LANES;
@@ -263,12 +330,12 @@ __global__ __launch_bounds__(LANES > kBlock ? LANES : kBlock) void k_rows(RowArg
                 for (int u = 0; u < U; ++u) {
                     const int v = t0 + l + u * LANES;
                     if constexpr (Op::kIndexed) {
-                        Op::acc(accq[0], t[u].x, v);
-                        Op::acc(accq[1 % (Op::kIndexed ? 4 : 1)], t[u].y, v);
-                        Op::acc(accq[2 % (Op::kIndexed ? 4 : 1)], t[u].z, v);
-                        Op::acc(accq[3 % (Op::kIndexed ? 4 : 1)], t[u].w, v);
+                        Op::acc(accq[0], t[u].x, v, prm);
+                        Op::acc(accq[1 % (Op::kIndexed ? 4 : 1)], t[u].y, v, prm);
+                        Op::acc(accq[2 % (Op::kIndexed ? 4 : 1)], t[u].z, v, prm);
+                        Op::acc(accq[3 % (Op::kIndexed ? 4 : 1)], t[u].w, v, prm);
                     } else {
-                        acc4<Op>(acc, t[u], 4 * v);
+                        acc4<Op>(acc, t[u], 4 * v, prm);
                     }
                 }
             }
@@ -279,17 +346,17 @@ __global__ __launch_bounds__(LANES > kBlock ? LANES : kBlock) void k_rows(RowArg
                     if (v < nv) {
                         const float4 t = pv[v];
                         if constexpr (Op::kIndexed) {
-                            Op::acc(accq[0], t.x, v);
-                            Op::acc(accq[1 % (Op::kIndexed ? 4 : 1)], t.y, v);
-                            Op::acc(accq[2 % (Op::kIndexed ? 4 : 1)], t.z, v);
-                            Op::acc(accq[3 % (Op::kIndexed ? 4 : 1)], t.w, v);
+                            Op::acc(accq[0], t.x, v, prm);
+                            Op::acc(accq[1 % (Op::kIndexed ? 4 : 1)], t.y, v, prm);
+                            Op::acc(accq[2 % (Op::kIndexed ? 4 : 1)], t.z, v, prm);
+                            Op::acc(accq[3 % (Op::kIndexed ? 4 : 1)], t.w, v, prm);
                         } else {
-                            acc4<Op>(acc, t, 4 * v);
+                            acc4<Op>(acc, t, 4 * v, prm);
                         }
                     }
                 }
             }
-            for (int e = 4 * nv + s * LANES + l; e < a.R; e += a.S * LANES) Op::acc(acc, p[e], e);
+            for (int e = 4 * nv + s * LANES + l; e < a.R; e += a.S * LANES) Op::acc(acc, p[e], e, prm);
         } else {
             int t0 = s * TILE;
             for (; t0 + TILE <= a.R; t0 += step) {
@@ -297,13 +364,13 @@ __global__ __launch_bounds__(LANES > kBlock ? LANES : kBlock) void k_rows(RowArg
 #pragma unroll
                 for (int u = 0; u < U; ++u) x[u] = p[t0 + l + u * LANES];
 #pragma unroll
-                for (int u = 0; u < U; ++u) Op::acc(acc, x[u], t0 + l + u * LANES);
+                for (int u = 0; u < U; ++u) Op::acc(acc, x[u], t0 + l + u * LANES, prm);
             }
             if (t0 < a.R) {
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const int e = t0 + l + u * LANES;
-                    if (e < a.R) Op::acc(acc, p[e], e);
+                    if (e < a.R) Op::acc(acc, p[e], e, prm);
                 }
             }
         }
@@ -356,6 +423,7 @@ __global__ __launch_bounds__(BLK) void k_cols(ColArgs a) {
     using Acc = typename Op::Acc;
     using State = typename Op::State;
     constexpr int TY = BLK / TX;
+    const float prm = a.fin.p;  // op parameter (NORM exponent)
     const int tid = threadIdx.x;
     const int tx = tid % TX;
     const int ty = tid / TX;
@@ -386,18 +454,18 @@ __global__ __launch_bounds__(BLK) void k_cols(ColArgs a) {
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const int ru = r + u * rstep;
-                    Op::acc(acc[0], t[u].x, ru);
-                    Op::acc(acc[1 % VEC], t[u].y, ru);
-                    Op::acc(acc[2 % VEC], t[u].z, ru);
-                    Op::acc(acc[3 % VEC], t[u].w, ru);
+                    Op::acc(acc[0], t[u].x, ru, prm);
+                    Op::acc(acc[1 % VEC], t[u].y, ru, prm);
+                    Op::acc(acc[2 % VEC], t[u].z, ru, prm);
+                    Op::acc(acc[3 % VEC], t[u].w, ru, prm);
                 }
             }
             for (; r < R; r += rstep) {
                 float4 t = *reinterpret_cast<const float4*>(base + (long long)r * a.rs);
-                Op::acc(acc[0], t.x, r);
-                Op::acc(acc[1 % VEC], t.y, r);
-                Op::acc(acc[2 % VEC], t.z, r);
-                Op::acc(acc[3 % VEC], t.w, r);
+                Op::acc(acc[0], t.x, r, prm);
+                Op::acc(acc[1 % VEC], t.y, r, prm);
+                Op::acc(acc[2 % VEC], t.z, r, prm);
+                Op::acc(acc[3 % VEC], t.w, r, prm);
             }
         } else {
             const int nj = (int)min((long long)VEC, a.inner - col0);
@@ -405,7 +473,7 @@ __global__ __launch_bounds__(BLK) void k_cols(ColArgs a) {
                 const float* q = base + (long long)r * a.rs;
 #pragma unroll
                 for (int j = 0; j < VEC; ++j)
-                    if (j < nj) Op::acc(acc[j], q[j], r);
+                    if (j < nj) Op::acc(acc[j], q[j], r, prm);
             }
         }
     }
@@ -465,6 +533,7 @@ template <class Op>
 __global__ __launch_bounds__(kBlock) void k_general(GenArgs a) {
     using Acc = typename Op::Acc;
     using State = typename Op::State;
+    const float prm = a.fin.p;  // op parameter (NORM exponent)
     const long long o = blockIdx.x / a.S;
     const int s = blockIdx.x % a.S;
     long long base = 0;
@@ -484,7 +553,7 @@ __global__ __launch_bounds__(kBlock) void k_general(GenArgs a) {
             off += (rem % a.rsz[d]) * a.rst[d];
             rem /= a.rsz[d];
         }
-        Op::acc(acc, a.in[base + off], j);
+        Op::acc(acc, a.in[base + off], j, prm);
     }
     State st = block_reduce<Op>(Op::state(acc));
     if (threadIdx.x == 0) {
@@ -550,9 +619,13 @@ struct Plan {
     long long nout = 1, count = 1;
 };
 
-size_t state_size(int op) {
+bool norm_is_inf(double p) { return std::isinf(p); }
+
+size_t state_size(int op, double p) {
     switch (op) {
-        case TPR_SUM: case TPR_MEAN: return sizeof(SumS);
+        case TPR_SUM: case TPR_MEAN: case TPR_PROD: return sizeof(SumS);
+        case TPR_NORM: return norm_is_inf(p) ? sizeof(ArgS) : sizeof(SumS);
+        case TPR_ALL: case TPR_ANY: return sizeof(BoolS);
         case TPR_AMAX: case TPR_AMIN: case TPR_ARGMAX: case TPR_ARGMIN: return sizeof(ArgS);
         default: return sizeof(WelS);
     }
@@ -569,7 +642,7 @@ int validate(const tpr_reduce_desc* d) {
     if (!d) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: null descriptor");
     if (d->ndim < 0 || d->ndim > TPR_MAX_DIMS)
         return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: ndim out of range [0, 8]");
-    if (d->op < TPR_SUM || d->op > TPR_STD) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: bad op");
+    if (d->op < TPR_SUM || d->op > TPR_MEDIAN) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: bad op");
     for (int i = 0; i < d->ndim; ++i)
         if (d->sizes[i] < 0) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: negative size");
     if (d->ndim < 32 && (d->reduce_mask >> d->ndim) != 0)
@@ -577,10 +650,22 @@ int validate(const tpr_reduce_desc* d) {
     if (d->in_dtype != TPR_FLOAT32)
         return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: only float32 input is implemented");
     switch (d->op) {
-        case TPR_SUM: case TPR_MEAN:
+        case TPR_SUM: case TPR_MEAN: case TPR_PROD:
             if (d->out_dtype != TPR_FLOAT32 && d->out_dtype != TPR_FLOAT64)
-                return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: sum/mean output must be float32 or float64");
+                return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: sum/mean/prod output must be float32 or float64");
             break;
+        case TPR_ALL: case TPR_ANY:
+            if (d->out_dtype != TPR_BOOL)
+                return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: all/any output must be bool");
+            break;
+        case TPR_MEDIAN: {
+            if (d->out_dtype != TPR_FLOAT32)
+                return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: median output must be float32");
+            const uint32_t all = d->ndim >= 32 ? 0xffffffffu : ((1u << d->ndim) - 1u);
+            if (d->ndim > 0 && d->reduce_mask != all)
+                return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_reduce: median reduces all dims only");
+            break;
+        }
         case TPR_AMAX: case TPR_AMIN:
             if (d->out_dtype != d->in_dtype)
                 return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: amax/amin output dtype must equal input dtype");
@@ -589,16 +674,16 @@ int validate(const tpr_reduce_desc* d) {
             if (d->out_dtype != TPR_INT64)
                 return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: argmax/argmin output must be int64");
             break;
-        default:
+        default:  // VAR, STD, NORM
             if (d->out_dtype != TPR_FLOAT32)
-                return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: var/std output must be float32");
+                return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: var/std/norm output must be float32");
     }
     return TPR_OK;
 }
 
 Plan make_plan(const tpr_reduce_desc* d, const void* in) {
     Plan p;
-    p.state_bytes = state_size(d->op);
+    p.state_bytes = state_size(d->op, d->p);
     const int nd = d->ndim;
     uint32_t mask = (nd == 0) ? 0u : d->reduce_mask;
     // counts (before dropping size-1 dims)
@@ -824,6 +909,167 @@ int run(const Plan& p, const float* in, void* out, void* ws, Fin fin, hipStream_
     return rc;
 }
 
+// ---------------------------------------------------------------------------
+// Median (median_kernel, ReductionKernels.cpp:874-901: the (n-1)/2-th smallest
+// element).  Exact radix select over ascending sortable keys in three passes of
+// 11/11/10 bits.  Each pass streams the input once: workgroups build LDS
+// histograms of the keys that match the prefix found so far and store them as
+// partials (no atomics in global memory, nothing to clear beforehand); one
+// workgroup then sums the partials and picks the digit.
+// ---------------------------------------------------------------------------
+constexpr int kMedBins = 2048;
+constexpr int kMedSelT = 1024;
+
+struct MedState {
+    uint32_t prefix;
+    uint32_t pmask;
+    long long kk;  // rank still to skip inside the current prefix
+};
+
+struct MedArgs {
+    const float* in;
+    long long n;
+    int G;            // histogram workgroups
+    int vec;          // 16-byte aligned input
+    uint32_t* hist;   // [G][kMedBins]
+    MedState* st;
+    float* out;
+};
+
+// Ascending sortable key: -0.0 -> +0.0, every NaN -> one canonical NaN above +inf.
+__device__ __forceinline__ uint32_t asc_key(float f) {
+    uint32_t u = __float_as_uint(f);
+    u = ((u & 0x7fffffffu) > 0x7f800000u) ? 0x7fc00000u : u;
+    u = (u == 0x80000000u) ? 0u : u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+template <int PASS>
+__global__ __launch_bounds__(kBlock) void k_med_hist(MedArgs a) {
+    constexpr int shift = PASS == 0 ? 21 : (PASS == 1 ? 10 : 0);
+    constexpr uint32_t dmask = PASS == 2 ? 1023u : 2047u;
+    __shared__ uint32_t h[kMedBins];
+    for (int i = threadIdx.x; i < kMedBins; i += kBlock) h[i] = 0;
+    uint32_t prefix = 0, pmask = 0;
+    if (PASS > 0) {
+        prefix = a.st->prefix;
+        pmask = a.st->pmask;
+    }
+    __syncthreads();
+    auto add = [&](float x) {
+        const uint32_t k = asc_key(x);
+        if ((k & pmask) == prefix) atomicAdd(&h[(k >> shift) & dmask], 1u);
+    };
+    const long long tid = (long long)blockIdx.x * kBlock + threadIdx.x;
+    const long long nthr = (long long)a.G * kBlock;
+    long long tail = 0;
+    if (a.vec) {
+        const long long nv = a.n >> 2;
+        const float4* v = reinterpret_cast<const float4*>(a.in);
+        for (long long i = tid; i < nv; i += nthr) {
+            const float4 t = v[i];
+            add(t.x);
+            add(t.y);
+            add(t.z);
+            add(t.w);
+        }
+        tail = nv << 2;
+    }
+    for (long long i = tail + tid; i < a.n; i += nthr) add(a.in[i]);
+    __syncthreads();
+    uint32_t* dst = a.hist + (long long)blockIdx.x * kMedBins;
+    for (int i = threadIdx.x; i < kMedBins; i += kBlock) dst[i] = h[i];
+}
+
+template <int PASS>
+__global__ __launch_bounds__(kMedSelT) void k_med_select(MedArgs a) {
+    constexpr int shift = PASS == 0 ? 21 : (PASS == 1 ? 10 : 0);
+    constexpr uint32_t dmask = PASS == 2 ? 1023u : 2047u;
+    __shared__ long long wsum[kMedSelT / kWave];
+    __shared__ MedState next;
+    const int t = threadIdx.x;
+    // thread t owns bins 2t and 2t+1
+    long long c0 = 0, c1 = 0;
+    for (int g = 0; g < a.G; ++g) {
+        const uint32_t* hg = a.hist + (long long)g * kMedBins;
+        c0 += hg[2 * t];
+        c1 += hg[2 * t + 1];
+    }
+    MedState cur;
+    if (PASS == 0) cur = {0u, 0u, (a.n - 1) / 2};
+    else cur = *a.st;
+    // exclusive prefix sum of (c0 + c1) over threads, in bin order
+    const long long own = c0 + c1;
+    long long inc = own;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const long long y = __shfl_up(inc, d, kWave);
+        if (__lane_id() >= d) inc += y;
+    }
+    const int w = t / kWave;
+    if (__lane_id() == kWave - 1) wsum[w] = inc;
+    __syncthreads();
+    long long before = 0;
+    for (int i = 0; i < w; ++i) before += wsum[i];
+    const long long excl = before + inc - own;
+    const long long kk = cur.kk;
+    if (kk >= excl && kk < excl + own) {
+        const bool first = kk < excl + c0;
+        const uint32_t digit = 2u * t + (first ? 0u : 1u);
+        next.prefix = cur.prefix | (digit << shift);
+        next.pmask = cur.pmask | (dmask << shift);
+        next.kk = kk - excl - (first ? 0 : c0);
+    }
+    __syncthreads();
+    if (t == 0) {
+        if (PASS < 2) {
+            *a.st = next;
+        } else {
+            const uint32_t key = next.prefix;
+            const uint32_t bits = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
+            a.out[0] = __uint_as_float(bits);
+        }
+    }
+}
+
+__global__ void k_med_fill(float* out, float v) { out[0] = v; }
+
+size_t median_ws_bytes(long long n, int* G) {
+    const long long g = std::max(1LL, std::min((long long)device_info().cus * 2, (n + 4095) / 4096));
+    if (G) *G = (int)g;
+    return 256 + (size_t)g * kMedBins * sizeof(uint32_t);
+}
+
+int run_median(const tpr_reduce_desc* d, const Plan& p, const float* in, void* out, void* ws, size_t ws_bytes,
+               hipStream_t st) {
+    (void)d;
+    if (p.count == 0) {
+        hipLaunchKernelGGL(k_med_fill, dim3(1), dim3(1), 0, st, static_cast<float*>(out), __builtin_nanf(""));
+        return check_launch("k_med_fill");
+    }
+    if (!(p.kind == P_ROWS && p.rows == 1))
+        return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_reduce: median needs a contiguous view (make it dense first)");
+    int G = 1;
+    const size_t need = median_ws_bytes(p.count, &G);
+    if (ws == nullptr || ws_bytes < need)
+        return fail(TPR_ERR_WORKSPACE, "tpr_reduce: workspace too small (need " + std::to_string(need) + " bytes)");
+    MedArgs a;
+    a.in = in;
+    a.n = p.count;
+    a.G = G;
+    a.vec = (reinterpret_cast<uintptr_t>(in) & 15u) == 0;
+    a.st = static_cast<MedState*>(ws);
+    a.hist = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + 256);
+    a.out = static_cast<float*>(out);
+    hipLaunchKernelGGL(k_med_hist<0>, dim3(G), dim3(kBlock), 0, st, a);
+    hipLaunchKernelGGL(k_med_select<0>, dim3(1), dim3(kMedSelT), 0, st, a);
+    hipLaunchKernelGGL(k_med_hist<1>, dim3(G), dim3(kBlock), 0, st, a);
+    hipLaunchKernelGGL(k_med_select<1>, dim3(1), dim3(kMedSelT), 0, st, a);
+    hipLaunchKernelGGL(k_med_hist<2>, dim3(G), dim3(kBlock), 0, st, a);
+    hipLaunchKernelGGL(k_med_select<2>, dim3(1), dim3(kMedSelT), 0, st, a);
+    return check_launch("k_med");
+}
+
 }  // namespace
 }  // namespace tpr
 
@@ -832,7 +1078,9 @@ extern "C" {
 size_t tpr_reduce_workspace_bytes(const tpr_reduce_desc* desc) {
     if (tpr::validate(desc) != TPR_OK) return 0;
     // alignment does not change the workspace size; plan with an aligned pointer
-    return tpr::make_plan(desc, nullptr).ws;
+    const tpr::Plan p = tpr::make_plan(desc, nullptr);
+    if (desc->op == TPR_MEDIAN) return p.count > 0 ? tpr::median_ws_bytes(p.count, nullptr) : 0;
+    return p.ws;
 }
 
 int tpr_reduce(const tpr_reduce_desc* desc, const void* in, void* out, void* workspace,
@@ -844,6 +1092,9 @@ int tpr_reduce(const tpr_reduce_desc* desc, const void* in, void* out, void* wor
     if (p.nout == 0) return TPR_OK;
     if (!out) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: null output");
     if (!in && p.count > 0) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: null input");
+    if (desc->op == TPR_MEDIAN)
+        return run_median(desc, p, static_cast<const float*>(in), out, workspace, workspace_bytes,
+                          static_cast<hipStream_t>(stream));
     if (p.ws > 0 && (workspace == nullptr || workspace_bytes < p.ws))
         return fail(TPR_ERR_WORKSPACE, "tpr_reduce: workspace too small (need " +
                                            std::to_string(p.ws) + " bytes)");
@@ -852,12 +1103,25 @@ int tpr_reduce(const tpr_reduce_desc* desc, const void* in, void* out, void* wor
     fin.out_f64 = desc->out_dtype == TPR_FLOAT64;
     fin.count = (double)(desc->count_override > 0 ? desc->count_override : p.count);
     fin.corr = (double)desc->correction;
+    fin.p = (float)desc->p;
+    fin.inv_p = 1.0 / desc->p;
     const float* x = static_cast<const float*>(in);
     hipStream_t st = static_cast<hipStream_t>(stream);
     switch (desc->op) {
         case TPR_SUM: case TPR_MEAN: return run<SumOp>(p, x, out, workspace, fin, st);
+        case TPR_PROD: return run<ProdOp>(p, x, out, workspace, fin, st);
         case TPR_AMAX: case TPR_ARGMAX: return run<ArgOp<true>>(p, x, out, workspace, fin, st);
         case TPR_AMIN: case TPR_ARGMIN: return run<ArgOp<false>>(p, x, out, workspace, fin, st);
+        case TPR_ALL: return run<BoolOp<false>>(p, x, out, workspace, fin, st);
+        case TPR_ANY: return run<BoolOp<true>>(p, x, out, workspace, fin, st);
+        case TPR_NORM:
+            if (norm_is_inf(desc->p)) {
+                if (desc->p > 0) return run<ArgOp<true, int, true>>(p, x, out, workspace, fin, st);
+                return run<ArgOp<false, int, true>>(p, x, out, workspace, fin, st);
+            }
+            if (desc->p == 1.0) return run<NormOp<1>>(p, x, out, workspace, fin, st);
+            if (desc->p == 2.0) return run<NormOp<2>>(p, x, out, workspace, fin, st);
+            return run<NormOp<0>>(p, x, out, workspace, fin, st);
         default: return run<WelfordOp>(p, x, out, workspace, fin, st);
     }
 }

@@ -2,7 +2,7 @@
 reduction tests assert, as data (inputs + expected outputs), one record per
 assertion, each citing the test line it comes from.  Nothing here imports or
 runs the reference; the values are transcribed from its test files:
-  test/test_cuda_reductions.py:19-98, test/test_reduction.py:35-57
+  test/test_cuda_reductions.py:19-98, test/test_reduction.py:5-57
 """
 import json
 import math
@@ -35,6 +35,19 @@ CASES = [
          expect=[1, 0, 1], expect_shape=[3]),
     dict(src="test/test_reduction.py:50-52", op="argmax", x=[1.0, 5.0, 2.0, 4.0, 3.0, 6.0], shape=[2, 3], dims=[1],
          expect=[1, 2], expect_shape=[2]),
+    dict(src="test/test_cuda_reductions.py:66-69", op="prod", x=[1.0, 2.0, 3.0, 4.0], shape=[4], dims=None, expect=24.0),
+    dict(src="test/test_cuda_reductions.py:71-75", op="norm", x=[3.0, 4.0], shape=[2], dims=None, expect=5.0),
+    dict(src="test/test_reduction.py:5-8", op="prod", x=[1.0, 2.0, 3.0, 4.0], shape=[2, 2], dims=None, expect=24.0),
+    dict(src="test/test_reduction.py:11-13", op="prod", x=[1.0, 2.0, 3.0, 4.0], shape=[2, 2], dims=[0],
+         expect=[3.0, 8.0], expect_shape=[2]),
+    dict(src="test/test_reduction.py:15-17", op="prod", x=[1.0, 2.0, 3.0, 4.0], shape=[2, 2], dims=[1],
+         expect=[2.0, 12.0], expect_shape=[2]),
+    dict(src="test/test_reduction.py:20-21", op="any", x=[1.0, 0.0, 1.0, 1.0], shape=[2, 2], dims=None, expect=True),
+    dict(src="test/test_reduction.py:20-22", op="all", x=[1.0, 0.0, 1.0, 1.0], shape=[2, 2], dims=None, expect=False),
+    dict(src="test/test_reduction.py:24-25", op="all", x=[1.0, 1.0], shape=[2], dims=None, expect=True),
+    dict(src="test/test_reduction.py:27-28", op="any", x=[0.0, 0.0], shape=[2], dims=None, expect=False),
+    dict(src="test/test_reduction.py:31-33", op="all", x=[1.0, 0.0, 1.0, 1.0], shape=[2, 2], dims=[0],
+         expect=[True, False], expect_shape=[2]),
     dict(src="test/test_reduction.py:55", op="sum", x=[1.0, 2.0, 3.0, 4.0], shape=[2, 2], dims=None, expect=10.0),
     dict(src="test/test_reduction.py:56", op="mean", x=[1.0, 2.0, 3.0, 4.0], shape=[2, 2], dims=None, expect=2.5),
 ]

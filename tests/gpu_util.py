@@ -12,11 +12,17 @@ def device_view(torch, base_np, view_np):
     return t.as_strided(view_np.shape, [s // 4 for s in view_np.strides], off)
 
 
-def fp64_reference(v, op, dims, correction=1):
+def fp64_reference(v, op, dims, correction=1, p=2.0):
     x = v.astype(np.float64)
     ax = None if dims is None else tuple(dims)
     if op == "sum":
         return x.sum(axis=ax)
+    if op == "prod":
+        return x.prod(axis=ax)
+    if op == "norm":
+        with np.errstate(divide="ignore", over="ignore"):
+            s = (np.abs(x) ** p).sum(axis=ax)
+            return s ** (1.0 / p)
     if op == "mean":
         return x.mean(axis=ax) if x.size else np.full(np.sum(x, axis=ax).shape, np.nan)
     if op in ("var", "std"):

@@ -36,7 +36,7 @@ def test_abi_version():
 
 def test_descriptor_layout_matches_header():
     # int32 x4, int64[8] x2, uint32, int32, int64 x2
-    assert ctypes.sizeof(_capi.ReduceDesc) == 16 + 128 + 8 + 16
+    assert ctypes.sizeof(_capi.ReduceDesc) == 16 + 128 + 8 + 16 + 8
 
 
 def test_argument_validation_without_gpu():

@@ -6,8 +6,9 @@ import pytest
 import tensorplay_amd as tp
 from tensorplay_amd import _C
 
-SCHEMAS = ["argmax", "argmin", "max", "max.dim", "mean", "mean.dim", "min", "min.dim", "std", "std.dim",
-           "sum", "sum.dim_IntList", "topk", "var", "var.dim"]
+SCHEMAS = sorted(["argmax", "argmin", "max", "max.dim", "mean", "mean.dim", "min", "min.dim", "std", "std.dim",
+                  "sum", "sum.dim_IntList", "topk", "var", "var.dim", "prod", "prod.dim_IntList", "all", "all.dim",
+                  "any", "any.dim", "median", "norm", "norm.dim"])
 
 
 def test_rocm_key_registers_every_schema():

@@ -35,6 +35,14 @@ def _call(case):
         return O.var(x, dims)
     if op == "std":
         return O.std(x, dims)
+    if op == "prod":
+        return O.prod(x, dims, keep)
+    if op == "norm":
+        return O.norm(x, case.get("p", 2.0), dims, keep)
+    if op == "all":
+        return O.all_(x, dims, keep)
+    if op == "any":
+        return O.any_(x, dims, keep)
     raise ValueError(op)
 
 
@@ -198,3 +206,80 @@ def test_topk_values_match_torch():
     tv, ti = torch.topk(torch.from_numpy(x), 50)
     np.testing.assert_array_equal(v, tv.numpy())
     np.testing.assert_array_equal(i, ti.numpy())  # no ties in continuous data
+
+
+# ---- prod / all / any / norm / median ----
+
+@pytest.mark.parametrize("shape,dims", [((9,), None), ((7, 5), [1]), ((7, 5), [0]), ((3, 4, 5), [0, 2])])
+def test_prod_is_sequential_fp32(shape, dims):
+    # prod_kernel multiplies sequentially in float: np.multiply.accumulate in
+    # float32 is that fold, bit for bit
+    x = _rng(40).uniform(0.5, 1.5, size=shape).astype(np.float32)
+    got = O.prod(x, dims)
+    if dims is None:
+        assert got == np.multiply.accumulate(x.ravel(), dtype=np.float32)[-1]
+    else:
+        keep = [d for d in range(x.ndim) if d not in dims]
+        xt = np.transpose(x, keep + dims).reshape(int(np.prod([shape[d] for d in keep])), -1)
+        exp = np.multiply.accumulate(xt, axis=1, dtype=np.float32)[:, -1]
+        np.testing.assert_array_equal(got.ravel(), exp)
+
+
+def test_all_any_brute_force():
+    x = np.array([[0.0, -0.0, np.nan, 1.0], [2.0, 3.0, -1.0, np.inf], [0.0, 0.0, -0.0, 0.0]], np.float32)
+    nz = (x != 0)  # numpy: NaN != 0 is True, -0.0 != 0 is False
+    assert O.all_(x) == nz.all() and O.any_(x) == nz.any()
+    for d in (0, 1):
+        np.testing.assert_array_equal(O.all_(x, [d]), nz.all(axis=d))
+        np.testing.assert_array_equal(O.any_(x, [d]), nz.any(axis=d))
+    e = np.zeros((0, 3), np.float32)
+    assert O.all_(e) and not O.any_(e)
+    np.testing.assert_array_equal(O.all_(e, [0]), [True, True, True])
+    np.testing.assert_array_equal(O.any_(e, [0]), [False, False, False])
+
+
+@pytest.mark.parametrize("p", [1.0, 2.0, 3.0, 0.5, np.inf, -np.inf])
+@pytest.mark.parametrize("shape,dims", [((10,), None), ((5, 5), None), ((5, 5), [0]), ((5, 5), [1]),
+                                        ((3, 4, 6), [0, 2])])
+def test_norm_matches_torch(p, shape, dims):
+    # the reference's own test compares norm with torch at rtol 1e-5
+    # (test/test_statistical.py:51-66, tolerance :10-17)
+    torch = pytest.importorskip("torch")
+    x = _rng(41).standard_normal(shape).astype(np.float32)
+    got = O.norm(x, p, dims)
+    t = torch.from_numpy(x)
+    exp = t.norm(p=p) if dims is None else t.norm(p=p, dim=dims)
+    np.testing.assert_allclose(np.asarray(got), exp.numpy(), rtol=1e-5, atol=1e-8)
+
+
+def test_norm_special_p():
+    x = np.array([3.0, -4.0, 0.0], np.float32)
+    assert O.norm(x, 2.0) == 5.0
+    assert O.norm(x, np.inf) == 4.0 and O.norm(x, -np.inf) == 0.0
+    assert O.norm(x, 1.0) == 7.0
+    assert O.norm(x, 0.0) == np.inf            # pow(0, 0) = 1 -> sum 3 -> 3^(1/0)
+    assert O.norm(x[:1], 0.0) == 1.0
+    assert O.norm(np.array([np.nan, 1.0], np.float32), np.inf) == 1.0  # NaN never wins the max
+    with pytest.raises(RuntimeError):
+        O.norm(np.zeros(0, np.float32), np.inf)
+
+
+def test_median_brute_force():
+    rng = _rng(42)
+    for n in range(1, 40):
+        x = rng.integers(-5, 6, size=n).astype(np.float32)  # many ties
+        assert O.median(x) == np.sort(x)[(n - 1) // 2]
+    x = np.arange(1001, dtype=np.float32)[::-1].copy()
+    assert O.median(x) == 500.0
+    assert O.median(np.arange(1000, dtype=np.float32)) == 499.0  # lower median for even n
+    assert np.isnan(O.median(np.zeros(0, np.float32)))
+    # NaN ranks above every number (np.sort puts NaN last)
+    y = np.array([np.nan, 1.0, np.nan, -np.inf, 2.0], np.float32)
+    assert O.median(y) == np.sort(y)[2]
+    z = np.array([-0.0, -0.0, -0.0], np.float32)
+    m = O.median(z)
+    assert m == 0.0 and not np.signbit(m)  # a zero median comes back as +0.0
+    # strided view
+    w = rng.standard_normal((6, 7)).astype(np.float32)[:, ::2]
+    assert O.median(w) == np.sort(w.ravel())[(w.size - 1) // 2]
+

@@ -29,17 +29,32 @@ def _reset_knobs():
         _capi.debug_set(k, 0)
 
 
-def gpu(t, op, dims, correction=1):
-    out = _capi.reduce(t, op, dims, correction=correction)
+def gpu(t, op, dims, correction=1, p=2.0):
+    out = _capi.reduce(t, op, dims, correction=correction, p=p)
     torch.cuda.synchronize()
     return out.cpu().numpy()
 
 
-def check(v, t, op, dims, correction=1):
+def check(v, t, op, dims, correction=1, p=2.0):
     """Compare one reduction of the numpy view v / torch view t."""
-    print(f"case op={op} shape={v.shape} strides={v.strides} dims={dims}", flush=True)
-    got = gpu(t, op, dims, correction)
-    if op in ("amax", "amin"):
+    print(f"case op={op} shape={v.shape} strides={v.strides} dims={dims} p={p}", flush=True)
+    got = gpu(t, op, dims, correction, p)
+    full = dims is None or len(dims) == v.ndim
+    if op in ("all", "any"):
+        f = O.all_ if op == "all" else O.any_
+        exp = f(v) if full else f(v, list(dims))
+        np.testing.assert_array_equal(got.reshape(np.shape(exp)), exp)
+    elif op == "median":
+        assert_bits_equal(got.reshape(()), np.float32(O.median(v)))
+    elif op == "norm" and np.isinf(p):
+        if full and v.size == 0:
+            return
+        exp = np.float32(O.norm(v, p)) if full else O.norm(v, p, list(dims))
+        assert_bits_equal(got.reshape(np.shape(exp)), exp)
+    elif op in ("prod", "norm"):
+        ref = fp64_reference(v, op, dims, correction, p)
+        assert_close_rel(got.reshape(np.shape(ref)), ref)
+    elif op in ("amax", "amin"):
         f = O.amax if op == "amax" else O.amin
         if dims is None or len(dims) == v.ndim:
             if v.size == 0:
@@ -254,3 +269,102 @@ def test_few_long_rows():
         t = torch.from_numpy(x).cuda()
         for op in OPS:
             check(x, t, op, [1])
+
+
+# ---- prod / norm / all / any / median ----
+
+NEW_OPS = [("prod", 2.0), ("all", 2.0), ("any", 2.0), ("norm", 2.0), ("norm", 1.0), ("norm", 3.0),
+           ("norm", 0.5), ("norm", float("inf")), ("norm", float("-inf"))]
+
+
+@pytest.mark.parametrize("op,p", NEW_OPS, ids=[f"{o}{p}" for o, p in NEW_OPS])
+def test_new_ops_random_layouts(op, p):
+    rng = np.random.default_rng(14)
+    for base, v in _views(rng):
+        if op == "prod":  # keep products representable: values near 1
+            base[...] = rng.uniform(0.99, 1.01, size=base.shape).astype(np.float32)
+        if op in ("all", "any"):  # plenty of exact zeros
+            base[...] = np.where(rng.random(base.shape) < 0.3, np.float32(0.0), base)
+        t = device_view(torch, base, v)
+        for dims in _dim_sets(v.ndim):
+            check(v, t, op, dims, p=p)
+
+
+@pytest.mark.parametrize("knob,values", [("general", [1]), ("splits", [1, 3, 64]), ("lanes", [16, 256, 1024]),
+                                         ("tx", [64, 256]), ("nt", [1])])
+def test_new_ops_forced_plans(knob, values):
+    rng = np.random.default_rng(15)
+    b = rng.uniform(0.99, 1.01, size=(37, 1029)).astype(np.float32)
+    b[5, 7] = 0.0
+    b[9] = 0.0
+    c = rng.uniform(0.99, 1.01, size=(5, 300, 36)).astype(np.float32)
+    c[2, :, 3] = 0.0
+    for val in values:
+        _capi.debug_set(knob, val)
+        for op, p in NEW_OPS:
+            check(b, torch.from_numpy(b).cuda(), op, [1], p=p)
+            check(b, torch.from_numpy(b).cuda(), op, None, p=p)
+            check(c, torch.from_numpy(c).cuda(), op, [1], p=p)
+            check(c, torch.from_numpy(c).cuda(), op, [0], p=p)
+
+
+def test_new_ops_special_values():
+    x = np.array([[np.nan, -0.0, 0.0, 1.0, 1.0],
+                  [np.nan, np.nan, np.nan, np.nan, np.nan],
+                  [0.0, -0.0, 0.0, -0.0, 0.0],
+                  [3.0, -np.inf, 2.0, np.inf, 1.0]], np.float32)
+    t = torch.from_numpy(x).cuda()
+    for op in ("all", "any"):
+        for dims in ([1], [0], None):
+            check(x, t, op, dims)
+    for p in (float("inf"), float("-inf")):
+        for dims in ([1], [0], None):
+            check(x, t, op="norm", dims=dims, p=p)
+    # norm p=0: |x|^0 = 1 for every element, sum n, n^(1/0) = inf (the reference composite)
+    z = np.array([[0.0, 2.0, 0.0]], np.float32)
+    got = gpu(torch.from_numpy(z).cuda(), "norm", None, p=0.0)
+    assert np.isinf(got) and got > 0
+    # empty extents: prod 1, all true, any false, norm 0
+    e = torch.zeros((0, 3), device="cuda")
+    assert (gpu(e, "prod", [0]) == 1).all()
+    assert gpu(e, "all", [0]).all() and not gpu(e, "any", [0]).any()
+    assert (gpu(e, "norm", [0]) == 0).all()
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 1000, 1001, 4096 + 3, 1 << 20, (1 << 22) + 5])
+def test_median_sizes(n):
+    rng = np.random.default_rng(16 + n % 97)
+    x = rng.standard_normal(n).astype(np.float32)
+    check(x, torch.from_numpy(x).cuda(), "median", None)
+    # heavy ties and a misaligned start
+    y = rng.integers(-3, 4, size=n + 1).astype(np.float32)
+    check(y[1:], device_view(torch, y, y[1:]), "median", None)
+
+
+def test_median_special_values():
+    x = np.array([np.nan, 1.0, np.nan, -np.inf, 2.0, -0.0, 0.0, np.inf, np.nan], np.float32)
+    for k in range(1, len(x) + 1):
+        v = np.ascontiguousarray(x[:k])
+        check(v, torch.from_numpy(v).cuda(), "median", None)
+    z = np.full(5, -0.0, np.float32)
+    got = gpu(torch.from_numpy(z).cuda(), "median", None)
+    assert got == 0.0 and not np.signbit(got)
+    assert np.isnan(gpu(torch.zeros(0, device="cuda"), "median", None))
+    m = torch.from_numpy(np.arange(24, dtype=np.float32).reshape(2, 3, 4)).cuda()
+    check(m.cpu().numpy(), m, "median", None)
+    with pytest.raises(_capi.TprError):  # strided views must be made dense first
+        _capi.reduce(m[:, :, ::2], "median", None)
+    with pytest.raises(_capi.TprError):  # full reductions only
+        _capi.reduce(m, "median", [1])
+
+
+def test_new_ops_config_shapes():
+    # the headline shape through the new ops (sizes the tests run in seconds)
+    rng = np.random.default_rng(17)
+    x = rng.uniform(0.999, 1.001, size=(64, 1024, 1024)).astype(np.float32)
+    t = torch.from_numpy(x).cuda()
+    check(x, t, "prod", [1])
+    check(x, t, "norm", [2], p=2.0)
+    check(x, t, "norm", [0], p=float("inf"))
+    check(x, t, "any", [0])
+

@@ -157,3 +157,56 @@ def test_caching_allocator_reuses_blocks():
     for _ in range(20):
         t.sum(1).numpy()
     assert tp.rocm.memory_stats()["device_allocs"] == before
+
+
+# ---- prod / all / any / norm / median through the dispatcher ---------------------------------
+def test_prod_known_answers():
+    # test/test_cuda_reductions.py:66-69, test/test_reduction.py:5-17
+    assert tp.tensor([1.0, 2.0, 3.0, 4.0], device=DEV).prod().item() == 24.0
+    x = tp.tensor(np.array([[1.0, 2.0], [3.0, 4.0]], np.float32), device=DEV)
+    assert x.prod().item() == 24.0
+    p0, p1 = x.prod(dim=0), x.prod(dim=1)
+    assert p0[0].item() == 3.0 and p0[1].item() == 8.0
+    assert p1[0].item() == 2.0 and p1[1].item() == 12.0
+    assert x.prod(dim=[1], keepdim=True).shape == [2, 1]
+
+
+def test_all_any_known_answers():
+    # test/test_reduction.py:19-33
+    x = tp.tensor(np.array([[1, 0], [1, 1]], np.float32), device=DEV)
+    assert x.any().item() is True and x.all().item() is False
+    assert tp.tensor(np.array([1, 1], np.float32), device=DEV).all().item() is True
+    assert tp.tensor(np.array([0, 0], np.float32), device=DEV).any().item() is False
+    a0 = x.all(dim=0)
+    assert a0.dtype == tp.bool_ and a0[0].item() is True and a0[1].item() is False
+    assert x.any(dim=[1], keepdim=True).shape == [2, 1]
+
+
+def test_norm_known_answer_and_vs_torch():
+    # test/test_cuda_reductions.py:71-75 and test/test_statistical.py:51-66
+    assert tp.tensor([3.0, 4.0], device=DEV).norm().item() == 5.0
+    rng = np.random.default_rng(7)
+    for shape in [(10,), (5, 5)]:
+        data = torch.from_numpy(rng.standard_normal(shape).astype(np.float32))
+        t = tp.tensor(data.numpy(), device=DEV)
+        for p in [1.0, 2.0, float("inf"), float("-inf"), 3.0]:
+            close(t.norm(p=p).cpu(), data.norm(p=p))
+            if len(shape) > 1:
+                close(t.norm(dim=[0], p=p).cpu(), data.norm(dim=0, p=p))
+                close(t.norm(dim=[1], p=p, keepdim=True).cpu(), data.norm(dim=1, p=p, keepdim=True))
+    with pytest.raises(RuntimeError):
+        tp.empty([0], device=DEV).norm(p=float("inf"))
+
+
+def test_median_vs_oracle():
+    rng = np.random.default_rng(8)
+    for shape in [(7,), (4, 6), (3, 5, 7), (1000, 33)]:
+        x = rng.standard_normal(shape).astype(np.float32)
+        t = tp.tensor(x, device=DEV)
+        got = t.median()
+        assert got.shape == [] and got.item() == float(O.median(x))
+        # non-contiguous views are made dense first
+        tt = t.permute(list(range(len(shape)))[::-1])
+        assert tt.median().item() == float(O.median(np.ascontiguousarray(x.transpose())))
+    e = tp.empty([0, 3], device=DEV).median()
+    assert e.shape == [1] and math.isnan(e.item())
