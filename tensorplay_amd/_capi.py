@@ -119,13 +119,24 @@ def _stream(torch, device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
-def default_out_dtype(op):
+def default_out_dtype(op, in_dtype=FLOAT32):
     op = OP_NAMES[op] if isinstance(op, str) else op
     if op in (ARGMAX, ARGMIN):
         return INT64
     if op in (ALL, ANY):
         return BOOL
+    if in_dtype != FLOAT32:
+        if op in (SUM, PROD):
+            return INT64
+        if op in (AMAX, AMIN):
+            return in_dtype
     return FLOAT32
+
+
+def _torch_dtypes():
+    import torch
+    return {torch.float32: FLOAT32, torch.float64: FLOAT64, torch.int64: INT64, torch.int32: INT32,
+            torch.int16: INT16, torch.int8: INT8, torch.uint8: UINT8, torch.bool: BOOL}
 
 
 def reduce(x, op, dims=None, correction=1, out_dtype=None, count_override=0, p=2.0):
@@ -139,10 +150,12 @@ def reduce(x, op, dims=None, correction=1, out_dtype=None, count_override=0, p=2
     else:
         rd = sorted(set((d + nd) if d < 0 else d for d in dims))
     kept = [x.shape[i] for i in range(nd) if i not in rd]
-    od = default_out_dtype(op) if out_dtype is None else out_dtype
-    tdt = {FLOAT32: torch.float32, FLOAT64: torch.float64, INT64: torch.int64, BOOL: torch.bool}[od]
+    tmap = _torch_dtypes()
+    idt = tmap[x.dtype]
+    od = default_out_dtype(op, idt) if out_dtype is None else out_dtype
+    tdt = {v: k for k, v in tmap.items()}[od]
     out = torch.empty(kept, dtype=tdt, device=x.device)
-    desc = make_desc(op, list(x.shape), list(x.stride()), rd, od, correction, count_override, p=p)
+    desc = make_desc(op, list(x.shape), list(x.stride()), rd, od, correction, count_override, in_dtype=idt, p=p)
     L = lib()
     wsb = L.tpr_reduce_workspace_bytes(ctypes.byref(desc))
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)

@@ -58,6 +58,20 @@ void require_float32_input(const Tensor& self, const char* op) {
     if (self.dim() > TPR_MAX_DIMS) TP_THROW(NotImplementedError, std::string(op) + ": more than 8 dims on ROCm");
 }
 
+// sum/mean/prod, max/min, argmax/argmin and all/any also take the signed
+// integer dtypes, UInt8 and Bool (the reference instantiates them for every
+// scalar type); UInt16/32/64 have no ROCm kernel.
+void require_reducible_input(const Tensor& self, const char* op) {
+    switch (self.dtype()) {
+        case DType::Float32: case DType::UInt8: case DType::Int8: case DType::Int16: case DType::Int32:
+        case DType::Int64: case DType::Bool: break;
+        default:
+            TP_THROW(NotImplementedError, std::string(op) + " not implemented for dtype " + toString(self.dtype()) +
+                                              " on ROCm");
+    }
+    if (self.dim() > TPR_MAX_DIMS) TP_THROW(NotImplementedError, std::string(op) + ": more than 8 dims on ROCm");
+}
+
 Tensor launch(const Tensor& self, int op, uint32_t mask, DType out_dtype, const std::vector<int64_t>& out_shape,
               int64_t correction, int64_t count_override, const char* name, double p = 2.0) {
     Tensor out = Tensor::empty(out_shape, out_dtype, self.device());
@@ -100,28 +114,28 @@ DType mean_out_dtype(const Tensor& self, DType dtype) {
 
 // sum_kernel (ReductionKernels.cpp:72-106)
 Tensor sum_kernel(const Tensor& self, DType dtype) {
-    require_float32_input(self, "sum");
+    require_reducible_input(self, "sum");
     return launch(self, TPR_SUM, all_dims(self), sum_out_dtype(self, dtype), {}, 0, 0, "sum");
 }
 
 // sum_dim_kernel (ReductionKernels.cpp:108-189); empty dims -> full sum
 Tensor sum_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, bool keepdim, DType dtype) {
     if (dims.empty()) return sum_kernel(self, dtype);
-    require_float32_input(self, "sum");
+    require_reducible_input(self, "sum");
     const auto shape = reductionShape(self.shape(), dims, keepdim);
     return launch(self, TPR_SUM, mask_of(self, dims), sum_out_dtype(self, dtype), shape, 0, 0, "sum");
 }
 
 // mean_kernel (ReductionKernels.cpp:191-196)
 Tensor mean_kernel(const Tensor& self, DType dtype) {
-    require_float32_input(self, "mean");
+    require_reducible_input(self, "mean");
     return launch(self, TPR_MEAN, all_dims(self), mean_out_dtype(self, dtype), {}, 0, 0, "mean");
 }
 
 // mean_dim_kernel (ReductionKernels.cpp:198-211)
 Tensor mean_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, bool keepdim, DType dtype) {
     if (dims.empty()) return mean_kernel(self, dtype);
-    require_float32_input(self, "mean");
+    require_reducible_input(self, "mean");
     const auto shape = reductionShape(self.shape(), dims, keepdim);
     return launch(self, TPR_MEAN, mask_of(self, dims), mean_out_dtype(self, dtype), shape, 0,
                   listed_count(self, dims), "mean");
@@ -129,12 +143,12 @@ Tensor mean_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, boo
 
 // max_kernel / min_kernel (ReductionKernels.cpp:231-254, :317-340): empty -> RuntimeError
 Tensor max_kernel(const Tensor& self) {
-    require_float32_input(self, "max");
+    require_reducible_input(self, "max");
     if (self.numel() == 0) TP_THROW(RuntimeError, "max(): Expected reduction dim to be non-empty");
     return launch(self, TPR_AMAX, all_dims(self), self.dtype(), {}, 0, 0, "max");
 }
 Tensor min_kernel(const Tensor& self) {
-    require_float32_input(self, "min");
+    require_reducible_input(self, "min");
     if (self.numel() == 0) TP_THROW(RuntimeError, "min(): Expected reduction dim to be non-empty");
     return launch(self, TPR_AMIN, all_dims(self), self.dtype(), {}, 0, 0, "min");
 }
@@ -142,13 +156,13 @@ Tensor min_kernel(const Tensor& self) {
 // max_dim_kernel / min_dim_kernel (ReductionKernels.cpp:256-315, :342-401)
 Tensor max_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, bool keepdim) {
     if (dims.empty()) return max_kernel(self);
-    require_float32_input(self, "max");
+    require_reducible_input(self, "max");
     return launch(self, TPR_AMAX, mask_of(self, dims), self.dtype(), reductionShape(self.shape(), dims, keepdim), 0,
                   0, "max");
 }
 Tensor min_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, bool keepdim) {
     if (dims.empty()) return min_kernel(self);
-    require_float32_input(self, "min");
+    require_reducible_input(self, "min");
     return launch(self, TPR_AMIN, mask_of(self, dims), self.dtype(), reductionShape(self.shape(), dims, keepdim), 0,
                   0, "min");
 }
@@ -160,7 +174,7 @@ Tensor min_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, bool
 // dims in their original order.
 static Tensor arg_kernel(const Tensor& self, std::optional<int64_t> dim, bool keepdim, bool is_max) {
     const char* name = is_max ? "argmax" : "argmin";
-    require_float32_input(self, name);
+    require_reducible_input(self, name);
     const int op = is_max ? TPR_ARGMAX : TPR_ARGMIN;
     if (!dim.has_value()) return launch(self, op, all_dims(self), DType::Int64, {}, 0, 0, name);
     int64_t d = *dim;
@@ -208,12 +222,12 @@ Tensor std_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, int6
 // sum (integral -> Int64); float inputs multiply in fp64 here (the reference
 // multiplies in the output dtype).  Empty dims -> full product.
 Tensor prod_kernel(const Tensor& self, DType dtype) {
-    require_float32_input(self, "prod");
+    require_reducible_input(self, "prod");
     return launch(self, TPR_PROD, all_dims(self), sum_out_dtype(self, dtype), {}, 0, 0, "prod");
 }
 Tensor prod_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, bool keepdim, DType dtype) {
     if (dims.empty()) return prod_kernel(self, dtype);
-    require_float32_input(self, "prod");
+    require_reducible_input(self, "prod");
     const auto shape = reductionShape(self.shape(), dims, keepdim);
     return launch(self, TPR_PROD, mask_of(self, dims), sum_out_dtype(self, dtype), shape, 0, 0, "prod");
 }
@@ -222,7 +236,7 @@ Tensor prod_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, boo
 // (ReductionKernels.cpp:517-677): Bool output, x != 0 is true (NaN is true).
 static Tensor bool_reduce(const Tensor& self, const std::vector<int64_t>* dims, bool keepdim, bool is_any) {
     const char* name = is_any ? "any" : "all";
-    require_float32_input(self, name);
+    require_reducible_input(self, name);
     const int op = is_any ? TPR_ANY : TPR_ALL;
     if (!dims || dims->empty()) return launch(self, op, all_dims(self), DType::Bool, {}, 0, 0, name);
     return launch(self, op, mask_of(self, *dims), DType::Bool, reductionShape(self.shape(), *dims, keepdim), 0, 0,

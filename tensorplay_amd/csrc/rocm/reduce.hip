@@ -203,6 +203,7 @@ struct Fin {
     double count;   // divisor count (reference semantics, duplicates included)
     double corr;    // VAR/STD correction
     float p;        // NORM exponent (passed to every op's acc; only NormOp reads it)
+    int out_esize;  // bytes per output element (integer amax/amin write the input dtype)
     double inv_p;   // NORM: 1/p
 };
 
@@ -638,6 +639,8 @@ long long pow2_ceil(long long v) {
     return p;
 }
 
+int esize_of(int dt);
+
 int validate(const tpr_reduce_desc* d) {
     if (!d) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: null descriptor");
     if (d->ndim < 0 || d->ndim > TPR_MAX_DIMS)
@@ -647,8 +650,34 @@ int validate(const tpr_reduce_desc* d) {
         if (d->sizes[i] < 0) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: negative size");
     if (d->ndim < 32 && (d->reduce_mask >> d->ndim) != 0)
         return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: reduce_mask names a dim >= ndim");
-    if (d->in_dtype != TPR_FLOAT32)
-        return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: only float32 input is implemented");
+    if (d->in_dtype != TPR_FLOAT32) {
+        if (esize_of(d->in_dtype) == 0)
+            return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: input dtype not implemented");
+        switch (d->op) {
+            case TPR_SUM: case TPR_PROD:
+                if (d->out_dtype != TPR_INT64)
+                    return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: integer sum/prod output must be int64");
+                return TPR_OK;
+            case TPR_MEAN:
+                if (d->out_dtype != TPR_FLOAT32 && d->out_dtype != TPR_FLOAT64)
+                    return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: mean output must be float32 or float64");
+                return TPR_OK;
+            case TPR_AMAX: case TPR_AMIN:
+                if (d->out_dtype != d->in_dtype)
+                    return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: amax/amin output dtype must equal input dtype");
+                return TPR_OK;
+            case TPR_ARGMAX: case TPR_ARGMIN:
+                if (d->out_dtype != TPR_INT64)
+                    return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: argmax/argmin output must be int64");
+                return TPR_OK;
+            case TPR_ALL: case TPR_ANY:
+                if (d->out_dtype != TPR_BOOL)
+                    return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: all/any output must be bool");
+                return TPR_OK;
+            default:
+                return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: var/std/norm/median need float32 input");
+        }
+    }
     switch (d->op) {
         case TPR_SUM: case TPR_MEAN: case TPR_PROD:
             if (d->out_dtype != TPR_FLOAT32 && d->out_dtype != TPR_FLOAT64)
@@ -910,6 +939,466 @@ int run(const Plan& p, const float* in, void* out, void* ws, Fin fin, hipStream_
 }
 
 // ---------------------------------------------------------------------------
+// Integer and bool inputs (int8/int16/int32/int64/uint8/bool): sum/mean/prod,
+// amax/amin/argmax/argmin and all/any.  Semantics of the reference's integer
+// instantiations (ReductionKernels.cpp): mean converts to Float32 first
+// (IntMeanOp), sum/prod accumulate in Int64
+// (AccumulateType, :31-35; wrap-around, so the result does not depend on the
+// order), max/min/argmax/argmin start from numeric_limits::lowest/max with the
+// strict compare (:213-229), all/any test x != 0.  Results are bit-exact.
+// The kernels read 16-byte vectors of 16/sizeof(T) elements; the planner is
+// the float one, re-tuned for the element size (adapt_plan_int).
+// ---------------------------------------------------------------------------
+struct SumI { long long s; };
+struct ArgSI { long long v; long long i; };
+
+__device__ __forceinline__ long long wrap_add(long long a, long long b) {
+    return (long long)((unsigned long long)a + (unsigned long long)b);
+}
+__device__ __forceinline__ long long wrap_mul(long long a, long long b) {
+    return (long long)((unsigned long long)a * (unsigned long long)b);
+}
+
+template <class T, bool PROD>
+struct IntSumOp {
+    static constexpr bool kIndexed = false;
+    using Acc = long long;
+    using State = SumI;
+    using Wide = IntSumOp;
+    __device__ static Acc init() { return PROD ? 1 : 0; }
+    template <class I>
+    __device__ static void acc(Acc& a, T x, I, float) { a = PROD ? wrap_mul(a, (long long)x) : wrap_add(a, (long long)x); }
+    __device__ static State state(Acc a) { return {a}; }
+    __device__ static State identity() { return {PROD ? 1 : 0}; }
+    __device__ static State comb(State a, State b) { return {PROD ? wrap_mul(a.s, b.s) : wrap_add(a.s, b.s)}; }
+    __device__ static State shfl(State s, int m) { return {__shfl_xor(s.s, m, kWave)}; }
+};
+
+// Mean of an integer input: the reference converts the input to Float32 first
+// (mean_kernel / mean_dim_kernel pick Float32, sum_kernel's `.to(out_dtype)`,
+// ReductionKernels.cpp:81-84,120-123), so the sum is a floating-point sum of
+// the fp32-rounded values: no Int64 wrap-around.  Accumulated here in fp64.
+template <class T>
+struct IntMeanOp {
+    static constexpr bool kIndexed = false;
+    using Acc = double;
+    using State = SumS;
+    using Wide = IntMeanOp;
+    __device__ static Acc init() { return 0.0; }
+    template <class I>
+    __device__ static void acc(Acc& a, T x, I, float) { a += (double)(float)x; }
+    __device__ static State state(Acc a) { return {a}; }
+    __device__ static State identity() { return {0.0}; }
+    __device__ static State comb(State a, State b) { return {a.s + b.s}; }
+    __device__ static State shfl(State s, int m) { return {__shfl_xor(s.s, m, kWave)}; }
+};
+
+template <class T>
+struct IntLimits {
+    static constexpr long long lo = sizeof(T) == 1 ? (T(-1) < T(0) ? -128LL : 0LL)
+                                  : sizeof(T) == 2 ? -32768LL
+                                  : sizeof(T) == 4 ? -2147483648LL : (-9223372036854775807LL - 1);
+    static constexpr long long hi = sizeof(T) == 1 ? (T(-1) < T(0) ? 127LL : 255LL)
+                                  : sizeof(T) == 2 ? 32767LL
+                                  : sizeof(T) == 4 ? 2147483647LL : 9223372036854775807LL;
+};
+
+// Strict compare in index order (first index wins), from lowest / highest.
+template <class T, bool IS_MAX, class IdxT = int>
+struct IntArgOp {
+    static constexpr bool kIndexed = true;
+    static constexpr IdxT kNone = (IdxT)(sizeof(IdxT) == 4 ? 0x7fffffff : kSentinel);
+    struct Acc { long long v; IdxT i; };
+    using State = ArgSI;
+    using Wide = IntArgOp<T, IS_MAX, long long>;
+    __device__ static Acc init() { return {IS_MAX ? IntLimits<T>::lo : IntLimits<T>::hi, kNone}; }
+    template <class I>
+    __device__ static void acc(Acc& a, T x, I i, float) {
+        const long long v = (long long)x;
+        const bool t = IS_MAX ? (v > a.v) : (v < a.v);
+        a.v = t ? v : a.v;
+        a.i = t ? (IdxT)i : a.i;
+    }
+    __device__ static State state(Acc a) { return {a.v, a.i == kNone ? kSentinel : (long long)a.i}; }
+    __device__ static State identity() { return {IS_MAX ? IntLimits<T>::lo : IntLimits<T>::hi, kSentinel}; }
+    __device__ static State comb(State a, State b) {
+        bool t = IS_MAX ? (b.v > a.v) : (b.v < a.v);
+        t = t || (b.v == a.v && b.i < a.i);
+        return t ? b : a;
+    }
+    __device__ static State shfl(State s, int m) { return {__shfl_xor(s.v, m, kWave), __shfl_xor(s.i, m, kWave)}; }
+};
+
+template <class T, bool ANY>
+struct IntBoolOp {
+    static constexpr bool kIndexed = false;
+    using Acc = int;
+    using State = BoolS;
+    using Wide = IntBoolOp;
+    __device__ static Acc init() { return ANY ? 0 : 1; }
+    template <class I>
+    __device__ static void acc(Acc& a, T x, I, float) {
+        if constexpr (ANY) a |= (x != T(0)) ? 1 : 0;
+        else a &= (x != T(0)) ? 1 : 0;
+    }
+    __device__ static State state(Acc a) { return {a}; }
+    __device__ static State identity() { return {ANY ? 0 : 1}; }
+    __device__ static State comb(State a, State b) { return {ANY ? (a.b | b.b) : (a.b & b.b)}; }
+    __device__ static State shfl(State s, int m) { return {__shfl_xor(s.b, m, kWave)}; }
+};
+
+__device__ __forceinline__ void fin_write(const SumI& s, const Fin&, void* out, long long o) {
+    ((long long*)out)[o] = s.s;
+}
+
+__device__ __forceinline__ void fin_write(const ArgSI& s, const Fin& f, void* out, long long o) {
+    if (f.op == TPR_ARGMAX || f.op == TPR_ARGMIN) {
+        ((long long*)out)[o] = (s.i == kSentinel) ? 0 : s.i;
+        return;
+    }
+    switch (f.out_esize) {  // amax / amin: the input dtype
+        case 1: ((unsigned char*)out)[o] = (unsigned char)s.v; break;
+        case 2: ((short*)out)[o] = (short)s.v; break;
+        case 4: ((int*)out)[o] = (int)s.v; break;
+        default: ((long long*)out)[o] = s.v;
+    }
+}
+
+struct ArgsI {
+    const void* in;
+    // rows
+    long long rows, R, row_stride;
+    // cols
+    long long outer, os, rs, inner, ncb;
+    int S;
+    void* out;
+    void* part;
+    Fin fin;
+};
+
+template <class T, int NV>
+struct alignas(16) Vec16 {
+    T v[NV];
+};
+
+template <class Op, int LANES>
+__device__ __forceinline__ typename Op::State combine_lanes(typename Op::State st, int tid) {
+    using State = typename Op::State;
+    constexpr int BLK = LANES > kBlock ? LANES : kBlock;
+    constexpr int SUBW = LANES < kWave ? LANES : kWave;
+    st = group_reduce_sub_wave<Op, SUBW>(st);
+    if constexpr (LANES > kWave) {
+        constexpr int WPG = LANES / kWave;
+        __shared__ State sh[BLK / kWave];
+        const int w = tid / kWave;
+        const int g = tid / LANES;
+        if (__lane_id() == 0) sh[w] = st;
+        __syncthreads();
+        if (tid % LANES == 0) {
+            State r = sh[g * WPG];
+#pragma unroll
+            for (int i = 1; i < WPG; ++i) r = Op::comb(r, sh[g * WPG + i]);
+            st = r;
+        }
+    }
+    return st;
+}
+
+// Row kernel for integer inputs: [rows, R], R contiguous; NV elements per
+// 16-byte vector (1 = scalar loads).  Split s takes vectors s*LANES + l + k*S*LANES.
+template <class Op, class T, int NV, int LANES>
+__global__ __launch_bounds__(LANES > kBlock ? LANES : kBlock) void k_rows_i(ArgsI a) {
+    using Acc = typename Op::Acc;
+    constexpr int BLK = LANES > kBlock ? LANES : kBlock;
+    constexpr int GROUPS = (LANES >= BLK) ? 1 : BLK / LANES;
+    const float prm = a.fin.p;
+    const int tid = threadIdx.x;
+    const int g = tid / LANES;
+    const int l = tid % LANES;
+    const long long rb = blockIdx.x / a.S;
+    const int s = blockIdx.x % a.S;
+    const long long row = rb * GROUPS + g;
+    Acc acc = Op::init();
+    if (row < a.rows) {
+        const T* p = static_cast<const T*>(a.in) + row * a.row_stride;
+        const int R = (int)a.R;
+        int tail = 0;
+        if constexpr (NV > 1) {
+            const int nv = R / NV;
+            const Vec16<T, NV>* pv = reinterpret_cast<const Vec16<T, NV>*>(p);
+            for (int v = s * LANES + l; v < nv; v += a.S * LANES) {
+                const Vec16<T, NV> t = pv[v];
+#pragma unroll
+                for (int j = 0; j < NV; ++j) Op::acc(acc, t.v[j], v * NV + j, prm);
+            }
+            tail = nv * NV;
+        }
+        for (int e = tail + s * LANES + l; e < R; e += a.S * LANES) Op::acc(acc, p[e], e, prm);
+    }
+    typename Op::State st = combine_lanes<Op, LANES>(Op::state(acc), tid);
+    if (l == 0 && row < a.rows) {
+        if (a.S == 1) fin_write(st, a.fin, a.out, row);
+        else reinterpret_cast<typename Op::State*>(a.part)[(long long)s * a.rows + row] = st;
+    }
+}
+
+// Column kernel for integer inputs: [outer, R, inner], inner contiguous; TX
+// threads across inner (NV columns each), 256/TX thread rows across R.
+template <class Op, class T, int NV, int TX>
+__global__ __launch_bounds__(kBlock) void k_cols_i(ArgsI a) {
+    using Acc = typename Op::Acc;
+    using State = typename Op::State;
+    constexpr int TY = kBlock / TX;
+    const float prm = a.fin.p;
+    const int tid = threadIdx.x;
+    const int tx = tid % TX;
+    const int ty = tid / TX;
+    const int s = blockIdx.x % a.S;
+    const long long ob = blockIdx.x / a.S;
+    const long long cb = ob % a.ncb;
+    const long long o = ob / a.ncb;
+    const long long col0 = (cb * TX + tx) * NV;
+    Acc acc[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) acc[j] = Op::init();
+    if (col0 < a.inner) {
+        const T* base = static_cast<const T*>(a.in) + o * a.os + col0;
+        const int R = (int)a.R;
+        const int rstep = TY * a.S;
+        if (NV > 1 && col0 + NV <= a.inner) {
+            for (int r = s * TY + ty; r < R; r += rstep) {
+                const Vec16<T, NV> t = *reinterpret_cast<const Vec16<T, NV>*>(base + (long long)r * a.rs);
+#pragma unroll
+                for (int j = 0; j < NV; ++j) Op::acc(acc[j], t.v[j], r, prm);
+            }
+        } else {
+            const int nj = (int)min((long long)NV, a.inner - col0);
+            for (int r = s * TY + ty; r < R; r += rstep) {
+                const T* q = base + (long long)r * a.rs;
+#pragma unroll
+                for (int j = 0; j < NV; ++j)
+                    if (j < nj) Op::acc(acc[j], q[j], r, prm);
+            }
+        }
+    }
+    State st[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) st[j] = Op::state(acc[j]);
+    if constexpr (TY > 1) {
+        __shared__ State sh[(TY > 1 ? TY / 2 : 1) * TX * NV];
+#pragma unroll
+        for (int half = TY / 2; half >= 1; half /= 2) {
+            if (ty >= half && ty < 2 * half) {
+#pragma unroll
+                for (int j = 0; j < NV; ++j) sh[((ty - half) * TX + tx) * NV + j] = st[j];
+            }
+            __syncthreads();
+            if (ty < half) {
+#pragma unroll
+                for (int j = 0; j < NV; ++j) st[j] = Op::comb(st[j], sh[(ty * TX + tx) * NV + j]);
+            }
+            __syncthreads();
+        }
+    }
+    if (ty == 0) {
+        const long long nout = a.outer * a.inner;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const long long c = col0 + j;
+            if (c < a.inner) {
+                const long long oi = o * a.inner + c;
+                if (a.S == 1) fin_write(st[j], a.fin, a.out, oi);
+                else reinterpret_cast<State*>(a.part)[(long long)s * nout + oi] = st[j];
+            }
+        }
+    }
+}
+
+struct GenArgsI {
+    const void* in;
+    int nk, nr;
+    long long ksz[TPR_MAX_DIMS], kst[TPR_MAX_DIMS];
+    long long rsz[TPR_MAX_DIMS], rst[TPR_MAX_DIMS];
+    long long nout, count, seg;
+    int S;
+    void* out;
+    void* part;
+    Fin fin;
+};
+
+template <class Op, class T>
+__global__ __launch_bounds__(kBlock) void k_general_i(GenArgsI a) {
+    using Acc = typename Op::Acc;
+    using State = typename Op::State;
+    const float prm = a.fin.p;
+    const long long o = blockIdx.x / a.S;
+    const int s = blockIdx.x % a.S;
+    long long base = 0;
+    {
+        long long rem = o;
+        for (int d = a.nk - 1; d >= 0; --d) {
+            base += (rem % a.ksz[d]) * a.kst[d];
+            rem /= a.ksz[d];
+        }
+    }
+    const T* in = static_cast<const T*>(a.in);
+    Acc acc = Op::init();
+    const long long beg = (long long)s * a.seg;
+    const long long end = min(a.count, beg + a.seg);
+    for (long long j = beg + threadIdx.x; j < end; j += kBlock) {
+        long long rem = j, off = 0;
+        for (int d = a.nr - 1; d >= 0; --d) {
+            off += (rem % a.rsz[d]) * a.rst[d];
+            rem /= a.rsz[d];
+        }
+        Op::acc(acc, in[base + off], j, prm);
+    }
+    State st = block_reduce<Op>(Op::state(acc));
+    if (threadIdx.x == 0) {
+        if (a.S == 1) fin_write(st, a.fin, a.out, o);
+        else reinterpret_cast<State*>(a.part)[(long long)s * a.nout + o] = st;
+    }
+}
+
+int esize_of(int dt) {
+    switch (dt) {
+        case TPR_UINT8: case TPR_INT8: case TPR_BOOL: return 1;
+        case TPR_INT16: return 2;
+        case TPR_INT32: return 4;
+        case TPR_INT64: return 8;
+        default: return 0;
+    }
+}
+
+size_t int_state_size(int op) {
+    switch (op) {
+        case TPR_SUM: case TPR_PROD: return sizeof(SumI);
+        case TPR_MEAN: return sizeof(SumS);
+        case TPR_ALL: case TPR_ANY: return sizeof(BoolS);
+        default: return sizeof(ArgSI);
+    }
+}
+
+// Re-tunes a float plan for integer elements of `es` bytes (NV = 16/es per
+// vector).  Rows: lanes rounded up to 16/64/256/1024.  Columns: 256-thread
+// workgroups, TX 64/128/256, splits recomputed on NV-wide columns.  The
+// workspace size depends on the descriptor only, never on the pointer.
+void adapt_plan_int(Plan& p, const tpr_reduce_desc* d, const void* in, int es) {
+    const int NV = 16 / es;
+    const bool aligned16 = (reinterpret_cast<uintptr_t>(in) & 15u) == 0;
+    const auto& dev = device_info();
+    const long long target = (long long)dev.cus * 512;
+    p.state_bytes = int_state_size(d->op);
+    if (p.kind == P_ROWS) {
+        p.vec = (aligned16 && (p.rows == 1 || p.row_stride % NV == 0) && p.R >= NV) ? NV : 1;
+        int L = 16;
+        while (L < p.lanes && L < 1024) L *= 4;
+        p.lanes = L;
+        if (knobs().splits <= 0) {
+            const long long threads = p.rows * p.lanes;
+            const long long vecs = std::max(1LL, ceil_div(p.R, (long long)NV * p.lanes));
+            p.S = threads < target ? std::max(1LL, std::min(ceil_div(target, threads), vecs)) : 1;
+        }
+    } else if (p.kind == P_COLS) {
+        p.vec = (aligned16 && p.rs % NV == 0 && (p.outer == 1 || p.os % NV == 0) && p.inner >= NV) ? NV : 1;
+        p.colblock = kBlock;
+        const long long colsv = ceil_div(p.inner, NV);
+        if (!(knobs().tx == 64 || knobs().tx == 128 || knobs().tx == 256))
+            p.tx = (p.outer * ceil_div(colsv, 256) * kBlock >= target || p.R < 16) ? 256 : 64;
+        p.ncb = ceil_div(ceil_div(p.inner, p.vec), p.tx);
+        const long long ty = kBlock / p.tx;
+        const long long threads = p.outer * ceil_div(colsv, p.tx) * kBlock;
+        long long S = 1;
+        if (threads < target) S = std::min(ceil_div(target, threads), std::max(1LL, p.R / (ty * 8)));
+        if (knobs().splits > 0) S = knobs().splits;
+        p.S = std::max(1LL, std::min(S, ceil_div(p.R, ty)));
+    }
+    p.ws = (p.S > 1) ? (size_t)p.S * (size_t)p.nout * p.state_bytes : 0;
+}
+
+template <class Op, class T>
+int run_int_op(const Plan& p, const void* in, void* out, void* ws, Fin fin, hipStream_t st) {
+    constexpr int NV = 16 / (int)sizeof(T);
+    if (p.kind == P_ROWS) {
+        ArgsI a{};
+        a.in = in; a.rows = p.rows; a.R = p.R; a.row_stride = p.row_stride;
+        a.S = (int)p.S; a.out = out; a.part = ws; a.fin = fin;
+        const long long groups = (p.lanes >= kBlock) ? 1 : kBlock / p.lanes;
+        const dim3 grid(ceil_div(p.rows, groups) * p.S);
+        const dim3 blk(p.lanes > kBlock ? p.lanes : kBlock);
+#define TPR_ROWS_I(L)                                                                               \
+    case L:                                                                                         \
+        if (p.vec > 1) hipLaunchKernelGGL((k_rows_i<Op, T, NV, L>), grid, blk, 0, st, a);          \
+        else hipLaunchKernelGGL((k_rows_i<Op, T, 1, L>), grid, blk, 0, st, a);                     \
+        break;
+        switch (p.lanes) {
+            TPR_ROWS_I(16)
+            TPR_ROWS_I(64)
+            TPR_ROWS_I(256)
+            TPR_ROWS_I(1024)
+            default: return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: lanes must be 16/64/256/1024 for integer inputs");
+        }
+#undef TPR_ROWS_I
+    } else if (p.kind == P_COLS) {
+        ArgsI a{};
+        a.in = in; a.outer = p.outer; a.os = p.os; a.R = p.R; a.rs = p.rs; a.inner = p.inner; a.ncb = p.ncb;
+        a.S = (int)p.S; a.out = out; a.part = ws; a.fin = fin;
+        const dim3 grid(p.outer * p.ncb * p.S);
+#define TPR_COLS_I(TXV)                                                                             \
+    if (p.tx == TXV) {                                                                              \
+        if (p.vec > 1) hipLaunchKernelGGL((k_cols_i<Op, T, NV, TXV>), grid, dim3(kBlock), 0, st, a); \
+        else hipLaunchKernelGGL((k_cols_i<Op, T, 1, TXV>), grid, dim3(kBlock), 0, st, a);          \
+    }
+        TPR_COLS_I(256)
+        else TPR_COLS_I(128)
+        else TPR_COLS_I(64)
+        else return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: tx must be 64, 128 or 256");
+#undef TPR_COLS_I
+    } else {
+        GenArgsI a{};
+        a.in = in; a.nk = p.nk; a.nr = p.nr;
+        for (int i = 0; i < TPR_MAX_DIMS; ++i) {
+            a.ksz[i] = i < p.nk ? p.ksz[i] : 1;
+            a.kst[i] = i < p.nk ? p.kst[i] : 0;
+            a.rsz[i] = i < p.nr ? p.rsz[i] : 1;
+            a.rst[i] = i < p.nr ? p.rst[i] : 0;
+        }
+        a.nout = p.nout; a.count = p.count; a.seg = p.seg; a.S = (int)p.S;
+        a.out = out; a.part = ws; a.fin = fin;
+        hipLaunchKernelGGL((k_general_i<typename Op::Wide, T>), dim3(p.nout * p.S), dim3(kBlock), 0, st, a);
+    }
+    int rc = check_launch("k_reduce_int");
+    if (rc != TPR_OK) return rc;
+    if (p.S > 1) rc = launch_finalize<Op>(p, out, ws, fin, st);
+    return rc;
+}
+
+template <class T>
+int run_int_t(int op, const Plan& p, const void* in, void* out, void* ws, Fin fin, hipStream_t st) {
+    switch (op) {
+        case TPR_SUM: return run_int_op<IntSumOp<T, false>, T>(p, in, out, ws, fin, st);
+        case TPR_MEAN: return run_int_op<IntMeanOp<T>, T>(p, in, out, ws, fin, st);
+        case TPR_PROD: return run_int_op<IntSumOp<T, true>, T>(p, in, out, ws, fin, st);
+        case TPR_AMAX: case TPR_ARGMAX: return run_int_op<IntArgOp<T, true>, T>(p, in, out, ws, fin, st);
+        case TPR_AMIN: case TPR_ARGMIN: return run_int_op<IntArgOp<T, false>, T>(p, in, out, ws, fin, st);
+        case TPR_ALL: return run_int_op<IntBoolOp<T, false>, T>(p, in, out, ws, fin, st);
+        case TPR_ANY: return run_int_op<IntBoolOp<T, true>, T>(p, in, out, ws, fin, st);
+        default: return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: op not implemented for integer inputs");
+    }
+}
+
+int run_int(const tpr_reduce_desc* d, const Plan& p, const void* in, void* out, void* ws, Fin fin, hipStream_t st) {
+    switch (d->in_dtype) {
+        case TPR_UINT8: case TPR_BOOL: return run_int_t<unsigned char>(d->op, p, in, out, ws, fin, st);
+        case TPR_INT8: return run_int_t<signed char>(d->op, p, in, out, ws, fin, st);
+        case TPR_INT16: return run_int_t<short>(d->op, p, in, out, ws, fin, st);
+        case TPR_INT32: return run_int_t<int>(d->op, p, in, out, ws, fin, st);
+        default: return run_int_t<long long>(d->op, p, in, out, ws, fin, st);
+    }
+}
+
+
+// ---------------------------------------------------------------------------
 // Median (median_kernel, ReductionKernels.cpp:874-901: the (n-1)/2-th smallest
 // element).  Exact radix select over ascending sortable keys in three passes of
 // 11/11/10 bits.  Each pass streams the input once: workgroups build LDS
@@ -1078,8 +1567,9 @@ extern "C" {
 size_t tpr_reduce_workspace_bytes(const tpr_reduce_desc* desc) {
     if (tpr::validate(desc) != TPR_OK) return 0;
     // alignment does not change the workspace size; plan with an aligned pointer
-    const tpr::Plan p = tpr::make_plan(desc, nullptr);
+    tpr::Plan p = tpr::make_plan(desc, nullptr);
     if (desc->op == TPR_MEDIAN) return p.count > 0 ? tpr::median_ws_bytes(p.count, nullptr) : 0;
+    if (desc->in_dtype != TPR_FLOAT32) tpr::adapt_plan_int(p, desc, nullptr, tpr::esize_of(desc->in_dtype));
     return p.ws;
 }
 
@@ -1095,6 +1585,8 @@ int tpr_reduce(const tpr_reduce_desc* desc, const void* in, void* out, void* wor
     if (desc->op == TPR_MEDIAN)
         return run_median(desc, p, static_cast<const float*>(in), out, workspace, workspace_bytes,
                           static_cast<hipStream_t>(stream));
+    const bool int_in = desc->in_dtype != TPR_FLOAT32;
+    if (int_in) adapt_plan_int(p, desc, in, esize_of(desc->in_dtype));
     if (p.ws > 0 && (workspace == nullptr || workspace_bytes < p.ws))
         return fail(TPR_ERR_WORKSPACE, "tpr_reduce: workspace too small (need " +
                                            std::to_string(p.ws) + " bytes)");
@@ -1105,8 +1597,10 @@ int tpr_reduce(const tpr_reduce_desc* desc, const void* in, void* out, void* wor
     fin.corr = (double)desc->correction;
     fin.p = (float)desc->p;
     fin.inv_p = 1.0 / desc->p;
-    const float* x = static_cast<const float*>(in);
+    fin.out_esize = int_in ? esize_of(desc->in_dtype) : 4;
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (int_in) return run_int(desc, p, in, out, workspace, fin, st);
+    const float* x = static_cast<const float*>(in);
     switch (desc->op) {
         case TPR_SUM: case TPR_MEAN: return run<SumOp>(p, x, out, workspace, fin, st);
         case TPR_PROD: return run<ProdOp>(p, x, out, workspace, fin, st);

@@ -44,8 +44,15 @@ def test_argument_validation_without_gpu():
     d = _capi.make_desc("sum", [4, 4], [4, 1], [1], _capi.FLOAT32)
     d.in_dtype = _capi.INT32
     rc = L.tpr_reduce(ctypes.byref(d), None, None, None, 0, None)
-    assert rc == _capi.ERR_UNSUPPORTED_DTYPE
+    assert rc == _capi.ERR_UNSUPPORTED_DTYPE  # integral sums write Int64
+    assert b"int64" in L.tpr_last_error()
+    d = _capi.make_desc("var", [4, 4], [4, 1], [1], _capi.FLOAT32)
+    d.in_dtype = _capi.INT32
+    assert L.tpr_reduce(ctypes.byref(d), None, None, None, 0, None) == _capi.ERR_UNSUPPORTED_DTYPE
     assert b"float32" in L.tpr_last_error()
+    d = _capi.make_desc("sum", [4, 4], [4, 1], [1], _capi.FLOAT32)
+    d.in_dtype = 99
+    assert L.tpr_reduce(ctypes.byref(d), None, None, None, 0, None) == _capi.ERR_UNSUPPORTED_DTYPE
     d = _capi.make_desc("argmax", [4, 4], [4, 1], [1], _capi.FLOAT32)
     assert L.tpr_reduce(ctypes.byref(d), None, None, None, 0, None) == _capi.ERR_INVALID_ARG
     rc = L.tpr_topk(None, _capi.FLOAT32, 2, 5, 5, 6, 1, 1, None, None, None, 0, None)

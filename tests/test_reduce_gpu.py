@@ -368,3 +368,110 @@ def test_new_ops_config_shapes():
     check(x, t, "norm", [0], p=float("inf"))
     check(x, t, "any", [0])
 
+
+
+# ---- integer and bool inputs ----
+# Integer reductions are exact and order-independent (Int64 wrap-around sums
+# and products; mean is a float sum of the fp32-converted values, within
+# the float tolerance, strict-compare max/min/argmax with the first index, x != 0 for
+# all/any), so numpy's own reductions are their closed forms: bit-exact.
+
+INT_DTYPES = ["int32", "int64", "uint8", "int8", "int16", "bool"]
+INT_OPS = ["sum", "prod", "mean", "amax", "amin", "argmax", "argmin", "all", "any"]
+
+
+def _np_int_ref(v, op, dims):
+    ax = None if dims is None else tuple(dims)
+    if op == "sum":
+        return v.astype(np.int64).sum(axis=ax)
+    if op == "prod":
+        return v.astype(np.int64).prod(axis=ax)
+    if op == "mean":  # the reference converts to Float32 before summing
+        return v.astype(np.float32).astype(np.float64).mean(axis=ax)
+    if op in ("amax", "amin"):
+        if v.size == 0:
+            return None
+        return (np.max if op == "amax" else np.min)(v, axis=ax)
+    if op in ("argmax", "argmin"):
+        f = np.argmax if op == "argmax" else np.argmin
+        if dims is None:
+            return np.int64(f(v.ravel()))
+        return f(v, axis=dims[0]).astype(np.int64)
+    if op == "all":
+        return (v != 0).all(axis=ax)
+    return (v != 0).any(axis=ax)
+
+
+def _int_view_data(rng, dt, shape):
+    if dt == "bool":
+        return rng.random(shape) < 0.7
+    info = np.iinfo(dt)
+    if dt in ("int32", "int64"):
+        b = rng.integers(-5, 6, size=shape).astype(dt)  # ties for argmax
+        big = rng.integers(info.min // 2, info.max // 2, size=shape, dtype=dt)
+        return np.where(rng.random(shape) < 0.5, big, b)  # wrap-around sums / products
+    return rng.integers(info.min, int(info.max) + 1, size=shape).astype(dt)
+
+
+def check_int(v, t, op, dims):
+    print(f"case int op={op} dtype={v.dtype} shape={v.shape} strides={v.strides} dims={dims}", flush=True)
+    if op in ("argmax", "argmin") and dims is not None and len(dims) > 1:
+        return
+    exp = _np_int_ref(v, op, dims)
+    if exp is None:
+        return
+    got = _capi.reduce(t, op, dims).cpu().numpy()
+    exp = np.asarray(exp)
+    if op == "mean":
+        assert_close_rel(got.reshape(exp.shape), exp)
+    else:
+        with np.errstate(over="ignore"):
+            np.testing.assert_array_equal(got.reshape(exp.shape), exp.astype(got.dtype))
+
+
+@pytest.mark.parametrize("dt", INT_DTYPES)
+def test_integer_inputs_random_layouts(dt):
+    rng = np.random.default_rng(18)
+    tdt = getattr(torch, dt)
+    for shape in [(7,), (33, 5), (5, 1000), (16, 4096), (3, 17, 129), (4, 8, 6, 5), (2, 70001)]:
+        b = _int_view_data(rng, dt, shape)
+        t = torch.from_numpy(b).cuda()
+        views = [(b, t)]
+        if b.ndim >= 2:
+            views.append((b[:, 1:], t[:, 1:]))          # misaligned rows
+            views.append((b.T, t.permute(*reversed(range(t.ndim)))))  # transposed (general / cols)
+            views.append((b[:, ::3], t[:, ::3]))        # stepped inner dim
+        for v, tv in views:
+            for dims in _dim_sets(v.ndim):
+                for op in INT_OPS:
+                    check_int(v, tv, op, dims)
+
+
+@pytest.mark.parametrize("knob,values", [("general", [1]), ("splits", [1, 3, 64]), ("lanes", [16, 64, 256, 1024]),
+                                         ("tx", [64, 128, 256])])
+def test_integer_forced_plans(knob, values):
+    rng = np.random.default_rng(19)
+    a = _int_view_data(rng, "int32", (37, 1029))
+    c = _int_view_data(rng, "uint8", (5, 300, 36))
+    for val in values:
+        _capi.debug_set(knob, val)
+        for op in INT_OPS:
+            check_int(a, torch.from_numpy(a).cuda(), op, [1])
+            check_int(a, torch.from_numpy(a).cuda(), op, None)
+            check_int(c, torch.from_numpy(c).cuda(), op, [1])
+            check_int(c, torch.from_numpy(c).cuda(), op, [0])
+
+
+def test_integer_extremes_and_empty():
+    x = np.array([[np.iinfo(np.int64).min] * 3, [np.iinfo(np.int64).max, 1, np.iinfo(np.int64).max]], np.int64)
+    t = torch.from_numpy(x).cuda()
+    for op in INT_OPS:
+        for dims in (None, [0], [1]):
+            check_int(x, t, op, dims)
+    # all elements at the lowest value: argmax stays at index 0 (strict compare)
+    y = np.full(1000, np.iinfo(np.int32).min, np.int32)
+    assert int(_capi.reduce(torch.from_numpy(y).cuda(), "argmax", None).cpu()) == 0
+    e = torch.zeros((0, 4), dtype=torch.int32, device="cuda")
+    assert (_capi.reduce(e, "sum", [0]).cpu().numpy() == 0).all()
+    assert (_capi.reduce(e, "prod", [0]).cpu().numpy() == 1).all()
+    assert _capi.reduce(e, "all", [0]).cpu().numpy().all()

@@ -118,7 +118,15 @@ def test_dims_dtypes_and_errors():
         tp.empty([0], device=DEV).max()
     assert math.isnan(tp.empty([0], device=DEV).var().item())
     with pytest.raises(NotImplementedError):
-        tp.tensor(np.ones(3, np.int64), device=DEV).sum()
+        tp.tensor(np.ones(3, np.int64), device=DEV).var()
+    # integral inputs: sum -> Int64 (DType.h promotion), mean -> Float32, max keeps the dtype
+    i = tp.tensor(np.array([[3, -7, 5], [2, 9, 9]], np.int32), device=DEV)
+    si = i.sum()
+    assert si.dtype == tp.int64 and si.item() == 21
+    assert i.mean().dtype == tp.float32 and abs(i.mean().item() - 3.5) < 1e-6
+    assert i.max().dtype == tp.int32 and i.max().item() == 9
+    np.testing.assert_array_equal(i.argmax(1).numpy(), [2, 1])  # first of the tied 9s
+    np.testing.assert_array_equal(i.sum([0]).numpy(), [5, 2, 14])
     # strided (non-contiguous) inputs reduce without a copy
     p = t.permute([2, 0, 1])
     np.testing.assert_allclose(p.mean(1).numpy(), a.transpose(2, 0, 1).astype(np.float64).mean(1), rtol=1e-5)
