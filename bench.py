@@ -93,6 +93,25 @@ def topk_call(torch, capi, x, k, stream):
     return c
 
 
+KIND_NAMES = {0: "k_copy_contig", 1: "k_copy_rows", 2: "k_copy_tile", 3: "k_copy_elem"}
+
+
+def copy_kernel_name(plan):
+    return KIND_NAMES[plan & 3] + ("_v" if plan & 2 == 2 and plan & 4 else "")
+
+
+def copy_call(torch, capi, dst, src, stream):
+    tmap = capi._torch_dtypes()
+    desc = capi.make_copy_desc(list(dst.shape), list(dst.stride()), list(src.stride()), tmap[dst.dtype],
+                               tmap[src.dtype])
+    L = capi.lib()
+    c = Call(L.tpr_copy, (ctypes.byref(desc), ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(src.data_ptr()),
+                          stream))
+    c.keep = (desc, dst)
+    c.bytes = src.numel() * src.element_size() + dst.numel() * dst.element_size()
+    return c
+
+
 def time_calls(torch, step_fns, steps, warmup):
     """Run warmup, then time `steps` iterations of step_fns[i % len] with HIP events."""
     for i in range(warmup):
@@ -260,6 +279,22 @@ def main():
         extras["C5_logits_256x151936"] = e5
         keep_c5 = b5[0]
         del b5, c5, c5a
+        # copy_ (strided / casting) on the C2 geometry: read + write bytes
+        ecp = {}
+        cases = {"permute_1_2_0": (lambda b: b.permute(1, 2, 0), torch.float32),
+                 "transpose_1_2": (lambda b: b.transpose(1, 2), torch.float32),
+                 "clone_dense": (lambda b: b, torch.float32),
+                 "cast_f32_to_f64": (lambda b: b, torch.float64)}
+        for name, (view, odt) in cases.items():
+            outs = [torch.empty(view(bufs[0]).shape, dtype=odt, device=dev) for _ in range(2)]
+            cc = [copy_call(torch, capi, outs[i % 2], view(bufs[i % nbuf]), stream) for i in range(6)]
+            ms = time_calls(torch, cc, max(steps, 12), warmup)
+            by = cc[0].bytes
+            ecp[name] = {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
+                         "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4), "alg_bytes": by,
+                         "kernel": copy_kernel_name(capi.copy_plan(outs[0], view(bufs[0])))}
+            del outs, cc
+        extras["copy_C2_64x1024x1024"] = ecp
     if args.calibrate_copy:
         xc = gen(torch, (64 << 20,), "normal", 6000, dev)
         for _ in range(3):

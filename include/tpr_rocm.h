@@ -127,7 +127,34 @@ int tpr_topk(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t 
              int64_t k, int32_t largest, int32_t sorted, void* out_values, void* out_indices,
              void* workspace, size_t workspace_bytes, void* stream);
 
-/* Strided -> dense copy (row-major over sizes).  Counterpart of the CUDA
+/* Strided, casting copy: dst[idx] = static_cast<dst_dtype>(src[idx]) for
+ * every index of sizes[0..ndim).  Strides are in elements, per side; a
+ * stride-0 source dim broadcasts.  Replaces DispatchStub::call("copy_",
+ * DispatchKey::CUDA, self, src) -> copy_kernel / copy_cast_kernel_impl
+ * (/root/reference/p10/src/backend/cuda/CopyKernels.cu:42-157) for a
+ * device-resident source; casts follow the CPU path's static_cast
+ * (/root/reference/p10/src/backend/cpu/CopyKernels.cpp:27-55).  Overlapping
+ * destination elements are undefined, as in the reference. */
+typedef struct tpr_copy_desc {
+    int32_t ndim;
+    int32_t dst_dtype;   /* tpr_dtype */
+    int32_t src_dtype;   /* tpr_dtype */
+    int32_t reserved0;
+    int64_t sizes[TPR_MAX_DIMS];
+    int64_t dst_strides[TPR_MAX_DIMS];
+    int64_t src_strides[TPR_MAX_DIMS];
+} tpr_copy_desc;
+
+int tpr_copy(const tpr_copy_desc* desc, void* dst, const void* src, void* stream);
+
+/* Kernel the planner picks for this copy: bits 0-1 = 0 dense run, 1 rows,
+ * 2 LDS tiles, 3 per element; bit 2 set = the 16-byte vector variant;
+ * -1 = bad descriptor.  Host only, launches nothing; a test hook with no
+ * reference counterpart. */
+int tpr_copy_plan(const tpr_copy_desc* desc, const void* dst, const void* src);
+
+/* Strided -> dense copy (row-major over sizes); tpr_copy with a dense
+ * destination and equal dtypes.  Counterpart of the CUDA
  * backend's copy_cast_kernel_impl / copy_kernel
  * (/root/reference/p10/src/backend/cuda/CopyKernels.cu:42-157) for the layout
  * normalisation the reduction path needs (Tensor::contiguous, topk on a

@@ -11,6 +11,7 @@ Parity status of each function (see tests/test_oracle.py):
   var_all, var_dim (+std)               pinned: known answers (test_cuda_reductions.py:78-91) + torch.var/std
                                         at the reference's own rtol (test_statistical.py:10-17)
   topk                                  pinned: np.argsort(kind="stable") on canonical keys + torch.topk values
+  copy                                  pinned: numpy astype on the same views (C casts), brute force on tiny shapes
 """
 import ctypes
 import os
@@ -54,6 +55,7 @@ def lib():
         L.or_norm_all.argtypes = [vp, i32, _i64p, _i64p, ctypes.c_double, _f32p]; L.or_norm_all.restype = i32
         L.or_norm_dim.argtypes = [vp, i32, _i64p, _i64p, u32, ctypes.c_double, vp]
         L.or_median.argtypes = [vp, i32, _i64p, _i64p]; L.or_median.restype = ctypes.c_float
+        L.or_copy.argtypes = [vp, i32, _i64p, vp, i32, _i64p, i32, _i64p]; L.or_copy.restype = i32
         L.or_topk.argtypes = [vp, i64, i64, i64, i64, i32, vp, vp]
         L.or_topk_mt.argtypes = [vp, i64, i64, i64, i64, i32, vp, vp, i32]
         _lib = L
@@ -229,3 +231,24 @@ def topk(x2d, k, largest=True, threads=1):
     else:
         L.or_topk_mt(*args, threads)
     return vals, idx
+
+
+# P10 ScalarType numbering of numpy dtypes
+DTYPE_CODES = {np.dtype(np.uint8): 0, np.dtype(np.int8): 1, np.dtype(np.int16): 2, np.dtype(np.int32): 3,
+               np.dtype(np.int64): 4, np.dtype(np.uint16): 5, np.dtype(np.uint32): 6, np.dtype(np.uint64): 7,
+               np.dtype(np.float32): 8, np.dtype(np.float64): 9, np.dtype(np.bool_): 10}
+
+
+def copy(dst, src):
+    """copy_ of `src` into `dst` (numpy arrays of one shape, any strides,
+    including stride-0 broadcast views of src).  Writes dst in place."""
+    L = lib()
+    assert dst.shape == src.shape
+    nd = dst.ndim
+    sz = (ctypes.c_int64 * max(nd, 1))(*dst.shape)
+    ds = (ctypes.c_int64 * max(nd, 1))(*[s // dst.itemsize for s in dst.strides])
+    ss = (ctypes.c_int64 * max(nd, 1))(*[s // src.itemsize for s in src.strides])
+    rc = L.or_copy(ctypes.c_void_p(dst.ctypes.data), DTYPE_CODES[dst.dtype], ds,
+                   ctypes.c_void_p(src.ctypes.data), DTYPE_CODES[src.dtype], ss, nd, sz)
+    assert rc == 0
+    return dst

@@ -73,6 +73,12 @@ void or_topk(const float* x, int64_t rows, int64_t cols, int64_t row_stride, int
 void or_topk_mt(const float* x, int64_t rows, int64_t cols, int64_t row_stride, int64_t k,
                 int largest, float* out_vals, int64_t* out_idx, int n_threads);
 
+/* copy_ (cpu/CopyKernels.cpp:27-55, :73-127): dst[idx] = (dst type) src[idx]
+ * over sizes, strides in elements per side, dtypes numbered as P10's
+ * ScalarType (UInt8 0 .. Bool 10).  Returns 0, or -1 for an unknown dtype. */
+int or_copy(void* dst, int dst_dtype, const int64_t* dst_strides, const void* src, int src_dtype,
+            const int64_t* src_strides, int ndim, const int64_t* sizes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -63,7 +63,8 @@ def from_torch(t):
     import torch
     if not t.is_cuda:
         return _C.tensor(t.detach().numpy(), None, "cpu")
-    dt = {torch.float32: float32, torch.float64: float64, torch.int64: int64, torch.int32: int32}[t.dtype]
+    dt = {torch.float32: float32, torch.float64: float64, torch.int64: int64, torch.int32: int32,
+          torch.int16: int16, torch.int8: int8, torch.uint8: uint8, torch.bool: bool_}[t.dtype]
     return _C._from_device_ptr(t.data_ptr(), list(t.shape), list(t.stride()), dt, t.device.index or 0, t)
 
 

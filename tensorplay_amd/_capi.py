@@ -27,13 +27,29 @@ OP_NAMES = {"sum": SUM, "mean": MEAN, "amax": AMAX, "amin": AMIN, "argmax": ARGM
             "any": ANY, "median": MEDIAN}
 
 EXPORTED = ["tpr_reduce_workspace_bytes", "tpr_reduce", "tpr_topk_workspace_bytes", "tpr_topk",
-            "tpr_copy_strided", "tpr_last_error", "tpr_abi_version", "tpr_debug_set"]
+            "tpr_copy", "tpr_copy_plan", "tpr_copy_strided", "tpr_last_error", "tpr_abi_version",
+            "tpr_debug_set"]
+# tpr_copy_plan kinds (bits 0-1) and the vector-variant flag (bit 2)
+COPY_CONTIG, COPY_ROWS, COPY_TILE, COPY_ELEM = range(4)
+COPY_VEC = 4
 
 
 class TprError(RuntimeError):
     def __init__(self, status, msg):
         super().__init__(f"tpr status {status}: {msg}")
         self.status = status
+
+
+class CopyDesc(ctypes.Structure):
+    _fields_ = [
+        ("ndim", ctypes.c_int32),
+        ("dst_dtype", ctypes.c_int32),
+        ("src_dtype", ctypes.c_int32),
+        ("reserved0", ctypes.c_int32),
+        ("sizes", ctypes.c_int64 * MAX_DIMS),
+        ("dst_strides", ctypes.c_int64 * MAX_DIMS),
+        ("src_strides", ctypes.c_int64 * MAX_DIMS),
+    ]
 
 
 class ReduceDesc(ctypes.Structure):
@@ -72,6 +88,11 @@ def lib():
         L.tpr_topk_workspace_bytes.restype = sz
         L.tpr_topk.argtypes = [vp, i32, i64, i64, i64, i64, i32, i32, vp, vp, vp, sz, vp]
         L.tpr_topk.restype = ctypes.c_int
+        cdp = ctypes.POINTER(CopyDesc)
+        L.tpr_copy.argtypes = [cdp, vp, vp, vp]
+        L.tpr_copy.restype = ctypes.c_int
+        L.tpr_copy_plan.argtypes = [cdp, vp, vp]
+        L.tpr_copy_plan.restype = ctypes.c_int
         L.tpr_copy_strided.argtypes = [vp, i32, i32, i64p, i64p, vp, vp]
         L.tpr_copy_strided.restype = ctypes.c_int
         L.tpr_last_error.argtypes = []
@@ -135,8 +156,12 @@ def default_out_dtype(op, in_dtype=FLOAT32):
 
 def _torch_dtypes():
     import torch
-    return {torch.float32: FLOAT32, torch.float64: FLOAT64, torch.int64: INT64, torch.int32: INT32,
-            torch.int16: INT16, torch.int8: INT8, torch.uint8: UINT8, torch.bool: BOOL}
+    m = {torch.float32: FLOAT32, torch.float64: FLOAT64, torch.int64: INT64, torch.int32: INT32,
+         torch.int16: INT16, torch.int8: INT8, torch.uint8: UINT8, torch.bool: BOOL}
+    for name, code in (("uint16", UINT16), ("uint32", UINT32), ("uint64", UINT64)):
+        if hasattr(torch, name):
+            m[getattr(torch, name)] = code
+    return m
 
 
 def reduce(x, op, dims=None, correction=1, out_dtype=None, count_override=0, p=2.0):
@@ -179,6 +204,37 @@ def topk(x2d, k, largest=True, sorted=True):
                       ctypes.c_void_p(idx.data_ptr()), ctypes.c_void_p(ws.data_ptr()), wsb,
                       _stream(torch, x2d.device)))
     return vals, idx
+
+
+def make_copy_desc(shape, dst_strides, src_strides, dst_dtype, src_dtype):
+    d = CopyDesc()
+    d.ndim = len(shape)
+    if d.ndim > MAX_DIMS:
+        raise ValueError("at most 8 dims")
+    d.dst_dtype, d.src_dtype = dst_dtype, src_dtype
+    for i, n in enumerate(shape):
+        d.sizes[i] = n
+        d.dst_strides[i] = dst_strides[i]
+        d.src_strides[i] = src_strides[i]
+    return d
+
+
+def copy_(dst, src):
+    """dst[...] = src[...] cast to dst's dtype, both torch device tensors of one
+    shape at any strides (src may be an expanded view).  Returns dst."""
+    import torch
+    tmap = _torch_dtypes()
+    assert list(dst.shape) == list(src.shape), "copy_: shapes differ"
+    d = make_copy_desc(list(dst.shape), list(dst.stride()), list(src.stride()), tmap[dst.dtype], tmap[src.dtype])
+    _check(lib().tpr_copy(ctypes.byref(d), ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(src.data_ptr()),
+                          _stream(torch, dst.device)))
+    return dst
+
+
+def copy_plan(dst, src):
+    tmap = _torch_dtypes()
+    d = make_copy_desc(list(dst.shape), list(dst.stride()), list(src.stride()), tmap[dst.dtype], tmap[src.dtype])
+    return lib().tpr_copy_plan(ctypes.byref(d), ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(src.data_ptr()))
 
 
 def copy_strided(x):

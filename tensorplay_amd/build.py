@@ -10,6 +10,7 @@ Usage: python -m tensorplay_amd.build  (or tensorplay_amd.build.build_all()).
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
@@ -34,6 +35,15 @@ def _run(cmd):
     subprocess.run(cmd, check=True)
 
 
+def _run_all(cmds):
+    """Independent compiles in parallel (at most 8 jobs)."""
+    if not cmds:
+        return
+    with ThreadPoolExecutor(max_workers=min(8, len(cmds))) as ex:
+        for f in [ex.submit(_run, c) for c in cmds]:
+            f.result()
+
+
 def _newer(target, deps):
     if not os.path.exists(target):
         return True
@@ -45,20 +55,21 @@ def build_tpr(force=True):
     os.makedirs(BUILD, exist_ok=True)
     inc = ["-I", os.path.join(ROOT, "include"), "-I", os.path.join(CSRC, "rocm")]
     headers = [os.path.join(ROOT, "include", "tpr_rocm.h"), os.path.join(CSRC, "rocm", "common.h")]
-    objs = []
+    objs, cmds = [], []
     for src in ROCM_SOURCES:
         s = os.path.join(CSRC, src)
         o = os.path.join(BUILD, os.path.basename(src) + ".o")
         if force or _newer(o, [s] + headers):
             lang = ["-x", "hip"] if src.endswith(".cpp") else []
-            _run([HIPCC] + HIP_FLAGS + inc + lang + ["-c", s, "-o", o])
+            cmds.append([HIPCC] + HIP_FLAGS + inc + lang + ["-c", s, "-o", o])
         objs.append(o)
+    _run_all(cmds)
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", LIB_TPR] + objs)
     return LIB_TPR
 
 
 CORE_SOURCES = ["core/Dispatcher.cpp", "core/Allocator.cpp", "core/Tensor.cpp",
-                "core/ROCmReductionKernels.cpp", "core/bindings.cpp"]
+                "core/ROCmReductionKernels.cpp", "core/CopyKernels.cpp", "core/bindings.cpp"]
 CXX = os.environ.get("CXX", "g++")
 
 
@@ -74,13 +85,14 @@ def build_core(force=True):
     flags = ["-O2", "-std=c++17", "-fPIC", "-D__HIP_PLATFORM_AMD__", "-fvisibility=hidden", "-Wall"]
     headers = [os.path.join(CSRC, "core", h) for h in os.listdir(os.path.join(CSRC, "core")) if h.endswith(".h")]
     headers.append(os.path.join(ROOT, "include", "tpr_rocm.h"))
-    objs = []
+    objs, cmds = [], []
     for src in CORE_SOURCES:
         s = os.path.join(CSRC, src)
         o = os.path.join(BUILD, os.path.basename(src) + ".o")
         if force or _newer(o, [s] + headers):
-            _run([CXX] + flags + inc + ["-c", s, "-o", o])
+            cmds.append([CXX] + flags + inc + ["-c", s, "-o", o])
         objs.append(o)
+    _run_all(cmds)
     _run([CXX, "-shared", "-o", out] + objs +
          ["-L", PKG, "-ltpr_rocm", "-L", "/opt/rocm/lib", "-lamdhip64",
           "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,/opt/rocm/lib"])

@@ -26,27 +26,6 @@ int64_t wrap_dim(int64_t d, int64_t ndim, bool index_error) {
     return w;
 }
 
-// Host strided gather into a dense buffer (CPU tensors).
-void host_gather(const char* base, size_t esz, const std::vector<int64_t>& sizes,
-                 const std::vector<int64_t>& strides, char* dst) {
-    int64_t n = 1;
-    for (auto s : sizes) n *= s;
-    if (n == 0) return;
-    const int nd = (int)sizes.size();
-    std::vector<int64_t> idx(nd, 0);
-    int64_t off = 0;
-    for (int64_t i = 0; i < n; ++i) {
-        std::memcpy(dst + i * esz, base + off * (int64_t)esz, esz);
-        for (int d = nd - 1; d >= 0; --d) {
-            idx[d]++;
-            off += strides[d];
-            if (idx[d] < sizes[d]) break;
-            off -= strides[d] * sizes[d];
-            idx[d] = 0;
-        }
-    }
-}
-
 }  // namespace
 
 std::vector<int64_t> Tensor::contiguousStrides(const std::vector<int64_t>& shape) {
@@ -182,37 +161,28 @@ Tensor Tensor::reshape(const std::vector<int64_t>& shape) const {
     return c.as_strided(s, contiguousStrides(s), c.impl_->offset);
 }
 
+// Tensor.cpp:473-513 of the reference: clone = empty + copy_, contiguous =
+// clone when not contiguous, to(dtype) = empty of the new dtype + copy_.
 Tensor Tensor::contiguous() const {
     if (is_contiguous()) return *this;
-    Tensor out = empty(impl_->sizes, impl_->dtype, device());
-    if (numel() == 0) return out;
-    if (device().is_cpu()) {
-        host_gather(static_cast<const char*>(data_ptr()), element_size(), impl_->sizes, impl_->strides,
-                    static_cast<char*>(out.data_ptr()));
-        return out;
-    }
-    if (dim() > TPR_MAX_DIMS) TP_THROW(NotImplementedError, "contiguous: more than 8 dims on ROCm");
-    DeviceGuard g(device());
-    const int rc = tpr_copy_strided(data_ptr(), (int32_t)element_size(), (int32_t)dim(), impl_->sizes.data(),
-                                    impl_->strides.data(), out.data_ptr(), currentStream(device().index));
-    if (rc != TPR_OK) TP_THROW(RuntimeError, tpr_last_error());
-    return out;
+    return clone();
 }
 
 Tensor Tensor::clone() const {
-    if (!is_contiguous()) return contiguous();
     Tensor out = empty(impl_->sizes, impl_->dtype, device());
-    const size_t nb = (size_t)numel() * element_size();
-    if (nb == 0) return out;
-    if (device().is_cpu()) {
-        std::memcpy(out.data_ptr(), data_ptr(), nb);
-    } else {
-        DeviceGuard g(device());
-        hip_check(hipMemcpyAsync(out.data_ptr(), data_ptr(), nb, hipMemcpyDeviceToDevice,
-                                 (hipStream_t)currentStream(device().index)),
-                  "hipMemcpyAsync D2D");
-    }
+    out.copy_(*this);
     return out;
+}
+
+Tensor Tensor::to(DType dtype) const {
+    if (dtype == impl_->dtype) return *this;
+    Tensor out = empty(impl_->sizes, dtype, device());
+    out.copy_(*this);
+    return out;
+}
+
+Tensor& Tensor::copy_(const Tensor& src) {
+    return DispatchStub<Tensor&, Tensor&, const Tensor&>::call("copy_", computeDispatchKey(device()), *this, src);
 }
 
 Tensor Tensor::to(const Device& target) const {

@@ -68,6 +68,8 @@ public:
     Tensor contiguous() const;
     Tensor clone() const;
     Tensor to(const Device& device) const;
+    Tensor to(DType dtype) const;                  // cast (copy_ into a new tensor)
+    Tensor& copy_(const Tensor& src);              // copy_ (dispatched on this tensor's device)
     Tensor cpu() const { return to(Device(DeviceType::CPU)); }
     // Copies the (logically ordered) elements into a dense host buffer.
     void copyToHost(void* dst) const;

@@ -139,7 +139,11 @@ PYBIND11_MODULE(_C, m) {
         .def("transpose", &Tensor::transpose)
         .def("permute", [](const Tensor& x, const std::vector<int64_t>& d) { return x.permute(d); })
         .def("reshape", [](const Tensor& x, const std::vector<int64_t>& s) { return x.reshape(s); })
-        .def("to", [](const Tensor& x, const py::object& dev) { return x.to(to_device(dev)); })
+        .def("to", [](const Tensor& x, const py::object& arg) {
+            if (py::isinstance<DType>(arg)) return x.to(arg.cast<DType>());
+            return x.to(to_device(arg));
+        })
+        .def("copy_", [](Tensor& x, const Tensor& src) { return x.copy_(src); }, py::arg("src"))
         .def("cpu", &Tensor::cpu)
         .def("rocm", [](const Tensor& x, int index) { return x.to(Device(DeviceType::ROCm, index)); },
              py::arg("index") = 0)

@@ -404,12 +404,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kBufWord3 = 0x00020000;  // raw buffer resource, 32-bit data (gfx9 family)
 constexpr int kNT = 2;                 // cache policy bit: nontemporal (the row is read once)
 
-// 128-bit load marked nontemporal: the row is read once.
-__device__ __forceinline__ float4 ld4_nt(const float* p) {
-    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
-    return make_float4(v.x, v.y, v.z, v.w);
-}
-
 // Segment loads go through a buffer resource whose range is the segment: the
 // hardware range check is per dword, so a load past the segment end returns 0
 // and moves no data.  Slice loads are therefore unconditional (a prefetch past

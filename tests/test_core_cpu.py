@@ -8,13 +8,14 @@ from tensorplay_amd import _C
 
 SCHEMAS = sorted(["argmax", "argmin", "max", "max.dim", "mean", "mean.dim", "min", "min.dim", "std", "std.dim",
                   "sum", "sum.dim_IntList", "topk", "var", "var.dim", "prod", "prod.dim_IntList", "all", "all.dim",
-                  "any", "any.dim", "median", "norm", "norm.dim"])
+                  "any", "any.dim", "median", "norm", "norm.dim", "copy_"])
 
 
 def test_rocm_key_registers_every_schema():
     # config/native_functions.yaml:695-809 reduction rows (+ topk), registered by name
     assert _C._registered_ops("ROCm") == SCHEMAS
-    assert _C._registered_ops("CPU") == []
+    # the host key carries only the copy_ plumbing of this package's host tensors
+    assert _C._registered_ops("CPU") == ["copy_"]
 
 
 def test_schema_file_matches_registry():
@@ -24,8 +25,9 @@ def test_schema_file_matches_registry():
     rows = yaml.safe_load(open(path))
     names = sorted(r["func"].split("(")[0] for r in rows)
     assert names == SCHEMAS
-    adapters = open(os.path.join(os.path.dirname(tp.__file__), "csrc", "core", "ROCmReductionKernels.cpp")).read()
+    core = os.path.join(os.path.dirname(tp.__file__), "csrc", "core")
     for r in rows:
+        adapters = open(os.path.join(core, r.get("source", "ROCmReductionKernels.cpp"))).read()
         name = r["func"].split("(")[0]
         assert f'("{name}", rocm::{r["adapter"]})' in adapters
         assert f'm.impl<{r["stub"].replace("const std::vector<int64_t>&", "V")}>("{name}"' in adapters

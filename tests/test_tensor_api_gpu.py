@@ -218,3 +218,41 @@ def test_median_vs_oracle():
         assert tt.median().item() == float(O.median(np.ascontiguousarray(x.transpose())))
     e = tp.empty([0, 3], device=DEV).median()
     assert e.shape == [1] and math.isnan(e.item())
+
+
+# ---- copy_ / to(dtype) / contiguous / clone through the dispatcher ("copy_" on the ROCm key) ----
+def test_copy_to_dtype_and_contiguous():
+    rng = np.random.default_rng(40)
+    a = (rng.standard_normal((6, 70, 33)) * 50).astype(np.float32)
+    t = tp.tensor(a, device=DEV)
+    p = t.permute([2, 0, 1])
+    c = p.contiguous()
+    assert c.is_contiguous() and c.shape == [33, 6, 70]
+    np.testing.assert_array_equal(c.numpy(), np.ascontiguousarray(a.transpose(2, 0, 1)))
+    # casts: reference static_cast semantics (truncation toward zero, x != 0 for bool)
+    np.testing.assert_array_equal(t.to(tp.int32).numpy(), a.astype(np.int32))
+    np.testing.assert_array_equal(p.to(tp.float64).numpy(), a.transpose(2, 0, 1).astype(np.float64))
+    np.testing.assert_array_equal(t.to(tp.bool_).numpy(), a != 0)
+    assert t.to(tp.float32) is not None and t.to(tp.float32).data_ptr() == t.data_ptr()  # same dtype: no copy
+    # clone of a view is dense and independent
+    k = p.clone()
+    assert k.is_contiguous() and k.data_ptr() != t.data_ptr()
+    # copy_ into a strided destination view, device and host sources
+    d = tp.tensor(np.zeros((70, 6), np.float64), device=DEV)
+    d.transpose(0, 1).copy_(t.sum([2]))
+    np.testing.assert_allclose(d.numpy(), a.astype(np.float64).sum(2).T, rtol=1e-5)
+    h = tp.tensor(np.arange(12, dtype=np.int64).reshape(3, 4))          # host source -> device
+    r = tp.empty([4, 3], tp.float32, device=DEV)
+    r.copy_(h.transpose(0, 1))
+    np.testing.assert_array_equal(r.numpy(), np.arange(12).reshape(3, 4).T.astype(np.float32))
+    back = tp.empty([3, 4], tp.int16)                                    # device source -> host, with a cast
+    back.copy_(r.transpose(0, 1))
+    np.testing.assert_array_equal(back.numpy(), np.arange(12).reshape(3, 4).astype(np.int16))
+    with pytest.raises(RuntimeError, match="Sizes do not match"):
+        r.copy_(t)
+    # equal numel, different shapes: read in row-major order
+    f = tp.empty([12], tp.float32, device=DEV)
+    f.copy_(r)
+    np.testing.assert_array_equal(f.numpy(), r.numpy().ravel())
+    # reductions of an integer tensor made by a cast on the device
+    np.testing.assert_array_equal(t.to(tp.int64).sum([1]).numpy(), a.astype(np.int64).sum(1))
