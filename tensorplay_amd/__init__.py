@@ -7,7 +7,7 @@ module functions of /root/reference/tensorplay/functional.py:401-432.  Tensors
 live on ``"cpu"`` or ``"rocm[:N]"``; reductions run on ROCm devices only (the
 CPU key has no kernels here -- that path stays TensorPlay's own).
 
-The native library must be built (``python -m tensorplay_amd.build``); there is
+The native library must be built (``python tensorplay_amd/build.py``); there is
 no fallback.
 """
 try:

@@ -5,7 +5,7 @@ to reach the backend from Python; the C++ host core (tensorplay_amd._C) calls
 the same entry points directly.  Device memory and streams come from PyTorch
 (plumbing only): tensors are passed as raw device pointers + element strides.
 
-The library must have been built (python -m tensorplay_amd.build); loading
+The library must have been built (python tensorplay_amd/build.py); loading
 fails loudly otherwise -- there is no CPU fallback.
 """
 import ctypes
@@ -75,7 +75,7 @@ def lib():
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
-            raise ImportError(f"{LIB_PATH} is not built; run `python -m tensorplay_amd.build`")
+            raise ImportError(f"{LIB_PATH} is not built; run `python tensorplay_amd/build.py`")
         L = ctypes.CDLL(LIB_PATH)
         vp, sz, i32, i64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_int64
         dp = ctypes.POINTER(ReduceDesc)

@@ -5,7 +5,7 @@
                    allocator, reduction adapters) + Python bindings; links
                    libtpr_rocm.so
 
-Usage: python -m tensorplay_amd.build  (or tensorplay_amd.build.build_all()).
+Usage: python tensorplay_amd/build.py  (or tensorplay_amd.build.build_all()).
 """
 import os
 import subprocess
