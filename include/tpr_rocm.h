@@ -162,6 +162,69 @@ int tpr_copy_plan(const tpr_copy_desc* desc, const void* dst, const void* src);
 int tpr_copy_strided(const void* in, int32_t elem_size, int32_t ndim, const int64_t* sizes,
                      const int64_t* in_strides, void* out, void* stream);
 
+/* Softmax family along one dim of a logical [outer, n, inner] view (the
+ * softmax dim is n).  Modes:
+ *   TPR_SOFTMAX_FWD      out = exp(x - max) / sum(exp(x - max))
+ *   TPR_LOG_SOFTMAX_FWD  out = (x - max) - log(sum(exp(x - max)))
+ *     replacing softmax_kernel / log_softmax_kernel
+ *     (/root/reference/p10/src/backend/cpu/PointwiseKernels.cpp:519-545) and
+ *     softmax_kernel_cudnn / log_softmax_kernel_cudnn
+ *     (/root/reference/p10/src/backend/cuda/ActivationKernels.cu:136-181);
+ *     max ignores NaN, a NaN in a slice makes the slice NaN, and a slice with
+ *     no value above -inf is NaN, as the reference composite;
+ *   TPR_SOFTMAX_BWD      out = (g - sum(g * y)) * y
+ *   TPR_LOG_SOFTMAX_BWD  out = g - exp(y) * sum(g)
+ *     the autograd formulas of /root/reference/config/derivatives.yaml:91-95,
+ *     with a = g (dL/dy) and b = y (the forward output).
+ * a: x (forward) or g (backward), strides a_strides (elements, per logical
+ * dim); b: y (backward only, strides b_strides; NULL forward).  out is written
+ * dense row-major [outer, n, inner].  Float32 only.  No workspace. */
+enum tpr_softmax_mode {
+    TPR_SOFTMAX_FWD = 0,
+    TPR_LOG_SOFTMAX_FWD = 1,
+    TPR_SOFTMAX_BWD = 2,
+    TPR_LOG_SOFTMAX_BWD = 3
+};
+
+typedef struct tpr_softmax_desc {
+    int32_t mode;  /* enum tpr_softmax_mode */
+    int32_t dtype; /* TPR_FLOAT32 */
+    int64_t outer, n, inner;
+    int64_t a_strides[3];
+    int64_t b_strides[3];
+} tpr_softmax_desc;
+
+int tpr_softmax(const tpr_softmax_desc* desc, const void* a, const void* b, void* out, void* stream);
+
+/* nll_loss forward (/root/reference/p10/src/backend/cpu/LossKernels.cpp:12-55;
+ * CUDA nll_loss_cuda, /root/reference/p10/src/backend/cuda/LossKernels.cu:66-113).
+ * input: float32 [n, c] with strides (s0, s1); target: int64 [n], stride ts;
+ * weight: float32 [c] dense or NULL.  reduction 0 = none (out: float32 [n],
+ * dense), 1 = mean, 2 = sum (out: one float32).  total_weight (one float32)
+ * receives the sum of weight[target] over samples whose target is not
+ * ignore_index, for every reduction.  A target outside [0, c) that is not
+ * ignore_index contributes nothing and sets *status (one device int32) to 1;
+ * otherwise *status is 0 (the reference CPU path raises "Target out of
+ * bounds"; the adapter reads the flag and raises the same).  Loss and weight
+ * sums accumulate in fp64; mean divides by the float32-rounded total weight
+ * when it is > 0, as the reference.  Workspace: tpr_nll_loss_workspace_bytes. */
+size_t tpr_nll_loss_workspace_bytes(int64_t n);
+int tpr_nll_loss(const void* input, int32_t dtype, int64_t n, int64_t c, int64_t s0, int64_t s1,
+                 const int64_t* target, int64_t ts, const void* weight, int64_t reduction,
+                 int64_t ignore_index, void* out, void* total_weight, int32_t* status,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* nll_loss_backward (/root/reference/p10/src/backend/cpu/LossKernels.cpp:57-101;
+ * CUDA /root/reference/p10/src/backend/cuda/LossKernels.cu:115-170): writes the
+ * dense float32 [n, c] grad_input in one pass: 0 everywhere except
+ * grad_input[i, target[i]] = -weight[target[i]] * g_i for samples whose target
+ * is in [0, c) and not ignore_index.  g_i = grad_output[i * gs] (reduction 0)
+ * or grad_output[0]; reduction 1 divides it by *total_weight (device float32)
+ * when that is > 0. */
+int tpr_nll_loss_backward(const void* grad_output, int64_t gs, const int64_t* target, int64_t ts,
+                          const void* weight, const void* total_weight, int64_t n, int64_t c,
+                          int64_t reduction, int64_t ignore_index, void* grad_input, void* stream);
+
 /* Thread-local message for the last non-OK status on this thread. */
 const char* tpr_last_error(void);
 
@@ -176,6 +239,7 @@ int32_t tpr_abi_version(void);
  * "unroll" (1, 2 or 4 vectors in flight per thread in the row/column kernels,
  * 0 = automatic), "colblock" (256, 512 or 1024 threads per column-kernel
  * workgroup, 0 = automatic),
+ * "smx_two_pass" (1 = softmax rows always take the two-pass kernel),
  * "topk_variant" (wave kernel prefetch depth: 1 = none, 2 = one slice, 3 = two
  * slices; 0 = automatic), "topk_waves" (8 or 16 waves per wave-kernel
  * workgroup, 0 = automatic).

@@ -11,6 +11,11 @@ Parity status of each function (see tests/test_oracle.py):
   var_all, var_dim (+std)               pinned: known answers (test_cuda_reductions.py:78-91) + torch.var/std
                                         at the reference's own rtol (test_statistical.py:10-17)
   topk                                  pinned: np.argsort(kind="stable") on canonical keys + torch.topk values
+  softmax, log_softmax                  pinned: known answer (test_pointwise.py:154-172) + torch fp64 softmax /
+                                        log_softmax within fp32 rounding; NaN / inf rows by brute force
+  softmax_bwd (both modes)              pinned: torch.autograd fp64 gradients of softmax / log_softmax
+  nll_loss, nll_loss_backward           pinned: torch.nn.functional.nll_loss (+ autograd) in fp64 with weights,
+                                        ignore_index and every reduction; closed form -x[i, t_i]
   copy                                  pinned: numpy astype on the same views (C casts), brute force on tiny shapes
 """
 import ctypes
@@ -58,6 +63,10 @@ def lib():
         L.or_copy.argtypes = [vp, i32, _i64p, vp, i32, _i64p, i32, _i64p]; L.or_copy.restype = i32
         L.or_topk.argtypes = [vp, i64, i64, i64, i64, i32, vp, vp]
         L.or_topk_mt.argtypes = [vp, i64, i64, i64, i64, i32, vp, vp, i32]
+        L.or_softmax.argtypes = [vp, i64, i64, i64, i32, vp]
+        L.or_softmax_bwd.argtypes = [vp, vp, i64, i64, i64, i32, vp]
+        L.or_nll_loss.argtypes = [vp, i64, i64, vp, vp, i64, i64, vp, vp]; L.or_nll_loss.restype = i32
+        L.or_nll_loss_backward.argtypes = [vp, vp, vp, i64, i64, i32, ctypes.c_float, i64, i64, vp]
         _lib = L
     return _lib
 
@@ -252,3 +261,69 @@ def copy(dst, src):
                    ctypes.c_void_p(src.ctypes.data), DTYPE_CODES[src.dtype], ss, nd, sz)
     assert rc == 0
     return dst
+
+
+def _dim3(x, dim):
+    """Dense float32 copy of x viewed as [outer, n, inner] around `dim`."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    nd = x.ndim
+    d = (dim + max(nd, 1)) % max(nd, 1) if nd else 0
+    shp = x.shape if nd else (1,)
+    outer = int(np.prod(shp[:d])) if d else 1
+    inner = int(np.prod(shp[d + 1:])) if d + 1 < len(shp) else 1
+    return x, outer, (shp[d] if nd else 1), inner
+
+
+def softmax(x, dim, log=False):
+    """softmax / log_softmax along `dim` (PointwiseKernels.cpp:519-545)."""
+    x, outer, n, inner = _dim3(x, dim)
+    y = np.empty_like(x)
+    lib().or_softmax(ctypes.c_void_p(x.ctypes.data), outer, n, inner, int(log), ctypes.c_void_p(y.ctypes.data))
+    return y
+
+
+def log_softmax(x, dim):
+    return softmax(x, dim, log=True)
+
+
+def softmax_backward(grad, y, dim, log=False):
+    """Gradient of softmax (log=False) or log_softmax (log=True) given its output y
+    (config/derivatives.yaml:91-95)."""
+    g, outer, n, inner = _dim3(grad, dim)
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    gx = np.empty_like(g)
+    lib().or_softmax_bwd(ctypes.c_void_p(g.ctypes.data), ctypes.c_void_p(y.ctypes.data), outer, n, inner,
+                         int(log), ctypes.c_void_p(gx.ctypes.data))
+    return gx
+
+
+def nll_loss(x, target, weight=None, reduction=1, ignore_index=-100):
+    """(output, total_weight) of nll_loss_kernel (LossKernels.cpp:12-55); raises
+    RuntimeError("Target out of bounds") as the reference."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    t = np.ascontiguousarray(target, dtype=np.int64)
+    w = None if weight is None else np.ascontiguousarray(weight, dtype=np.float32)
+    N, C = x.shape
+    out = np.zeros(N if reduction == 0 else 1, dtype=np.float32)
+    tw = np.zeros(1, dtype=np.float32)
+    rc = lib().or_nll_loss(ctypes.c_void_p(x.ctypes.data), N, C, ctypes.c_void_p(t.ctypes.data),
+                           None if w is None else ctypes.c_void_p(w.ctypes.data), reduction, ignore_index,
+                           ctypes.c_void_p(out.ctypes.data), ctypes.c_void_p(tw.ctypes.data))
+    if rc:
+        raise RuntimeError("Target out of bounds")
+    return (out if reduction == 0 else out.reshape(())), tw
+
+
+def nll_loss_backward(grad, target, C, weight=None, reduction=1, ignore_index=-100, total_weight=None):
+    """grad_input [N, C] of nll_loss_backward_kernel (LossKernels.cpp:57-101)."""
+    g = np.ascontiguousarray(np.asarray(grad, dtype=np.float32).reshape(-1))
+    t = np.ascontiguousarray(target, dtype=np.int64)
+    w = None if weight is None else np.ascontiguousarray(weight, dtype=np.float32)
+    N = t.shape[0]
+    gi = np.empty((N, C), dtype=np.float32)
+    has_tw = total_weight is not None
+    tw = float(np.asarray(total_weight, dtype=np.float32).reshape(-1)[0]) if has_tw else 0.0
+    lib().or_nll_loss_backward(ctypes.c_void_p(g.ctypes.data), ctypes.c_void_p(t.ctypes.data),
+                               None if w is None else ctypes.c_void_p(w.ctypes.data), reduction, ignore_index,
+                               int(has_tw), tw, N, C, ctypes.c_void_p(gi.ctypes.data))
+    return gi

@@ -79,6 +79,16 @@ void or_topk_mt(const float* x, int64_t rows, int64_t cols, int64_t row_stride, 
 int or_copy(void* dst, int dst_dtype, const int64_t* dst_strides, const void* src, int src_dtype,
             const int64_t* src_strides, int ndim, const int64_t* sizes);
 
+/* Softmax family and nll_loss (tp_cpu_softmax.c): dense [outer, n, inner]
+ * float32; see that file for the reference lines each follows. */
+void or_softmax(const float* x, int64_t outer, int64_t n, int64_t inner, int32_t log_mode, float* y);
+void or_softmax_bwd(const float* g, const float* y, int64_t outer, int64_t n, int64_t inner, int32_t log_mode,
+                    float* gx);
+int32_t or_nll_loss(const float* x, int64_t N, int64_t C, const int64_t* t, const float* w, int64_t reduction,
+                    int64_t ignore_index, float* out, float* total_weight);
+void or_nll_loss_backward(const float* g, const int64_t* t, const float* w, int64_t reduction,
+                          int64_t ignore_index, int32_t has_tw, float tw_in, int64_t N, int64_t C, float* gi);
+
 #ifdef __cplusplus
 }
 #endif

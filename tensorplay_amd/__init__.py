@@ -3,7 +3,9 @@
 The Python surface mirrors the parts of TensorPlay this path touches:
 ``Tensor`` methods sum/mean/max/min/argmax/argmin/var/std (the overload set of
 /root/reference/src/bindings/python/Tensor.cpp:1099-1224) plus ``topk``, and the
-module functions of /root/reference/tensorplay/functional.py:401-432.  Tensors
+module functions of /root/reference/tensorplay/functional.py:401-432, plus
+softmax / log_softmax / nll_loss (functional.py:313-317, 496-500) and their
+gradients.  Tensors
 live on ``"cpu"`` or ``"rocm[:N]"``; reductions run on ROCm devices only (the
 CPU key has no kernels here -- that path stays TensorPlay's own).
 
@@ -131,6 +133,43 @@ def norm(input, p=2.0, dim=None, keepdim=False):
 
 def topk(input, k, dim=-1, largest=True, sorted=True):
     return input.topk(k, dim, largest, sorted)
+
+
+def softmax(input, dim, dtype=None):
+    return input.softmax(dim, dtype)
+
+
+def log_softmax(input, dim, dtype=None):
+    return input.log_softmax(dim, dtype)
+
+
+def nll_loss(input, target, weight=None, reduction=1, ignore_index=-100):
+    """(output, total_weight), as tensorplay/functional.py:496-497."""
+    return _C.nll_loss(input, target, weight, reduction, ignore_index)
+
+
+def nll_loss_backward(grad_output, input, target, weight=None, reduction=1, ignore_index=-100,
+                      total_weight=None):
+    return _C.nll_loss_backward(grad_output, input, target, weight, reduction, ignore_index, total_weight)
+
+
+def _softmax_backward_data(grad_output, output, dim):
+    return _C._softmax_backward_data(grad_output, output, dim)
+
+
+def _log_softmax_backward_data(grad_output, output, dim):
+    return _C._log_softmax_backward_data(grad_output, output, dim)
+
+
+_REDUCTION = {"none": 0, "mean": 1, "sum": 2}
+
+
+def cross_entropy(input, target, weight=None, ignore_index=-100, reduction="mean"):
+    """nll_loss(log_softmax(input, 1), target, ...), the composition of
+    tensorplay/nn/functional.py:442-444 (forward only; its gradient is
+    _log_softmax_backward_data(nll_loss_backward(...), log_probs, 1))."""
+    out, _ = nll_loss(log_softmax(input, 1), target, weight, _REDUCTION[reduction], ignore_index)
+    return out
 
 
 class rocm:

@@ -28,7 +28,10 @@ OP_NAMES = {"sum": SUM, "mean": MEAN, "amax": AMAX, "amin": AMIN, "argmax": ARGM
 
 EXPORTED = ["tpr_reduce_workspace_bytes", "tpr_reduce", "tpr_topk_workspace_bytes", "tpr_topk",
             "tpr_copy", "tpr_copy_plan", "tpr_copy_strided", "tpr_last_error", "tpr_abi_version",
-            "tpr_debug_set"]
+            "tpr_debug_set", "tpr_softmax", "tpr_nll_loss_workspace_bytes", "tpr_nll_loss",
+            "tpr_nll_loss_backward"]
+# enum tpr_softmax_mode
+SOFTMAX_FWD, LOG_SOFTMAX_FWD, SOFTMAX_BWD, LOG_SOFTMAX_BWD = range(4)
 # tpr_copy_plan kinds (bits 0-1) and the vector-variant flag (bit 2)
 COPY_CONTIG, COPY_ROWS, COPY_TILE, COPY_ELEM = range(4)
 COPY_VEC = 4
@@ -68,6 +71,18 @@ class ReduceDesc(ctypes.Structure):
     ]
 
 
+class SoftmaxDesc(ctypes.Structure):
+    _fields_ = [
+        ("mode", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("outer", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+        ("inner", ctypes.c_int64),
+        ("a_strides", ctypes.c_int64 * 3),
+        ("b_strides", ctypes.c_int64 * 3),
+    ]
+
+
 _lib = None
 
 
@@ -101,6 +116,14 @@ def lib():
         L.tpr_abi_version.restype = i32
         L.tpr_debug_set.argtypes = [ctypes.c_char_p, i64]
         L.tpr_debug_set.restype = ctypes.c_int
+        L.tpr_softmax.argtypes = [ctypes.POINTER(SoftmaxDesc), vp, vp, vp, vp]
+        L.tpr_softmax.restype = ctypes.c_int
+        L.tpr_nll_loss_workspace_bytes.argtypes = [i64]
+        L.tpr_nll_loss_workspace_bytes.restype = sz
+        L.tpr_nll_loss.argtypes = [vp, i32, i64, i64, i64, i64, vp, i64, vp, i64, i64, vp, vp, vp, vp, sz, vp]
+        L.tpr_nll_loss.restype = ctypes.c_int
+        L.tpr_nll_loss_backward.argtypes = [vp, i64, vp, i64, vp, vp, i64, i64, i64, i64, vp, vp]
+        L.tpr_nll_loss_backward.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -247,3 +270,98 @@ def copy_strided(x):
     _check(lib().tpr_copy_strided(ctypes.c_void_p(x.data_ptr()), x.element_size(), nd, sizes, strides,
                                   ctypes.c_void_p(out.data_ptr()), _stream(torch, x.device)))
     return out
+
+
+def _view3(x, dim):
+    """(outer, n, inner) extents and element strides of x around `dim`, or None
+    when the outer or inner dims do not collapse to one stride."""
+    nd = x.dim()
+    if nd == 0:
+        return (1, 1, 1), (1, 1, 1)
+    d = dim % nd
+
+    def collapse(lo, hi):
+        size, stride, first = 1, 1, True
+        for i in range(hi - 1, lo - 1, -1):
+            if x.shape[i] == 1:
+                continue
+            if first:
+                stride, first = x.stride(i), False
+            elif x.stride(i) != stride * size:
+                return None
+            size *= x.shape[i]
+        if any(x.shape[i] == 0 for i in range(lo, hi)):
+            size = 0
+        return size, stride
+    o, i = collapse(0, d), collapse(d + 1, nd)
+    if o is None or i is None:
+        return None
+    n = x.shape[d]
+    so = o[1] if o[0] != 1 else n * i[0]
+    si = i[1] if i[0] != 1 else 1
+    return (o[0], n, i[0]), (so, x.stride(d), si)
+
+
+def softmax(x, dim=-1, log=False, grad_of=None):
+    """Softmax / log_softmax of a float32 device tensor along `dim` through
+    tpr_softmax; with grad_of=y, the gradient given g = x and the forward
+    output y.  Returns a dense tensor of x's shape."""
+    import torch
+    a, b = x, grad_of
+    v = _view3(a, dim)
+    if v is None:
+        a = a.contiguous()
+        v = _view3(a, dim)
+    vb = None
+    if b is not None:
+        vb = _view3(b, dim)
+        if vb is None:
+            b = b.contiguous()
+            vb = _view3(b, dim)
+    out = torch.empty(list(x.shape), dtype=torch.float32, device=x.device)
+    d = SoftmaxDesc()
+    d.mode = (LOG_SOFTMAX_BWD if log else SOFTMAX_BWD) if b is not None else (LOG_SOFTMAX_FWD if log else SOFTMAX_FWD)
+    d.dtype = FLOAT32
+    d.outer, d.n, d.inner = v[0]
+    for k in range(3):
+        d.a_strides[k] = v[1][k]
+        d.b_strides[k] = vb[1][k] if vb is not None else 0
+    _check(lib().tpr_softmax(ctypes.byref(d), ctypes.c_void_p(a.data_ptr()),
+                             ctypes.c_void_p(b.data_ptr() if b is not None else 0),
+                             ctypes.c_void_p(out.data_ptr()), _stream(torch, x.device)))
+    return out
+
+
+def nll_loss(x, target, weight=None, reduction=1, ignore_index=-100):
+    """(output, total_weight, status) of tpr_nll_loss on device tensors; status
+    is the device int32 out-of-range flag (not synchronised)."""
+    import torch
+    n, c = x.shape
+    out = torch.empty((n,) if reduction == 0 else (), dtype=torch.float32, device=x.device)
+    tw = torch.empty((1,), dtype=torch.float32, device=x.device)
+    status = torch.empty((1,), dtype=torch.int32, device=x.device)
+    L = lib()
+    wsb = L.tpr_nll_loss_workspace_bytes(n)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
+    _check(L.tpr_nll_loss(ctypes.c_void_p(x.data_ptr()), FLOAT32, n, c, x.stride(0), x.stride(1),
+                          ctypes.c_void_p(target.data_ptr()), target.stride(0),
+                          ctypes.c_void_p(weight.data_ptr() if weight is not None else 0), reduction, ignore_index,
+                          ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(tw.data_ptr()),
+                          ctypes.c_void_p(status.data_ptr()), ctypes.c_void_p(ws.data_ptr()), wsb,
+                          _stream(torch, x.device)))
+    return out, tw, status
+
+
+def nll_loss_backward(grad, target, n, c, weight=None, reduction=1, ignore_index=-100, total_weight=None,
+                      device=None):
+    """Dense [n, c] grad_input of tpr_nll_loss_backward."""
+    import torch
+    gi = torch.empty((n, c), dtype=torch.float32, device=device or grad.device)
+    g = grad.reshape(-1)
+    _check(lib().tpr_nll_loss_backward(ctypes.c_void_p(g.data_ptr()), g.stride(0) if g.numel() else 1,
+                                       ctypes.c_void_p(target.data_ptr()), target.stride(0),
+                                       ctypes.c_void_p(weight.data_ptr() if weight is not None else 0),
+                                       ctypes.c_void_p(total_weight.data_ptr() if total_weight is not None else 0),
+                                       n, c, reduction, ignore_index, ctypes.c_void_p(gi.data_ptr()),
+                                       _stream(torch, gi.device)))
+    return gi

@@ -26,7 +26,8 @@ HIP_FLAGS = [
     "-Wall", "-Wno-unused-result",
 ]
 
-ROCM_SOURCES = ["rocm/capi.cpp", "rocm/reduce.hip", "rocm/topk.hip", "rocm/copy.hip"]
+ROCM_SOURCES = ["rocm/capi.cpp", "rocm/reduce.hip", "rocm/topk.hip", "rocm/copy.hip",
+                "rocm/softmax.hip", "rocm/loss.hip"]
 LIB_TPR = os.path.join(PKG, "libtpr_rocm.so")
 
 
@@ -69,7 +70,8 @@ def build_tpr(force=True):
 
 
 CORE_SOURCES = ["core/Dispatcher.cpp", "core/Allocator.cpp", "core/Tensor.cpp",
-                "core/ROCmReductionKernels.cpp", "core/CopyKernels.cpp", "core/bindings.cpp"]
+                "core/ROCmReductionKernels.cpp", "core/CopyKernels.cpp", "core/ROCmSoftmaxLossKernels.cpp",
+                "core/bindings.cpp"]
 CXX = os.environ.get("CXX", "g++")
 
 

@@ -332,6 +332,36 @@ std::tuple<Tensor, Tensor> Tensor::topk(int64_t k, int64_t dim, bool largest, bo
     return DispatchStub<std::tuple<Tensor, Tensor>, const Tensor&, int64_t, int64_t, bool, bool>::call(
         "topk", TP_KEY, *this, k, dim, largest, sorted);
 }
+Tensor Tensor::softmax(int64_t dim, DType dtype) const {
+    return DispatchStub<Tensor, const Tensor&, int64_t, DType>::call("softmax", TP_KEY, *this, dim, dtype);
+}
+Tensor Tensor::log_softmax(int64_t dim, DType dtype) const {
+    return DispatchStub<Tensor, const Tensor&, int64_t, DType>::call("log_softmax", TP_KEY, *this, dim, dtype);
+}
 #undef TP_KEY
+
+std::tuple<Tensor, Tensor> nll_loss(const Tensor& self, const Tensor& target, const std::optional<Tensor>& weight,
+                                    int64_t reduction, int64_t ignore_index) {
+    return DispatchStub<std::tuple<Tensor, Tensor>, const Tensor&, const Tensor&, std::optional<Tensor>, int64_t,
+                        int64_t>::call("nll_loss", computeDispatchKey(self.device()), self, target, weight, reduction,
+                                       ignore_index);
+}
+Tensor nll_loss_backward(const Tensor& grad_output, const Tensor& self, const Tensor& target,
+                         const std::optional<Tensor>& weight, int64_t reduction, int64_t ignore_index,
+                         const Tensor& total_weight) {
+    return DispatchStub<Tensor, const Tensor&, const Tensor&, const Tensor&, std::optional<Tensor>, int64_t, int64_t,
+                        const Tensor&>::call("nll_loss_backward", computeDispatchKey(grad_output.device()),
+                                             grad_output, self, target, weight, reduction, ignore_index,
+                                             total_weight);
+}
+Tensor _softmax_backward_data(const Tensor& grad_output, const Tensor& output, int64_t dim, DType input_dtype) {
+    return DispatchStub<Tensor, const Tensor&, const Tensor&, int64_t, DType>::call(
+        "_softmax_backward_data", computeDispatchKey(grad_output.device()), grad_output, output, dim, input_dtype);
+}
+Tensor _log_softmax_backward_data(const Tensor& grad_output, const Tensor& output, int64_t dim, DType input_dtype) {
+    return DispatchStub<Tensor, const Tensor&, const Tensor&, int64_t, DType>::call(
+        "_log_softmax_backward_data", computeDispatchKey(grad_output.device()), grad_output, output, dim,
+        input_dtype);
+}
 
 }  // namespace tensorplay

@@ -100,12 +100,28 @@ public:
     Tensor median() const;                                                                         // median
     Tensor norm(double p = 2.0) const;                                                             // norm
     Tensor norm(const std::vector<int64_t>& dim, double p = 2.0, bool keepdim = false) const;      // norm.dim
+    Tensor softmax(int64_t dim, DType dtype = DType::Undefined) const;                            // softmax
+    Tensor log_softmax(int64_t dim, DType dtype = DType::Undefined) const;                        // log_softmax
     // topk (schema added by this backend; TensorPlay has none)
     std::tuple<Tensor, Tensor> topk(int64_t k, int64_t dim = -1, bool largest = true, bool sorted = true) const;
 
 private:
     std::shared_ptr<TensorImpl> impl_;
 };
+
+// Function-only schemas (config/native_functions.yaml:904-914), dispatched on
+// the device of the first tensor argument.
+std::tuple<Tensor, Tensor> nll_loss(const Tensor& self, const Tensor& target, const std::optional<Tensor>& weight,
+                                    int64_t reduction = 1, int64_t ignore_index = -100);
+Tensor nll_loss_backward(const Tensor& grad_output, const Tensor& self, const Tensor& target,
+                         const std::optional<Tensor>& weight, int64_t reduction, int64_t ignore_index,
+                         const Tensor& total_weight);
+// Softmax gradients as single ops (added by this backend; TensorPlay's autograd
+// composes config/derivatives.yaml:91-95 from sum / mul / sub / exp).
+Tensor _softmax_backward_data(const Tensor& grad_output, const Tensor& output, int64_t dim,
+                              DType input_dtype = DType::Float32);
+Tensor _log_softmax_backward_data(const Tensor& grad_output, const Tensor& output, int64_t dim,
+                                  DType input_dtype = DType::Float32);
 
 // Output shape of a reduction over `dims` (ReductionKernels.cpp:48-70 semantics:
 // negative dims wrap, out-of-range dims raise RuntimeError).

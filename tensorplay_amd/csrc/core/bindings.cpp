@@ -226,7 +226,34 @@ PYBIND11_MODULE(_C, m) {
              py::arg("p") = 2.0, py::arg("keepdim") = false)
         .def("topk", [](const Tensor& s, int64_t k, int64_t d, bool largest, bool sorted) {
             return s.topk(k, d, largest, sorted);
-        }, py::arg("k"), py::arg("dim") = -1, py::arg("largest") = true, py::arg("sorted") = true);
+        }, py::arg("k"), py::arg("dim") = -1, py::arg("largest") = true, py::arg("sorted") = true)
+        .def("softmax", [](const Tensor& s, int64_t d, std::optional<DType> dt) { return s.softmax(d, opt_dtype(dt)); },
+             py::arg("dim"), py::arg("dtype") = py::none())
+        .def("log_softmax", [](const Tensor& s, int64_t d, std::optional<DType> dt) {
+            return s.log_softmax(d, opt_dtype(dt));
+        }, py::arg("dim"), py::arg("dtype") = py::none());
+
+    // ---- function-only schemas (tensorplay/functional.py:313-317, 496-500) ----
+    m.def("softmax", [](const Tensor& s, int64_t d, std::optional<DType> dt) { return s.softmax(d, opt_dtype(dt)); },
+          py::arg("self"), py::arg("dim"), py::arg("dtype") = py::none());
+    m.def("log_softmax", [](const Tensor& s, int64_t d, std::optional<DType> dt) {
+        return s.log_softmax(d, opt_dtype(dt));
+    }, py::arg("self"), py::arg("dim"), py::arg("dtype") = py::none());
+    m.def("nll_loss", [](const Tensor& s, const Tensor& t, std::optional<Tensor> w, int64_t r, int64_t ig) {
+        return nll_loss(s, t, w, r, ig);
+    }, py::arg("self"), py::arg("target"), py::arg("weight") = py::none(), py::arg("reduction") = 1,
+       py::arg("ignore_index") = -100);
+    m.def("nll_loss_backward", [](const Tensor& g, const Tensor& s, const Tensor& t, std::optional<Tensor> w,
+                                  int64_t r, int64_t ig, std::optional<Tensor> tw) {
+        return nll_loss_backward(g, s, t, w, r, ig, tw.value_or(Tensor()));
+    }, py::arg("grad_output"), py::arg("self"), py::arg("target"), py::arg("weight") = py::none(),
+       py::arg("reduction") = 1, py::arg("ignore_index") = -100, py::arg("total_weight") = py::none());
+    m.def("_softmax_backward_data", [](const Tensor& g, const Tensor& y, int64_t d) {
+        return _softmax_backward_data(g, y, d, DType::Float32);
+    }, py::arg("grad_output"), py::arg("output"), py::arg("dim"));
+    m.def("_log_softmax_backward_data", [](const Tensor& g, const Tensor& y, int64_t d) {
+        return _log_softmax_backward_data(g, y, d, DType::Float32);
+    }, py::arg("grad_output"), py::arg("output"), py::arg("dim"));
 
     // ---- factories ----
     m.def("tensor", &from_numpy, py::arg("data"), py::arg("dtype") = py::none(), py::arg("device") = "cpu");

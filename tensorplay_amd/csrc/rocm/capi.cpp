@@ -56,7 +56,7 @@ extern "C" {
 
 const char* tpr_last_error(void) { return tpr::g_last_error.c_str(); }
 
-int32_t tpr_abi_version(void) { return (1 << 16) | 2; }
+int32_t tpr_abi_version(void) { return (1 << 16) | 3; }
 
 int tpr_debug_set(const char* key, int64_t value) {
     if (!key) return tpr::fail(TPR_ERR_INVALID_ARG, "tpr_debug_set: null key");
@@ -71,6 +71,7 @@ int tpr_debug_set(const char* key, int64_t value) {
     else if (!std::strcmp(key, "unroll")) k.unroll = value;
     else if (!std::strcmp(key, "colblock")) k.colblock = value;
     else if (!std::strcmp(key, "nt")) k.nt = value;
+    else if (!std::strcmp(key, "smx_two_pass")) k.smx_two_pass = value;
     else return tpr::fail(TPR_ERR_INVALID_ARG, std::string("tpr_debug_set: unknown key ") + key);
     return TPR_OK;
 }

@@ -34,6 +34,7 @@ struct DebugKnobs {
     int64_t unroll = 0;
     int64_t colblock = 0;
     int64_t nt = 0;
+    int64_t smx_two_pass = 0;
 };
 DebugKnobs& knobs();
 

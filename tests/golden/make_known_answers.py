@@ -52,8 +52,24 @@ CASES = [
     dict(src="test/test_reduction.py:56", op="mean", x=[1.0, 2.0, 3.0, 4.0], shape=[2, 2], dims=None, expect=2.5),
 ]
 
+_E = [math.exp(1.0), math.exp(2.0), math.exp(3.0)]
+_T = sum(_E)
+
+# Softmax-family known answers (test/test_pointwise.py:154-174): softmax of
+# [[1, 2, 3], [1, 2, 3]] along dim 1 is e^i / (e + e^2 + e^3) per row (places=5),
+# and every row sums to 1 (places=5).
+SOFTMAX_CASES = [
+    dict(src="test/test_pointwise.py:155-174", op="softmax", x=[1.0, 2.0, 3.0, 1.0, 2.0, 3.0], shape=[2, 3],
+         dim=1, expect=[e / _T for e in _E] * 2, expect_shape=[2, 3], places=5),
+    dict(src="test/test_pointwise.py:159-162", op="softmax_rowsum", x=[1.0, 2.0, 3.0, 1.0, 2.0, 3.0], shape=[2, 3],
+         dim=1, expect=[1.0, 1.0], expect_shape=[2], places=5),
+]
+
 if __name__ == "__main__":
-    out = os.path.join(os.path.dirname(os.path.abspath(__file__)), "reference_known_answers.json")
-    with open(out, "w") as f:
-        json.dump(CASES, f, indent=1)
-    print("wrote", out, len(CASES), "cases")
+    here = os.path.dirname(os.path.abspath(__file__))
+    for name, cases in (("reference_known_answers.json", CASES),
+                        ("reference_known_answers_softmax.json", SOFTMAX_CASES)):
+        out = os.path.join(here, name)
+        with open(out, "w") as f:
+            json.dump(cases, f, indent=1)
+        print("wrote", out, len(cases), "cases")

@@ -63,3 +63,44 @@ def assert_bits_equal(got, expect):
         np.testing.assert_array_equal(got.view(np.uint32), expect.astype(np.float32).view(np.uint32))
     else:
         np.testing.assert_array_equal(got, expect)
+
+
+def softmax_reference(x64, dim, log):
+    """fp64 softmax / log_softmax of x64 along dim with the reference's NaN
+    rules (max ignores NaN; a NaN, or no value above -inf, makes the slice NaN)."""
+    x = np.moveaxis(np.asarray(x64, np.float64), dim, -1)
+    with np.errstate(invalid="ignore", over="ignore"):
+        m = np.max(np.where(np.isnan(x), -np.inf, x), axis=-1, keepdims=True)
+        d = x - m
+        e = np.exp(d)
+        s = e.sum(-1, keepdims=True)
+        lse = np.log(s)
+        y = d - lse if log else e / s
+    y = np.where(np.isnan(s) | (m == -np.inf), np.nan, y)
+    return np.moveaxis(y, -1, dim), np.moveaxis(np.broadcast_to(lse, x.shape), -1, dim)
+
+
+def softmax_error(got, x64, dim, log):
+    """Max error of an fp32 softmax / log_softmax in units of its tolerance:
+    softmax 1e-5 relative; log_softmax 1e-5 * (|y| + |log-sum-exp|) absolute
+    (the terms it subtracts).  NaN / +-inf positions must match exactly.
+    Returns the worst ratio (<= 1 passes)."""
+    ref, lse = softmax_reference(x64, dim, log)
+    got = np.asarray(got, np.float64)
+    assert got.shape == ref.shape
+    nan_r = np.isnan(ref)
+    np.testing.assert_array_equal(np.isnan(got), nan_r)
+    inf_r = np.isinf(ref)
+    np.testing.assert_array_equal(got[inf_r], ref[inf_r])
+    ok = ~nan_r & ~inf_r
+    if not ok.any():
+        return 0.0
+    if log:
+        tol = 1e-5 * (np.abs(ref) + np.abs(lse))
+    else:
+        tol = 1e-5 * np.abs(ref)
+    with np.errstate(invalid="ignore"):
+        err = np.abs(got - ref)
+    ratio = np.where(ok, err / np.maximum(tol, 1e-38), 0.0)
+    ratio = np.where(ok & (err == 0), 0.0, ratio)
+    return float(ratio.max())

@@ -71,3 +71,27 @@ def test_empty_output_is_a_no_op_without_gpu():
     d = _capi.make_desc("sum", [0, 4], [4, 1], [1], _capi.FLOAT32)
     assert L.tpr_reduce(ctypes.byref(d), None, None, None, 0, None) == _capi.OK
     assert L.tpr_topk(None, _capi.FLOAT32, 3, 5, 5, 0, 1, 1, None, None, None, 0, None) == _capi.OK
+
+
+def test_softmax_loss_validation_without_gpu():
+    L = _capi.lib()
+    assert ctypes.sizeof(_capi.SoftmaxDesc) == 8 + 24 + 48
+    d = _capi.SoftmaxDesc()
+    d.mode, d.dtype, d.outer, d.n, d.inner = 0, _capi.FLOAT64, 2, 3, 1
+    assert L.tpr_softmax(ctypes.byref(d), None, None, None, None) == _capi.ERR_UNSUPPORTED_DTYPE
+    d.dtype, d.mode = _capi.FLOAT32, 7
+    assert L.tpr_softmax(ctypes.byref(d), None, None, None, None) == _capi.ERR_INVALID_ARG
+    d.mode, d.n = _capi.SOFTMAX_FWD, 0
+    assert L.tpr_softmax(ctypes.byref(d), None, None, None, None) == _capi.OK  # empty: no launch
+    d.n, d.mode = 3, _capi.SOFTMAX_BWD
+    assert L.tpr_softmax(ctypes.byref(d), 16, None, 16, None) == _capi.ERR_INVALID_ARG  # y missing
+    assert L.tpr_nll_loss_workspace_bytes(1) > 0
+    args = [None, _capi.FLOAT32, 4, 3, 3, 1, None, 1, None, 3, -100, None, None, None, None, 0, None]
+    assert L.tpr_nll_loss(*args) == _capi.ERR_INVALID_ARG and b"reduction" in L.tpr_last_error()
+    args[1] = _capi.FLOAT64
+    assert L.tpr_nll_loss(*args) == _capi.ERR_UNSUPPORTED_DTYPE
+    args[1], args[9] = _capi.FLOAT32, 1
+    args[11], args[12], args[6], args[0] = 16, 16, 16, 16
+    assert L.tpr_nll_loss(*args) == _capi.ERR_WORKSPACE
+    assert L.tpr_nll_loss_backward(None, 1, None, 1, None, None, 0, 5, 1, -100, None, None) == _capi.OK
+    assert L.tpr_nll_loss_backward(None, 1, None, 1, None, None, 2, 5, 4, -100, None, None) == _capi.ERR_INVALID_ARG

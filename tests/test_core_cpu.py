@@ -8,7 +8,8 @@ from tensorplay_amd import _C
 
 SCHEMAS = sorted(["argmax", "argmin", "max", "max.dim", "mean", "mean.dim", "min", "min.dim", "std", "std.dim",
                   "sum", "sum.dim_IntList", "topk", "var", "var.dim", "prod", "prod.dim_IntList", "all", "all.dim",
-                  "any", "any.dim", "median", "norm", "norm.dim", "copy_"])
+                  "any", "any.dim", "median", "norm", "norm.dim", "copy_", "softmax", "log_softmax",
+                  "_softmax_backward_data", "_log_softmax_backward_data", "nll_loss", "nll_loss_backward"])
 
 
 def test_rocm_key_registers_every_schema():
@@ -41,6 +42,10 @@ def test_missing_kernel_is_not_implemented_error():
         t.sum(0)
     with pytest.raises(NotImplementedError, match="topk"):
         t.topk(1)
+    with pytest.raises(NotImplementedError, match="softmax"):
+        t.softmax(1)
+    with pytest.raises(NotImplementedError, match="nll_loss"):
+        tp.nll_loss(t, tp.tensor(np.array([0, 1], np.int64)))
 
 
 def test_reduction_shape_rules():

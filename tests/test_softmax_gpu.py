@@ -1,0 +1,256 @@
+"""GPU parity of tpr_softmax (softmax / log_softmax forward and backward) and
+tpr_nll_loss / tpr_nll_loss_backward through the C-ABI.
+
+Tolerances (stated here, asserted below):
+  * softmax: |y - y64| <= 1e-5 |y64| per element against fp64; log_softmax:
+    <= 1e-5 (|y64| + |log-sum-exp|); NaN / inf positions exact.  The CPU path's
+    own error (the oracle restatement of the reference composite) is printed
+    beside it.
+  * softmax gradients: <= 1e-5 of the magnitudes the formula combines
+    ((|g| + sum|g*y|) * y, resp. |g| + exp(y) * sum|g|) against fp64 autograd.
+  * nll_loss: per-sample losses and unit-weight totals bit-exact against the
+    oracle; weighted totals, mean and sum within 1e-6 relative; the backward
+    gradient bit-exact given the same total weight.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tensorplay_amd import _capi
+from tests.gpu_util import assert_bits_equal, device_view, softmax_error
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(autouse=True)
+def _reset_knobs():
+    yield
+    for k in ("smx_two_pass", "general", "nt"):
+        _capi.debug_set(k, 0)
+
+
+def check_fwd(base, v, dim, log):
+    print(f"case softmax shape={v.shape} strides={v.strides} dim={dim} log={log}", flush=True)
+    t = device_view(torch, base, v)
+    got = _capi.softmax(t, dim, log=log)
+    torch.cuda.synchronize()
+    r = softmax_error(got.cpu().numpy(), v.astype(np.float64), dim, log)
+    assert r <= 1.0, f"error {r:.2f}x the tolerance"
+    return r
+
+
+ROW_NS = [1, 3, 17, 64, 100, 256, 1000, 1001, 1024, 4096, 5000, 16383, 16384, 32768, 32772, 40000, 70001]
+
+
+@pytest.mark.parametrize("log", [False, True])
+@pytest.mark.parametrize("two_pass", [0, 1])
+def test_rows_every_variant(log, two_pass):
+    _capi.debug_set("smx_two_pass", two_pass)
+    rng = np.random.default_rng(11)
+    for n in ROW_NS:
+        rows = 5 if n > 4096 else 37
+        x = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+        check_fwd(x, x, 1, log)
+
+
+@pytest.mark.parametrize("log", [False, True])
+def test_rows_misaligned_and_strided(log):
+    rng = np.random.default_rng(12)
+    b = rng.standard_normal((40, 1030)).astype(np.float32)
+    check_fwd(b, b[1:, 1:], 1, log)      # rows not 16-byte aligned -> scalar loads
+    check_fwd(b, b[:, 2:1026], 1, log)   # aligned start, row stride 1030 (not a multiple of 4)
+    check_fwd(b, b[::3, :1024], 1, log)  # stepped rows
+    check_fwd(b, b[:, ::2], 1, log)      # stepped softmax dim -> strided kernel
+    check_fwd(b, b.T, 1, log)            # transposed: the dim is the outer stride-1 one
+    check_fwd(b, b, 0, log)              # dim 0 of a row-major matrix
+
+
+@pytest.mark.parametrize("log", [False, True])
+def test_strided_dims(log):
+    rng = np.random.default_rng(13)
+    for shape, dim in [((4, 300, 33), 1), ((8, 512, 96), 1), ((300, 70), 0), ((2, 3, 4, 5), 2), ((7, 1, 9), 1),
+                       ((3, 5, 2), 0), ((1, 2000, 64), 1)]:
+        x = (rng.standard_normal(shape) * 2).astype(np.float32)
+        check_fwd(x, x, dim, log)
+    _capi.debug_set("general", 1)        # the strided kernel on a contiguous last dim too
+    x = rng.standard_normal((9, 700)).astype(np.float32)
+    check_fwd(x, x, 1, log)
+
+
+@pytest.mark.parametrize("log", [False, True])
+@pytest.mark.parametrize("two_pass", [0, 1])
+def test_nan_inf_slices(log, two_pass):
+    _capi.debug_set("smx_two_pass", two_pass)
+    inf, nan = np.inf, np.nan
+    rng = np.random.default_rng(14)
+    for n in (8, 1000, 3001):
+        x = rng.standard_normal((7, n)).astype(np.float32)
+        x[0, n // 2] = nan
+        x[1, :] = -inf
+        x[2, :] = -inf
+        x[2, 1::2] = nan
+        x[3, n - 1] = inf
+        x[4, : n // 2] = -inf        # leading -inf then finite values
+        x[5, :] = 0.0
+        x[6, 0] = 80.0               # one dominant value
+        check_fwd(x, x, 1, log)
+        check_fwd(x, x.T, 0, log)    # the same slices through the strided kernel
+
+
+def test_large_logits_c5_shape():
+    # BASELINE configs[4]-shaped logits: [256, 151936] ~ N(0, 3) + 8 boosted positions per row
+    rng = np.random.default_rng(15)
+    x = (rng.standard_normal((256, 151936)) * 3).astype(np.float32)
+    for r in range(256):
+        x[r, rng.choice(151936, 8, replace=False)] += 15.0
+    t = torch.from_numpy(x).cuda()
+    for log in (False, True):
+        got = _capi.softmax(t, -1, log=log).cpu().numpy()
+        r = softmax_error(got[:32], x[:32].astype(np.float64), 1, log)
+        assert r <= 1.0
+        # size-independent property on every row: softmax rows sum to 1
+        if not log:
+            s = got.astype(np.float64).sum(1)
+            assert np.all(np.abs(s - 1.0) <= 1e-4)
+
+
+def test_cpu_path_error_is_reported():
+    # The reference composite's own error on the same input (fp32 sequential sum)
+    rng = np.random.default_rng(16)
+    x = (rng.standard_normal((64, 4096)) * 3).astype(np.float32)
+    t = torch.from_numpy(x).cuda()
+    for log in (False, True):
+        g = softmax_error(_capi.softmax(t, 1, log=log).cpu().numpy(), x.astype(np.float64), 1, log)
+        c = softmax_error(O.softmax(x, 1, log=log), x.astype(np.float64), 1, log)
+        print(f"softmax log={log}: GPU error {g:.3f}x tolerance, CPU path {c:.3f}x")
+        assert g <= 1.0
+
+
+def test_empty_and_scalar():
+    for shape, dim in [((0, 5), 1), ((5, 0), 1), ((3, 0, 4), 0)]:
+        t = torch.empty(shape, dtype=torch.float32, device="cuda")
+        assert tuple(_capi.softmax(t, dim).shape) == shape
+    t = torch.tensor(2.5, device="cuda")
+    assert float(_capi.softmax(t, 0).cpu()) == 1.0
+    assert float(_capi.softmax(t, 0, log=True).cpu()) == 0.0
+
+
+# ---- backward -------------------------------------------------------------------------------
+def check_bwd(shape, dim, log, seed, view=None):
+    rng = np.random.default_rng(seed)
+    x64 = rng.standard_normal(shape) * 2
+    g64 = rng.standard_normal(shape)
+    tx = torch.from_numpy(x64).requires_grad_(True)
+    ty = torch.log_softmax(tx, dim) if log else torch.softmax(tx, dim)
+    ty.backward(torch.from_numpy(g64))
+    ref = tx.grad.numpy()
+    y = ty.detach().numpy().astype(np.float32)
+    g = g64.astype(np.float32)
+    print(f"case softmax_bwd shape={shape} dim={dim} log={log}", flush=True)
+    tg, tyy = torch.from_numpy(g).cuda(), torch.from_numpy(y).cuda()
+    if view == "T":
+        tg, tyy = tg.t().contiguous().t(), tyy.t().contiguous().t()  # same values, column-major storage
+    got = _capi.softmax(tg, dim, log=log, grad_of=tyy).cpu().numpy().astype(np.float64)
+    y64, gg = y.astype(np.float64), g.astype(np.float64)
+    if log:
+        tol = 1e-5 * (np.abs(gg) + np.exp(y64) * np.abs(gg).sum(dim, keepdims=True))
+    else:
+        tol = 1e-5 * (np.abs(gg) + np.abs(gg * y64).sum(dim, keepdims=True)) * np.abs(y64) + 1e-30
+    assert np.all(np.abs(got - ref) <= tol)
+    # against the oracle's restatement of the autograd composite, same tolerance
+    assert np.all(np.abs(got - O.softmax_backward(g, y, dim, log=log)) <= 2 * tol)
+
+
+@pytest.mark.parametrize("log", [False, True])
+@pytest.mark.parametrize("two_pass", [0, 1])
+def test_backward_rows(log, two_pass):
+    _capi.debug_set("smx_two_pass", two_pass)
+    for i, n in enumerate([3, 64, 1000, 1001, 4096, 16384, 20000]):
+        check_bwd((6, n), 1, log, 100 + i)
+
+
+@pytest.mark.parametrize("log", [False, True])
+def test_backward_strided(log):
+    check_bwd((4, 300, 33), 1, log, 200)
+    check_bwd((300, 70), 0, log, 201)
+    check_bwd((50, 80), 1, log, 202, view="T")
+
+
+# ---- nll_loss ------------------------------------------------------------------------------
+def nll_case(N, C, reduction, weighted, seed, x_step=1, t_step=1, ignore=-100):
+    rng = np.random.default_rng(seed)
+    xb = rng.standard_normal((N, C * x_step)).astype(np.float32)
+    x = xb[:, ::x_step]
+    tb = rng.integers(0, C, N * t_step).astype(np.int64)
+    if N > 4:
+        tb[::7] = ignore
+    t = tb[::t_step]
+    w = rng.uniform(0.1, 2.0, C).astype(np.float32) if weighted else None
+    print(f"case nll N={N} C={C} reduction={reduction} weighted={weighted} steps={x_step},{t_step}", flush=True)
+    tx = device_view(torch, xb, x)
+    tt = torch.from_numpy(tb).cuda()[::t_step]
+    tw_ = None if w is None else torch.from_numpy(w).cuda()
+    out, tw, status = _capi.nll_loss(tx, tt, tw_, reduction, ignore)
+    torch.cuda.synchronize()
+    assert int(status.cpu()) == 0
+    eo, etw = O.nll_loss(np.ascontiguousarray(x), t, w, reduction, ignore)
+    got_tw = tw.cpu().numpy()
+    keep = (t != ignore)
+    wt = np.ones(C, np.float32) if w is None else w
+    losses = np.zeros(N, np.float32)
+    losses[keep] = -x[keep, t[keep]] * wt[t[keep]]     # float32, as the reference
+    tw64 = wt[t[keep]].astype(np.float64).sum()
+    if weighted:
+        # fp64 accumulation of the weights; the reference's fp32 running sum is printed beside it
+        assert abs(float(got_tw[0]) - tw64) <= 1e-6 * tw64
+        print(f"  total_weight rel. error: GPU {abs(float(got_tw[0]) - tw64) / tw64:.2e}, "
+              f"CPU path {abs(float(etw[0]) - tw64) / tw64:.2e}")
+    else:
+        assert_bits_equal(got_tw, etw)
+    if reduction == 0:
+        assert_bits_equal(out.cpu().numpy(), eo)
+    else:
+        ref = losses.astype(np.float64).sum()
+        if reduction == 1 and tw64 > 0:
+            ref /= tw64
+        assert abs(float(out.cpu()) - ref) <= 1e-6 * abs(ref)
+        if not weighted:
+            assert abs(float(out.cpu()) - float(eo)) <= 1e-6 * abs(float(eo))
+    # backward: same total weight on both sides -> bit-exact
+    g = rng.standard_normal(N if reduction == 0 else ()).astype(np.float32)
+    gi = _capi.nll_loss_backward(torch.from_numpy(g).cuda(), tt, N, C, tw_, reduction, ignore, tw)
+    egi = O.nll_loss_backward(g, t, C, w, reduction, ignore, got_tw)
+    assert_bits_equal(gi.cpu().numpy(), egi)
+
+
+@pytest.mark.parametrize("reduction", [0, 1, 2])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_nll_loss_shapes(reduction, weighted):
+    for i, (N, C) in enumerate([(1, 1), (37, 10), (5000, 3), (300000, 5), (64, 1000), (16, 1024), (8, 4097),
+                                (4, 151936)]):
+        nll_case(N, C, reduction, weighted, 300 + i)
+
+
+def test_nll_loss_strided_and_ignore_index():
+    nll_case(100, 33, 1, True, 400, x_step=3, t_step=2)
+    nll_case(100, 2048, 0, False, 401, x_step=2)
+    nll_case(50, 9, 2, False, 402, ignore=4)      # ignore_index inside [0, C)
+
+
+def test_nll_loss_status_flag():
+    x = torch.zeros((3, 4), device="cuda")
+    for bad in (4, -1):
+        t = torch.tensor([0, bad, 2], dtype=torch.int64, device="cuda")
+        _, _, status = _capi.nll_loss(x, t, None, 1, -100)
+        assert int(status.cpu()) == 1
+    t = torch.tensor([0, -100, 2], dtype=torch.int64, device="cuda")
+    _, tw, status = _capi.nll_loss(x, t, None, 1, -100)
+    assert int(status.cpu()) == 0 and float(tw.cpu()) == 2.0
+
+
+def test_nll_loss_empty_batch():
+    x = torch.zeros((0, 4), device="cuda")
+    t = torch.zeros((0,), dtype=torch.int64, device="cuda")
+    out, tw, status = _capi.nll_loss(x, t, None, 1, -100)
+    assert float(out.cpu()) == 0.0 and float(tw.cpu()) == 0.0 and int(status.cpu()) == 0

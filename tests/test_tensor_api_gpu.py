@@ -256,3 +256,91 @@ def test_copy_to_dtype_and_contiguous():
     np.testing.assert_array_equal(f.numpy(), r.numpy().ravel())
     # reductions of an integer tensor made by a cast on the device
     np.testing.assert_array_equal(t.to(tp.int64).sum([1]).numpy(), a.astype(np.int64).sum(1))
+
+
+# ---- softmax family and nll_loss through the dispatcher ---------------------------------------
+def test_softmax_known_answer():
+    # test/test_pointwise.py:154-174
+    x = tp.tensor(np.array([[1.0, 2.0, 3.0], [1.0, 2.0, 3.0]], np.float32), device=DEV)
+    y = x.softmax(dim=1)
+    assert y.shape == [2, 3]
+    for v in y.sum(dim=[1]).numpy().tolist():
+        assert round(v - 1.0, 5) == 0
+    e = [math.exp(1), math.exp(2), math.exp(3)]
+    for a, b in zip(y.numpy()[0].tolist(), [v / sum(e) for v in e]):
+        assert round(a - b, 5) == 0
+
+
+def test_log_softmax_matches_torch():
+    # test/test_op_parity.py:141-158 (forward; tol 1e-4 there, 1e-5 here)
+    rng = np.random.default_rng(60)
+    for shape, dim in [((32, 10), 1), ((4, 300, 33), 1), ((300, 70), 0), ((3, 5000), -1)]:
+        x = rng.standard_normal(shape).astype(np.float32)
+        tx = tp.tensor(x, device=DEV)
+        close(tx.log_softmax(dim), torch.log_softmax(torch.from_numpy(x), dim), rtol=1e-5, atol=1e-5)
+        close(tp.softmax(tx, dim), torch.softmax(torch.from_numpy(x), dim), rtol=1e-5, atol=1e-7)
+
+
+def test_softmax_dtype_rules():
+    xi = tp.tensor(np.array([[1, 2, 3]], np.int64), device=DEV)
+    y = xi.softmax(1)  # integral input computes in Float32 (PointwiseKernels.cpp:521)
+    assert y.dtype == tp.float32
+    close(y, torch.softmax(torch.tensor([[1.0, 2.0, 3.0]]), 1))
+    x = tp.tensor(np.ones((2, 3), np.float32), device=DEV)
+    with pytest.raises(NotImplementedError):
+        x.softmax(1, tp.float64)
+    with pytest.raises(IndexError):
+        x.softmax(2)
+
+
+def test_softmax_backward_ops_match_torch_autograd():
+    rng = np.random.default_rng(61)
+    x = rng.standard_normal((16, 257)).astype(np.float32)
+    g = rng.standard_normal((16, 257)).astype(np.float32)
+    for log in (False, True):
+        tx = torch.from_numpy(x).requires_grad_(True)
+        ty = torch.log_softmax(tx, 1) if log else torch.softmax(tx, 1)
+        ty.backward(torch.from_numpy(g))
+        y = tp.tensor(ty.detach().numpy(), device=DEV)
+        f = tp._log_softmax_backward_data if log else tp._softmax_backward_data
+        close(f(tp.tensor(g, device=DEV), y, 1), tx.grad, rtol=1e-4, atol=1e-6)
+
+
+def test_nll_loss_and_cross_entropy_match_torch():
+    # test/test_op_parity.py:160-198, test/test_cpu_precision.py:165-190 (N=32, C=10)
+    rng = np.random.default_rng(42)
+    x = rng.standard_normal((32, 10)).astype(np.float32)
+    t = rng.integers(0, 10, 32).astype(np.int64)
+    w = rng.uniform(0.5, 1.5, 10).astype(np.float32)
+    tx, tt, tw = tp.tensor(x, device=DEV), tp.tensor(t, device=DEV), tp.tensor(w, device=DEV)
+    for red, name in ((0, "none"), (1, "mean"), (2, "sum")):
+        for wt in (None, tw):
+            out, total = tp.nll_loss(tx, tt, wt, red)
+            ref = torch.nn.functional.nll_loss(torch.from_numpy(x), torch.from_numpy(t),
+                                               None if wt is None else torch.from_numpy(w), reduction=name)
+            close(out, ref, rtol=1e-6, atol=1e-7)
+            assert total.shape == [1]
+    # cross entropy forward + backward (log_softmax -> nll_loss, then the two gradient ops)
+    xt = torch.from_numpy(x).requires_grad_(True)
+    lt = torch.nn.functional.cross_entropy(xt, torch.from_numpy(t))
+    lt.backward()
+    logp = tx.log_softmax(1)
+    loss, total = tp.nll_loss(logp, tt, None, 1)
+    assert abs(loss.item() - lt.item()) <= 1e-6 * abs(lt.item())
+    assert abs(tp.cross_entropy(tx, tt).item() - lt.item()) <= 1e-6 * abs(lt.item())
+    one = tp.tensor(np.array(1.0, np.float32), device=DEV)
+    g_logp = tp.nll_loss_backward(one, logp, tt, None, 1, -100, total)
+    gx = tp._log_softmax_backward_data(g_logp, logp, 1)
+    close(gx, xt.grad, rtol=1e-5, atol=1e-7)
+    # total_weight omitted: recomputed from target (LossKernels.cpp:67-76)
+    close(tp.nll_loss_backward(one, logp, tt, None, 1, -100, None), torch.from_numpy(g_logp.numpy()), rtol=0, atol=0)
+
+
+def test_nll_loss_errors():
+    x = tp.tensor(np.zeros((2, 3), np.float32), device=DEV)
+    with pytest.raises(RuntimeError, match="Target out of bounds"):
+        tp.nll_loss(x, tp.tensor(np.array([0, 3], np.int64), device=DEV))
+    with pytest.raises(NotImplementedError):
+        tp.nll_loss(x, tp.tensor(np.array([0, 1], np.int32), device=DEV))
+    with pytest.raises(ValueError):
+        tp.nll_loss(x, tp.tensor(np.array([0, 1], np.int64), device=DEV), None, 3)
