@@ -112,6 +112,43 @@ def copy_call(torch, capi, dst, src, stream):
     return c
 
 
+def softmax_call(torch, capi, x, dim, mode, stream, y=None):
+    """Pre-bound tpr_softmax on x (forward) or on g = x with output y (backward)."""
+    v = capi._view3(x, dim)
+    out = torch.empty(list(x.shape), dtype=torch.float32, device=x.device)
+    d = capi.SoftmaxDesc()
+    d.mode, d.dtype = mode, capi.FLOAT32
+    d.outer, d.n, d.inner = v[0]
+    vb = capi._view3(y, dim) if y is not None else None
+    for k in range(3):
+        d.a_strides[k] = v[1][k]
+        d.b_strides[k] = vb[1][k] if vb is not None else 0
+    L = capi.lib()
+    wsb = L.tpr_softmax_workspace_bytes(ctypes.byref(d))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
+    c = Call(L.tpr_softmax, (ctypes.byref(d), ctypes.c_void_p(x.data_ptr()),
+                             ctypes.c_void_p(y.data_ptr() if y is not None else 0),
+                             ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ws.data_ptr()), wsb, stream))
+    c.keep = (d, out, ws)
+    c.bytes = x.numel() * 4 * (3 if y is not None else 2)
+    return c
+
+
+def nll_bwd_call(torch, capi, n, c, target, g, tw, stream):
+    gi = torch.empty((n, c), dtype=torch.float32, device=target.device)
+    call = Call(capi.lib().tpr_nll_loss_backward, (ctypes.c_void_p(g.data_ptr()), 1, ctypes.c_void_p(target.data_ptr()),
+                                                   1, ctypes.c_void_p(0), ctypes.c_void_p(tw.data_ptr()), n, c, 1,
+                                                   -100, ctypes.c_void_p(gi.data_ptr()), stream))
+    call.keep = (gi,)
+    call.bytes = n * c * 4 + n * 8
+    return call
+
+
+def rate(ms, by):
+    return {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1), "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4),
+            "alg_bytes": by}
+
+
 def time_calls(torch, step_fns, steps, warmup):
     """Run warmup, then time `steps` iterations of step_fns[i % len] with HIP events."""
     for i in range(warmup):
@@ -244,6 +281,14 @@ def main():
                                           "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4),
                                           "rows_per_s": round(1024 / (ms * 1e-3), 1)}
         keep_c3 = b3[0]
+        # softmax / log_softmax along the rows of the same tensors (register-resident rows)
+        esm3 = {}
+        for name, mode in (("softmax", capi.SOFTMAX_FWD), ("log_softmax", capi.LOG_SOFTMAX_FWD)):
+            cs = [softmax_call(torch, capi, b, -1, mode, stream) for b in b3[:4]]
+            ms = time_calls(torch, cs, max(steps, 12), warmup)
+            esm3[name] = rate(ms, cs[0].bytes)
+            del cs
+        extras["softmax_C3_1024x32768"] = esm3
         del b3, c3
         # C4: full-tensor reductions of 2^28 N(0.5, 2)
         x4 = gen(torch, (1 << 28,), "normal", 4000, dev) * 2.0 + 0.5
@@ -277,6 +322,26 @@ def main():
         e5["argmax_dim-1"] = {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
                               "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4)}
         extras["C5_logits_256x151936"] = e5
+        # softmax family on the same logits: softmax / log_softmax forward (read + write), softmax
+        # backward (read g and y, write the gradient), and nll_loss backward (write [256, 151936])
+        esm = {}
+        for name, mode in (("softmax", capi.SOFTMAX_FWD), ("log_softmax", capi.LOG_SOFTMAX_FWD)):
+            cs = [softmax_call(torch, capi, b, -1, mode, stream) for b in b5[:3]]
+            ms = time_calls(torch, cs, max(steps, 10), warmup)
+            esm[name] = rate(ms, cs[0].bytes)
+            del cs
+        cs = [softmax_call(torch, capi, b5[i], -1, capi.SOFTMAX_BWD, stream, y=b5[i + 1]) for i in (0, 2)]
+        ms = time_calls(torch, cs, max(steps, 10), warmup)
+        esm["softmax_backward"] = rate(ms, cs[0].bytes)
+        del cs
+        tgt = torch.randint(0, 151936, (256,), device=dev, dtype=torch.int64)
+        one = torch.ones((), device=dev)
+        tw = torch.full((1,), 256.0, device=dev)
+        cs = [nll_bwd_call(torch, capi, 256, 151936, tgt, one, tw, stream) for _ in range(3)]
+        ms = time_calls(torch, cs, max(steps, 10), warmup)
+        esm["nll_loss_backward"] = rate(ms, cs[0].bytes)
+        del cs
+        extras["softmax_C5_logits_256x151936"] = esm
         keep_c5 = b5[0]
         del b5, c5, c5a
         # copy_ (strided / casting) on the C2 geometry: read + write bytes
@@ -295,6 +360,11 @@ def main():
                          "kernel": copy_kernel_name(capi.copy_plan(outs[0], view(bufs[0])))}
             del outs, cc
         extras["copy_C2_64x1024x1024"] = ecp
+        # softmax over the middle (strided) dim of the C2 geometry
+        cs = [softmax_call(torch, capi, bufs[i], 1, capi.SOFTMAX_FWD, stream) for i in range(2)]
+        ms = time_calls(torch, cs, max(steps, 8), warmup)
+        extras["softmax_C2_dim1_64x1024x1024"] = rate(ms, cs[0].bytes)
+        del cs
     if args.calibrate_copy:
         xc = gen(torch, (64 << 20,), "normal", 6000, dev)
         for _ in range(3):

@@ -178,7 +178,10 @@ int tpr_copy_strided(const void* in, int32_t elem_size, int32_t ndim, const int6
  *     with a = g (dL/dy) and b = y (the forward output).
  * a: x (forward) or g (backward), strides a_strides (elements, per logical
  * dim); b: y (backward only, strides b_strides; NULL forward).  out is written
- * dense row-major [outer, n, inner].  Float32 only.  No workspace. */
+ * dense row-major [outer, n, inner].  Float32 only.  Workspace:
+ * tpr_softmax_workspace_bytes(desc) bytes (0 for most shapes; rows longer than
+ * the register-resident kernels hold, when there are few of them, use
+ * per-chunk partial statistics). */
 enum tpr_softmax_mode {
     TPR_SOFTMAX_FWD = 0,
     TPR_LOG_SOFTMAX_FWD = 1,
@@ -194,7 +197,9 @@ typedef struct tpr_softmax_desc {
     int64_t b_strides[3];
 } tpr_softmax_desc;
 
-int tpr_softmax(const tpr_softmax_desc* desc, const void* a, const void* b, void* out, void* stream);
+size_t tpr_softmax_workspace_bytes(const tpr_softmax_desc* desc);
+int tpr_softmax(const tpr_softmax_desc* desc, const void* a, const void* b, void* out, void* workspace,
+                size_t workspace_bytes, void* stream);
 
 /* nll_loss forward (/root/reference/p10/src/backend/cpu/LossKernels.cpp:12-55;
  * CUDA nll_loss_cuda, /root/reference/p10/src/backend/cuda/LossKernels.cu:66-113).
@@ -240,6 +245,9 @@ int32_t tpr_abi_version(void);
  * 0 = automatic), "colblock" (256, 512 or 1024 threads per column-kernel
  * workgroup, 0 = automatic),
  * "smx_two_pass" (1 = softmax rows always take the two-pass kernel),
+ * "smx_split" (1 / -1 = long softmax rows always / never split over chunk
+ * workgroups, 0 = automatic), "smx_lanes" (512 = softmax rows of 16385..32768
+ * floats on 512-thread workgroups, 0 = automatic),
  * "topk_variant" (wave kernel prefetch depth: 1 = none, 2 = one slice, 3 = two
  * slices; 0 = automatic), "topk_waves" (8 or 16 waves per wave-kernel
  * workgroup, 0 = automatic).

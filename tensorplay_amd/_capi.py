@@ -28,7 +28,7 @@ OP_NAMES = {"sum": SUM, "mean": MEAN, "amax": AMAX, "amin": AMIN, "argmax": ARGM
 
 EXPORTED = ["tpr_reduce_workspace_bytes", "tpr_reduce", "tpr_topk_workspace_bytes", "tpr_topk",
             "tpr_copy", "tpr_copy_plan", "tpr_copy_strided", "tpr_last_error", "tpr_abi_version",
-            "tpr_debug_set", "tpr_softmax", "tpr_nll_loss_workspace_bytes", "tpr_nll_loss",
+            "tpr_debug_set", "tpr_softmax", "tpr_softmax_workspace_bytes", "tpr_nll_loss_workspace_bytes", "tpr_nll_loss",
             "tpr_nll_loss_backward"]
 # enum tpr_softmax_mode
 SOFTMAX_FWD, LOG_SOFTMAX_FWD, SOFTMAX_BWD, LOG_SOFTMAX_BWD = range(4)
@@ -116,7 +116,9 @@ def lib():
         L.tpr_abi_version.restype = i32
         L.tpr_debug_set.argtypes = [ctypes.c_char_p, i64]
         L.tpr_debug_set.restype = ctypes.c_int
-        L.tpr_softmax.argtypes = [ctypes.POINTER(SoftmaxDesc), vp, vp, vp, vp]
+        L.tpr_softmax.argtypes = [ctypes.POINTER(SoftmaxDesc), vp, vp, vp, vp, sz, vp]
+        L.tpr_softmax_workspace_bytes.argtypes = [ctypes.POINTER(SoftmaxDesc)]
+        L.tpr_softmax_workspace_bytes.restype = sz
         L.tpr_softmax.restype = ctypes.c_int
         L.tpr_nll_loss_workspace_bytes.argtypes = [i64]
         L.tpr_nll_loss_workspace_bytes.restype = sz
@@ -326,9 +328,13 @@ def softmax(x, dim=-1, log=False, grad_of=None):
     for k in range(3):
         d.a_strides[k] = v[1][k]
         d.b_strides[k] = vb[1][k] if vb is not None else 0
-    _check(lib().tpr_softmax(ctypes.byref(d), ctypes.c_void_p(a.data_ptr()),
-                             ctypes.c_void_p(b.data_ptr() if b is not None else 0),
-                             ctypes.c_void_p(out.data_ptr()), _stream(torch, x.device)))
+    L = lib()
+    wsb = L.tpr_softmax_workspace_bytes(ctypes.byref(d))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
+    _check(L.tpr_softmax(ctypes.byref(d), ctypes.c_void_p(a.data_ptr()),
+                         ctypes.c_void_p(b.data_ptr() if b is not None else 0),
+                         ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ws.data_ptr()), wsb,
+                         _stream(torch, x.device)))
     return out
 
 

@@ -99,8 +99,11 @@ Tensor run_softmax(const Tensor& a, const Tensor* b, int64_t d, int mode, const 
         desc.a_strides[i] = sa[i];
         desc.b_strides[i] = sb[i];
     }
+    const size_t wsb = tpr_softmax_workspace_bytes(&desc);
+    std::shared_ptr<void> ws;
+    if (wsb) ws = allocate(wsb, a.device());
     DeviceGuard guard(a.device());
-    const int rc = tpr_softmax(&desc, av.data_ptr(), b ? bv.data_ptr() : nullptr, out.data_ptr(),
+    const int rc = tpr_softmax(&desc, av.data_ptr(), b ? bv.data_ptr() : nullptr, out.data_ptr(), ws.get(), wsb,
                                currentStream(a.device().index));
     if (rc != TPR_OK) throw_status(rc, name);
     return out;

@@ -35,6 +35,8 @@ struct DebugKnobs {
     int64_t colblock = 0;
     int64_t nt = 0;
     int64_t smx_two_pass = 0;
+    int64_t smx_lanes = 0;
+    int64_t smx_split = 0;
 };
 DebugKnobs& knobs();
 

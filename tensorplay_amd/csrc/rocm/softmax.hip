@@ -38,6 +38,9 @@ constexpr float kL2E = 1.4426950408889634f;
 enum { FWD = 0, FWD_LOG = 1, BWD = 2, BWD_LOG = 3 };
 
 __device__ __forceinline__ float ex(float d) { return exp2f(d * kL2E); }
+// Terms of a sum of exponentials: the bare hardware exp2 (no rescaling for
+// results below 2^-126, which are below a sum's rounding anyway).
+__device__ __forceinline__ float exs(float d) { return __builtin_amdgcn_exp2f(d * kL2E); }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -98,7 +101,7 @@ __device__ __forceinline__ void ms_merge(float& m, float& s, float m2, float s2)
         s += s2;
         return;
     }
-    s = (m == -INFINITY ? s : s * ex(m - M)) + (m2 == -INFINITY ? s2 : s2 * ex(m2 - M));
+    s = (m == -INFINITY ? s : s * exs(m - M)) + (m2 == -INFINITY ? s2 : s2 * exs(m2 - M));
     m = M;
 }
 
@@ -109,7 +112,7 @@ __device__ __forceinline__ void ms_add(float& m, float& s, const float* x) {
 #pragma unroll
     for (int i = 1; i < K; ++i) cm = fmaxf(cm, x[i]);
     if (cm > m) {
-        s = (m == -INFINITY) ? s : s * ex(m - cm);
+        s = (m == -INFINITY) ? s : s * exs(m - cm);
         m = cm;
     }
     if (m == -INFINITY) {
@@ -117,7 +120,7 @@ __device__ __forceinline__ void ms_add(float& m, float& s, const float* x) {
         for (int i = 0; i < K; ++i) s += (x[i] != x[i]) ? x[i] : 0.0f;
     } else {
 #pragma unroll
-        for (int i = 0; i < K; ++i) s += ex(x[i] - m);
+        for (int i = 0; i < K; ++i) s += exs(x[i] - m);
     }
 }
 
@@ -159,6 +162,8 @@ struct SmxArgs {
     long long rows, n;
     long long sa, sb;  // row strides of a and b (elements)
     int nt;            // nontemporal loads / stores
+    int chunks;        // split rows: chunks per row
+    float2* part;      // split rows: [rows, chunks] partial statistics
 };
 
 // ---------------------------------------------------------------------------
@@ -211,7 +216,7 @@ __global__ __launch_bounds__(G > 256 ? G : 256) void k_smx_rows(SmxArgs p) {
 #pragma unroll
             for (int j = 0; j < V; ++j)
 #pragma unroll
-                for (int c = 0; c < VW; ++c) s += ex(a[j][c] - m);
+                for (int c = 0; c < VW; ++c) s += exs(a[j][c] - m);
         }
         s = grp<G, false>(s, sh[1]);
         if (m == -INFINITY) {  // no value above -inf in the slice: NaN, as the reference
@@ -247,37 +252,67 @@ __global__ __launch_bounds__(G > 256 ? G : 256) void k_smx_rows(SmxArgs p) {
 // Long rows: one 1024-thread workgroup per row, two streaming passes.  Pass 1
 // accumulates the online (max, sum) state (forward) or the dot / sum
 // (backward); pass 2 re-reads the row and writes the output.  Pass 1 uses
-// ordinary loads so the row stays in the caches for pass 2.
+// ordinary loads so the row stays in the caches for pass 2.  Both passes keep
+// two tiles in flight: the loads of tile t+1 are issued before tile t is
+// consumed (one workgroup per CU has to cover the memory latency alone).
 // ---------------------------------------------------------------------------
 template <int MODE, int VW, int U>
 __global__ __launch_bounds__(1024) void k_smx_rows2(SmxArgs p) {
     constexpr int T = 1024;
     constexpr bool BW = MODE >= BWD;
+    constexpr int UB = BW ? U : 1;
     constexpr long long TILE = (long long)T * VW * U;
     __shared__ float sh[2][T / kWave];
     const long long row = blockIdx.x;
+    const long long n = p.n;
     const float* pa = p.a + row * p.sa;
     const float* pb = BW ? p.b + row * p.sb : nullptr;
     float* po = p.out + row * p.n;
     const int t = threadIdx.x;
 
-    float st0, st1 = 0.0f;
-    if constexpr (!BW) {
-        float m = -INFINITY, s = 0.0f;
-        for (long long base = 0; base < p.n; base += TILE) {
-            float x[U][VW];
+    auto load = [&](float (&xa)[U][VW], float (&xb)[UB][VW], long long base, int nt) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const long long e = base + ((long long)u * T + t) * VW;
-                if (e < p.n) {
-                    Vec<VW>::load(x[u], pa + e, 0);
-                } else {
+        for (int u = 0; u < U; ++u) {
+            const long long e = base + ((long long)u * T + t) * VW;
+            if (e < n) {
+                Vec<VW>::load(xa[u], pa + e, nt);
+                if constexpr (BW) Vec<VW>::load(xb[u], pb + e, nt);
+            } else {
 #pragma unroll
-                    for (int c = 0; c < VW; ++c) x[u][c] = -INFINITY;
+                for (int c = 0; c < VW; ++c) {
+                    xa[u][c] = BW ? 0.0f : -INFINITY;
+                    if constexpr (BW) xb[u][c] = 0.0f;
                 }
             }
-            ms_add<U * VW>(m, s, &x[0][0]);
         }
+    };
+
+    float a0[U][VW], b0[UB][VW], a1[U][VW], b1[UB][VW];
+    float m = -INFINITY, s = 0.0f;
+    auto consume = [&](float (&xa)[U][VW], float (&xb)[UB][VW]) {
+        if constexpr (!BW) {
+            ms_add<U * VW>(m, s, &xa[0][0]);
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int c = 0; c < VW; ++c) s += (MODE == BWD) ? xa[u][c] * xb[u][c] : xa[u][c];
+        }
+    };
+    load(a0, b0, 0, 0);
+    for (long long base = 0;;) {
+        if (base + TILE < n) load(a1, b1, base + TILE, 0);
+        consume(a0, b0);
+        base += TILE;
+        if (base >= n) break;
+        if (base + TILE < n) load(a0, b0, base + TILE, 0);
+        consume(a1, b1);
+        base += TILE;
+        if (base >= n) break;
+    }
+
+    float st0, st1 = 0.0f;
+    if constexpr (!BW) {
         grp_ms<T>(m, s, sh[0], sh[1]);
         if (m == -INFINITY) {
             st0 = NAN;
@@ -287,33 +322,135 @@ __global__ __launch_bounds__(1024) void k_smx_rows2(SmxArgs p) {
             st1 = (MODE == FWD) ? 1.0f / s : logf(s);
         }
     } else {
-        float s = 0.0f;
-        for (long long base = 0; base < p.n; base += TILE) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const long long e = base + ((long long)u * T + t) * VW;
-                if (e < p.n) {
-                    float g[VW], y[VW];
-                    Vec<VW>::load(g, pa + e, 0);
-                    Vec<VW>::load(y, pb + e, 0);
-#pragma unroll
-                    for (int c = 0; c < VW; ++c) s += (MODE == BWD) ? g[c] * y[c] : g[c];
-                }
-            }
-        }
         st0 = grp<T, false>(s, sh[0]);
     }
 
-    for (long long base = 0; base < p.n; base += TILE) {
+    auto emit = [&](float (&xa)[U][VW], float (&xb)[UB][VW], long long base) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const long long e = base + ((long long)u * T + t) * VW;
-            if (e < p.n) {
-                float x[VW], y[VW], o[VW];
-                Vec<VW>::load(x, pa + e, p.nt);
-                if constexpr (BW) Vec<VW>::load(y, pb + e, p.nt);
+            if (e < n) {
+                float o[VW];
 #pragma unroll
-                for (int c = 0; c < VW; ++c) o[c] = outv<MODE>(x[c], BW ? y[c] : 0.0f, st0, st1);
+                for (int c = 0; c < VW; ++c) o[c] = outv<MODE>(xa[u][c], BW ? xb[u][c] : 0.0f, st0, st1);
+                Vec<VW>::store(po + e, o, p.nt);
+            }
+        }
+    };
+    load(a0, b0, 0, p.nt);
+    for (long long base = 0;;) {
+        if (base + TILE < n) load(a1, b1, base + TILE, p.nt);
+        emit(a0, b0, base);
+        base += TILE;
+        if (base >= n) break;
+        if (base + TILE < n) load(a0, b0, base + TILE, p.nt);
+        emit(a1, b1, base);
+        base += TILE;
+        if (base >= n) break;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Split long rows (few rows, e.g. LLM vocabulary logits): each row is cut into
+// kChunk-element chunks, one 256-thread workgroup per (row, chunk) in both
+// kernels, so the chip is full however few rows there are.
+//   k_smx_part:  partial statistics of the chunk -> part[row, chunk]
+//                (forward: online (max, sum); backward: sum(g*y) or sum(g));
+//   k_smx_apply: every thread merges the row's partials in chunk order (the
+//                same result in every workgroup of the row), then re-reads its
+//                chunk and writes the output.
+// ---------------------------------------------------------------------------
+constexpr int kChunk = 8192;
+
+template <int MODE, int VW>
+__global__ __launch_bounds__(256) void k_smx_part(SmxArgs p) {
+    constexpr bool BW = MODE >= BWD;
+    constexpr int U = 8 / VW;                 // 8 floats per thread per step
+    constexpr int STEP = 256 * VW * U;        // 2048 floats
+    __shared__ float sh[2][256 / kWave];
+    const long long row = blockIdx.x / p.chunks;
+    const long long c0 = (long long)(blockIdx.x - row * p.chunks) * kChunk;
+    const float* pa = p.a + row * p.sa;
+    const float* pb = BW ? p.b + row * p.sb : nullptr;
+    const int t = threadIdx.x;
+    float m = -INFINITY, s = 0.0f;
+#pragma unroll
+    for (int it = 0; it < kChunk / STEP; ++it) {
+        float x[U][VW], y[BW ? U : 1][VW];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const long long e = c0 + it * STEP + ((long long)u * 256 + t) * VW;
+            if (e < p.n) {
+                Vec<VW>::load(x[u], pa + e, 0);
+                if constexpr (BW) Vec<VW>::load(y[u], pb + e, 0);
+            } else {
+#pragma unroll
+                for (int c = 0; c < VW; ++c) {
+                    x[u][c] = BW ? 0.0f : -INFINITY;
+                    if constexpr (BW) y[u][c] = 0.0f;
+                }
+            }
+        }
+        if constexpr (!BW) {
+            ms_add<U * VW>(m, s, &x[0][0]);
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int c = 0; c < VW; ++c) s += (MODE == BWD) ? x[u][c] * y[u][c] : x[u][c];
+        }
+    }
+    if constexpr (!BW) grp_ms<256>(m, s, sh[0], sh[1]);
+    else s = grp<256, false>(s, sh[0]);
+    if (t == 0) p.part[blockIdx.x] = make_float2(m, s);
+}
+
+template <int MODE, int VW>
+__global__ __launch_bounds__(256) void k_smx_apply(SmxArgs p) {
+    constexpr bool BW = MODE >= BWD;
+    constexpr int U = 8 / VW;
+    constexpr int STEP = 256 * VW * U;
+    const long long row = blockIdx.x / p.chunks;
+    const long long c0 = (long long)(blockIdx.x - row * p.chunks) * kChunk;
+    const float* pa = p.a + row * p.sa;
+    const float* pb = BW ? p.b + row * p.sb : nullptr;
+    float* po = p.out + row * p.n;
+    const int t = threadIdx.x;
+    const float2* pp = p.part + row * p.chunks;
+    float st0, st1 = 0.0f;
+    if constexpr (!BW) {
+        float m = pp[0].x, s = pp[0].y;
+        for (int k = 1; k < p.chunks; ++k) ms_merge(m, s, pp[k].x, pp[k].y);
+        if (m == -INFINITY) {
+            st0 = NAN;
+            st1 = NAN;
+        } else {
+            st0 = m;
+            st1 = (MODE == FWD) ? 1.0f / s : logf(s);
+        }
+    } else {
+        float s = pp[0].y;
+        for (int k = 1; k < p.chunks; ++k) s += pp[k].y;
+        st0 = s;
+    }
+#pragma unroll
+    for (int it = 0; it < kChunk / STEP; ++it) {
+        float x[U][VW], y[BW ? U : 1][VW];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const long long e = c0 + it * STEP + ((long long)u * 256 + t) * VW;
+            if (e < p.n) {
+                Vec<VW>::load(x[u], pa + e, p.nt);
+                if constexpr (BW) Vec<VW>::load(y[u], pb + e, p.nt);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const long long e = c0 + it * STEP + ((long long)u * 256 + t) * VW;
+            if (e < p.n) {
+                float o[VW];
+#pragma unroll
+                for (int c = 0; c < VW; ++c) o[c] = outv<MODE>(x[u][c], BW ? y[u][c] : 0.0f, st0, st1);
                 Vec<VW>::store(po + e, o, p.nt);
             }
         }
@@ -417,8 +554,10 @@ int launch_rows(const SmxArgs& a, hipStream_t st) {
     return check_launch("tpr_softmax (rows)");
 }
 
-// Single-pass variants: VW = 4 -> G in {16, 64, 256, 1024}, V in {1, 2, 4, 8}
-// (backward: V <= 4, two loaded operands); VW = 1 -> G in {64, 256, 1024},
+// Single-pass variants: VW = 4 -> G in {16, 64, 256, 1024}, V in {1, 2, 4, 8},
+// and forward rows of 16385..32768 floats on 512 lanes with V = 16 (two
+// workgroups per CU, so one loads while the other reduces: 67% vs 55% of the
+// HBM peak with one 1024-lane workgroup per CU); VW = 1 -> G in {64, 256, 1024},
 // V in {4, 16} (backward: 4).  Returns -1 when the row is too long.
 template <int MODE>
 int rows_single(const SmxArgs& a, int vw, hipStream_t st) {
@@ -426,13 +565,16 @@ int rows_single(const SmxArgs& a, int vw, hipStream_t st) {
     const long long n = a.n;
     if (vw == 4) {
         const long long q = (n + 3) / 4;  // vectors per row
-        const int vmax = BW ? 4 : 8;
+        const int vmax = 8;
         auto pick = [&](int g) -> int {  // smallest V with g*V >= q, or 0
             for (int v = 1; v <= vmax; v *= 2)
                 if ((long long)g * v >= q) return v;
             return 0;
         };
         // fewest lanes that keep V <= 4, else the widest workgroup with V = 8
+        if constexpr (!BW) {
+            if (knobs().smx_lanes != 1024 && q > 4096 && q <= 8192) return launch_rows<MODE, 512, 16, 4>(a, st);
+        }
         for (int g : {16, 64, 256, 1024}) {
             const int v = pick(g);
             if (v == 0 || (v > 4 && g < 1024)) continue;
@@ -441,8 +583,7 @@ int rows_single(const SmxArgs& a, int vw, hipStream_t st) {
         case 1: return launch_rows<MODE, GG, 1, 4>(a, st);                         \
         case 2: return launch_rows<MODE, GG, 2, 4>(a, st);                         \
         case 4: return launch_rows<MODE, GG, 4, 4>(a, st);                         \
-        default: if constexpr (!BW) return launch_rows<MODE, GG, 8, 4>(a, st);     \
-                 return -1;                                                        \
+        default: return launch_rows<MODE, GG, 8, 4>(a, st);                        \
     }
             switch (g) {
                 case 16: TPR_SMX_V(16)
@@ -469,15 +610,39 @@ int rows_single(const SmxArgs& a, int vw, hipStream_t st) {
     return -1;
 }
 
+long long split_chunks(long long n) { return (n + kChunk - 1) / kChunk; }
+
+// Rows too long for registers: split over (row, chunk) workgroups when the rows
+// alone cannot fill the chip, else one 1024-thread workgroup per row.
+bool use_split(long long rows, long long n) {
+    const long long force = knobs().smx_split;
+    if (force) return force > 0;
+    (void)n;
+    return rows < device_info().cus;
+}
+
 template <int MODE>
-int run_rows(const SmxArgs& a, int vw, hipStream_t st) {
+int run_rows(const SmxArgs& a0, int vw, hipStream_t st) {
+    SmxArgs a = a0;
     const int two_pass = knobs().smx_two_pass;
     if (!two_pass) {
         const int rc = rows_single<MODE>(a, vw, st);
         if (rc >= 0) return rc;
     }
-    if (vw == 4) hipLaunchKernelGGL((k_smx_rows2<MODE, 4, 4>), dim3((unsigned)a.rows), dim3(1024), 0, st, a);
-    else hipLaunchKernelGGL((k_smx_rows2<MODE, 1, 8>), dim3((unsigned)a.rows), dim3(1024), 0, st, a);
+    constexpr bool BW = MODE >= BWD;
+    if (a.part) {
+        const long long blocks = a.rows * a.chunks;
+        if (vw == 4) {
+            hipLaunchKernelGGL((k_smx_part<MODE, 4>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+            hipLaunchKernelGGL((k_smx_apply<MODE, 4>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+        } else {
+            hipLaunchKernelGGL((k_smx_part<MODE, 1>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+            hipLaunchKernelGGL((k_smx_apply<MODE, 1>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+        }
+        return check_launch("tpr_softmax (split rows)");
+    }
+    if (vw == 4) hipLaunchKernelGGL((k_smx_rows2<MODE, 4, BW ? 2 : 4>), dim3((unsigned)a.rows), dim3(1024), 0, st, a);
+    else hipLaunchKernelGGL((k_smx_rows2<MODE, 1, BW ? 8 : 16>), dim3((unsigned)a.rows), dim3(1024), 0, st, a);
     return check_launch("tpr_softmax (long rows)");
 }
 
@@ -496,7 +661,38 @@ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 }  // namespace
 }  // namespace tpr
 
-extern "C" int tpr_softmax(const tpr_softmax_desc* d, const void* a, const void* b, void* out, void* stream) {
+namespace tpr {
+namespace {
+bool rows_path(const tpr_softmax_desc* d) {
+    const bool bw = d->mode >= TPR_SOFTMAX_BWD;
+    return d->inner == 1 && d->a_strides[1] == 1 && (!bw || d->b_strides[1] == 1) && d->outer <= 0x7fffffffLL &&
+           knobs().general == 0;
+}
+
+// Workspace of the split-row kernels (zero when they are not used): one float2
+// per (row, chunk).  Independent of pointer alignment: it assumes the scalar
+// single-pass capacity (16384 floats forward, 4096 backward).
+size_t smx_workspace(const tpr_softmax_desc* d) {
+    if (!rows_path(d) || d->outer == 0 || d->n == 0) return 0;
+    const bool bw = d->mode >= TPR_SOFTMAX_BWD;
+    const long long cap1 = bw ? 4096 : 16384;
+    if (!(knobs().smx_two_pass || d->n > cap1)) return 0;
+    if (!use_split(d->outer, d->n)) return 0;
+    const long long blocks = d->outer * split_chunks(d->n);
+    if (blocks > 0x7fffffffLL) return 0;
+    return (size_t)blocks * sizeof(float2);
+}
+}  // namespace
+}  // namespace tpr
+
+extern "C" size_t tpr_softmax_workspace_bytes(const tpr_softmax_desc* d) {
+    if (!d || d->mode < TPR_SOFTMAX_FWD || d->mode > TPR_LOG_SOFTMAX_BWD || d->outer < 0 || d->n < 0 || d->inner < 0)
+        return 0;
+    return tpr::smx_workspace(d);
+}
+
+extern "C" int tpr_softmax(const tpr_softmax_desc* d, const void* a, const void* b, void* out, void* workspace,
+                           size_t workspace_bytes, void* stream) {
     using namespace tpr;
     if (!d) return fail(TPR_ERR_INVALID_ARG, "tpr_softmax: null descriptor");
     if (d->mode < TPR_SOFTMAX_FWD || d->mode > TPR_LOG_SOFTMAX_BWD)
@@ -511,10 +707,15 @@ extern "C" int tpr_softmax(const tpr_softmax_desc* d, const void* a, const void*
     const float* pb = static_cast<const float*>(b);
     float* po = static_cast<float*>(out);
 
-    const bool rows = d->inner == 1 && d->a_strides[1] == 1 && (!bw || d->b_strides[1] == 1) &&
-                      d->outer <= 0x7fffffffLL && knobs().general == 0;
-    if (rows) {
-        SmxArgs r{pa, pb, po, d->outer, d->n, d->a_strides[0], bw ? d->b_strides[0] : 0, 0};
+    if (rows_path(d)) {
+        SmxArgs r{pa, pb, po, d->outer, d->n, d->a_strides[0], bw ? d->b_strides[0] : 0, 0, 0, nullptr};
+        const size_t wsn = smx_workspace(d);
+        if (wsn) {
+            if (!workspace || workspace_bytes < wsn)
+                return fail(TPR_ERR_WORKSPACE, "tpr_softmax: workspace smaller than tpr_softmax_workspace_bytes");
+            r.part = static_cast<float2*>(workspace);
+            r.chunks = (int)split_chunks(d->n);
+        }
         const long long bytes = d->outer * d->n * 4LL * (bw ? 3 : 2);
         r.nt = knobs().nt ? (knobs().nt > 0) : (bytes >= (256LL << 20));
         const bool v4 = d->n % 4 == 0 && al16(pa) && al16(po) && (d->outer == 1 || r.sa % 4 == 0) &&

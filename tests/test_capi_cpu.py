@@ -78,13 +78,21 @@ def test_softmax_loss_validation_without_gpu():
     assert ctypes.sizeof(_capi.SoftmaxDesc) == 8 + 24 + 48
     d = _capi.SoftmaxDesc()
     d.mode, d.dtype, d.outer, d.n, d.inner = 0, _capi.FLOAT64, 2, 3, 1
-    assert L.tpr_softmax(ctypes.byref(d), None, None, None, None) == _capi.ERR_UNSUPPORTED_DTYPE
+    assert L.tpr_softmax(ctypes.byref(d), None, None, None, None, 0, None) == _capi.ERR_UNSUPPORTED_DTYPE
     d.dtype, d.mode = _capi.FLOAT32, 7
-    assert L.tpr_softmax(ctypes.byref(d), None, None, None, None) == _capi.ERR_INVALID_ARG
+    assert L.tpr_softmax(ctypes.byref(d), None, None, None, None, 0, None) == _capi.ERR_INVALID_ARG
     d.mode, d.n = _capi.SOFTMAX_FWD, 0
-    assert L.tpr_softmax(ctypes.byref(d), None, None, None, None) == _capi.OK  # empty: no launch
+    assert L.tpr_softmax(ctypes.byref(d), None, None, None, None, 0, None) == _capi.OK  # empty: no launch
     d.n, d.mode = 3, _capi.SOFTMAX_BWD
-    assert L.tpr_softmax(ctypes.byref(d), 16, None, 16, None) == _capi.ERR_INVALID_ARG  # y missing
+    assert L.tpr_softmax(ctypes.byref(d), 16, None, 16, None, 0, None) == _capi.ERR_INVALID_ARG  # y missing
+    d.mode, d.outer, d.n, d.inner = _capi.SOFTMAX_FWD, 256, 151936, 1
+    d.a_strides[0], d.a_strides[1] = 151936, 1
+    assert L.tpr_softmax_workspace_bytes(ctypes.byref(d)) == 256 * 19 * 8   # split rows
+    assert L.tpr_softmax(ctypes.byref(d), 16, None, 16, None, 0, None) == _capi.ERR_WORKSPACE
+    d.outer = 4096
+    assert L.tpr_softmax_workspace_bytes(ctypes.byref(d)) == 0              # one workgroup per row
+    d.n = 1000
+    assert L.tpr_softmax_workspace_bytes(ctypes.byref(d)) == 0              # register-resident rows
     assert L.tpr_nll_loss_workspace_bytes(1) > 0
     args = [None, _capi.FLOAT32, 4, 3, 3, 1, None, 1, None, 3, -100, None, None, None, None, 0, None]
     assert L.tpr_nll_loss(*args) == _capi.ERR_INVALID_ARG and b"reduction" in L.tpr_last_error()

@@ -26,7 +26,7 @@ torch = pytest.importorskip("torch")
 @pytest.fixture(autouse=True)
 def _reset_knobs():
     yield
-    for k in ("smx_two_pass", "general", "nt"):
+    for k in ("smx_two_pass", "smx_split", "smx_lanes", "general", "nt"):
         _capi.debug_set(k, 0)
 
 
@@ -43,10 +43,21 @@ def check_fwd(base, v, dim, log):
 ROW_NS = [1, 3, 17, 64, 100, 256, 1000, 1001, 1024, 4096, 5000, 16383, 16384, 32768, 32772, 40000, 70001]
 
 
+# (two_pass, split, lanes): automatic; every row through the two-pass kernel with
+# one workgroup per row; through the split (row, chunk) kernels; 512-lane rows
+PLANS = [(0, 0, 0), (1, -1, 0), (1, 1, 0), (0, 0, 512)]
+
+
+def set_plan(plan):
+    _capi.debug_set("smx_two_pass", plan[0])
+    _capi.debug_set("smx_split", plan[1])
+    _capi.debug_set("smx_lanes", plan[2])
+
+
 @pytest.mark.parametrize("log", [False, True])
-@pytest.mark.parametrize("two_pass", [0, 1])
-def test_rows_every_variant(log, two_pass):
-    _capi.debug_set("smx_two_pass", two_pass)
+@pytest.mark.parametrize("plan", PLANS)
+def test_rows_every_variant(log, plan):
+    set_plan(plan)
     rng = np.random.default_rng(11)
     for n in ROW_NS:
         rows = 5 if n > 4096 else 37
@@ -79,12 +90,12 @@ def test_strided_dims(log):
 
 
 @pytest.mark.parametrize("log", [False, True])
-@pytest.mark.parametrize("two_pass", [0, 1])
-def test_nan_inf_slices(log, two_pass):
-    _capi.debug_set("smx_two_pass", two_pass)
+@pytest.mark.parametrize("plan", PLANS[:3])
+def test_nan_inf_slices(log, plan):
+    set_plan(plan)
     inf, nan = np.inf, np.nan
     rng = np.random.default_rng(14)
-    for n in (8, 1000, 3001):
+    for n in (8, 1000, 3001, 20000):
         x = rng.standard_normal((7, n)).astype(np.float32)
         x[0, n // 2] = nan
         x[1, :] = -inf
@@ -105,7 +116,8 @@ def test_large_logits_c5_shape():
     for r in range(256):
         x[r, rng.choice(151936, 8, replace=False)] += 15.0
     t = torch.from_numpy(x).cuda()
-    for log in (False, True):
+    for log, split in ((False, 0), (True, 0), (False, -1)):
+        _capi.debug_set("smx_split", split)
         got = _capi.softmax(t, -1, log=log).cpu().numpy()
         r = softmax_error(got[:32], x[:32].astype(np.float64), 1, log)
         assert r <= 1.0
@@ -163,9 +175,9 @@ def check_bwd(shape, dim, log, seed, view=None):
 
 
 @pytest.mark.parametrize("log", [False, True])
-@pytest.mark.parametrize("two_pass", [0, 1])
-def test_backward_rows(log, two_pass):
-    _capi.debug_set("smx_two_pass", two_pass)
+@pytest.mark.parametrize("plan", PLANS[:3])
+def test_backward_rows(log, plan):
+    set_plan(plan)
     for i, n in enumerate([3, 64, 1000, 1001, 4096, 16384, 20000]):
         check_bwd((6, n), 1, log, 100 + i)
 
