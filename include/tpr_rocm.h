@@ -111,6 +111,24 @@ size_t tpr_reduce_workspace_bytes(const tpr_reduce_desc* desc);
 int tpr_reduce(const tpr_reduce_desc* desc, const void* in, void* out,
                void* workspace, size_t workspace_bytes, void* stream);
 
+/* Gradient of a SUM / MEAN / VAR / STD reduction with respect to its input:
+ * the formulas of /root/reference/config/derivatives.yaml:82-86 (sum, mean)
+ * and :182-186 (var, std), which TensorPlay's autograd composes from expand /
+ * div.Scalar / mul / sub / mean, fused into one pass here:
+ *   SUM:  gx = g;   MEAN: gx = g / count;
+ *   VAR:  gx = (g * 2) * (x - mean) / (count - correction);
+ *   STD:  gx = g * (x - mean) / (result * (count - correction)),
+ * evaluated in float32 in that order (the divisions by count as the
+ * reference's div.Scalar, in double).  `desc` is the forward descriptor (op,
+ * in_dtype = out_dtype = FLOAT32, x's sizes / strides, reduce_mask,
+ * correction, count_override as for tpr_reduce).  grad_out and result (STD
+ * only) are dense over the kept dims, as tpr_reduce writes them; `in` (x) is
+ * read by VAR / STD only; grad_in is written dense row-major over sizes.  VAR
+ * and STD recompute the mean with tpr_reduce into the workspace. */
+size_t tpr_reduce_backward_workspace_bytes(const tpr_reduce_desc* desc);
+int tpr_reduce_backward(const tpr_reduce_desc* desc, const void* grad_out, const void* in, const void* result,
+                        void* grad_in, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Top-k along the last dim of a [rows, cols] view whose rows start
  * row_stride elements apart (elements within a row are contiguous).
  * Outputs are dense [rows, k]: values in the input dtype, indices int64.

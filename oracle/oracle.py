@@ -16,6 +16,8 @@ Parity status of each function (see tests/test_oracle.py):
   softmax_bwd (both modes)              pinned: torch.autograd fp64 gradients of softmax / log_softmax
   nll_loss, nll_loss_backward           pinned: torch.nn.functional.nll_loss (+ autograd) in fp64 with weights,
                                         ignore_index and every reduction; closed form -x[i, t_i]
+  reduce_backward (sum/mean/var/std)    pinned: torch.autograd fp64 gradients of sum / mean / var / std,
+                                        full and along dims, corrections 0 / 1 / 2
   copy                                  pinned: numpy astype on the same views (C casts), brute force on tiny shapes
 """
 import ctypes
@@ -327,3 +329,38 @@ def nll_loss_backward(grad, target, C, weight=None, reduction=1, ignore_index=-1
                                None if w is None else ctypes.c_void_p(w.ctypes.data), reduction, ignore_index,
                                int(has_tw), tw, N, C, ctypes.c_void_p(gi.ctypes.data))
     return gi
+
+
+def reduce_backward(grad, x, op, dims=None, correction=1, result=None):
+    """Gradient of sum / mean / var / std w.r.t. x given the output gradient,
+    restating config/derivatives.yaml:82-86, :182-186 as TensorPlay's autograd
+    evaluates them, op by op in float32:
+      sum:  grad.expand(self.shape())
+      mean: grad.expand(self.shape()) / self.numel()          div.Scalar: (float)(a / (double)n)
+      var:  grad * 2 * (self - self.mean()) / (self.numel() - correction)
+      std:  grad * (self - self.mean()) / (result * (self.numel() - correction))
+    (mul.Scalar by an integer Scalar multiplies in float, ArithmeticKernels.cpp:1469-1491;
+    div.Scalar divides in double, :1502-1532).  dims None / empty = the full
+    reduction; with dims the same formulas apply per output (count = the product
+    of the listed dims' sizes, duplicates included)."""
+    x = np.asarray(x, dtype=np.float32)
+    nd = x.ndim
+    full = not dims
+    rd = list(range(nd)) if full else _wrap_dims(nd, dims)
+    count = int(np.prod([x.shape[d] for d in rd])) if rd else 1
+    kshape = [1 if i in rd else x.shape[i] for i in range(nd)]
+    g = np.asarray(grad, dtype=np.float32).reshape(kshape)
+    if op == "sum":
+        return np.ascontiguousarray(np.broadcast_to(g, x.shape))
+    if op == "mean":
+        return np.ascontiguousarray(np.broadcast_to((g.astype(np.float64) / count).astype(np.float32), x.shape))
+    m = np.asarray(mean(x, None if full else rd, keepdim=True), np.float32).reshape(kshape)
+    if op == "var":
+        t = (g * np.float32(2)) * (x - m)
+        return (t.astype(np.float64) / float(count - correction)).astype(np.float32)
+    if op == "std":
+        r = np.asarray(result, dtype=np.float32).reshape(kshape)
+        t = g * (x - m)
+        with np.errstate(divide="ignore", invalid="ignore"):
+            return t / (r * np.float32(count - correction))
+    raise ValueError(op)

@@ -161,6 +161,22 @@ def _log_softmax_backward_data(grad_output, output, dim):
     return _C._log_softmax_backward_data(grad_output, output, dim)
 
 
+def sum_backward(grad, input, dim=(), keepdim=False):
+    return _C.sum_backward(grad, input, list(dim), keepdim)
+
+
+def mean_backward(grad, input, dim=(), keepdim=False):
+    return _C.mean_backward(grad, input, list(dim), keepdim)
+
+
+def var_backward(grad, input, dim=(), correction=1, keepdim=False):
+    return _C.var_backward(grad, input, list(dim), correction, keepdim)
+
+
+def std_backward(grad, input, result, dim=(), correction=1, keepdim=False):
+    return _C.std_backward(grad, input, result, list(dim), correction, keepdim)
+
+
 _REDUCTION = {"none": 0, "mean": 1, "sum": 2}
 
 

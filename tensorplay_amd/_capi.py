@@ -29,7 +29,7 @@ OP_NAMES = {"sum": SUM, "mean": MEAN, "amax": AMAX, "amin": AMIN, "argmax": ARGM
 EXPORTED = ["tpr_reduce_workspace_bytes", "tpr_reduce", "tpr_topk_workspace_bytes", "tpr_topk",
             "tpr_copy", "tpr_copy_plan", "tpr_copy_strided", "tpr_last_error", "tpr_abi_version",
             "tpr_debug_set", "tpr_softmax", "tpr_softmax_workspace_bytes", "tpr_nll_loss_workspace_bytes", "tpr_nll_loss",
-            "tpr_nll_loss_backward"]
+            "tpr_nll_loss_backward", "tpr_reduce_backward_workspace_bytes", "tpr_reduce_backward"]
 # enum tpr_softmax_mode
 SOFTMAX_FWD, LOG_SOFTMAX_FWD, SOFTMAX_BWD, LOG_SOFTMAX_BWD = range(4)
 # tpr_copy_plan kinds (bits 0-1) and the vector-variant flag (bit 2)
@@ -117,6 +117,10 @@ def lib():
         L.tpr_debug_set.argtypes = [ctypes.c_char_p, i64]
         L.tpr_debug_set.restype = ctypes.c_int
         L.tpr_softmax.argtypes = [ctypes.POINTER(SoftmaxDesc), vp, vp, vp, vp, sz, vp]
+        L.tpr_reduce_backward_workspace_bytes.argtypes = [dp]
+        L.tpr_reduce_backward_workspace_bytes.restype = sz
+        L.tpr_reduce_backward.argtypes = [dp, vp, vp, vp, vp, vp, sz, vp]
+        L.tpr_reduce_backward.restype = ctypes.c_int
         L.tpr_softmax_workspace_bytes.argtypes = [ctypes.POINTER(SoftmaxDesc)]
         L.tpr_softmax_workspace_bytes.restype = sz
         L.tpr_softmax.restype = ctypes.c_int
@@ -370,4 +374,25 @@ def nll_loss_backward(grad, target, n, c, weight=None, reduction=1, ignore_index
                                        ctypes.c_void_p(total_weight.data_ptr() if total_weight is not None else 0),
                                        n, c, reduction, ignore_index, ctypes.c_void_p(gi.data_ptr()),
                                        _stream(torch, gi.device)))
+    return gi
+
+
+def reduce_backward(grad, x, op, dims=None, correction=1, result=None, count_override=0):
+    """Gradient of reduce(x, op, dims) for op in sum / mean / var / std given the
+    output gradient `grad` (dense over the kept dims) and, for std, the forward
+    result.  Returns a dense tensor of x's shape."""
+    import torch
+    nd = x.dim()
+    rd = list(range(nd)) if dims is None else sorted(set((d + nd) if d < 0 else d for d in dims))
+    desc = make_desc(op, list(x.shape), list(x.stride()), rd, FLOAT32, correction, count_override)
+    gi = torch.empty(list(x.shape), dtype=torch.float32, device=x.device)
+    g = grad.contiguous()
+    r = result.contiguous() if result is not None else None
+    L = lib()
+    wsb = L.tpr_reduce_backward_workspace_bytes(ctypes.byref(desc))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
+    _check(L.tpr_reduce_backward(ctypes.byref(desc), ctypes.c_void_p(g.data_ptr()), ctypes.c_void_p(x.data_ptr()),
+                                 ctypes.c_void_p(r.data_ptr() if r is not None else 0),
+                                 ctypes.c_void_p(gi.data_ptr()), ctypes.c_void_p(ws.data_ptr()), wsb,
+                                 _stream(torch, x.device)))
     return gi

@@ -354,6 +354,62 @@ std::tuple<Tensor, Tensor> topk_kernel(const Tensor& self, int64_t k, int64_t di
     return {vals, idx};
 }
 
+// Gradients of sum / mean / var / std (config/derivatives.yaml:82-86,
+// :182-186) as single fused ops.  `dim` empty = the full reduction (the only
+// form derivatives.yaml lists); a dim list gives the same formulas per output.
+// grad: float32 with one element per output (either keepdim shape).
+static Tensor reduce_backward(int op, const char* name, const Tensor& grad, const Tensor& self, const Tensor* result,
+                              const std::vector<int64_t>& dims, int64_t correction) {
+    require_float32_input(self, name);
+    if (grad.dtype() != DType::Float32 || (result && result->dtype() != DType::Float32))
+        TP_THROW(NotImplementedError, std::string(name) + ": float32 only on ROCm");
+    const uint32_t mask = dims.empty() ? all_dims(self) : mask_of(self, dims);
+    int64_t nout = 1;
+    for (int64_t i = 0; i < self.dim(); ++i)
+        if (!((mask >> i) & 1u)) nout *= self.size(i);
+    if (grad.numel() != nout || (result && result->numel() != nout))
+        TP_THROW(RuntimeError, std::string(name) + ": grad has the wrong number of elements");
+    if (!(grad.device() == self.device())) TP_THROW(RuntimeError, std::string(name) + ": tensors on different devices");
+    const Tensor g = grad.contiguous();
+    const Tensor r = result ? result->contiguous() : Tensor();
+    Tensor out = Tensor::empty(self.shape(), DType::Float32, self.device());
+    tpr_reduce_desc d;
+    std::memset(&d, 0, sizeof(d));
+    d.op = op;
+    d.in_dtype = TPR_FLOAT32;
+    d.out_dtype = TPR_FLOAT32;
+    d.ndim = (int32_t)self.dim();
+    for (int i = 0; i < d.ndim; ++i) {
+        d.sizes[i] = self.shape()[i];
+        d.strides[i] = self.strides()[i];
+    }
+    d.reduce_mask = mask;
+    d.correction = correction;
+    d.count_override = dims.empty() ? 0 : listed_count(self, dims);
+    const size_t wsb = tpr_reduce_backward_workspace_bytes(&d);
+    std::shared_ptr<void> ws;
+    if (wsb) ws = allocate(wsb, self.device());
+    DeviceGuard guard(self.device());
+    const int rc = tpr_reduce_backward(&d, g.data_ptr(), self.data_ptr(), result ? r.data_ptr() : nullptr,
+                                       out.data_ptr(), ws.get(), wsb, currentStream(self.device().index));
+    if (rc != TPR_OK) throw_status(rc, name);
+    return out;
+}
+Tensor sum_backward_kernel(const Tensor& grad, const Tensor& self, const std::vector<int64_t>& dims, bool) {
+    return reduce_backward(TPR_SUM, "sum_backward", grad, self, nullptr, dims, 0);
+}
+Tensor mean_backward_kernel(const Tensor& grad, const Tensor& self, const std::vector<int64_t>& dims, bool) {
+    return reduce_backward(TPR_MEAN, "mean_backward", grad, self, nullptr, dims, 0);
+}
+Tensor var_backward_kernel(const Tensor& grad, const Tensor& self, const std::vector<int64_t>& dims, int64_t correction,
+                           bool) {
+    return reduce_backward(TPR_VAR, "var_backward", grad, self, nullptr, dims, correction);
+}
+Tensor std_backward_kernel(const Tensor& grad, const Tensor& self, const Tensor& result,
+                           const std::vector<int64_t>& dims, int64_t correction, bool) {
+    return reduce_backward(TPR_STD, "std_backward", grad, self, &result, dims, correction);
+}
+
 }  // namespace rocm
 
 TENSORPLAY_LIBRARY_IMPL(ROCm, ReductionKernels) {
@@ -382,6 +438,10 @@ TENSORPLAY_LIBRARY_IMPL(ROCm, ReductionKernels) {
     m.impl<Tensor(const Tensor&, double)>("norm", rocm::norm_kernel);
     m.impl<Tensor(const Tensor&, V, double, bool)>("norm.dim", rocm::norm_dim_kernel);
     m.impl<std::tuple<Tensor, Tensor>(const Tensor&, int64_t, int64_t, bool, bool)>("topk", rocm::topk_kernel);
+    m.impl<Tensor(const Tensor&, const Tensor&, V, bool)>("sum_backward", rocm::sum_backward_kernel);
+    m.impl<Tensor(const Tensor&, const Tensor&, V, bool)>("mean_backward", rocm::mean_backward_kernel);
+    m.impl<Tensor(const Tensor&, const Tensor&, V, int64_t, bool)>("var_backward", rocm::var_backward_kernel);
+    m.impl<Tensor(const Tensor&, const Tensor&, const Tensor&, V, int64_t, bool)>("std_backward", rocm::std_backward_kernel);
 }
 
 }  // namespace tensorplay

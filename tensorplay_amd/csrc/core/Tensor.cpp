@@ -364,4 +364,23 @@ Tensor _log_softmax_backward_data(const Tensor& grad_output, const Tensor& outpu
         input_dtype);
 }
 
+using IntList = const std::vector<int64_t>&;
+Tensor sum_backward(const Tensor& grad, const Tensor& self, IntList dim, bool keepdim) {
+    return DispatchStub<Tensor, const Tensor&, const Tensor&, IntList, bool>::call(
+        "sum_backward", computeDispatchKey(self.device()), grad, self, dim, keepdim);
+}
+Tensor mean_backward(const Tensor& grad, const Tensor& self, IntList dim, bool keepdim) {
+    return DispatchStub<Tensor, const Tensor&, const Tensor&, IntList, bool>::call(
+        "mean_backward", computeDispatchKey(self.device()), grad, self, dim, keepdim);
+}
+Tensor var_backward(const Tensor& grad, const Tensor& self, IntList dim, int64_t correction, bool keepdim) {
+    return DispatchStub<Tensor, const Tensor&, const Tensor&, IntList, int64_t, bool>::call(
+        "var_backward", computeDispatchKey(self.device()), grad, self, dim, correction, keepdim);
+}
+Tensor std_backward(const Tensor& grad, const Tensor& self, const Tensor& result, IntList dim, int64_t correction,
+                    bool keepdim) {
+    return DispatchStub<Tensor, const Tensor&, const Tensor&, const Tensor&, IntList, int64_t, bool>::call(
+        "std_backward", computeDispatchKey(self.device()), grad, self, result, dim, correction, keepdim);
+}
+
 }  // namespace tensorplay

@@ -123,6 +123,15 @@ Tensor _softmax_backward_data(const Tensor& grad_output, const Tensor& output, i
 Tensor _log_softmax_backward_data(const Tensor& grad_output, const Tensor& output, int64_t dim,
                                   DType input_dtype = DType::Float32);
 
+// Gradients of sum / mean / var / std (config/derivatives.yaml:82-86, :182-186)
+// as single ops (added by this backend); dim empty = the full reduction.
+Tensor sum_backward(const Tensor& grad, const Tensor& self, const std::vector<int64_t>& dim, bool keepdim);
+Tensor mean_backward(const Tensor& grad, const Tensor& self, const std::vector<int64_t>& dim, bool keepdim);
+Tensor var_backward(const Tensor& grad, const Tensor& self, const std::vector<int64_t>& dim, int64_t correction,
+                    bool keepdim);
+Tensor std_backward(const Tensor& grad, const Tensor& self, const Tensor& result, const std::vector<int64_t>& dim,
+                    int64_t correction, bool keepdim);
+
 // Output shape of a reduction over `dims` (ReductionKernels.cpp:48-70 semantics:
 // negative dims wrap, out-of-range dims raise RuntimeError).
 std::vector<int64_t> reductionShape(const std::vector<int64_t>& shape, const std::vector<int64_t>& dims, bool keepdim);

@@ -248,6 +248,17 @@ PYBIND11_MODULE(_C, m) {
         return nll_loss_backward(g, s, t, w, r, ig, tw.value_or(Tensor()));
     }, py::arg("grad_output"), py::arg("self"), py::arg("target"), py::arg("weight") = py::none(),
        py::arg("reduction") = 1, py::arg("ignore_index") = -100, py::arg("total_weight") = py::none());
+    m.def("sum_backward", [](const Tensor& g, const Tensor& s, const V& d, bool k) { return sum_backward(g, s, d, k); },
+          py::arg("grad"), py::arg("self"), py::arg("dim") = V{}, py::arg("keepdim") = false);
+    m.def("mean_backward", [](const Tensor& g, const Tensor& s, const V& d, bool k) { return mean_backward(g, s, d, k); },
+          py::arg("grad"), py::arg("self"), py::arg("dim") = V{}, py::arg("keepdim") = false);
+    m.def("var_backward", [](const Tensor& g, const Tensor& s, const V& d, int64_t c, bool k) {
+        return var_backward(g, s, d, c, k);
+    }, py::arg("grad"), py::arg("self"), py::arg("dim") = V{}, py::arg("correction") = 1, py::arg("keepdim") = false);
+    m.def("std_backward", [](const Tensor& g, const Tensor& s, const Tensor& r, const V& d, int64_t c, bool k) {
+        return std_backward(g, s, r, d, c, k);
+    }, py::arg("grad"), py::arg("self"), py::arg("result"), py::arg("dim") = V{}, py::arg("correction") = 1,
+       py::arg("keepdim") = false);
     m.def("_softmax_backward_data", [](const Tensor& g, const Tensor& y, int64_t d) {
         return _softmax_backward_data(g, y, d, DType::Float32);
     }, py::arg("grad_output"), py::arg("output"), py::arg("dim"));

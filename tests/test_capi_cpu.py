@@ -85,9 +85,9 @@ def test_softmax_loss_validation_without_gpu():
     assert L.tpr_softmax(ctypes.byref(d), None, None, None, None, 0, None) == _capi.OK  # empty: no launch
     d.n, d.mode = 3, _capi.SOFTMAX_BWD
     assert L.tpr_softmax(ctypes.byref(d), 16, None, 16, None, 0, None) == _capi.ERR_INVALID_ARG  # y missing
-    d.mode, d.outer, d.n, d.inner = _capi.SOFTMAX_FWD, 256, 151936, 1
+    d.mode, d.outer, d.n, d.inner = _capi.SOFTMAX_FWD, 64, 151936, 1
     d.a_strides[0], d.a_strides[1] = 151936, 1
-    assert L.tpr_softmax_workspace_bytes(ctypes.byref(d)) == 256 * 19 * 8   # split rows
+    assert L.tpr_softmax_workspace_bytes(ctypes.byref(d)) == 64 * 19 * 8    # few long rows: split
     assert L.tpr_softmax(ctypes.byref(d), 16, None, 16, None, 0, None) == _capi.ERR_WORKSPACE
     d.outer = 4096
     assert L.tpr_softmax_workspace_bytes(ctypes.byref(d)) == 0              # one workgroup per row
