@@ -144,6 +144,24 @@ def nll_bwd_call(torch, capi, n, c, target, g, tw, stream):
     return call
 
 
+def reduce_bwd_call(torch, capi, x, op, dims, stream, g, res=None):
+    nd = x.dim()
+    rd = list(range(nd)) if dims is None else sorted(set((d + nd) % nd for d in dims))
+    desc = capi.make_desc(op, list(x.shape), list(x.stride()), rd, capi.FLOAT32, 1)
+    gi = torch.empty(list(x.shape), dtype=torch.float32, device=x.device)
+    L = capi.lib()
+    wsb = L.tpr_reduce_backward_workspace_bytes(ctypes.byref(desc))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
+    c = Call(L.tpr_reduce_backward, (ctypes.byref(desc), ctypes.c_void_p(g.data_ptr()), ctypes.c_void_p(x.data_ptr()),
+                                     ctypes.c_void_p(res.data_ptr() if res is not None else 0),
+                                     ctypes.c_void_p(gi.data_ptr()), ctypes.c_void_p(ws.data_ptr()), wsb, stream))
+    c.keep = (desc, gi, ws, g, res)
+    # algorithmic bytes: write the gradient; var / std also read x twice (the mean's
+    # reduction pass and the gradient pass), as the mean is not an input
+    c.bytes = x.numel() * 4 * (3 if op in ("var", "std") else 1)
+    return c
+
+
 def rate(ms, by):
     return {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1), "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4),
             "alg_bytes": by}
@@ -360,6 +378,19 @@ def main():
                          "kernel": copy_kernel_name(capi.copy_plan(outs[0], view(bufs[0])))}
             del outs, cc
         extras["copy_C2_64x1024x1024"] = ecp
+        # gradients of the C2 reductions (var / std over dim=-1, mean over dim=1) and of a full sum
+        erb = {}
+        for op, dims in (("var", [-1]), ("std", [-1]), ("mean", [1]), ("sum", None)):
+            nd = 3
+            rd = list(range(nd)) if dims is None else [d % nd for d in dims]
+            kept = [bufs[0].shape[i] for i in range(nd) if i not in rd]
+            g = torch.randn(kept, device=dev)
+            res = torch.rand(kept, device=dev) + 0.5 if op == "std" else None
+            cs = [reduce_bwd_call(torch, capi, bufs[i], op, dims, stream, g, res) for i in range(nbuf)]
+            ms = time_calls(torch, cs, max(steps, 9), warmup)
+            erb[f"{op}_backward_dim{'' if dims is None else dims[0]}"] = rate(ms, cs[0].bytes)
+            del cs
+        extras["reduce_backward_C2_64x1024x1024"] = erb
         # softmax over the middle (strided) dim of the C2 geometry
         cs = [softmax_call(torch, capi, bufs[i], 1, capi.SOFTMAX_FWD, stream) for i in range(2)]
         ms = time_calls(torch, cs, max(steps, 8), warmup)

@@ -124,7 +124,8 @@ int tpr_reduce(const tpr_reduce_desc* desc, const void* in, void* out,
  * correction, count_override as for tpr_reduce).  grad_out and result (STD
  * only) are dense over the kept dims, as tpr_reduce writes them; `in` (x) is
  * read by VAR / STD only; grad_in is written dense row-major over sizes.  VAR
- * and STD recompute the mean with tpr_reduce into the workspace. */
+ * and STD recompute the mean with tpr_reduce into the workspace; MEAN divides
+ * grad_out by the count there, once per output. */
 size_t tpr_reduce_backward_workspace_bytes(const tpr_reduce_desc* desc);
 int tpr_reduce_backward(const tpr_reduce_desc* desc, const void* grad_out, const void* in, const void* result,
                         void* grad_in, void* workspace, size_t workspace_bytes, void* stream);

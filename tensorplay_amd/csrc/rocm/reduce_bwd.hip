@@ -30,8 +30,30 @@
 namespace tpr {
 namespace {
 
+// Division of a 32-bit index by an invariant divisor d >= 1 as a multiply-high
+// (Granlund & Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, unsigned case): with l = ceil(log2 d) and
+// m = floor(2^32 (2^l - d) / d) + 1, n / d = (umulhi(n, m) + n) >> l for every
+// n < 2^32 (the sum is formed in 64 bits).
+struct FastDiv {
+    unsigned m;
+    unsigned l;
+};
+
+FastDiv make_fastdiv(unsigned long long d) {
+    unsigned l = 0;
+    while ((1ULL << l) < d) ++l;
+    const unsigned long long m = (((1ULL << 32) * ((1ULL << l) - d)) / d) + 1;
+    return FastDiv{(unsigned)m, l};
+}
+
+__device__ __forceinline__ unsigned fastdiv(unsigned n, FastDiv f) {
+    return (unsigned)(((unsigned long long)__umulhi(n, f.m) + n) >> f.l);
+}
+
 struct RbArgs {
     int nd;
+    FastDiv fd[TPR_MAX_DIMS];
     long long sizes[TPR_MAX_DIMS];
     long long xs[TPR_MAX_DIMS];  // input strides (elements)
     long long os[TPR_MAX_DIMS];  // per-output value strides (0 on reduced dims)
@@ -54,7 +76,7 @@ __device__ __forceinline__ float bwd_value(const RbArgs& a, long long xo, long l
     if constexpr (OP == B_SUM) {
         return g;
     } else if constexpr (OP == B_MEAN) {
-        return (float)((double)g / a.count);
+        return g;  // divided by count per output beforehand (k_mean_scale)
     } else if constexpr (OP == B_VAR) {
         const float t = (g * 2.0f) * (a.x[xo] - a.mean[so]);
         return (float)((double)t / a.denom);
@@ -76,8 +98,11 @@ __global__ __launch_bounds__(256) void k_red_bwd(RbArgs a) {
         long long xo = 0, so = 0;
         for (int d = last; d >= 0; --d) {
             const IdxT sz = (IdxT)a.sizes[d];
-            const IdxT c = e % sz;
-            e /= sz;
+            IdxT q;
+            if constexpr (sizeof(IdxT) == 4) q = fastdiv(e, a.fd[d]);
+            else q = e / sz;
+            const IdxT c = e - q * sz;
+            e = q;
             xo += (long long)c * a.xs[d];
             so += (long long)c * a.os[d];
         }
@@ -95,8 +120,147 @@ __global__ __launch_bounds__(256) void k_red_bwd(RbArgs a) {
     }
 }
 
+// Rows of the innermost merged dim (at least 1024 elements): a workgroup
+// covers 256 * VEC * 4 consecutive outputs of one row (long rows, split in
+// `chunks` pieces) or of rpb = CH / L whole rows (short rows).  The first rpb
+// threads find the rows' offsets once (into LDS); every thread then issues the
+// loads of its four vectors before any store, so short rows do not serialise
+// on load latency.  INNER: 0 = the innermost dim is reduced (g / mean / result
+// are one value per row), 1 = it is kept with unit stride in the per-output
+// arrays (loaded as vectors beside x).
+template <int OP, int VEC, int INNER>
+__global__ __launch_bounds__(256) void k_red_bwd_rows(RbArgs a, long long chunks, int rpb, long long rows) {
+    constexpr int CH = 256 * VEC * 4;
+    constexpr bool XS = OP == B_VAR || OP == B_STD;
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    __shared__ long long sxo[4], sso[4];
+    const int last = a.nd - 1;
+    const long long L = a.sizes[last];
+    const long long grp = blockIdx.x / chunks;
+    const long long c0 = (blockIdx.x - grp * chunks) * (long long)CH;
+    const int t = threadIdx.x;
+    if (t < rpb) {
+        long long xo = 0, so = 0, r = grp * rpb + t;
+        if (r < rows) {
+            for (int d = last - 1; d >= 0; --d) {
+                const long long c = r % a.sizes[d];
+                r /= a.sizes[d];
+                xo += c * a.xs[d];
+                so += c * a.os[d];
+            }
+        }
+        sxo[t] = xo;
+        sso[t] = so;
+    }
+    __syncthreads();
+    const long long xs = a.xs[last];
+
+    float gv[4][VEC], mv[4][VEC], rv[4][VEC], xv[4][VEC];
+    long long oo[4];  // output offset of each vector, -1 = none
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const long long e = c0 + ((long long)u * 256 + t) * VEC;
+        const long long rr = e / L;
+        const long long i = e - rr * L;
+        const long long row = grp * rpb + rr;
+        oo[u] = -1;
+        if (rr >= rpb || row >= rows) continue;
+        oo[u] = row * L + i;
+        const long long xo = sxo[rr], so = sso[rr];
+        if constexpr (INNER == 0) {
+            const float g1 = a.g[so];
+            const float m1 = XS ? a.mean[so] : 0.0f;
+            const float r1 = OP == B_STD ? a.res[so] : 0.0f;
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) {
+                gv[u][k] = g1;
+                mv[u][k] = m1;
+                rv[u][k] = r1;
+            }
+        } else if constexpr (VEC == 4) {
+            const f32x4 q = *reinterpret_cast<const f32x4*>(a.g + so + i);
+            gv[u][0] = q.x; gv[u][1] = q.y; gv[u][2] = q.z; gv[u][3] = q.w;
+            if constexpr (XS) {
+                const f32x4 w = *reinterpret_cast<const f32x4*>(a.mean + so + i);
+                mv[u][0] = w.x; mv[u][1] = w.y; mv[u][2] = w.z; mv[u][3] = w.w;
+            }
+            if constexpr (OP == B_STD) {
+                const f32x4 w = *reinterpret_cast<const f32x4*>(a.res + so + i);
+                rv[u][0] = w.x; rv[u][1] = w.y; rv[u][2] = w.z; rv[u][3] = w.w;
+            }
+        } else {
+            gv[u][0] = a.g[so + i];
+            if constexpr (XS) mv[u][0] = a.mean[so + i];
+            if constexpr (OP == B_STD) rv[u][0] = a.res[so + i];
+        }
+        if constexpr (XS) {
+            if (VEC == 4 && xs == 1) {
+                const f32x4 w = *reinterpret_cast<const f32x4*>(a.x + xo + i);
+                xv[u][0] = w.x; xv[u][1] = w.y; xv[u][2] = w.z; xv[u][3] = w.w;
+            } else {
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) xv[u][k] = a.x[xo + (i + k) * xs];
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        if (oo[u] < 0) continue;
+        float o[VEC];
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+            if constexpr (OP == B_SUM || OP == B_MEAN) {
+                o[k] = gv[u][k];  // MEAN: g was divided by count per output beforehand
+            } else if constexpr (OP == B_VAR) {
+                const float tt = (gv[u][k] * 2.0f) * (xv[u][k] - mv[u][k]);
+                o[k] = (float)((double)tt / a.denom);
+            } else {
+                const float tt = gv[u][k] * (xv[u][k] - mv[u][k]);
+                o[k] = tt / (rv[u][k] * a.denom_f);
+            }
+        }
+        if constexpr (VEC == 4) {
+            f32x4 w = {o[0], o[1], o[2], o[3]};
+            __builtin_nontemporal_store(w, reinterpret_cast<f32x4*>(a.gi + oo[u]));
+        } else {
+            __builtin_nontemporal_store(o[0], a.gi + oo[u]);
+        }
+    }
+}
+
+// MEAN: q[o] = (float)((double)g[o] / count) once per output (the gradient is
+// then a broadcast of q, as for SUM).
+__global__ __launch_bounds__(256) void k_mean_scale(const float* g, float* q, long long n, double count) {
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256)
+        q[i] = (float)((double)g[i] / count);
+}
+
 template <int OP>
 int launch_bwd(const RbArgs& a, hipStream_t st) {
+    const long long L = a.sizes[a.nd - 1];
+    const long long os = a.os[a.nd - 1];
+    if (L >= 1024 && (os == 0 || os == 1)) {
+        auto al = [](const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+        // vectors: whole 16-byte groups on every side that is read or written per element
+        const bool v4 = L % 4 == 0 && al(a.gi) && (a.xs[a.nd - 1] != 1 || al(a.x)) &&
+                        (os == 0 || (al(a.g) && al(a.mean) && al(a.res)));
+        const long long ch = 256LL * (v4 ? 4 : 1) * 4;
+        const long long chunks = (L + ch - 1) / ch;
+        const long long rows = a.total / L;
+        const int rpb = L < ch ? (int)(ch / L) : 1;  // short rows: several per workgroup
+        const long long blocks = (rows + rpb - 1) / rpb * chunks;
+        if (blocks <= 0x7fffffffLL) {
+            const dim3 gr((unsigned)blocks), bl(256);
+            if (os == 0) {
+                if (v4) hipLaunchKernelGGL((k_red_bwd_rows<OP, 4, 0>), gr, bl, 0, st, a, chunks, rpb, rows);
+                else hipLaunchKernelGGL((k_red_bwd_rows<OP, 1, 0>), gr, bl, 0, st, a, chunks, rpb, rows);
+            } else {
+                if (v4) hipLaunchKernelGGL((k_red_bwd_rows<OP, 4, 1>), gr, bl, 0, st, a, chunks, rpb, rows);
+                else hipLaunchKernelGGL((k_red_bwd_rows<OP, 1, 1>), gr, bl, 0, st, a, chunks, rpb, rows);
+            }
+            return check_launch("tpr_reduce_backward");
+        }
+    }
     const bool v4 = a.sizes[a.nd - 1] % 4 == 0 && (reinterpret_cast<uintptr_t>(a.gi) & 15) == 0;
     const long long nvec = a.total / (v4 ? 4 : 1);
     long long blocks = (nvec + 255) / 256;
@@ -104,12 +268,14 @@ int launch_bwd(const RbArgs& a, hipStream_t st) {
     if (blocks > cap) blocks = cap;
     if (blocks < 1) blocks = 1;
     const bool small = a.total < (1LL << 31);
+    RbArgs b = a;
+    for (int d = 0; d < a.nd; ++d) b.fd[d] = make_fastdiv((unsigned long long)a.sizes[d]);
     if (v4) {
-        if (small) hipLaunchKernelGGL((k_red_bwd<OP, 4, unsigned>), dim3((unsigned)blocks), dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_red_bwd<OP, 4, long long>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+        if (small) hipLaunchKernelGGL((k_red_bwd<OP, 4, unsigned>), dim3((unsigned)blocks), dim3(256), 0, st, b);
+        else hipLaunchKernelGGL((k_red_bwd<OP, 4, long long>), dim3((unsigned)blocks), dim3(256), 0, st, b);
     } else {
-        if (small) hipLaunchKernelGGL((k_red_bwd<OP, 1, unsigned>), dim3((unsigned)blocks), dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_red_bwd<OP, 1, long long>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+        if (small) hipLaunchKernelGGL((k_red_bwd<OP, 1, unsigned>), dim3((unsigned)blocks), dim3(256), 0, st, b);
+        else hipLaunchKernelGGL((k_red_bwd<OP, 1, long long>), dim3((unsigned)blocks), dim3(256), 0, st, b);
     }
     return check_launch("tpr_reduce_backward");
 }
@@ -140,6 +306,7 @@ uint32_t full_mask(const tpr_reduce_desc* d) { return d->ndim == 0 ? 0u : ((1u <
 extern "C" size_t tpr_reduce_backward_workspace_bytes(const tpr_reduce_desc* d) {
     using namespace tpr;
     if (!d || d->ndim < 0 || d->ndim > TPR_MAX_DIMS) return 0;
+    if (d->op == TPR_MEAN) return align256((size_t)kept_count(d) * sizeof(float));
     if (d->op != TPR_VAR && d->op != TPR_STD) return 0;
     const tpr_reduce_desc m = mean_desc(d);
     return align256((size_t)kept_count(d) * sizeof(float)) + tpr_reduce_workspace_bytes(&m);
@@ -180,6 +347,19 @@ extern "C" int tpr_reduce_backward(const tpr_reduce_desc* d, const void* grad_ou
     a.denom = (double)(count - d->correction);
     a.denom_f = (float)(count - d->correction);
 
+    if (d->op == TPR_MEAN) {
+        const size_t need = tpr_reduce_backward_workspace_bytes(d);
+        if (!workspace || workspace_bytes < need)
+            return fail(TPR_ERR_WORKSPACE, "tpr_reduce_backward: workspace smaller than tpr_reduce_backward_workspace_bytes");
+        const long long nout = kept_count(d);
+        long long blocks = (nout + 255) / 256;
+        if (blocks > 4096) blocks = 4096;
+        float* q = static_cast<float*>(workspace);
+        hipLaunchKernelGGL(k_mean_scale, dim3((unsigned)blocks), dim3(256), 0, st, a.g, q, nout, a.count);
+        const int rc = check_launch("tpr_reduce_backward (mean scale)");
+        if (rc != TPR_OK) return rc;
+        a.g = q;
+    }
     if (d->op == TPR_VAR || d->op == TPR_STD) {
         const size_t need = tpr_reduce_backward_workspace_bytes(d);
         if (!workspace || workspace_bytes < need)

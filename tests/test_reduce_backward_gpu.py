@@ -48,7 +48,8 @@ def test_shapes_and_layouts(op):
     rng = np.random.default_rng(7)
     cases = []
     for shape, dims in [((1000,), None), ((33, 65), [1]), ((33, 65), [0]), ((4, 5, 6), [0, 2]), ((4, 5, 6), [1]),
-                        ((4, 5, 6), None), ((7, 3, 2, 5), [-1, 1]), ((64, 1024), [1]), ((1, 3, 1), [1])]:
+                        ((4, 5, 6), None), ((7, 3, 2, 5), [-1, 1]), ((64, 1024), [1]), ((1, 3, 1), [1]),
+                        ((3, 1500), [0]), ((5, 2048), [0]), ((5, 3, 2048), [1]), ((2, 9000), [0])]:
         b = (rng.standard_normal(shape) * 2 + 0.5).astype(np.float32)
         cases.append((b, b, dims))
     b = (rng.standard_normal((40, 64)) + 1).astype(np.float32)
