@@ -162,6 +162,20 @@ def reduce_bwd_call(torch, capi, x, op, dims, stream, g, res=None):
     return c
 
 
+def sample_call(torch, capi, x, k, temperature, top_p, u, stream):
+    rows, cols = x.shape
+    out = torch.empty((rows,), dtype=torch.int64, device=x.device)
+    L = capi.lib()
+    wsb = L.tpr_sample_workspace_bytes(capi.FLOAT32, rows, cols, k)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
+    c = Call(L.tpr_sample, (ctypes.c_void_p(x.data_ptr()), capi.FLOAT32, rows, cols, x.stride(0), k,
+                            ctypes.c_float(temperature), ctypes.c_float(top_p), ctypes.c_void_p(u.data_ptr()),
+                            ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ws.data_ptr()), wsb, stream))
+    c.keep = (out, ws, u)
+    c.bytes = x.numel() * 4 + rows * 12
+    return c
+
+
 def rate(ms, by):
     return {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1), "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4),
             "alg_bytes": by}
@@ -339,6 +353,12 @@ def main():
         by = 256 * 151936 * 4 + c5a[0].out_bytes
         e5["argmax_dim-1"] = {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
                               "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        # top-k (k=50) -> top-p (0.9) sampling of one token per row, T = 0.7
+        uu = torch.rand((256,), device=dev)
+        cs = [sample_call(torch, capi, b, 50, 0.7, 0.9, uu, stream) for b in b5]
+        ms = time_calls(torch, cs, max(steps, 10), warmup)
+        e5["sample_topk50_topp0.9"] = dict(rate(ms, cs[0].bytes), rows_per_s=round(256 / (ms * 1e-3), 1))
+        del cs
         extras["C5_logits_256x151936"] = e5
         # softmax family on the same logits: softmax / log_softmax forward (read + write), softmax
         # backward (read g and y, write the gradient), and nll_loss backward (write [256, 151936])

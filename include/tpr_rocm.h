@@ -146,6 +146,22 @@ int tpr_topk(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t 
              int64_t k, int32_t largest, int32_t sorted, void* out_values, void* out_indices,
              void* workspace, size_t workspace_bytes, void* stream);
 
+/* Top-k / top-p (nucleus) sampling of one token id per row of float32 logits
+ * (a consumer of tpr_topk; TensorPlay has no sampler, so the definition is
+ * this build's): for the k largest logits of a row, sorted v_0 >= ... >=
+ * v_{k-1} (ties to the lowest index, as tpr_topk),
+ *   p_j = exp(v_j / T - v_0 / T),  c_j = p_0 + ... + p_j,
+ *   m   = the first j with c_j >= top_p * c_{k-1},
+ *   out = the column index of the first j <= m with c_j > u * c_m,
+ * with u = uniforms[row] in [0, 1) (device float32 [rows], drawn by the
+ * caller).  temperature <= 0 selects v_0 (greedy).  top_p in (0, 1], 1 <= k <=
+ * min(cols, 1024).  out_ids: device int64 [rows].  Workspace:
+ * tpr_sample_workspace_bytes (the candidates plus tpr_topk's). */
+size_t tpr_sample_workspace_bytes(int32_t dtype, int64_t rows, int64_t cols, int64_t k);
+int tpr_sample(const void* logits, int32_t dtype, int64_t rows, int64_t cols, int64_t row_stride, int64_t k,
+               float temperature, float top_p, const float* uniforms, int64_t* out_ids, void* workspace,
+               size_t workspace_bytes, void* stream);
+
 /* Strided, casting copy: dst[idx] = static_cast<dst_dtype>(src[idx]) for
  * every index of sizes[0..ndim).  Strides are in elements, per side; a
  * stride-0 source dim broadcasts.  Replaces DispatchStub::call("copy_",

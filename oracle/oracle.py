@@ -18,6 +18,8 @@ Parity status of each function (see tests/test_oracle.py):
                                         ignore_index and every reduction; closed form -x[i, t_i]
   reduce_backward (sum/mean/var/std)    pinned: torch.autograd fp64 gradients of sum / mean / var / std,
                                         full and along dims, corrections 0 / 1 / 2
+  sample (top-k / top-p)                pinned: inverse-CDF over the full softmax when k = cols and top_p = 1;
+                                        argmax when k = 1 or T <= 0; brute-force frequencies over a grid of u
   copy                                  pinned: numpy astype on the same views (C casts), brute force on tiny shapes
 """
 import ctypes
@@ -364,3 +366,35 @@ def reduce_backward(grad, x, op, dims=None, correction=1, result=None):
         with np.errstate(divide="ignore", invalid="ignore"):
             return t / (r * np.float32(count - correction))
     raise ValueError(op)
+
+
+def sample(x2d, u, k, temperature=1.0, top_p=1.0):
+    """Top-k / top-p sampling (this build's definition; TensorPlay has none):
+    the k largest logits per row (topk order: descending, ties to the lowest
+    index), p_j = exp(v_j/T - v_0/T), c_j = cumulative sums, nucleus 0..m with m
+    the first j where c_j >= top_p * c_{k-1}, then the first j <= m with
+    c_j > u * c_m.  T <= 0 is greedy.  Computed in float64.
+    Returns (ids, margin): margin is the smallest relative distance of the two
+    decision thresholds (top_p cut, u draw) to a cumulative sum -- where it is
+    below the float32 rounding of the GPU's sums, either neighbour is a valid
+    draw."""
+    x2d = np.asarray(x2d, np.float32)
+    rows = x2d.shape[0]
+    vals, idx = topk(x2d, k)
+    if not temperature > 0:
+        return idx[:, 0].copy(), np.full(rows, np.inf)
+    ids = np.empty(rows, np.int64)
+    margin = np.empty(rows)
+    for r in range(rows):
+        z = vals[r].astype(np.float64) / temperature
+        p = np.exp(z - z[0])
+        c = np.cumsum(p)
+        cut = top_p * c[-1]
+        hit = np.nonzero(c >= cut)[0]
+        m = int(hit[0]) if hit.size else k - 1
+        thr = float(u[r]) * c[m]
+        hit = np.nonzero(c[: m + 1] > thr)[0]
+        j = int(hit[0]) if hit.size else m
+        ids[r] = idx[r, j]
+        margin[r] = min(np.min(np.abs(c - cut)) / c[-1], np.min(np.abs(c[: m + 1] - thr)) / c[m])
+    return ids, margin

@@ -161,6 +161,11 @@ def _log_softmax_backward_data(grad_output, output, dim):
     return _C._log_softmax_backward_data(grad_output, output, dim)
 
 
+def topk_topp_sample(input, uniforms, k=50, temperature=1.0, top_p=1.0):
+    """One token id per row of the last dim: top-k, then the top-p nucleus, drawn with `uniforms`."""
+    return _C.topk_topp_sample(input, uniforms, k, temperature, top_p)
+
+
 def sum_backward(grad, input, dim=(), keepdim=False):
     return _C.sum_backward(grad, input, list(dim), keepdim)
 

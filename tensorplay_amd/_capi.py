@@ -29,7 +29,8 @@ OP_NAMES = {"sum": SUM, "mean": MEAN, "amax": AMAX, "amin": AMIN, "argmax": ARGM
 EXPORTED = ["tpr_reduce_workspace_bytes", "tpr_reduce", "tpr_topk_workspace_bytes", "tpr_topk",
             "tpr_copy", "tpr_copy_plan", "tpr_copy_strided", "tpr_last_error", "tpr_abi_version",
             "tpr_debug_set", "tpr_softmax", "tpr_softmax_workspace_bytes", "tpr_nll_loss_workspace_bytes", "tpr_nll_loss",
-            "tpr_nll_loss_backward", "tpr_reduce_backward_workspace_bytes", "tpr_reduce_backward"]
+            "tpr_nll_loss_backward", "tpr_reduce_backward_workspace_bytes", "tpr_reduce_backward",
+            "tpr_sample_workspace_bytes", "tpr_sample"]
 # enum tpr_softmax_mode
 SOFTMAX_FWD, LOG_SOFTMAX_FWD, SOFTMAX_BWD, LOG_SOFTMAX_BWD = range(4)
 # tpr_copy_plan kinds (bits 0-1) and the vector-variant flag (bit 2)
@@ -121,6 +122,10 @@ def lib():
         L.tpr_reduce_backward_workspace_bytes.restype = sz
         L.tpr_reduce_backward.argtypes = [dp, vp, vp, vp, vp, vp, sz, vp]
         L.tpr_reduce_backward.restype = ctypes.c_int
+        L.tpr_sample_workspace_bytes.argtypes = [i32, i64, i64, i64]
+        L.tpr_sample_workspace_bytes.restype = sz
+        L.tpr_sample.argtypes = [vp, i32, i64, i64, i64, i64, ctypes.c_float, ctypes.c_float, vp, vp, vp, sz, vp]
+        L.tpr_sample.restype = ctypes.c_int
         L.tpr_softmax_workspace_bytes.argtypes = [ctypes.POINTER(SoftmaxDesc)]
         L.tpr_softmax_workspace_bytes.restype = sz
         L.tpr_softmax.restype = ctypes.c_int
@@ -396,3 +401,20 @@ def reduce_backward(grad, x, op, dims=None, correction=1, result=None, count_ove
                                  ctypes.c_void_p(gi.data_ptr()), ctypes.c_void_p(ws.data_ptr()), wsb,
                                  _stream(torch, x.device)))
     return gi
+
+
+def sample(logits2d, uniforms, k, temperature=1.0, top_p=1.0):
+    """One token id per row of a 2-D float32 device tensor (unit inner stride)
+    through tpr_sample; uniforms: float32 device tensor [rows] in [0, 1)."""
+    import torch
+    rows, cols = logits2d.shape
+    out = torch.empty((rows,), dtype=torch.int64, device=logits2d.device)
+    L = lib()
+    wsb = L.tpr_sample_workspace_bytes(FLOAT32, rows, cols, k)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=logits2d.device)
+    u = uniforms.contiguous()
+    _check(L.tpr_sample(ctypes.c_void_p(logits2d.data_ptr()), FLOAT32, rows, cols, logits2d.stride(0), k,
+                        float(temperature), float(top_p), ctypes.c_void_p(u.data_ptr()),
+                        ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ws.data_ptr()), wsb,
+                        _stream(torch, logits2d.device)))
+    return out

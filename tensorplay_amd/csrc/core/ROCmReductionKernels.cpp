@@ -354,6 +354,35 @@ std::tuple<Tensor, Tensor> topk_kernel(const Tensor& self, int64_t k, int64_t di
     return {vals, idx};
 }
 
+// topk_topp_sample(Tensor self, Tensor uniforms, int64_t k=50, double temperature=1.0,
+//                  double top_p=1.0) -> Tensor
+// New schema (TensorPlay has no sampler): one token id (Int64) per row of the
+// last dim of float32 logits, drawn from the top-k / top-p nucleus with the
+// caller's uniforms (one per row, in [0, 1)); definition in include/tpr_rocm.h.
+Tensor topk_topp_sample_kernel(const Tensor& self, const Tensor& uniforms, int64_t k, double temperature,
+                               double top_p) {
+    require_float32_input(self, "topk_topp_sample");
+    if (self.dim() == 0) TP_THROW(RuntimeError, "topk_topp_sample: logits need at least one dim");
+    if (uniforms.dtype() != DType::Float32) TP_THROW(NotImplementedError, "topk_topp_sample: uniforms must be float32");
+    const int64_t n = self.size(-1);
+    std::vector<int64_t> lead(self.shape().begin(), self.shape().end() - 1);
+    int64_t rows = 1;
+    for (auto s : lead) rows *= s;
+    if (uniforms.numel() != rows) TP_THROW(RuntimeError, "topk_topp_sample: one uniform per row expected");
+    const Tensor x = self.contiguous();
+    const Tensor u = uniforms.contiguous();
+    Tensor out = Tensor::empty(lead, DType::Int64, self.device());
+    const size_t wsb = tpr_sample_workspace_bytes(TPR_FLOAT32, rows, n, k);
+    std::shared_ptr<void> ws;
+    if (wsb) ws = allocate(wsb, self.device());
+    DeviceGuard guard(self.device());
+    const int rc = tpr_sample(x.data_ptr(), TPR_FLOAT32, rows, n, n, k, (float)temperature, (float)top_p,
+                              static_cast<const float*>(u.data_ptr()), static_cast<int64_t*>(out.data_ptr()), ws.get(),
+                              wsb, currentStream(self.device().index));
+    if (rc != TPR_OK) throw_status(rc, "topk_topp_sample");
+    return out;
+}
+
 // Gradients of sum / mean / var / std (config/derivatives.yaml:82-86,
 // :182-186) as single fused ops.  `dim` empty = the full reduction (the only
 // form derivatives.yaml lists); a dim list gives the same formulas per output.
@@ -438,6 +467,7 @@ TENSORPLAY_LIBRARY_IMPL(ROCm, ReductionKernels) {
     m.impl<Tensor(const Tensor&, double)>("norm", rocm::norm_kernel);
     m.impl<Tensor(const Tensor&, V, double, bool)>("norm.dim", rocm::norm_dim_kernel);
     m.impl<std::tuple<Tensor, Tensor>(const Tensor&, int64_t, int64_t, bool, bool)>("topk", rocm::topk_kernel);
+    m.impl<Tensor(const Tensor&, const Tensor&, int64_t, double, double)>("topk_topp_sample", rocm::topk_topp_sample_kernel);
     m.impl<Tensor(const Tensor&, const Tensor&, V, bool)>("sum_backward", rocm::sum_backward_kernel);
     m.impl<Tensor(const Tensor&, const Tensor&, V, bool)>("mean_backward", rocm::mean_backward_kernel);
     m.impl<Tensor(const Tensor&, const Tensor&, V, int64_t, bool)>("var_backward", rocm::var_backward_kernel);

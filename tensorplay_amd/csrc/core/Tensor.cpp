@@ -364,6 +364,10 @@ Tensor _log_softmax_backward_data(const Tensor& grad_output, const Tensor& outpu
         input_dtype);
 }
 
+Tensor topk_topp_sample(const Tensor& self, const Tensor& uniforms, int64_t k, double temperature, double top_p) {
+    return DispatchStub<Tensor, const Tensor&, const Tensor&, int64_t, double, double>::call(
+        "topk_topp_sample", computeDispatchKey(self.device()), self, uniforms, k, temperature, top_p);
+}
 using IntList = const std::vector<int64_t>&;
 Tensor sum_backward(const Tensor& grad, const Tensor& self, IntList dim, bool keepdim) {
     return DispatchStub<Tensor, const Tensor&, const Tensor&, IntList, bool>::call(

@@ -123,6 +123,10 @@ Tensor _softmax_backward_data(const Tensor& grad_output, const Tensor& output, i
 Tensor _log_softmax_backward_data(const Tensor& grad_output, const Tensor& output, int64_t dim,
                                   DType input_dtype = DType::Float32);
 
+// Top-k / top-p sampling of one Int64 id per row of the last dim (added by this
+// backend; TensorPlay has no sampler).
+Tensor topk_topp_sample(const Tensor& self, const Tensor& uniforms, int64_t k = 50, double temperature = 1.0,
+                        double top_p = 1.0);
 // Gradients of sum / mean / var / std (config/derivatives.yaml:82-86, :182-186)
 // as single ops (added by this backend); dim empty = the full reduction.
 Tensor sum_backward(const Tensor& grad, const Tensor& self, const std::vector<int64_t>& dim, bool keepdim);

@@ -248,6 +248,9 @@ PYBIND11_MODULE(_C, m) {
         return nll_loss_backward(g, s, t, w, r, ig, tw.value_or(Tensor()));
     }, py::arg("grad_output"), py::arg("self"), py::arg("target"), py::arg("weight") = py::none(),
        py::arg("reduction") = 1, py::arg("ignore_index") = -100, py::arg("total_weight") = py::none());
+    m.def("topk_topp_sample", [](const Tensor& s, const Tensor& u, int64_t k, double t, double p) {
+        return topk_topp_sample(s, u, k, t, p);
+    }, py::arg("self"), py::arg("uniforms"), py::arg("k") = 50, py::arg("temperature") = 1.0, py::arg("top_p") = 1.0);
     m.def("sum_backward", [](const Tensor& g, const Tensor& s, const V& d, bool k) { return sum_backward(g, s, d, k); },
           py::arg("grad"), py::arg("self"), py::arg("dim") = V{}, py::arg("keepdim") = false);
     m.def("mean_backward", [](const Tensor& g, const Tensor& s, const V& d, bool k) { return mean_backward(g, s, d, k); },

@@ -10,7 +10,7 @@ SCHEMAS = sorted(["argmax", "argmin", "max", "max.dim", "mean", "mean.dim", "min
                   "sum", "sum.dim_IntList", "topk", "var", "var.dim", "prod", "prod.dim_IntList", "all", "all.dim",
                   "any", "any.dim", "median", "norm", "norm.dim", "copy_", "softmax", "log_softmax",
                   "_softmax_backward_data", "_log_softmax_backward_data", "nll_loss", "nll_loss_backward",
-                  "sum_backward", "mean_backward", "var_backward", "std_backward"])
+                  "sum_backward", "mean_backward", "var_backward", "std_backward", "topk_topp_sample"])
 
 
 def test_rocm_key_registers_every_schema():

@@ -1,0 +1,73 @@
+"""GPU parity of tpr_sample (top-k / top-p sampling) through the C-ABI and the
+dispatcher, against the oracle.  The draw depends on float comparisons against
+cumulative sums, which the GPU forms in float32 and the oracle in float64: ids
+must be equal wherever both decision thresholds are further than 1e-5 (relative)
+from every cumulative sum; closer than that, the GPU id must still lie in the
+oracle's nucleus (a boundary draw).  Greedy and k = 1 cases are bit-exact."""
+import numpy as np
+import pytest
+
+import tensorplay_amd as tp
+from oracle import oracle as O
+from tensorplay_amd import _capi
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+def check(x, u, k, T, top_p):
+    print(f"case sample shape={x.shape} k={k} T={T} top_p={top_p}", flush=True)
+    got = _capi.sample(torch.from_numpy(x).cuda(), torch.from_numpy(u).cuda(), k, T, top_p).cpu().numpy()
+    exp, margin = O.sample(x, u, k, T, top_p)
+    sure = margin > 1e-5
+    np.testing.assert_array_equal(got[sure], exp[sure])
+    if (~sure).any():
+        _, idx = O.topk(x, k)
+        for r in np.nonzero(~sure)[0]:
+            assert got[r] in idx[r]
+    return int((~sure).sum())
+
+
+def test_parameter_grid():
+    rng = np.random.default_rng(30)
+    for rows, cols in [(1, 1), (7, 10), (33, 1000), (16, 32768)]:
+        x = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
+        u = rng.random(rows).astype(np.float32)
+        for k in sorted({1, min(cols, 7), min(cols, 50), min(cols, 64), min(cols, 100), min(cols, 1024)}):
+            for T in (0.0, 0.7, 1.0, 2.0):
+                for top_p in (0.1, 0.5, 0.9, 1.0):
+                    check(x, u, k, T, top_p)
+
+
+def test_llm_logits_c5_shape():
+    # [256, 151936] N(0, 3) logits with 8 boosted positions per row, k = 50
+    rng = np.random.default_rng(31)
+    x = (rng.standard_normal((256, 151936)) * 3).astype(np.float32)
+    for r in range(256):
+        x[r, rng.choice(151936, 8, replace=False)] += 15.0
+    u = rng.random(256).astype(np.float32)
+    for T, top_p in ((1.0, 0.9), (0.7, 0.95), (1.3, 1.0)):
+        check(x, u, 50, T, top_p)
+
+
+def test_ties_and_greedy():
+    x = np.zeros((4, 300), np.float32)
+    x[:, 5] = x[:, 17] = 2.0
+    u = np.array([0.0, 0.4, 0.6, 0.99], np.float32)
+    got = _capi.sample(torch.from_numpy(x).cuda(), torch.from_numpy(u).cuda(), 2, 1.0, 1.0).cpu().numpy()
+    np.testing.assert_array_equal(got, [5, 5, 17, 17])   # equal halves: u < 0.5 -> index 5
+    got = _capi.sample(torch.from_numpy(x).cuda(), torch.from_numpy(u).cuda(), 10, 0.0, 0.5).cpu().numpy()
+    np.testing.assert_array_equal(got, [5, 5, 5, 5])
+
+
+def test_dispatcher_op():
+    rng = np.random.default_rng(32)
+    x = rng.standard_normal((3, 4, 500)).astype(np.float32)
+    u = rng.random(12).astype(np.float32)
+    ids = tp.topk_topp_sample(tp.tensor(x, device="rocm"), tp.tensor(u.reshape(3, 4), device="rocm"), 20, 0.8, 0.9)
+    assert ids.shape == [3, 4] and ids.dtype == tp.int64
+    exp, margin = O.sample(x.reshape(12, 500), u, 20, 0.8, 0.9)
+    got = ids.numpy().reshape(12)
+    assert np.array_equal(got[margin > 1e-5], exp[margin > 1e-5])
+    with pytest.raises(RuntimeError):
+        tp.topk_topp_sample(tp.tensor(x, device="rocm"), tp.tensor(u, device="rocm"), 20, 1.0, 1.5)
