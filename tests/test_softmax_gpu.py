@@ -81,12 +81,18 @@ def test_rows_misaligned_and_strided(log):
 def test_strided_dims(log):
     rng = np.random.default_rng(13)
     for shape, dim in [((4, 300, 33), 1), ((8, 512, 96), 1), ((300, 70), 0), ((2, 3, 4, 5), 2), ((7, 1, 9), 1),
-                       ((3, 5, 2), 0), ((1, 2000, 64), 1)]:
+                       ((3, 5, 2), 0), ((1, 2000, 64), 1), ((2, 300, 128), 1), ((3, 64, 20), 1), ((5, 7, 36), 1),
+                       ((130, 1000), 0)]:
         x = (rng.standard_normal(shape) * 2).astype(np.float32)
         check_fwd(x, x, dim, log)
-    _capi.debug_set("general", 1)        # the strided kernel on a contiguous last dim too
+    b = (rng.standard_normal((3, 200, 68)) * 2).astype(np.float32)
+    check_fwd(b, b[:, :, 4:], 1, log)    # inner 64 from a 16-byte aligned offset: float4 columns
+    check_fwd(b, b[:, :, 1:65], 1, log)  # misaligned start: scalar columns
+    _capi.debug_set("general", 1)        # the scalar strided kernel on a contiguous last dim too,
     x = rng.standard_normal((9, 700)).astype(np.float32)
     check_fwd(x, x, 1, log)
+    x = (rng.standard_normal((8, 512, 96)) * 2).astype(np.float32)
+    check_fwd(x, x, 1, log)              # and on a float4-eligible strided dim
 
 
 @pytest.mark.parametrize("log", [False, True])
@@ -106,7 +112,9 @@ def test_nan_inf_slices(log, plan):
         x[5, :] = 0.0
         x[6, 0] = 80.0               # one dominant value
         check_fwd(x, x, 1, log)
-        check_fwd(x, x.T, 0, log)    # the same slices through the strided kernel
+        check_fwd(x, x.T, 0, log)    # the same slices through the strided kernel (scalar columns)
+        y = np.ascontiguousarray(x.T)
+        check_fwd(y, y, 0, log)      # ... and float4 columns when n % 4 == 0
 
 
 def test_large_logits_c5_shape():
@@ -185,6 +193,8 @@ def test_backward_rows(log, plan):
 @pytest.mark.parametrize("log", [False, True])
 def test_backward_strided(log):
     check_bwd((4, 300, 33), 1, log, 200)
+    check_bwd((4, 300, 64), 1, log, 203)
+    check_bwd((3, 50, 20), 1, log, 204)
     check_bwd((300, 70), 0, log, 201)
     check_bwd((50, 80), 1, log, 202, view="T")
 
