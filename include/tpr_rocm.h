@@ -156,7 +156,8 @@ int tpr_topk(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t 
  * with u = uniforms[row] in [0, 1) (device float32 [rows], drawn by the
  * caller).  temperature <= 0 selects v_0 (greedy).  top_p in (0, 1], 1 <= k <=
  * min(cols, 1024).  out_ids: device int64 [rows].  Workspace:
- * tpr_sample_workspace_bytes (the candidates plus tpr_topk's). */
+ * tpr_sample_workspace_bytes (tpr_topk's: the draw runs in top-k's last
+ * phase, nothing else is written). */
 size_t tpr_sample_workspace_bytes(int32_t dtype, int64_t rows, int64_t cols, int64_t k);
 int tpr_sample(const void* logits, int32_t dtype, int64_t rows, int64_t cols, int64_t row_stride, int64_t k,
                float temperature, float top_p, const float* uniforms, int64_t* out_ids, void* workspace,

@@ -27,8 +27,7 @@ HIP_FLAGS = [
 ]
 
 ROCM_SOURCES = ["rocm/capi.cpp", "rocm/reduce.hip", "rocm/topk.hip", "rocm/copy.hip",
-                "rocm/softmax.hip", "rocm/loss.hip", "rocm/reduce_bwd.hip",
-                "rocm/sample.hip"]
+                "rocm/softmax.hip", "rocm/loss.hip", "rocm/reduce_bwd.hip"]
 LIB_TPR = os.path.join(PKG, "libtpr_rocm.so")
 
 

@@ -111,7 +111,89 @@ struct TopkArgs {
     unsigned long long* part;  // [rows][nseg][k] composites when nseg > 1
     float* out_v;
     long long* out_i;
+    // sampling (tpr_sample): instead of writing values / indices, draw one id
+    // per row from the sorted top k (see sample_from_sel)
+    int sample;
+    float temperature, top_p;
+    const float* u;
+    long long* ids;
 };
+
+// Top-k / top-p draw from a row's sorted selection (composites in rank order),
+// run by one wave (threads 0..63):  p_j = exp(v_j/T - v_0/T), c_j = p_0 + .. +
+// p_j, m = first j with c_j >= top_p * c_{k-1}, id = index of the first j <= m
+// with c_j > u * c_m; T <= 0 takes the first.  Each lane owns a contiguous
+// block of <= 16 candidates: serial sums inside the block, a wave scan of the
+// block totals, ballots for the two searches.
+__device__ void sample_from_sel(const TopkArgs& a, long long row, const float* p, const unsigned long long* sel,
+                                int k) {
+    const int lane = threadIdx.x;
+    if (!(a.temperature > 0.0f)) {
+        if (lane == 0) a.ids[row] = (long long)comp_index(sel[0]);
+        return;
+    }
+    const int per = (k + 63) / 64;
+    const int j0 = lane * per;
+    const float z0 = selected_value(p, (uint32_t)(sel[0] >> 32), comp_index(sel[0]), a.largest) / a.temperature;
+    float pr[16];
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const int j = j0 + q;
+        pr[q] = 0.0f;
+        if (q < per && j < k) {
+            const float v = selected_value(p, (uint32_t)(sel[j] >> 32), comp_index(sel[j]), a.largest);
+            pr[q] = expf(v / a.temperature - z0);
+            s += pr[q];
+        }
+    }
+    float incl = s;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float t = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += t;
+    }
+    const float excl = incl - s;
+    const float cut = a.top_p * __shfl(incl, 63, 64);
+    int mj = 0x7fffffff;
+    float c = excl;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const int j = j0 + q;
+        if (q < per && j < k) {
+            c += pr[q];
+            if (c >= cut && mj == 0x7fffffff) mj = j;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mj = min(mj, __shfl_xor(mj, o, 64));
+    const int m = (mj == 0x7fffffff) ? k - 1 : mj;
+    float cm_l = 0.0f;
+    c = excl;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const int j = j0 + q;
+        if (q < per && j < k) {
+            c += pr[q];
+            if (j == m) cm_l = c;
+        }
+    }
+    const float thr = a.u[row] * __shfl(cm_l, m / per, 64);
+    int pj = 0x7fffffff;
+    c = excl;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const int j = j0 + q;
+        if (q < per && j <= m) {
+            c += pr[q];
+            if (c > thr && pj == 0x7fffffff) pj = j;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) pj = min(pj, __shfl_xor(pj, o, 64));
+    if (pj > m) pj = m;
+    if (lane == 0) a.ids[row] = (long long)comp_index(sel[pj]);
+}
 
 // Small shared state of the workgroup-level helpers.
 struct BlockScratch {
@@ -372,7 +454,9 @@ __device__ void exact_select(BlockScratch& bs, unsigned long long* cand, const f
 // is not split, else the k composites for the merge pass.
 __device__ __forceinline__ void write_segment(const TopkArgs& a, long long row, int seg, const float* p,
                                               const unsigned long long* sel, int k) {
-    if (a.nseg == 1) {
+    if (a.nseg == 1 && a.sample) {
+        if (threadIdx.x < 64) sample_from_sel(a, row, p, sel, k);
+    } else if (a.nseg == 1) {
         for (int i = threadIdx.x; i < k; i += blockDim.x) {
             const uint32_t idx = comp_index(sel[i]);
             a.out_v[row * k + i] = selected_value(p, (uint32_t)(sel[i] >> 32), idx, a.largest);
@@ -762,6 +846,10 @@ __global__ __launch_bounds__(kMergeT) void k_topk_merge(TopkArgs a) {
     __syncthreads();
     rank_select<kMergeT>(sh.cand, sh.rank, sh.sel, m, k);
     const float* p = a.in + row * a.row_stride;
+    if (a.sample) {
+        if (threadIdx.x < 64) sample_from_sel(a, row, p, sh.sel, k);
+        return;
+    }
     for (int i = threadIdx.x; i < k; i += kMergeT) {
         const uint32_t idx = comp_index(sh.sel[i]);
         a.out_v[row * k + i] = selected_value(p, (uint32_t)(sh.sel[i] >> 32), idx, a.largest);
@@ -829,18 +917,22 @@ size_t tpr_topk_workspace_bytes(int32_t dtype, int64_t rows, int64_t cols, int64
     return tpr::plan_topk(rows, cols, k).ws;
 }
 
-int tpr_topk(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t row_stride,
-             int64_t k, int32_t largest, int32_t sorted, void* out_values, void* out_indices,
-             void* workspace, size_t workspace_bytes, void* stream) {
-    using namespace tpr;
-    (void)sorted;
+}  // extern "C"
+
+namespace tpr {
+namespace {
+// tpr_topk, or (smp != nullptr) tpr_sample: the same selection with the draw
+// in the final phase.
+int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t row_stride, int64_t k,
+                int32_t largest, void* out_values, void* out_indices, void* workspace, size_t workspace_bytes,
+                void* stream, const TopkArgs* smp) {
     if (dtype != TPR_FLOAT32) return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_topk: only float32 is implemented");
     if (rows < 0 || cols < 0) return fail(TPR_ERR_INVALID_ARG, "tpr_topk: negative shape");
     if (k < 0 || k > cols) return fail(TPR_ERR_INVALID_ARG, "tpr_topk: selected index k out of range");
     if (rows == 0 || k == 0) return TPR_OK;
     if (cols > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: rows longer than 2^31-1");
     if (k > kKMax) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: k > 1024 is not implemented");
-    if (!in || !out_values || !out_indices) return fail(TPR_ERR_INVALID_ARG, "tpr_topk: null pointer");
+    if (!in || (!smp && (!out_values || !out_indices))) return fail(TPR_ERR_INVALID_ARG, "tpr_topk: null pointer");
     const TopkPlan pl = plan_topk(rows, cols, k);
     if (rows * (long long)pl.nseg > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: grid too large");
     if (pl.ws > 0 && (workspace == nullptr || workspace_bytes < pl.ws))
@@ -858,6 +950,11 @@ int tpr_topk(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t 
     a.part = static_cast<unsigned long long*>(workspace);
     a.out_v = static_cast<float*>(out_values);
     a.out_i = static_cast<long long*>(out_indices);
+    a.sample = smp ? 1 : 0;
+    a.temperature = smp ? smp->temperature : 0.0f;
+    a.top_p = smp ? smp->top_p : 1.0f;
+    a.u = smp ? smp->u : nullptr;
+    a.ids = smp ? smp->ids : nullptr;
     const bool vec = ((reinterpret_cast<uintptr_t>(in) & 15u) == 0) && (rows == 1 || row_stride % 4 == 0);
     hipStream_t st = static_cast<hipStream_t>(stream);
     const long long grid = rows * pl.nseg;
@@ -887,6 +984,42 @@ int tpr_topk(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t 
     if (rc != TPR_OK || pl.nseg == 1) return rc;
     hipLaunchKernelGGL(k_topk_merge, dim3(rows), dim3(kMergeT), 0, st, a);
     return check_launch("k_topk_merge");
+}
+}  // namespace
+}  // namespace tpr
+
+extern "C" {
+
+int tpr_topk(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t row_stride,
+             int64_t k, int32_t largest, int32_t sorted, void* out_values, void* out_indices,
+             void* workspace, size_t workspace_bytes, void* stream) {
+    (void)sorted;
+    return tpr::topk_launch(in, dtype, rows, cols, row_stride, k, largest, out_values, out_indices, workspace,
+                            workspace_bytes, stream, nullptr);
+}
+
+size_t tpr_sample_workspace_bytes(int32_t dtype, int64_t rows, int64_t cols, int64_t k) {
+    return tpr_topk_workspace_bytes(dtype, rows, cols, k);
+}
+
+int tpr_sample(const void* logits, int32_t dtype, int64_t rows, int64_t cols, int64_t row_stride, int64_t k,
+               float temperature, float top_p, const float* uniforms, int64_t* out_ids, void* workspace,
+               size_t workspace_bytes, void* stream) {
+    using namespace tpr;
+    if (dtype != TPR_FLOAT32) return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_sample: float32 logits only");
+    if (rows < 0 || cols < 0) return fail(TPR_ERR_INVALID_ARG, "tpr_sample: negative shape");
+    if (k < 1 || k > cols) return fail(TPR_ERR_INVALID_ARG, "tpr_sample: k must be in [1, cols]");
+    if (k > kKMax) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_sample: k > 1024 is not implemented");
+    if (!(top_p > 0.0f) || top_p > 1.0f) return fail(TPR_ERR_INVALID_ARG, "tpr_sample: top_p must be in (0, 1]");
+    if (rows == 0) return TPR_OK;
+    if (!logits || !uniforms || !out_ids) return fail(TPR_ERR_INVALID_ARG, "tpr_sample: null pointer");
+    TopkArgs smp{};
+    smp.temperature = temperature;
+    smp.top_p = top_p;
+    smp.u = uniforms;
+    smp.ids = reinterpret_cast<long long*>(out_ids);
+    return topk_launch(logits, dtype, rows, cols, row_stride, k, 1, nullptr, nullptr, workspace, workspace_bytes,
+                       stream, &smp);
 }
 
 }  // extern "C"
