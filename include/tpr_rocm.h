@@ -70,8 +70,10 @@ enum tpr_reduce_op {
  *  - out_dtype: SUM/MEAN/PROD: FLOAT32 or FLOAT64.  AMAX/AMIN: the input
  *    dtype.  ARGMAX/ARGMIN: INT64 (index along the reduced dims, row-major;
  *    first index wins ties; NaN never wins, as the reference's strict
- *    compare).  VAR/STD/NORM/MEDIAN: FLOAT32.  ALL/ANY: BOOL (one byte, 0/1;
- *    an element counts as true when it is != 0, so NaN is true).
+ *    compare).  VAR/STD/NORM/MEDIAN: FLOAT32 (FLOAT64 for a FLOAT64 input:
+ *    every op but MEDIAN takes FLOAT64 inputs and computes in double).
+ *    ALL/ANY: BOOL (one byte, 0/1; an element counts as true when it is != 0,
+ *    so NaN is true).
  *  - NORM: (sum |x|^p)^(1/p); p = +inf / -inf: max / min of |x| (NaN ignored,
  *    as AMAX/AMIN); p = 0 gives the reference's n^(1/0).
  *  - MEDIAN: lower median ((n-1)/2-th smallest) of all elements; -0.0 == +0.0

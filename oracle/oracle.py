@@ -20,6 +20,8 @@ Parity status of each function (see tests/test_oracle.py):
                                         full and along dims, corrections 0 / 1 / 2
   sample (top-k / top-p)                pinned: inverse-CDF over the full softmax when k = cols and top_p = 1;
                                         argmax when k = 1 or T <= 0; brute-force frequencies over a grid of u
+  reduce_f64 (float64 inputs)           pinned: math.fsum / numpy fp64 reductions, argmax first occurrence,
+                                        torch.var / torch.std / torch.norm in fp64
   copy                                  pinned: numpy astype on the same views (C casts), brute force on tiny shapes
 """
 import ctypes
@@ -398,3 +400,43 @@ def sample(x2d, u, k, temperature=1.0, top_p=1.0):
         ids[r] = idx[r, j]
         margin[r] = min(np.min(np.abs(c - cut)) / c[-1], np.min(np.abs(c[: m + 1] - thr)) / c[m])
     return ids, margin
+
+
+def reduce_f64(x, op, dims=None, correction=1, p=2.0):
+    """Float64 reductions as TensorPlay's CPU path computes them for Float64
+    tensors (ReductionKernels.cpp, AccumulateType<double> = double): sums and
+    products accumulate sequentially in double in memory order; max / min /
+    argmax / argmin use the strict compare from -inf / +inf (NaN ignored, first
+    index wins); var / std are the two-pass mean / (x - mean)^2 / sum /
+    (n - correction) composite in double; norm is (sum |x|^p)^(1/p).  Numpy,
+    sequential where the reference is (np.add.accumulate / np.multiply.accumulate)."""
+    x = np.asarray(x, dtype=np.float64)
+    nd = x.ndim
+    ax = tuple(range(nd)) if not dims else tuple(_wrap_dims(nd, dims))
+    kept = [i for i in range(nd) if i not in ax]
+    y = np.moveaxis(x, kept + list(ax), list(range(nd))).reshape([x.shape[i] for i in kept] + [-1])
+    if op == "sum":
+        return np.add.accumulate(y, axis=-1)[..., -1] if y.shape[-1] else np.zeros(y.shape[:-1])
+    if op == "mean":
+        return reduce_f64(x, "sum", dims) / y.shape[-1]
+    if op == "prod":
+        return np.multiply.accumulate(y, axis=-1)[..., -1] if y.shape[-1] else np.ones(y.shape[:-1])
+    if op in ("amax", "amin", "argmax", "argmin"):
+        is_max = op in ("amax", "argmax")
+        z = np.where(np.isnan(y), -np.inf if is_max else np.inf, y)
+        i = np.argmax(z, axis=-1) if is_max else np.argmin(z, axis=-1)
+        v = np.take_along_axis(z, i[..., None], -1)[..., 0]
+        return v if op in ("amax", "amin") else i.astype(np.int64)
+    if op in ("var", "std"):
+        n = y.shape[-1]
+        m = np.add.accumulate(y, axis=-1)[..., -1:] / n
+        d = (y - m) ** 2
+        v = np.add.accumulate(d, axis=-1)[..., -1] / max(0, n - correction)
+        return np.sqrt(v) if op == "std" else v
+    if op == "norm":
+        if np.isinf(p):
+            a = np.abs(y)
+            return a.max(axis=-1) if p > 0 else a.min(axis=-1)
+        with np.errstate(divide="ignore"):
+            return np.add.accumulate(np.abs(y) ** p, axis=-1)[..., -1] ** (1.0 / p)
+    raise ValueError(op)

@@ -180,6 +180,8 @@ def default_out_dtype(op, in_dtype=FLOAT32):
         return INT64
     if op in (ALL, ANY):
         return BOOL
+    if in_dtype == FLOAT64:
+        return FLOAT64   # sum / mean / prod / amax / amin / var / std / norm of float64
     if in_dtype != FLOAT32:
         if op in (SUM, PROD):
             return INT64

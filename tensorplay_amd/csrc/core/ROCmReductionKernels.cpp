@@ -58,13 +58,22 @@ void require_float32_input(const Tensor& self, const char* op) {
     if (self.dim() > TPR_MAX_DIMS) TP_THROW(NotImplementedError, std::string(op) + ": more than 8 dims on ROCm");
 }
 
-// sum/mean/prod, max/min, argmax/argmin and all/any also take the signed
-// integer dtypes, UInt8 and Bool (the reference instantiates them for every
-// scalar type); UInt16/32/64 have no ROCm kernel.
+// var/std/norm: Float32 or Float64 (computed in double for Float64, as the
+// reference's AccumulateType<double>).
+void require_float_input(const Tensor& self, const char* op) {
+    if (self.dtype() != DType::Float32 && self.dtype() != DType::Float64)
+        TP_THROW(NotImplementedError, std::string(op) + " not implemented for dtype " + toString(self.dtype()) +
+                                          " on ROCm (float32 / float64)");
+    if (self.dim() > TPR_MAX_DIMS) TP_THROW(NotImplementedError, std::string(op) + ": more than 8 dims on ROCm");
+}
+
+// sum/mean/prod, max/min, argmax/argmin and all/any also take Float64, the
+// signed integer dtypes, UInt8 and Bool (the reference instantiates them for
+// every scalar type); UInt16/32/64 have no ROCm kernel.
 void require_reducible_input(const Tensor& self, const char* op) {
     switch (self.dtype()) {
-        case DType::Float32: case DType::UInt8: case DType::Int8: case DType::Int16: case DType::Int32:
-        case DType::Int64: case DType::Bool: break;
+        case DType::Float32: case DType::Float64: case DType::UInt8: case DType::Int8: case DType::Int16:
+        case DType::Int32: case DType::Int64: case DType::Bool: break;
         default:
             TP_THROW(NotImplementedError, std::string(op) + " not implemented for dtype " + toString(self.dtype()) +
                                               " on ROCm");
@@ -193,14 +202,14 @@ Tensor argmin_kernel(const Tensor& self, std::optional<int64_t> dim, bool keepdi
 // var_kernel / std_kernel (ReductionKernels.cpp:817-827, :849-851)
 static Tensor var_full(const Tensor& self, int64_t correction, bool take_sqrt) {
     const char* name = take_sqrt ? "std" : "var";
-    require_float32_input(self, name);
+    require_float_input(self, name);
     return launch(self, take_sqrt ? TPR_STD : TPR_VAR, all_dims(self), self.dtype(), {}, correction, 0, name);
 }
 // var_dim_kernel / std_dim_kernel (ReductionKernels.cpp:829-847, :853-855)
 static Tensor var_dims(const Tensor& self, const std::vector<int64_t>& dims, int64_t correction, bool keepdim,
                        bool take_sqrt) {
     const char* name = take_sqrt ? "std" : "var";
-    require_float32_input(self, name);
+    require_float_input(self, name);
     // An empty dim list is the full-tensor variance here.  (The reference's
     // var_dim_kernel with {} centres on the un-divided full sum and divides by
     // max(0, 1 - correction); that result is not meaningful and is not copied.)
@@ -256,13 +265,13 @@ Tensor any_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, bool
 // Every p is served on ROCm (the CUDA path serves p = 2 only,
 // ReductionKernels.cu:295-321).
 Tensor norm_kernel(const Tensor& self, double p) {
-    require_float32_input(self, "norm");
+    require_float_input(self, "norm");
     if (std::isinf(p) && self.numel() == 0)
         TP_THROW(RuntimeError, std::string(p > 0 ? "max" : "min") + "(): Expected reduction dim to be non-empty");
     return launch(self, TPR_NORM, all_dims(self), self.dtype(), {}, 0, 0, "norm", p);
 }
 Tensor norm_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, double p, bool keepdim) {
-    require_float32_input(self, "norm");
+    require_float_input(self, "norm");
     if (dims.empty()) return norm_kernel(self, p);
     const auto shape = reductionShape(self.shape(), dims, keepdim);
     return launch(self, TPR_NORM, mask_of(self, dims), self.dtype(), shape, 0, 0, "norm", p);

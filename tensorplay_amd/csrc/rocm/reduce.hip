@@ -232,6 +232,11 @@ __device__ __forceinline__ void fin_write(const WelS& s, const Fin& f, void* out
     double dm = s.mean - mp;
     double m2 = s.m2 + s.n * dm * dm;
     double div = fmax(0.0, f.count - f.corr);
+    if (f.out_f64) {  // float64 input: var / std in double
+        const double v = m2 / div;
+        ((double*)out)[o] = (f.op == TPR_STD) ? sqrt(v) : v;
+        return;
+    }
     float var = (float)(m2 / div);
     ((float*)out)[o] = (f.op == TPR_STD) ? sqrtf(var) : var;
 }
@@ -650,6 +655,28 @@ int validate(const tpr_reduce_desc* d) {
         if (d->sizes[i] < 0) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: negative size");
     if (d->ndim < 32 && (d->reduce_mask >> d->ndim) != 0)
         return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: reduce_mask names a dim >= ndim");
+    if (d->in_dtype == TPR_FLOAT64) {
+        switch (d->op) {
+            case TPR_SUM: case TPR_MEAN: case TPR_PROD:
+                if (d->out_dtype != TPR_FLOAT32 && d->out_dtype != TPR_FLOAT64)
+                    return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: sum/mean/prod output must be float32 or float64");
+                return TPR_OK;
+            case TPR_AMAX: case TPR_AMIN: case TPR_VAR: case TPR_STD: case TPR_NORM:
+                if (d->out_dtype != TPR_FLOAT64)
+                    return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: float64 amax/amin/var/std/norm write float64");
+                return TPR_OK;
+            case TPR_ARGMAX: case TPR_ARGMIN:
+                if (d->out_dtype != TPR_INT64)
+                    return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: argmax/argmin output must be int64");
+                return TPR_OK;
+            case TPR_ALL: case TPR_ANY:
+                if (d->out_dtype != TPR_BOOL)
+                    return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: all/any output must be bool");
+                return TPR_OK;
+            default:
+                return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_reduce: median of float64 is not implemented");
+        }
+    }
     if (d->in_dtype != TPR_FLOAT32) {
         if (esize_of(d->in_dtype) == 0)
             return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: input dtype not implemented");
@@ -1260,13 +1287,128 @@ __global__ __launch_bounds__(kBlock) void k_general_i(GenArgsI a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Float64 inputs: the reference computes in double for Float64 tensors
+// (AccumulateType<double> = double, ReductionKernels.cpp:27-35; its CUDA path
+// reduces Float64 through cuDNN with CUDNN_DATA_DOUBLE,
+// ReductionKernels.cu:155-165).  The integer kernels above are generic in the
+// element type, so Float64 reuses them (two doubles per 16-byte vector) with
+// these double policies: sums / products / norms in double, max / min /
+// argmax / argmin with the same strict compare (NaN ignored, first index
+// wins), Welford in double, all / any as x != 0.
+// ---------------------------------------------------------------------------
+template <bool PROD>
+struct F64SumOp {
+    static constexpr bool kIndexed = false;
+    using Acc = double;
+    using State = SumS;
+    using Wide = F64SumOp;
+    __device__ static Acc init() { return PROD ? 1.0 : 0.0; }
+    template <class I>
+    __device__ static void acc(Acc& a, double x, I, float) { a = PROD ? a * x : a + x; }
+    __device__ static State state(Acc a) { return {a}; }
+    __device__ static State identity() { return {PROD ? 1.0 : 0.0}; }
+    __device__ static State comb(State a, State b) { return {PROD ? a.s * b.s : a.s + b.s}; }
+    __device__ static State shfl(State s, int m) { return {__shfl_xor(s.s, m, kWave)}; }
+};
+
+template <int KIND>  // 1: |x|, 2: x*x, 0: pow(|x|, p)
+struct F64NormOp {
+    static constexpr bool kIndexed = false;
+    using Acc = double;
+    using State = SumS;
+    using Wide = F64NormOp;
+    __device__ static Acc init() { return 0.0; }
+    template <class I>
+    __device__ static void acc(Acc& a, double x, I, float p) {
+        if constexpr (KIND == 1) a += fabs(x);
+        else if constexpr (KIND == 2) a = fma(x, x, a);
+        else a += pow(fabs(x), (double)p);
+    }
+    __device__ static State state(Acc a) { return {a}; }
+    __device__ static State identity() { return {0.0}; }
+    __device__ static State comb(State a, State b) { return {a.s + b.s}; }
+    __device__ static State shfl(State s, int m) { return {__shfl_xor(s.s, m, kWave)}; }
+};
+
+struct ArgSD { double v; long long i; };
+
+template <bool IS_MAX, class IdxT = int, bool ABS = false>
+struct F64ArgOp {
+    static constexpr bool kIndexed = true;
+    static constexpr IdxT kNone = (IdxT)(sizeof(IdxT) == 4 ? 0x7fffffff : kSentinel);
+    struct Acc { double v; IdxT i; };
+    using State = ArgSD;
+    using Wide = F64ArgOp<IS_MAX, long long, ABS>;
+    __device__ static Acc init() { return {IS_MAX ? -(double)INFINITY : (double)INFINITY, kNone}; }
+    template <class I>
+    __device__ static void acc(Acc& a, double x, I i, float) {
+        if constexpr (ABS) x = fabs(x);
+        const bool t = IS_MAX ? (x > a.v) : (x < a.v);
+        a.v = t ? x : a.v;
+        a.i = t ? (IdxT)i : a.i;
+    }
+    __device__ static State state(Acc a) { return {a.v, a.i == kNone ? kSentinel : (long long)a.i}; }
+    __device__ static State identity() { return {IS_MAX ? -(double)INFINITY : (double)INFINITY, kSentinel}; }
+    __device__ static State comb(State a, State b) {
+        bool t = IS_MAX ? (b.v > a.v) : (b.v < a.v);
+        t = t || (b.v == a.v && b.i < a.i);
+        return t ? b : a;
+    }
+    __device__ static State shfl(State s, int m) { return {__shfl_xor(s.v, m, kWave), __shfl_xor(s.i, m, kWave)}; }
+};
+
+struct WelAccD { double k; long long n; double s1, s2; };
+
+// Welford over double inputs: per-thread sums shifted by the thread's first
+// element, merged with the same Chan combine as WelfordOp.
+struct F64WelfordOp {
+    static constexpr bool kIndexed = false;
+    using Acc = WelAccD;
+    using State = WelS;
+    using Wide = F64WelfordOp;
+    __device__ static Acc init() { return {0.0, 0, 0.0, 0.0}; }
+    template <class I>
+    __device__ static void acc(Acc& a, double x, I, float) {
+        a.k = (a.n == 0) ? x : a.k;
+        const double d = x - a.k;
+        a.s1 += d;
+        a.s2 = fma(d, d, a.s2);
+        a.n += 1;
+    }
+    __device__ static State state(Acc a) {
+        if (a.n == 0) return {0.0, 0.0, 0.0};
+        const double n = (double)a.n;
+        const double m = a.s1 / n;
+        return {n, a.k + m, fmax(0.0, a.s2 - a.s1 * m)};
+    }
+    __device__ static State identity() { return WelfordOp::identity(); }
+    __device__ static State comb(State a, State b) { return WelfordOp::comb(a, b); }
+    __device__ static State shfl(State s, int m) { return WelfordOp::shfl(s, m); }
+};
+
+__device__ __forceinline__ void fin_write(const ArgSD& s, const Fin& f, void* out, long long o) {
+    if (f.op == TPR_AMAX || f.op == TPR_AMIN || f.op == TPR_NORM) ((double*)out)[o] = s.v;
+    else ((long long*)out)[o] = (s.i == kSentinel) ? 0 : s.i;
+}
+
 int esize_of(int dt) {
     switch (dt) {
         case TPR_UINT8: case TPR_INT8: case TPR_BOOL: return 1;
         case TPR_INT16: return 2;
         case TPR_INT32: return 4;
-        case TPR_INT64: return 8;
+        case TPR_INT64: case TPR_FLOAT64: return 8;
         default: return 0;
+    }
+}
+
+size_t f64_state_size(int op, double p) {
+    switch (op) {
+        case TPR_SUM: case TPR_MEAN: case TPR_PROD: return sizeof(SumS);
+        case TPR_NORM: return std::isinf(p) ? sizeof(ArgSD) : sizeof(SumS);
+        case TPR_ALL: case TPR_ANY: return sizeof(BoolS);
+        case TPR_AMAX: case TPR_AMIN: case TPR_ARGMAX: case TPR_ARGMIN: return sizeof(ArgSD);
+        default: return sizeof(WelS);
     }
 }
 
@@ -1288,7 +1430,7 @@ void adapt_plan_int(Plan& p, const tpr_reduce_desc* d, const void* in, int es) {
     const bool aligned16 = (reinterpret_cast<uintptr_t>(in) & 15u) == 0;
     const auto& dev = device_info();
     const long long target = (long long)dev.cus * 512;
-    p.state_bytes = int_state_size(d->op);
+    p.state_bytes = d->in_dtype == TPR_FLOAT64 ? f64_state_size(d->op, d->p) : int_state_size(d->op);
     if (p.kind == P_ROWS) {
         p.vec = (aligned16 && (p.rows == 1 || p.row_stride % NV == 0) && p.R >= NV) ? NV : 1;
         int L = 16;
@@ -1384,6 +1526,28 @@ int run_int_t(int op, const Plan& p, const void* in, void* out, void* ws, Fin fi
         case TPR_ALL: return run_int_op<IntBoolOp<T, false>, T>(p, in, out, ws, fin, st);
         case TPR_ANY: return run_int_op<IntBoolOp<T, true>, T>(p, in, out, ws, fin, st);
         default: return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: op not implemented for integer inputs");
+    }
+}
+
+int run_f64(const tpr_reduce_desc* d, const Plan& p, const void* in, void* out, void* ws, Fin fin, hipStream_t st) {
+    using T = double;
+    switch (d->op) {
+        case TPR_SUM: case TPR_MEAN: return run_int_op<F64SumOp<false>, T>(p, in, out, ws, fin, st);
+        case TPR_PROD: return run_int_op<F64SumOp<true>, T>(p, in, out, ws, fin, st);
+        case TPR_AMAX: case TPR_ARGMAX: return run_int_op<F64ArgOp<true>, T>(p, in, out, ws, fin, st);
+        case TPR_AMIN: case TPR_ARGMIN: return run_int_op<F64ArgOp<false>, T>(p, in, out, ws, fin, st);
+        case TPR_ALL: return run_int_op<IntBoolOp<T, false>, T>(p, in, out, ws, fin, st);
+        case TPR_ANY: return run_int_op<IntBoolOp<T, true>, T>(p, in, out, ws, fin, st);
+        case TPR_NORM:
+            if (std::isinf(d->p)) {
+                if (d->p > 0) return run_int_op<F64ArgOp<true, int, true>, T>(p, in, out, ws, fin, st);
+                return run_int_op<F64ArgOp<false, int, true>, T>(p, in, out, ws, fin, st);
+            }
+            if (d->p == 1.0) return run_int_op<F64NormOp<1>, T>(p, in, out, ws, fin, st);
+            if (d->p == 2.0) return run_int_op<F64NormOp<2>, T>(p, in, out, ws, fin, st);
+            return run_int_op<F64NormOp<0>, T>(p, in, out, ws, fin, st);
+        case TPR_VAR: case TPR_STD: return run_int_op<F64WelfordOp, T>(p, in, out, ws, fin, st);
+        default: return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_reduce: op not implemented for float64 inputs");
     }
 }
 
@@ -1599,6 +1763,7 @@ int tpr_reduce(const tpr_reduce_desc* desc, const void* in, void* out, void* wor
     fin.inv_p = 1.0 / desc->p;
     fin.out_esize = int_in ? esize_of(desc->in_dtype) : 4;
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (desc->in_dtype == TPR_FLOAT64) return run_f64(desc, p, in, out, workspace, fin, st);
     if (int_in) return run_int(desc, p, in, out, workspace, fin, st);
     const float* x = static_cast<const float*>(in);
     switch (desc->op) {
