@@ -63,10 +63,12 @@ def reduce_call(torch, capi, x, op, dims, stream, correction=1):
     nd = x.dim()
     rd = sorted(set((d + nd) % nd for d in dims)) if dims is not None else list(range(nd))
     kept = [x.shape[i] for i in range(nd) if i not in rd]
-    od = capi.default_out_dtype(op)
-    tdt = torch.int64 if od == capi.INT64 else torch.float32
+    tmap = capi._torch_dtypes()
+    idt = tmap[x.dtype]
+    od = capi.default_out_dtype(op, idt)
+    tdt = {v: k for k, v in tmap.items()}[od]
     out = torch.empty(kept, dtype=tdt, device=x.device)
-    desc = capi.make_desc(op, list(x.shape), list(x.stride()), rd, od, correction)
+    desc = capi.make_desc(op, list(x.shape), list(x.stride()), rd, od, correction, in_dtype=idt)
     L = capi.lib()
     wsb = L.tpr_reduce_workspace_bytes(ctypes.byref(desc))
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
@@ -333,6 +335,17 @@ def main():
                       "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4)}
         extras["C4_full_2^28"] = c4
         del x4
+        # the same 1 GiB as float64 (2^27 elements): reductions computed in double
+        x4d = gen(torch, (1 << 27,), "normal", 4001, dev).double() * 2.0 + 0.5
+        c4d = {}
+        for op in ("sum", "amax", "argmax", "var"):
+            c = reduce_call(torch, capi, x4d, op, None, stream)
+            ms = time_calls(torch, [c], max(steps // 2, 5), 2)
+            by = (1 << 27) * 8 + c.out_bytes
+            c4d[op] = {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
+                       "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        extras["C4_full_f64_2^27"] = c4d
+        del x4d
         # C5: topk k=50 + argmax dim=-1 of [256,151936] N(0,3) + 8 boosted positions per row
         b5 = []
         for i in range(5):

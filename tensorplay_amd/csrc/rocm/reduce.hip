@@ -1098,6 +1098,7 @@ struct ArgsI {
     // cols
     long long outer, os, rs, inner, ncb;
     int S;
+    int nt;  // nontemporal input loads
     void* out;
     void* part;
     Fin fin;
@@ -1107,6 +1108,19 @@ template <class T, int NV>
 struct alignas(16) Vec16 {
     T v[NV];
 };
+
+// 16-byte load of NV elements; `nt` marks it nontemporal (read once).
+template <class T, int NV>
+__device__ __forceinline__ Vec16<T, NV> ld16(const Vec16<T, NV>* p, int nt) {
+    if (nt) {
+        typedef int i32x4 __attribute__((ext_vector_type(4)));
+        const i32x4 r = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p));
+        Vec16<T, NV> t;
+        __builtin_memcpy(&t, &r, 16);
+        return t;
+    }
+    return *p;
+}
 
 template <class Op, int LANES>
 __device__ __forceinline__ typename Op::State combine_lanes(typename Op::State st, int tid) {
@@ -1153,8 +1167,21 @@ __global__ __launch_bounds__(LANES > kBlock ? LANES : kBlock) void k_rows_i(Args
         if constexpr (NV > 1) {
             const int nv = R / NV;
             const Vec16<T, NV>* pv = reinterpret_cast<const Vec16<T, NV>*>(p);
-            for (int v = s * LANES + l; v < nv; v += a.S * LANES) {
-                const Vec16<T, NV> t = pv[v];
+            const int step = a.S * LANES;
+            int v = s * LANES + l;
+            // four vectors in flight per lane; each lane still visits its
+            // elements in increasing index order
+            for (; v + 3 * step < nv; v += 4 * step) {
+                Vec16<T, NV> t[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) t[u] = ld16(pv + v + u * step, a.nt);
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int j = 0; j < NV; ++j) Op::acc(acc, t[u].v[j], (v + u * step) * NV + j, prm);
+            }
+            for (; v < nv; v += step) {
+                const Vec16<T, NV> t = ld16(pv + v, a.nt);
 #pragma unroll
                 for (int j = 0; j < NV; ++j) Op::acc(acc, t.v[j], v * NV + j, prm);
             }
@@ -1193,8 +1220,20 @@ __global__ __launch_bounds__(kBlock) void k_cols_i(ArgsI a) {
         const int R = (int)a.R;
         const int rstep = TY * a.S;
         if (NV > 1 && col0 + NV <= a.inner) {
-            for (int r = s * TY + ty; r < R; r += rstep) {
-                const Vec16<T, NV> t = *reinterpret_cast<const Vec16<T, NV>*>(base + (long long)r * a.rs);
+            int r = s * TY + ty;
+            // four rows in flight per thread, visited in increasing row order
+            for (; r + 3 * rstep < R; r += 4 * rstep) {
+                Vec16<T, NV> t[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    t[u] = ld16(reinterpret_cast<const Vec16<T, NV>*>(base + (long long)(r + u * rstep) * a.rs), a.nt);
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int j = 0; j < NV; ++j) Op::acc(acc[j], t[u].v[j], r + u * rstep, prm);
+            }
+            for (; r < R; r += rstep) {
+                const Vec16<T, NV> t = ld16(reinterpret_cast<const Vec16<T, NV>*>(base + (long long)r * a.rs), a.nt);
 #pragma unroll
                 for (int j = 0; j < NV; ++j) Op::acc(acc[j], t.v[j], r, prm);
             }
@@ -1465,6 +1504,7 @@ int run_int_op(const Plan& p, const void* in, void* out, void* ws, Fin fin, hipS
         ArgsI a{};
         a.in = in; a.rows = p.rows; a.R = p.R; a.row_stride = p.row_stride;
         a.S = (int)p.S; a.out = out; a.part = ws; a.fin = fin;
+        a.nt = (p.rows * p.R * (long long)sizeof(T) >= (64LL << 20)) ? 1 : 0;
         const long long groups = (p.lanes >= kBlock) ? 1 : kBlock / p.lanes;
         const dim3 grid(ceil_div(p.rows, groups) * p.S);
         const dim3 blk(p.lanes > kBlock ? p.lanes : kBlock);
@@ -1485,6 +1525,7 @@ int run_int_op(const Plan& p, const void* in, void* out, void* ws, Fin fin, hipS
         ArgsI a{};
         a.in = in; a.outer = p.outer; a.os = p.os; a.R = p.R; a.rs = p.rs; a.inner = p.inner; a.ncb = p.ncb;
         a.S = (int)p.S; a.out = out; a.part = ws; a.fin = fin;
+        a.nt = (p.outer * p.R * p.inner * (long long)sizeof(T) >= (64LL << 20)) ? 1 : 0;
         const dim3 grid(p.outer * p.ncb * p.S);
 #define TPR_COLS_I(TXV)                                                                             \
     if (p.tx == TXV) {                                                                              \
