@@ -517,11 +517,34 @@ __device__ __forceinline__ void load_slice(float4 (&cur)[SV], __amdgpu_buffer_rs
     }
 }
 
+// f2key in selects and one sign-mask xor (no per-element branches):
+// u ^ (sign ? 0xffffffff : 0x80000000) is the same order-preserving map, and
+// lmask = largest ? 0 : ~0 folds the inversion in.  Returns exactly f2key(f, largest).
+__device__ __forceinline__ uint32_t f2key_sel(float f, uint32_t lmask) {
+    uint32_t u = __float_as_uint(f);
+    u = (u == 0x80000000u) ? 0u : u;                          // -0 -> +0
+    u = ((u & 0x7fffffffu) > 0x7f800000u) ? 0x7fc00000u : u;  // canonical NaN
+    const uint32_t m = (uint32_t)((int32_t)u >> 31) | 0x80000000u;
+    return (u ^ m) ^ lmask;
+}
+
 // Sortable keys of one slice; elements at or past `hi` get key 0 (below every
-// threshold).  Branch-free: a select per element.
+// threshold).  A slice wholly inside the segment (every one but the last; the
+// test is wave-uniform) takes no bounds test at all.
 template <int SV>
 __device__ __forceinline__ void slice_keys(const float4 (&cur)[SV], int base, int hi, int largest,
                                            uint32_t (&key)[4 * SV]) {
+    if (hi - base >= 256 * SV) {
+        const uint32_t lm = largest ? 0u : 0xffffffffu;
+#pragma unroll
+        for (int j = 0; j < SV; ++j) {
+            key[4 * j + 0] = f2key_sel(cur[j].x, lm);
+            key[4 * j + 1] = f2key_sel(cur[j].y, lm);
+            key[4 * j + 2] = f2key_sel(cur[j].z, lm);
+            key[4 * j + 3] = f2key_sel(cur[j].w, lm);
+        }
+        return;
+    }
     const int lim = hi - base - 4 * (int)__lane_id();  // element e = base + 4*lane + 256*j + q is valid iff 256*j + q < lim
 #pragma unroll
     for (int j = 0; j < SV; ++j) {
@@ -761,13 +784,24 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(6, 8))) void
         float4 cur[kV];
         load_chunk<VEC>(cur, p, cbase, hi);
         uint32_t key[4 * kV];
+        if (cbase + kCH <= hi) {  // whole chunk inside the segment (uniform): no bounds tests
+            const uint32_t lm = largest ? 0u : 0xffffffffu;
 #pragma unroll
-        for (int j = 0; j < kV; ++j) {
-            const int e = cbase + 4 * (j * kT + tid);
-            key[4 * j + 0] = (e + 0 < hi) ? f2key(cur[j].x, largest) : 0u;
-            key[4 * j + 1] = (e + 1 < hi) ? f2key(cur[j].y, largest) : 0u;
-            key[4 * j + 2] = (e + 2 < hi) ? f2key(cur[j].z, largest) : 0u;
-            key[4 * j + 3] = (e + 3 < hi) ? f2key(cur[j].w, largest) : 0u;
+            for (int j = 0; j < kV; ++j) {
+                key[4 * j + 0] = f2key_sel(cur[j].x, lm);
+                key[4 * j + 1] = f2key_sel(cur[j].y, lm);
+                key[4 * j + 2] = f2key_sel(cur[j].z, lm);
+                key[4 * j + 3] = f2key_sel(cur[j].w, lm);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kV; ++j) {
+                const int e = cbase + 4 * (j * kT + tid);
+                key[4 * j + 0] = (e + 0 < hi) ? f2key(cur[j].x, largest) : 0u;
+                key[4 * j + 1] = (e + 1 < hi) ? f2key(cur[j].y, largest) : 0u;
+                key[4 * j + 2] = (e + 2 < hi) ? f2key(cur[j].z, largest) : 0u;
+                key[4 * j + 3] = (e + 3 < hi) ? f2key(cur[j].w, largest) : 0u;
+            }
         }
         if (c == 0) {
             const uint32_t rth = wave_rth_of_lane_max(key, 4 * kV, r);
