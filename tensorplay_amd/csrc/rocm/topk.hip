@@ -636,6 +636,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
             for (int q = 0; q < 4 * SV; ++q) {
                 const bool pass = key[q] >= T;
                 const unsigned long long b = __ballot(pass);
+                if (b == 0ull) continue;  // uniform: most slots hold no candidate
                 if (pass)
                     list[pos + __popcll(b & lt)] =
                         comp_key(key[q], (uint32_t)(base + 4 * ((q >> 2) * 64 + lane) + (q & 3)));
