@@ -63,19 +63,28 @@ constexpr int kSlice = 64 * 16;               // elements per wave slice (4 floa
 constexpr int kWaveMinSeg = kW * kSlice;      // every wave has a full first slice (8192)
 constexpr long long kWaveMaxSeg = 1LL << 28;  // longest wave-kernel segment (32-bit byte offsets)
 
+// Order-preserving float -> uint32 map: non-negative u -> u | 2^31, negative
+// u -> ~u + 1 (two's-complement negate of the magnitude's image), so -0.0 and
+// +0.0 land on the same key 2^31; every NaN is first made 0x7fc00000 (above
+// +inf).  lmask = 0 keeps the order (largest), ~0 reverses it (smallest).
+// Valid keys are never 0: 0 marks "no element".  Branch-free: one NaN select,
+// an arithmetic shift, xor, subtract, xor.
+__device__ __forceinline__ uint32_t f2key_sel(float f, uint32_t lmask) {
+    const uint32_t b = __float_as_uint(f);
+    const uint32_t u = ((b & 0x7fffffffu) > 0x7f800000u) ? 0x7fc00000u : b;
+    const uint32_t m = (uint32_t)((int32_t)u >> 31);
+    return ((u ^ (m | 0x80000000u)) - m) ^ lmask;
+}
+
 __device__ __forceinline__ uint32_t f2key(float f, int largest) {
-    uint32_t u = __float_as_uint(f);
-    u = ((u & 0x7fffffffu) > 0x7f800000u) ? 0x7fc00000u : u;  // canonical NaN
-    u = (u == 0x80000000u) ? 0u : u;                          // -0 -> +0
-    uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return largest ? k : ~k;  // valid keys are never 0: 0 marks "no element"
+    return f2key_sel(f, largest ? 0u : 0xffffffffu);
 }
 
 // Inverse of f2key.  Exact except for the two canonicalised cases (-0.0 comes
 // back as +0.0, any NaN as 0x7fc00000); callers re-read the input for those.
 __device__ __forceinline__ uint32_t key2bits(uint32_t key, int largest) {
     const uint32_t k = largest ? key : ~key;
-    return (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+    return (k & 0x80000000u) ? (k & 0x7fffffffu) : (0u - k);
 }
 
 // Output value of a selected element: from its key, or from the input row when
@@ -517,16 +526,6 @@ __device__ __forceinline__ void load_slice(float4 (&cur)[SV], __amdgpu_buffer_rs
     }
 }
 
-// f2key in selects and one sign-mask xor (no per-element branches):
-// u ^ (sign ? 0xffffffff : 0x80000000) is the same order-preserving map, and
-// lmask = largest ? 0 : ~0 folds the inversion in.  Returns exactly f2key(f, largest).
-__device__ __forceinline__ uint32_t f2key_sel(float f, uint32_t lmask) {
-    uint32_t u = __float_as_uint(f);
-    u = (u == 0x80000000u) ? 0u : u;                          // -0 -> +0
-    u = ((u & 0x7fffffffu) > 0x7f800000u) ? 0x7fc00000u : u;  // canonical NaN
-    const uint32_t m = (uint32_t)((int32_t)u >> 31) | 0x80000000u;
-    return (u ^ m) ^ lmask;
-}
 
 // Sortable keys of one slice; elements at or past `hi` get key 0 (below every
 // threshold).  A slice wholly inside the segment (every one but the last; the
