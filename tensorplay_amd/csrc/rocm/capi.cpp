@@ -74,6 +74,7 @@ int tpr_debug_set(const char* key, int64_t value) {
     else if (!std::strcmp(key, "smx_two_pass")) k.smx_two_pass = value;
     else if (!std::strcmp(key, "smx_lanes")) k.smx_lanes = value;
     else if (!std::strcmp(key, "smx_split")) k.smx_split = value;
+    else if (!std::strcmp(key, "smx_res")) k.smx_res = value;
     else return tpr::fail(TPR_ERR_INVALID_ARG, std::string("tpr_debug_set: unknown key ") + key);
     return TPR_OK;
 }

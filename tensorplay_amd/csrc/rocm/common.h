@@ -37,6 +37,7 @@ struct DebugKnobs {
     int64_t smx_two_pass = 0;
     int64_t smx_lanes = 0;
     int64_t smx_split = 0;
+    int64_t smx_res = 0;
 };
 DebugKnobs& knobs();
 

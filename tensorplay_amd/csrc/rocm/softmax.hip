@@ -26,6 +26,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <string>
 
@@ -348,6 +349,109 @@ __global__ __launch_bounds__(1024) void k_smx_rows2(SmxArgs p) {
         base += TILE;
         if (base >= n) break;
     }
+}
+
+// ---------------------------------------------------------------------------
+// Rows too long for registers alone but short enough for one CU (kResMin to
+// kResMax floats, e.g. LLM vocabularies of 128K-152K): one 512-thread
+// workgroup per row holds the row in registers (kResVR float4 per lane) plus
+// LDS (the remaining vl float4 per lane, loaded straight from global memory
+// into LDS without passing through registers).  Read once, write once, where
+// the two-pass kernel reads twice.  Forward only.
+//   vector v = j * 512 + t of the row is register r[j] of thread t for
+//   j < kResVR, and lds[(j - kResVR) * 512 + t] after that.
+// ---------------------------------------------------------------------------
+constexpr int kResT = 512;
+constexpr int kResVR = 56;                       // float4 per lane in registers (224 VGPRs)
+constexpr int kResLdsMax = 160 * 1024;           // LDS of one gfx950 workgroup
+constexpr int kResVLMax = kResLdsMax / (kResT * 16) - 1;  // float4 per lane in LDS (19; 4 KB spare)
+constexpr long long kResMax = (long long)kResT * 4 * (kResVR + kResVLMax);  // 153600 floats
+constexpr long long kResMin = (long long)kResT * 4 * kResVR;                // 114688 floats
+
+constexpr int kBufWord3 = 0x00020000;  // raw buffer resource, 32-bit data (gfx9 family)
+
+// Row loads and stores go through buffer resources spanning the row, with
+// 32-bit offsets (no 64-bit address per vector).  The host sends only rows of
+// at least kResMin floats, so every register vector is inside the row; the
+// LDS part is guarded.
+template <int MODE, int NT>
+__global__ __launch_bounds__(kResT) void k_smx_res(SmxArgs p, int vl) {
+    extern __shared__ f32x4 lds[];
+    __shared__ float sh[2][kResT / kWave];
+    constexpr int aux = NT ? 2 : 0;  // cache policy: nontemporal
+    const int t = threadIdx.x;
+    const long long row = blockIdx.x;
+    const float* ra = p.a + row * p.sa;
+    float* ro = p.out + row * p.n;
+    const int nb = (int)(p.n * 4);
+    const __amdgpu_buffer_rsrc_t ba = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(ra), (short)0, nb, kBufWord3);
+    const __amdgpu_buffer_rsrc_t bo = __builtin_amdgcn_make_buffer_rsrc(ro, (short)0, nb, kBufWord3);
+    const int q = (int)(p.n >> 2);  // float4 per row
+    const f32x4 ninf = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+
+    // LDS part first: the loads need no registers, so all of them are in
+    // flight while the register part is issued behind them.
+    const int wbase = t & ~(kWave - 1);
+    const f32x4* pa = reinterpret_cast<const f32x4*>(ra);
+    for (int j = 0; j < vl; ++j) {
+        const int v = (kResVR + j) * kResT + t;
+        if (v < q)
+            __builtin_amdgcn_global_load_lds(
+                (const void*)(pa + v),
+                (__attribute__((address_space(3))) void*)(lds + j * kResT + wbase), 16, 0, 0);
+    }
+    f32x4 r[kResVR];
+#pragma unroll
+    for (int j = 0; j < kResVR; ++j) r[j] = __builtin_amdgcn_raw_buffer_load_b128(ba, (j * kResT + t) * 16, 0, aux);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the LDS loads have landed
+    __syncthreads();
+
+    auto ldsv = [&](int j) -> f32x4 {
+        return ((kResVR + j) * kResT + t < q) ? lds[j * kResT + t] : ninf;
+    };
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kResVR; ++j) m = fmaxf(fmaxf(m, fmaxf(r[j].x, r[j].y)), fmaxf(r[j].z, r[j].w));
+    for (int j = 0; j < vl; ++j) {
+        const f32x4 x = ldsv(j);
+        m = fmaxf(fmaxf(m, fmaxf(x.x, x.y)), fmaxf(x.z, x.w));
+    }
+    m = grp<kResT, true>(m, sh[0]);
+    // per-lane sum in short chains (groups of 8 vectors, then the groups and
+    // the LDS part): ~300 terms per lane, summed sequentially, would cost
+    // accuracy next to the two-pass kernel
+    float s = 0.0f;
+    if (m != -INFINITY) {
+        auto vs = [&](f32x4 x) { return (exs(x.x - m) + exs(x.y - m)) + (exs(x.z - m) + exs(x.w - m)); };
+        static_assert(kResVR % 8 == 0, "register vectors come in groups of 8");
+#pragma unroll
+        for (int g = 0; g < kResVR / 8; ++g) {
+            float gs = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) gs += vs(r[8 * g + j]) + vs(r[8 * g + j + 1]);
+            s += gs;
+        }
+        float sl = 0.0f;
+        for (int j = 0; j < vl; ++j) sl += vs(ldsv(j));
+        s += sl;
+    }
+    s = grp<kResT, false>(s, sh[1]);
+    float st0, st1;
+    if (m == -INFINITY) {  // no value above -inf in the slice: NaN, as the reference
+        st0 = NAN;
+        st1 = NAN;
+    } else {
+        st0 = m;
+        st1 = (MODE == FWD) ? 1.0f / s : logf(s);
+    }
+    auto outq = [&](f32x4 x) -> f32x4 {
+        return f32x4{outv<MODE>(x.x, 0.0f, st0, st1), outv<MODE>(x.y, 0.0f, st0, st1),
+                     outv<MODE>(x.z, 0.0f, st0, st1), outv<MODE>(x.w, 0.0f, st0, st1)};
+    };
+#pragma unroll
+    for (int j = 0; j < kResVR; ++j) __builtin_amdgcn_raw_buffer_store_b128(outq(r[j]), bo, (j * kResT + t) * 16, 0, aux);
+    for (int j = 0; j < vl; ++j)
+        __builtin_amdgcn_raw_buffer_store_b128(outq(lds[j * kResT + t]), bo, ((kResVR + j) * kResT + t) * 16, 0, aux);
 }
 
 // ---------------------------------------------------------------------------
@@ -742,6 +846,27 @@ int run_rows(const SmxArgs& a0, int vw, hipStream_t st) {
         if (rc >= 0) return rc;
     }
     constexpr bool BW = MODE >= BWD;
+    if constexpr (!BW) {
+        // one row per CU in registers + LDS (read once) unless the rows are
+        // too few to fill the chip, where the split kernels spread each row
+        if (!two_pass && !a.part && vw == 4 && a.n >= kResMin && a.n <= kResMax && knobs().smx_res >= 0) {
+            const long long q = a.n / 4;
+            const long long jl = (q + kResT - 1) / kResT;  // float4 per lane
+            const int vl = (int)std::max(0LL, jl - kResVR);
+            const size_t lds_bytes = (size_t)vl * kResT * 16;
+            if (lds_bytes > 65536) {
+                for (const void* f : {reinterpret_cast<const void*>(&k_smx_res<MODE, 0>),
+                                      reinterpret_cast<const void*>(&k_smx_res<MODE, 1>)}) {
+                    const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
+                    if (e != hipSuccess)
+                        return fail(TPR_ERR_HIP, std::string("tpr_softmax: LDS attribute: ") + hipGetErrorString(e));
+                }
+            }
+            if (a.nt) hipLaunchKernelGGL((k_smx_res<MODE, 1>), dim3((unsigned)a.rows), dim3(kResT), lds_bytes, st, a, vl);
+            else hipLaunchKernelGGL((k_smx_res<MODE, 0>), dim3((unsigned)a.rows), dim3(kResT), lds_bytes, st, a, vl);
+            return check_launch("tpr_softmax (rows in registers + LDS)");
+        }
+    }
     if (a.part) {
         const long long blocks = a.rows * a.chunks;
         if (vw == 4) {
