@@ -16,8 +16,10 @@
 // and three temporaries).  Here one kernel does it:
 //   * rows that fit in registers (up to 32768 floats per 1024-thread
 //     workgroup) are read once and written once -- k_smx_rows;
-//   * longer rows stream twice: an online (max, sum-of-exp) pass, then the
-//     output pass -- k_smx_rows2;
+//   * forward rows up to 153600 floats stay on one CU, in registers plus
+//     LDS, and are also read once -- k_smx_res;
+//   * longer rows (and backward rows beyond registers) stream twice: an
+//     online (max, sum-of-exp) pass, then the output pass -- k_smx_rows2;
 //   * a strided softmax dim (inner extent > 1, or a non-unit dim stride)
 //     keeps one column per lane, thread rows across the dim, an LDS merge of
 //     the per-wave states, and also streams twice -- k_smx_cols.
@@ -352,8 +354,8 @@ __global__ __launch_bounds__(1024) void k_smx_rows2(SmxArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// Rows too long for registers alone but short enough for one CU (kResMin to
-// kResMax floats, e.g. LLM vocabularies of 128K-152K): one 512-thread
+// Rows too long for the register-only kernel but short enough for one CU
+// (32769 to 153600 floats, e.g. LLM vocabularies of 50K-152K): one 512-thread
 // workgroup per row holds the row in registers (kResVR float4 per lane) plus
 // LDS (the remaining vl float4 per lane, loaded straight from global memory
 // into LDS without passing through registers).  Read once, write once, where
@@ -362,19 +364,22 @@ __global__ __launch_bounds__(1024) void k_smx_rows2(SmxArgs p) {
 //   j < kResVR, and lds[(j - kResVR) * 512 + t] after that.
 // ---------------------------------------------------------------------------
 constexpr int kResT = 512;
-constexpr int kResVR = 56;                       // float4 per lane in registers (224 VGPRs)
 constexpr int kResLdsMax = 160 * 1024;           // LDS of one gfx950 workgroup
 constexpr int kResVLMax = kResLdsMax / (kResT * 16) - 1;  // float4 per lane in LDS (19; 4 KB spare)
-constexpr long long kResMax = (long long)kResT * 4 * (kResVR + kResVLMax);  // 153600 floats
-constexpr long long kResMin = (long long)kResT * 4 * kResVR;                // 114688 floats
+// VR = float4 per lane in registers: 56 (224 VGPRs), 40, 24 or 8.  A kernel
+// with VR takes rows of VR * 2048 .. (VR + 19) * 2048 floats; together they
+// cover 16384 .. 153600.
+constexpr long long res_min(int vr) { return (long long)kResT * 4 * vr; }
+constexpr long long res_max(int vr) { return (long long)kResT * 4 * (vr + kResVLMax); }
+constexpr long long kResMax = res_max(56);       // 153600 floats
 
 constexpr int kBufWord3 = 0x00020000;  // raw buffer resource, 32-bit data (gfx9 family)
 
 // Row loads and stores go through buffer resources spanning the row, with
 // 32-bit offsets (no 64-bit address per vector).  The host sends only rows of
-// at least kResMin floats, so every register vector is inside the row; the
+// at least res_min(kResVR) floats, so every register vector is inside the row; the
 // LDS part is guarded.
-template <int MODE, int NT>
+template <int MODE, int NT, int kResVR>
 __global__ __launch_bounds__(kResT) void k_smx_res(SmxArgs p, int vl) {
     extern __shared__ f32x4 lds[];
     __shared__ float sh[2][kResT / kWave];
@@ -837,6 +842,38 @@ bool use_split(long long rows, long long n) {
     return rows < device_info().cus;
 }
 
+template <int MODE, int NT, int VR>
+int launch_res_vr(const SmxArgs& a, hipStream_t st) {
+    const long long q = a.n / 4;
+    const long long jl = (q + kResT - 1) / kResT;  // float4 per lane
+    const int vl = (int)std::max(0LL, jl - VR);
+    const size_t lds_bytes = (size_t)vl * kResT * 16;
+    if (lds_bytes > 65536) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_smx_res<MODE, NT, VR>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
+        if (e != hipSuccess) return fail(TPR_ERR_HIP, std::string("tpr_softmax: LDS attribute: ") + hipGetErrorString(e));
+    }
+    hipLaunchKernelGGL((k_smx_res<MODE, NT, VR>), dim3((unsigned)a.rows), dim3(kResT), lds_bytes, st, a, vl);
+    return check_launch("tpr_softmax (rows in registers + LDS)");
+}
+
+// Rows of res_min(vr) .. res_max(vr) floats, vr in {56, 40, 24, 8}.
+template <int MODE>
+int launch_res(const SmxArgs& a, int vr, hipStream_t st) {
+    if (a.n < res_min(vr) || a.n > res_max(vr))
+        return fail(TPR_ERR_INVALID_ARG, "tpr_softmax: row length outside the resident kernel's range");
+#define TPR_RES(V) \
+    case V: return a.nt ? launch_res_vr<MODE, 1, V>(a, st) : launch_res_vr<MODE, 0, V>(a, st);
+    switch (vr) {
+        TPR_RES(56)
+        TPR_RES(40)
+        TPR_RES(24)
+        TPR_RES(8)
+        default: return fail(TPR_ERR_INVALID_ARG, "tpr_softmax: no resident kernel with that register count");
+    }
+#undef TPR_RES
+}
+
 template <int MODE>
 int run_rows(const SmxArgs& a0, int vw, hipStream_t st) {
     SmxArgs a = a0;
@@ -849,22 +886,11 @@ int run_rows(const SmxArgs& a0, int vw, hipStream_t st) {
     if constexpr (!BW) {
         // one row per CU in registers + LDS (read once) unless the rows are
         // too few to fill the chip, where the split kernels spread each row
-        if (!two_pass && !a.part && vw == 4 && a.n >= kResMin && a.n <= kResMax && knobs().smx_res >= 0) {
-            const long long q = a.n / 4;
-            const long long jl = (q + kResT - 1) / kResT;  // float4 per lane
-            const int vl = (int)std::max(0LL, jl - kResVR);
-            const size_t lds_bytes = (size_t)vl * kResT * 16;
-            if (lds_bytes > 65536) {
-                for (const void* f : {reinterpret_cast<const void*>(&k_smx_res<MODE, 0>),
-                                      reinterpret_cast<const void*>(&k_smx_res<MODE, 1>)}) {
-                    const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
-                    if (e != hipSuccess)
-                        return fail(TPR_ERR_HIP, std::string("tpr_softmax: LDS attribute: ") + hipGetErrorString(e));
-                }
-            }
-            if (a.nt) hipLaunchKernelGGL((k_smx_res<MODE, 1>), dim3((unsigned)a.rows), dim3(kResT), lds_bytes, st, a, vl);
-            else hipLaunchKernelGGL((k_smx_res<MODE, 0>), dim3((unsigned)a.rows), dim3(kResT), lds_bytes, st, a, vl);
-            return check_launch("tpr_softmax (rows in registers + LDS)");
+        if (!two_pass && !a.part && vw == 4 && a.n <= kResMax && knobs().smx_res >= 0) {
+            int vr = 0;
+            for (int c : {56, 40, 24, 8})
+                if (vr == 0 && a.n >= res_min(c)) vr = c;
+            if (vr) return launch_res<MODE>(a, vr, st);
         }
     }
     if (a.part) {

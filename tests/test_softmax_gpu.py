@@ -120,21 +120,23 @@ def test_nan_inf_slices(log, plan):
 @pytest.mark.parametrize("log", [False, True])
 @pytest.mark.parametrize("res", [0, -1])
 def test_rows_held_in_registers_and_lds(log, res):
-    # rows of 114688..153600 floats (vocabulary-sized): one 512-thread workgroup
-    # per row keeps 56 float4 per lane in registers and the rest in LDS
-    # (res=0); res=-1 sends the same rows through the two-pass kernel.
+    # rows of 32769..153600 floats (vocabulary-sized): one 512-thread workgroup
+    # per row keeps 8, 24, 40 or 56 float4 per lane in registers and the rest
+    # in LDS (res=0), at the edges of each kernel's range; res=-1 sends the
+    # same rows through the two-pass kernel.
     _capi.debug_set("smx_split", -1)
     _capi.debug_set("smx_res", res)
     inf, nan = np.inf, np.nan
     rng = np.random.default_rng(16)
-    for n in (114688, 114692, 128256, 131072, 151936, 153596, 153600):
+    for n in (32772, 40000, 49152, 50260, 55296, 65536, 81920, 88064, 100000, 114688, 114692, 128256, 131072,
+              151936, 153596, 153600):
         x = (rng.standard_normal((9, n)) * 3).astype(np.float32)
         x[0, n - 1] = nan            # NaN in the LDS part
         x[1, 5] = nan                # NaN in the register part
         x[2, :] = -inf
         x[3, n - 1] = inf            # +inf in the last vector
         x[4, : n - 7] = -inf         # only the tail is finite
-        x[5, 100000] = 90.0          # dominant value in the register part
+        x[5, n // 5] = 90.0          # dominant value in the register part
         x[6, n - 3] = 90.0           # dominant value in the LDS part
         check_fwd(x, x, 1, log)
     # a row longer than the resident capacity goes to the two-pass kernel
