@@ -285,8 +285,8 @@ int32_t tpr_abi_version(void);
  * "smx_two_pass" (1 = softmax rows always take the two-pass kernel),
  * "smx_split" (1 / -1 = long softmax rows always / never split over chunk
  * workgroups, 0 = automatic), "smx_lanes" (512 = softmax rows of 16385..32768
- * floats on 512-thread workgroups, 0 = automatic), "smx_res" (-1 = never hold
- * long forward softmax rows in registers + LDS, 0 = automatic),
+ * floats on 512-thread workgroups, 0 = automatic), "smx_res" (-1 = never hold long
+ * softmax rows or strided-dim slices on chip: two-pass kernels, 0 = automatic),
  * "topk_variant" (wave kernel prefetch depth: 1 = none, 2 = one slice, 3 = two
  * slices; 0 = automatic), "topk_waves" (8 or 16 waves per wave-kernel
  * workgroup, 0 = automatic).

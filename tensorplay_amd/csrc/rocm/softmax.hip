@@ -763,6 +763,124 @@ __global__ __launch_bounds__(kWave * BY) void k_smx_cols4(SmxColArgs p) {
     }
 }
 
+// Strided dim held in registers: like k_smx_cols4, but a wave covers 64/CW
+// rows x 4*CW columns (CW lanes of float4 per row: 16 -> 256 contiguous bytes,
+// 8 -> 128), BY waves, and each lane keeps its V rows (r = rl + (64/CW) w +
+// i * RS) in registers, so the slice is read once and written from registers.
+// For n <= RS * V.
+template <int MODE, int BY, int V, int CW>
+__global__ __launch_bounds__(kWave * BY) void k_smx_cols4r(SmxColArgs p) {
+    constexpr bool BW = MODE >= BWD;
+    constexpr int RW = kWave / CW;  // rows per wave step
+    constexpr int RS = RW * BY;      // rows per workgroup step
+    __shared__ float shm[BY][CW][4];
+    __shared__ float shs[BY][CW][4];
+    const int lane = threadIdx.x % kWave;
+    const int w = threadIdx.x / kWave;
+    const int cl = lane % CW, rl = lane / CW;
+    const long long ncg = (p.inner + 4 * CW - 1) / (4 * CW);
+    const long long o = blockIdx.x / ncg;
+    const long long c = (blockIdx.x - o * ncg) * (4 * CW) + 4 * cl;  // first column of this lane
+    const bool live = c < p.inner;
+    const float* pa = p.a + o * p.a_so + (live ? c : 0);
+    const float* pb = BW ? p.b + o * p.b_so + (live ? c : 0) : nullptr;
+    float* po = p.out + o * p.n * p.inner + (live ? c : 0);
+    const int n = live ? (int)p.n : 0;
+    const int r0 = rl + RW * w;
+
+    float x[V][4], y[BW ? V : 1][4];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int r = r0 + i * RS;
+        if (r < n) {
+            Vec<4>::load(x[i], pa + r * p.a_sn, p.nt);
+            if constexpr (BW) Vec<4>::load(y[i], pb + r * p.b_sn, p.nt);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                x[i][q] = BW ? 0.0f : -INFINITY;
+                if constexpr (BW) y[i][q] = 0.0f;
+            }
+        }
+    }
+    float m[4], sm[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if constexpr (!BW) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < V; ++i) mx = fmaxf(mx, x[i][q]);
+            float sv = 0.0f;
+            if (mx != -INFINITY) {
+#pragma unroll
+                for (int i = 0; i < V; ++i) sv += exs(x[i][q] - mx);
+            } else {
+#pragma unroll
+                for (int i = 0; i < V; ++i) sv += (x[i][q] != x[i][q]) ? x[i][q] : 0.0f;  // NaN stays
+            }
+            m[q] = mx;
+            sm[q] = sv;
+        } else {
+            float sv = 0.0f;
+#pragma unroll
+            for (int i = 0; i < V; ++i) sv += (MODE == BWD) ? x[i][q] * y[i][q] : x[i][q];
+            m[q] = 0.0f;
+            sm[q] = sv;
+        }
+    }
+    // merge the wave's RW row lanes (xor CW .. 32), then the BY waves via LDS
+#pragma unroll
+    for (int off = CW; off <= 32; off <<= 1) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float m2 = __shfl_xor(m[q], off, kWave), s2 = __shfl_xor(sm[q], off, kWave);
+            if constexpr (!BW) ms_merge(m[q], sm[q], m2, s2);
+            else sm[q] += s2;
+        }
+    }
+    if (rl == 0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            shm[w][cl][q] = m[q];
+            shs[w][cl][q] = sm[q];
+        }
+    }
+    __syncthreads();
+    float st0[4], st1[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float M = shm[0][cl][q], S = shs[0][cl][q];
+#pragma unroll
+        for (int k = 1; k < BY; ++k) {
+            if constexpr (!BW) ms_merge(M, S, shm[k][cl][q], shs[k][cl][q]);
+            else S += shs[k][cl][q];
+        }
+        if constexpr (!BW) {
+            if (M == -INFINITY) {
+                st0[q] = NAN;
+                st1[q] = NAN;
+            } else {
+                st0[q] = M;
+                st1[q] = (MODE == FWD) ? 1.0f / S : logf(S);
+            }
+        } else {
+            st0[q] = S;
+            st1[q] = 0.0f;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int r = r0 + i * RS;
+        if (r < n) {
+            float out[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) out[q] = outv<MODE>(x[i][q], BW ? y[i][q] : 0.0f, st0[q], st1[q]);
+            Vec<4>::store(po + (long long)r * p.inner, out, p.nt);
+        }
+    }
+}
+
+
 // ---------------------------------------------------------------------------
 // Host planner
 // ---------------------------------------------------------------------------
@@ -921,6 +1039,21 @@ int run_cols(const SmxColArgs& a, hipStream_t st) {
         if (blocks <= 0x7fffffffLL) {
             // more waves along longer dims (measured at [64, 1024, 1024] dim 1: 16 waves 150 us,
             // 8 waves 160 us; at [16, 256, 8192] dim 1: 8 waves 70 us, 16 waves 92 us)
+            // slices of 65..1024 rows (backward, two inputs: ..256) stay in
+            // registers: read once
+            if (a.n > 64 && a.n <= (BW ? 256 : 1024) && knobs().smx_res >= 0 && knobs().smx_two_pass == 0) {
+                // 64-column groups (CW = 16); 32-column groups (CW = 8, two
+                // workgroups per CU) measured slower: 143 vs 131 us at [64, 1024,
+                // 1024] dim 1, 193 vs 111 us at [2048, 128, 256]
+                const unsigned g = (unsigned)(a.outer * ((a.inner + 63) / 64));
+                if (a.n <= 128) hipLaunchKernelGGL((k_smx_cols4r<MODE, 8, 4, 16>), dim3(g), dim3(kWave * 8), 0, st, a);
+                else if (a.n <= 256) hipLaunchKernelGGL((k_smx_cols4r<MODE, 8, 8, 16>), dim3(g), dim3(kWave * 8), 0, st, a);
+                else if constexpr (!BW) {
+                    if (a.n <= 512) hipLaunchKernelGGL((k_smx_cols4r<MODE, 16, 8, 16>), dim3(g), dim3(kWave * 16), 0, st, a);
+                    else hipLaunchKernelGGL((k_smx_cols4r<MODE, 16, 16, 16>), dim3(g), dim3(kWave * 16), 0, st, a);
+                }
+                return check_launch("tpr_softmax (strided dim, in registers)");
+            }
             int by = a.n >= 1024 ? 16 : (a.n >= 128 ? 8 : 4);
             if (knobs().colblock == 256 || knobs().colblock == 512 || knobs().colblock == 1024) by = (int)knobs().colblock / 64;
             if (by == 16) hipLaunchKernelGGL((k_smx_cols4<MODE, 16>), dim3((unsigned)blocks), dim3(kWave * 16), 0, st, a);

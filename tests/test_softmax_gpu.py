@@ -96,6 +96,26 @@ def test_strided_dims(log):
 
 
 @pytest.mark.parametrize("log", [False, True])
+@pytest.mark.parametrize("res", [0, -1])
+def test_strided_dim_held_in_registers(log, res):
+    # float4 column slices of 65..1024 rows stay in registers (res=0: 64-column
+    # groups, 8 or 16 waves, 4/8/16 rows per lane; res=-1: the two-pass column
+    # kernel), at the edges of each variant, with ragged column groups and
+    # NaN / inf columns.
+    _capi.debug_set("smx_res", res)
+    rng = np.random.default_rng(17)
+    inf, nan = np.inf, np.nan
+    for n in (65, 128, 129, 256, 257, 512, 513, 1000, 1024, 1025):
+        for inner in (64, 200, 264):
+            x = (rng.standard_normal((3, n, inner)) * 2).astype(np.float32)
+            x[0, n // 2, 1] = nan
+            x[1, :, 2] = -inf
+            x[2, n - 1, 3] = inf
+            x[2, : n - 1, 5] = -inf
+            check_fwd(x, x, 1, log)
+
+
+@pytest.mark.parametrize("log", [False, True])
 @pytest.mark.parametrize("plan", PLANS[:3])
 def test_nan_inf_slices(log, plan):
     set_plan(plan)
@@ -224,6 +244,10 @@ def test_backward_strided(log):
     check_bwd((3, 50, 20), 1, log, 204)
     check_bwd((300, 70), 0, log, 201)
     check_bwd((50, 80), 1, log, 202, view="T")
+    check_bwd((2, 129, 68), 1, log, 205)   # column slices held in registers
+    check_bwd((2, 256, 64), 1, log, 206)
+    check_bwd((2, 200, 300), 1, log, 208)  # 32-column groups
+    check_bwd((2, 257, 64), 1, log, 207)   # two-pass column kernel
 
 
 # ---- nll_loss ------------------------------------------------------------------------------
