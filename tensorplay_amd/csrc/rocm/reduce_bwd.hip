@@ -121,19 +121,24 @@ __global__ __launch_bounds__(256) void k_red_bwd(RbArgs a) {
 }
 
 // Rows of the innermost merged dim (at least 1024 elements): a workgroup
-// covers 256 * VEC * 4 consecutive outputs of one row (long rows, split in
+// covers 256 * VEC * U consecutive outputs of one row (long rows, split in
 // `chunks` pieces) or of rpb = CH / L whole rows (short rows).  The first rpb
 // threads find the rows' offsets once (into LDS); every thread then issues the
-// loads of its four vectors before any store, so short rows do not serialise
-// on load latency.  INNER: 0 = the innermost dim is reduced (g / mean / result
+// loads of its U vectors before any store, so short rows do not serialise on
+// load latency.  U = 4 for var / std (they read x) and for rows shorter than
+// 4096 elements (a workgroup then covers several rows); U = 1 for sum / mean
+// over long rows, which only write: one 16-byte store per thread over a grid
+// covering the whole output writes faster than several per thread (measured
+// on MI355X, a 256 MiB broadcast: 40 us against 45-52 us with 2-8 stores per
+// thread; with 1024-element rows U = 1 was slower, 65 against 51 us).  INNER: 0 = the innermost dim is reduced (g / mean / result
 // are one value per row), 1 = it is kept with unit stride in the per-output
 // arrays (loaded as vectors beside x).
-template <int OP, int VEC, int INNER>
+template <int OP, int VEC, int INNER, int U>
 __global__ __launch_bounds__(256) void k_red_bwd_rows(RbArgs a, long long chunks, int rpb, long long rows) {
-    constexpr int CH = 256 * VEC * 4;
+    constexpr int CH = 256 * VEC * U;
     constexpr bool XS = OP == B_VAR || OP == B_STD;
     typedef float f32x4 __attribute__((ext_vector_type(4)));
-    __shared__ long long sxo[4], sso[4];
+    __shared__ long long sxo[4], sso[4];  // rpb <= CH / 1024 <= 4
     const int last = a.nd - 1;
     const long long L = a.sizes[last];
     const long long grp = blockIdx.x / chunks;
@@ -155,10 +160,10 @@ __global__ __launch_bounds__(256) void k_red_bwd_rows(RbArgs a, long long chunks
     __syncthreads();
     const long long xs = a.xs[last];
 
-    float gv[4][VEC], mv[4][VEC], rv[4][VEC], xv[4][VEC];
-    long long oo[4];  // output offset of each vector, -1 = none
+    float gv[U][VEC], mv[U][VEC], rv[U][VEC], xv[U][VEC];
+    long long oo[U];  // output offset of each vector, -1 = none
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < U; ++u) {
         const long long e = c0 + ((long long)u * 256 + t) * VEC;
         const long long rr = e / L;
         const long long i = e - rr * L;
@@ -204,7 +209,7 @@ __global__ __launch_bounds__(256) void k_red_bwd_rows(RbArgs a, long long chunks
         }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < U; ++u) {
         if (oo[u] < 0) continue;
         float o[VEC];
 #pragma unroll
@@ -239,25 +244,28 @@ template <int OP>
 int launch_bwd(const RbArgs& a, hipStream_t st) {
     const long long L = a.sizes[a.nd - 1];
     const long long os = a.os[a.nd - 1];
-    if (L >= 1024 && (os == 0 || os == 1)) {
+    if (L >= 1024 && (os == 0 || os == 1) && knobs().general == 0) {
         auto al = [](const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
         // vectors: whole 16-byte groups on every side that is read or written per element
         const bool v4 = L % 4 == 0 && al(a.gi) && (a.xs[a.nd - 1] != 1 || al(a.x)) &&
                         (os == 0 || (al(a.g) && al(a.mean) && al(a.res)));
-        const long long ch = 256LL * (v4 ? 4 : 1) * 4;
+        const int u = (OP == B_VAR || OP == B_STD || L < 4096) ? 4 : 1;
+        const long long ch = 256LL * (v4 ? 4 : 1) * u;
         const long long chunks = (L + ch - 1) / ch;
         const long long rows = a.total / L;
         const int rpb = L < ch ? (int)(ch / L) : 1;  // short rows: several per workgroup
         const long long blocks = (rows + rpb - 1) / rpb * chunks;
         if (blocks <= 0x7fffffffLL) {
             const dim3 gr((unsigned)blocks), bl(256);
+#define TPR_RB_ROWS(VV, II)                                                                                 \
+    if (u == 4) hipLaunchKernelGGL((k_red_bwd_rows<OP, VV, II, 4>), gr, bl, 0, st, a, chunks, rpb, rows);     \
+    else hipLaunchKernelGGL((k_red_bwd_rows<OP, VV, II, 1>), gr, bl, 0, st, a, chunks, rpb, rows);
             if (os == 0) {
-                if (v4) hipLaunchKernelGGL((k_red_bwd_rows<OP, 4, 0>), gr, bl, 0, st, a, chunks, rpb, rows);
-                else hipLaunchKernelGGL((k_red_bwd_rows<OP, 1, 0>), gr, bl, 0, st, a, chunks, rpb, rows);
+                if (v4) { TPR_RB_ROWS(4, 0) } else { TPR_RB_ROWS(1, 0) }
             } else {
-                if (v4) hipLaunchKernelGGL((k_red_bwd_rows<OP, 4, 1>), gr, bl, 0, st, a, chunks, rpb, rows);
-                else hipLaunchKernelGGL((k_red_bwd_rows<OP, 1, 1>), gr, bl, 0, st, a, chunks, rpb, rows);
+                if (v4) { TPR_RB_ROWS(4, 1) } else { TPR_RB_ROWS(1, 1) }
             }
+#undef TPR_RB_ROWS
             return check_launch("tpr_reduce_backward");
         }
     }
