@@ -87,6 +87,10 @@ def test_vector_tiles_full_and_edge(src):
         check(base, t, dst, expect_kind=T | (_capi.COPY_VEC if vec_ok else 0))
         p = base.transpose(2, 0, 1)   # permute: I = merged (2*144), J = 272
         check(base, p, dst, expect_kind=T | (_capi.COPY_VEC if vec_ok else 0))
+        # I = 96 < 128: 4-byte pairs take 64 x 64 tiles instead of 128 x 64
+        base = src_values(rng, src, dst, (3, 96, 208))
+        vec_ok = 96 % (16 // np.dtype(dst).itemsize) == 0
+        check(base, base.transpose(0, 2, 1), dst, expect_kind=T | (_capi.COPY_VEC if vec_ok else 0))
 
 
 def test_ragged_and_tail_shapes():
