@@ -72,6 +72,9 @@ enum tpr_reduce_op {
  *    first index wins ties; NaN never wins, as the reference's strict
  *    compare).  VAR/STD/NORM/MEDIAN: FLOAT32 (FLOAT64 for a FLOAT64 input:
  *    every op but MEDIAN takes FLOAT64 inputs and computes in double).
+ *    Integer and BOOL inputs (every signed and unsigned width) take SUM/PROD
+ *    (INT64 output, wrap-around), MEAN (of the values converted to float32),
+ *    AMAX/AMIN, ARGMAX/ARGMIN (unsigned order for UINT*) and ALL/ANY.
  *    ALL/ANY: BOOL (one byte, 0/1; an element counts as true when it is != 0,
  *    so NaN is true).
  *  - NORM: (sum |x|^p)^(1/p); p = +inf / -inf: max / min of |x| (NaN ignored,

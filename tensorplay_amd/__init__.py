@@ -33,6 +33,9 @@ int8 = DType.int8
 int16 = DType.int16
 int32 = DType.int32
 int64 = DType.int64
+uint16 = DType.uint16
+uint32 = DType.uint32
+uint64 = DType.uint64
 float32 = DType.float32
 float64 = DType.float64
 bool_ = DType.bool

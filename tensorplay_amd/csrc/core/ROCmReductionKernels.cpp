@@ -68,12 +68,13 @@ void require_float_input(const Tensor& self, const char* op) {
 }
 
 // sum/mean/prod, max/min, argmax/argmin and all/any also take Float64, the
-// signed integer dtypes, UInt8 and Bool (the reference instantiates them for
-// every scalar type); UInt16/32/64 have no ROCm kernel.
+// every integer dtype and Bool (the reference instantiates them for every
+// scalar type).
 void require_reducible_input(const Tensor& self, const char* op) {
     switch (self.dtype()) {
         case DType::Float32: case DType::Float64: case DType::UInt8: case DType::Int8: case DType::Int16:
-        case DType::Int32: case DType::Int64: case DType::Bool: break;
+        case DType::Int32: case DType::Int64: case DType::UInt16: case DType::UInt32: case DType::UInt64:
+        case DType::Bool: break;
         default:
             TP_THROW(NotImplementedError, std::string(op) + " not implemented for dtype " + toString(self.dtype()) +
                                               " on ROCm");

@@ -31,6 +31,9 @@ DType dtype_from_numpy(const py::dtype& dt) {
     if (k == 'i' && sz == 2) return DType::Int16;
     if (k == 'i' && sz == 1) return DType::Int8;
     if (k == 'u' && sz == 1) return DType::UInt8;
+    if (k == 'u' && sz == 2) return DType::UInt16;
+    if (k == 'u' && sz == 4) return DType::UInt32;
+    if (k == 'u' && sz == 8) return DType::UInt64;
     if (k == 'b') return DType::Bool;
     TP_THROW(TypeError, "unsupported numpy dtype");
 }
@@ -44,6 +47,9 @@ py::dtype numpy_dtype(DType t) {
         case DType::Int16: return py::dtype::of<int16_t>();
         case DType::Int8: return py::dtype::of<int8_t>();
         case DType::UInt8: return py::dtype::of<uint8_t>();
+        case DType::UInt16: return py::dtype::of<uint16_t>();
+        case DType::UInt32: return py::dtype::of<uint32_t>();
+        case DType::UInt64: return py::dtype::of<uint64_t>();
         case DType::Bool: return py::dtype::of<bool>();
         default: TP_THROW(TypeError, "no numpy dtype for this tensor dtype");
     }

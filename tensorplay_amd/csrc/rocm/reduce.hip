@@ -204,6 +204,7 @@ struct Fin {
     double corr;    // VAR/STD correction
     float p;        // NORM exponent (passed to every op's acc; only NormOp reads it)
     int out_esize;  // bytes per output element (integer amax/amin write the input dtype)
+    int out_umap;   // UInt64 amax/amin: undo the key's top-bit flip
     double inv_p;   // NORM: 1/p
 };
 
@@ -1023,12 +1024,26 @@ struct IntMeanOp {
     __device__ static State shfl(State s, int m) { return {__shfl_xor(s.s, m, kWave)}; }
 };
 
+// Order-preserving signed 64-bit key of an integer element: the value itself,
+// except for UInt64, whose top bit is flipped (so 2^63.. sort above 0..2^63-1);
+// fin_write flips it back for amax / amin (Fin::out_umap).
+template <class T>
+__device__ __forceinline__ long long ikey(T x) {
+    if constexpr (sizeof(T) == 8 && T(-1) > T(0)) return (long long)((unsigned long long)x ^ 0x8000000000000000ull);
+    else return (long long)x;
+}
+
+// Keys of the dtype's lowest and highest values.
 template <class T>
 struct IntLimits {
-    static constexpr long long lo = sizeof(T) == 1 ? (T(-1) < T(0) ? -128LL : 0LL)
+    static constexpr bool U = T(-1) > T(0);
+    static constexpr long long lo = U ? (sizeof(T) == 8 ? (-9223372036854775807LL - 1) : 0LL)
+                                  : sizeof(T) == 1 ? -128LL
                                   : sizeof(T) == 2 ? -32768LL
                                   : sizeof(T) == 4 ? -2147483648LL : (-9223372036854775807LL - 1);
-    static constexpr long long hi = sizeof(T) == 1 ? (T(-1) < T(0) ? 127LL : 255LL)
+    static constexpr long long hi = U ? (sizeof(T) == 1 ? 255LL : sizeof(T) == 2 ? 65535LL
+                                         : sizeof(T) == 4 ? 4294967295LL : 9223372036854775807LL)
+                                  : sizeof(T) == 1 ? 127LL
                                   : sizeof(T) == 2 ? 32767LL
                                   : sizeof(T) == 4 ? 2147483647LL : 9223372036854775807LL;
 };
@@ -1044,7 +1059,7 @@ struct IntArgOp {
     __device__ static Acc init() { return {IS_MAX ? IntLimits<T>::lo : IntLimits<T>::hi, kNone}; }
     template <class I>
     __device__ static void acc(Acc& a, T x, I i, float) {
-        const long long v = (long long)x;
+        const long long v = ikey(x);
         const bool t = IS_MAX ? (v > a.v) : (v < a.v);
         a.v = t ? v : a.v;
         a.i = t ? (IdxT)i : a.i;
@@ -1090,7 +1105,7 @@ __device__ __forceinline__ void fin_write(const ArgSI& s, const Fin& f, void* ou
         case 1: ((unsigned char*)out)[o] = (unsigned char)s.v; break;
         case 2: ((short*)out)[o] = (short)s.v; break;
         case 4: ((int*)out)[o] = (int)s.v; break;
-        default: ((long long*)out)[o] = s.v;
+        default: ((long long*)out)[o] = f.out_umap ? (long long)((unsigned long long)s.v ^ 0x8000000000000000ull) : s.v;
     }
 }
 
@@ -1437,9 +1452,9 @@ __device__ __forceinline__ void fin_write(const ArgSD& s, const Fin& f, void* ou
 int esize_of(int dt) {
     switch (dt) {
         case TPR_UINT8: case TPR_INT8: case TPR_BOOL: return 1;
-        case TPR_INT16: return 2;
-        case TPR_INT32: return 4;
-        case TPR_INT64: case TPR_FLOAT64: return 8;
+        case TPR_INT16: case TPR_UINT16: return 2;
+        case TPR_INT32: case TPR_UINT32: return 4;
+        case TPR_INT64: case TPR_UINT64: case TPR_FLOAT64: return 8;
         default: return 0;
     }
 }
@@ -1601,6 +1616,9 @@ int run_int(const tpr_reduce_desc* d, const Plan& p, const void* in, void* out, 
         case TPR_INT8: return run_int_t<signed char>(d->op, p, in, out, ws, fin, st);
         case TPR_INT16: return run_int_t<short>(d->op, p, in, out, ws, fin, st);
         case TPR_INT32: return run_int_t<int>(d->op, p, in, out, ws, fin, st);
+        case TPR_UINT16: return run_int_t<unsigned short>(d->op, p, in, out, ws, fin, st);
+        case TPR_UINT32: return run_int_t<unsigned int>(d->op, p, in, out, ws, fin, st);
+        case TPR_UINT64: return run_int_t<unsigned long long>(d->op, p, in, out, ws, fin, st);
         default: return run_int_t<long long>(d->op, p, in, out, ws, fin, st);
     }
 }
@@ -1806,6 +1824,7 @@ int tpr_reduce(const tpr_reduce_desc* desc, const void* in, void* out, void* wor
     fin.p = (float)desc->p;
     fin.inv_p = 1.0 / desc->p;
     fin.out_esize = int_in ? esize_of(desc->in_dtype) : 4;
+    fin.out_umap = desc->in_dtype == TPR_UINT64 ? 1 : 0;
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (desc->in_dtype == TPR_FLOAT64) return run_f64(desc, p, in, out, workspace, fin, st);
     if (int_in) return run_int(desc, p, in, out, workspace, fin, st);

@@ -376,7 +376,7 @@ def test_new_ops_config_shapes():
 # the float tolerance, strict-compare max/min/argmax with the first index, x != 0 for
 # all/any), so numpy's own reductions are their closed forms: bit-exact.
 
-INT_DTYPES = ["int32", "int64", "uint8", "int8", "int16", "bool"]
+INT_DTYPES = ["int32", "int64", "uint8", "int8", "int16", "uint16", "uint32", "uint64", "bool"]
 INT_OPS = ["sum", "prod", "mean", "amax", "amin", "argmax", "argmin", "all", "any"]
 
 
@@ -410,6 +410,10 @@ def _int_view_data(rng, dt, shape):
         b = rng.integers(-5, 6, size=shape).astype(dt)  # ties for argmax
         big = rng.integers(info.min // 2, info.max // 2, size=shape, dtype=dt)
         return np.where(rng.random(shape) < 0.5, big, b)  # wrap-around sums / products
+    if dt == "uint64":  # values on both sides of 2^63 (the kernel's key flips the top bit)
+        b = rng.integers(0, 6, size=shape).astype(dt)
+        big = rng.integers(0, info.max, size=shape, dtype=np.uint64, endpoint=True)
+        return np.where(rng.random(shape) < 0.5, big, b)
     return rng.integers(info.min, int(info.max) + 1, size=shape).astype(dt)
 
 
@@ -468,6 +472,16 @@ def test_integer_extremes_and_empty():
     for op in INT_OPS:
         for dims in (None, [0], [1]):
             check_int(x, t, op, dims)
+    u = np.array([[0, 2**63, 2**64 - 1, 2**63 - 1], [2**63 - 1, 2**63, 1, 0], [5, 5, 5, 5]], np.uint64)
+    for op in INT_OPS:
+        for dims in (None, [0], [1]):
+            check_int(u, torch.from_numpy(u).cuda(), op, dims)
+    for dt in ("uint16", "uint32"):
+        info = np.iinfo(dt)
+        w = np.array([[0, info.max, info.max // 2 + 1], [info.max, 0, 1]], dt)
+        for op in INT_OPS:
+            for dims in (None, [0], [1]):
+                check_int(w, torch.from_numpy(w).cuda(), op, dims)
     # all elements at the lowest value: argmax stays at index 0 (strict compare)
     y = np.full(1000, np.iinfo(np.int32).min, np.int32)
     assert int(_capi.reduce(torch.from_numpy(y).cuda(), "argmax", None).cpu()) == 0

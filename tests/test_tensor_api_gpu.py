@@ -127,6 +127,12 @@ def test_dims_dtypes_and_errors():
     assert i.max().dtype == tp.int32 and i.max().item() == 9
     np.testing.assert_array_equal(i.argmax(1).numpy(), [2, 1])  # first of the tied 9s
     np.testing.assert_array_equal(i.sum([0]).numpy(), [5, 2, 14])
+    # unsigned 64-bit: values above 2^63 order as unsigned; sum wraps as Int64
+    u = tp.tensor(np.array([[1, 2**63 + 5, 7], [2**64 - 1, 3, 2**63]], np.uint64), device=DEV)
+    assert u.max().dtype == tp.uint64 and int(u.max().numpy()) == 2**64 - 1
+    np.testing.assert_array_equal(u.argmax(1).numpy(), [1, 0])
+    np.testing.assert_array_equal(u.min([1]).numpy(), np.array([1, 3], np.uint64))
+    assert u.sum().item() == int(np.array([1, 2**63 + 5, 7, 2**64 - 1, 3, 2**63], np.uint64).astype(np.int64).sum())
     # strided (non-contiguous) inputs reduce without a copy
     p = t.permute([2, 0, 1])
     np.testing.assert_allclose(p.mean(1).numpy(), a.transpose(2, 0, 1).astype(np.float64).mean(1), rtol=1e-5)
