@@ -158,9 +158,9 @@ def reduce_bwd_call(torch, capi, x, op, dims, stream, g, res=None):
                                      ctypes.c_void_p(res.data_ptr() if res is not None else 0),
                                      ctypes.c_void_p(gi.data_ptr()), ctypes.c_void_p(ws.data_ptr()), wsb, stream))
     c.keep = (desc, gi, ws, g, res)
-    # algorithmic bytes: write the gradient; var / std also read x twice (the mean's
-    # reduction pass and the gradient pass), as the mean is not an input
-    c.bytes = x.numel() * 4 * (3 if op in ("var", "std") else 1)
+    # algorithmic bytes: write the gradient; var / std also read x once (the
+    # least any implementation reads: the mean is not an input)
+    c.bytes = x.numel() * 4 * (2 if op in ("var", "std") else 1)
     return c
 
 

@@ -233,6 +233,92 @@ __global__ __launch_bounds__(256) void k_red_bwd_rows(RbArgs a, long long chunks
     }
 }
 
+// VAR / STD over one innermost reduced run (unit stride in x, 16-byte
+// aligned, length L % 4 == 0, L <= 256 * V, every other dim kept): one wave per
+// row holds the row in registers (V float4 per lane), forms the row's mean
+// itself (fp32 lane sums combined in fp64, then / count as tpr_reduce's MEAN)
+// and writes the gradient from registers, so x is read once instead of twice
+// (the MEAN pass and the gradient pass).
+template <int OP, int V>
+__global__ __launch_bounds__(256) void k_vs_bwd_rows(RbArgs a, long long rows) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63;
+    const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // uniform per wave; no barriers below
+    const int last = a.nd - 1;
+    const int q = (int)(a.sizes[last] >> 2);  // float4 per row
+    long long xo = 0, so = 0, r = row;
+    for (int d = last - 1; d >= 0; --d) {
+        const long long c = r % a.sizes[d];
+        r /= a.sizes[d];
+        xo += c * a.xs[d];
+        so += c * a.os[d];
+    }
+    const f32x4* px = reinterpret_cast<const f32x4*>(a.x + xo);
+    f32x4 v[V];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int e = j * 64 + lane;
+        if (e < q) {
+            v[j] = __builtin_nontemporal_load(px + e);
+            s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+        }
+    }
+    double sd = s;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sd += __shfl_xor(sd, o, 64);
+    const float mean = (float)(sd / a.count);
+    const float g = a.g[so];
+    const float rs = OP == B_STD ? a.res[so] : 0.0f;
+    f32x4* po = reinterpret_cast<f32x4*>(a.gi + row * (long long)a.sizes[last]);
+    auto f = [&](float x) -> float {
+        if constexpr (OP == B_VAR) {
+            const float tt = (g * 2.0f) * (x - mean);
+            return (float)((double)tt / a.denom);
+        } else {
+            const float tt = g * (x - mean);
+            return tt / (rs * a.denom_f);
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int e = j * 64 + lane;
+        if (e < q) {
+            const f32x4 o = {f(v[j].x), f(v[j].y), f(v[j].z), f(v[j].w)};
+            __builtin_nontemporal_store(o, po + e);
+        }
+    }
+}
+
+// Rows of one fused VAR / STD gradient (k_vs_bwd_rows); false when the layout
+// does not fit it.
+template <int OP>
+bool launch_vs_rows(const RbArgs& a, hipStream_t st) {
+    const int last = a.nd - 1;
+    const long long L = a.sizes[last];
+    if (a.os[last] != 0 || a.xs[last] != 1 || L % 4 != 0 || L > 4096 || knobs().general != 0) return false;
+    for (int d = 0; d < last; ++d)
+        if (a.os[d] == 0) return false;  // another reduced dim: the mean spans more than one run
+    auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if (!al(a.x) || !al(a.gi)) return false;
+    for (int d = 0; d < last; ++d)
+        if (a.xs[d] % 4 != 0) return false;  // every row start 16-byte aligned
+    const long long rows = a.total / L;
+    const long long blocks = (rows + 3) / 4;
+    if (blocks > 0x7fffffffLL) return false;
+    const int v = L <= 256 ? 1 : L <= 512 ? 2 : L <= 1024 ? 4 : L <= 2048 ? 8 : 16;
+    const dim3 gr((unsigned)blocks), bl(256);
+    switch (v) {
+        case 1: hipLaunchKernelGGL((k_vs_bwd_rows<OP, 1>), gr, bl, 0, st, a, rows); break;
+        case 2: hipLaunchKernelGGL((k_vs_bwd_rows<OP, 2>), gr, bl, 0, st, a, rows); break;
+        case 4: hipLaunchKernelGGL((k_vs_bwd_rows<OP, 4>), gr, bl, 0, st, a, rows); break;
+        case 8: hipLaunchKernelGGL((k_vs_bwd_rows<OP, 8>), gr, bl, 0, st, a, rows); break;
+        default: hipLaunchKernelGGL((k_vs_bwd_rows<OP, 16>), gr, bl, 0, st, a, rows); break;
+    }
+    return true;
+}
+
 // MEAN: q[o] = (float)((double)g[o] / count) once per output (the gradient is
 // then a broadcast of q, as for SUM).
 __global__ __launch_bounds__(256) void k_mean_scale(const float* g, float* q, long long n, double count) {
@@ -372,12 +458,6 @@ extern "C" int tpr_reduce_backward(const tpr_reduce_desc* d, const void* grad_ou
         const size_t need = tpr_reduce_backward_workspace_bytes(d);
         if (!workspace || workspace_bytes < need)
             return fail(TPR_ERR_WORKSPACE, "tpr_reduce_backward: workspace smaller than tpr_reduce_backward_workspace_bytes");
-        const tpr_reduce_desc m = mean_desc(d);
-        float* mean = static_cast<float*>(workspace);
-        const size_t moff = align256((size_t)kept_count(d) * sizeof(float));
-        const int rc = tpr_reduce(&m, in, mean, static_cast<char*>(workspace) + moff, workspace_bytes - moff, stream);
-        if (rc != TPR_OK) return rc;
-        a.mean = mean;
     }
 
     // per-output strides: dense row-major over the kept dims
@@ -418,6 +498,18 @@ extern "C" int tpr_reduce_backward(const tpr_reduce_desc* d, const void* grad_ou
         nd = 1;
     }
     a.nd = nd;
+    if (d->op == TPR_VAR || d->op == TPR_STD) {
+        // one pass when the reduced run fits a wave's registers, else the
+        // MEAN reduction into the workspace and the streaming gradient pass
+        const bool fused = d->op == TPR_VAR ? launch_vs_rows<B_VAR>(a, st) : launch_vs_rows<B_STD>(a, st);
+        if (fused) return check_launch("tpr_reduce_backward (var/std rows)");
+        const tpr_reduce_desc m = mean_desc(d);
+        float* mean = static_cast<float*>(workspace);
+        const size_t moff = align256((size_t)kept_count(d) * sizeof(float));
+        const int rc = tpr_reduce(&m, in, mean, static_cast<char*>(workspace) + moff, workspace_bytes - moff, stream);
+        if (rc != TPR_OK) return rc;
+        a.mean = mean;
+    }
     switch (d->op) {
         case TPR_SUM: return launch_bwd<B_SUM>(a, st);
         case TPR_MEAN: return launch_bwd<B_MEAN>(a, st);

@@ -43,6 +43,25 @@ def check(base, v, op, dims, correction, seed):
         assert e_gpu <= 1.0
 
 
+@pytest.mark.parametrize("op", ["var", "std"])
+def test_var_std_rows_in_registers(op):
+    # an innermost reduced run of <= 4096 elements (multiple of 4, aligned):
+    # one wave per row computes the mean itself and writes the gradient from
+    # registers (1, 2, 4, 8 or 16 float4 per lane, partial last vectors)
+    rng = np.random.default_rng(9)
+    cases = []
+    for shape, dims in [((16, 4096), [1]), ((9, 260), [1]), ((3, 5, 8), [2]), ((4, 6, 512), [-1]),
+                        ((2, 3, 2048), [2]), ((5, 1028), [1])]:
+        b = (rng.standard_normal(shape) * 3 + 1).astype(np.float32)
+        cases.append((b, b, dims))
+    b = (rng.standard_normal((6, 10, 132)) * 2).astype(np.float32)
+    cases.append((b, b[:, ::2, :128], [2]))   # stepped kept dim, row starts 16-byte aligned
+    cases.append((b, b[:, :, 4:], [2]))       # rows of 128 from an aligned offset
+    for i, (base, v, dims) in enumerate(cases):
+        for c in (0, 1):
+            check(base, v, op, dims, c, 300 + i)
+
+
 @pytest.mark.parametrize("op", ["sum", "mean", "var", "std"])
 def test_shapes_and_layouts(op):
     rng = np.random.default_rng(7)
