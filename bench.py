@@ -381,10 +381,11 @@ def main():
             ms = time_calls(torch, cs, max(steps, 10), warmup)
             esm[name] = rate(ms, cs[0].bytes)
             del cs
-        cs = [softmax_call(torch, capi, b5[i], -1, capi.SOFTMAX_BWD, stream, y=b5[i + 1]) for i in (0, 2)]
-        ms = time_calls(torch, cs, max(steps, 10), warmup)
-        esm["softmax_backward"] = rate(ms, cs[0].bytes)
-        del cs
+        for name, mode in (("softmax_backward", capi.SOFTMAX_BWD), ("log_softmax_backward", capi.LOG_SOFTMAX_BWD)):
+            cs = [softmax_call(torch, capi, b5[i], -1, mode, stream, y=b5[i + 1]) for i in (0, 2)]
+            ms = time_calls(torch, cs, max(steps, 10), warmup)
+            esm[name] = rate(ms, cs[0].bytes)
+            del cs
         tgt = torch.randint(0, 151936, (256,), device=dev, dtype=torch.int64)
         one = torch.ones((), device=dev)
         tw = torch.full((1,), 256.0, device=dev)

@@ -273,13 +273,16 @@ __global__ __launch_bounds__(1024) void k_smx_rows2(SmxArgs p) {
     float* po = p.out + row * p.n;
     const int t = threadIdx.x;
 
-    auto load = [&](float (&xa)[U][VW], float (&xb)[UB][VW], long long base, int nt) {
+    // wb: also load y (pass 1 of the log_softmax gradient needs g only)
+    auto load = [&](float (&xa)[U][VW], float (&xb)[UB][VW], long long base, int nt, bool wb) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const long long e = base + ((long long)u * T + t) * VW;
             if (e < n) {
                 Vec<VW>::load(xa[u], pa + e, nt);
-                if constexpr (BW) Vec<VW>::load(xb[u], pb + e, nt);
+                if constexpr (BW) {
+                    if (wb) Vec<VW>::load(xb[u], pb + e, nt);
+                }
             } else {
 #pragma unroll
                 for (int c = 0; c < VW; ++c) {
@@ -302,13 +305,14 @@ __global__ __launch_bounds__(1024) void k_smx_rows2(SmxArgs p) {
                 for (int c = 0; c < VW; ++c) s += (MODE == BWD) ? xa[u][c] * xb[u][c] : xa[u][c];
         }
     };
-    load(a0, b0, 0, 0);
+    constexpr bool WB1 = MODE == BWD;  // pass 1 reads y
+    load(a0, b0, 0, 0, WB1);
     for (long long base = 0;;) {
-        if (base + TILE < n) load(a1, b1, base + TILE, 0);
+        if (base + TILE < n) load(a1, b1, base + TILE, 0, WB1);
         consume(a0, b0);
         base += TILE;
         if (base >= n) break;
-        if (base + TILE < n) load(a0, b0, base + TILE, 0);
+        if (base + TILE < n) load(a0, b0, base + TILE, 0, WB1);
         consume(a1, b1);
         base += TILE;
         if (base >= n) break;
@@ -340,13 +344,13 @@ __global__ __launch_bounds__(1024) void k_smx_rows2(SmxArgs p) {
             }
         }
     };
-    load(a0, b0, 0, p.nt);
+    load(a0, b0, 0, p.nt, true);
     for (long long base = 0;;) {
-        if (base + TILE < n) load(a1, b1, base + TILE, p.nt);
+        if (base + TILE < n) load(a1, b1, base + TILE, p.nt, true);
         emit(a0, b0, base);
         base += TILE;
         if (base >= n) break;
-        if (base + TILE < n) load(a0, b0, base + TILE, p.nt);
+        if (base + TILE < n) load(a0, b0, base + TILE, p.nt, true);
         emit(a1, b1, base);
         base += TILE;
         if (base >= n) break;
@@ -491,7 +495,7 @@ __global__ __launch_bounds__(256) void k_smx_part(SmxArgs p) {
             const long long e = c0 + it * STEP + ((long long)u * 256 + t) * VW;
             if (e < p.n) {
                 Vec<VW>::load(x[u], pa + e, 0);
-                if constexpr (BW) Vec<VW>::load(y[u], pb + e, 0);
+                if constexpr (MODE == BWD) Vec<VW>::load(y[u], pb + e, 0);  // BWD_LOG: sum(g) needs no y
             } else {
 #pragma unroll
                 for (int c = 0; c < VW; ++c) {
@@ -688,7 +692,7 @@ __global__ __launch_bounds__(kWave * BY) void k_smx_cols4(SmxColArgs p) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             Vec<4>::load(x[u], pa + (r + (long long)u * RS) * p.a_sn, 0);
-            if constexpr (BW) Vec<4>::load(y[u], pb + (r + (long long)u * RS) * p.b_sn, 0);
+            if constexpr (MODE == BWD) Vec<4>::load(y[u], pb + (r + (long long)u * RS) * p.b_sn, 0);
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -706,7 +710,7 @@ __global__ __launch_bounds__(kWave * BY) void k_smx_cols4(SmxColArgs p) {
     for (; r < n; r += RS) {
         float x[4], y[4];
         Vec<4>::load(x, pa + r * p.a_sn, 0);
-        if constexpr (BW) Vec<4>::load(y, pb + r * p.b_sn, 0);
+        if constexpr (MODE == BWD) Vec<4>::load(y, pb + r * p.b_sn, 0);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             if constexpr (!BW) ms_add<1>(m[q], sm[q], &x[q]);
