@@ -463,6 +463,100 @@ __global__ __launch_bounds__(kResT) void k_smx_res(SmxArgs p, int vl) {
         __builtin_amdgcn_raw_buffer_store_b128(outq(lds[j * kResT + t]), bo, ((kResVR + j) * kResT + t) * 16, 0, aux);
 }
 
+// The gradients on the same layout, with g held on chip (registers + LDS):
+//   log_softmax (BWD_LOG): gx = g - exp(y) * sum(g): the sum comes from the
+//     held g, then y streams past once: g, y and gx each cross HBM once;
+//   softmax (BWD): gx = (g - sum(g * y)) * y: y streams past twice (the dot,
+//     then the output), g once: four transfers where the two-pass kernel
+//     makes five.
+template <int MODE, int NT, int kResVR>
+__global__ __launch_bounds__(kResT) void k_smx_res_bwd(SmxArgs p, int vl) {
+    extern __shared__ f32x4 lds[];
+    __shared__ float sh[kResT / kWave];
+    constexpr int aux = NT ? 2 : 0;
+    const int t = threadIdx.x;
+    const long long row = blockIdx.x;
+    const float* ra = p.a + row * p.sa;
+    const float* rb = p.b + row * p.sb;
+    float* ro = p.out + row * p.n;
+    const int nb = (int)(p.n * 4);
+    const __amdgpu_buffer_rsrc_t ba = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(ra), (short)0, nb, kBufWord3);
+    const __amdgpu_buffer_rsrc_t bb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(rb), (short)0, nb, kBufWord3);
+    const __amdgpu_buffer_rsrc_t bo = __builtin_amdgcn_make_buffer_rsrc(ro, (short)0, nb, kBufWord3);
+    const int q = (int)(p.n >> 2);
+    const int wbase = t & ~(kWave - 1);
+    const f32x4* pa = reinterpret_cast<const f32x4*>(ra);
+    for (int j = 0; j < vl; ++j) {
+        const int v = (kResVR + j) * kResT + t;
+        if (v < q)
+            __builtin_amdgcn_global_load_lds(
+                (const void*)(pa + v),
+                (__attribute__((address_space(3))) void*)(lds + j * kResT + wbase), 16, 0, 0);
+    }
+    f32x4 r[kResVR];
+#pragma unroll
+    for (int j = 0; j < kResVR; ++j) r[j] = __builtin_amdgcn_raw_buffer_load_b128(ba, (j * kResT + t) * 16, 0, aux);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the LDS loads have landed
+    __syncthreads();
+    auto vs = [](f32x4 x) { return (x.x + x.y) + (x.z + x.w); };
+    auto vd = [](f32x4 x, f32x4 y) { return (x.x * y.x + x.y * y.y) + (x.z * y.z + x.w * y.w); };
+    float s = 0.0f;
+    // BWD: the dot's y loads go in blocks of YB vectors per lane, each block in
+    // its own basic block behind an opaque always-true test, so the compiler
+    // cannot hoist every y load next to the held g (that spills)
+    constexpr int YB = kResVR >= 56 ? 2 : 4;
+    int live = 1;
+    if constexpr (MODE == BWD) asm volatile("s_mov_b32 %0, 1" : "=s"(live));
+#pragma unroll
+    for (int g = 0; g < kResVR / 8; ++g) {
+        float gs = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 8 / YB; ++h) {
+            if constexpr (MODE == BWD_LOG) {
+#pragma unroll
+                for (int j = 0; j < YB; ++j) gs += vs(r[8 * g + YB * h + j]);
+            } else if (live) {
+                f32x4 y[YB];
+#pragma unroll
+                for (int j = 0; j < YB; ++j)
+                    y[j] = __builtin_amdgcn_raw_buffer_load_b128(bb, ((8 * g + YB * h + j) * kResT + t) * 16, 0, 0);
+#pragma unroll
+                for (int j = 0; j < YB; ++j) gs += vd(r[8 * g + YB * h + j], y[j]);
+                asm volatile("" : "+v"(gs));
+            }
+        }
+        s += gs;
+    }
+    float sl = 0.0f;
+    for (int j = 0; j < vl; ++j) {
+        const int v = (kResVR + j) * kResT + t;
+        if (v < q) {
+            if constexpr (MODE == BWD_LOG) sl += vs(lds[j * kResT + t]);
+            else sl += vd(lds[j * kResT + t], __builtin_amdgcn_raw_buffer_load_b128(bb, v * 16, 0, 0));
+        }
+    }
+    s = grp<kResT, false>(s + sl, sh);
+    // an opaque zero soffset for the output pass's y loads: otherwise the
+    // compiler reuses the dot pass's loads (and products) and keeps them live
+    // next to g, which spills
+    int z0 = 0;
+    if constexpr (MODE == BWD) asm volatile("s_mov_b32 %0, 0" : "=s"(z0));
+    auto outq = [&](f32x4 g, f32x4 y) -> f32x4 {
+        return f32x4{outv<MODE>(g.x, y.x, s, 0.0f), outv<MODE>(g.y, y.y, s, 0.0f),
+                     outv<MODE>(g.z, y.z, s, 0.0f), outv<MODE>(g.w, y.w, s, 0.0f)};
+    };
+#pragma unroll
+    for (int j = 0; j < kResVR; ++j) {
+        const f32x4 y = __builtin_amdgcn_raw_buffer_load_b128(bb, (j * kResT + t) * 16, z0, aux);
+        __builtin_amdgcn_raw_buffer_store_b128(outq(r[j], y), bo, (j * kResT + t) * 16, 0, aux);
+    }
+    for (int j = 0; j < vl; ++j) {
+        const int off = ((kResVR + j) * kResT + t) * 16;
+        const f32x4 y = __builtin_amdgcn_raw_buffer_load_b128(bb, off, z0, aux);
+        __builtin_amdgcn_raw_buffer_store_b128(outq(lds[j * kResT + t], y), bo, off, 0, aux);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Split long rows (few rows, e.g. LLM vocabulary logits): each row is cut into
 // kChunk-element chunks, one 256-thread workgroup per (row, chunk) in both
@@ -970,12 +1064,17 @@ int launch_res_vr(const SmxArgs& a, hipStream_t st) {
     const long long jl = (q + kResT - 1) / kResT;  // float4 per lane
     const int vl = (int)std::max(0LL, jl - VR);
     const size_t lds_bytes = (size_t)vl * kResT * 16;
+    constexpr bool BW = MODE >= BWD;
+    const void* fn = BW ? reinterpret_cast<const void*>(&k_smx_res_bwd<BW ? MODE : BWD, NT, VR>)
+                        : reinterpret_cast<const void*>(&k_smx_res<BW ? FWD : MODE, NT, VR>);
     if (lds_bytes > 65536) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_smx_res<MODE, NT, VR>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
+        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
         if (e != hipSuccess) return fail(TPR_ERR_HIP, std::string("tpr_softmax: LDS attribute: ") + hipGetErrorString(e));
     }
-    hipLaunchKernelGGL((k_smx_res<MODE, NT, VR>), dim3((unsigned)a.rows), dim3(kResT), lds_bytes, st, a, vl);
+    if constexpr (BW)
+        hipLaunchKernelGGL((k_smx_res_bwd<MODE, NT, VR>), dim3((unsigned)a.rows), dim3(kResT), lds_bytes, st, a, vl);
+    else
+        hipLaunchKernelGGL((k_smx_res<MODE, NT, VR>), dim3((unsigned)a.rows), dim3(kResT), lds_bytes, st, a, vl);
     return check_launch("tpr_softmax (rows in registers + LDS)");
 }
 
@@ -1005,9 +1104,10 @@ int run_rows(const SmxArgs& a0, int vw, hipStream_t st) {
         if (rc >= 0) return rc;
     }
     constexpr bool BW = MODE >= BWD;
-    if constexpr (!BW) {
+    {
         // one row per CU in registers + LDS (read once) unless the rows are
         // too few to fill the chip, where the split kernels spread each row
+        // (forward: x held; gradients: g held, y streamed)
         if (!two_pass && !a.part && vw == 4 && a.n <= kResMax && knobs().smx_res >= 0) {
             int vr = 0;
             for (int c : {56, 40, 24, 8})

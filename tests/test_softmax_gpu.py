@@ -238,6 +238,18 @@ def test_backward_rows(log, plan):
 
 
 @pytest.mark.parametrize("log", [False, True])
+@pytest.mark.parametrize("res", [0, -1])
+def test_backward_long_rows(log, res):
+    # softmax / log_softmax gradients over rows of 32769..153600: g held in
+    # registers + LDS while y streams (res=0; once for log_softmax, twice for
+    # softmax), or the two-pass kernel (res=-1)
+    _capi.debug_set("smx_split", -1)
+    _capi.debug_set("smx_res", res)
+    for i, n in enumerate([32772, 50260, 114688, 151936, 153600]):
+        check_bwd((3, n), 1, log, 400 + i)
+
+
+@pytest.mark.parametrize("log", [False, True])
 def test_backward_strided(log):
     check_bwd((4, 300, 33), 1, log, 200)
     check_bwd((4, 300, 64), 1, log, 203)
