@@ -164,12 +164,17 @@ __device__ __forceinline__ float nll_grad_value(const NllBwdArgs& a, long long i
     return -w * g;
 }
 
-// Rows of at least 1024 elements: workgroup (row, chunk) writes 4096
-// consecutive elements of one row with 16-byte stores (VW = 4) or 1024 with
-// scalar stores (VW = 1).
+// Rows of at least 1024 elements: workgroup (row, chunk) writes 256 * kNllU
+// 16-byte vectors (VW = 4) or scalars (VW = 1) of one row.
+// Vectors each thread of the row kernel writes: one (a write-only kernel runs
+// fastest with one 16-byte store per thread over a grid covering the output:
+// measured on MI355X, a 256 MiB fill takes 40 us against 45-52 us with 2-8
+// stores per thread).
+constexpr int kNllU = 1;
+
 template <int VW>
 __global__ __launch_bounds__(kNllBlock) void k_nll_bwd_rows(NllBwdArgs a) {
-    constexpr long long CH = (long long)kNllBlock * 4 * VW;
+    constexpr long long CH = (long long)kNllBlock * kNllU * VW;
     const long long row = blockIdx.x / a.chunks;
     const long long base = (blockIdx.x - row * a.chunks) * CH;
     const long long t = a.t[row * a.ts];
@@ -177,7 +182,7 @@ __global__ __launch_bounds__(kNllBlock) void k_nll_bwd_rows(NllBwdArgs a) {
     const float v = hit ? nll_grad_value(a, row, t) : 0.0f;
     float* out = a.gi + row * a.c;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kNllU; ++u) {
         const long long e = base + ((long long)u * kNllBlock + threadIdx.x) * VW;
         if (e >= a.c) break;
         if constexpr (VW == 4) {
@@ -260,7 +265,7 @@ extern "C" int tpr_nll_loss_backward(const void* grad_output, int64_t gs, const 
                  n, c, reduction, ignore_index, static_cast<float*>(grad_input), 0};
     if (c >= 1024) {
         const bool v4 = c % 4 == 0 && (reinterpret_cast<uintptr_t>(grad_input) & 15) == 0;
-        const long long ch = (long long)kNllBlock * 4 * (v4 ? 4 : 1);
+        const long long ch = (long long)kNllBlock * kNllU * (v4 ? 4 : 1);
         a.chunks = (c + ch - 1) / ch;
         const long long blocks = n * a.chunks;
         if (blocks > 0x7fffffffLL) return fail(TPR_ERR_INVALID_ARG, "tpr_nll_loss_backward: too large");
