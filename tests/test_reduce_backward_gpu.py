@@ -44,7 +44,7 @@ def check(base, v, op, dims, correction, seed):
 
 
 @pytest.mark.parametrize("op", ["var", "std"])
-def test_var_std_rows_in_registers(op):
+def test_var_std_slices_in_registers(op):
     # an innermost reduced run of <= 4096 elements (multiple of 4, aligned):
     # one wave per row computes the mean itself and writes the gradient from
     # registers (1, 2, 4, 8 or 16 float4 per lane, partial last vectors)
@@ -57,6 +57,12 @@ def test_var_std_rows_in_registers(op):
     b = (rng.standard_normal((6, 10, 132)) * 2).astype(np.float32)
     cases.append((b, b[:, ::2, :128], [2]))   # stepped kept dim, row starts 16-byte aligned
     cases.append((b, b[:, :, 4:], [2]))       # rows of 128 from an aligned offset
+    # a reduced middle dim of <= 1024 rows over a kept contiguous inner dim:
+    # column slices held in registers (8 or 16 waves, 4..32 rows per lane)
+    for shape, dims in [((4, 300, 64), [1]), ((3, 1000, 68), [1]), ((700, 36), [0]), ((2, 513, 128), [1]),
+                        ((2, 1024, 8), [1]), ((5, 100, 200), [1]), ((3, 129, 12), [1])]:
+        b2 = (rng.standard_normal(shape) * 3 + 1).astype(np.float32)
+        cases.append((b2, b2, dims))
     for i, (base, v, dims) in enumerate(cases):
         for c in (0, 1):
             check(base, v, op, dims, c, 300 + i)
