@@ -14,12 +14,14 @@
 //
 // The reference materialises max, shifted, exp and sum tensors (five passes
 // and three temporaries).  Here one kernel does it:
-//   * rows that fit in registers (up to 32768 floats per 1024-thread
-//     workgroup) are read once and written once -- k_smx_rows;
-//   * forward rows up to 153600 floats stay on one CU, in registers plus
-//     LDS, and are also read once -- k_smx_res;
-//   * longer rows (and backward rows beyond registers) stream twice: an
-//     online (max, sum-of-exp) pass, then the output pass -- k_smx_rows2;
+//   * rows shorter than 16384 floats (or a few long rows, up to 32768)
+//     stay in registers: read once and written once -- k_smx_rows;
+//   * rows of 16384..153600 floats, at least one per CU, stay on one CU in
+//     registers plus LDS and are also read once -- k_smx_res (forward),
+//     k_smx_res_bwd (gradients: g held, y streamed);
+//   * longer rows stream twice: an online (max, sum-of-exp) pass, then the
+//     output pass -- k_smx_rows2, or split over (row, chunk) workgroups when
+//     the rows are fewer than the CUs -- k_smx_part / k_smx_apply;
 //   * a strided softmax dim (inner extent > 1, or a non-unit dim stride)
 //     keeps one column per lane, thread rows across the dim, an LDS merge of
 //     the per-wave states, and also streams twice -- k_smx_cols.
@@ -358,12 +360,12 @@ __global__ __launch_bounds__(1024) void k_smx_rows2(SmxArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// Rows too long for the register-only kernel but short enough for one CU
-// (32769 to 153600 floats, e.g. LLM vocabularies of 50K-152K): one 512-thread
+// Rows of 16384 to 153600 floats (e.g. LLM vocabularies of 32K-152K), short
+// enough for one CU: one 512-thread
 // workgroup per row holds the row in registers (kResVR float4 per lane) plus
 // LDS (the remaining vl float4 per lane, loaded straight from global memory
 // into LDS without passing through registers).  Read once, write once, where
-// the two-pass kernel reads twice.  Forward only.
+// the two-pass kernel reads twice.  Forward here; gradients k_smx_res_bwd.
 //   vector v = j * 512 + t of the row is register r[j] of thread t for
 //   j < kResVR, and lds[(j - kResVR) * 512 + t] after that.
 // ---------------------------------------------------------------------------
@@ -372,7 +374,7 @@ constexpr int kResLdsMax = 160 * 1024;           // LDS of one gfx950 workgroup
 constexpr int kResVLMax = kResLdsMax / (kResT * 16) - 1;  // float4 per lane in LDS (19; 4 KB spare)
 // VR = float4 per lane in registers: 56 (224 VGPRs), 40, 24 or 8.  A kernel
 // with VR takes rows of VR * 2048 .. (VR + 19) * 2048 floats; together they
-// cover 16384 .. 153600.
+// cover 16384 .. 153600 (the largest VR whose minimum the row reaches).
 constexpr long long res_min(int vr) { return (long long)kResT * 4 * vr; }
 constexpr long long res_max(int vr) { return (long long)kResT * 4 * (vr + kResVLMax); }
 constexpr long long kResMax = res_max(56);       // 153600 floats
@@ -1099,22 +1101,23 @@ template <int MODE>
 int run_rows(const SmxArgs& a0, int vw, hipStream_t st) {
     SmxArgs a = a0;
     const int two_pass = knobs().smx_two_pass;
+    // rows of 16384..153600 floats, at least one per CU: one row per CU in
+    // registers + LDS (forward: x held; gradients: g held, y streamed).
+    // Measured on MI355X at [1024, 32768] against the register-only kernels:
+    // softmax 44.6 vs 48.8 us, log_softmax 43.6 vs 50.7 us, their gradients
+    // 74.6 / 68.0 vs 79.2 / 80.9 us.  Fewer rows than CUs take the split
+    // (row, chunk) kernels below, which use the whole chip.
+    if (!two_pass && knobs().smx_res >= 0 && !a.part && vw == 4 && a.n >= res_min(8) && a.n <= kResMax) {
+        int vr = 0;
+        for (int c : {56, 40, 24, 8})
+            if (vr == 0 && a.n >= res_min(c)) vr = c;
+        return launch_res<MODE>(a, vr, st);
+    }
     if (!two_pass) {
         const int rc = rows_single<MODE>(a, vw, st);
         if (rc >= 0) return rc;
     }
     constexpr bool BW = MODE >= BWD;
-    {
-        // one row per CU in registers + LDS (read once) unless the rows are
-        // too few to fill the chip, where the split kernels spread each row
-        // (forward: x held; gradients: g held, y streamed)
-        if (!two_pass && !a.part && vw == 4 && a.n <= kResMax && knobs().smx_res >= 0) {
-            int vr = 0;
-            for (int c : {56, 40, 24, 8})
-                if (vr == 0 && a.n >= res_min(c)) vr = c;
-            if (vr) return launch_res<MODE>(a, vr, st);
-        }
-    }
     if (a.part) {
         const long long blocks = a.rows * a.chunks;
         if (vw == 4) {

@@ -140,7 +140,7 @@ def test_nan_inf_slices(log, plan):
 @pytest.mark.parametrize("log", [False, True])
 @pytest.mark.parametrize("res", [0, -1])
 def test_rows_held_in_registers_and_lds(log, res):
-    # rows of 32769..153600 floats (vocabulary-sized): one 512-thread workgroup
+    # rows of 16384..153600 floats (vocabulary-sized): one 512-thread workgroup
     # per row keeps 8, 24, 40 or 56 float4 per lane in registers and the rest
     # in LDS (res=0), at the edges of each kernel's range; res=-1 sends the
     # same rows through the two-pass kernel.
@@ -148,8 +148,8 @@ def test_rows_held_in_registers_and_lds(log, res):
     _capi.debug_set("smx_res", res)
     inf, nan = np.inf, np.nan
     rng = np.random.default_rng(16)
-    for n in (32772, 40000, 49152, 50260, 55296, 65536, 81920, 88064, 100000, 114688, 114692, 128256, 131072,
-              151936, 153596, 153600):
+    for n in (16384, 20000, 32768, 32772, 40000, 49152, 50260, 55296, 65536, 81920, 88064, 100000, 114688, 114692,
+              128256, 131072, 151936, 153596, 153600):
         x = (rng.standard_normal((9, n)) * 3).astype(np.float32)
         x[0, n - 1] = nan            # NaN in the LDS part
         x[1, 5] = nan                # NaN in the register part
@@ -240,12 +240,12 @@ def test_backward_rows(log, plan):
 @pytest.mark.parametrize("log", [False, True])
 @pytest.mark.parametrize("res", [0, -1])
 def test_backward_long_rows(log, res):
-    # softmax / log_softmax gradients over rows of 32769..153600: g held in
+    # softmax / log_softmax gradients over rows of 16384..153600: g held in
     # registers + LDS while y streams (res=0; once for log_softmax, twice for
     # softmax), or the two-pass kernel (res=-1)
     _capi.debug_set("smx_split", -1)
     _capi.debug_set("smx_res", res)
-    for i, n in enumerate([32772, 50260, 114688, 151936, 153600]):
+    for i, n in enumerate([16384, 20000, 32772, 50260, 114688, 151936, 153600]):
         check_bwd((3, n), 1, log, 400 + i)
 
 
