@@ -162,6 +162,9 @@ def test_rows_held_in_registers_and_lds(log, res):
     # a row longer than the resident capacity goes to the two-pass kernel
     x = rng.standard_normal((3, 153604)).astype(np.float32)
     check_fwd(x, x, 1, log)
+    # rows that are a window of wider rows (row stride 20004 > n = 20000)
+    w = (rng.standard_normal((4, 20004)) * 3).astype(np.float32)
+    check_fwd(w, w[:, :20000], 1, log)
 
 
 def test_large_logits_c5_shape():
