@@ -31,6 +31,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <string>
 
@@ -1070,8 +1071,19 @@ int launch_res_vr(const SmxArgs& a, hipStream_t st) {
     const void* fn = BW ? reinterpret_cast<const void*>(&k_smx_res_bwd<BW ? MODE : BWD, NT, VR>)
                         : reinterpret_cast<const void*>(&k_smx_res<BW ? FWD : MODE, NT, VR>);
     if (lds_bytes > 65536) {
-        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
-        if (e != hipSuccess) return fail(TPR_ERR_HIP, std::string("tpr_softmax: LDS attribute: ") + hipGetErrorString(e));
+        // once per device for this kernel: allow the largest dynamic LDS it
+        // ever takes (kResVLMax float4 per lane)
+        static std::atomic<unsigned long long> done{0};
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+        const unsigned long long bit = 1ull << (dev & 63);
+        if (!(done.load(std::memory_order_acquire) & bit)) {
+            const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     kResVLMax * kResT * 16);
+            if (e != hipSuccess)
+                return fail(TPR_ERR_HIP, std::string("tpr_softmax: LDS attribute: ") + hipGetErrorString(e));
+            done.fetch_or(bit, std::memory_order_acq_rel);
+        }
     }
     if constexpr (BW)
         hipLaunchKernelGGL((k_smx_res_bwd<MODE, NT, VR>), dim3((unsigned)a.rows), dim3(kResT), lds_bytes, st, a, vl);
