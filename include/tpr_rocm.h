@@ -282,7 +282,7 @@ int32_t tpr_abi_version(void);
  * 0 = automatic), "general" (1 = always use the generic strided kernel),
  * "topk_fallback" (1 = always take top-k's exact multi-pass path), "tx" (64, 128
  * or 256: threads across the contiguous dim in the column kernel, 0 = automatic),
- * "unroll" (1, 2 or 4 vectors in flight per thread in the row/column kernels,
+ * "unroll" (1, 2 or 4 vectors in flight per thread in the row/column and gradient-row kernels,
  * 0 = automatic), "colblock" (256, 512 or 1024 threads per column-kernel
  * workgroup, 0 = automatic),
  * "smx_two_pass" (1 = softmax rows always take the two-pass kernel),

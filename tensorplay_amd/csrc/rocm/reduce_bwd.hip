@@ -125,12 +125,12 @@ __global__ __launch_bounds__(256) void k_red_bwd(RbArgs a) {
 // `chunks` pieces) or of rpb = CH / L whole rows (short rows).  The first rpb
 // threads find the rows' offsets once (into LDS); every thread then issues the
 // loads of its U vectors before any store, so short rows do not serialise on
-// load latency.  U = 4 for var / std (they read x) and for rows shorter than
-// 4096 elements (a workgroup then covers several rows); U = 1 for sum / mean
-// over long rows, which only write: one 16-byte store per thread over a grid
-// covering the whole output writes faster than several per thread (measured
-// on MI355X, a 256 MiB broadcast: 40 us against 45-52 us with 2-8 stores per
-// thread; with 1024-element rows U = 1 was slower, 65 against 51 us).  INNER: 0 = the innermost dim is reduced (g / mean / result
+// load latency.  U = 4 for var / std (they read x), 2 for sum / mean over
+// rows shorter than 4096 elements (a workgroup then covers one or two rows)
+// and 1 for sum / mean over long rows, which only write: one 16-byte store per
+// thread over a grid covering the whole output writes faster than several per
+// thread (measured on MI355X, a 256 MiB broadcast: 40 us against 45-52 us with
+// 2-8 stores per thread).  INNER: 0 = the innermost dim is reduced (g / mean / result
 // are one value per row), 1 = it is kept with unit stride in the per-output
 // arrays (loaded as vectors beside x).
 template <int OP, int VEC, int INNER, int U>
@@ -443,7 +443,12 @@ int launch_bwd(const RbArgs& a, hipStream_t st) {
         // vectors: whole 16-byte groups on every side that is read or written per element
         const bool v4 = L % 4 == 0 && al(a.gi) && (a.xs[a.nd - 1] != 1 || al(a.x)) &&
                         (os == 0 || (al(a.g) && al(a.mean) && al(a.res)));
-        const int u = (OP == B_VAR || OP == B_STD || L < 4096) ? 4 : 1;
+        // vectors per thread: 4 when x is read (var / std), else 2 for rows
+        // shorter than 4096 (measured on MI355X at [64, 1024, 1024]: mean / sum
+        // backward over dim 1, rows of 1024, 43-45 us against 50 us with 4 and
+        // 51-58 us with 1) and 1 for long rows
+        int u = (OP == B_VAR || OP == B_STD) ? 4 : (L < 4096 ? 2 : 1);
+        if (knobs().unroll == 1 || knobs().unroll == 2 || knobs().unroll == 4) u = (int)knobs().unroll;
         const long long ch = 256LL * (v4 ? 4 : 1) * u;
         const long long chunks = (L + ch - 1) / ch;
         const long long rows = a.total / L;
@@ -453,6 +458,7 @@ int launch_bwd(const RbArgs& a, hipStream_t st) {
             const dim3 gr((unsigned)blocks), bl(256);
 #define TPR_RB_ROWS(VV, II)                                                                                 \
     if (u == 4) hipLaunchKernelGGL((k_red_bwd_rows<OP, VV, II, 4>), gr, bl, 0, st, a, chunks, rpb, rows);     \
+    else if (u == 2) hipLaunchKernelGGL((k_red_bwd_rows<OP, VV, II, 2>), gr, bl, 0, st, a, chunks, rpb, rows); \
     else hipLaunchKernelGGL((k_red_bwd_rows<OP, VV, II, 1>), gr, bl, 0, st, a, chunks, rpb, rows);
             if (os == 0) {
                 if (v4) { TPR_RB_ROWS(4, 0) } else { TPR_RB_ROWS(1, 0) }
