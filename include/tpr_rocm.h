@@ -274,7 +274,7 @@ int tpr_nll_loss_backward(const void* grad_output, int64_t gs, const int64_t* ta
 /* Thread-local message for the last non-OK status on this thread. */
 const char* tpr_last_error(void);
 
-/* ABI version (major << 16 | minor). */
+/* ABI version (major << 16 | minor); 1.4 accepts UINT16/32/64 reduction inputs. */
 int32_t tpr_abi_version(void);
 
 /* Tuning / test hook: force plan choices.  Keys: "splits" (row/full/column

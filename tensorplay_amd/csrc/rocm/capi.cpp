@@ -56,7 +56,7 @@ extern "C" {
 
 const char* tpr_last_error(void) { return tpr::g_last_error.c_str(); }
 
-int32_t tpr_abi_version(void) { return (1 << 16) | 3; }
+int32_t tpr_abi_version(void) { return (1 << 16) | 4; }
 
 int tpr_debug_set(const char* key, int64_t value) {
     if (!key) return tpr::fail(TPR_ERR_INVALID_ARG, "tpr_debug_set: null key");
