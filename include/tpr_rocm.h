@@ -219,7 +219,8 @@ int tpr_copy_strided(const void* in, int32_t elem_size, int32_t ndim, const int6
  *     with a = g (dL/dy) and b = y (the forward output).
  * a: x (forward) or g (backward), strides a_strides (elements, per logical
  * dim); b: y (backward only, strides b_strides; NULL forward).  out is written
- * dense row-major [outer, n, inner].  Float32 only.  Workspace:
+ * dense row-major [outer, n, inner], in the input dtype: FLOAT32, or FLOAT64
+ * (computed in double; the reference composite keeps the input dtype).  Workspace:
  * tpr_softmax_workspace_bytes(desc) bytes (0 for most shapes; rows longer than
  * the register-resident kernels hold, when there are few of them, use
  * per-chunk partial statistics). */
@@ -232,7 +233,7 @@ enum tpr_softmax_mode {
 
 typedef struct tpr_softmax_desc {
     int32_t mode;  /* enum tpr_softmax_mode */
-    int32_t dtype; /* TPR_FLOAT32 */
+    int32_t dtype; /* TPR_FLOAT32 or TPR_FLOAT64 (a, b and out alike) */
     int64_t outer, n, inner;
     int64_t a_strides[3];
     int64_t b_strides[3];

@@ -316,7 +316,7 @@ def _view3(x, dim):
 
 
 def softmax(x, dim=-1, log=False, grad_of=None):
-    """Softmax / log_softmax of a float32 device tensor along `dim` through
+    """Softmax / log_softmax of a float32 or float64 device tensor along `dim` through
     tpr_softmax; with grad_of=y, the gradient given g = x and the forward
     output y.  Returns a dense tensor of x's shape."""
     import torch
@@ -331,10 +331,10 @@ def softmax(x, dim=-1, log=False, grad_of=None):
         if vb is None:
             b = b.contiguous()
             vb = _view3(b, dim)
-    out = torch.empty(list(x.shape), dtype=torch.float32, device=x.device)
+    out = torch.empty(list(x.shape), dtype=x.dtype, device=x.device)
     d = SoftmaxDesc()
     d.mode = (LOG_SOFTMAX_BWD if log else SOFTMAX_BWD) if b is not None else (LOG_SOFTMAX_FWD if log else SOFTMAX_FWD)
-    d.dtype = FLOAT32
+    d.dtype = FLOAT64 if x.dtype == torch.float64 else FLOAT32
     d.outer, d.n, d.inner = v[0]
     for k in range(3):
         d.a_strides[k] = v[1][k]

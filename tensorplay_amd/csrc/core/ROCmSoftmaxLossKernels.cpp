@@ -87,11 +87,11 @@ Tensor run_softmax(const Tensor& a, const Tensor* b, int64_t d, int mode, const 
         int64_t e2[3];
         bv = view3(*b, d, e2, sb);
     }
-    Tensor out = Tensor::empty(a.shape(), DType::Float32, a.device());
+    Tensor out = Tensor::empty(a.shape(), a.dtype(), a.device());
     tpr_softmax_desc desc;
     std::memset(&desc, 0, sizeof(desc));
     desc.mode = mode;
-    desc.dtype = TPR_FLOAT32;
+    desc.dtype = a.dtype() == DType::Float64 ? TPR_FLOAT64 : TPR_FLOAT32;
     desc.outer = ext[0];
     desc.n = ext[1];
     desc.inner = ext[2];
@@ -116,9 +116,9 @@ Tensor softmax_common(const Tensor& self, int64_t dim, DType dtype, bool log) {
     const char* name = log ? "log_softmax" : "softmax";
     DType out = dtype == DType::Undefined ? self.dtype() : dtype;
     if (isIntegralType(out, false)) out = DType::Float32;
-    if (out != DType::Float32)
+    if (out != DType::Float32 && out != DType::Float64)
         TP_THROW(NotImplementedError, std::string(name) + " not implemented for dtype " + toString(out) +
-                                          " on ROCm (float32 only)");
+                                          " on ROCm (float32 / float64)");
     if (self.dim() > TPR_MAX_DIMS) TP_THROW(NotImplementedError, std::string(name) + ": more than 8 dims on ROCm");
     const int64_t d = wrap_dim(dim, self.dim());
     const Tensor x = self.dtype() == out ? self : self.to(out);
@@ -135,11 +135,11 @@ Tensor log_softmax_kernel(const Tensor& self, int64_t dim, DType dtype) {
 // _softmax_backward_data / _log_softmax_backward_data: the gradient formulas
 // of config/derivatives.yaml:91-95 as one fused kernel (TensorPlay composes
 // them from sum / mul / sub / exp in its autograd; PyTorch names these ops
-// this way).  grad_output and output: float32, same shape.
+// this way).  grad_output and output: float32 or float64 (the same), same shape.
 static Tensor softmax_bwd_common(const Tensor& grad, const Tensor& output, int64_t dim, bool log) {
     const char* name = log ? "_log_softmax_backward_data" : "_softmax_backward_data";
-    if (grad.dtype() != DType::Float32 || output.dtype() != DType::Float32)
-        TP_THROW(NotImplementedError, std::string(name) + ": float32 only on ROCm");
+    if ((grad.dtype() != DType::Float32 && grad.dtype() != DType::Float64) || output.dtype() != grad.dtype())
+        TP_THROW(NotImplementedError, std::string(name) + ": float32 or float64 (both alike) on ROCm");
     if (grad.shape() != output.shape()) TP_THROW(RuntimeError, std::string(name) + ": grad/output shape mismatch");
     if (!(grad.device() == output.device())) TP_THROW(RuntimeError, std::string(name) + ": tensors on different devices");
     if (grad.dim() > TPR_MAX_DIMS) TP_THROW(NotImplementedError, std::string(name) + ": more than 8 dims on ROCm");

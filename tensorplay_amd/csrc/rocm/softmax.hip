@@ -983,6 +983,136 @@ __global__ __launch_bounds__(kWave * BY) void k_smx_cols4r(SmxColArgs p) {
 
 
 // ---------------------------------------------------------------------------
+// Float64 inputs (the reference's composite runs in the input dtype, so a
+// Float64 tensor gives a Float64 softmax).  Same semantics as the float32
+// kernels, computed in double with exp / log: two passes over a slice.
+//   k_smx_f64_rows: unit-stride dim, one 256-thread workgroup per slice;
+//   k_smx_f64_cols: any other layout, one thread per (outer, inner) slice
+//                   (consecutive threads take consecutive inner indices).
+// ---------------------------------------------------------------------------
+struct SmxF64Args {
+    const double* a;
+    const double* b;
+    double* out;  // dense [outer, n, inner]
+    long long outer, n, inner;
+    long long a_so, a_sn, a_si;
+    long long b_so, b_sn, b_si;
+};
+
+__device__ __forceinline__ void ms_merge_d(double& m, double& s, double m2, double s2) {
+    const double M = fmax(m, m2);
+    if (M == -INFINITY) {
+        s += s2;
+        return;
+    }
+    s = (m == -INFINITY ? s : s * exp(m - M)) + (m2 == -INFINITY ? s2 : s2 * exp(m2 - M));
+    m = M;
+}
+
+__device__ __forceinline__ void ms_add_d(double& m, double& s, double x) {
+    if (x > m) {  // a NaN x never raises m
+        s = (m == -INFINITY) ? s : s * exp(m - x);
+        m = x;
+    }
+    if (m == -INFINITY) s += (x != x) ? x : 0.0;
+    else s += exp(x - m);
+}
+
+template <int MODE>
+__device__ __forceinline__ double outv_d(double a, double b, double st0, double st1) {
+    if constexpr (MODE == FWD) return exp(a - st0) * st1;
+    else if constexpr (MODE == FWD_LOG) return (a - st0) - st1;
+    else if constexpr (MODE == BWD) return (a - st0) * b;
+    else return a - exp(b) * st0;
+}
+
+template <int MODE>
+__device__ __forceinline__ void fin_d(double m, double s, double& st0, double& st1) {
+    if constexpr (MODE < BWD) {
+        if (m == -INFINITY) {
+            st0 = NAN;
+            st1 = NAN;
+        } else {
+            st0 = m;
+            st1 = (MODE == FWD) ? 1.0 / s : log(s);
+        }
+    } else {
+        st0 = s;
+        st1 = 0.0;
+    }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void k_smx_f64_rows(SmxF64Args p) {
+    constexpr bool BW = MODE >= BWD;
+    __shared__ double shm[4], shs[4];
+    const long long row = blockIdx.x;
+    const double* pa = p.a + row * p.a_so;
+    const double* pb = BW ? p.b + row * p.b_so : nullptr;
+    double* po = p.out + row * p.n;
+    const int t = threadIdx.x;
+    double m = -INFINITY, s = 0.0;
+    for (long long e = t; e < p.n; e += 256) {
+        if constexpr (!BW) ms_add_d(m, s, pa[e]);
+        else s += (MODE == BWD) ? pa[e] * pb[e] : pa[e];
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const double m2 = __shfl_xor(m, o, kWave), s2 = __shfl_xor(s, o, kWave);
+        if constexpr (!BW) ms_merge_d(m, s, m2, s2);
+        else s += s2;
+    }
+    if (__lane_id() == 0) {
+        shm[t / kWave] = m;
+        shs[t / kWave] = s;
+    }
+    __syncthreads();
+    m = shm[0];
+    s = shs[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) {
+        if constexpr (!BW) ms_merge_d(m, s, shm[i], shs[i]);
+        else s += shs[i];
+    }
+    double st0, st1;
+    fin_d<MODE>(m, s, st0, st1);
+    for (long long e = t; e < p.n; e += 256) po[e] = outv_d<MODE>(pa[e], BW ? pb[e] : 0.0, st0, st1);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void k_smx_f64_cols(SmxF64Args p) {
+    constexpr bool BW = MODE >= BWD;
+    const long long cols = p.outer * p.inner;
+    for (long long c = (long long)blockIdx.x * 256 + threadIdx.x; c < cols; c += (long long)gridDim.x * 256) {
+        const long long o = c / p.inner, i = c - o * p.inner;
+        const double* pa = p.a + o * p.a_so + i * p.a_si;
+        const double* pb = BW ? p.b + o * p.b_so + i * p.b_si : nullptr;
+        double* po = p.out + o * p.n * p.inner + i;
+        double m = -INFINITY, s = 0.0;
+        for (long long r = 0; r < p.n; ++r) {
+            if constexpr (!BW) ms_add_d(m, s, pa[r * p.a_sn]);
+            else s += (MODE == BWD) ? pa[r * p.a_sn] * pb[r * p.b_sn] : pa[r * p.a_sn];
+        }
+        double st0, st1;
+        fin_d<MODE>(m, s, st0, st1);
+        for (long long r = 0; r < p.n; ++r)
+            po[r * p.inner] = outv_d<MODE>(pa[r * p.a_sn], BW ? pb[r * p.b_sn] : 0.0, st0, st1);
+    }
+}
+
+template <int MODE>
+int run_f64(const SmxF64Args& a, hipStream_t st) {
+    if (a.inner == 1 && a.a_sn == 1 && (MODE < BWD || a.b_sn == 1)) {
+        hipLaunchKernelGGL((k_smx_f64_rows<MODE>), dim3((unsigned)a.outer), dim3(256), 0, st, a);
+    } else {
+        const long long cols = a.outer * a.inner;
+        const long long blocks = std::max(1LL, std::min((cols + 255) / 256, (long long)device_info().cus * 16));
+        hipLaunchKernelGGL((k_smx_f64_cols<MODE>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+    }
+    return check_launch("tpr_softmax (float64)");
+}
+
+// ---------------------------------------------------------------------------
 // Host planner
 // ---------------------------------------------------------------------------
 template <int MODE, int G, int V, int VW>
@@ -1206,7 +1336,7 @@ bool rows_path(const tpr_softmax_desc* d) {
 // per (row, chunk).  Independent of pointer alignment: it assumes the scalar
 // single-pass capacity (16384 floats forward, 4096 backward).
 size_t smx_workspace(const tpr_softmax_desc* d) {
-    if (!rows_path(d) || d->outer == 0 || d->n == 0) return 0;
+    if (d->dtype == TPR_FLOAT64 || !rows_path(d) || d->outer == 0 || d->n == 0) return 0;
     const bool bw = d->mode >= TPR_SOFTMAX_BWD;
     const long long cap1 = bw ? 4096 : 16384;
     if (!(knobs().smx_two_pass || d->n > cap1)) return 0;
@@ -1230,12 +1360,25 @@ extern "C" int tpr_softmax(const tpr_softmax_desc* d, const void* a, const void*
     if (!d) return fail(TPR_ERR_INVALID_ARG, "tpr_softmax: null descriptor");
     if (d->mode < TPR_SOFTMAX_FWD || d->mode > TPR_LOG_SOFTMAX_BWD)
         return fail(TPR_ERR_INVALID_ARG, "tpr_softmax: unknown mode");
-    if (d->dtype != TPR_FLOAT32) return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_softmax: float32 only");
+    if (d->dtype != TPR_FLOAT32 && d->dtype != TPR_FLOAT64)
+        return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_softmax: float32 and float64 only");
     if (d->outer < 0 || d->n < 0 || d->inner < 0) return fail(TPR_ERR_INVALID_ARG, "tpr_softmax: negative extent");
     if (d->outer == 0 || d->n == 0 || d->inner == 0) return TPR_OK;
     const bool bw = d->mode >= TPR_SOFTMAX_BWD;
     if (!a || !out || (bw && !b)) return fail(TPR_ERR_INVALID_ARG, "tpr_softmax: null pointer");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (d->dtype == TPR_FLOAT64) {
+        if (d->outer > 0x7fffffffLL) return fail(TPR_ERR_INVALID_ARG, "tpr_softmax: too many slices");
+        SmxF64Args f{static_cast<const double*>(a), static_cast<const double*>(b), static_cast<double*>(out),
+                     d->outer, d->n, d->inner, d->a_strides[0], d->a_strides[1], d->a_strides[2],
+                     bw ? d->b_strides[0] : 0, bw ? d->b_strides[1] : 0, bw ? d->b_strides[2] : 0};
+        switch (d->mode) {
+            case TPR_SOFTMAX_FWD: return run_f64<FWD>(f, st);
+            case TPR_LOG_SOFTMAX_FWD: return run_f64<FWD_LOG>(f, st);
+            case TPR_SOFTMAX_BWD: return run_f64<BWD>(f, st);
+            default: return run_f64<BWD_LOG>(f, st);
+        }
+    }
     const float* pa = static_cast<const float*>(a);
     const float* pb = static_cast<const float*>(b);
     float* po = static_cast<float*>(out);

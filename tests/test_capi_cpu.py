@@ -77,8 +77,11 @@ def test_softmax_loss_validation_without_gpu():
     L = _capi.lib()
     assert ctypes.sizeof(_capi.SoftmaxDesc) == 8 + 24 + 48
     d = _capi.SoftmaxDesc()
-    d.mode, d.dtype, d.outer, d.n, d.inner = 0, _capi.FLOAT64, 2, 3, 1
+    d.mode, d.dtype, d.outer, d.n, d.inner = 0, _capi.INT32, 2, 3, 1
     assert L.tpr_softmax(ctypes.byref(d), None, None, None, None, 0, None) == _capi.ERR_UNSUPPORTED_DTYPE
+    d.dtype = _capi.FLOAT64  # float64 is served: a null pointer is the error now
+    assert L.tpr_softmax(ctypes.byref(d), None, None, None, None, 0, None) == _capi.ERR_INVALID_ARG
+    assert L.tpr_softmax_workspace_bytes(ctypes.byref(d)) == 0
     d.dtype, d.mode = _capi.FLOAT32, 7
     assert L.tpr_softmax(ctypes.byref(d), None, None, None, None, 0, None) == _capi.ERR_INVALID_ARG
     d.mode, d.n = _capi.SOFTMAX_FWD, 0

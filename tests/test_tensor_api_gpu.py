@@ -293,8 +293,9 @@ def test_softmax_dtype_rules():
     assert y.dtype == tp.float32
     close(y, torch.softmax(torch.tensor([[1.0, 2.0, 3.0]]), 1))
     x = tp.tensor(np.ones((2, 3), np.float32), device=DEV)
-    with pytest.raises(NotImplementedError):
-        x.softmax(1, tp.float64)
+    y64 = x.softmax(1, tp.float64)  # dtype given: computed in Float64 (PointwiseKernels.cpp:520-523)
+    assert y64.dtype == tp.float64
+    np.testing.assert_allclose(y64.numpy(), np.full((2, 3), 1.0 / 3.0), rtol=1e-15)
     with pytest.raises(IndexError):
         x.softmax(2)
 
