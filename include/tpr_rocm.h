@@ -70,18 +70,20 @@ enum tpr_reduce_op {
  *  - out_dtype: SUM/MEAN/PROD: FLOAT32 or FLOAT64.  AMAX/AMIN: the input
  *    dtype.  ARGMAX/ARGMIN: INT64 (index along the reduced dims, row-major;
  *    first index wins ties; NaN never wins, as the reference's strict
- *    compare).  VAR/STD/NORM/MEDIAN: FLOAT32 (FLOAT64 for a FLOAT64 input:
- *    every op but MEDIAN takes FLOAT64 inputs and computes in double).
+ *    compare).  VAR/STD/NORM: FLOAT32 (FLOAT64 for a FLOAT64 input: every op
+ *    takes FLOAT64 inputs and computes in double).  MEDIAN: the input dtype.
  *    Integer and BOOL inputs (every signed and unsigned width) take SUM/PROD
  *    (INT64 output, wrap-around), MEAN (of the values converted to float32),
- *    AMAX/AMIN, ARGMAX/ARGMIN (unsigned order for UINT*) and ALL/ANY.
+ *    AMAX/AMIN, ARGMAX/ARGMIN (unsigned order for UINT*), ALL/ANY and MEDIAN.
  *    ALL/ANY: BOOL (one byte, 0/1; an element counts as true when it is != 0,
  *    so NaN is true).
  *  - NORM: (sum |x|^p)^(1/p); p = +inf / -inf: max / min of |x| (NaN ignored,
  *    as AMAX/AMIN); p = 0 gives the reference's n^(1/0).
- *  - MEDIAN: lower median ((n-1)/2-th smallest) of all elements; -0.0 == +0.0
- *    (a zero median is returned as +0.0); NaN ranks above every number.  Only
- *    full reductions of a contiguous view (TPR_ERR_NOT_IMPLEMENTED otherwise).
+ *  - MEDIAN: lower median ((n-1)/2-th smallest) of all elements, output in the
+ *    input dtype (every dtype); -0.0 == +0.0 (a zero median is returned as
+ *    +0.0); NaN ranks above every number.  Only full reductions of a
+ *    contiguous view (TPR_ERR_NOT_IMPLEMENTED otherwise); an empty input is
+ *    NaN for FLOAT32 and TPR_ERR_INVALID_ARG for the other dtypes.
  *  - count_override > 0 replaces the element count used by MEAN/VAR/STD (the
  *    reference multiplies the size of every listed dim, duplicates included,
  *    ReductionKernels.cpp:203-208 and :840-845); 0 = product of reduced sizes.

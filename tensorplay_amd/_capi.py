@@ -185,7 +185,7 @@ def default_out_dtype(op, in_dtype=FLOAT32):
     if in_dtype != FLOAT32:
         if op in (SUM, PROD):
             return INT64
-        if op in (AMAX, AMIN):
+        if op in (AMAX, AMIN, MEDIAN):
             return in_dtype
     return FLOAT32
 

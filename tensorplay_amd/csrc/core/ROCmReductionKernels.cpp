@@ -278,17 +278,17 @@ Tensor norm_dim_kernel(const Tensor& self, const std::vector<int64_t>& dims, dou
     return launch(self, TPR_NORM, mask_of(self, dims), self.dtype(), shape, 0, 0, "norm", p);
 }
 
-// median_kernel (ReductionKernels.cpp:874-901): lower median of all elements,
-// a 0-dim tensor of the input dtype; an empty input gives a one-element NaN
+// median_kernel (ReductionKernels.cpp:874-901): lower median of all elements
+// (every dtype the reference instantiates), a 0-dim tensor of the input dtype; an empty input gives a one-element NaN
 // tensor (shape [1]), as the reference's Tensor::tensor({NaN}).
 Tensor median_kernel(const Tensor& self) {
-    require_float32_input(self, "median");
-    if (self.numel() == 0) {
-        const Tensor flat = self.contiguous().reshape({0});
+    require_reducible_input(self, "median");
+    if (self.numel() == 0) {  // Float32 NaN whatever the input dtype, as the reference
+        const Tensor flat = Tensor::empty({0}, DType::Float32, self.device());
         return launch(flat, TPR_MEDIAN, 1u, DType::Float32, {}, 0, 0, "median").reshape({1});
     }
     const Tensor x = self.contiguous();
-    return launch(x, TPR_MEDIAN, all_dims(x), DType::Float32, {}, 0, 0, "median");
+    return launch(x, TPR_MEDIAN, all_dims(x), x.dtype(), {}, 0, 0, "median");
 }
 
 // topk(Tensor self, int64_t k, int64_t dim=-1, bool largest=true, bool sorted=true)

@@ -23,6 +23,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -674,8 +676,16 @@ int validate(const tpr_reduce_desc* d) {
                 if (d->out_dtype != TPR_BOOL)
                     return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: all/any output must be bool");
                 return TPR_OK;
+            case TPR_MEDIAN: {
+                if (d->out_dtype != d->in_dtype)
+                    return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: median output dtype must equal input dtype");
+                const uint32_t all = d->ndim >= 32 ? 0xffffffffu : ((1u << d->ndim) - 1u);
+                if (d->ndim > 0 && d->reduce_mask != all)
+                    return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_reduce: median reduces all dims only");
+                return TPR_OK;
+            }
             default:
-                return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_reduce: median of float64 is not implemented");
+                return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_reduce: op not implemented for float64");
         }
     }
     if (d->in_dtype != TPR_FLOAT32) {
@@ -702,8 +712,16 @@ int validate(const tpr_reduce_desc* d) {
                 if (d->out_dtype != TPR_BOOL)
                     return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: all/any output must be bool");
                 return TPR_OK;
+            case TPR_MEDIAN: {
+                if (d->out_dtype != d->in_dtype)
+                    return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: median output dtype must equal input dtype");
+                const uint32_t all = d->ndim >= 32 ? 0xffffffffu : ((1u << d->ndim) - 1u);
+                if (d->ndim > 0 && d->reduce_mask != all)
+                    return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_reduce: median reduces all dims only");
+                return TPR_OK;
+            }
             default:
-                return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: var/std/norm/median need float32 input");
+                return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_reduce: var/std/norm need a float32 or float64 input");
         }
     }
     switch (d->op) {
@@ -1749,15 +1767,175 @@ __global__ __launch_bounds__(kMedSelT) void k_med_select(MedArgs a) {
 
 __global__ void k_med_fill(float* out, float v) { out[0] = v; }
 
+// Median of the other dtypes (float64, every integer width, bool; the
+// reference's median_kernel instantiates every scalar type): the same radix
+// select on an ascending key of the element's width, 11 bits per pass from the
+// top; the last pass writes the element back in its own dtype.
+struct MedStateG {
+    unsigned long long prefix;
+    unsigned long long pmask;
+    long long kk;
+};
+
+template <class T>
+struct MedKey {
+    static constexpr int kBits = (int)sizeof(T) * 8;
+    static constexpr int kPasses = (kBits + 10) / 11;
+    __device__ static unsigned long long key(T x) {
+        if constexpr (std::is_same<T, double>::value) {
+            unsigned long long u = (unsigned long long)__double_as_longlong(x);
+            if ((u & 0x7fffffffffffffffull) > 0x7ff0000000000000ull) u = 0x7ff8000000000000ull;  // one NaN
+            if (u == 0x8000000000000000ull) u = 0;                                            // -0 -> +0
+            return (u & 0x8000000000000000ull) ? ~u : (u | 0x8000000000000000ull);
+        } else if constexpr (T(-1) < T(0)) {  // signed: flip the sign bit
+            return (unsigned long long)(typename std::make_unsigned<T>::type)x ^ (1ull << (kBits - 1));
+        } else {
+            return (unsigned long long)x;
+        }
+    }
+    __device__ static T value(unsigned long long k) {
+        if constexpr (std::is_same<T, double>::value) {
+            const unsigned long long u = (k & 0x8000000000000000ull) ? (k & 0x7fffffffffffffffull) : ~k;
+            return __longlong_as_double((long long)u);
+        } else if constexpr (T(-1) < T(0)) {
+            return (T)(typename std::make_unsigned<T>::type)(k ^ (1ull << (kBits - 1)));
+        } else {
+            return (T)k;
+        }
+    }
+};
+
+template <class T, int PASS>
+struct MedPass {
+    static constexpr int hi = MedKey<T>::kBits - 11 * PASS;
+    static constexpr int w = hi < 11 ? hi : 11;
+    static constexpr int shift = hi - w;
+    static constexpr unsigned long long dmask = (1ull << w) - 1ull;
+};
+
+struct MedArgsG {
+    const void* in;
+    long long n;
+    int G;
+    uint32_t* hist;  // [G][kMedBins]
+    MedStateG* st;
+    void* out;
+};
+
+template <class T, int PASS>
+__global__ __launch_bounds__(kBlock) void k_medg_hist(MedArgsG a) {
+    using P = MedPass<T, PASS>;
+    __shared__ uint32_t h[kMedBins];
+    for (int i = threadIdx.x; i < kMedBins; i += kBlock) h[i] = 0;
+    unsigned long long prefix = 0, pmask = 0;
+    if (PASS > 0) {
+        prefix = a.st->prefix;
+        pmask = a.st->pmask;
+    }
+    __syncthreads();
+    const T* in = static_cast<const T*>(a.in);
+    const long long nthr = (long long)a.G * kBlock;
+    for (long long i = (long long)blockIdx.x * kBlock + threadIdx.x; i < a.n; i += nthr) {
+        const unsigned long long k = MedKey<T>::key(in[i]);
+        if ((k & pmask) == prefix) atomicAdd(&h[(k >> P::shift) & P::dmask], 1u);
+    }
+    __syncthreads();
+    uint32_t* dst = a.hist + (long long)blockIdx.x * kMedBins;
+    for (int i = threadIdx.x; i < kMedBins; i += kBlock) dst[i] = h[i];
+}
+
+template <class T, int PASS>
+__global__ __launch_bounds__(kMedSelT) void k_medg_select(MedArgsG a) {
+    using P = MedPass<T, PASS>;
+    __shared__ long long wsum[kMedSelT / kWave];
+    __shared__ MedStateG next;
+    const int t = threadIdx.x;
+    long long c0 = 0, c1 = 0;  // thread t owns bins 2t and 2t+1
+    for (int g = 0; g < a.G; ++g) {
+        const uint32_t* hg = a.hist + (long long)g * kMedBins;
+        c0 += hg[2 * t];
+        c1 += hg[2 * t + 1];
+    }
+    MedStateG cur;
+    if (PASS == 0) cur = {0ull, 0ull, (a.n - 1) / 2};
+    else cur = *a.st;
+    const long long own = c0 + c1;
+    long long inc = own;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const long long y = __shfl_up(inc, d, kWave);
+        if (__lane_id() >= d) inc += y;
+    }
+    const int w = t / kWave;
+    if (__lane_id() == kWave - 1) wsum[w] = inc;
+    __syncthreads();
+    long long before = 0;
+    for (int i = 0; i < w; ++i) before += wsum[i];
+    const long long excl = before + inc - own;
+    const long long kk = cur.kk;
+    if (kk >= excl && kk < excl + own) {
+        const bool first = kk < excl + c0;
+        const unsigned long long digit = 2ull * t + (first ? 0ull : 1ull);
+        next.prefix = cur.prefix | (digit << P::shift);
+        next.pmask = cur.pmask | (P::dmask << P::shift);
+        next.kk = kk - excl - (first ? 0 : c0);
+    }
+    __syncthreads();
+    if (t == 0) {
+        if (PASS + 1 < MedKey<T>::kPasses) *a.st = next;
+        else static_cast<T*>(a.out)[0] = MedKey<T>::value(next.prefix);
+    }
+}
+
+template <class T, int PASS>
+void launch_medg(const MedArgsG& a, hipStream_t st) {
+    if constexpr (PASS < MedKey<T>::kPasses) {
+        hipLaunchKernelGGL((k_medg_hist<T, PASS>), dim3(a.G), dim3(kBlock), 0, st, a);
+        hipLaunchKernelGGL((k_medg_select<T, PASS>), dim3(1), dim3(kMedSelT), 0, st, a);
+        launch_medg<T, PASS + 1>(a, st);
+    }
+}
+
 size_t median_ws_bytes(long long n, int* G) {
     const long long g = std::max(1LL, std::min((long long)device_info().cus * 2, (n + 4095) / 4096));
     if (G) *G = (int)g;
     return 256 + (size_t)g * kMedBins * sizeof(uint32_t);
 }
 
-int run_median(const tpr_reduce_desc* d, const Plan& p, const float* in, void* out, void* ws, size_t ws_bytes,
+template <class T>
+int run_median_g(const Plan& p, const void* in, void* out, void* ws, hipStream_t st) {
+    MedArgsG a;
+    a.in = in;
+    a.n = p.count;
+    median_ws_bytes(p.count, &a.G);
+    a.st = static_cast<MedStateG*>(ws);
+    a.hist = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + 256);
+    a.out = out;
+    launch_medg<T, 0>(a, st);
+    return check_launch("k_medg");
+}
+
+int run_median(const tpr_reduce_desc* d, const Plan& p, const void* vin, void* out, void* ws, size_t ws_bytes,
                hipStream_t st) {
-    (void)d;
+    const float* in = static_cast<const float*>(vin);
+    if (d->in_dtype != TPR_FLOAT32) {
+        if (p.count == 0) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: median of an empty non-float32 input");
+        if (!(p.kind == P_ROWS && p.rows == 1))
+            return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_reduce: median needs a contiguous view (make it dense first)");
+        if (ws == nullptr || ws_bytes < median_ws_bytes(p.count, nullptr))
+            return fail(TPR_ERR_WORKSPACE, "tpr_reduce: workspace too small for median");
+        switch (d->in_dtype) {
+            case TPR_FLOAT64: return run_median_g<double>(p, vin, out, ws, st);
+            case TPR_INT8: return run_median_g<signed char>(p, vin, out, ws, st);
+            case TPR_INT16: return run_median_g<short>(p, vin, out, ws, st);
+            case TPR_INT32: return run_median_g<int>(p, vin, out, ws, st);
+            case TPR_INT64: return run_median_g<long long>(p, vin, out, ws, st);
+            case TPR_UINT16: return run_median_g<unsigned short>(p, vin, out, ws, st);
+            case TPR_UINT32: return run_median_g<unsigned int>(p, vin, out, ws, st);
+            case TPR_UINT64: return run_median_g<unsigned long long>(p, vin, out, ws, st);
+            default: return run_median_g<unsigned char>(p, vin, out, ws, st);  // UINT8, BOOL (0 / 1)
+        }
+    }
     if (p.count == 0) {
         hipLaunchKernelGGL(k_med_fill, dim3(1), dim3(1), 0, st, static_cast<float*>(out), __builtin_nanf(""));
         return check_launch("k_med_fill");
@@ -1809,8 +1987,7 @@ int tpr_reduce(const tpr_reduce_desc* desc, const void* in, void* out, void* wor
     if (!out) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: null output");
     if (!in && p.count > 0) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: null input");
     if (desc->op == TPR_MEDIAN)
-        return run_median(desc, p, static_cast<const float*>(in), out, workspace, workspace_bytes,
-                          static_cast<hipStream_t>(stream));
+        return run_median(desc, p, in, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
     const bool int_in = desc->in_dtype != TPR_FLOAT32;
     if (int_in) adapt_plan_int(p, desc, in, esize_of(desc->in_dtype));
     if (p.ws > 0 && (workspace == nullptr || workspace_bytes < p.ws))

@@ -50,6 +50,11 @@ def test_argument_validation_without_gpu():
     d.in_dtype = _capi.INT32
     assert L.tpr_reduce(ctypes.byref(d), None, None, None, 0, None) == _capi.ERR_UNSUPPORTED_DTYPE
     assert b"float32" in L.tpr_last_error()
+    # median of an integer input writes the input dtype (workspace for the radix passes)
+    d = _capi.make_desc("median", [4, 4], [4, 1], [0, 1], _capi.INT32, in_dtype=_capi.INT32)
+    assert L.tpr_reduce_workspace_bytes(ctypes.byref(d)) > 0
+    d.out_dtype = _capi.FLOAT32
+    assert L.tpr_reduce(ctypes.byref(d), None, None, None, 0, None) == _capi.ERR_INVALID_ARG
     d = _capi.make_desc("sum", [4, 4], [4, 1], [1], _capi.FLOAT32)
     d.in_dtype = 99
     assert L.tpr_reduce(ctypes.byref(d), None, None, None, 0, None) == _capi.ERR_UNSUPPORTED_DTYPE

@@ -341,6 +341,40 @@ def test_median_sizes(n):
     check(y[1:], device_view(torch, y, y[1:]), "median", None)
 
 
+@pytest.mark.parametrize("dt", ["float64", "int8", "uint8", "int16", "uint16", "int32", "uint32", "int64", "uint64",
+                                "bool"])
+def test_median_other_dtypes(dt):
+    # median of every other dtype (radix select on the element width's key):
+    # the lower median, bit-exact against numpy's sort, in the input dtype
+    rng = np.random.default_rng(23)
+    for n in (1, 2, 7, 1000, 4097, 100003):
+        if dt == "bool":
+            x = rng.random(n) < 0.4
+        elif dt == "float64":
+            x = rng.standard_normal(n) * 1e3
+            x[: n // 7] = np.round(x[: n // 7])  # ties
+            if n > 3:
+                x[1], x[2] = -0.0, 0.0
+        else:
+            info = np.iinfo(dt)
+            lo, hi = int(info.min), int(info.max)
+            if dt == "uint64":
+                x = rng.integers(0, hi, size=n, dtype=np.uint64, endpoint=True)
+            elif dt == "int64":
+                x = rng.integers(lo, hi, size=n, dtype=np.int64, endpoint=True)
+            else:
+                x = rng.integers(lo, hi + 1, size=n).astype(dt)
+            x[: n // 5] = x[0]  # duplicates
+        print(f"case median dtype={dt} n={n}", flush=True)
+        got = _capi.reduce(torch.from_numpy(x).cuda(), "median", None).cpu().numpy()
+        exp = np.sort(x, kind="stable")[(n - 1) // 2]
+        assert got.dtype == x.dtype
+        if dt == "float64" and exp == 0:
+            assert float(got) == 0.0 and not np.signbit(got)  # a zero median comes back as +0.0
+        else:
+            assert_bits_equal(np.asarray(got).reshape(()), np.asarray(exp).reshape(()))
+
+
 def test_median_special_values():
     x = np.array([np.nan, 1.0, np.nan, -np.inf, 2.0, -0.0, 0.0, np.inf, np.nan], np.float32)
     for k in range(1, len(x) + 1):

@@ -222,6 +222,10 @@ def test_median_vs_oracle():
         # non-contiguous views are made dense first
         tt = t.permute(list(range(len(shape)))[::-1])
         assert tt.median().item() == float(O.median(np.ascontiguousarray(x.transpose())))
+    i = tp.tensor(np.array([[5, -3, 9], [2, 2, 7]], np.int32), device=DEV)
+    assert i.median().dtype == tp.int32 and i.median().item() == 2  # lower median keeps the dtype
+    d = tp.tensor(np.array([0.5, -1.5, 3.25, 2.0]), device=DEV)
+    assert d.median().dtype == tp.float64 and d.median().item() == 0.5
     e = tp.empty([0, 3], device=DEV).median()
     assert e.shape == [1] and math.isnan(e.item())
 
