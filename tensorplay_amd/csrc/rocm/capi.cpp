@@ -27,22 +27,20 @@ int check_launch(const char* what) {
     return TPR_OK;
 }
 
-const DeviceInfo& device_info() {
+DeviceInfo device_info() {
+    // One atomic per device: 0 = not read yet.  Racing first callers each read
+    // the attribute and store the same value, so no lock is needed.
     static constexpr int kMaxDev = 64;
-    static DeviceInfo infos[kMaxDev];
-    static std::atomic<int> ready[kMaxDev];
+    static std::atomic<int> cus_of[kMaxDev];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) dev = 0;
-    if (!ready[dev].load(std::memory_order_acquire)) {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            cus <= 0) {
+    int cus = cus_of[dev].load(std::memory_order_relaxed);
+    if (cus == 0) {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
             cus = 256;
-        }
-        infos[dev].cus = cus;  // every racing writer stores the same value
-        ready[dev].store(1, std::memory_order_release);
+        cus_of[dev].store(cus, std::memory_order_relaxed);
     }
-    return infos[dev];
+    return DeviceInfo{cus};
 }
 
 DebugKnobs& knobs() {
@@ -75,6 +73,7 @@ int tpr_debug_set(const char* key, int64_t value) {
     else if (!std::strcmp(key, "smx_lanes")) k.smx_lanes = value;
     else if (!std::strcmp(key, "smx_split")) k.smx_split = value;
     else if (!std::strcmp(key, "smx_res")) k.smx_res = value;
+    else if (!std::strcmp(key, "rowreg")) k.rowreg = value;
     else return tpr::fail(TPR_ERR_INVALID_ARG, std::string("tpr_debug_set: unknown key ") + key);
     return TPR_OK;
 }

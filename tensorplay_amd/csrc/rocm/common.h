@@ -3,6 +3,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <atomic>
 #include <string>
 
 #include "tpr_rocm.h"
@@ -16,28 +18,34 @@ void set_error(const std::string& msg);
 int fail(int status, const std::string& msg);
 int check_launch(const char* what);
 
-// Device facts used by the planners (cached per device, set on first use).
+// Device facts used by the planners (read once per device, then cached).
 struct DeviceInfo {
     int cus;  // compute units (256 on MI355X)
 };
-const DeviceInfo& device_info();
+DeviceInfo device_info();
 
-// Process-wide tuning overrides (tpr_debug_set).
+// Process-wide plan overrides for tests and tuning sweeps (tpr_debug_set).
+// All zero in normal use.  Each knob is an atomic, so a thread that sets one
+// while another plans a launch is not a data race; a launch reads each knob
+// once, but a sweep that changes knobs while other threads launch gets plans
+// that mix old and new values, so sweeps run single-threaded.
+using Knob = std::atomic<int64_t>;
 struct DebugKnobs {
-    int64_t splits = 0;
-    int64_t lanes = 0;
-    int64_t general = 0;
-    int64_t topk_fallback = 0;
-    int64_t tx = 0;
-    int64_t topk_variant = 0;
-    int64_t topk_waves = 0;
-    int64_t unroll = 0;
-    int64_t colblock = 0;
-    int64_t nt = 0;
-    int64_t smx_two_pass = 0;
-    int64_t smx_lanes = 0;
-    int64_t smx_split = 0;
-    int64_t smx_res = 0;
+    Knob splits{0};
+    Knob lanes{0};
+    Knob general{0};
+    Knob topk_fallback{0};
+    Knob tx{0};
+    Knob topk_variant{0};
+    Knob topk_waves{0};
+    Knob unroll{0};
+    Knob colblock{0};
+    Knob nt{0};
+    Knob smx_two_pass{0};
+    Knob smx_lanes{0};
+    Knob smx_split{0};
+    Knob smx_res{0};
+    Knob rowreg{0};
 };
 DebugKnobs& knobs();
 

@@ -25,7 +25,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 @pytest.fixture(autouse=True)
 def _reset_knobs():
     yield
-    for k in ("splits", "lanes", "general", "tx", "unroll", "colblock", "nt"):
+    for k in ("splits", "lanes", "general", "tx", "unroll", "colblock", "nt", "rowreg"):
         _capi.debug_set(k, 0)
 
 
@@ -157,6 +157,28 @@ def test_forced_plans(knob, values):
             if knob != "lanes":
                 check(c, torch.from_numpy(c).cuda(), op, [1])
                 check(c, torch.from_numpy(c).cuda(), op, [0])
+
+
+@pytest.mark.parametrize("rowreg", [1, -1])
+def test_register_rows(rowreg):
+    """k_rows_reg (zero-identity ops over rows of 65-1024 float4, loads past the
+    row end read 0): row lengths 1-8 waves wide with ragged ends, row counts that
+    leave the last workgroup partly empty, and a row stride wider than the row."""
+    rng = np.random.default_rng(21)
+    _capi.debug_set("rowreg", rowreg)
+    for rows, cols in ((3, 260), (5, 516), (7, 1028), (9, 2052), (6, 4096), (1, 4092), (513, 2048)):
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        x[0] = 0.0
+        x[0, -1] = -0.5  # any: only the last element of the row is nonzero
+        if rows > 1:
+            x[1] = 0.0   # any: all-zero row
+        t = torch.from_numpy(x).cuda()
+        for op in ("sum", "mean", "any"):
+            check(x, t, op, [1])
+        for p in (1.0, 2.0):
+            check(x, t, "norm", [1], p=p)
+        w = x[:, : cols - 4]  # rows 16-byte aligned, row stride > row length
+        check(w, device_view(torch, x, w), "sum", [1])
 
 
 def test_special_values():
