@@ -5,8 +5,8 @@
 #include <cstdlib>
 #include <mutex>
 #include <unordered_map>
-#include <vector>
 
+#include "CachingAllocatorCore.h"
 #include "Exception.h"
 
 namespace tensorplay {
@@ -16,102 +16,78 @@ void hip_check(hipError_t e, const char* what) {
     if (e != hipSuccess) TP_THROW(RuntimeError, std::string(what) + ": " + hipGetErrorString(e));
 }
 
-// Size classes: 512 B granularity below 1 MiB, 2 MiB granularity above.
-size_t round_size(size_t n) {
-    if (n == 0) n = 1;
-    const size_t small = 512, large = 2u << 20;
-    return n < (1u << 20) ? (n + small - 1) / small * small : (n + large - 1) / large * large;
-}
+// Runtime calls of one device for CachingAllocatorCore.
+struct HipBackend {
+    using Event = hipEvent_t;
+    int dev = 0;
 
-struct DeviceCache {
-    std::unordered_map<size_t, std::vector<void*>> free_blocks;
-    AllocatorStats stats;
-};
-
-class ROCmCachingAllocator {
-public:
-    void* allocate(size_t& size, int dev) {
-        size = round_size(size);
-        {
-            std::lock_guard<std::mutex> g(mu_);
-            auto& c = caches_[dev];
-            c.stats.requests++;
-            auto it = c.free_blocks.find(size);
-            if (it != c.free_blocks.end() && !it->second.empty()) {
-                void* p = it->second.back();
-                it->second.pop_back();
-                c.stats.cached_bytes -= (int64_t)size;
-                c.stats.allocated_bytes += (int64_t)size;
-                return p;
-            }
-        }
+    void* raw_alloc(size_t n) {
         DeviceGuard guard(Device(DeviceType::ROCm, dev));
         void* p = nullptr;
-        hipError_t e = hipMalloc(&p, size);
+        const hipError_t e = hipMalloc(&p, n);
         if (e == hipErrorOutOfMemory) {
             (void)hipGetLastError();
-            release_all(dev);
-            e = hipMalloc(&p, size);
+            return nullptr;
         }
         hip_check(e, "hipMalloc");
-        std::lock_guard<std::mutex> g(mu_);
-        auto& c = caches_[dev];
-        c.stats.device_allocs++;
-        c.stats.allocated_bytes += (int64_t)size;
         return p;
     }
-
-    void free(void* p, size_t size, int dev) {
-        std::lock_guard<std::mutex> g(mu_);
-        auto& c = caches_[dev];
-        c.free_blocks[size].push_back(p);
-        c.stats.allocated_bytes -= (int64_t)size;
-        c.stats.cached_bytes += (int64_t)size;
+    void raw_free(void* p) {
+        DeviceGuard guard(Device(DeviceType::ROCm, dev));
+        (void)hipFree(p);
     }
-
-    void release_all(int dev) {
-        std::vector<void*> blocks;
-        {
-            std::lock_guard<std::mutex> g(mu_);
-            auto& c = caches_[dev];
-            for (auto& kv : c.free_blocks) {
-                for (void* p : kv.second) blocks.push_back(p);
-                c.stats.cached_bytes -= (int64_t)(kv.first * kv.second.size());
-            }
-            c.free_blocks.clear();
+    Event record(void* stream) {
+        DeviceGuard guard(Device(DeviceType::ROCm, dev));
+        hipEvent_t e = nullptr;
+        hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreateWithFlags");
+        hip_check(hipEventRecord(e, static_cast<hipStream_t>(stream)), "hipEventRecord");
+        return e;
+    }
+    bool done(Event e) {
+        const hipError_t r = hipEventQuery(e);
+        if (r == hipErrorNotReady) {
+            (void)hipGetLastError();
+            return false;
         }
-        if (blocks.empty()) return;
+        hip_check(r, "hipEventQuery");
+        return true;
+    }
+    void destroy(Event e) { (void)hipEventDestroy(e); }
+    void wait_all() {
         DeviceGuard guard(Device(DeviceType::ROCm, dev));
         (void)hipDeviceSynchronize();
-        for (void* p : blocks) (void)hipFree(p);
     }
+};
 
-    void release_everything() {
-        std::vector<int> devs;
-        {
-            std::lock_guard<std::mutex> g(mu_);
-            for (auto& kv : caches_) devs.push_back(kv.first);
-        }
-        for (int d : devs) release_all(d);
-    }
+using DeviceCache = CachingAllocatorCore<HipBackend>;
 
-    AllocatorStats stats(int dev) {
+class ROCmAllocators {
+public:
+    DeviceCache& of(int dev) {
         std::lock_guard<std::mutex> g(mu_);
-        return caches_[dev].stats;
+        auto it = caches_.find(dev);
+        if (it == caches_.end()) it = caches_.emplace(dev, new DeviceCache(HipBackend{dev})).first;
+        return *it->second;  // never erased: blocks outlive any lookup
+    }
+    std::vector<DeviceCache*> all() {
+        std::lock_guard<std::mutex> g(mu_);
+        std::vector<DeviceCache*> v;
+        for (auto& kv : caches_) v.push_back(kv.second);
+        return v;
     }
 
 private:
     std::mutex mu_;
-    std::unordered_map<int, DeviceCache> caches_;
+    std::unordered_map<int, DeviceCache*> caches_;
 };
 
-ROCmCachingAllocator& rocm_allocator() {
-    static ROCmCachingAllocator* a = new ROCmCachingAllocator();  // outlives every tensor
+ROCmAllocators& rocm_allocators() {
+    static ROCmAllocators* a = new ROCmAllocators();  // outlives every tensor
     return *a;
 }
 
-std::mutex g_stream_mu;
-std::unordered_map<int, void*> g_streams;
+// The current stream of each device, per host thread.
+thread_local std::unordered_map<int, void*> t_streams;
 
 }  // namespace
 
@@ -124,13 +100,30 @@ std::shared_ptr<void> allocate(size_t nbytes, const Device& device) {
     }
     size_t size = nbytes;
     const int dev = device.index;
-    void* p = rocm_allocator().allocate(size, dev);
-    return std::shared_ptr<void>(p, [size, dev](void* q) { rocm_allocator().free(q, size, dev); });
+    DeviceCache& cache = rocm_allocators().of(dev);
+    void* p = cache.allocate(size, currentStream(dev));
+    if (!p) TP_THROW(RuntimeError, "hipMalloc: out of memory allocating " + std::to_string(size) + " bytes");
+    return std::shared_ptr<void>(p, [&cache](void* q) { cache.free(q); });
 }
 
-AllocatorStats allocatorStats(int device_index) { return rocm_allocator().stats(device_index); }
+void recordStream(void* block, int device_index, void* stream) {
+    rocm_allocators().of(device_index).record_stream(block, stream);
+}
 
-void emptyCache() { rocm_allocator().release_everything(); }
+AllocatorStats allocatorStats(int device_index) {
+    const CacheStats c = rocm_allocators().of(device_index).stats();
+    AllocatorStats s;
+    s.allocated_bytes = c.allocated_bytes;
+    s.cached_bytes = c.cached_bytes;
+    s.pending_bytes = c.pending_bytes;
+    s.device_allocs = c.device_allocs;
+    s.requests = c.requests;
+    return s;
+}
+
+void emptyCache() {
+    for (DeviceCache* c : rocm_allocators().all()) c->release_all();
+}
 
 int rocmDeviceCount() {
     int n = 0;
@@ -142,15 +135,11 @@ int rocmDeviceCount() {
 }
 
 void* currentStream(int device_index) {
-    std::lock_guard<std::mutex> g(g_stream_mu);
-    auto it = g_streams.find(device_index);
-    return it == g_streams.end() ? nullptr : it->second;
+    auto it = t_streams.find(device_index);
+    return it == t_streams.end() ? nullptr : it->second;
 }
 
-void setCurrentStream(int device_index, void* stream) {
-    std::lock_guard<std::mutex> g(g_stream_mu);
-    g_streams[device_index] = stream;
-}
+void setCurrentStream(int device_index, void* stream) { t_streams[device_index] = stream; }
 
 void synchronize(int device_index) {
     DeviceGuard guard(Device(DeviceType::ROCm, device_index));

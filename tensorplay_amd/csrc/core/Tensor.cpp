@@ -387,4 +387,8 @@ Tensor std_backward(const Tensor& grad, const Tensor& self, const Tensor& result
         "std_backward", computeDispatchKey(self.device()), grad, self, result, dim, correction, keepdim);
 }
 
+void Tensor::record_stream(void* stream) const {
+    if (device().is_rocm()) recordStream(impl_->storage->data.get(), device().index, stream);
+}
+
 }  // namespace tensorplay

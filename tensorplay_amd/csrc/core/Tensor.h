@@ -56,6 +56,10 @@ public:
     int64_t storage_offset() const { return impl_->offset; }
     DType dtype() const { return impl_->dtype; }
     Device device() const { return impl_->storage->device; }
+    // Marks this tensor's device memory as used on `stream` (a hipStream_t)
+    // besides the stream it was allocated on: freeing it then waits for the
+    // work queued on `stream` before the memory is reused.
+    void record_stream(void* stream) const;
     size_t element_size() const { return elementSize(impl_->dtype); }
     bool is_contiguous() const;
     void* data_ptr() const;  // address of element [0, ..., 0]

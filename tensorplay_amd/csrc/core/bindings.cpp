@@ -142,6 +142,8 @@ PYBIND11_MODULE(_C, m) {
         .def("contiguous", &Tensor::contiguous)
         .def("clone", &Tensor::clone)
         .def("data_ptr", [](const Tensor& x) { return reinterpret_cast<uintptr_t>(x.data_ptr()); })
+        .def("record_stream", [](const Tensor& x, uintptr_t s) { x.record_stream(reinterpret_cast<void*>(s)); },
+             py::arg("stream"))
         .def("transpose", &Tensor::transpose)
         .def("permute", [](const Tensor& x, const std::vector<int64_t>& d) { return x.permute(d); })
         .def("reshape", [](const Tensor& x, const std::vector<int64_t>& s) { return x.reshape(s); })
@@ -308,6 +310,7 @@ PYBIND11_MODULE(_C, m) {
         py::dict d;
         d["allocated_bytes"] = s.allocated_bytes;
         d["cached_bytes"] = s.cached_bytes;
+        d["pending_bytes"] = s.pending_bytes;
         d["device_allocs"] = s.device_allocs;
         d["requests"] = s.requests;
         return d;
