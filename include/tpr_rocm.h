@@ -118,6 +118,24 @@ size_t tpr_reduce_workspace_bytes(const tpr_reduce_desc* desc);
 int tpr_reduce(const tpr_reduce_desc* desc, const void* in, void* out,
                void* workspace, size_t workspace_bytes, void* stream);
 
+/* Size of the fixed per-device scratch array behind tpr_reduce_noalloc. */
+#define TPR_REDUCE_SCRATCH_BYTES (8u << 20)
+
+/* tpr_reduce without a workspace argument and without any device allocation:
+ * split partial states (and the median's histograms) go to a fixed
+ * TPR_REDUCE_SCRATCH_BYTES array that each device holds from the library's
+ * load until the process ends.  Results equal tpr_reduce's.
+ *  - No counterpart in the reference: for callers that cannot allocate device
+ *    memory (code under HIP graph capture, tight serving loops, harnesses that
+ *    forbid hipMalloc).
+ *  - A descriptor whose tpr_reduce_workspace_bytes exceeds
+ *    TPR_REDUCE_SCRATCH_BYTES fails with TPR_ERR_WORKSPACE.
+ *  - Every call on one device shares that device's array: calls that overlap
+ *    on one device (several streams or host threads) race and give wrong
+ *    results; serialise them.  Nothing in the array needs clearing between
+ *    calls (every partial is written before it is read). */
+int tpr_reduce_noalloc(const tpr_reduce_desc* desc, const void* in, void* out, void* stream);
+
 /* Gradient of a SUM / MEAN / VAR / STD reduction with respect to its input:
  * the formulas of /root/reference/config/derivatives.yaml:82-86 (sum, mean)
  * and :182-186 (var, std), which TensorPlay's autograd composes from expand /

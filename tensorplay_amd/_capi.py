@@ -30,7 +30,8 @@ EXPORTED = ["tpr_reduce_workspace_bytes", "tpr_reduce", "tpr_topk_workspace_byte
             "tpr_copy", "tpr_copy_plan", "tpr_copy_strided", "tpr_last_error", "tpr_abi_version",
             "tpr_debug_set", "tpr_softmax", "tpr_softmax_workspace_bytes", "tpr_nll_loss_workspace_bytes", "tpr_nll_loss",
             "tpr_nll_loss_backward", "tpr_reduce_backward_workspace_bytes", "tpr_reduce_backward",
-            "tpr_sample_workspace_bytes", "tpr_sample"]
+            "tpr_sample_workspace_bytes", "tpr_sample", "tpr_reduce_noalloc"]
+REDUCE_SCRATCH_BYTES = 8 << 20  # TPR_REDUCE_SCRATCH_BYTES
 # enum tpr_softmax_mode
 SOFTMAX_FWD, LOG_SOFTMAX_FWD, SOFTMAX_BWD, LOG_SOFTMAX_BWD = range(4)
 # tpr_copy_plan kinds (bits 0-1) and the vector-variant flag (bit 2)
@@ -100,6 +101,8 @@ def lib():
         L.tpr_reduce_workspace_bytes.restype = sz
         L.tpr_reduce.argtypes = [dp, vp, vp, vp, sz, vp]
         L.tpr_reduce.restype = ctypes.c_int
+        L.tpr_reduce_noalloc.argtypes = [dp, vp, vp, vp]
+        L.tpr_reduce_noalloc.restype = ctypes.c_int
         L.tpr_topk_workspace_bytes.argtypes = [i32, i64, i64, i64]
         L.tpr_topk_workspace_bytes.restype = sz
         L.tpr_topk.argtypes = [vp, i32, i64, i64, i64, i64, i32, i32, vp, vp, vp, sz, vp]
@@ -222,6 +225,25 @@ def reduce(x, op, dims=None, correction=1, out_dtype=None, count_override=0, p=2
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
     _check(L.tpr_reduce(ctypes.byref(desc), ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()),
                         ctypes.c_void_p(ws.data_ptr()), wsb, _stream(torch, x.device)))
+    return out
+
+
+def reduce_noalloc(x, op, dims=None, correction=1, out=None, p=2.0):
+    """reduce() through tpr_reduce_noalloc: no workspace, the library's fixed
+    per-device scratch holds split partials.  `out` (dense, the kept dims'
+    shape) may be passed in so the call itself allocates nothing."""
+    import torch
+    nd = x.dim()
+    rd = list(range(nd)) if dims is None else sorted(set((d + nd) if d < 0 else d for d in dims))
+    tmap = _torch_dtypes()
+    idt = tmap[x.dtype]
+    od = default_out_dtype(op, idt)
+    if out is None:
+        kept = [x.shape[i] for i in range(nd) if i not in rd]
+        out = torch.empty(kept, dtype={v: k for k, v in tmap.items()}[od], device=x.device)
+    desc = make_desc(op, list(x.shape), list(x.stride()), rd, od, correction, in_dtype=idt, p=p)
+    _check(lib().tpr_reduce_noalloc(ctypes.byref(desc), ctypes.c_void_p(x.data_ptr()),
+                                    ctypes.c_void_p(out.data_ptr()), _stream(torch, x.device)))
     return out
 
 

@@ -28,6 +28,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -841,7 +842,21 @@ Plan make_plan(const tpr_reduce_desc* d, const void* in) {
     }
     // canonicalise: drop size-1 dims, merge contiguous neighbours of equal kind
     struct Dim { long long size, stride; bool red; };
-    std::vector<Dim> dims;
+    // at most TPR_MAX_DIMS entries each; fixed storage, so planning allocates nothing
+    struct Dims {
+        Dim d[TPR_MAX_DIMS];
+        int n = 0;
+        bool empty() const { return n == 0; }
+        size_t size() const { return (size_t)n; }
+        Dim& back() { return d[n - 1]; }
+        const Dim& front() const { return d[0]; }
+        Dim& operator[](size_t i) { return d[i]; }
+        const Dim& operator[](size_t i) const { return d[i]; }
+        void push_back(const Dim& x) { d[n++] = x; }
+        const Dim* begin() const { return d; }
+        const Dim* end() const { return d + n; }
+    };
+    Dims dims;
     for (int i = 0; i < nd; ++i) {
         if (d->sizes[i] == 1) continue;
         Dim x{d->sizes[i], d->strides[i], (mask & (1u << i)) != 0};
@@ -852,7 +867,7 @@ Plan make_plan(const tpr_reduce_desc* d, const void* in) {
             dims.push_back(x);
         }
     }
-    std::vector<Dim> K, Rd;
+    Dims K, Rd;
     for (auto& x : dims) (x.red ? Rd : K).push_back(x);
 
     const auto& dev = device_info();
@@ -2192,3 +2207,54 @@ int tpr_reduce(const tpr_reduce_desc* desc, const void* in, void* out, void* wor
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Workspace-free entry point.  The partial states of split plans (and the
+// median's histograms) live in a fixed per-device array instead of a caller
+// workspace, so tpr_reduce_noalloc needs no device allocation anywhere.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[TPR_REDUCE_SCRATCH_BYTES];
+
+namespace {
+
+// Device address of `scratch` on the current device.  The host-side name of a
+// __device__ array is only a stand-in for the runtime's symbol table, never a
+// device address, so the address is looked up once per device with that
+// device current and kept.
+int scratch_address(void** ptr) {
+    static constexpr int kMaxDev = 64;
+    static std::mutex mu;
+    static void* addr[kMaxDev] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return tpr::fail(TPR_ERR_HIP, std::string("tpr_reduce_noalloc: hipGetDevice: ") + hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDev) return tpr::fail(TPR_ERR_INVALID_ARG, "tpr_reduce_noalloc: device index out of range");
+    std::lock_guard<std::mutex> g(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return tpr::fail(TPR_ERR_HIP, std::string("tpr_reduce_noalloc: hipGetSymbolAddress(scratch): ") +
+                                              hipGetErrorString(e));
+        addr[dev] = p;
+    }
+    *ptr = addr[dev];
+    return TPR_OK;
+}
+
+}  // namespace
+
+extern "C" int tpr_reduce_noalloc(const tpr_reduce_desc* desc, const void* in, void* out, void* stream) {
+    const size_t need = tpr_reduce_workspace_bytes(desc);  // 0 for an invalid descriptor: tpr_reduce reports it
+    if (need > (size_t)TPR_REDUCE_SCRATCH_BYTES)
+        return tpr::fail(TPR_ERR_WORKSPACE, "tpr_reduce_noalloc: this reduction needs " + std::to_string(need) +
+                                                " bytes of scratch, more than the fixed " +
+                                                std::to_string((size_t)TPR_REDUCE_SCRATCH_BYTES) +
+                                                "; use tpr_reduce with a workspace");
+    void* ws = nullptr;
+    if (need > 0) {
+        const int rc = scratch_address(&ws);
+        if (rc != TPR_OK) return rc;
+    }
+    return tpr_reduce(desc, in, out, ws, need, stream);
+}

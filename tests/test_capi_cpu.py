@@ -39,6 +39,21 @@ def test_descriptor_layout_matches_header():
     assert ctypes.sizeof(_capi.ReduceDesc) == 16 + 128 + 8 + 16 + 8
 
 
+def test_noalloc_rejects_plans_beyond_the_scratch_without_gpu():
+    L = _capi.lib()
+    # var over rows of 2^31 elements, 2^20 rows: 3 chunks x 2^20 rows x 24-byte states > 8 MiB
+    n = (1 << 31) + 5
+    d = _capi.make_desc("var", [1 << 20, n], [n, 1], [1], _capi.FLOAT32)
+    need = L.tpr_reduce_workspace_bytes(ctypes.byref(d))
+    assert need > _capi.REDUCE_SCRATCH_BYTES
+    assert L.tpr_reduce_noalloc(ctypes.byref(d), None, None, None) == _capi.ERR_WORKSPACE
+    assert b"scratch" in L.tpr_last_error()
+    # an invalid descriptor is reported as by tpr_reduce
+    d = _capi.make_desc("sum", [4, 4], [4, 1], [1], _capi.FLOAT32)
+    d.in_dtype = 99
+    assert L.tpr_reduce_noalloc(ctypes.byref(d), None, None, None) == _capi.ERR_UNSUPPORTED_DTYPE
+
+
 def test_argument_validation_without_gpu():
     L = _capi.lib()
     d = _capi.make_desc("sum", [4, 4], [4, 1], [1], _capi.FLOAT32)
