@@ -43,7 +43,15 @@ def parse():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB copy (PMC calibration for FETCH/WRITE_SIZE)")
     ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "pmc_traffic.json"))
+    ap.add_argument("--only", default="",
+                    help="comma list of extra sections to run (default: all): " + ",".join(SECTIONS))
+    ap.add_argument("--no-headline", action="store_true",
+                    help="skip the headline step (profiling one section alone; `value` is then null)")
+    ap.add_argument("--no-accuracy", action="store_true", help="skip the fp64 error report")
     return ap.parse_args()
+
+
+SECTIONS = ["C1", "C3", "C4", "C4f64", "C5", "softmax", "copy", "reduce_backward", "softmax_cols", "topk_short"]
 
 
 class Call:
@@ -224,6 +232,10 @@ def main():
     torch.cuda.set_device(dev)
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     steps, warmup = args.steps, args.warmup
+    only = set(x for x in args.only.split(",") if x) or set(SECTIONS)
+    bad = only - set(SECTIONS)
+    if bad:
+        sys.exit(f"bench.py: unknown sections {sorted(bad)}; choose from {SECTIONS}")
 
     # ---------------- headline: configs[1] --------------------------------------
     shape2 = (64, 1024, 1024)
@@ -234,119 +246,142 @@ def main():
     calls = [[reduce_call(torch, capi, b, op, dims, stream) for (op, dims) in ops2] for b in bufs]
     op_bytes = [in_bytes + c.out_bytes for c in calls[0]]
     step_bytes = sum(op_bytes)
+    result = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+              "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+              "data": "synthetic: torch.randn N(0,1) seeded on device, 3 rotating 256 MiB buffers "
+                      "(each op reads a different buffer than the op before it)",
+              "config": {"workload": "configs[1]: fp32 [64,1024,1024]; mean dim=1, amax+argmax dim=0, "
+                                     "var+std dim=-1 (unbiased). configs[1] is the configuration the metric's "
+                                     "strided-reduction bandwidth is quoted on and covers five of the path's "
+                                     "ops in one step; configs[3] (the largest, 1 GiB full reductions) is "
+                                     "measured below under configs.C4_full_2^28",
+                         "step_alg_bytes": step_bytes}}
 
-    # Op j of step i reads buffer (5i + j) % 3, so consecutive ops never read the
-    # buffer the previous op just streamed (no reuse through the 256 MB MALL).
-    def make_step(i):
-        seq = [calls[(len(ops2) * i + j) % nbuf][j] for j in range(len(ops2))]
+    if not args.no_headline:
+        # Op j of step i reads buffer (5i + j) % 3, so consecutive ops never read the
+        # buffer the previous op just streamed (no reuse through the 256 MB MALL).
+        def make_step(i):
+            seq = [calls[(len(ops2) * i + j) % nbuf][j] for j in range(len(ops2))]
 
-        def f():
-            for c in seq:
-                c()
-        return f
+            def f():
+                for c in seq:
+                    c()
+            return f
 
-    step_fns = [make_step(i) for i in range(nbuf)]
-    ms_step = time_calls(torch, step_fns, steps, warmup)
-    value = step_bytes / (ms_step * 1e-3) / 1e9
+        step_fns = [make_step(i) for i in range(nbuf)]
+        ms_step = time_calls(torch, step_fns, steps, warmup)
+        value = step_bytes / (ms_step * 1e-3) / 1e9
 
-    breakdown = {}
-    for j, (op, dims) in enumerate(ops2):
-        fns = [calls[i][j] for i in range(nbuf)]
-        ms = time_calls(torch, fns, steps, warmup)
-        gbs = op_bytes[j] / (ms * 1e-3) / 1e9
-        breakdown[f"{op}_dim{dims[0]}"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1),
-                                           "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
-                                           "alg_bytes": op_bytes[j]}
-    dom_name, dom = max(breakdown.items(), key=lambda kv: kv[1]["ms"])
-    dom_j = [f"{op}_dim{dims[0]}" for (op, dims) in ops2].index(dom_name)
-    dom_ms = dom["ms"]  # average launch duration over the timed loop of that op alone
-    dom_gbs = op_bytes[dom_j] / (dom_ms * 1e-3) / 1e9
+        breakdown = {}
+        for j, (op, dims) in enumerate(ops2):
+            fns = [calls[i][j] for i in range(nbuf)]
+            ms = time_calls(torch, fns, steps, warmup)
+            gbs = op_bytes[j] / (ms * 1e-3) / 1e9
+            breakdown[f"{op}_dim{dims[0]}"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1),
+                                               "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+                                               "alg_bytes": op_bytes[j], "kernel": DOMINANT_KERNEL[f"{op}_dim{dims[0]}"]}
+        dom_name, dom = max(breakdown.items(), key=lambda kv: kv[1]["ms"])
+        dom_j = [f"{op}_dim{dims[0]}" for (op, dims) in ops2].index(dom_name)
+        dom_ms = dom["ms"]  # average launch duration over the timed loop of that op alone
+        dom_gbs = op_bytes[dom_j] / (dom_ms * 1e-3) / 1e9
 
-    traffic = None
-    if os.path.exists(args.traffic_file):
-        try:
-            tf = json.load(open(args.traffic_file))
-            traffic = tf.get(dom_name, {}).get("hbm_bytes_per_launch")
-        except Exception:
-            traffic = None
+        traffic = None
+        if os.path.exists(args.traffic_file):
+            try:
+                tf = json.load(open(args.traffic_file))
+                traffic = tf.get(dom_name, {}).get("hbm_bytes_per_launch")
+            except Exception:
+                traffic = None
+        result.update({"value": round(value, 1), "ms_per_step": round(ms_step, 5)})
+        result["config"]["frac_of_peak"] = round(value / HBM_PEAK_GBS, 4)
+        result["roofline"] = {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                              "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                              "op": dom_name, "kernel": DOMINANT_KERNEL.get(dom_name, "?"),
+                              "avg_launch_ms": round(dom_ms, 5), "alg_bytes_per_launch": op_bytes[dom_j],
+                              "timing": "HIP events on the launch stream, average over the op's own timed loop"}
+        result["breakdown"] = breakdown
 
-    result = {
-        "metric": METRIC,
-        "value": round(value, 1),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": warmup,
-        "ms_per_step": round(ms_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic: torch.randn N(0,1) seeded on device, 3 rotating 256 MiB buffers "
-                "(each op reads a different buffer than the op before it)",
-        "config": {"workload": "configs[1]: fp32 [64,1024,1024]; mean dim=1, amax+argmax dim=0, "
-                               "var+std dim=-1 (unbiased)",
-                   "frac_of_peak": round(value / HBM_PEAK_GBS, 4),
-                   "step_alg_bytes": step_bytes},
-        "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "op": dom_name, "kernel": DOMINANT_KERNEL.get(dom_name, "?"),
-                     "avg_launch_ms": round(dom_ms, 5), "alg_bytes_per_launch": op_bytes[dom_j]},
-        "breakdown": breakdown,
-    }
+    keep = {"C2": bufs[0]}
+    result["configs"] = run_sections(torch, capi, only, stream, steps, warmup, bufs, keep)
+    if args.calibrate_copy:
+        xc = gen(torch, (64 << 20,), "normal", 6000, dev)
+        for _ in range(3):
+            capi.copy_strided(xc)
+        torch.cuda.synchronize()
 
-    # ---------------- other BASELINE configs --------------------------------------
+    # ---------------- CPU baseline and accuracy (rank 0, N = 1) -------------------
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(bufs[0], ops2, op_bytes)
+        if "C3" in keep and "C5" in keep:
+            result["cpu_baseline"]["configs"] = cpu_extras(keep["C3"], keep["C5"])
+    else:
+        result["cpu_baseline"] = None
+    if not args.no_accuracy:
+        result["accuracy"] = accuracy(torch, capi, keep)
+    print(json.dumps(result), flush=True)
+
+
+def timed(torch, calls, steps, warmup, by, **extra):
+    ms = time_calls(torch, calls, steps, warmup)
+    return dict(rate(ms, by), **extra)
+
+
+def run_sections(torch, capi, only, stream, steps, warmup, bufs, keep):
+    """The other BASELINE configs and the widened rows, each timed the same way
+    (HIP events, inputs rotated so each launch reads HBM)."""
+    dev = bufs[0].device
+    nbuf = len(bufs)
     extras = {}
-    if not args.no_extras:
-        # C1: sum dim=-1 of [4096,4096]
+    if "C1" in only:
+        # C1: sum dim=-1 of [4096,4096] (12 rotating 64 MiB buffers)
         b1 = [gen(torch, (4096, 4096), "normal", 2000 + i, dev) for i in range(12)]
         c1 = [reduce_call(torch, capi, b, "sum", [-1], stream) for b in b1]
-        ms = time_calls(torch, c1, max(steps, 24), warmup)
         by = 4096 * 4096 * 4 + c1[0].out_bytes
-        extras["C1_sum_dim-1_4096x4096"] = {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
-                                            "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        extras["C1_sum_dim-1_4096x4096"] = timed(torch, c1, max(steps, 24) * 4, warmup, by,
+                                                 kernel="k_rows_reg<SumOp,2,8,512>")
+        keep["C1"] = b1[0]
         del b1, c1
-        # C3: topk k=64 of [1024,32768] U(-1,1)
+    if "C3" in only or "softmax" in only:
         b3 = [gen(torch, (1024, 32768), "uniform", 3000 + i, dev) for i in range(6)]
-        c3 = [topk_call(torch, capi, b, 64, stream) for b in b3]
-        ms = time_calls(torch, c3, max(steps, 12), warmup)
-        by = 1024 * 32768 * 4 + c3[0].out_bytes
-        extras["C3_topk64_1024x32768"] = {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
-                                          "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4),
-                                          "rows_per_s": round(1024 / (ms * 1e-3), 1)}
-        keep_c3 = b3[0]
-        # softmax / log_softmax along the rows of the same tensors (register-resident rows)
-        esm3 = {}
-        for name, mode in (("softmax", capi.SOFTMAX_FWD), ("log_softmax", capi.LOG_SOFTMAX_FWD)):
-            cs = [softmax_call(torch, capi, b, -1, mode, stream) for b in b3[:4]]
-            ms = time_calls(torch, cs, max(steps, 12), warmup)
-            esm3[name] = rate(ms, cs[0].bytes)
-            del cs
-        extras["softmax_C3_1024x32768"] = esm3
-        del b3, c3
+        keep["C3"] = b3[0]
+        if "C3" in only:
+            # C3: topk k=64 of [1024,32768] U(-1,1)
+            c3 = [topk_call(torch, capi, b, 64, stream) for b in b3]
+            by = 1024 * 32768 * 4 + c3[0].out_bytes
+            r = timed(torch, c3, max(steps, 12), warmup, by)
+            r["rows_per_s"] = round(1024 / (r["ms"] * 1e-3), 1)
+            extras["C3_topk64_1024x32768"] = r
+            del c3
+        if "softmax" in only:
+            # softmax / log_softmax along the rows of the same tensors (register-resident rows)
+            esm3 = {}
+            for name, mode in (("softmax", capi.SOFTMAX_FWD), ("log_softmax", capi.LOG_SOFTMAX_FWD)):
+                cs = [softmax_call(torch, capi, b, -1, mode, stream) for b in b3[:4]]
+                esm3[name] = timed(torch, cs, max(steps, 12), warmup, cs[0].bytes)
+                del cs
+            extras["softmax_C3_1024x32768"] = esm3
+        del b3
+    if "C4" in only:
         # C4: full-tensor reductions of 2^28 N(0.5, 2)
         x4 = gen(torch, (1 << 28,), "normal", 4000, dev) * 2.0 + 0.5
         c4 = {}
         for op in ("sum", "mean", "amax", "argmax", "var", "std"):
             c = reduce_call(torch, capi, x4, op, None, stream)
-            ms = time_calls(torch, [c], max(steps // 2, 5), 2)
-            by = (1 << 28) * 4 + c.out_bytes
-            c4[op] = {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
-                      "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4)}
+            c4[op] = timed(torch, [c], max(steps // 2, 5), 2, (1 << 28) * 4 + c.out_bytes)
         extras["C4_full_2^28"] = c4
+        keep["C4"] = x4
         del x4
+    if "C4f64" in only:
         # the same 1 GiB as float64 (2^27 elements): reductions computed in double
         x4d = gen(torch, (1 << 27,), "normal", 4001, dev).double() * 2.0 + 0.5
         c4d = {}
         for op in ("sum", "amax", "argmax", "var"):
             c = reduce_call(torch, capi, x4d, op, None, stream)
-            ms = time_calls(torch, [c], max(steps // 2, 5), 2)
-            by = (1 << 27) * 8 + c.out_bytes
-            c4d[op] = {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
-                       "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4)}
+            c4d[op] = timed(torch, [c], max(steps // 2, 5), 2, (1 << 27) * 8 + c.out_bytes)
         extras["C4_full_f64_2^27"] = c4d
         del x4d
-        # C5: topk k=50 + argmax dim=-1 of [256,151936] N(0,3) + 8 boosted positions per row
+    if "C5" in only or "softmax" in only:
+        # C5: [256,151936] N(0,3) + 8 boosted positions per row
         b5 = []
         for i in range(5):
             x = gen(torch, (256, 151936), "normal", 5000 + i, dev) * 3.0
@@ -355,47 +390,43 @@ def main():
             pos = torch.stack([torch.randperm(151936, generator=g)[:8] for _ in range(256)]).to(dev)
             x.scatter_add_(1, pos, torch.full((256, 8), 15.0, device=dev))
             b5.append(x)
-        c5 = [topk_call(torch, capi, b, 50, stream) for b in b5]
-        ms = time_calls(torch, c5, max(steps, 10), warmup)
-        by = 256 * 151936 * 4 + c5[0].out_bytes
-        e5 = {"topk50": {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
-                         "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4),
-                         "rows_per_s": round(256 / (ms * 1e-3), 1)}}
-        c5a = [reduce_call(torch, capi, b, "argmax", [-1], stream) for b in b5]
-        ms = time_calls(torch, c5a, max(steps, 10), warmup)
-        by = 256 * 151936 * 4 + c5a[0].out_bytes
-        e5["argmax_dim-1"] = {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
-                              "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4)}
-        # top-k (k=50) -> top-p (0.9) sampling of one token per row, T = 0.7
-        uu = torch.rand((256,), device=dev)
-        cs = [sample_call(torch, capi, b, 50, 0.7, 0.9, uu, stream) for b in b5]
-        ms = time_calls(torch, cs, max(steps, 10), warmup)
-        e5["sample_topk50_topp0.9"] = dict(rate(ms, cs[0].bytes), rows_per_s=round(256 / (ms * 1e-3), 1))
-        del cs
-        extras["C5_logits_256x151936"] = e5
-        # softmax family on the same logits: softmax / log_softmax forward (read + write), softmax
-        # backward (read g and y, write the gradient), and nll_loss backward (write [256, 151936])
-        esm = {}
-        for name, mode in (("softmax", capi.SOFTMAX_FWD), ("log_softmax", capi.LOG_SOFTMAX_FWD)):
-            cs = [softmax_call(torch, capi, b, -1, mode, stream) for b in b5[:3]]
-            ms = time_calls(torch, cs, max(steps, 10), warmup)
-            esm[name] = rate(ms, cs[0].bytes)
+        keep["C5"] = b5[0]
+        if "C5" in only:
+            c5 = [topk_call(torch, capi, b, 50, stream) for b in b5]
+            by = 256 * 151936 * 4 + c5[0].out_bytes
+            e5 = {"topk50": timed(torch, c5, max(steps, 10), warmup, by)}
+            e5["topk50"]["rows_per_s"] = round(256 / (e5["topk50"]["ms"] * 1e-3), 1)
+            c5a = [reduce_call(torch, capi, b, "argmax", [-1], stream) for b in b5]
+            e5["argmax_dim-1"] = timed(torch, c5a, max(steps, 10), warmup, 256 * 151936 * 4 + c5a[0].out_bytes)
+            # top-k (k=50) -> top-p (0.9) sampling of one token per row, T = 0.7
+            uu = torch.rand((256,), device=dev)
+            cs = [sample_call(torch, capi, b, 50, 0.7, 0.9, uu, stream) for b in b5]
+            e5["sample_topk50_topp0.9"] = timed(torch, cs, max(steps, 10), warmup, cs[0].bytes)
+            e5["sample_topk50_topp0.9"]["rows_per_s"] = round(256 / (e5["sample_topk50_topp0.9"]["ms"] * 1e-3), 1)
+            extras["C5_logits_256x151936"] = e5
+            del c5, c5a, cs
+        if "softmax" in only:
+            # softmax / log_softmax forward (read + write), their gradients (read g and y, write the
+            # gradient), and nll_loss backward (write [256, 151936])
+            esm = {}
+            for name, mode in (("softmax", capi.SOFTMAX_FWD), ("log_softmax", capi.LOG_SOFTMAX_FWD)):
+                cs = [softmax_call(torch, capi, b, -1, mode, stream) for b in b5[:3]]
+                esm[name] = timed(torch, cs, max(steps, 10), warmup, cs[0].bytes)
+                del cs
+            for name, mode in (("softmax_backward", capi.SOFTMAX_BWD),
+                               ("log_softmax_backward", capi.LOG_SOFTMAX_BWD)):
+                cs = [softmax_call(torch, capi, b5[i], -1, mode, stream, y=b5[i + 1]) for i in (0, 2)]
+                esm[name] = timed(torch, cs, max(steps, 10), warmup, cs[0].bytes)
+                del cs
+            tgt = torch.randint(0, 151936, (256,), device=dev, dtype=torch.int64)
+            one = torch.ones((), device=dev)
+            tw = torch.full((1,), 256.0, device=dev)
+            cs = [nll_bwd_call(torch, capi, 256, 151936, tgt, one, tw, stream) for _ in range(3)]
+            esm["nll_loss_backward"] = timed(torch, cs, max(steps, 10), warmup, cs[0].bytes)
             del cs
-        for name, mode in (("softmax_backward", capi.SOFTMAX_BWD), ("log_softmax_backward", capi.LOG_SOFTMAX_BWD)):
-            cs = [softmax_call(torch, capi, b5[i], -1, mode, stream, y=b5[i + 1]) for i in (0, 2)]
-            ms = time_calls(torch, cs, max(steps, 10), warmup)
-            esm[name] = rate(ms, cs[0].bytes)
-            del cs
-        tgt = torch.randint(0, 151936, (256,), device=dev, dtype=torch.int64)
-        one = torch.ones((), device=dev)
-        tw = torch.full((1,), 256.0, device=dev)
-        cs = [nll_bwd_call(torch, capi, 256, 151936, tgt, one, tw, stream) for _ in range(3)]
-        ms = time_calls(torch, cs, max(steps, 10), warmup)
-        esm["nll_loss_backward"] = rate(ms, cs[0].bytes)
-        del cs
-        extras["softmax_C5_logits_256x151936"] = esm
-        keep_c5 = b5[0]
-        del b5, c5, c5a
+            extras["softmax_C5_logits_256x151936"] = esm
+        del b5
+    if "copy" in only:
         # copy_ (strided / casting) on the C2 geometry: read + write bytes
         ecp = {}
         cases = {"permute_1_2_0": (lambda b: b.permute(1, 2, 0), torch.float32),
@@ -405,13 +436,11 @@ def main():
         for name, (view, odt) in cases.items():
             outs = [torch.empty(view(bufs[0]).shape, dtype=odt, device=dev) for _ in range(2)]
             cc = [copy_call(torch, capi, outs[i % 2], view(bufs[i % nbuf]), stream) for i in range(6)]
-            ms = time_calls(torch, cc, max(steps, 12), warmup)
-            by = cc[0].bytes
-            ecp[name] = {"ms": round(ms, 5), "GB/s": round(by / ms / 1e6, 1),
-                         "frac_of_peak": round(by / ms / 1e6 / HBM_PEAK_GBS, 4), "alg_bytes": by,
-                         "kernel": copy_kernel_name(capi.copy_plan(outs[0], view(bufs[0])))}
+            ecp[name] = timed(torch, cc, max(steps, 12), warmup, cc[0].bytes,
+                              kernel=copy_kernel_name(capi.copy_plan(outs[0], view(bufs[0]))))
             del outs, cc
         extras["copy_C2_64x1024x1024"] = ecp
+    if "reduce_backward" in only:
         # gradients of the C2 reductions (var / std over dim=-1, mean over dim=1) and of a full sum
         erb = {}
         for op, dims in (("var", [-1]), ("std", [-1]), ("mean", [1]), ("sum", None)):
@@ -421,30 +450,93 @@ def main():
             g = torch.randn(kept, device=dev)
             res = torch.rand(kept, device=dev) + 0.5 if op == "std" else None
             cs = [reduce_bwd_call(torch, capi, bufs[i], op, dims, stream, g, res) for i in range(nbuf)]
-            ms = time_calls(torch, cs, max(steps, 9), warmup)
-            erb[f"{op}_backward_dim{'' if dims is None else dims[0]}"] = rate(ms, cs[0].bytes)
+            erb[f"{op}_backward_dim{'' if dims is None else dims[0]}"] = timed(torch, cs, max(steps, 9), warmup,
+                                                                                 cs[0].bytes)
             del cs
         extras["reduce_backward_C2_64x1024x1024"] = erb
+    if "softmax_cols" in only:
         # softmax over the middle (strided) dim of the C2 geometry
         cs = [softmax_call(torch, capi, bufs[i], 1, capi.SOFTMAX_FWD, stream) for i in range(2)]
-        ms = time_calls(torch, cs, max(steps, 8), warmup)
-        extras["softmax_C2_dim1_64x1024x1024"] = rate(ms, cs[0].bytes)
+        extras["softmax_C2_dim1_64x1024x1024"] = timed(torch, cs, max(steps, 8), warmup, cs[0].bytes)
         del cs
-    if args.calibrate_copy:
-        xc = gen(torch, (64 << 20,), "normal", 6000, dev)
-        for _ in range(3):
-            capi.copy_strided(xc)
-        torch.cuda.synchronize()
-    result["configs"] = extras
+    if "topk_short" in only:
+        # many short rows (one wave per row) and a large k, beside the BASELINE top-k configs
+        ets = {}
+        for (rows, cols, k) in ((65536, 256, 8), (16384, 1024, 32), (4096, 2048, 1000)):
+            nb = max(3, (768 << 20) // (rows * cols * 4))
+            bs = [gen(torch, (rows, cols), "uniform", 7000 + i, dev) for i in range(nb)]
+            cs = [topk_call(torch, capi, b, k, stream) for b in bs]
+            r = timed(torch, cs, max(steps, 12), warmup, rows * cols * 4 + cs[0].out_bytes)
+            r["rows_per_s"] = round(rows / (r["ms"] * 1e-3), 1)
+            ets[f"topk{k}_{rows}x{cols}"] = r
+            del bs, cs
+        extras["topk_short_rows"] = ets
+    return extras
 
-    # ---------------- CPU baseline (oracle restatement, 1 core) -------------------
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(bufs[0], ops2, op_bytes)
-        if not args.no_extras:
-            result["cpu_baseline"]["configs"] = cpu_extras(keep_c3, keep_c5)
-    else:
-        result["cpu_baseline"] = None
-    print(json.dumps(result), flush=True)
+
+def _err_stats(got, ref, x_abs_sum=None):
+    """Max and median relative error of `got` against the fp64 `ref`, and the
+    normwise error max |got - ref| / sum |x| over each output's inputs."""
+    import numpy as np
+    got = np.asarray(got, np.float64).reshape(-1)
+    ref = np.asarray(ref, np.float64).reshape(-1)
+    rel = np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)
+    out = {"max_rel": float(f"{rel.max():.3e}"), "median_rel": float(f"{np.median(rel):.3e}")}
+    if x_abs_sum is not None:
+        nw = np.abs(got - ref) / np.maximum(np.asarray(x_abs_sum, np.float64).reshape(-1), 1e-30)
+        out["normwise"] = float(f"{nw.max():.3e}")
+    return out
+
+
+def accuracy(torch, capi, keep):
+    """Error of this backend's GPU result and of TensorPlay's CPU path (the C
+    restatement in oracle/, same input) against an fp64 host reference, per op
+    and config (north_star: <= 1e-5 relative for fp32 sum/mean/var/std,
+    reported beside the CPU path's own error)."""
+    import numpy as np
+    from oracle import oracle as O
+
+    def gpu(t, op, dims):
+        r = capi.reduce(t, op, dims)
+        torch.cuda.synchronize()
+        return r.cpu().numpy()
+
+    acc = {"reference": "numpy float64 on the same fp32 input; cpu_path = oracle/tp_cpu_reduce.c "
+                        "(TensorPlay's CPU reduction order and accumulation types)",
+           "bound": "gpu max_rel <= 1e-5"}
+    if "C1" in keep:
+        x = keep["C1"].cpu().numpy()
+        x64 = x.astype(np.float64)
+        ref, asum = x64.sum(1), np.abs(x64).sum(1)
+        acc["C1_sum_dim-1"] = {"gpu": _err_stats(gpu(keep["C1"], "sum", [-1]), ref, asum),
+                               "cpu_path": _err_stats(O.sum(x, [-1]), ref, asum)}
+    x = keep["C2"].cpu().numpy()
+    x64 = x.astype(np.float64)
+    ref, asum = x64.mean(1), np.abs(x64).mean(1)
+    c2 = {"mean_dim1": {"gpu": _err_stats(gpu(keep["C2"], "mean", [1]), ref, asum),
+                        "cpu_path": _err_stats(O.mean(x, [1]), ref, asum)}}
+    v = x64.var(2, ddof=1)
+    c2["var_dim-1"] = {"gpu": _err_stats(gpu(keep["C2"], "var", [-1]), v), "cpu_path": _err_stats(O.var(x, [-1]), v)}
+    c2["std_dim-1"] = {"gpu": _err_stats(gpu(keep["C2"], "std", [-1]), np.sqrt(v)),
+                       "cpu_path": _err_stats(O.std(x, [-1]), np.sqrt(v))}
+    acc["C2"] = c2
+    del x, x64
+    if "C4" in keep:
+        x = keep["C4"].cpu().numpy()
+        x64 = x.astype(np.float64)
+        s, asum = x64.sum(), np.abs(x64).sum()
+        m = s / x.size
+        v = x64.var(ddof=1)
+        del x64
+        c4 = {"sum": {"gpu": _err_stats(gpu(keep["C4"], "sum", None), s, asum),
+                      "cpu_path": _err_stats(O.sum(x), s, asum)},
+              "mean": {"gpu": _err_stats(gpu(keep["C4"], "mean", None), m, asum / x.size),
+                       "cpu_path": _err_stats(O.mean(x), m, asum / x.size)},
+              "var": {"gpu": _err_stats(gpu(keep["C4"], "var", None), v), "cpu_path": _err_stats(O.var(x), v)},
+              "std": {"gpu": _err_stats(gpu(keep["C4"], "std", None), np.sqrt(v)),
+                      "cpu_path": _err_stats(O.std(x), np.sqrt(v))}}
+        acc["C4"] = c4
+    return acc
 
 
 def cpu_baseline(x_dev, ops2, op_bytes, budget_s=10.0):
