@@ -46,6 +46,8 @@ struct DebugKnobs {
     Knob smx_split{0};
     Knob smx_res{0};
     Knob rowreg{0};
+    Knob topk_short{0};
+    Knob topk_radix{0};
 };
 DebugKnobs& knobs();
 

@@ -52,7 +52,7 @@ constexpr int kMaxW = 16;        // most waves of any top-k workgroup (1024 thre
 constexpr int kV = 4;            // float4 loads per thread per chunk (block kernel)
 constexpr int kCH = kT * 4 * kV; // elements per block-kernel chunk (8192)
 constexpr int kB = 2048;         // block candidate list capacity
-constexpr int kKMax = 1024;      // largest k
+constexpr int kKMax = 1024;      // largest k of the segment kernels (larger k: k_topk_radix)
 constexpr int kMergeT = 256;     // merge workgroup
 constexpr int kMergeMax = 4096;  // candidates a merge workgroup ranks (nseg * k)
 
@@ -528,6 +528,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kBufWord3 = 0x00020000;  // raw buffer resource, 32-bit data (gfx9 family)
 constexpr int kNT = 2;                 // cache policy bit: nontemporal (the row is read once)
 
+// One float through a buffer resource (the 32-bit buffer load returns the raw
+// bits as an unsigned int: reinterpret, never convert).
+__device__ __forceinline__ float buf_ld_f32(__amdgpu_buffer_rsrc_t r, int off) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kNT));
+}
+
 // Segment loads go through a buffer resource whose range is the segment: the
 // hardware range check is per dword, so a load past the segment end returns 0
 // and moves no data.  Slice loads are therefore unconditional (a prefetch past
@@ -549,10 +555,8 @@ __device__ __forceinline__ void load_slice(float4 (&cur)[SV], __amdgpu_buffer_rs
             const f32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kNT);
             cur[j] = make_float4(v.x, v.y, v.z, v.w);
         } else {
-            cur[j] = make_float4(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kNT),
-                                 __builtin_amdgcn_raw_buffer_load_b32(r, off + 4, 0, kNT),
-                                 __builtin_amdgcn_raw_buffer_load_b32(r, off + 8, 0, kNT),
-                                 __builtin_amdgcn_raw_buffer_load_b32(r, off + 12, 0, kNT));
+            cur[j] = make_float4(buf_ld_f32(r, off), buf_ld_f32(r, off + 4), buf_ld_f32(r, off + 8),
+                                 buf_ld_f32(r, off + 12));
         }
     }
 }
@@ -912,6 +916,259 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(6, 8))) void
     write_segment(a, row, seg, p, sel, k);
 }
 
+// ---------------------------------------------------------------------------
+// Short rows (cols <= 4096, k <= 64): L lanes per row, G = 64 / L rows per
+// wave, 4 waves per workgroup and no workgroup barrier.  Each lane holds E4
+// float4 of its row in registers (lane sl, vector j: elements
+// 4*(j*L + sl) .. +3, so the L lanes of a row read 16*L contiguous bytes per
+// vector), so the row is read from HBM exactly once and selected without
+// touching memory again:
+//   * bound: a bitonic sort of the L per-lane maxima inside the row's lane
+//     group gives their k-th largest T0 (k <= L), which has >= k elements at
+//     or above it;
+//   * candidates: the elements >= T0 (usually a few times k) go to a
+//     row-private LDS list at positions from a group prefix scan of the lanes'
+//     counts;
+//   * ranking: rank = number of candidates with a larger composite
+//     (composites are distinct), ranks < k are written in order;
+//   * exact path, when more than 8L elements tie at or above T0 (all-equal
+//     rows, long runs): the exact k-th key T* by a 32-step bit search over the
+//     keys in registers, every key > T* plus the lowest-index keys == T*
+//     (index order: vector j, then lane, then component), then the ranking.
+// ---------------------------------------------------------------------------
+constexpr int kShortT = 256;  // threads per short-row workgroup (4 waves)
+constexpr int kShortMaxCols = 4096;
+constexpr int kShortMaxK = 64;
+
+template <int L>
+__device__ __forceinline__ int group_sum(int v) {
+#pragma unroll
+    for (int o = 1; o < L; o <<= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Inclusive prefix sum over the lanes of an L-lane group (sl = lane in group).
+template <int L>
+__device__ __forceinline__ int group_scan(int v, int sl) {
+#pragma unroll
+    for (int o = 1; o < L; o <<= 1) {
+        const int t = __shfl_up(v, o, 64);
+        if (sl >= o) v += t;
+    }
+    return v;
+}
+
+// k-th largest (1 <= k <= L) of the values m held by the L lanes of each group.
+template <int L>
+__device__ __forceinline__ uint32_t group_kth_largest(uint32_t m, int k, int sl) {
+    uint32_t v = m;
+#pragma unroll
+    for (int size = 2; size <= L; size <<= 1) {
+#pragma unroll
+        for (int stride = size / 2; stride > 0; stride >>= 1) {
+            const uint32_t o = __shfl_xor(v, stride, 64);
+            const bool asc = (sl & size) == 0;
+            const bool lower = (sl & stride) == 0;
+            v = (lower == asc) ? min(v, o) : max(v, o);
+        }
+    }
+    // ascending within the group: position L - k holds the k-th largest
+    return __shfl(v, ((int)__lane_id() & ~(L - 1)) + (L - k), 64);
+}
+
+template <int L, int E4, bool VEC>
+__global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
+    constexpr int G = 64 / L;
+    constexpr int E = 4 * E4;
+    constexpr int C = 8 * L;  // candidate capacity of one row
+    constexpr int RPB = (kShortT / 64) * G;
+    __shared__ unsigned long long cl[RPB][C];
+    const int lane = __lane_id();
+    const int grp = lane / L;
+    const int sl = lane % L;
+    const int slot = (threadIdx.x / 64) * G + grp;
+    const long long row = (long long)blockIdx.x * RPB + slot;
+    const bool live = row < a.rows;
+    const int cols = a.cols;
+    const int k = a.k;
+    const int largest = a.largest;
+    const float* p = a.in + (live ? row * a.row_stride : 0);
+    const __amdgpu_buffer_rsrc_t rs = segment_rsrc(p, live ? cols : 0);
+
+    float4 x[E4];
+#pragma unroll
+    for (int j = 0; j < E4; ++j) {
+        const int off = 16 * (j * L + sl);
+        if constexpr (VEC) {
+            const f32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kNT);
+            x[j] = make_float4(v.x, v.y, v.z, v.w);
+        } else {
+            x[j] = make_float4(buf_ld_f32(rs, off), buf_ld_f32(rs, off + 4), buf_ld_f32(rs, off + 8),
+                               buf_ld_f32(rs, off + 12));
+        }
+    }
+    uint32_t key[E];
+    const uint32_t lm = largest ? 0u : 0xffffffffu;
+    if (cols == 4 * E4 * L) {  // every element of every lane is in the row
+#pragma unroll
+        for (int j = 0; j < E4; ++j) {
+            key[4 * j + 0] = f2key_sel(x[j].x, lm);
+            key[4 * j + 1] = f2key_sel(x[j].y, lm);
+            key[4 * j + 2] = f2key_sel(x[j].z, lm);
+            key[4 * j + 3] = f2key_sel(x[j].w, lm);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < E4; ++j) {
+            const int e = 4 * (j * L + sl);
+            key[4 * j + 0] = (e + 0 < cols) ? f2key_sel(x[j].x, lm) : 0u;
+            key[4 * j + 1] = (e + 1 < cols) ? f2key_sel(x[j].y, lm) : 0u;
+            key[4 * j + 2] = (e + 2 < cols) ? f2key_sel(x[j].z, lm) : 0u;
+            key[4 * j + 3] = (e + 3 < cols) ? f2key_sel(x[j].w, lm) : 0u;
+        }
+    }
+    if (!live) {
+#pragma unroll
+        for (int q = 0; q < E; ++q) key[q] = 0u;
+    }
+
+    uint32_t mx = 0;
+#pragma unroll
+    for (int q = 0; q < E; ++q) mx = max(mx, key[q]);
+    const uint32_t T = max(group_kth_largest<L>(mx, k, sl), 1u);  // valid keys are >= 1
+    int n = 0;
+#pragma unroll
+    for (int q = 0; q < E; ++q) n += (key[q] >= T) ? 1 : 0;
+    const int incl = group_scan<L>(n, sl);
+    int c = __shfl(incl, grp * L + L - 1, 64);  // candidates of this row
+    unsigned long long* list = cl[slot];
+    if (c <= C) {
+        int pos = incl - n;
+#pragma unroll
+        for (int q = 0; q < E; ++q) {
+            if (key[q] >= T) list[pos++] = comp_key(key[q], (uint32_t)(4 * ((q >> 2) * L + sl) + (q & 3)));
+        }
+    } else {
+        // exact k-th key by bit search over every key of the row
+        uint32_t pre = 0;
+        for (int b = 31; b >= 0; --b) {
+            const uint32_t cand = pre | (1u << b);
+            int cnt = 0;
+#pragma unroll
+            for (int q = 0; q < E; ++q) cnt += (key[q] >= cand) ? 1 : 0;
+            if (group_sum<L>(cnt) >= k) pre = cand;
+        }
+        int ng = 0;
+#pragma unroll
+        for (int q = 0; q < E; ++q) ng += (key[q] > pre) ? 1 : 0;
+        const int gincl = group_scan<L>(ng, sl);
+        const int cgt = __shfl(gincl, grp * L + L - 1, 64);  // < k
+        int pos = gincl - ng;
+#pragma unroll
+        for (int q = 0; q < E; ++q) {
+            if (key[q] > pre) list[pos++] = comp_key(key[q], (uint32_t)(4 * ((q >> 2) * L + sl) + (q & 3)));
+        }
+        // keys == pre in index order (vector j, lane, component) until k are taken
+        int taken = cgt;
+#pragma unroll
+        for (int j = 0; j < E4; ++j) {
+            int ne = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ne += (key[4 * j + q] == pre) ? 1 : 0;
+            const int einc = group_scan<L>(ne, sl);
+            int at = taken + einc - ne;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (key[4 * j + q] == pre) {
+                    if (at < k) list[at] = comp_key(pre, (uint32_t)(4 * (j * L + sl) + q));
+                    ++at;
+                }
+            }
+            taken += __shfl(einc, grp * L + L - 1, 64);
+        }
+        c = k;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int i = sl; i < c; i += L) {
+        const unsigned long long ci = list[i];
+        int r = 0;
+        for (int j = 0; j < c; ++j) r += (list[j] > ci) ? 1 : 0;
+        if (r < k && live) {
+            const uint32_t idx = comp_index(ci);
+            a.out_v[row * k + r] = selected_value(p, (uint32_t)(ci >> 32), idx, largest);
+            a.out_i[row * k + r] = (long long)idx;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Large k (k > 128, or k > 64 on rows the wave kernel does not take): one
+// 1024-thread workgroup per row.  Exact radix select of the k-th key in four
+// 8-bit passes over the row with LDS histograms (exact_select), the k
+// selected composites gathered (every larger key, then the lowest-index equal
+// keys), then a bitonic sort of the k survivors, padded to a power of two with
+// zero composites (below every element), in LDS for k <= kRadixLds, else in
+// the row's slice of the workspace.
+// ---------------------------------------------------------------------------
+constexpr int kRadixT = 1024;
+constexpr int kRadixLds = 4096;  // composites sorted in LDS (32 KiB)
+
+__host__ __device__ inline int pow2_at_least(int v) {
+    int p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+// Descending bitonic sort of c[0..n) (n a power of two) by the NT threads.
+template <int NT>
+__device__ void bitonic_desc(unsigned long long* c, int n) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size / 2; stride > 0; stride >>= 1) {
+            for (int t = threadIdx.x; t < n / 2; t += NT) {
+                const int i = 2 * stride * (t / stride) + (t % stride);
+                const int j = i + stride;
+                const unsigned long long ci = c[i], cj = c[j];
+                const bool desc = (i & size) == 0;  // this block's final direction
+                if (desc ? (ci < cj) : (ci > cj)) {
+                    c[i] = cj;
+                    c[j] = ci;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+struct RadixShared {
+    unsigned long long cand[kRadixLds];
+    BlockScratch bs;
+};
+
+__global__ __launch_bounds__(kRadixT) void k_topk_radix(TopkArgs a, unsigned long long* gcand) {
+    __shared__ RadixShared sh;
+    const long long row = blockIdx.x;
+    const float* p = a.in + row * a.row_stride;
+    const int k = a.k;
+    const int n2 = pow2_at_least(k);
+    unsigned long long* cand = (n2 <= kRadixLds) ? sh.cand : gcand + row * (long long)n2;
+    exact_select<kRadixT>(sh.bs, cand, p, 0, a.cols, k, a.largest);
+    for (int i = k + threadIdx.x; i < n2; i += kRadixT) cand[i] = 0ull;
+    __syncthreads();
+    bitonic_desc<kRadixT>(cand, n2);
+    if (a.sample) {
+        if (threadIdx.x < 64) sample_from_sel(a, row, p, cand, k);
+        return;
+    }
+    for (int i = threadIdx.x; i < k; i += kRadixT) {
+        const unsigned long long c = cand[i];
+        const uint32_t idx = comp_index(c);
+        a.out_v[row * k + i] = selected_value(p, (uint32_t)(c >> 32), idx, a.largest);
+        a.out_i[row * k + i] = (long long)idx;
+    }
+}
+
 struct MergeShared {
     unsigned long long cand[kMergeMax];
     int rank[kMergeMax];
@@ -989,6 +1246,21 @@ TopkPlan plan_topk(long long rows, long long cols, long long k) {
     return pl;
 }
 
+// Large k takes the radix-select kernel (any k <= cols); so does k > 128, and
+// k > 64 on rows shorter than the wave kernel's minimum segment.
+bool radix_route(long long cols, long long k) {
+    if (k > kKMax) return true;
+    if (knobs().topk_radix < 0 || knobs().topk_fallback) return false;
+    if (knobs().topk_radix > 0) return true;
+    return k > kWaveK || (k > kShortMaxK && cols < kWaveMinSeg);
+}
+
+// Workspace of the radix kernel: composites sorted outside LDS.
+size_t radix_ws(long long rows, long long k) {
+    const long long n2 = pow2_at_least((int)k);
+    return n2 > kRadixLds ? (size_t)rows * (size_t)n2 * sizeof(unsigned long long) : 0;
+}
+
 }  // namespace
 }  // namespace tpr
 
@@ -996,7 +1268,8 @@ extern "C" {
 
 size_t tpr_topk_workspace_bytes(int32_t dtype, int64_t rows, int64_t cols, int64_t k) {
     (void)dtype;
-    if (rows <= 0 || cols <= 0 || k <= 0 || k > cols || k > tpr::kKMax || cols > 0x7fffffffLL) return 0;
+    if (rows <= 0 || cols <= 0 || k <= 0 || k > cols || cols > 0x7fffffffLL) return 0;
+    if (tpr::radix_route(cols, k)) return tpr::radix_ws(rows, k);
     return tpr::plan_topk(rows, cols, k).ws;
 }
 
@@ -1004,6 +1277,34 @@ size_t tpr_topk_workspace_bytes(int32_t dtype, int64_t rows, int64_t cols, int64
 
 namespace tpr {
 namespace {
+// Short rows: L = lanes per row (>= k, >= cols / 64, >= 16), E4 = float4 per lane.
+template <int L, int E4>
+void launch_short_le(const TopkArgs& a, bool vec, hipStream_t st) {
+    constexpr int RPB = (kShortT / 64) * (64 / L);
+    const dim3 grid((unsigned)((a.rows + RPB - 1) / RPB));
+    if (vec) hipLaunchKernelGGL((k_topk_short<L, E4, true>), grid, dim3(kShortT), 0, st, a);
+    else hipLaunchKernelGGL((k_topk_short<L, E4, false>), grid, dim3(kShortT), 0, st, a);
+}
+
+template <int L>
+void launch_short_l(const TopkArgs& a, bool vec, hipStream_t st) {
+    const int e4 = (a.cols + 4 * L - 1) / (4 * L);
+    if (e4 <= 1) launch_short_le<L, 1>(a, vec, st);
+    else if (e4 <= 2) launch_short_le<L, 2>(a, vec, st);
+    else if (e4 <= 4) launch_short_le<L, 4>(a, vec, st);
+    else if (e4 <= 8) launch_short_le<L, 8>(a, vec, st);
+    else launch_short_le<L, 16>(a, vec, st);
+}
+
+int launch_short(const TopkArgs& a, bool vec, hipStream_t st) {
+    int L = 16;
+    while (L < a.k || L * 64 < a.cols) L *= 2;
+    if (L == 16) launch_short_l<16>(a, vec, st);
+    else if (L == 32) launch_short_l<32>(a, vec, st);
+    else launch_short_l<64>(a, vec, st);
+    return check_launch("k_topk_short");
+}
+
 // tpr_topk, or (smp != nullptr) tpr_sample: the same selection with the draw
 // in the final phase.
 int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t row_stride, int64_t k,
@@ -1014,9 +1315,10 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     if (k < 0 || k > cols) return fail(TPR_ERR_INVALID_ARG, "tpr_topk: selected index k out of range");
     if (rows == 0 || k == 0) return TPR_OK;
     if (cols > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: rows longer than 2^31-1");
-    if (k > kKMax) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: k > 1024 is not implemented");
     if (!in || (!smp && (!out_values || !out_indices))) return fail(TPR_ERR_INVALID_ARG, "tpr_topk: null pointer");
-    const TopkPlan pl = plan_topk(rows, cols, k);
+    if (rows > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: more than 2^31-1 rows");
+    const bool radix = radix_route(cols, k);
+    const TopkPlan pl = radix ? TopkPlan{1, (int)cols, false, 8, radix_ws(rows, k)} : plan_topk(rows, cols, k);
     if (rows * (long long)pl.nseg > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: grid too large");
     if (pl.ws > 0 && (workspace == nullptr || workspace_bytes < pl.ws))
         return fail(TPR_ERR_WORKSPACE, "tpr_topk: workspace too small (need " + std::to_string(pl.ws) + " bytes)");
@@ -1040,6 +1342,14 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     a.ids = smp ? smp->ids : nullptr;
     const bool vec = ((reinterpret_cast<uintptr_t>(in) & 15u) == 0) && (rows == 1 || row_stride % 4 == 0);
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (radix) {
+        hipLaunchKernelGGL(k_topk_radix, dim3(rows), dim3(kRadixT), 0, st, a,
+                           static_cast<unsigned long long*>(workspace));
+        return check_launch("k_topk_radix");
+    }
+    if (!smp && k <= kShortMaxK && cols <= kShortMaxCols && knobs().topk_short >= 0 && knobs().topk_fallback == 0 &&
+        knobs().splits <= 0)
+        return launch_short(a, vec, st);
     const long long grid = rows * pl.nseg;
     if (pl.wave) {
         // 512-thread workgroups (many rows): 8 waves/SIMD without prefetch.

@@ -14,7 +14,7 @@ torch = pytest.importorskip("torch")
 @pytest.fixture(autouse=True)
 def _reset_knobs():
     yield
-    for k in ("topk_fallback", "topk_variant", "topk_waves", "splits"):
+    for k in ("topk_fallback", "topk_variant", "topk_waves", "splits", "topk_short"):
         _capi.debug_set(k, 0)
 
 
@@ -65,6 +65,12 @@ def test_strided_and_misaligned_rows():
     check(b, b[:, 1:], 33)            # misaligned rows, odd stride
     check(b, b[::2, :4096], 64)       # row stride 2*5003
     check(b, b[:, 3:3 + 1031], 100)
+    # long misaligned rows: the wave kernel's 32-bit buffer loads
+    c = rng.standard_normal((4, 40003)).astype(np.float32)
+    for k in (1, 50, 128):
+        check(c, c[:, 1:], k)
+        check(c, c[:, 1:], k, False)
+    check(c, c[:, 2:], 64)
 
 
 def test_config3_uniform():
@@ -154,3 +160,78 @@ def test_denormals_signed_zeros_and_infinities(waves):
     for k in (1, 5, 64, 128):
         check(x, x, k, True)
         check(x, x, k, False)
+
+
+@pytest.mark.parametrize("short", [1, -1])
+def test_short_rows(short):
+    """Rows of <= 4096 elements with k <= 64 take the lane-group kernel (16, 32
+    or 64 lanes per row, rows held in registers); -1 forces the workgroup
+    kernels for the same cases.  Ragged row lengths, row counts that leave a
+    workgroup partly empty, misaligned rows, ties, NaN / +-0 / +-inf."""
+    _capi.debug_set("topk_short", short)
+    rng = np.random.default_rng(28)
+    for rows, cols in [(1, 5), (7, 16), (33, 64), (19, 255), (130, 256), (9, 1000), (5, 2049), (6, 4096),
+                       (3, 4093)]:
+        x = rng.uniform(-1, 1, (rows, cols)).astype(np.float32)
+        for k in sorted({1, min(cols, 3), min(cols, 8), min(cols, 17), min(cols, 32), min(cols, 64)}):
+            check(x, x, k, True)
+            check(x, x, k, False)
+    b = rng.standard_normal((40, 1031)).astype(np.float32)
+    check(b, b[:, 1:1025], 16)          # misaligned rows: scalar loads
+    check(b, b[::3, :600], 50)
+    # exact path: more than 8 lanes' worth of elements tie at or above the bound
+    t = np.full((5, 3000), 2.0, np.float32)
+    t[1, ::2] = 1.0
+    t[2] = np.round(rng.standard_normal(3000) * 2) / 2
+    t[3, 100:2100] = 7.0
+    t[4] = np.where(rng.random(3000) < 0.5, -0.0, 0.0)
+    for k in (1, 10, 33, 64):
+        check(t, t, k, True)
+        check(t, t, k, False)
+    s = rng.standard_normal((8, 512)).astype(np.float32)
+    s[0, ::5] = np.nan
+    s[1, :] = -np.inf
+    s[2, 7] = np.inf
+    s[3, :] = np.float32(1e-45)
+    s[3, 300] = -np.float32(1e-45)
+    for k in (1, 7, 64):
+        check(s, s, k, True)
+        check(s, s, k, False)
+
+
+def test_short_rows_many():
+    # BASELINE-like volumes of short rows: every row and every output checked
+    rng = np.random.default_rng(29)
+    x = rng.uniform(-1, 1, (65536, 256)).astype(np.float32)
+    check(x, x, 8)
+    y = rng.standard_normal((16384, 1024)).astype(np.float32)
+    check(y, y, 32)
+
+
+@pytest.mark.parametrize("force", [0, 1])
+def test_radix_select_large_k(force):
+    """k_topk_radix: exact 8-bit radix select of the k-th key, then a bitonic
+    sort of the k survivors (in LDS up to 4096, in the workspace beyond).
+    force=1 sends small k through it as well."""
+    _capi.debug_set("topk_radix", force)
+    rng = np.random.default_rng(30)
+    x = rng.standard_normal((7, 5000)).astype(np.float32)
+    x[1] = np.round(x[1] * 2) / 2            # heavy ties
+    x[2] = 3.0                                # all equal
+    x[3, ::3] = np.nan
+    x[4] = np.where(rng.random(5000) < 0.5, -0.0, 0.0)
+    for k in (1, 65, 129, 1000, 1025, 4096, 4097, 5000):
+        check(x, x, k, True)
+        check(x, x, k, False)
+    y = rng.uniform(-1, 1, (3, 20000)).astype(np.float32)
+    check(y, y, 8193)                         # workspace sort (k > 4096)
+    check(y, y[:, 1:], 3000, False)           # misaligned rows
+
+
+def test_large_k_configs():
+    rng = np.random.default_rng(31)
+    x = rng.uniform(-1, 1, (4096, 2048)).astype(np.float32)
+    check(x, x, 1000)
+    c3 = rng.uniform(-1, 1, (1024, 32768)).astype(np.float32)
+    check(c3, c3, 2048)
+    check(c3[:256], c3[:256], 4096)
