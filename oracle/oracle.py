@@ -370,7 +370,7 @@ def reduce_backward(grad, x, op, dims=None, correction=1, result=None):
     raise ValueError(op)
 
 
-def sample(x2d, u, k, temperature=1.0, top_p=1.0):
+def sample(x2d, u, k, temperature=1.0, top_p=1.0, details=False):
     """Top-k / top-p sampling (this build's definition; TensorPlay has none):
     the k largest logits per row (topk order: descending, ties to the lowest
     index), p_j = exp(v_j/T - v_0/T), c_j = cumulative sums, nucleus 0..m with m
@@ -379,14 +379,21 @@ def sample(x2d, u, k, temperature=1.0, top_p=1.0):
     Returns (ids, margin): margin is the smallest relative distance of the two
     decision thresholds (top_p cut, u draw) to a cumulative sum -- where it is
     below the float32 rounding of the GPU's sums, either neighbour is a valid
-    draw."""
+    draw.  details=True also returns, per row, the nucleus end m, the drawn
+    position j (both in top-k order) and the cut's own relative margin."""
     x2d = np.asarray(x2d, np.float32)
     rows = x2d.shape[0]
     vals, idx = topk(x2d, k)
     if not temperature > 0:
+        if details:
+            z = np.zeros(rows, np.int64)
+            return idx[:, 0].copy(), np.full(rows, np.inf), z, z.copy(), np.full(rows, np.inf)
         return idx[:, 0].copy(), np.full(rows, np.inf)
     ids = np.empty(rows, np.int64)
     margin = np.empty(rows)
+    ms = np.empty(rows, np.int64)
+    js = np.empty(rows, np.int64)
+    cut_margin = np.empty(rows)
     for r in range(rows):
         z = vals[r].astype(np.float64) / temperature
         p = np.exp(z - z[0])
@@ -398,7 +405,11 @@ def sample(x2d, u, k, temperature=1.0, top_p=1.0):
         hit = np.nonzero(c[: m + 1] > thr)[0]
         j = int(hit[0]) if hit.size else m
         ids[r] = idx[r, j]
-        margin[r] = min(np.min(np.abs(c - cut)) / c[-1], np.min(np.abs(c[: m + 1] - thr)) / c[m])
+        cut_margin[r] = np.min(np.abs(c - cut)) / c[-1]
+        margin[r] = min(cut_margin[r], np.min(np.abs(c[: m + 1] - thr)) / c[m])
+        ms[r], js[r] = m, j
+    if details:
+        return ids, margin, ms, js, cut_margin
     return ids, margin
 
 

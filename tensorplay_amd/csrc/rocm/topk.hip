@@ -958,9 +958,10 @@ __device__ __forceinline__ int group_scan(int v, int sl) {
     return v;
 }
 
-// k-th largest (1 <= k <= L) of the values m held by the L lanes of each group.
+// Bitonic sort (ascending) of the values m held by the L lanes of each group:
+// lane sl of the group returns the sl-th smallest.
 template <int L>
-__device__ __forceinline__ uint32_t group_kth_largest(uint32_t m, int k, int sl) {
+__device__ __forceinline__ uint32_t group_sort_asc(uint32_t m, int sl) {
     uint32_t v = m;
 #pragma unroll
     for (int size = 2; size <= L; size <<= 1) {
@@ -972,8 +973,50 @@ __device__ __forceinline__ uint32_t group_kth_largest(uint32_t m, int k, int sl)
             v = (lower == asc) ? min(v, o) : max(v, o);
         }
     }
-    // ascending within the group: position L - k holds the k-th largest
-    return __shfl(v, ((int)__lane_id() & ~(L - 1)) + (L - k), 64);
+    return v;
+}
+
+__device__ __forceinline__ void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// hist_threshold for one L-lane group: bins [T, T + 256 << shift), lane sl of
+// the group owns bins sl*NB .. sl*NB + NB-1.  Returns the lower edge of the bin
+// where the count from the top first reaches k (T when it never does).
+template <int L>
+__device__ __forceinline__ uint32_t group_hist_threshold(const uint32_t* hist, int k, uint32_t T, int shift,
+                                                         int sl, int grp) {
+    constexpr int NB = 256 / L;
+    uint32_t h[NB];
+    int own = 0;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        h[b] = hist[sl * NB + b];
+        own += (int)h[b];
+    }
+    int suf = own;  // inclusive suffix sum over the group's lanes >= sl
+#pragma unroll
+    for (int o = 1; o < L; o <<= 1) {
+        const int t = __shfl_down(suf, o, 64);
+        if (sl + o < L) suf += t;
+    }
+    const unsigned long long gmask = (L == 64) ? ~0ull : ((1ull << L) - 1ull);
+    const unsigned long long ok = (__ballot(suf >= k) >> (grp * L)) & gmask;
+    if (ok == 0ull) return T;
+    const int hl = 63 - __clzll((long long)ok);  // highest lane of the group whose suffix reaches k
+    uint32_t tn = 0;
+    if (sl == hl) {
+        int cum = suf - own;
+        int b = NB - 1;
+        for (; b > 0; --b) {
+            if (cum + (int)h[b] >= k) break;
+            cum += (int)h[b];
+        }
+        tn = T + ((uint32_t)(sl * NB + b) << shift);
+    }
+    return __shfl(tn, grp * L + hl, 64);
 }
 
 template <int L, int E4, bool VEC>
@@ -983,6 +1026,7 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
     constexpr int C = 8 * L;  // candidate capacity of one row
     constexpr int RPB = (kShortT / 64) * G;
     __shared__ unsigned long long cl[RPB][C];
+    __shared__ uint32_t hl[RPB][256];
     const int lane = __lane_id();
     const int grp = lane / L;
     const int sl = lane % L;
@@ -1035,7 +1079,9 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
     uint32_t mx = 0;
 #pragma unroll
     for (int q = 0; q < E; ++q) mx = max(mx, key[q]);
-    const uint32_t T = max(group_kth_largest<L>(mx, k, sl), 1u);  // valid keys are >= 1
+    const uint32_t srt = group_sort_asc<L>(mx, sl);
+    const uint32_t T = max(__shfl(srt, grp * L + (L - k), 64), 1u);  // k-th largest lane max; valid keys are >= 1
+    const uint32_t gmax = __shfl(srt, grp * L + L - 1, 64);
     int n = 0;
 #pragma unroll
     for (int q = 0; q < E; ++q) n += (key[q] >= T) ? 1 : 0;
@@ -1047,6 +1093,39 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
 #pragma unroll
         for (int q = 0; q < E; ++q) {
             if (key[q] >= T) list[pos++] = comp_key(key[q], (uint32_t)(4 * ((q >> 2) * L + sl) + (q & 3)));
+        }
+        if (c * c > 256 * L && c > 2 * k) {
+            // Raise the bound with a 256-bin histogram of the candidates over
+            // [T, row max] (the lower edge of the bin where the count from the
+            // top reaches k), so the ranking below sees about k entries.  Only
+            // when ranking all c candidates (c * c / L compares per lane) costs
+            // more than the histogram (measured on MI355X: [16384, 1024] k = 32
+            // 70 -> 38 us; [65536, 256] k = 8, about 30 candidates, is faster
+            // without it: 19.8 us against 24.8 us).
+            constexpr int PER = C / L;
+            uint32_t* hist = hl[slot];
+            wave_sync_lds();
+            unsigned long long mine[PER];
+#pragma unroll
+            for (int r = 0; r < PER; ++r) mine[r] = (sl + r * L < c) ? list[sl + r * L] : 0ull;
+#pragma unroll
+            for (int b = 0; b < 256 / L; ++b) hist[sl * (256 / L) + b] = 0u;
+            const int shift = hist_shift(gmax, T);
+            wave_sync_lds();
+#pragma unroll
+            for (int r = 0; r < PER; ++r)
+                if (mine[r]) atomicAdd(&hist[((uint32_t)(mine[r] >> 32) - T) >> shift], 1u);
+            wave_sync_lds();
+            const uint32_t T1 = group_hist_threshold<L>(hist, k, T, shift, sl, grp);
+            int nk = 0;
+#pragma unroll
+            for (int r = 0; r < PER; ++r) nk += (mine[r] && (uint32_t)(mine[r] >> 32) >= T1) ? 1 : 0;
+            const int kinc = group_scan<L>(nk, sl);
+            c = __shfl(kinc, grp * L + L - 1, 64);
+            int kpos = kinc - nk;
+#pragma unroll
+            for (int r = 0; r < PER; ++r)
+                if (mine[r] && (uint32_t)(mine[r] >> 32) >= T1) list[kpos++] = mine[r];
         }
     } else {
         // exact k-th key by bit search over every key of the row
@@ -1088,9 +1167,7 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
         }
         c = k;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    wave_sync_lds();
     for (int i = sl; i < c; i += L) {
         const unsigned long long ci = list[i];
         int r = 0;
@@ -1112,8 +1189,9 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
 // zero composites (below every element), in LDS for k <= kRadixLds, else in
 // the row's slice of the workspace.
 // ---------------------------------------------------------------------------
-constexpr int kRadixT = 1024;
+constexpr int kRadixT = 256;    // threads per row (several rows per CU)
 constexpr int kRadixLds = 4096;  // composites sorted in LDS (32 KiB)
+constexpr int kRadixBins = 2048; // 11-bit digits: passes over key bits 31..21, 20..10, 9..0
 
 __host__ __device__ inline int pow2_at_least(int v) {
     int p = 1;
@@ -1143,8 +1221,115 @@ __device__ void bitonic_desc(unsigned long long* c, int n) {
 
 struct RadixShared {
     unsigned long long cand[kRadixLds];
-    BlockScratch bs;
+    uint32_t hist[kRadixBins];
+    int wtot[kRadixT / 64];
+    int digit, kk, count, eq_taken;
 };
+
+// Inclusive suffix sum over the workgroup's threads (thread t gets the sum of
+// v over threads t .. NT-1).  Ends with a barrier.
+template <int NT>
+__device__ int block_suffix_incl(int v, int* wtot) {
+    constexpr int NW = NT / 64;
+    const int lane = __lane_id();
+    const int w = threadIdx.x / 64;
+    int suf = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_down(suf, o, 64);
+        if (lane + o < 64) suf += t;
+    }
+    if (lane == 0) wtot[w] = suf;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NW; ++i)
+        if (i > w) suf += wtot[i];
+    __syncthreads();
+    return suf;
+}
+
+// Exact top-k selection of p[0..n) into cand[0..k) (unordered): the k-th key T
+// by three radix passes over the keys (11, 11, 10 bits; each pass counts the
+// keys that match the digits found so far in a 2048-bin LDS histogram), then
+// every key > T and the lowest-index keys == T.
+template <int NT>
+__device__ void radix_select(RadixShared& sh, unsigned long long* cand, const float* p, int n, int k,
+                             int largest) {
+    constexpr int BPT = kRadixBins / NT;  // histogram bins per thread in the digit search
+    const int tid = threadIdx.x;
+    const int lane = __lane_id();
+    const int w = tid / 64;
+    uint32_t prefix = 0, pmask = 0;
+    int kk = k;
+    for (int pass = 0; pass < 3; ++pass) {
+        const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+        const uint32_t dmask = pass < 2 ? 0x7ffu : 0x3ffu;
+        for (int i = tid; i < kRadixBins; i += NT) sh.hist[i] = 0u;
+        __syncthreads();
+        for (int e = tid; e < n; e += NT) {
+            const uint32_t key = f2key(p[e], largest);
+            if ((key & pmask) == prefix) atomicAdd(&sh.hist[(key >> shift) & dmask], 1u);
+        }
+        __syncthreads();
+        uint32_t h[BPT];
+        int own = 0;
+#pragma unroll
+        for (int b = 0; b < BPT; ++b) {
+            h[b] = sh.hist[tid * BPT + b];
+            own += (int)h[b];
+        }
+        const int suf = block_suffix_incl<NT>(own, sh.wtot);
+        if (suf >= kk && suf - own < kk) {  // the thread whose bins hold the kk-th key from the top
+            int cum = suf - own;
+            int b = BPT - 1;
+            for (; b > 0; --b) {
+                if (cum + (int)h[b] >= kk) break;
+                cum += (int)h[b];
+            }
+            sh.digit = tid * BPT + b;
+            sh.kk = kk - cum;
+        }
+        __syncthreads();
+        prefix |= (uint32_t)sh.digit << shift;
+        pmask |= dmask << shift;
+        kk = sh.kk;
+        __syncthreads();
+    }
+    const uint32_t T = prefix;  // the k-th key; take kk of the keys equal to it
+    if (tid == 0) {
+        sh.count = 0;
+        sh.eq_taken = 0;
+    }
+    __syncthreads();
+    for (int base = 0; base < n; base += NT) {
+        const int e = base + tid;
+        const uint32_t key = (e < n) ? f2key(p[e], largest) : 0u;
+        if (e < n && key > T) cand[atomicAdd(&sh.count, 1)] = comp_key(key, (uint32_t)e);
+        const bool eq = (e < n) && key == T;
+        const unsigned long long bal = __ballot(eq);
+        if (lane == 0) sh.wtot[w] = __popcll(bal);
+        __syncthreads();
+        int before = sh.eq_taken + __popcll(bal & lanemask_lt());
+        int total = 0;
+        for (int i = 0; i < NT / 64; ++i) {
+            if (i < w) before += sh.wtot[i];
+            total += sh.wtot[i];
+        }
+        if (eq && before < kk) cand[atomicAdd(&sh.count, 1)] = comp_key(key, (uint32_t)e);
+        __syncthreads();
+        if (tid == 0) sh.eq_taken += total;
+        __syncthreads();
+        if (sh.eq_taken >= kk && base + NT < n) {
+            // every equal key needed is taken: the rest only adds keys > T
+            for (int e2 = base + NT + tid; e2 < n; e2 += NT) {
+                const uint32_t k2 = f2key(p[e2], largest);
+                if (k2 > T) cand[atomicAdd(&sh.count, 1)] = comp_key(k2, (uint32_t)e2);
+            }
+            break;
+        }
+    }
+    __syncthreads();
+}
 
 __global__ __launch_bounds__(kRadixT) void k_topk_radix(TopkArgs a, unsigned long long* gcand) {
     __shared__ RadixShared sh;
@@ -1153,7 +1338,7 @@ __global__ __launch_bounds__(kRadixT) void k_topk_radix(TopkArgs a, unsigned lon
     const int k = a.k;
     const int n2 = pow2_at_least(k);
     unsigned long long* cand = (n2 <= kRadixLds) ? sh.cand : gcand + row * (long long)n2;
-    exact_select<kRadixT>(sh.bs, cand, p, 0, a.cols, k, a.largest);
+    radix_select<kRadixT>(sh, cand, p, a.cols, k, a.largest);
     for (int i = k + threadIdx.x; i < n2; i += kRadixT) cand[i] = 0ull;
     __syncthreads();
     bitonic_desc<kRadixT>(cand, n2);

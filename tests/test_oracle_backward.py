@@ -1,6 +1,8 @@
 """Pins the oracle's reduction gradients (oracle.reduce_backward, the
 derivatives.yaml formulas op by op in float32) against torch.autograd in fp64,
 full and along dims.  CPU only."""
+import zlib
+
 import numpy as np
 import pytest
 
@@ -47,7 +49,7 @@ CASES = [((1000,), None), ((33, 65), [1]), ((33, 65), [0]), ((4, 5, 6), [0, 2]),
 @pytest.mark.parametrize("op", ["sum", "mean", "var", "std"])
 @pytest.mark.parametrize("shape,dims", CASES)
 def test_reduce_backward_matches_torch_autograd(op, shape, dims):
-    rng = np.random.default_rng(hash((op, shape)) % 2**32)
+    rng = np.random.default_rng(zlib.crc32(f"{op}-{shape}".encode()))
     x = (rng.standard_normal(shape) * 2 + 0.5).astype(np.float32)
     for correction in ((1,) if op in ("sum", "mean") else (0, 1, 2)):
         y_shape = np.sum(x, axis=None if dims is None else tuple(dims)).shape

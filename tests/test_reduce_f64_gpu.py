@@ -105,3 +105,23 @@ def test_dispatcher_f64():
     assert t.mean().dtype == tp.float64
     m = t.median()  # lower median in float64
     assert m.dtype == tp.float64 and m.item() == np.sort(x.ravel())[(x.size - 1) // 2]
+
+
+def test_median_float64_special_values():
+    """float64 median: NaN ranks above every number (canonicalised), -inf/+inf at
+    the ends, -0.0 == +0.0 (returned as +0.0); against np.sort for every prefix
+    length, bit-exact."""
+    x = np.array([np.nan, 1.0, np.nan, -np.inf, 2.0, -0.0, 0.0, np.inf, np.nan, -1e-310, 1e-310], np.float64)
+    for k in range(1, len(x) + 1):
+        v = np.ascontiguousarray(x[:k])
+        print(f"case median f64 n={k}", flush=True)
+        got = _capi.reduce(torch.from_numpy(v).cuda(), "median", None).cpu().numpy().reshape(())
+        srt = np.sort(np.where(v == 0, 0.0, v))   # np.sort puts NaN last, as the key order
+        exp = srt[(k - 1) // 2]
+        if np.isnan(exp):
+            assert np.isnan(got)
+        else:
+            assert got.view(np.uint64) == np.float64(exp).view(np.uint64), (k, got, exp)
+    z = np.full(4, -0.0, np.float64)
+    got = _capi.reduce(torch.from_numpy(z).cuda(), "median", None).cpu().numpy().reshape(())
+    assert got == 0.0 and not np.signbit(got)

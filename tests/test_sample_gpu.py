@@ -18,14 +18,37 @@ torch = pytest.importorskip("torch")
 def check(x, u, k, T, top_p):
     print(f"case sample shape={x.shape} k={k} T={T} top_p={top_p}", flush=True)
     got = _capi.sample(torch.from_numpy(x).cuda(), torch.from_numpy(u).cuda(), k, T, top_p).cpu().numpy()
-    exp, margin = O.sample(x, u, k, T, top_p)
+    exp, margin, m, j, cut_margin = O.sample(x, u, k, T, top_p, details=True)
     sure = margin > 1e-5
     np.testing.assert_array_equal(got[sure], exp[sure])
     if (~sure).any():
         _, idx = O.topk(x, k)
         for r in np.nonzero(~sure)[0]:
-            assert got[r] in idx[r]
+            # a boundary draw: the GPU's position in the top-k order is the
+            # oracle's or a neighbour, and inside the oracle's nucleus 0..m
+            # (0..m+1 when the top-p cut itself is within float32 rounding)
+            pos = np.nonzero(idx[r] == got[r])[0]
+            assert pos.size == 1, (r, got[r])
+            m_hi = m[r] + (1 if cut_margin[r] <= 1e-5 else 0)
+            assert pos[0] <= m_hi, (r, pos[0], m[r])
+            assert abs(int(pos[0]) - int(j[r])) <= 1, (r, pos[0], j[r])
     return int((~sure).sum())
+
+
+def test_boundary_draws_stay_in_the_nucleus():
+    # u placed exactly on cumulative sums and top_p exactly on c_j / c_{k-1}:
+    # every row is a boundary case, checked by the nucleus rule above
+    rng = np.random.default_rng(33)
+    x = (rng.standard_normal((64, 500)) * 2).astype(np.float32)
+    _, _, m, j, _ = O.sample(x, np.full(64, 0.5, np.float32), 20, 1.0, 1.0, details=True)
+    vals, _ = O.topk(x, 20)
+    p = np.exp(vals.astype(np.float64) - vals[:, :1])
+    c = np.cumsum(p, axis=1)
+    u = (c[np.arange(64), rng.integers(0, 19, 64)] / c[:, -1]).astype(np.float32)
+    n = check(x, u, 20, 1.0, 1.0)
+    assert n > 0  # the construction produced boundary rows
+    top_p = float(c[0, 9] / c[0, -1])
+    check(x, rng.random(64).astype(np.float32), 20, 1.0, top_p)
 
 
 def test_parameter_grid():
