@@ -248,6 +248,41 @@ def topk(x2d, k, largest=True, threads=1):
     return vals, idx
 
 
+def sort_keys(x):
+    """Ascending sortable unsigned keys of any numpy dtype, the order tpr_topk
+    uses: floats by value with -0.0 == +0.0 and every NaN above +inf, signed
+    integers by value (sign bit flipped), unsigned integers and bool as they
+    are.  uint64 for 8-byte dtypes, uint32 otherwise."""
+    x = np.asarray(x)
+    if x.dtype == np.bool_:
+        return x.astype(np.uint32)
+    if x.dtype.kind == "f":
+        bits, ut, sign, qnan = ((np.uint64, np.uint64, np.uint64(1 << 63), np.uint64(0x7ff8000000000000))
+                                if x.dtype.itemsize == 8 else
+                                (np.uint32, np.uint32, np.uint32(1 << 31), np.uint32(0x7fc00000)))
+        u = x.view(bits).copy()
+        u[np.isnan(x)] = qnan
+        neg = (u & sign) != 0
+        out = np.where(neg, (~u) + ut(1), u | sign)  # -0.0 and +0.0 both map to `sign`
+        return out.astype(ut)
+    ut = np.uint64 if x.dtype.itemsize == 8 else np.uint32
+    if x.dtype.kind == "i":
+        w = x.dtype.itemsize * 8
+        u = x.view({1: np.uint8, 2: np.uint16, 4: np.uint32, 8: np.uint64}[x.dtype.itemsize])
+        return (u ^ np.array(1 << (w - 1), u.dtype)).astype(ut)
+    return x.astype(ut)
+
+
+def topk_any(x2d, k, largest=True):
+    """Top-k of a 2-D array of any dtype in this build's order (tpr_topk):
+    key descending (ascending for largest=False), equal keys by lowest index;
+    values are the selected elements.  numpy stable sort on sort_keys."""
+    x2d = np.asarray(x2d)
+    key = sort_keys(x2d)
+    order = np.argsort(~key if largest else key, axis=1, kind="stable")[:, :k]
+    return np.take_along_axis(x2d, order, axis=1), order.astype(np.int64)
+
+
 # P10 ScalarType numbering of numpy dtypes
 DTYPE_CODES = {np.dtype(np.uint8): 0, np.dtype(np.int8): 1, np.dtype(np.int16): 2, np.dtype(np.int32): 3,
                np.dtype(np.int64): 4, np.dtype(np.uint16): 5, np.dtype(np.uint32): 6, np.dtype(np.uint64): 7,

@@ -248,16 +248,18 @@ def reduce_noalloc(x, op, dims=None, correction=1, out=None, p=2.0):
 
 
 def topk(x2d, k, largest=True, sorted=True):
-    """Top-k along the last dim of a 2-D float32 device tensor (unit inner stride)."""
+    """Top-k along the last dim of a 2-D device tensor of any supported dtype
+    (unit inner stride).  Values keep the input dtype."""
     import torch
     assert x2d.dim() == 2 and (x2d.stride(1) == 1 or x2d.shape[1] <= 1)
     rows, cols = x2d.shape
-    vals = torch.empty((rows, k), dtype=torch.float32, device=x2d.device)
+    dt = _torch_dtypes()[x2d.dtype]
+    vals = torch.empty((rows, k), dtype=x2d.dtype, device=x2d.device)
     idx = torch.empty((rows, k), dtype=torch.int64, device=x2d.device)
     L = lib()
-    wsb = L.tpr_topk_workspace_bytes(FLOAT32, rows, cols, k)
+    wsb = L.tpr_topk_workspace_bytes(dt, rows, cols, k)
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x2d.device)
-    _check(L.tpr_topk(ctypes.c_void_p(x2d.data_ptr()), FLOAT32, rows, cols, x2d.stride(0), k,
+    _check(L.tpr_topk(ctypes.c_void_p(x2d.data_ptr()), dt, rows, cols, x2d.stride(0), k,
                       int(largest), int(sorted), ctypes.c_void_p(vals.data_ptr()),
                       ctypes.c_void_p(idx.data_ptr()), ctypes.c_void_p(ws.data_ptr()), wsb,
                       _stream(torch, x2d.device)))

@@ -297,7 +297,9 @@ Tensor median_kernel(const Tensor& self) {
 // contiguous when it is not already; the results are returned with `dim` in its
 // original position, dense.
 std::tuple<Tensor, Tensor> topk_kernel(const Tensor& self, int64_t k, int64_t dim, bool largest, bool sorted) {
-    require_float32_input(self, "topk");
+    // every dtype: values keep the input dtype (tpr_topk orders by the dtype's
+    // sortable key: floats with -0.0 == +0.0 and NaN largest, integers by value)
+    if (self.dim() > TPR_MAX_DIMS) TP_THROW(NotImplementedError, "topk: more than 8 dims on ROCm");
     const int64_t nd = self.dim();
     const int64_t d = (nd == 0) ? 0 : wrap(dim, nd);
     const int64_t n = (nd == 0) ? 1 : self.size(d);
@@ -342,11 +344,12 @@ std::tuple<Tensor, Tensor> topk_kernel(const Tensor& self, int64_t k, int64_t di
     oshape.push_back(k);
     Tensor vals = Tensor::empty(oshape, self.dtype(), self.device());
     Tensor idx = Tensor::empty(oshape, DType::Int64, self.device());
-    const size_t wsb = tpr_topk_workspace_bytes(TPR_FLOAT32, rows, n, k);
+    const int32_t tdt = (int32_t)self.dtype();  // P10 ScalarType numbering == tpr_dtype
+    const size_t wsb = tpr_topk_workspace_bytes(tdt, rows, n, k);
     std::shared_ptr<void> ws;
     if (wsb) ws = allocate(wsb, self.device());
     DeviceGuard guard(self.device());
-    const int rc = tpr_topk(x.data_ptr(), TPR_FLOAT32, rows, n, row_stride, k, largest ? 1 : 0, sorted ? 1 : 0,
+    const int rc = tpr_topk(x.data_ptr(), tdt, rows, n, row_stride, k, largest ? 1 : 0, sorted ? 1 : 0,
                             vals.data_ptr(), idx.data_ptr(), ws.get(), wsb, currentStream(self.device().index));
     if (rc != TPR_OK) throw_status(rc, "topk");
     if (nd > 0 && d != nd - 1) {

@@ -39,6 +39,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <string>
 
 #include "common.h"
@@ -1199,15 +1200,55 @@ __host__ __device__ inline int pow2_at_least(int v) {
     return p;
 }
 
+
+// Ascending sortable key of an element of any dtype, as an unsigned integer of
+// the element's width (32 bits for elements of at most 4 bytes): floats as
+// f2key (-0.0 == +0.0, every NaN above +inf), signed integers with the sign
+// bit flipped, unsigned integers and bool as they are; inverted for
+// largest = 0.
+template <class T>
+struct SortKey {
+    using K = typename std::conditional<(sizeof(T) > 4), unsigned long long, uint32_t>::type;
+    static constexpr int kBits = 8 * (int)sizeof(T);
+    __device__ static K of(T x, int largest) {
+        K k;
+        if constexpr (std::is_same<T, float>::value) {
+            return f2key(x, largest);
+        } else if constexpr (std::is_same<T, double>::value) {
+            const unsigned long long b = (unsigned long long)__double_as_longlong(x);
+            const unsigned long long u =
+                ((b & 0x7fffffffffffffffull) > 0x7ff0000000000000ull) ? 0x7ff8000000000000ull : b;
+            const unsigned long long m = (unsigned long long)((long long)u >> 63);
+            k = (u ^ (m | 0x8000000000000000ull)) - m;
+        } else if constexpr (std::is_signed<T>::value) {
+            using U = typename std::make_unsigned<T>::type;
+            k = (K)(U)((U)x ^ (U)((U)1 << (kBits - 1)));
+        } else {
+            k = (K)x;
+        }
+        if (!largest) k = ~k & (kBits == 64 ? ~(K)0 : (K)(((unsigned long long)1 << kBits) - 1));
+        return k;
+    }
+};
+
+// Composite (key, index) ordered by key, then by lowest index; never 0 for an
+// element (0 pads the bitonic sort).
+template <class K>
+struct Comp {
+    using C = typename std::conditional<(sizeof(K) > 4), unsigned __int128, unsigned long long>::type;
+    __device__ static C make(K key, uint32_t idx) { return ((C)key << 32) | (C)(0xffffffffu - idx); }
+    __device__ static uint32_t index(C c) { return 0xffffffffu - (uint32_t)(c & (C)0xffffffffu); }
+};
+
 // Descending bitonic sort of c[0..n) (n a power of two) by the NT threads.
-template <int NT>
-__device__ void bitonic_desc(unsigned long long* c, int n) {
+template <int NT, class C>
+__device__ void bitonic_desc(C* c, int n) {
     for (int size = 2; size <= n; size <<= 1) {
         for (int stride = size / 2; stride > 0; stride >>= 1) {
             for (int t = threadIdx.x; t < n / 2; t += NT) {
                 const int i = 2 * stride * (t / stride) + (t % stride);
                 const int j = i + stride;
-                const unsigned long long ci = c[i], cj = c[j];
+                const C ci = c[i], cj = c[j];
                 const bool desc = (i & size) == 0;  // this block's final direction
                 if (desc ? (ci < cj) : (ci > cj)) {
                     c[i] = cj;
@@ -1219,8 +1260,13 @@ __device__ void bitonic_desc(unsigned long long* c, int n) {
     }
 }
 
+// Composites sorted in LDS: 32 KiB of them (4096 for 32-bit keys, 2048 for 64-bit).
+template <class T>
+constexpr int radix_lds_count() { return sizeof(T) > 4 ? 2048 : kRadixLds; }
+
+template <class T>
 struct RadixShared {
-    unsigned long long cand[kRadixLds];
+    typename Comp<typename SortKey<T>::K>::C cand[radix_lds_count<T>()];
     uint32_t hist[kRadixBins];
     int wtot[kRadixT / 64];
     int digit, kk, count, eq_taken;
@@ -1249,26 +1295,28 @@ __device__ int block_suffix_incl(int v, int* wtot) {
 }
 
 // Exact top-k selection of p[0..n) into cand[0..k) (unordered): the k-th key T
-// by three radix passes over the keys (11, 11, 10 bits; each pass counts the
-// keys that match the digits found so far in a 2048-bin LDS histogram), then
-// every key > T and the lowest-index keys == T.
-template <int NT>
-__device__ void radix_select(RadixShared& sh, unsigned long long* cand, const float* p, int n, int k,
-                             int largest) {
+// by radix passes over the key bits from the top, 11 bits per pass (each pass
+// counts the keys that match the digits found so far in a 2048-bin LDS
+// histogram), then every key > T and the lowest-index keys == T.
+template <int NT, class T>
+__device__ void radix_select(RadixShared<T>& sh, typename Comp<typename SortKey<T>::K>::C* cand, const T* p, int n,
+                             int k, int largest) {
+    using K = typename SortKey<T>::K;
+    using CP = Comp<K>;
     constexpr int BPT = kRadixBins / NT;  // histogram bins per thread in the digit search
     const int tid = threadIdx.x;
     const int lane = __lane_id();
     const int w = tid / 64;
-    uint32_t prefix = 0, pmask = 0;
+    K prefix = 0, pmask = 0;
     int kk = k;
-    for (int pass = 0; pass < 3; ++pass) {
-        const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-        const uint32_t dmask = pass < 2 ? 0x7ffu : 0x3ffu;
+    for (int hi = SortKey<T>::kBits; hi > 0; hi -= 11) {
+        const int shift = hi > 11 ? hi - 11 : 0;
+        const K dmask = (K)((1u << (hi - shift)) - 1u);
         for (int i = tid; i < kRadixBins; i += NT) sh.hist[i] = 0u;
         __syncthreads();
         for (int e = tid; e < n; e += NT) {
-            const uint32_t key = f2key(p[e], largest);
-            if ((key & pmask) == prefix) atomicAdd(&sh.hist[(key >> shift) & dmask], 1u);
+            const K key = SortKey<T>::of(p[e], largest);
+            if ((key & pmask) == prefix) atomicAdd(&sh.hist[(uint32_t)((key >> shift) & dmask)], 1u);
         }
         __syncthreads();
         uint32_t h[BPT];
@@ -1290,12 +1338,12 @@ __device__ void radix_select(RadixShared& sh, unsigned long long* cand, const fl
             sh.kk = kk - cum;
         }
         __syncthreads();
-        prefix |= (uint32_t)sh.digit << shift;
+        prefix |= (K)sh.digit << shift;
         pmask |= dmask << shift;
         kk = sh.kk;
         __syncthreads();
     }
-    const uint32_t T = prefix;  // the k-th key; take kk of the keys equal to it
+    const K Tk = prefix;  // the k-th key; take kk of the keys equal to it
     if (tid == 0) {
         sh.count = 0;
         sh.eq_taken = 0;
@@ -1303,9 +1351,9 @@ __device__ void radix_select(RadixShared& sh, unsigned long long* cand, const fl
     __syncthreads();
     for (int base = 0; base < n; base += NT) {
         const int e = base + tid;
-        const uint32_t key = (e < n) ? f2key(p[e], largest) : 0u;
-        if (e < n && key > T) cand[atomicAdd(&sh.count, 1)] = comp_key(key, (uint32_t)e);
-        const bool eq = (e < n) && key == T;
+        const K key = (e < n) ? SortKey<T>::of(p[e], largest) : (K)0;
+        if (e < n && key > Tk) cand[atomicAdd(&sh.count, 1)] = CP::make(key, (uint32_t)e);
+        const bool eq = (e < n) && key == Tk;
         const unsigned long long bal = __ballot(eq);
         if (lane == 0) sh.wtot[w] = __popcll(bal);
         __syncthreads();
@@ -1315,15 +1363,15 @@ __device__ void radix_select(RadixShared& sh, unsigned long long* cand, const fl
             if (i < w) before += sh.wtot[i];
             total += sh.wtot[i];
         }
-        if (eq && before < kk) cand[atomicAdd(&sh.count, 1)] = comp_key(key, (uint32_t)e);
+        if (eq && before < kk) cand[atomicAdd(&sh.count, 1)] = CP::make(key, (uint32_t)e);
         __syncthreads();
         if (tid == 0) sh.eq_taken += total;
         __syncthreads();
         if (sh.eq_taken >= kk && base + NT < n) {
             // every equal key needed is taken: the rest only adds keys > T
             for (int e2 = base + NT + tid; e2 < n; e2 += NT) {
-                const uint32_t k2 = f2key(p[e2], largest);
-                if (k2 > T) cand[atomicAdd(&sh.count, 1)] = comp_key(k2, (uint32_t)e2);
+                const K k2 = SortKey<T>::of(p[e2], largest);
+                if (k2 > Tk) cand[atomicAdd(&sh.count, 1)] = CP::make(k2, (uint32_t)e2);
             }
             break;
         }
@@ -1331,25 +1379,30 @@ __device__ void radix_select(RadixShared& sh, unsigned long long* cand, const fl
     __syncthreads();
 }
 
-__global__ __launch_bounds__(kRadixT) void k_topk_radix(TopkArgs a, unsigned long long* gcand) {
-    __shared__ RadixShared sh;
+// Values are the selected elements themselves (re-read at their index).
+template <class T>
+__global__ __launch_bounds__(kRadixT) void k_topk_radix(TopkArgs a, void* gcand) {
+    using C = typename Comp<typename SortKey<T>::K>::C;
+    __shared__ RadixShared<T> sh;
     const long long row = blockIdx.x;
-    const float* p = a.in + row * a.row_stride;
+    const T* p = reinterpret_cast<const T*>(a.in) + row * a.row_stride;
     const int k = a.k;
     const int n2 = pow2_at_least(k);
-    unsigned long long* cand = (n2 <= kRadixLds) ? sh.cand : gcand + row * (long long)n2;
-    radix_select<kRadixT>(sh, cand, p, a.cols, k, a.largest);
-    for (int i = k + threadIdx.x; i < n2; i += kRadixT) cand[i] = 0ull;
+    C* cand = (n2 <= radix_lds_count<T>()) ? sh.cand : static_cast<C*>(gcand) + row * (long long)n2;
+    radix_select<kRadixT, T>(sh, cand, p, a.cols, k, a.largest);
+    for (int i = k + threadIdx.x; i < n2; i += kRadixT) cand[i] = (C)0;
     __syncthreads();
-    bitonic_desc<kRadixT>(cand, n2);
-    if (a.sample) {
-        if (threadIdx.x < 64) sample_from_sel(a, row, p, cand, k);
-        return;
+    bitonic_desc<kRadixT, C>(cand, n2);
+    if constexpr (std::is_same<T, float>::value) {
+        if (a.sample) {
+            if (threadIdx.x < 64) sample_from_sel(a, row, p, cand, k);
+            return;
+        }
     }
+    T* ov = reinterpret_cast<T*>(a.out_v);
     for (int i = threadIdx.x; i < k; i += kRadixT) {
-        const unsigned long long c = cand[i];
-        const uint32_t idx = comp_index(c);
-        a.out_v[row * k + i] = selected_value(p, (uint32_t)(c >> 32), idx, a.largest);
+        const uint32_t idx = Comp<typename SortKey<T>::K>::index(cand[i]);
+        ov[row * k + i] = p[idx];
         a.out_i[row * k + i] = (long long)idx;
     }
 }
@@ -1431,19 +1484,33 @@ TopkPlan plan_topk(long long rows, long long cols, long long k) {
     return pl;
 }
 
-// Large k takes the radix-select kernel (any k <= cols); so does k > 128, and
-// k > 64 on rows shorter than the wave kernel's minimum segment.
-bool radix_route(long long cols, long long k) {
-    if (k > kKMax) return true;
+int dtype_size(int32_t dtype) {
+    switch (dtype) {
+        case TPR_UINT8: case TPR_INT8: case TPR_BOOL: return 1;
+        case TPR_INT16: case TPR_UINT16: return 2;
+        case TPR_INT32: case TPR_UINT32: case TPR_FLOAT32: return 4;
+        case TPR_INT64: case TPR_UINT64: case TPR_FLOAT64: return 8;
+        default: return 0;
+    }
+}
+
+// Large k takes the radix-select kernel (any k <= cols, any dtype); so does
+// k > 128, k > 64 on rows shorter than the wave kernel's minimum segment, and
+// every input dtype but float32.
+bool radix_route(long long cols, long long k, int32_t dtype = TPR_FLOAT32) {
+    if (k > kKMax || dtype != TPR_FLOAT32) return true;
     if (knobs().topk_radix < 0 || knobs().topk_fallback) return false;
     if (knobs().topk_radix > 0) return true;
     return k > kWaveK || (k > kShortMaxK && cols < kWaveMinSeg);
 }
 
-// Workspace of the radix kernel: composites sorted outside LDS.
-size_t radix_ws(long long rows, long long k) {
+// Workspace of the radix kernel: composites sorted outside LDS (8 bytes each
+// for elements of at most 4 bytes, 16 for 8-byte elements).
+size_t radix_ws(long long rows, long long k, int32_t dtype = TPR_FLOAT32) {
     const long long n2 = pow2_at_least((int)k);
-    return n2 > kRadixLds ? (size_t)rows * (size_t)n2 * sizeof(unsigned long long) : 0;
+    const bool wide = dtype_size(dtype) == 8;
+    const long long lds = wide ? 2048 : kRadixLds;
+    return n2 > lds ? (size_t)rows * (size_t)n2 * (wide ? 16 : 8) : 0;
 }
 
 }  // namespace
@@ -1452,9 +1519,8 @@ size_t radix_ws(long long rows, long long k) {
 extern "C" {
 
 size_t tpr_topk_workspace_bytes(int32_t dtype, int64_t rows, int64_t cols, int64_t k) {
-    (void)dtype;
-    if (rows <= 0 || cols <= 0 || k <= 0 || k > cols || cols > 0x7fffffffLL) return 0;
-    if (tpr::radix_route(cols, k)) return tpr::radix_ws(rows, k);
+    if (rows <= 0 || cols <= 0 || k <= 0 || k > cols || cols > 0x7fffffffLL || tpr::dtype_size(dtype) == 0) return 0;
+    if (tpr::radix_route(cols, k, dtype)) return tpr::radix_ws(rows, k, dtype);
     return tpr::plan_topk(rows, cols, k).ws;
 }
 
@@ -1495,15 +1561,16 @@ int launch_short(const TopkArgs& a, bool vec, hipStream_t st) {
 int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t row_stride, int64_t k,
                 int32_t largest, void* out_values, void* out_indices, void* workspace, size_t workspace_bytes,
                 void* stream, const TopkArgs* smp) {
-    if (dtype != TPR_FLOAT32) return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_topk: only float32 is implemented");
+    if (dtype_size(dtype) == 0) return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_topk: unknown dtype");
+    if (smp && dtype != TPR_FLOAT32) return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_sample: float32 logits only");
     if (rows < 0 || cols < 0) return fail(TPR_ERR_INVALID_ARG, "tpr_topk: negative shape");
     if (k < 0 || k > cols) return fail(TPR_ERR_INVALID_ARG, "tpr_topk: selected index k out of range");
     if (rows == 0 || k == 0) return TPR_OK;
     if (cols > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: rows longer than 2^31-1");
     if (!in || (!smp && (!out_values || !out_indices))) return fail(TPR_ERR_INVALID_ARG, "tpr_topk: null pointer");
     if (rows > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: more than 2^31-1 rows");
-    const bool radix = radix_route(cols, k);
-    const TopkPlan pl = radix ? TopkPlan{1, (int)cols, false, 8, radix_ws(rows, k)} : plan_topk(rows, cols, k);
+    const bool radix = radix_route(cols, k, dtype);
+    const TopkPlan pl = radix ? TopkPlan{1, (int)cols, false, 8, radix_ws(rows, k, dtype)} : plan_topk(rows, cols, k);
     if (rows * (long long)pl.nseg > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: grid too large");
     if (pl.ws > 0 && (workspace == nullptr || workspace_bytes < pl.ws))
         return fail(TPR_ERR_WORKSPACE, "tpr_topk: workspace too small (need " + std::to_string(pl.ws) + " bytes)");
@@ -1528,8 +1595,19 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     const bool vec = ((reinterpret_cast<uintptr_t>(in) & 15u) == 0) && (rows == 1 || row_stride % 4 == 0);
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (radix) {
-        hipLaunchKernelGGL(k_topk_radix, dim3(rows), dim3(kRadixT), 0, st, a,
-                           static_cast<unsigned long long*>(workspace));
+        const dim3 g((unsigned)rows), b(kRadixT);
+        switch (dtype) {
+            case TPR_FLOAT32: hipLaunchKernelGGL(k_topk_radix<float>, g, b, 0, st, a, workspace); break;
+            case TPR_FLOAT64: hipLaunchKernelGGL(k_topk_radix<double>, g, b, 0, st, a, workspace); break;
+            case TPR_INT8: hipLaunchKernelGGL(k_topk_radix<signed char>, g, b, 0, st, a, workspace); break;
+            case TPR_INT16: hipLaunchKernelGGL(k_topk_radix<short>, g, b, 0, st, a, workspace); break;
+            case TPR_INT32: hipLaunchKernelGGL(k_topk_radix<int>, g, b, 0, st, a, workspace); break;
+            case TPR_INT64: hipLaunchKernelGGL(k_topk_radix<long long>, g, b, 0, st, a, workspace); break;
+            case TPR_UINT16: hipLaunchKernelGGL(k_topk_radix<unsigned short>, g, b, 0, st, a, workspace); break;
+            case TPR_UINT32: hipLaunchKernelGGL(k_topk_radix<unsigned int>, g, b, 0, st, a, workspace); break;
+            case TPR_UINT64: hipLaunchKernelGGL(k_topk_radix<unsigned long long>, g, b, 0, st, a, workspace); break;
+            default: hipLaunchKernelGGL(k_topk_radix<unsigned char>, g, b, 0, st, a, workspace); break;  // UINT8, BOOL
+        }
         return check_launch("k_topk_radix");
     }
     if (!smp && k <= kShortMaxK && cols <= kShortMaxCols && knobs().topk_short >= 0 && knobs().topk_fallback == 0 &&

@@ -77,8 +77,13 @@ def test_argument_validation_without_gpu():
     assert L.tpr_reduce(ctypes.byref(d), None, None, None, 0, None) == _capi.ERR_INVALID_ARG
     rc = L.tpr_topk(None, _capi.FLOAT32, 2, 5, 5, 6, 1, 1, None, None, None, 0, None)
     assert rc == _capi.ERR_INVALID_ARG and b"k out of range" in L.tpr_last_error()
+    rc = L.tpr_topk(None, 77, 2, 5, 5, 1, 1, 1, None, None, None, 0, None)
+    assert rc == _capi.ERR_UNSUPPORTED_DTYPE  # every tpr_dtype is served; unknown codes are not
     rc = L.tpr_topk(None, _capi.FLOAT64, 2, 5, 5, 1, 1, 1, None, None, None, 0, None)
-    assert rc == _capi.ERR_UNSUPPORTED_DTYPE
+    assert rc == _capi.ERR_INVALID_ARG  # float64 is served: the null input is the error
+    assert L.tpr_topk_workspace_bytes(_capi.INT64, 4, 10000, 2000) == 0          # 2048 composites in LDS
+    assert L.tpr_topk_workspace_bytes(_capi.INT64, 4, 10000, 3000) == 4 * 4096 * 16  # sorted in the workspace
+    assert L.tpr_topk_workspace_bytes(_capi.INT32, 4, 10000, 3000) == 0          # 4096 composites in LDS
     with pytest.raises(_capi.TprError):
         _capi.debug_set("no_such_knob", 1)
     d = _capi.make_desc("sum", [4], [1], [0], _capi.FLOAT32)

@@ -235,3 +235,38 @@ def test_large_k_configs():
     c3 = rng.uniform(-1, 1, (1024, 32768)).astype(np.float32)
     check(c3, c3, 2048)
     check(c3[:256], c3[:256], 4096)
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.int8, np.int16, np.int32, np.int64, np.uint8, np.uint16,
+                                np.uint32, np.uint64, np.bool_])
+def test_other_dtypes(dt):
+    """tpr_topk on every dtype (the radix-select kernel with the dtype's sortable
+    key): values (bit-exact, in the input dtype) and indices against
+    oracle.topk_any, with ties, extremes, NaN / +-0 for float64, k up to cols."""
+    rng = np.random.default_rng(42)
+    rows, cols = 9, 3001
+    if dt == np.bool_:
+        x = rng.random((rows, cols)) < 0.3
+    elif dt == np.float64:
+        x = rng.standard_normal((rows, cols))
+        x[0, ::7] = np.nan
+        x[1] = np.where(rng.random(cols) < 0.5, -0.0, 0.0)
+        x[2, :50] = np.inf
+        x[3] = np.round(x[3] * 3)
+    else:
+        info = np.iinfo(dt)
+        x = rng.integers(info.min, info.max, size=(rows, cols), dtype=dt, endpoint=True)
+        x[0, 100:300] = info.max
+        x[1, 100:300] = info.min
+        x[2] = x[2] % 5
+    t = torch.from_numpy(x).cuda()
+    for k in (1, 10, 64, 1000, cols):
+        for largest in (True, False):
+            print(f"case topk dtype={np.dtype(dt).name} k={k} largest={largest}", flush=True)
+            gv, gi = _capi.topk(t, k, largest)
+            torch.cuda.synchronize()
+            ev, ei = O.topk_any(x, k, largest)
+            np.testing.assert_array_equal(gi.cpu().numpy(), ei)
+            g = gv.cpu().numpy()
+            assert g.dtype == ev.dtype
+            np.testing.assert_array_equal(g.view(np.uint8), ev.view(np.uint8))
