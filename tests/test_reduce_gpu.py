@@ -159,6 +159,20 @@ def test_forced_plans(knob, values):
                 check(c, torch.from_numpy(c).cuda(), op, [0])
 
 
+def test_rows_eight_vectors_in_flight():
+    """k_rows with 32 lanes and 8 vectors per lane in flight (the planner's pick
+    for rows of 1024 floats), forced on other lengths too: tails, partial tiles."""
+    rng = np.random.default_rng(22)
+    _capi.debug_set("lanes", 32)
+    _capi.debug_set("unroll", 8)
+    for rows, cols in ((33, 1024), (7, 1028), (5, 2048), (9, 1000), (3, 4100)):
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        x[0, [3, cols - 1]] = 9.0  # tie: the lowest index wins
+        t = torch.from_numpy(x).cuda()
+        for op in OPS:
+            check(x, t, op, [1])
+
+
 @pytest.mark.parametrize("rowreg", [1, -1])
 def test_register_rows(rowreg):
     """k_rows_reg (zero-identity ops over rows of 65-1024 float4, loads past the
