@@ -475,6 +475,71 @@ __global__ __launch_bounds__(BLK) void k_rows_reg(RowArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// var / std over rows that fill WPR waves exactly (R == 4 * 64 * WPR * NV):
+// every element is shifted by the row's first element K (one scalar load per
+// wave), so the shifted sums S1 = sum(x - K), S2 = sum((x - K)^2) of all lanes
+// add up directly -- no per-lane Welford state, no Chan merges, one divide per
+// row: mean = K + S1/n, M2 = S2 - S1^2/n (fp64; K is an element of the row, the
+// same kind of shift the per-thread Welford accumulator uses).  Four chains per
+// lane (one per float4 component), all loads issued before the first add.
+// ---------------------------------------------------------------------------
+template <int NV, int WPR, int BLK>
+__global__ __launch_bounds__(BLK) void k_rows_reg_var(RowArgs a) {
+    constexpr int RPB = BLK / (kWave * WPR);
+    static_assert(RPB >= 1 && RPB * kWave * WPR == BLK, "BLK must hold whole rows");
+    const int w = threadIdx.x / kWave;
+    const int l = __lane_id();
+    const int sub = w % WPR;
+    const long long row = (long long)blockIdx.x * RPB + w / WPR;
+    const bool live = row < a.rows;
+    const float* p = a.in + (live ? row * a.row_stride : 0);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), (short)0, live ? (int)(a.R * 4) : 0, kBufWord3);
+    f32x4 t[NV];
+#pragma unroll
+    for (int u = 0; u < NV; ++u)
+        t[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, ((sub * NV + u) * kWave + l) * 16, 0, kAuxNT));
+    const double Kd = live ? (double)__uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(p[0]))) : 0.0;
+    double s1[4] = {0.0, 0.0, 0.0, 0.0}, s2[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+        const double d0 = (double)t[u].x - Kd, d1 = (double)t[u].y - Kd;
+        const double d2 = (double)t[u].z - Kd, d3 = (double)t[u].w - Kd;
+        s1[0] += d0; s2[0] = fma(d0, d0, s2[0]);
+        s1[1] += d1; s2[1] = fma(d1, d1, s2[1]);
+        s1[2] += d2; s2[2] = fma(d2, d2, s2[2]);
+        s1[3] += d3; s2[3] = fma(d3, d3, s2[3]);
+    }
+    double S1 = (s1[0] + s1[1]) + (s1[2] + s1[3]);
+    double S2 = (s2[0] + s2[1]) + (s2[2] + s2[3]);
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) {
+        S1 += __shfl_xor(S1, m, kWave);
+        S2 += __shfl_xor(S2, m, kWave);
+    }
+    if constexpr (WPR > 1) {
+        __shared__ double sh1[BLK / kWave], sh2[BLK / kWave];
+        if (l == 0) {
+            sh1[w] = S1;
+            sh2[w] = S2;
+        }
+        __syncthreads();
+        if (sub == 0 && l == 0) {
+#pragma unroll
+            for (int i = 1; i < WPR; ++i) {
+                S1 += sh1[w + i];
+                S2 += sh2[w + i];
+            }
+        }
+    }
+    if (sub == 0 && l == 0 && live) {
+        const double n = (double)a.R;
+        const double m = S1 / n;
+        fin_write(WelS{n, Kd + m, fmax(0.0, S2 - S1 * m)}, a.fin, a.out, row);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Column kernel: [outer, R, inner], inner contiguous.  TX threads across the
 // inner dim (VEC elements each), TY = 256/TX threads across R.
 // blockIdx.x = (o * ncb + cb) * S + split.
@@ -683,6 +748,7 @@ struct Plan {
     int nt = 0;      // rows/cols: nontemporal input loads
     int colblock = 256;  // cols: threads per workgroup
     int reg_wpr = 0;     // rows: > 0 selects k_rows_reg with this many waves per row
+    int var_nv = 0;      // rows, VAR/STD: > 0 selects k_rows_reg_var (float4 per lane; reg_wpr waves per row)
     long long S = 1;
     // A reduced run of 2^31 or more elements is cut into chunks of `chunk`
     // elements, one launch each (32-bit indices inside a launch); every launch
@@ -956,6 +1022,20 @@ Plan make_plan(const tpr_reduce_desc* d, const void* in) {
                 p.S = 1;
             }
         }
+        // var / std over rows of 1024, 2048 or 4096 floats (1, 2 or 4 waves of
+        // four float4 per lane, exactly): the shifted two-sum kernel.  Measured
+        // on MI355X: C2 var dim=-1 [65536, 1024] 39.9 us against 42.6 us,
+        // [4096, 4096] 12.0 against 16.7 us, [16384, 2048] 21.6 against 23.3 us;
+        // two float4 per lane (rows of 512) was slower than k_rows (48 us).
+        if ((d->op == TPR_VAR || d->op == TPR_STD) && p.vec == 4 && p.R % 4 == 0 && nv4 % (4 * kWave) == 0 &&
+            knobs().rowreg >= 0 && knobs().splits <= 0 && knobs().lanes <= 0) {
+            const long long wv = nv4 / (4 * kWave);
+            if ((wv == 1 || wv == 2 || wv == 4) && (knobs().rowreg > 0 || p.rows * wv >= (long long)dev.cus * 8)) {
+                p.reg_wpr = (int)wv;
+                p.var_nv = 4;
+                p.S = 1;
+            }
+        }
     } else if (!K.empty() && K.back().stride == 1 && Rd.size() == 1 &&
                (K.size() == 1 ? true : (K.size() == 2)) &&
                (K.size() == 1 ? (dims.front().red) : (dims.size() == 3 && dims[1].red))) {
@@ -1025,8 +1105,25 @@ int launch_rows_reg(const Plan& p, const float* in, void* out, Fin fin, hipStrea
     return check_launch("k_rows_reg");
 }
 
+int launch_rows_reg_var(const Plan& p, const float* in, void* out, Fin fin, hipStream_t st) {
+    RowArgs a{in, p.rows, p.R, p.row_stride, 1, p.nt, out, nullptr, fin};
+    const int nv = p.var_nv;
+    const int wpr = p.reg_wpr;
+#define TPR_VAR_CASE(NV, WPR, BLK)                                                                             \
+    if (nv == NV && wpr == WPR) {                                                                              \
+        hipLaunchKernelGGL((k_rows_reg_var<NV, WPR, BLK>), dim3(ceil_div(p.rows, BLK / (kWave * WPR))), dim3(BLK), 0, st, a); \
+        return check_launch("k_rows_reg_var");                                                                 \
+    }
+    TPR_VAR_CASE(4, 1, 256) TPR_VAR_CASE(4, 2, 256) TPR_VAR_CASE(4, 4, 256)
+#undef TPR_VAR_CASE
+    return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: no register-row var kernel for this row length");
+}
+
 template <class Op>
 int launch_rows(const Plan& p, const float* in, void* out, void* ws, Fin fin, hipStream_t st) {
+    if constexpr (std::is_same<Op, WelfordOp>::value) {
+        if (p.var_nv > 0) return launch_rows_reg_var(p, in, out, fin, st);
+    }
     if constexpr (kZeroIdentity<Op>) {
         if (p.reg_wpr > 0) return launch_rows_reg<Op>(p, in, out, fin, st);
     } else {
@@ -1680,7 +1777,8 @@ void adapt_plan_int(Plan& p, const tpr_reduce_desc* d, const void* in, int es) {
     const auto& dev = device_info();
     const long long target = (long long)dev.cus * 512;
     p.state_bytes = d->in_dtype == TPR_FLOAT64 ? f64_state_size(d->op, d->p) : int_state_size(d->op);
-    p.reg_wpr = 0;  // the register-row kernel reads float32 only
+    p.reg_wpr = 0;  // the register-row kernels read float32 only
+    p.var_nv = 0;
     if (p.kind == P_ROWS) {
         p.vec = (aligned16 && (p.rows == 1 || p.row_stride % NV == 0) && p.R >= NV) ? NV : 1;
         int L = 16;

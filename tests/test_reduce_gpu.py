@@ -159,6 +159,31 @@ def test_forced_plans(knob, values):
                 check(c, torch.from_numpy(c).cuda(), op, [0])
 
 
+@pytest.mark.parametrize("rowreg", [0, 1, -1])
+def test_var_rows_shifted_two_sums(rowreg):
+    """var / std over rows of 1024 / 2048 / 4096 floats take k_rows_reg_var
+    (every element shifted by the row's first element, fp64 two-sums); rowreg=1
+    forces it for few rows, -1 takes k_rows.  Offsets far from zero, an outlier
+    first element, tiny spread, NaN / inf rows, corrections 0-2."""
+    rng = np.random.default_rng(23)
+    _capi.debug_set("rowreg", rowreg)
+    for rows, cols in ((3, 1024), (5, 2048), (2, 4096), (4096, 1024)):
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        x[0] += np.float32(1e4)                       # large mean, unit spread
+        x[1] = np.float32(3.0) + x[1] * np.float32(1e-3)
+        if rows > 2:
+            x[2, 0] = np.float32(1e6)                 # the shift itself is an outlier
+        t = torch.from_numpy(x).cuda()
+        for op in ("var", "std"):
+            for corr in (0, 1, 2):
+                check(x, t, op, [1], correction=corr)
+        y = x[:2].copy()
+        y[0, 5] = np.nan
+        y[1, 7] = np.inf
+        g = gpu(torch.from_numpy(y).cuda(), "var", [1])
+        assert np.isnan(g).all()
+
+
 def test_rows_eight_vectors_in_flight():
     """k_rows with 32 lanes and 8 vectors per lane in flight (the planner's pick
     for rows of 1024 floats), forced on other lengths too: tails, partial tiles."""
