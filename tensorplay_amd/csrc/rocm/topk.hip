@@ -68,11 +68,10 @@ constexpr long long kWaveMaxSeg = 1LL << 28;  // longest wave-kernel segment (32
 // u -> ~u + 1 (two's-complement negate of the magnitude's image), so -0.0 and
 // +0.0 land on the same key 2^31; every NaN is first made 0x7fc00000 (above
 // +inf).  lmask = 0 keeps the order (largest), ~0 reverses it (smallest).
-// Valid keys are never 0: 0 marks "no element".  Branch-free: one NaN select,
-// an arithmetic shift, xor, subtract, xor.
+// Valid keys are never 0: 0 marks "no element".  Branch-free: one NaN compare
+// (f != f) and select, an arithmetic shift, xor, subtract, xor.
 __device__ __forceinline__ uint32_t f2key_sel(float f, uint32_t lmask) {
-    const uint32_t b = __float_as_uint(f);
-    const uint32_t u = ((b & 0x7fffffffu) > 0x7f800000u) ? 0x7fc00000u : b;
+    const uint32_t u = (f != f) ? 0x7fc00000u : __float_as_uint(f);
     const uint32_t m = (uint32_t)((int32_t)u >> 31);
     return ((u ^ (m | 0x80000000u)) - m) ^ lmask;
 }
@@ -1020,14 +1019,13 @@ __device__ __forceinline__ uint32_t group_hist_threshold(const uint32_t* hist, i
     return __shfl(tn, grp * L + hl, 64);
 }
 
-template <int L, int E4, bool VEC>
+template <int L, int E4, bool VEC, bool LG>
 __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
     constexpr int G = 64 / L;
     constexpr int E = 4 * E4;
     constexpr int C = 8 * L;  // candidate capacity of one row
     constexpr int RPB = (kShortT / 64) * G;
-    __shared__ unsigned long long cl[RPB][C];
-    __shared__ uint32_t hl[RPB][256];
+    __shared__ unsigned long long cl[RPB][C];  // C * 8 >= 1 KiB: also the row's histogram (see below)
     const int lane = __lane_id();
     const int grp = lane / L;
     const int sl = lane % L;
@@ -1036,7 +1034,7 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
     const bool live = row < a.rows;
     const int cols = a.cols;
     const int k = a.k;
-    const int largest = a.largest;
+    constexpr int largest = LG ? 1 : 0;
     const float* p = a.in + (live ? row * a.row_stride : 0);
     const __amdgpu_buffer_rsrc_t rs = segment_rsrc(p, live ? cols : 0);
 
@@ -1053,7 +1051,7 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
         }
     }
     uint32_t key[E];
-    const uint32_t lm = largest ? 0u : 0xffffffffu;
+    constexpr uint32_t lm = LG ? 0u : 0xffffffffu;
     if (cols == 4 * E4 * L) {  // every element of every lane is in the row
 #pragma unroll
         for (int j = 0; j < E4; ++j) {
@@ -1102,13 +1100,18 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
             // when ranking all c candidates (c * c / L compares per lane) costs
             // more than the histogram (measured on MI355X: [16384, 1024] k = 32
             // 70 -> 38 us; [65536, 256] k = 8, about 30 candidates, is faster
-            // without it: 19.8 us against 24.8 us).
+            // without it).
+            // The candidates move to registers and the row's list area holds the
+            // 256-bin histogram meanwhile (C composites = 8L * 8 bytes >= 1 KiB),
+            // which keeps the workgroup's LDS at the lists alone (occupancy).
             constexpr int PER = C / L;
-            uint32_t* hist = hl[slot];
+            static_assert(C * sizeof(unsigned long long) >= 256 * sizeof(uint32_t), "histogram fits the list");
+            uint32_t* hist = reinterpret_cast<uint32_t*>(list);
             wave_sync_lds();
             unsigned long long mine[PER];
 #pragma unroll
             for (int r = 0; r < PER; ++r) mine[r] = (sl + r * L < c) ? list[sl + r * L] : 0ull;
+            wave_sync_lds();  // every lane has its candidates before the area is cleared
 #pragma unroll
             for (int b = 0; b < 256 / L; ++b) hist[sl * (256 / L) + b] = 0u;
             const int shift = hist_shift(gmax, T);
@@ -1118,6 +1121,7 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
                 if (mine[r]) atomicAdd(&hist[((uint32_t)(mine[r] >> 32) - T) >> shift], 1u);
             wave_sync_lds();
             const uint32_t T1 = group_hist_threshold<L>(hist, k, T, shift, sl, grp);
+            wave_sync_lds();  // every lane has read its bins before the survivors overwrite them
             int nk = 0;
 #pragma unroll
             for (int r = 0; r < PER; ++r) nk += (mine[r] && (uint32_t)(mine[r] >> 32) >= T1) ? 1 : 0;
@@ -1533,8 +1537,13 @@ template <int L, int E4>
 void launch_short_le(const TopkArgs& a, bool vec, hipStream_t st) {
     constexpr int RPB = (kShortT / 64) * (64 / L);
     const dim3 grid((unsigned)((a.rows + RPB - 1) / RPB));
-    if (vec) hipLaunchKernelGGL((k_topk_short<L, E4, true>), grid, dim3(kShortT), 0, st, a);
-    else hipLaunchKernelGGL((k_topk_short<L, E4, false>), grid, dim3(kShortT), 0, st, a);
+    if (a.largest) {
+        if (vec) hipLaunchKernelGGL((k_topk_short<L, E4, true, true>), grid, dim3(kShortT), 0, st, a);
+        else hipLaunchKernelGGL((k_topk_short<L, E4, false, true>), grid, dim3(kShortT), 0, st, a);
+    } else {
+        if (vec) hipLaunchKernelGGL((k_topk_short<L, E4, true, false>), grid, dim3(kShortT), 0, st, a);
+        else hipLaunchKernelGGL((k_topk_short<L, E4, false, false>), grid, dim3(kShortT), 0, st, a);
+    }
 }
 
 template <int L>
@@ -1548,8 +1557,11 @@ void launch_short_l(const TopkArgs& a, bool vec, hipStream_t st) {
 }
 
 int launch_short(const TopkArgs& a, bool vec, hipStream_t st) {
+    // L >= 2k where possible: the bound is then the k-th largest of at least
+    // 2k lane maxima, well above their minimum, so fewer candidates reach the
+    // ranking ([16384, 1024] k = 32: 64 lanes of 16 elements instead of 32 of 32)
     int L = 16;
-    while (L < a.k || L * 64 < a.cols) L *= 2;
+    while (L < 64 && (L < 2 * a.k || L * 64 < a.cols)) L *= 2;
     if (L == 16) launch_short_l<16>(a, vec, st);
     else if (L == 32) launch_short_l<32>(a, vec, st);
     else launch_short_l<64>(a, vec, st);
