@@ -1559,9 +1559,12 @@ void launch_short_l(const TopkArgs& a, bool vec, hipStream_t st) {
 int launch_short(const TopkArgs& a, bool vec, hipStream_t st) {
     // L >= 2k where possible: the bound is then the k-th largest of at least
     // 2k lane maxima, well above their minimum, so fewer candidates reach the
-    // ranking ([16384, 1024] k = 32: 64 lanes of 16 elements instead of 32 of 32)
+    // ranking; and L >= cols / 16 where possible: at most 16 elements per lane
+    // keep the registers (and the occupancy) low.  Measured on MI355X (us):
+    // [16384, 1024] k = 32: L = 32 41.7, L = 64 18.8; k = 8: L = 16 24.7,
+    // L = 64 15.3; [65536, 256] k = 8: L = 16 19.1, L = 32 21.9.
     int L = 16;
-    while (L < 64 && (L < 2 * a.k || L * 64 < a.cols)) L *= 2;
+    while (L < 64 && (L < 2 * a.k || L * 16 < a.cols)) L *= 2;
     if (L == 16) launch_short_l<16>(a, vec, st);
     else if (L == 32) launch_short_l<32>(a, vec, st);
     else launch_short_l<64>(a, vec, st);
@@ -1622,8 +1625,12 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
         }
         return check_launch("k_topk_radix");
     }
-    if (!smp && k <= kShortMaxK && cols <= kShortMaxCols && knobs().topk_short >= 0 && knobs().topk_fallback == 0 &&
-        knobs().splits <= 0)
+    // Rows of more than 2048 elements with k > 32 leave the lane-group kernel
+    // too many candidates per lane: the wave kernel is faster there (MI355X,
+    // [4096, 4096] k = 64: 48.5 us against 53.5 us).
+    const bool short_fit = k <= kShortMaxK && cols <= kShortMaxCols && (cols <= 2048 || k <= 32);
+    if (!smp && (short_fit || (knobs().topk_short > 0 && k <= kShortMaxK && cols <= kShortMaxCols)) &&
+        knobs().topk_short >= 0 && knobs().topk_fallback == 0 && knobs().splits <= 0)
         return launch_short(a, vec, st);
     const long long grid = rows * pl.nseg;
     if (pl.wave) {
