@@ -29,7 +29,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
 # kernel each headline op launches (single-kernel plans at this shape)
 DOMINANT_KERNEL = {"mean_dim1": "k_cols<SumOp,4,64,4,512>",
                    "amax_dim0": "k_cols<ArgOp<true>,4,256,2,256>", "argmax_dim0": "k_cols<ArgOp<true>,4,256,2,256>",
-                   "var_dim-1": "k_rows_reg_var<4,2,256>", "std_dim-1": "k_rows_reg_var<4,2,256>"}
+                   "var_dim-1": "k_rows_reg_var<4,1,256>", "std_dim-1": "k_rows_reg_var<4,1,256>"}
 METRIC = "achieved HBM GB/s (% of MI355X peak) for sum/argmax/topk; rows/s topk"
 
 
