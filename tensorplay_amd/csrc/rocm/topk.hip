@@ -1250,7 +1250,7 @@ __device__ void bitonic_desc(C* c, int n) {
     for (int size = 2; size <= n; size <<= 1) {
         for (int stride = size / 2; stride > 0; stride >>= 1) {
             for (int t = threadIdx.x; t < n / 2; t += NT) {
-                const int i = 2 * stride * (t / stride) + (t % stride);
+                const int i = ((t & ~(stride - 1)) << 1) | (t & (stride - 1));  // stride: a power of two
                 const int j = i + stride;
                 const C ci = c[i], cj = c[j];
                 const bool desc = (i & size) == 0;  // this block's final direction
@@ -1411,6 +1411,303 @@ __global__ __launch_bounds__(kRadixT) void k_topk_radix(TopkArgs a, void* gcand)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Large k on rows of at most 32768 elements of <= 4 bytes (k_topk_rsel): one
+// workgroup of NT threads per row keeps the row's EPT keys per thread in
+// registers (element e = j*NT + t), read from HBM once.  The k-th key is
+// radix-selected over the registers with a 2048-bin LDS histogram, 11 bits per
+// pass, stopping as soon as the class of keys that share the found prefix
+// holds exactly the number still wanted (after two passes on most data).  The
+// k composites, padded with zeros to n = pow2(max(k, 64)), are then
+// bitonic-sorted by n / P threads holding P each (reg_sort_desc): exchanges at
+// a distance below P stay in registers, below 64*P in the wave (lane
+// permutes), only the rest go through LDS with a barrier.
+// ---------------------------------------------------------------------------
+constexpr int kRselMaxCols = 32768;
+
+__host__ __device__ constexpr int dtype_bytes(int32_t dtype) {
+    return (dtype == TPR_INT64 || dtype == TPR_UINT64 || dtype == TPR_FLOAT64) ? 8
+         : (dtype == TPR_INT32 || dtype == TPR_UINT32 || dtype == TPR_FLOAT32) ? 4
+         : (dtype == TPR_INT16 || dtype == TPR_UINT16) ? 2 : 1;
+}
+
+template <int NT>
+__device__ int block_prefix_excl(int v, int* wtot, int& total) {
+    constexpr int NW = NT / 64;
+    const int lane = __lane_id();
+    const int w = threadIdx.x / 64;
+    int inc = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += t;
+    }
+    if (lane == 63) wtot[w] = inc;
+    __syncthreads();
+    int before = 0;
+    total = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        const int c = wtot[i];
+        if (i < w) before += c;
+        total += c;
+    }
+    __syncthreads();
+    return before + inc - v;
+}
+
+// Lane lane ^ M's value: DPP quad permutes for M = 1, 2, ds_swizzle (xor
+// mask inside 32-lane halves) for M = 4 .. 16, ds_bpermute for M = 32.
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+    if constexpr (M == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // [1,0,3,2]
+    else if constexpr (M == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // [2,3,0,1]
+    else if constexpr (M < 32) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (M << 10) | 0x1F);
+    else return (uint32_t)__builtin_amdgcn_ds_bpermute((int)((__lane_id() ^ M) << 2), (int)v);
+}
+
+template <int M, int P>
+__device__ __forceinline__ void sort_lane_stage(unsigned long long (&x)[P], bool keep_max) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const uint32_t lo = xor_lane<M>((uint32_t)x[p]);
+        const uint32_t hi = xor_lane<M>((uint32_t)(x[p] >> 32));
+        const unsigned long long y = ((unsigned long long)hi << 32) | lo;
+        x[p] = ((x[p] > y) == keep_max) ? x[p] : y;
+    }
+}
+
+// Descending bitonic sort of n composites (n / P threads, a multiple of 64,
+// at most NT) held P per thread: thread t holds positions t*P .. t*P+P-1.
+// Distances below P: compare-exchanges in registers; below 64*P: the partner
+// lane's value by a lane permute; the rest through xb (LDS, NT*min(P, 4)
+// composites) with a barrier, which every thread of the workgroup reaches.
+template <int NT, int P>
+__device__ void reg_sort_desc(unsigned long long (&x)[P], unsigned long long* xb, int n) {
+    constexpr int Q = P < 4 ? P : 4;
+    const int t = threadIdx.x;
+    const bool active = t < n / P;  // whole waves
+    for (int s = 2; s <= n; s <<= 1) {
+        for (int d = s >> 1; d >= P; d >>= 1) {
+            const int m = d / P;  // partner thread t ^ m
+            const bool desc = ((t * P) & s) == 0;
+            const bool keep_max = ((t & m) == 0) == desc;
+            if (!active && m < 64) continue;
+            switch (m) {
+                case 1: sort_lane_stage<1, P>(x, keep_max); break;
+                case 2: sort_lane_stage<2, P>(x, keep_max); break;
+                case 4: sort_lane_stage<4, P>(x, keep_max); break;
+                case 8: sort_lane_stage<8, P>(x, keep_max); break;
+                case 16: sort_lane_stage<16, P>(x, keep_max); break;
+                case 32: sort_lane_stage<32, P>(x, keep_max); break;
+                default:
+#pragma unroll
+                    for (int p0 = 0; p0 < P; p0 += Q) {
+                        if (active) {
+#pragma unroll
+                            for (int q = 0; q < Q; ++q) xb[q * NT + t] = x[p0 + q];
+                        }
+                        __syncthreads();
+                        if (active) {
+#pragma unroll
+                            for (int q = 0; q < Q; ++q) {
+                                const unsigned long long y = xb[q * NT + (t ^ m)];
+                                x[p0 + q] = ((x[p0 + q] > y) == keep_max) ? x[p0 + q] : y;
+                            }
+                        }
+                        __syncthreads();
+                    }
+            }
+        }
+        if (!active) continue;
+#pragma unroll
+        for (int dd = P / 2; dd >= 1; dd >>= 1) {
+            if (dd < s) {
+#pragma unroll
+                for (int p = 0; p < P; ++p) {
+                    if ((p & dd) == 0) {
+                        const bool desc = ((t * P + p) & s) == 0;
+                        const unsigned long long u = x[p], v = x[p + dd];
+                        const bool sw = (u > v) != desc;
+                        x[p] = sw ? v : u;
+                        x[p + dd] = sw ? u : v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int NT, int P>
+struct RselShared {
+    static constexpr int kBuf = (NT * (P < 4 ? P : 4) > 1024) ? NT * (P < 4 ? P : 4) : 1024;
+    union {
+        uint32_t hist[kRadixBins];
+        unsigned long long buf[kBuf];  // exchanges, staging of the list, the sampler's sorted list
+    };
+    int wtot[NT / 64];
+    int digit, kk, cls;
+};
+
+template <class T, int NT, int EPT>
+__device__ __forceinline__ void rsel_load(uint32_t (&key)[EPT], const void* base, int cols, int largest) {
+    const T* p = static_cast<const T*>(base);
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int e = j * NT + (int)threadIdx.x;
+        key[j] = e < cols ? (uint32_t)SortKey<T>::of(p[e], largest) : 0u;
+    }
+}
+
+template <int NT, int EPT, int P>
+__global__ __launch_bounds__(NT) void k_topk_rsel(TopkArgs a, int dtype, int sort_n) {
+    using CP = Comp<uint32_t>;
+    constexpr int BPT = kRadixBins / NT;
+    __shared__ RselShared<NT, P> sh;
+    const int tid = threadIdx.x;
+    const long long row = blockIdx.x;
+    const int cols = a.cols, k = a.k;
+    const char* base = reinterpret_cast<const char*>(a.in) + row * a.row_stride * dtype_bytes(dtype);
+    uint32_t key[EPT];
+    switch (dtype) {
+        case TPR_FLOAT32: rsel_load<float, NT, EPT>(key, base, cols, a.largest); break;
+        case TPR_INT32: rsel_load<int, NT, EPT>(key, base, cols, a.largest); break;
+        case TPR_UINT32: rsel_load<unsigned int, NT, EPT>(key, base, cols, a.largest); break;
+        case TPR_INT16: rsel_load<short, NT, EPT>(key, base, cols, a.largest); break;
+        case TPR_UINT16: rsel_load<unsigned short, NT, EPT>(key, base, cols, a.largest); break;
+        case TPR_INT8: rsel_load<signed char, NT, EPT>(key, base, cols, a.largest); break;
+        default: rsel_load<unsigned char, NT, EPT>(key, base, cols, a.largest); break;  // UINT8, BOOL
+    }
+    // ---- radix select: prefix / pmask name the class of the k-th key ----
+    uint32_t prefix = 0, pmask = 0;
+    int kk = k;
+    bool whole = false;  // every key of the class is taken
+    for (int hi = 32; hi > 0 && !whole; hi -= 11) {
+        const int shift = hi > 11 ? hi - 11 : 0;
+        const uint32_t dmask = (1u << (hi - shift)) - 1u;
+#pragma unroll
+        for (int b = 0; b < BPT; ++b) sh.hist[tid * BPT + b] = 0u;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            if (j * NT + tid < cols && (key[j] & pmask) == prefix) atomicAdd(&sh.hist[(key[j] >> shift) & dmask], 1u);
+        __syncthreads();
+        uint32_t h[BPT];
+        int own = 0;
+#pragma unroll
+        for (int b = 0; b < BPT; ++b) {
+            h[b] = sh.hist[tid * BPT + b];
+            own += (int)h[b];
+        }
+        const int suf = block_suffix_incl<NT>(own, sh.wtot);
+        if (suf >= kk && suf - own < kk) {
+            int cum = suf - own;
+            int b = BPT - 1;
+            for (; b > 0; --b) {
+                if (cum + (int)h[b] >= kk) break;
+                cum += (int)h[b];
+            }
+            sh.digit = tid * BPT + b;
+            sh.kk = kk - cum;
+            sh.cls = (int)h[b];
+        }
+        __syncthreads();
+        prefix |= (uint32_t)sh.digit << shift;
+        pmask |= dmask << shift;
+        kk = sh.kk;
+        whole = sh.cls == kk;
+        __syncthreads();
+    }
+    // ---- the k selected: every key above the class, and the class whole or
+    // its kk lowest-index keys (exact ties) ----
+    uint32_t take = 0;  // bit j: key[j] is selected
+    int nt = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const bool v = j * NT + tid < cols;
+        const uint32_t hk = key[j] & pmask;
+        const bool s = v && (hk > prefix || (whole && hk == prefix));
+        take |= (uint32_t)s << j;
+        nt += s;
+    }
+    if (!whole) {
+        uint32_t eqm = 0;  // bit j: key[j] is in the class (equal to the k-th key)
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) eqm |= (uint32_t)(j * NT + tid < cols && key[j] == prefix) << j;
+        int run = 0;  // class members in element groups before j
+        const int w = tid / 64;
+#pragma unroll 1
+        for (int j = 0; j < EPT; ++j) {
+            const bool eq = (eqm >> j) & 1u;
+            const unsigned long long bal = __ballot(eq);
+            if (__lane_id() == 0) sh.wtot[w] = __popcll(bal);
+            __syncthreads();
+            int before = run + __popcll(bal & lanemask_lt());
+            for (int i = 0; i < NT / 64; ++i) {
+                if (i < w) before += sh.wtot[i];
+                run += sh.wtot[i];
+            }
+            __syncthreads();
+            if (eq && before < kk) {
+                take |= 1u << j;
+                ++nt;
+            }
+        }
+    }
+    int tot;
+    const int pos0 = block_prefix_excl<NT>(nt, sh.wtot, tot);
+    // ---- stage the list into sort order (position r -> thread r / P), NT*Q
+    // positions per round ----
+    unsigned long long x[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) x[p] = 0ull;
+    constexpr int Q = P < 4 ? P : 4;
+    constexpr int RND = NT * Q;
+    for (int r0 = 0; r0 < k; r0 += RND) {
+        int pos = pos0;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            if ((take >> j) & 1u) {
+                if (pos >= r0 && pos < r0 + RND) sh.buf[pos - r0] = CP::make(key[j], (uint32_t)(j * NT + tid));
+                ++pos;
+            }
+        }
+        __syncthreads();
+        const int first = tid * P;
+        if (first >= r0 && first < r0 + RND) {
+#pragma unroll
+            for (int p = 0; p < P; ++p)
+                if (first + p < k) x[p] = sh.buf[first + p - r0];
+        }
+        __syncthreads();
+    }
+    reg_sort_desc<NT, P>(x, sh.buf, sort_n);
+    if (dtype == TPR_FLOAT32 && a.sample) {
+        const int first = tid * P;
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+            if (first + p < k) sh.buf[first + p] = x[p];
+        __syncthreads();
+        if (tid < 64) sample_from_sel(a, row, reinterpret_cast<const float*>(base), sh.buf, k);
+        return;
+    }
+    const int first = tid * P;
+    long long* oi = a.out_i + row * k;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int r = first + p;
+        if (r < k) {
+            const uint32_t idx = CP::index(x[p]);
+            oi[r] = (long long)idx;
+            switch (dtype_bytes(dtype)) {
+                case 4: reinterpret_cast<uint32_t*>(a.out_v)[row * k + r] = reinterpret_cast<const uint32_t*>(base)[idx]; break;
+                case 2: reinterpret_cast<uint16_t*>(a.out_v)[row * k + r] = reinterpret_cast<const uint16_t*>(base)[idx]; break;
+                default: reinterpret_cast<uint8_t*>(a.out_v)[row * k + r] = reinterpret_cast<const uint8_t*>(base)[idx]; break;
+            }
+        }
+    }
+}
+
 struct MergeShared {
     unsigned long long cand[kMergeMax];
     int rank[kMergeMax];
@@ -1508,9 +1805,16 @@ bool radix_route(long long cols, long long k, int32_t dtype = TPR_FLOAT32) {
     return k > kWaveK || (k > kShortMaxK && cols < kWaveMinSeg);
 }
 
-// Workspace of the radix kernel: composites sorted outside LDS (8 bytes each
-// for elements of at most 4 bytes, 16 for 8-byte elements).
-size_t radix_ws(long long rows, long long k, int32_t dtype = TPR_FLOAT32) {
+// Rows the register-resident kernel takes (elements of <= 4 bytes, rows of
+// <= 32768); topk_radix = 2 forces the streaming kernel for them.
+bool rsel_route(long long cols, int32_t dtype) {
+    return dtype_size(dtype) <= 4 && cols <= kRselMaxCols && knobs().topk_radix != 2;
+}
+
+// Workspace of the streaming radix kernel: composites sorted outside LDS (8
+// bytes each for elements of at most 4 bytes, 16 for 8-byte elements).
+size_t radix_ws(long long rows, long long cols, long long k, int32_t dtype = TPR_FLOAT32) {
+    if (rsel_route(cols, dtype)) return 0;
     const long long n2 = pow2_at_least((int)k);
     const bool wide = dtype_size(dtype) == 8;
     const long long lds = wide ? 2048 : kRadixLds;
@@ -1524,7 +1828,7 @@ extern "C" {
 
 size_t tpr_topk_workspace_bytes(int32_t dtype, int64_t rows, int64_t cols, int64_t k) {
     if (rows <= 0 || cols <= 0 || k <= 0 || k > cols || cols > 0x7fffffffLL || tpr::dtype_size(dtype) == 0) return 0;
-    if (tpr::radix_route(cols, k, dtype)) return tpr::radix_ws(rows, k, dtype);
+    if (tpr::radix_route(cols, k, dtype)) return tpr::radix_ws(rows, cols, k, dtype);
     return tpr::plan_topk(rows, cols, k).ws;
 }
 
@@ -1571,6 +1875,37 @@ int launch_short(const TopkArgs& a, bool vec, hipStream_t st) {
     return check_launch("k_topk_short");
 }
 
+// Sort of n = pow2(max(k, 64)) composites, P = 4 per thread where n allows
+// (fewer waves for small n, more composites per thread when n > 4 * NT).
+// Measured on MI355X ([4096, 2048] k = 1000: P = 4 on 4 waves 73 us, P = 16
+// on one wave 108 us; [4096, 2048] k = 200: P = 4 on one wave 43 us, P = 1 on
+// 4 waves 51 us).
+template <int NT, int EPT>
+int launch_rsel_p(const TopkArgs& a, int32_t dtype, hipStream_t st) {
+    const int n = std::max(64, pow2_at_least(a.k));
+    const int P = std::min(n / 64, std::max(4, n / NT));
+    const dim3 g((unsigned)a.rows), b(NT);
+    if (P == 1) hipLaunchKernelGGL((k_topk_rsel<NT, EPT, 1>), g, b, 0, st, a, (int)dtype, n);
+    else if (P == 2) hipLaunchKernelGGL((k_topk_rsel<NT, EPT, 2>), g, b, 0, st, a, (int)dtype, n);
+    else if (P == 4) hipLaunchKernelGGL((k_topk_rsel<NT, EPT, 4>), g, b, 0, st, a, (int)dtype, n);
+    else if (P == 8) hipLaunchKernelGGL((k_topk_rsel<NT, EPT, 8>), g, b, 0, st, a, (int)dtype, n);
+    else if (P == 16) hipLaunchKernelGGL((k_topk_rsel<NT, EPT, 16>), g, b, 0, st, a, (int)dtype, n);
+    else if constexpr (NT == 1024 && EPT == 32) hipLaunchKernelGGL((k_topk_rsel<NT, EPT, 32>), g, b, 0, st, a, (int)dtype, n);
+    else return fail(TPR_ERR_INVALID_ARG, "tpr_topk: sort size beyond the workgroup");  // n <= NT * EPT
+    return check_launch("k_topk_rsel");
+}
+
+// Workgroup size and keys per thread by row length: NT * EPT >= cols, so
+// pow2(k) / NT <= EPT.
+int launch_rsel(const TopkArgs& a, int32_t dtype, hipStream_t st) {
+    if (a.cols <= 1024) return launch_rsel_p<256, 4>(a, dtype, st);
+    if (a.cols <= 2048) return launch_rsel_p<256, 8>(a, dtype, st);
+    if (a.cols <= 4096) return launch_rsel_p<256, 16>(a, dtype, st);
+    if (a.cols <= 8192) return launch_rsel_p<512, 16>(a, dtype, st);
+    if (a.cols <= 16384) return launch_rsel_p<1024, 16>(a, dtype, st);
+    return launch_rsel_p<1024, 32>(a, dtype, st);
+}
+
 // tpr_topk, or (smp != nullptr) tpr_sample: the same selection with the draw
 // in the final phase.
 int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t row_stride, int64_t k,
@@ -1585,7 +1920,7 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     if (!in || (!smp && (!out_values || !out_indices))) return fail(TPR_ERR_INVALID_ARG, "tpr_topk: null pointer");
     if (rows > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: more than 2^31-1 rows");
     const bool radix = radix_route(cols, k, dtype);
-    const TopkPlan pl = radix ? TopkPlan{1, (int)cols, false, 8, radix_ws(rows, k, dtype)} : plan_topk(rows, cols, k);
+    const TopkPlan pl = radix ? TopkPlan{1, (int)cols, false, 8, radix_ws(rows, cols, k, dtype)} : plan_topk(rows, cols, k);
     if (rows * (long long)pl.nseg > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: grid too large");
     if (pl.ws > 0 && (workspace == nullptr || workspace_bytes < pl.ws))
         return fail(TPR_ERR_WORKSPACE, "tpr_topk: workspace too small (need " + std::to_string(pl.ws) + " bytes)");
@@ -1609,6 +1944,8 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     a.ids = smp ? smp->ids : nullptr;
     const bool vec = ((reinterpret_cast<uintptr_t>(in) & 15u) == 0) && (rows == 1 || row_stride % 4 == 0);
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (radix && rsel_route(cols, dtype))
+        return launch_rsel(a, dtype, st);
     if (radix) {
         const dim3 g((unsigned)rows), b(kRadixT);
         switch (dtype) {

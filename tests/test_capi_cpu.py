@@ -83,7 +83,10 @@ def test_argument_validation_without_gpu():
     assert rc == _capi.ERR_INVALID_ARG  # float64 is served: the null input is the error
     assert L.tpr_topk_workspace_bytes(_capi.INT64, 4, 10000, 2000) == 0          # 2048 composites in LDS
     assert L.tpr_topk_workspace_bytes(_capi.INT64, 4, 10000, 3000) == 4 * 4096 * 16  # sorted in the workspace
-    assert L.tpr_topk_workspace_bytes(_capi.INT32, 4, 10000, 3000) == 0          # 4096 composites in LDS
+    assert L.tpr_topk_workspace_bytes(_capi.INT32, 4, 10000, 3000) == 0          # rows held in registers
+    assert L.tpr_topk_workspace_bytes(_capi.FLOAT32, 4, 32768, 20000) == 0       # rows held in registers
+    assert L.tpr_topk_workspace_bytes(_capi.INT32, 4, 40000, 3000) == 0          # streaming: 4096 in LDS
+    assert L.tpr_topk_workspace_bytes(_capi.INT32, 4, 40000, 5000) == 4 * 8192 * 8  # streaming: workspace sort
     with pytest.raises(_capi.TprError):
         _capi.debug_set("no_such_knob", 1)
     d = _capi.make_desc("sum", [4], [1], [0], _capi.FLOAT32)

@@ -53,7 +53,7 @@ def test_boundary_draws_stay_in_the_nucleus():
 
 def test_parameter_grid():
     rng = np.random.default_rng(30)
-    for rows, cols in [(1, 1), (7, 10), (33, 1000), (16, 32768)]:
+    for rows, cols in [(1, 1), (7, 10), (33, 1000), (16, 32768), (3, 40000)]:
         x = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
         u = rng.random(rows).astype(np.float32)
         for k in sorted({1, min(cols, 7), min(cols, 50), min(cols, 64), min(cols, 100), min(cols, 1024)}):

@@ -14,7 +14,7 @@ torch = pytest.importorskip("torch")
 @pytest.fixture(autouse=True)
 def _reset_knobs():
     yield
-    for k in ("topk_fallback", "topk_variant", "topk_waves", "splits", "topk_short"):
+    for k in ("topk_fallback", "topk_variant", "topk_waves", "splits", "topk_short", "topk_radix"):
         _capi.debug_set(k, 0)
 
 
@@ -208,11 +208,11 @@ def test_short_rows_many():
     check(y, y, 32)
 
 
-@pytest.mark.parametrize("force", [0, 1])
+@pytest.mark.parametrize("force", [0, 1, 2])
 def test_radix_select_large_k(force):
-    """k_topk_radix: exact 8-bit radix select of the k-th key, then a bitonic
-    sort of the k survivors (in LDS up to 4096, in the workspace beyond).
-    force=1 sends small k through it as well."""
+    """Large k: k_topk_rsel (rows of <= 32768 elements held in registers) or,
+    with force=2, the streaming k_topk_radix (bitonic sort in LDS up to 4096,
+    in the workspace beyond).  force=1 and 2 send small k through them too."""
     _capi.debug_set("topk_radix", force)
     rng = np.random.default_rng(30)
     x = rng.standard_normal((7, 5000)).astype(np.float32)
@@ -226,6 +226,27 @@ def test_radix_select_large_k(force):
     y = rng.uniform(-1, 1, (3, 20000)).astype(np.float32)
     check(y, y, 8193)                         # workspace sort (k > 4096)
     check(y, y[:, 1:], 3000, False)           # misaligned rows
+
+
+@pytest.mark.parametrize("cols", [700, 1024, 2000, 2048, 4000, 4096, 6000, 8192, 12000, 16384, 20000, 32768])
+def test_register_rows_large_k(cols):
+    """k_topk_rsel for every workgroup shape (256 threads x 4/8/16 keys, 512 x
+    16, 1024 x 16/32) and every sort width (1..32 composites per thread, one
+    to 16 waves): random rows, heavy ties (the index-ordered exact path when
+    the k-th key's class is larger than the number still wanted), all-equal
+    rows, NaN / +-0, rows of a strided view."""
+    rng = np.random.default_rng(cols)
+    x = rng.standard_normal((5, cols + 3)).astype(np.float32)
+    x[1] = np.round(x[1] * 2) / 2
+    x[2] = 1.5
+    x[3, ::5] = np.nan
+    x[4] = np.where(rng.random(cols + 3) < 0.5, -0.0, 0.0)
+    v = x[:, 3:]
+    ks = {1, 64, 65, 129, 255, 257, 1000, 1025, 2049, 4097, 8193, 16385, cols}
+    for k in sorted(k for k in ks if k <= cols):
+        check(x, v, k, True)
+        if k in (65, 1025, cols):
+            check(x, v, k, False)
 
 
 def test_large_k_configs():
@@ -260,9 +281,14 @@ def test_other_dtypes(dt):
         x[1, 100:300] = info.min
         x[2] = x[2] % 5
     t = torch.from_numpy(x).cuda()
-    for k in (1, 10, 64, 1000, cols):
+    cases = [(t, x, k) for k in (1, 10, 64, 1000, cols)]
+    if np.dtype(dt).itemsize <= 4:  # longer rows: 1024-thread workgroups (and the streaming kernel beyond 32768)
+        for n in (20000, 40000):
+            y = np.concatenate([x[:3]] * (n // cols + 1), axis=1)[:, :n].copy()
+            cases += [(torch.from_numpy(y).cuda(), y, k) for k in (100, 5000)]
+    for t, x, k in cases:
         for largest in (True, False):
-            print(f"case topk dtype={np.dtype(dt).name} k={k} largest={largest}", flush=True)
+            print(f"case topk dtype={np.dtype(dt).name} shape={x.shape} k={k} largest={largest}", flush=True)
             gv, gi = _capi.topk(t, k, largest)
             torch.cuda.synchronize()
             ev, ei = O.topk_any(x, k, largest)
