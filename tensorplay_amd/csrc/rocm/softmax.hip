@@ -986,7 +986,8 @@ __global__ __launch_bounds__(kWave * BY) void k_smx_cols4r(SmxColArgs p) {
 // Float64 inputs (the reference's composite runs in the input dtype, so a
 // Float64 tensor gives a Float64 softmax).  Same semantics as the float32
 // kernels, computed in double with exp / log: two passes over a slice.
-//   k_smx_f64_rows: unit-stride dim, one 256-thread workgroup per slice;
+//   k_smx_f64_rows: one 256-thread workgroup per slice: unit-stride slices,
+//                   and strided ones when there are fewer than 64 per CU;
 //   k_smx_f64_cols: any other layout, one thread per (outer, inner) slice
 //                   (consecutive threads take consecutive inner indices).
 // ---------------------------------------------------------------------------
@@ -1042,19 +1043,25 @@ __device__ __forceinline__ void fin_d(double m, double s, double& st0, double& s
     }
 }
 
-template <int MODE>
+// One 256-thread workgroup per slice.  UNIT: unit-stride slices (rows);
+// otherwise slice blockIdx.x = (outer, inner) walked with its strides, which
+// keeps few long strided slices (softmax over dim 0 of [1e6, 2]) on many
+// threads.
+template <int MODE, bool UNIT>
 __global__ __launch_bounds__(256) void k_smx_f64_rows(SmxF64Args p) {
     constexpr bool BW = MODE >= BWD;
     __shared__ double shm[4], shs[4];
-    const long long row = blockIdx.x;
-    const double* pa = p.a + row * p.a_so;
-    const double* pb = BW ? p.b + row * p.b_so : nullptr;
-    double* po = p.out + row * p.n;
+    const long long c = blockIdx.x;
+    const long long o = UNIT ? c : c / p.inner, i = UNIT ? 0 : c - o * p.inner;
+    const long long sa = UNIT ? 1 : p.a_sn, sb = UNIT ? 1 : p.b_sn, so = UNIT ? 1 : p.inner;
+    const double* pa = p.a + o * p.a_so + i * p.a_si;
+    const double* pb = BW ? p.b + o * p.b_so + i * p.b_si : nullptr;
+    double* po = p.out + o * p.n * p.inner + i;
     const int t = threadIdx.x;
     double m = -INFINITY, s = 0.0;
     for (long long e = t; e < p.n; e += 256) {
-        if constexpr (!BW) ms_add_d(m, s, pa[e]);
-        else s += (MODE == BWD) ? pa[e] * pb[e] : pa[e];
+        if constexpr (!BW) ms_add_d(m, s, pa[e * sa]);
+        else s += (MODE == BWD) ? pa[e * sa] * pb[e * sb] : pa[e * sa];
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
@@ -1076,7 +1083,8 @@ __global__ __launch_bounds__(256) void k_smx_f64_rows(SmxF64Args p) {
     }
     double st0, st1;
     fin_d<MODE>(m, s, st0, st1);
-    for (long long e = t; e < p.n; e += 256) po[e] = outv_d<MODE>(pa[e], BW ? pb[e] : 0.0, st0, st1);
+    for (long long e = t; e < p.n; e += 256)
+        po[e * so] = outv_d<MODE>(pa[e * sa], BW ? pb[e * sb] : 0.0, st0, st1);
 }
 
 template <int MODE>
@@ -1102,10 +1110,13 @@ __global__ __launch_bounds__(256) void k_smx_f64_cols(SmxF64Args p) {
 
 template <int MODE>
 int run_f64(const SmxF64Args& a, hipStream_t st) {
+    const long long cols = a.outer * a.inner;
     if (a.inner == 1 && a.a_sn == 1 && (MODE < BWD || a.b_sn == 1)) {
-        hipLaunchKernelGGL((k_smx_f64_rows<MODE>), dim3((unsigned)a.outer), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((k_smx_f64_rows<MODE, true>), dim3((unsigned)a.outer), dim3(256), 0, st, a);
+    } else if (cols < 64LL * device_info().cus && a.n >= 256) {
+        // fewer slices than 64 per CU: a workgroup per slice instead of a thread
+        hipLaunchKernelGGL((k_smx_f64_rows<MODE, false>), dim3((unsigned)cols), dim3(256), 0, st, a);
     } else {
-        const long long cols = a.outer * a.inner;
         const long long blocks = std::max(1LL, std::min((cols + 255) / 256, (long long)device_info().cus * 16));
         hipLaunchKernelGGL((k_smx_f64_cols<MODE>), dim3((unsigned)blocks), dim3(256), 0, st, a);
     }

@@ -173,7 +173,10 @@ def test_float64_inputs(log):
     # keeps the input dtype): rows and strided dims, NaN / inf slices, against
     # numpy / torch in float64 within 1e-12 relative
     rng = np.random.default_rng(21)
-    for shape, dim in [((7, 1000), 1), ((3, 40000), 1), ((4, 300, 33), 1), ((300, 70), 0), ((5, 3, 8), 2)]:
+    # strided dims: a workgroup per slice when there are few slices ([200000, 2] over dim 0), a thread per slice
+    # otherwise ([300, 20000] over dim 0)
+    for shape, dim in [((7, 1000), 1), ((3, 40000), 1), ((4, 300, 33), 1), ((300, 70), 0), ((5, 3, 8), 2),
+                       ((200000, 2), 0), ((3000, 64), 0), ((300, 20000), 0), ((100, 5), 0)]:
         x = rng.standard_normal(shape) * 3
         if x.ndim == 2 and dim == 1:
             x[0, 5] = np.nan
