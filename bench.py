@@ -48,6 +48,8 @@ def parse():
     ap.add_argument("--no-headline", action="store_true",
                     help="skip the headline step (profiling one section alone; `value` is then null)")
     ap.add_argument("--no-accuracy", action="store_true", help="skip the fp64 error report")
+    ap.add_argument("--vs-torch", action="store_true",
+                    help="also time PyTorch-ROCm's own kernels on the same shapes (reported under torch_rocm)")
     return ap.parse_args()
 
 
@@ -318,7 +320,52 @@ def main():
         result["cpu_baseline"] = None
     if not args.no_accuracy:
         result["accuracy"] = accuracy(torch, capi, keep)
+    if args.vs_torch:
+        del keep
+        result["torch_rocm"] = torch_rocm_times(torch, bufs, steps, warmup)
     print(json.dumps(result), flush=True)
+
+
+def torch_rocm_times(torch, bufs, steps, warmup):
+    """PyTorch-ROCm's own kernels on the same shapes and rotating inputs, timed
+    the same way (HIP events; `GB/s` = the same algorithmic bytes as ours)."""
+    dev = bufs[0].device
+    out = {}
+
+    def t(name, fns, by):
+        out[name] = rate(time_calls(torch, fns, max(steps, 10), warmup), by)
+
+    n2 = 64 * 1024 * 1024 * 4
+    t("C2_mean_dim1", [lambda b=b: b.mean(1) for b in bufs], n2 + 64 * 1024 * 4)
+    t("C2_amax_dim0", [lambda b=b: b.amax(0) for b in bufs], n2 + 1024 * 1024 * 4)
+    t("C2_argmax_dim0", [lambda b=b: b.argmax(0) for b in bufs], n2 + 1024 * 1024 * 8)
+    t("C2_var_dim-1", [lambda b=b: b.var(-1) for b in bufs], n2 + 64 * 1024 * 4)
+    t("C2_std_dim-1", [lambda b=b: b.std(-1) for b in bufs], n2 + 64 * 1024 * 4)
+    t("C2_clone", [lambda b=b: b.clone() for b in bufs], 2 * n2)
+    t("C2_permute_1_2_0", [lambda b=b: b.permute(1, 2, 0).contiguous() for b in bufs], 2 * n2)
+    t("C2_to_float64", [lambda b=b: b.to(torch.float64) for b in bufs], 3 * n2)
+    b1 = [gen(torch, (4096, 4096), "normal", 2000 + i, dev) for i in range(12)]
+    t("C1_sum_dim-1", [lambda b=b: b.sum(-1) for b in b1], 4096 * 4096 * 4 + 4096 * 4)
+    del b1
+    b3 = [gen(torch, (1024, 32768), "uniform", 3000 + i, dev) for i in range(6)]
+    t("C3_topk64", [lambda b=b: torch.topk(b, 64, dim=1) for b in b3], 1024 * 32768 * 4 + 1024 * 64 * 12)
+    t("C3_softmax", [lambda b=b: torch.softmax(b, -1) for b in b3[:4]], 2 * 1024 * 32768 * 4)
+    del b3
+    x4 = gen(torch, (1 << 28,), "normal", 4000, dev)
+    for op in ("sum", "amax", "argmax", "var"):
+        t(f"C4_{op}", [lambda op=op: getattr(x4, op)()], (1 << 28) * 4 + 8)
+    del x4
+    b5 = [gen(torch, (256, 151936), "normal", 5000 + i, dev) * 3.0 for i in range(5)]
+    n5 = 256 * 151936 * 4
+    t("C5_topk50", [lambda b=b: torch.topk(b, 50, dim=1) for b in b5], n5 + 256 * 50 * 12)
+    t("C5_argmax_dim-1", [lambda b=b: b.argmax(-1) for b in b5], n5 + 256 * 8)
+    t("C5_softmax", [lambda b=b: torch.softmax(b, -1) for b in b5[:3]], 2 * n5)
+    t("C5_log_softmax", [lambda b=b: torch.log_softmax(b, -1) for b in b5[:3]], 2 * n5)
+    del b5
+    b6 = [gen(torch, (4096, 2048), "uniform", 7000 + i, dev) for i in range(3)]
+    t("topk1000_4096x2048", [lambda b=b: torch.topk(b, 1000, dim=1) for b in b6], 4096 * 2048 * 4 + 4096 * 1000 * 12)
+    del b6
+    return out
 
 
 def timed(torch, calls, steps, warmup, by, **extra):
