@@ -13,7 +13,7 @@ from HBM.  Times come from HIP events on the stream the kernels run on.
 The other BASELINE configs (C1 sum, C3 topk, C4 full-tensor, C5 logits topk /
 argmax) are measured the same way and reported under "configs".
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--vs-torch]
 """
 import argparse
 import ctypes

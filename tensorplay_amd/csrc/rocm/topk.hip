@@ -1036,12 +1036,21 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
     const int k = a.k;
     constexpr int largest = LG ? 1 : 0;
     const float* p = a.in + (live ? row * a.row_stride : 0);
-    const __amdgpu_buffer_rsrc_t rs = segment_rsrc(p, live ? cols : 0);
+    // One buffer resource per wave (a per-lane resource would make every load
+    // a loop over the wave's distinct rows): it spans the wave's live rows, the
+    // lane group's row starts at grp * row_stride, and elements past a row's
+    // end but inside the span are masked below (keys 0).  The host keeps
+    // (G - 1) * row_stride + cols below 2^29 floats.
+    const long long row0 = (long long)blockIdx.x * RPB + __builtin_amdgcn_readfirstlane(threadIdx.x / 64) * G;
+    const long long nlive = min((long long)G, max(0LL, a.rows - row0));
+    const __amdgpu_buffer_rsrc_t rs = segment_rsrc(
+        a.in + (nlive > 0 ? row0 * a.row_stride : 0), nlive > 0 ? (int)((nlive - 1) * a.row_stride + cols) : 0);
+    const int rbase = grp * (int)a.row_stride * 4;
 
     float4 x[E4];
 #pragma unroll
     for (int j = 0; j < E4; ++j) {
-        const int off = 16 * (j * L + sl);
+        const int off = rbase + 16 * (j * L + sl);
         if constexpr (VEC) {
             const f32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kNT);
             x[j] = make_float4(v.x, v.y, v.z, v.w);
@@ -1965,8 +1974,10 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     // Rows of more than 2048 elements with k > 32 leave the lane-group kernel
     // too many candidates per lane: the wave kernel is faster there (MI355X,
     // [4096, 4096] k = 64: 48.5 us against 53.5 us).
-    const bool short_fit = k <= kShortMaxK && cols <= kShortMaxCols && (cols <= 2048 || k <= 32);
-    if (!smp && (short_fit || (knobs().topk_short > 0 && k <= kShortMaxK && cols <= kShortMaxCols)) &&
+    // (The lane-group kernel addresses up to 4 rows per wave with 32-bit offsets.)
+    const bool short_ok = k <= kShortMaxK && cols <= kShortMaxCols && 3 * row_stride + cols < (1LL << 29);
+    const bool short_fit = short_ok && (cols <= 2048 || k <= 32);
+    if (!smp && (short_fit || (knobs().topk_short > 0 && short_ok)) &&
         knobs().topk_short >= 0 && knobs().topk_fallback == 0 && knobs().splits <= 0)
         return launch_short(a, vec, st);
     const long long grid = rows * pl.nseg;
