@@ -446,7 +446,7 @@ __global__ __launch_bounds__(BLK) void k_rows_reg(RowArgs a) {
     constexpr int RPB = BLK / (kWave * WPR);
     static_assert(RPB >= 1 && RPB * kWave * WPR == BLK, "BLK must hold whole rows");
     const float prm = a.fin.p;
-    const int w = threadIdx.x / kWave;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform: scalar buffer resource
     const int l = __lane_id();
     const int sub = w % WPR;
     const long long row = (long long)blockIdx.x * RPB + w / WPR;
@@ -499,7 +499,7 @@ template <int NV, int WPR, int BLK>
 __global__ __launch_bounds__(BLK) void k_rows_reg_var(RowArgs a) {
     constexpr int RPB = BLK / (kWave * WPR);
     static_assert(RPB >= 1 && RPB * kWave * WPR == BLK, "BLK must hold whole rows");
-    const int w = threadIdx.x / kWave;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform: scalar buffer resource
     const int l = __lane_id();
     const int sub = w % WPR;
     const long long row = (long long)blockIdx.x * RPB + w / WPR;
