@@ -66,6 +66,7 @@ struct RbArgs {
     double count;   // element count of one reduction (mean's divisor)
     double denom;   // count - correction (var)
     float denom_f;  // (float)(count - correction) (std: result * Scalar)
+    double inv_denom;  // 1 / denom (the row kernel multiplies instead of dividing)
 };
 
 enum { B_SUM = 0, B_MEAN = 1, B_VAR = 2, B_STD = 3 };
@@ -248,11 +249,16 @@ __global__ __launch_bounds__(256) void k_vs_bwd_rows(RbArgs a, long long rows) {
     const int last = a.nd - 1;
     const int q = (int)(a.sizes[last] >> 2);  // float4 per row
     long long xo = 0, so = 0, r = row;
-    for (int d = last - 1; d >= 0; --d) {
-        const long long c = r % a.sizes[d];
-        r /= a.sizes[d];
-        xo += c * a.xs[d];
-        so += c * a.os[d];
+    if (last == 1) {  // one kept dim (the usual case after merging): no 64-bit divisions
+        xo = row * a.xs[0];
+        so = row * a.os[0];
+    } else {
+        for (int d = last - 1; d >= 0; --d) {
+            const long long c = r % a.sizes[d];
+            r /= a.sizes[d];
+            xo += c * a.xs[d];
+            so += c * a.os[d];
+        }
     }
     const f32x4* px = reinterpret_cast<const f32x4*>(a.x + xo);
     f32x4 v[V];
@@ -272,14 +278,13 @@ __global__ __launch_bounds__(256) void k_vs_bwd_rows(RbArgs a, long long rows) {
     const float g = a.g[so];
     const float rs = OP == B_STD ? a.res[so] : 0.0f;
     f32x4* po = reinterpret_cast<f32x4*>(a.gi + row * (long long)a.sizes[last]);
+    // one reciprocal per row instead of a divide per element: the double
+    // product rounds to the same float as the quotient except within ~2^-52 of
+    // a rounding boundary (one ulp then)
+    const double inv = OP == B_VAR ? a.inv_denom : 1.0 / (double)(rs * a.denom_f);
     auto f = [&](float x) -> float {
-        if constexpr (OP == B_VAR) {
-            const float tt = (g * 2.0f) * (x - mean);
-            return (float)((double)tt / a.denom);
-        } else {
-            const float tt = g * (x - mean);
-            return tt / (rs * a.denom_f);
-        }
+        const float tt = OP == B_VAR ? (g * 2.0f) * (x - mean) : g * (x - mean);
+        return (float)((double)tt * inv);
     };
 #pragma unroll
     for (int j = 0; j < V; ++j) {
@@ -335,7 +340,8 @@ __global__ __launch_bounds__(64 * BY) void k_vs_bwd_cols(RbArgs a, long long out
 #pragma unroll
         for (int k = 0; k < 4; ++k) shs[w][cl][k] = sm[k];
     __syncthreads();
-    float mean[4], g[4], rs[4];
+    float mean[4], g[4];
+    double inv[4];  // a reciprocal per column instead of a divide per element (as k_vs_bwd_rows)
     const long long so = o * a.os[0] + (live ? c : 0);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -344,16 +350,12 @@ __global__ __launch_bounds__(64 * BY) void k_vs_bwd_cols(RbArgs a, long long out
         for (int b = 0; b < BY; ++b) S += shs[b][cl][k];
         mean[k] = (float)(S / a.count);
         g[k] = live ? a.g[so + k] : 0.0f;
-        rs[k] = (OP == B_STD && live) ? a.res[so + k] : 0.0f;
+        const float rs = (OP == B_STD && live) ? a.res[so + k] : 0.0f;
+        inv[k] = OP == B_VAR ? a.inv_denom : 1.0 / (double)(rs * a.denom_f);
     }
     auto f = [&](float x, int k) -> float {
-        if constexpr (OP == B_VAR) {
-            const float tt = (g[k] * 2.0f) * (x - mean[k]);
-            return (float)((double)tt / a.denom);
-        } else {
-            const float tt = g[k] * (x - mean[k]);
-            return tt / (rs[k] * a.denom_f);
-        }
+        const float tt = OP == B_VAR ? (g[k] * 2.0f) * (x - mean[k]) : g[k] * (x - mean[k]);
+        return (float)((double)tt * inv[k]);
     };
     f32x4* qo = reinterpret_cast<f32x4*>(a.gi + o * (long long)R * inner + (live ? c : 0) + r0 * inner);
     const long long ostep = RS * inner / 4;
@@ -554,6 +556,7 @@ extern "C" int tpr_reduce_backward(const tpr_reduce_desc* d, const void* grad_ou
     a.count = (double)count;
     a.denom = (double)(count - d->correction);
     a.denom_f = (float)(count - d->correction);
+    a.inv_denom = 1.0 / a.denom;
 
     if (d->op == TPR_MEAN) {
         const size_t need = tpr_reduce_backward_workspace_bytes(d);
