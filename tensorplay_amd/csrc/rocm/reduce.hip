@@ -511,7 +511,11 @@ __global__ __launch_bounds__(BLK) void k_rows_reg_var(RowArgs a) {
 #pragma unroll
     for (int u = 0; u < NV; ++u)
         t[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, ((sub * NV + u) * kWave + l) * 16, 0, kAuxNT));
-    const double Kd = live ? (double)__uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(p[0]))) : 0.0;
+    // K through the vector memory path (a buffer load of the row's first word,
+    // the same cache line as lane 0's first vector load, which is in flight):
+    // a scalar load would fetch that line a second time
+    const double Kd = (double)__uint_as_float(
+        __builtin_amdgcn_readfirstlane(__builtin_amdgcn_raw_buffer_load_b32(rs, 0, 0, 0)));
     double s1[4] = {0.0, 0.0, 0.0, 0.0}, s2[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
