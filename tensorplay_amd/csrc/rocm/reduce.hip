@@ -1419,7 +1419,6 @@ struct ArgsI {
     // cols
     long long outer, os, rs, inner, ncb;
     int S;
-    int nt;  // nontemporal input loads
     void* out;
     void* part;
     Fin fin;
@@ -1432,17 +1431,20 @@ struct alignas(16) Vec16 {
     T v[NV];
 };
 
-// 16-byte load of NV elements; `nt` marks it nontemporal (read once).
+// 16-byte nontemporal load of NV elements (the row kernel's read-once
+// stream).  Measured on MI355X: float64 full reductions of 2^27 elements 171 ->
+// 155 us against plain loads; the column kernel keeps plain loads (nontemporal
+// ones were 2-6% slower there: int32 sum over dim 1 of [64, 1024, 1024] 44.9
+// against 42.4 us).  A runtime choice between the two is not possible here: the
+// compiler merges the two otherwise identical loads of the branches into one
+// and drops the nontemporal mark.
 template <class T, int NV>
-__device__ __forceinline__ Vec16<T, NV> ld16(const Vec16<T, NV>* p, int nt) {
-    if (nt) {
-        typedef int i32x4 __attribute__((ext_vector_type(4)));
-        const i32x4 r = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p));
-        Vec16<T, NV> t;
-        __builtin_memcpy(&t, &r, 16);
-        return t;
-    }
-    return *p;
+__device__ __forceinline__ Vec16<T, NV> ld16_nt(const Vec16<T, NV>* p) {
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    Vec16<T, NV> t;
+    const i32x4 r = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p));
+    __builtin_memcpy(&t, &r, 16);
+    return t;
 }
 
 template <class Op, int LANES>
@@ -1497,14 +1499,14 @@ __global__ __launch_bounds__(LANES > kBlock ? LANES : kBlock) void k_rows_i(Args
             for (; v + 3 * step < nv; v += 4 * step) {
                 Vec16<T, NV> t[4];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) t[u] = ld16(pv + v + u * step, a.nt);
+                for (int u = 0; u < 4; ++u) t[u] = ld16_nt(pv + v + u * step);
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
 #pragma unroll
                     for (int j = 0; j < NV; ++j) Op::acc(acc, t[u].v[j], (v + u * step) * NV + j, prm);
             }
             for (; v < nv; v += step) {
-                const Vec16<T, NV> t = ld16(pv + v, a.nt);
+                const Vec16<T, NV> t = ld16_nt(pv + v);
 #pragma unroll
                 for (int j = 0; j < NV; ++j) Op::acc(acc, t.v[j], v * NV + j, prm);
             }
@@ -1549,14 +1551,14 @@ __global__ __launch_bounds__(kBlock) void k_cols_i(ArgsI a) {
                 Vec16<T, NV> t[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
-                    t[u] = ld16(reinterpret_cast<const Vec16<T, NV>*>(base + (long long)(r + u * rstep) * a.rs), a.nt);
+                    t[u] = *reinterpret_cast<const Vec16<T, NV>*>(base + (long long)(r + u * rstep) * a.rs);
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
 #pragma unroll
                     for (int j = 0; j < NV; ++j) Op::acc(acc[j], t[u].v[j], r + u * rstep, prm);
             }
             for (; r < R; r += rstep) {
-                const Vec16<T, NV> t = ld16(reinterpret_cast<const Vec16<T, NV>*>(base + (long long)r * a.rs), a.nt);
+                const Vec16<T, NV> t = *reinterpret_cast<const Vec16<T, NV>*>(base + (long long)r * a.rs);
 #pragma unroll
                 for (int j = 0; j < NV; ++j) Op::acc(acc[j], t.v[j], r, prm);
             }
@@ -1830,7 +1832,6 @@ int launch_int_layout(const Plan& p, const void* in, void* out, void* ws, Fin fi
         a.in = in; a.rows = p.rows; a.R = p.R; a.row_stride = p.row_stride;
         a.S = (int)p.S; a.out = out; a.part = ws; a.fin = fin;
         a.idx_off = p.idx_off; a.partial = p.partial || p.S > 1;
-        a.nt = (p.rows * p.R * (long long)sizeof(T) >= (64LL << 20)) ? 1 : 0;
         const long long groups = (p.lanes >= kBlock) ? 1 : kBlock / p.lanes;
         const dim3 grid(ceil_div(p.rows, groups) * p.S);
         const dim3 blk(p.lanes > kBlock ? p.lanes : kBlock);
@@ -1852,7 +1853,6 @@ int launch_int_layout(const Plan& p, const void* in, void* out, void* ws, Fin fi
         a.in = in; a.outer = p.outer; a.os = p.os; a.R = p.R; a.rs = p.rs; a.inner = p.inner; a.ncb = p.ncb;
         a.S = (int)p.S; a.out = out; a.part = ws; a.fin = fin;
         a.idx_off = p.idx_off; a.partial = p.partial || p.S > 1;
-        a.nt = (p.outer * p.R * p.inner * (long long)sizeof(T) >= (64LL << 20)) ? 1 : 0;
         const dim3 grid(p.outer * p.ncb * p.S);
 #define TPR_COLS_I(TXV)                                                                             \
     if (p.tx == TXV) {                                                                              \
