@@ -145,22 +145,23 @@ struct RowsArgs {
     long long chunk;                         // elements per workgroup
 };
 
-__device__ __forceinline__ void outer_offsets(const RowsArgs& a, long long row, long long& doff, long long& soff) {
+__device__ __forceinline__ void outer_offsets(const RowsArgs& a, unsigned row, long long& doff, long long& soff) {
     doff = 0;
     soff = 0;
     for (int d = a.nouter - 1; d >= 0; --d) {
-        const long long q = row / a.osz[d];
-        const long long r = row - q * a.osz[d];
-        doff += r * a.ods[d];
-        soff += r * a.oss[d];
+        const unsigned m = a.osz[d] > 0xffffffffLL ? 0xffffffffu : (unsigned)a.osz[d];
+        const unsigned q = row / m, r = row - q * m;  // 32-bit: row < 2^32
+        doff += (long long)r * a.ods[d];
+        soff += (long long)r * a.oss[d];
         row = q;
     }
 }
 
 template <class D, class S, bool VEC>
 __global__ __launch_bounds__(kCopyBlock) void k_copy_rows(RowsArgs a) {
-    const long long row = blockIdx.x / a.nchunk;
-    const long long c = blockIdx.x - row * a.nchunk;
+    const unsigned nch = a.nchunk > 0xffffffffLL ? 0xffffffffu : (unsigned)a.nchunk;
+    const unsigned row = blockIdx.x / nch;
+    const long long c = blockIdx.x - row * nch;
     long long doff, soff;
     outer_offsets(a, row, doff, soff);
     D* dst = static_cast<D*>(a.dst) + doff;
@@ -190,23 +191,36 @@ struct TileArgs {
     long long bds[TPR_MAX_DIMS], bss[TPR_MAX_DIMS];
 };
 
+// 32-bit division of a workgroup index (< 2^32) by m: a divisor of 2^32 or
+// more leaves the index whole.  A 64-bit division is a long software sequence.
+__device__ __forceinline__ unsigned div32(unsigned& b, long long m) {
+    const unsigned d = m > 0xffffffffLL ? 0xffffffffu : (unsigned)m;
+    const unsigned q = b / d, r = b - q * d;
+    b = q;
+    return r;
+}
+
+// The tile (ti, tj) and batch offsets of this workgroup.
+__device__ __forceinline__ void tile_origin(const TileArgs& a, long long& ti, long long& tj, long long& doff,
+                                            long long& soff) {
+    unsigned b = blockIdx.x;
+    ti = div32(b, a.tilesI);
+    tj = div32(b, a.tilesJ);
+    doff = 0;
+    soff = 0;
+    for (int d = a.nb - 1; d >= 0; --d) {
+        const long long r = div32(b, a.bsz[d]);
+        doff += r * a.bds[d];
+        soff += r * a.bss[d];
+    }
+}
+
 template <class D, class S>
 __global__ __launch_bounds__(kCopyBlock) void k_copy_tile(TileArgs a) {
     // +1 element of padding per row: column walks hit distinct banks for 4-byte D
     __shared__ D tile[kTile][kTile + 1];
-    long long b = blockIdx.x;
-    const long long ti = b % a.tilesI;
-    b /= a.tilesI;
-    const long long tj = b % a.tilesJ;
-    b /= a.tilesJ;
-    long long doff = 0, soff = 0;
-    for (int d = a.nb - 1; d >= 0; --d) {
-        const long long q = b / a.bsz[d];
-        const long long r = b - q * a.bsz[d];
-        doff += r * a.bds[d];
-        soff += r * a.bss[d];
-        b = q;
-    }
+    long long ti, tj, doff, soff;
+    tile_origin(a, ti, tj, doff, soff);
     D* dst = static_cast<D*>(a.dst) + doff;
     const S* src = static_cast<const S*>(a.src) + soff;
     const long long i0 = ti * kTile, j0 = tj * kTile;
@@ -240,19 +254,8 @@ __global__ __launch_bounds__(kCopyBlock) void k_copy_tile_v(TileArgs a) {
     constexpr int VS = 16 / (int)sizeof(D);
     struct alignas(16) OutV { D v[VS]; };
     __shared__ D tile[TJ][TI + 1];
-    long long b = blockIdx.x;
-    const long long ti = b % a.tilesI;
-    b /= a.tilesI;
-    const long long tj = b % a.tilesJ;
-    b /= a.tilesJ;
-    long long doff = 0, soff = 0;
-    for (int d = a.nb - 1; d >= 0; --d) {
-        const long long q = b / a.bsz[d];
-        const long long r = b - q * a.bsz[d];
-        doff += r * a.bds[d];
-        soff += r * a.bss[d];
-        b = q;
-    }
+    long long ti, tj, doff, soff;
+    tile_origin(a, ti, tj, doff, soff);
     const long long i0 = ti * TI, j0 = tj * TJ;
     D* dst = static_cast<D*>(a.dst) + doff + i0 + j0 * a.dsJ;
     const S* src = static_cast<const S*>(a.src) + soff + j0 + i0 * a.ssI;
