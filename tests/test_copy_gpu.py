@@ -147,3 +147,26 @@ def test_full_size_permutes_match_numpy():
     o64 = torch.empty(x.shape, dtype=torch.float64, device="cuda")
     _capi.copy_(o64, x)
     assert torch.equal(o64.cpu(), x.cpu().double())
+    # the dense clone (nontemporal accesses from 64 MiB)
+    oc = torch.empty_like(x)
+    assert _capi.copy_plan(oc, x) == C | _capi.COPY_VEC
+    _capi.copy_(oc, x)
+    assert torch.equal(oc, x)
+
+
+def test_large_same_type_copies_other_widths():
+    """Copies of 64 MiB or more between equal dtypes take nontemporal loads and
+    stores: 1-, 2- and 8-byte tiles and dense runs, bit-exact against numpy."""
+    rng = np.random.default_rng(12)
+    cases = [(np.uint8, (64, 1024, 1024), (0, 2, 1)), (np.int16, (32, 1024, 1024), (1, 2, 0)),
+             (np.int64, (16, 1024, 1024), (0, 2, 1)), (np.float64, (8, 1024, 1024), None)]
+    for dt, shape, perm in cases:
+        xn = rng.integers(-100, 100, size=shape).astype(dt)
+        x = torch.from_numpy(xn).cuda()
+        v = x if perm is None else x.permute(*perm)
+        print(f"case large copy {np.dtype(dt).name} {shape} perm={perm}", flush=True)
+        out = torch.empty(v.shape, dtype=x.dtype, device="cuda")
+        _capi.copy_(out, v)
+        ref = xn if perm is None else np.ascontiguousarray(xn.transpose(perm))
+        np.testing.assert_array_equal(out.cpu().numpy(), ref)
+        del x, v, out
