@@ -441,12 +441,16 @@ int launch_copy(const CopyPlan& p, void* dst, const void* src, hipStream_t st) {
         if (p.vec) {
             const long long per_block = (long long)kCopyBlock * kChunkVecs * VecT<D, S>::V;
             const long long blocks = (p.n + per_block - 1) / per_block;
-            // Nontemporal loads and stores for large same-size copies.  Measured on
-            // MI355X: a 256 MiB clone 88.4 -> 82.9 us; a 16 MiB clone (cache
-            // resident) 6.1 -> 6.7 us and float32 -> float64 at 256 MiB 136 -> 195 us
-            // with them, so those keep plain accesses.
-            if constexpr (sizeof(D) == sizeof(S)) {
-                if (bytes >= (64LL << 20)) {
+            // Nontemporal loads (and, for same-size copies, stores) from 64 MiB
+            // when the destination element is not wider than the source.
+            // Measured on MI355X at [64, 1024, 1024] float32 sources: clone 88.6 ->
+            // 83.0 us, to int32 88.2 -> 83.0, to int8 59.6 -> 57.5; float64 ->
+            // float32 135 -> 133.5; widening casts keep plain accesses (to float64
+            // 136.5 against 140 with nontemporal loads, 195 with nontemporal
+            // stores too); a 16 MiB clone (cache resident) is faster plain (6.1
+            // against 6.7 us).  The nt debug knob < 0 turns them off.
+            if constexpr (sizeof(D) <= sizeof(S)) {
+                if (bytes >= (64LL << 20) && knobs().nt >= 0) {
                     hipLaunchKernelGGL((k_copy_contig<D, S, true>), dim3((unsigned)blocks), dim3(kCopyBlock), 0, st, a);
                     return check_launch("k_copy_contig");
                 }
