@@ -34,6 +34,7 @@
 #include <atomic>
 #include <cmath>
 #include <string>
+#include <type_traits>
 
 #include "common.h"
 
@@ -50,32 +51,34 @@ __device__ __forceinline__ float exs(float d) { return __builtin_amdgcn_exp2f(d 
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-template <int VW>
-struct Vec;
-template <>
-struct Vec<4> {
-    __device__ static void load(float (&v)[4], const float* p, int nt) {
+// Row-segment loads / stores of VW floats; NT (nontemporal) is a template
+// parameter because a runtime choice compiles to plain accesses only: the
+// compiler merges the two branches' otherwise identical loads and stores and
+// drops the nontemporal mark.
+template <int VW, bool NT>
+__device__ __forceinline__ void vld(float (&v)[VW], const float* p) {
+    if constexpr (VW == 4) {
         f32x4 t;
-        if (nt) t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+        if constexpr (NT) t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
         else t = *reinterpret_cast<const f32x4*>(p);
         v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    } else {
+        if constexpr (NT) v[0] = __builtin_nontemporal_load(p);
+        else v[0] = *p;
     }
-    __device__ static void store(float* p, const float (&v)[4], int nt) {
-        f32x4 t = {v[0], v[1], v[2], v[3]};
-        if (nt) __builtin_nontemporal_store(t, reinterpret_cast<f32x4*>(p));
+}
+
+template <int VW, bool NT>
+__device__ __forceinline__ void vst(float* p, const float (&v)[VW]) {
+    if constexpr (VW == 4) {
+        const f32x4 t = {v[0], v[1], v[2], v[3]};
+        if constexpr (NT) __builtin_nontemporal_store(t, reinterpret_cast<f32x4*>(p));
         else *reinterpret_cast<f32x4*>(p) = t;
-    }
-};
-template <>
-struct Vec<1> {
-    __device__ static void load(float (&v)[1], const float* p, int nt) {
-        v[0] = nt ? __builtin_nontemporal_load(p) : *p;
-    }
-    __device__ static void store(float* p, const float (&v)[1], int nt) {
-        if (nt) __builtin_nontemporal_store(v[0], p);
+    } else {
+        if constexpr (NT) __builtin_nontemporal_store(v[0], p);
         else *p = v[0];
     }
-};
+}
 
 // Sum / max over G consecutive lanes (G <= 64: xor shuffles inside the wave;
 // G > 64: one workgroup of G threads, via `sh` (G / 64 floats, private to this
@@ -178,7 +181,7 @@ struct SmxArgs {
 // write once.  G <= 256: 256-thread workgroups holding 256/G rows; G > 256:
 // one row per G-thread workgroup.
 // ---------------------------------------------------------------------------
-template <int MODE, int G, int V, int VW>
+template <int MODE, int G, int V, int VW, bool NT>
 __global__ __launch_bounds__(G > 256 ? G : 256) void k_smx_rows(SmxArgs p) {
     constexpr int BLK = G > 256 ? G : 256;
     constexpr int RPB = BLK / G;
@@ -198,8 +201,8 @@ __global__ __launch_bounds__(G > 256 ? G : 256) void k_smx_rows(SmxArgs p) {
     for (int j = 0; j < V; ++j) {
         const long long e = ((long long)j * G + lane) * VW;
         if (live && e < p.n) {
-            Vec<VW>::load(a[j], pa + e, p.nt);
-            if constexpr (BW) Vec<VW>::load(b[j], pb + e, p.nt);
+            vld<VW, NT>(a[j], pa + e);
+            if constexpr (BW) vld<VW, NT>(b[j], pb + e);
         } else {
 #pragma unroll
             for (int c = 0; c < VW; ++c) {
@@ -249,7 +252,7 @@ __global__ __launch_bounds__(G > 256 ? G : 256) void k_smx_rows(SmxArgs p) {
             float o[VW];
 #pragma unroll
             for (int c = 0; c < VW; ++c) o[c] = outv<MODE>(a[j][c], BW ? b[j][c] : 0.0f, st0, st1);
-            Vec<VW>::store(po + e, o, p.nt);
+            vst<VW, NT>(po + e, o);
         }
     }
 }
@@ -262,7 +265,7 @@ __global__ __launch_bounds__(G > 256 ? G : 256) void k_smx_rows(SmxArgs p) {
 // two tiles in flight: the loads of tile t+1 are issued before tile t is
 // consumed (one workgroup per CU has to cover the memory latency alone).
 // ---------------------------------------------------------------------------
-template <int MODE, int VW, int U>
+template <int MODE, int VW, int U, bool NT>
 __global__ __launch_bounds__(1024) void k_smx_rows2(SmxArgs p) {
     constexpr int T = 1024;
     constexpr bool BW = MODE >= BWD;
@@ -277,14 +280,17 @@ __global__ __launch_bounds__(1024) void k_smx_rows2(SmxArgs p) {
     const int t = threadIdx.x;
 
     // wb: also load y (pass 1 of the log_softmax gradient needs g only)
-    auto load = [&](float (&xa)[U][VW], float (&xb)[UB][VW], long long base, int nt, bool wb) {
+    // ntc: std::bool_constant, nontemporal loads (pass 2 only: pass 1's data may
+    // still be in the Infinity Cache when pass 2 re-reads it)
+    auto load = [&](float (&xa)[U][VW], float (&xb)[UB][VW], long long base, auto ntc, bool wb) {
+        constexpr bool L_NT = decltype(ntc)::value;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const long long e = base + ((long long)u * T + t) * VW;
             if (e < n) {
-                Vec<VW>::load(xa[u], pa + e, nt);
+                vld<VW, L_NT>(xa[u], pa + e);
                 if constexpr (BW) {
-                    if (wb) Vec<VW>::load(xb[u], pb + e, nt);
+                    if (wb) vld<VW, L_NT>(xb[u], pb + e);
                 }
             } else {
 #pragma unroll
@@ -309,13 +315,13 @@ __global__ __launch_bounds__(1024) void k_smx_rows2(SmxArgs p) {
         }
     };
     constexpr bool WB1 = MODE == BWD;  // pass 1 reads y
-    load(a0, b0, 0, 0, WB1);
+    load(a0, b0, 0, std::false_type{}, WB1);
     for (long long base = 0;;) {
-        if (base + TILE < n) load(a1, b1, base + TILE, 0, WB1);
+        if (base + TILE < n) load(a1, b1, base + TILE, std::false_type{}, WB1);
         consume(a0, b0);
         base += TILE;
         if (base >= n) break;
-        if (base + TILE < n) load(a0, b0, base + TILE, 0, WB1);
+        if (base + TILE < n) load(a0, b0, base + TILE, std::false_type{}, WB1);
         consume(a1, b1);
         base += TILE;
         if (base >= n) break;
@@ -343,17 +349,17 @@ __global__ __launch_bounds__(1024) void k_smx_rows2(SmxArgs p) {
                 float o[VW];
 #pragma unroll
                 for (int c = 0; c < VW; ++c) o[c] = outv<MODE>(xa[u][c], BW ? xb[u][c] : 0.0f, st0, st1);
-                Vec<VW>::store(po + e, o, p.nt);
+                vst<VW, NT>(po + e, o);
             }
         }
     };
-    load(a0, b0, 0, p.nt, true);
+    load(a0, b0, 0, std::bool_constant<NT>{}, true);
     for (long long base = 0;;) {
-        if (base + TILE < n) load(a1, b1, base + TILE, p.nt, true);
+        if (base + TILE < n) load(a1, b1, base + TILE, std::bool_constant<NT>{}, true);
         emit(a0, b0, base);
         base += TILE;
         if (base >= n) break;
-        if (base + TILE < n) load(a0, b0, base + TILE, p.nt, true);
+        if (base + TILE < n) load(a0, b0, base + TILE, std::bool_constant<NT>{}, true);
         emit(a1, b1, base);
         base += TILE;
         if (base >= n) break;
@@ -591,8 +597,8 @@ __global__ __launch_bounds__(256) void k_smx_part(SmxArgs p) {
         for (int u = 0; u < U; ++u) {
             const long long e = c0 + it * STEP + ((long long)u * 256 + t) * VW;
             if (e < p.n) {
-                Vec<VW>::load(x[u], pa + e, 0);
-                if constexpr (MODE == BWD) Vec<VW>::load(y[u], pb + e, 0);  // BWD_LOG: sum(g) needs no y
+                vld<VW, false>(x[u], pa + e);
+                if constexpr (MODE == BWD) vld<VW, false>(y[u], pb + e);  // BWD_LOG: sum(g) needs no y
             } else {
 #pragma unroll
                 for (int c = 0; c < VW; ++c) {
@@ -615,7 +621,7 @@ __global__ __launch_bounds__(256) void k_smx_part(SmxArgs p) {
     if (t == 0) p.part[blockIdx.x] = make_float2(m, s);
 }
 
-template <int MODE, int VW>
+template <int MODE, int VW, bool NT>
 __global__ __launch_bounds__(256) void k_smx_apply(SmxArgs p) {
     constexpr bool BW = MODE >= BWD;
     constexpr int U = 8 / VW;
@@ -650,8 +656,8 @@ __global__ __launch_bounds__(256) void k_smx_apply(SmxArgs p) {
         for (int u = 0; u < U; ++u) {
             const long long e = c0 + it * STEP + ((long long)u * 256 + t) * VW;
             if (e < p.n) {
-                Vec<VW>::load(x[u], pa + e, p.nt);
-                if constexpr (BW) Vec<VW>::load(y[u], pb + e, p.nt);
+                vld<VW, NT>(x[u], pa + e);
+                if constexpr (BW) vld<VW, NT>(y[u], pb + e);
             }
         }
 #pragma unroll
@@ -661,7 +667,7 @@ __global__ __launch_bounds__(256) void k_smx_apply(SmxArgs p) {
                 float o[VW];
 #pragma unroll
                 for (int c = 0; c < VW; ++c) o[c] = outv<MODE>(x[u][c], BW ? y[u][c] : 0.0f, st0, st1);
-                Vec<VW>::store(po + e, o, p.nt);
+                vst<VW, NT>(po + e, o);
             }
         }
     }
@@ -788,8 +794,8 @@ __global__ __launch_bounds__(kWave * BY) void k_smx_cols4(SmxColArgs p) {
         float x[U][4], y[BW ? U : 1][4];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            Vec<4>::load(x[u], pa + (r + (long long)u * RS) * p.a_sn, 0);
-            if constexpr (MODE == BWD) Vec<4>::load(y[u], pb + (r + (long long)u * RS) * p.b_sn, 0);
+            vld<4, false>(x[u], pa + (r + (long long)u * RS) * p.a_sn);
+            if constexpr (MODE == BWD) vld<4, false>(y[u], pb + (r + (long long)u * RS) * p.b_sn);
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -806,8 +812,8 @@ __global__ __launch_bounds__(kWave * BY) void k_smx_cols4(SmxColArgs p) {
     }
     for (; r < n; r += RS) {
         float x[4], y[4];
-        Vec<4>::load(x, pa + r * p.a_sn, 0);
-        if constexpr (MODE == BWD) Vec<4>::load(y, pb + r * p.b_sn, 0);
+        vld<4, false>(x, pa + r * p.a_sn);
+        if constexpr (MODE == BWD) vld<4, false>(y, pb + r * p.b_sn);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             if constexpr (!BW) ms_add<1>(m[q], sm[q], &x[q]);
@@ -856,11 +862,11 @@ __global__ __launch_bounds__(kWave * BY) void k_smx_cols4(SmxColArgs p) {
     }
     for (r = rl + 4 * w; r < n; r += RS) {
         float x[4], y[4], out[4];
-        Vec<4>::load(x, pa + r * p.a_sn, p.nt);
-        if constexpr (BW) Vec<4>::load(y, pb + r * p.b_sn, p.nt);
+        vld<4, false>(x, pa + r * p.a_sn);
+        if constexpr (BW) vld<4, false>(y, pb + r * p.b_sn);
 #pragma unroll
         for (int q = 0; q < 4; ++q) out[q] = outv<MODE>(x[q], BW ? y[q] : 0.0f, st0[q], st1[q]);
-        Vec<4>::store(po + r * p.inner, out, p.nt);
+        vst<4, false>(po + r * p.inner, out);  // plain: nontemporal was slower here (dim 0 of [64, 1024, 1024]: 143 vs 129 us)
     }
 }
 
@@ -869,7 +875,7 @@ __global__ __launch_bounds__(kWave * BY) void k_smx_cols4(SmxColArgs p) {
 // 8 -> 128), BY waves, and each lane keeps its V rows (r = rl + (64/CW) w +
 // i * RS) in registers, so the slice is read once and written from registers.
 // For n <= RS * V.
-template <int MODE, int BY, int V, int CW>
+template <int MODE, int BY, int V, int CW, bool NT>
 __global__ __launch_bounds__(kWave * BY) void k_smx_cols4r(SmxColArgs p) {
     constexpr bool BW = MODE >= BWD;
     constexpr int RW = kWave / CW;  // rows per wave step
@@ -894,8 +900,8 @@ __global__ __launch_bounds__(kWave * BY) void k_smx_cols4r(SmxColArgs p) {
     for (int i = 0; i < V; ++i) {
         const int r = r0 + i * RS;
         if (r < n) {
-            Vec<4>::load(x[i], pa + r * p.a_sn, p.nt);
-            if constexpr (BW) Vec<4>::load(y[i], pb + r * p.b_sn, p.nt);
+            vld<4, NT>(x[i], pa + r * p.a_sn);
+            if constexpr (BW) vld<4, NT>(y[i], pb + r * p.b_sn);
         } else {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -976,7 +982,7 @@ __global__ __launch_bounds__(kWave * BY) void k_smx_cols4r(SmxColArgs p) {
             float out[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) out[q] = outv<MODE>(x[i][q], BW ? y[i][q] : 0.0f, st0[q], st1[q]);
-            Vec<4>::store(po + (long long)r * p.inner, out, p.nt);
+            vst<4, NT>(po + (long long)r * p.inner, out);
         }
     }
 }
@@ -1131,7 +1137,8 @@ int launch_rows(const SmxArgs& a, hipStream_t st) {
     constexpr int BLK = G > 256 ? G : 256;
     constexpr int RPB = BLK / G;
     const long long blocks = (a.rows + RPB - 1) / RPB;
-    hipLaunchKernelGGL((k_smx_rows<MODE, G, V, VW>), dim3((unsigned)blocks), dim3(BLK), 0, st, a);
+    if (a.nt) hipLaunchKernelGGL((k_smx_rows<MODE, G, V, VW, true>), dim3((unsigned)blocks), dim3(BLK), 0, st, a);
+    else hipLaunchKernelGGL((k_smx_rows<MODE, G, V, VW, false>), dim3((unsigned)blocks), dim3(BLK), 0, st, a);
     return check_launch("tpr_softmax (rows)");
 }
 
@@ -1275,15 +1282,19 @@ int run_rows(const SmxArgs& a0, int vw, hipStream_t st) {
         const long long blocks = a.rows * a.chunks;
         if (vw == 4) {
             hipLaunchKernelGGL((k_smx_part<MODE, 4>), dim3((unsigned)blocks), dim3(256), 0, st, a);
-            hipLaunchKernelGGL((k_smx_apply<MODE, 4>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+            if (a.nt) hipLaunchKernelGGL((k_smx_apply<MODE, 4, true>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((k_smx_apply<MODE, 4, false>), dim3((unsigned)blocks), dim3(256), 0, st, a);
         } else {
             hipLaunchKernelGGL((k_smx_part<MODE, 1>), dim3((unsigned)blocks), dim3(256), 0, st, a);
-            hipLaunchKernelGGL((k_smx_apply<MODE, 1>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+            if (a.nt) hipLaunchKernelGGL((k_smx_apply<MODE, 1, true>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((k_smx_apply<MODE, 1, false>), dim3((unsigned)blocks), dim3(256), 0, st, a);
         }
         return check_launch("tpr_softmax (split rows)");
     }
-    if (vw == 4) hipLaunchKernelGGL((k_smx_rows2<MODE, 4, BW ? 2 : 4>), dim3((unsigned)a.rows), dim3(1024), 0, st, a);
-    else hipLaunchKernelGGL((k_smx_rows2<MODE, 1, BW ? 8 : 16>), dim3((unsigned)a.rows), dim3(1024), 0, st, a);
+    if (vw == 4 && a.nt) hipLaunchKernelGGL((k_smx_rows2<MODE, 4, BW ? 2 : 4, true>), dim3((unsigned)a.rows), dim3(1024), 0, st, a);
+    else if (vw == 4) hipLaunchKernelGGL((k_smx_rows2<MODE, 4, BW ? 2 : 4, false>), dim3((unsigned)a.rows), dim3(1024), 0, st, a);
+    else if (a.nt) hipLaunchKernelGGL((k_smx_rows2<MODE, 1, BW ? 8 : 16, true>), dim3((unsigned)a.rows), dim3(1024), 0, st, a);
+    else hipLaunchKernelGGL((k_smx_rows2<MODE, 1, BW ? 8 : 16, false>), dim3((unsigned)a.rows), dim3(1024), 0, st, a);
     return check_launch("tpr_softmax (long rows)");
 }
 
@@ -1306,12 +1317,18 @@ int run_cols(const SmxColArgs& a, hipStream_t st) {
                 // workgroups per CU) measured slower: 143 vs 131 us at [64, 1024,
                 // 1024] dim 1, 193 vs 111 us at [2048, 128, 256]
                 const unsigned g = (unsigned)(a.outer * ((a.inner + 63) / 64));
-                if (a.n <= 128) hipLaunchKernelGGL((k_smx_cols4r<MODE, 8, 4, 16>), dim3(g), dim3(kWave * 8), 0, st, a);
-                else if (a.n <= 256) hipLaunchKernelGGL((k_smx_cols4r<MODE, 8, 8, 16>), dim3(g), dim3(kWave * 8), 0, st, a);
+#define TPR_C4R(BYV, VV)                                                                                          \
+    {                                                                                                             \
+        if (a.nt) hipLaunchKernelGGL((k_smx_cols4r<MODE, BYV, VV, 16, true>), dim3(g), dim3(kWave * BYV), 0, st, a); \
+        else hipLaunchKernelGGL((k_smx_cols4r<MODE, BYV, VV, 16, false>), dim3(g), dim3(kWave * BYV), 0, st, a); \
+    }
+                if (a.n <= 128) TPR_C4R(8, 4)
+                else if (a.n <= 256) TPR_C4R(8, 8)
                 else if constexpr (!BW) {
-                    if (a.n <= 512) hipLaunchKernelGGL((k_smx_cols4r<MODE, 16, 8, 16>), dim3(g), dim3(kWave * 16), 0, st, a);
-                    else hipLaunchKernelGGL((k_smx_cols4r<MODE, 16, 16, 16>), dim3(g), dim3(kWave * 16), 0, st, a);
+                    if (a.n <= 512) TPR_C4R(16, 8)
+                    else TPR_C4R(16, 16)
                 }
+#undef TPR_C4R
                 return check_launch("tpr_softmax (strided dim, in registers)");
             }
             int by = a.n >= 1024 ? 16 : (a.n >= 128 ? 8 : 4);
