@@ -116,6 +116,29 @@ def test_strided_dim_held_in_registers(log, res):
 
 
 @pytest.mark.parametrize("log", [False, True])
+def test_nontemporal_variants(log):
+    """The kernels' nontemporal instantiations (chosen from 256 MiB of traffic;
+    the nt knob forces them here on small shapes): rows through every plan,
+    strided slices held in registers, and the gradients over rows."""
+    _capi.debug_set("nt", 1)
+    rng = np.random.default_rng(19)
+    for plan in PLANS:
+        set_plan(plan)
+        for n in (100, 1024, 5000, 40000):
+            x = (rng.standard_normal((4, n)) * 3).astype(np.float32)
+            check_fwd(x, x, 1, log)
+    set_plan((0, 0, 0))
+    for n in (65, 256, 1000):
+        x = (rng.standard_normal((2, n, 200)) * 2).astype(np.float32)
+        x[0, n // 2, 1] = np.nan
+        check_fwd(x, x, 1, log)
+    for plan in PLANS[:3]:
+        set_plan(plan)
+        for i, n in enumerate([64, 4096, 20000]):
+            check_bwd((4, n), 1, log, 500 + i)
+
+
+@pytest.mark.parametrize("log", [False, True])
 @pytest.mark.parametrize("plan", PLANS[:3])
 def test_nan_inf_slices(log, plan):
     set_plan(plan)
