@@ -76,6 +76,7 @@ int tpr_debug_set(const char* key, int64_t value) {
     else if (!std::strcmp(key, "rowreg")) k.rowreg = value;
     else if (!std::strcmp(key, "topk_short")) k.topk_short = value;
     else if (!std::strcmp(key, "topk_radix")) k.topk_radix = value;
+    else if (!std::strcmp(key, "topk_dyn")) k.topk_dyn = value;
     else return tpr::fail(TPR_ERR_INVALID_ARG, std::string("tpr_debug_set: unknown key ") + key);
     return TPR_OK;
 }

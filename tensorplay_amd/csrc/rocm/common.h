@@ -48,6 +48,7 @@ struct DebugKnobs {
     Knob rowreg{0};
     Knob topk_short{0};
     Knob topk_radix{0};
+    Knob topk_dyn{0};
 };
 DebugKnobs& knobs();
 

@@ -123,6 +123,7 @@ struct TopkArgs {
     // sampling (tpr_sample): instead of writing values / indices, draw one id
     // per row from the sorted top k (see sample_from_sel)
     int sample;
+    int dyn;  // wave kernel: slices after the first ones handed out by an LDS counter
     float temperature, top_p;
     const float* u;
     long long* ids;
@@ -218,6 +219,7 @@ struct BlockScratch {
     int digit;
     int kk;
     int eq_taken;
+    int next_slice;  // wave kernel: next slice to hand out (dynamic assignment)
 };
 
 // r-th largest of the wave's per-lane maxima of `key` (0 if fewer than r lanes
@@ -617,6 +619,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
         bs.tshared = 1;
         bs.count = 0;
         bs.over = a.force_fallback;
+        bs.next_slice = 2 * kW;  // slices w and w + kW (prefetched) are static
     }
 
     // Wave slices are w, w+8, w+16, ...  PD = slices whose loads are in flight
@@ -703,6 +706,28 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
                 if (c >= nsl) break;
                 slice_keys(bufA, lo + c * kSl, hi, largest, key);
                 load_slice<VEC, SV>(bufA, rs, (c + 2 * kW) * kSl);
+            }
+        } else if (PD == 1 && NW == 16 && a.dyn) {
+            // Slices past the first two of each wave go to whichever wave asks
+            // next (an LDS counter), so the waves of a workgroup finish their
+            // streaming together instead of waiting at the gather for the ones
+            // that drew an extra slice or more candidates.  Only the 16-wave
+            // kernel (one workgroup per CU, 128 VGPRs): in the 8-wave kernels
+            // the extra code path made them spill.
+            auto grab = [&]() -> int {
+                int v = 0;
+                if (lane == 0) v = atomicAdd(&bs.next_slice, 1);
+                return __builtin_amdgcn_readfirstlane(v);
+            };
+            int nx = w + kW;  // already loading into bufA
+            while (c < nsl) {
+                if (c != w) {
+                    slice_keys(bufA, lo + c * kSl, hi, largest, key);
+                    nx = grab();
+                    load_slice<VEC, SV>(bufA, rs, nx * kSl);  // past the segment: reads 0, no traffic
+                }
+                if (!filter(lo + c * kSl)) { over = true; break; }
+                c = nx;
             }
         } else {
             for (; c < nsl; c += kW) {
@@ -1947,6 +1972,7 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     a.out_v = static_cast<float*>(out_values);
     a.out_i = static_cast<long long*>(out_indices);
     a.sample = smp ? 1 : 0;
+    a.dyn = knobs().topk_dyn >= 0 ? 1 : 0;
     a.temperature = smp ? smp->temperature : 0.0f;
     a.top_p = smp ? smp->top_p : 1.0f;
     a.u = smp ? smp->u : nullptr;

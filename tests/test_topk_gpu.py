@@ -14,7 +14,7 @@ torch = pytest.importorskip("torch")
 @pytest.fixture(autouse=True)
 def _reset_knobs():
     yield
-    for k in ("topk_fallback", "topk_variant", "topk_waves", "splits", "topk_short", "topk_radix"):
+    for k in ("topk_fallback", "topk_variant", "topk_waves", "splits", "topk_short", "topk_radix", "topk_dyn"):
         _capi.debug_set(k, 0)
 
 
@@ -81,7 +81,10 @@ def test_config3_uniform():
     check(x, x, 64)
 
 
-def test_config5_peaked_logits():
+@pytest.mark.parametrize("dyn", [0, -1])
+def test_config5_peaked_logits(dyn):
+    # dyn=0: the 16-wave kernel hands slices out dynamically; -1: static order
+    _capi.debug_set("topk_dyn", dyn)
     rng = np.random.default_rng(5)
     x = rng.standard_normal((256, 151936), dtype=np.float32) * np.float32(3.0)
     for r in range(256):
@@ -94,7 +97,8 @@ def test_config5_peaked_logits():
 @pytest.mark.parametrize("splits", [0, 1, 2, 3, 5])
 def test_wave_kernel_variants_and_segments(variant, splits, waves):
     # wave-kernel prefetch depths and workgroup sizes, rows cut into 1..5
-    # segments (merge pass)
+    # segments (merge pass); static slice order on odd split counts
+    _capi.debug_set("topk_dyn", -1 if splits % 2 else 0)
     _capi.debug_set("topk_variant", variant)
     _capi.debug_set("topk_waves", waves)
     _capi.debug_set("splits", splits)
