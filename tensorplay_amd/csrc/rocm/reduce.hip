@@ -1727,7 +1727,6 @@ struct WelAccD { double k; long long n; double s1, s2; };
 // Welford over double inputs: per-thread sums shifted by the thread's first
 // element, merged with the same Chan combine as WelfordOp.
 struct F64WelfordOp {
-    static constexpr bool kIndexed = false;
     using Acc = WelAccD;
     using State = WelS;
     using Wide = F64WelfordOp;
