@@ -983,6 +983,66 @@ __device__ __forceinline__ int group_scan(int v, int sl) {
     return v;
 }
 
+// Lane lane ^ M's value: DPP quad permutes for M = 1, 2, ds_swizzle (xor
+// mask inside 32-lane halves) for M = 4 .. 16, ds_bpermute for M = 32.
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+    if constexpr (M == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // [1,0,3,2]
+    else if constexpr (M == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // [2,3,0,1]
+    else if constexpr (M < 32) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (M << 10) | 0x1F);
+    else return (uint32_t)__builtin_amdgcn_ds_bpermute((int)((__lane_id() ^ M) << 2), (int)v);
+}
+
+template <int M, int P>
+__device__ __forceinline__ void sort_lane_stage(unsigned long long (&x)[P], bool keep_max) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const uint32_t lo = xor_lane<M>((uint32_t)x[p]);
+        const uint32_t hi = xor_lane<M>((uint32_t)(x[p] >> 32));
+        const unsigned long long y = ((unsigned long long)hi << 32) | lo;
+        x[p] = ((x[p] > y) == keep_max) ? x[p] : y;
+    }
+}
+
+// Descending bitonic sort of 64 * P composites held P per lane across one
+// wave (lane l holds positions l*P .. l*P+P-1): lane permutes for distances of
+// at least P, compare-exchanges in registers below.
+template <int P>
+__device__ __forceinline__ void wave_sort_desc(unsigned long long (&x)[P]) {
+    const int lane = __lane_id();
+#pragma unroll
+    for (int s = 2; s <= 64 * P; s <<= 1) {
+#pragma unroll
+        for (int d = s >> 1; d >= P; d >>= 1) {
+            const int m = d / P;  // partner lane lane ^ m
+            const bool keep_max = ((lane & m) == 0) == (((lane * P) & s) == 0);
+            switch (m) {
+                case 1: sort_lane_stage<1, P>(x, keep_max); break;
+                case 2: sort_lane_stage<2, P>(x, keep_max); break;
+                case 4: sort_lane_stage<4, P>(x, keep_max); break;
+                case 8: sort_lane_stage<8, P>(x, keep_max); break;
+                case 16: sort_lane_stage<16, P>(x, keep_max); break;
+                default: sort_lane_stage<32, P>(x, keep_max); break;
+            }
+        }
+#pragma unroll
+        for (int dd = P / 2; dd >= 1; dd >>= 1) {
+            if (dd < s) {
+#pragma unroll
+                for (int q = 0; q < P; ++q) {
+                    if ((q & dd) == 0) {
+                        const bool desc = ((lane * P + q) & s) == 0;
+                        const unsigned long long u = x[q], v = x[q + dd];
+                        const bool sw = (u > v) != desc;
+                        x[q] = sw ? v : u;
+                        x[q + dd] = sw ? u : v;
+                    }
+                }
+            }
+        }
+    }
+}
+
 // Bitonic sort (ascending) of the values m held by the L lanes of each group:
 // lane sl of the group returns the sl-th smallest.
 template <int L>
@@ -1042,6 +1102,14 @@ __device__ __forceinline__ uint32_t group_hist_threshold(const uint32_t* hist, i
         tn = T + ((uint32_t)(sl * NB + b) << shift);
     }
     return __shfl(tn, grp * L + hl, 64);
+}
+
+// Output r of a row: the value (exact, from the key or the input) and index.
+__device__ __forceinline__ void write_ranked(const TopkArgs& a, long long row, int k, const float* p, int largest,
+                                             int r, unsigned long long c) {
+    const uint32_t idx = comp_index(c);
+    a.out_v[row * k + r] = selected_value(p, (uint32_t)(c >> 32), idx, largest);
+    a.out_i[row * k + r] = (long long)idx;
 }
 
 template <int L, int E4, bool VEC, bool LG>
@@ -1207,6 +1275,22 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
         c = k;
     }
     wave_sync_lds();
+    if (L == 64 && c > 36 && c <= 128) {
+        // Few candidates per lane: a lane sort of 64 or 128 composites costs
+        // fewer instructions than c compares per candidate.  Lane sl ends with
+        // sorted positions sl*P .. sl*P+P-1.
+        if (c <= 64) {
+            unsigned long long x[1] = {sl < c ? list[sl] : 0ull};
+            wave_sort_desc<1>(x);
+            if (sl < k && live) write_ranked(a, row, k, p, largest, sl, x[0]);
+        } else {
+            unsigned long long x[2] = {2 * sl < c ? list[2 * sl] : 0ull, 2 * sl + 1 < c ? list[2 * sl + 1] : 0ull};
+            wave_sort_desc<2>(x);
+            if (2 * sl < k && live) write_ranked(a, row, k, p, largest, 2 * sl, x[0]);
+            if (2 * sl + 1 < k && live) write_ranked(a, row, k, p, largest, 2 * sl + 1, x[1]);
+        }
+        return;
+    }
     for (int i = sl; i < c; i += L) {
         const unsigned long long ci = list[i];
         int r = 0;
@@ -1488,27 +1572,6 @@ __device__ int block_prefix_excl(int v, int* wtot, int& total) {
     }
     __syncthreads();
     return before + inc - v;
-}
-
-// Lane lane ^ M's value: DPP quad permutes for M = 1, 2, ds_swizzle (xor
-// mask inside 32-lane halves) for M = 4 .. 16, ds_bpermute for M = 32.
-template <int M>
-__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
-    if constexpr (M == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // [1,0,3,2]
-    else if constexpr (M == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // [2,3,0,1]
-    else if constexpr (M < 32) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (M << 10) | 0x1F);
-    else return (uint32_t)__builtin_amdgcn_ds_bpermute((int)((__lane_id() ^ M) << 2), (int)v);
-}
-
-template <int M, int P>
-__device__ __forceinline__ void sort_lane_stage(unsigned long long (&x)[P], bool keep_max) {
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-        const uint32_t lo = xor_lane<M>((uint32_t)x[p]);
-        const uint32_t hi = xor_lane<M>((uint32_t)(x[p] >> 32));
-        const unsigned long long y = ((unsigned long long)hi << 32) | lo;
-        x[p] = ((x[p] > y) == keep_max) ? x[p] : y;
-    }
 }
 
 // Descending bitonic sort of n composites (n / P threads, a multiple of 64,

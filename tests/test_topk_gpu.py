@@ -210,6 +210,13 @@ def test_short_rows_many():
     check(x, x, 8)
     y = rng.standard_normal((16384, 1024)).astype(np.float32)
     check(y, y, 32)
+    # 64-lane rows whose candidates (37..128 after the bound) are ranked by a
+    # lane sort of one or two composites per lane instead of compares
+    for rows, cols, k in ((2048, 1024, 48), (1024, 2048, 64), (4096, 512, 40), (2048, 1024, 37)):
+        z = rng.standard_normal((rows, cols)).astype(np.float32)
+        z[::5] = np.round(z[::5] * 4) / 4  # ties among the candidates
+        check(z, z, k, True)
+        check(z, z, k, False)
 
 
 @pytest.mark.parametrize("force", [0, 1, 2])
