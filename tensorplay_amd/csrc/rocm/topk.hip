@@ -27,8 +27,9 @@
 //     select over its segment in global memory, then an index-ordered gather
 //     takes every larger key plus the lowest-index elements equal to the k-th.
 // Two variants of the segment kernel:
-//   k_topk_wave  (k <= 128, segments >= 8192): every wave streams its own
-//     1024-element slices (w, w+8, ...) into a wave-private list with no
+//   k_topk_wave  (k <= 128, segments >= 8192, or >= 4096 with 4-wave
+//     workgroups): every wave streams its own 1024-element slices (w, w+NW,
+//     ...) into a wave-private list with no
 //     workgroup barrier in the loop, so one wave's filtering overlaps the other
 //     waves' loads.  Waves share a monotone threshold through an LDS atomicMax;
 //     a published value always has >= k candidates at or above it in the
@@ -1847,11 +1848,26 @@ struct TopkPlan {
 // only when rows < CUs.  Every segment holds >= k elements (and, for the wave
 // kernel, a full first slice per wave), and the merge list fits one merge
 // workgroup.
+// Many rows of 4096 .. 16383 elements: 4-wave (256-thread) workgroups of the
+// wave kernel, so each wave streams two or more slices and a CU holds eight
+// rows.  Measured on MI355X (us, 8-wave wave kernel / workgroup kernels ->
+// 4 waves): [4096, 4096] k = 64 47.7 -> 29.2, [4096, 6000] k = 16 41.5 -> 26.0,
+// k = 100 105 -> 50, [4096, 8192] k = 64 44.0 -> 37.0, [2048, 12288] k = 64
+// 31.6 -> 26.6; [2048, 16384] even (32.7 / 32.0) and [512, 8192] slower (11.1 /
+// 12.0), so rows >= 4 per CU and rows shorter than 16384.  topk_waves = 4
+// (debug knob) forces it on every row of >= 4096 elements.
+bool wave4(long long rows, long long cols, long long k) {
+    if (k > kWaveK || cols < 4 * kSlice) return false;
+    if (knobs().topk_waves != 0) return knobs().topk_waves == 4;
+    return cols < 2 * kWaveMinSeg && rows >= 4LL * device_info().cus;
+}
+
 TopkPlan plan_topk(long long rows, long long cols, long long k) {
     TopkPlan pl{1, (int)cols, false, 8, 0};
     const int cus = device_info().cus;
-    const bool wave_ok = k <= kWaveK && cols >= kWaveMinSeg;
-    const int nw = (wave_ok && rows < 2LL * cus && cols >= 2 * kWaveMinSeg) ? 16 : 8;
+    const bool w4 = wave4(rows, cols, k);
+    const bool wave_ok = k <= kWaveK && (cols >= kWaveMinSeg || w4);
+    const int nw = w4 ? 4 : (wave_ok && rows < 2LL * cus && cols >= 2 * kWaveMinSeg) ? 16 : 8;
     const long long unit = wave_ok ? (long long)nw * kSlice : kCH;
     const long long units = (cols + unit - 1) / unit;
     const long long want = (nw == 16) ? cus : 2LL * cus;
@@ -1893,13 +1909,14 @@ int dtype_size(int32_t dtype) {
 }
 
 // Large k takes the radix-select kernel (any k <= cols, any dtype); so does
-// k > 128, k > 64 on rows shorter than the wave kernel's minimum segment, and
-// every input dtype but float32.
-bool radix_route(long long cols, long long k, int32_t dtype = TPR_FLOAT32) {
+// k > 128, k > 64 on rows shorter than the wave kernel's minimum segment
+// (8192, or 4096 where wave4 picks 4-wave workgroups), and every input dtype
+// but float32.
+bool radix_route(long long rows, long long cols, long long k, int32_t dtype = TPR_FLOAT32) {
     if (k > kKMax || dtype != TPR_FLOAT32) return true;
     if (knobs().topk_radix < 0 || knobs().topk_fallback) return false;
     if (knobs().topk_radix > 0) return true;
-    return k > kWaveK || (k > kShortMaxK && cols < kWaveMinSeg);
+    return k > kWaveK || (k > kShortMaxK && cols < kWaveMinSeg && !wave4(rows, cols, k));
 }
 
 // Rows the register-resident kernel takes (elements of <= 4 bytes, rows of
@@ -1925,7 +1942,7 @@ extern "C" {
 
 size_t tpr_topk_workspace_bytes(int32_t dtype, int64_t rows, int64_t cols, int64_t k) {
     if (rows <= 0 || cols <= 0 || k <= 0 || k > cols || cols > 0x7fffffffLL || tpr::dtype_size(dtype) == 0) return 0;
-    if (tpr::radix_route(cols, k, dtype)) return tpr::radix_ws(rows, cols, k, dtype);
+    if (tpr::radix_route(rows, cols, k, dtype)) return tpr::radix_ws(rows, cols, k, dtype);
     return tpr::plan_topk(rows, cols, k).ws;
 }
 
@@ -2016,7 +2033,7 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     if (cols > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: rows longer than 2^31-1");
     if (!in || (!smp && (!out_values || !out_indices))) return fail(TPR_ERR_INVALID_ARG, "tpr_topk: null pointer");
     if (rows > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: more than 2^31-1 rows");
-    const bool radix = radix_route(cols, k, dtype);
+    const bool radix = radix_route(rows, cols, k, dtype);
     const TopkPlan pl = radix ? TopkPlan{1, (int)cols, false, 8, radix_ws(rows, cols, k, dtype)} : plan_topk(rows, cols, k);
     if (rows * (long long)pl.nseg > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: grid too large");
     if (pl.ws > 0 && (workspace == nullptr || workspace_bytes < pl.ws))
@@ -2082,6 +2099,10 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
             else if (var == 1) hipLaunchKernelGGL((k_topk_wave<true, 4, 4, 0, 16>), dim3(grid), blk, 0, st, a);
             else if (var == 3) hipLaunchKernelGGL((k_topk_wave<true, 4, 4, 2, 16>), dim3(grid), blk, 0, st, a);
             else hipLaunchKernelGGL((k_topk_wave<true, 4, 4, 1, 16>), dim3(grid), blk, 0, st, a);
+        } else if (pl.nw == 4) {
+            if (!vec) hipLaunchKernelGGL((k_topk_wave<false, 4, 8, 0, 4>), dim3(grid), blk, 0, st, a);
+            else if (var == 2) hipLaunchKernelGGL((k_topk_wave<true, 4, 6, 1, 4>), dim3(grid), blk, 0, st, a);
+            else hipLaunchKernelGGL((k_topk_wave<true, 4, 8, 0, 4>), dim3(grid), blk, 0, st, a);
         } else {
             if (!vec) hipLaunchKernelGGL((k_topk_wave<false, 4, 6, 1, 8>), dim3(grid), blk, 0, st, a);
             else if (var == 1) hipLaunchKernelGGL((k_topk_wave<true, 4, 8, 0, 8>), dim3(grid), blk, 0, st, a);

@@ -92,7 +92,7 @@ def test_config5_peaked_logits(dyn):
     check(x, x, 50)
 
 
-@pytest.mark.parametrize("waves", [8, 16])
+@pytest.mark.parametrize("waves", [4, 8, 16])
 @pytest.mark.parametrize("variant", [1, 2, 3])
 @pytest.mark.parametrize("splits", [0, 1, 2, 3, 5])
 def test_wave_kernel_variants_and_segments(variant, splits, waves):
@@ -111,7 +111,7 @@ def test_wave_kernel_variants_and_segments(variant, splits, waves):
             check(x, x, k, largest)
 
 
-@pytest.mark.parametrize("waves", [8, 16])
+@pytest.mark.parametrize("waves", [4, 8, 16])
 @pytest.mark.parametrize("variant", [1, 2, 3])
 def test_rising_rows_stale_candidates(variant, waves):
     # Values trend upwards along the row, so every wave keeps finding better
@@ -129,7 +129,7 @@ def test_rising_rows_stale_candidates(variant, waves):
         check(x, x, k, False)
 
 
-@pytest.mark.parametrize("waves", [8, 16])
+@pytest.mark.parametrize("waves", [4, 8, 16])
 @pytest.mark.parametrize("variant", [1, 2, 3])
 def test_single_row_ragged_end(variant, waves):
     # one aligned row whose length is not a multiple of 4: the last 128-bit
@@ -146,7 +146,7 @@ def test_single_row_ragged_end(variant, waves):
             check(x, x, k, False)
 
 
-@pytest.mark.parametrize("waves", [8, 16])
+@pytest.mark.parametrize("waves", [4, 8, 16])
 def test_denormals_signed_zeros_and_infinities(waves):
     # Thresholds that land on +-0, denormals and +-inf: the float-domain filter
     # must agree with the key order (denormals kept, -0.0 == +0.0).
@@ -217,6 +217,24 @@ def test_short_rows_many():
         z[::5] = np.round(z[::5] * 4) / 4  # ties among the candidates
         check(z, z, k, True)
         check(z, z, k, False)
+
+
+def test_mid_rows_four_wave_workgroups():
+    # >= 4 rows per CU of 4096 .. 16383 elements take 4-wave workgroups of the
+    # wave kernel (k <= 128; also k of 65..128 below 8192 elements, which
+    # otherwise go to the radix select); adversarial rows take its exact path
+    rng = np.random.default_rng(31)
+    x = rng.uniform(-1, 1, (1100, 6000)).astype(np.float32)
+    x[3] = 2.0                               # all equal: list overflow -> exact path
+    x[5] = np.round(x[5] * 3) / 3            # heavy ties
+    x[7, ::11] = np.nan
+    x[9] = np.where(rng.random(6000) < 0.5, np.float32(0.0), np.float32(-0.0))
+    for k in (1, 16, 64, 100, 128):
+        check(x, x, k, True)
+        check(x, x, k, False)
+    y = rng.standard_normal((1024, 12289)).astype(np.float32)
+    check(y, y, 50)
+    check(y, y[:, 1:12289], 64)              # misaligned rows: scalar loads
 
 
 @pytest.mark.parametrize("force", [0, 1, 2])
