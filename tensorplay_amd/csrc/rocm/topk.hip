@@ -1854,12 +1854,14 @@ struct TopkPlan {
 // 4 waves): [4096, 4096] k = 64 47.7 -> 29.2, [4096, 6000] k = 16 41.5 -> 26.0,
 // k = 100 105 -> 50, [4096, 8192] k = 64 44.0 -> 37.0, [2048, 12288] k = 64
 // 31.6 -> 26.6; [2048, 16384] even (32.7 / 32.0) and [512, 8192] slower (11.1 /
-// 12.0), so rows >= 4 per CU and rows shorter than 16384.  topk_waves = 4
-// (debug knob) forces it on every row of >= 4096 elements.
+// 12.0), so rows >= 4 per CU and rows shorter than 16384.  Rows of exactly
+// 4096 with k > 32 take it at any row count: the lane-group kernel, which
+// could hold them, is slow there ([512, 4096] k = 64 33 us against 10).
+// topk_waves = 4 (debug knob) forces it on every row of >= 4096 elements.
 bool wave4(long long rows, long long cols, long long k) {
     if (k > kWaveK || cols < 4 * kSlice) return false;
     if (knobs().topk_waves != 0) return knobs().topk_waves == 4;
-    return cols < 2 * kWaveMinSeg && rows >= 4LL * device_info().cus;
+    return cols < 2 * kWaveMinSeg && (rows >= 4LL * device_info().cus || (cols <= kShortMaxCols && k > 32));
 }
 
 TopkPlan plan_topk(long long rows, long long cols, long long k) {
@@ -2077,12 +2079,15 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
         }
         return check_launch("k_topk_radix");
     }
-    // Rows of more than 2048 elements with k > 32 leave the lane-group kernel
-    // too many candidates per lane: the wave kernel is faster there (MI355X,
-    // [4096, 4096] k = 64: 48.5 us against 53.5 us).
+    // Rows of 4096 elements with k > 32 go to the 4-wave wave kernel instead
+    // (MI355X, [16384, 4096] k = 64: 98 us against 117; [2048, 4096]: 18
+    // against 37);
+    // every other row the lane-group kernel can hold is faster there than in
+    // the workgroup kernel ([16384, 3000] k = 64: 124 against 181 us;
+    // [8192, 2500] k = 40: 38 against 77 us).
     // (The lane-group kernel addresses up to 4 rows per wave with 32-bit offsets.)
     const bool short_ok = k <= kShortMaxK && cols <= kShortMaxCols && 3 * row_stride + cols < (1LL << 29);
-    const bool short_fit = short_ok && (cols <= 2048 || k <= 32);
+    const bool short_fit = short_ok && (cols <= 2048 || k <= 32 || !wave4(rows, cols, k));
     if (!smp && (short_fit || (knobs().topk_short > 0 && short_ok)) &&
         knobs().topk_short >= 0 && knobs().topk_fallback == 0 && knobs().splits <= 0)
         return launch_short(a, vec, st);
