@@ -56,7 +56,7 @@ constexpr int kCH = kT * 4 * kV; // elements per block-kernel chunk (8192)
 constexpr int kB = 2048;         // block candidate list capacity
 constexpr int kKMax = 1024;      // largest k of the segment kernels (larger k: k_topk_radix)
 constexpr int kMergeT = 256;     // merge workgroup
-constexpr int kMergeMax = 4096;  // candidates a merge workgroup ranks (nseg * k)
+constexpr int kMergeMax = 8192;  // candidates a merge workgroup ranks (nseg * k)
 
 constexpr int kWaveK = 128;                   // largest k of the wave kernel
 constexpr int kWB = 256;                      // per-wave list capacity
@@ -1663,9 +1663,15 @@ __global__ __launch_bounds__(NT) void k_topk_rsel(TopkArgs a, int dtype, int sor
     constexpr int BPT = kRadixBins / NT;
     __shared__ RselShared<NT, P> sh;
     const int tid = threadIdx.x;
-    const long long row = blockIdx.x;
-    const int cols = a.cols, k = a.k;
-    const char* base = reinterpret_cast<const char*>(a.in) + row * a.row_stride * dtype_bytes(dtype);
+    // nseg > 1: the row is cut into segments of seg_len elements, one
+    // workgroup each, whose k winners (sorted composites with row indices) go
+    // to the merge pass
+    const long long row = blockIdx.x / a.nseg;
+    const int seg = (int)(blockIdx.x % a.nseg);
+    const int lo = seg * a.seg_len;
+    const int cols = min(a.cols - lo, a.seg_len), k = a.k;
+    const char* rowbase = reinterpret_cast<const char*>(a.in) + row * a.row_stride * dtype_bytes(dtype);
+    const char* base = rowbase + (long long)lo * dtype_bytes(dtype);
     uint32_t key[EPT];
     switch (dtype) {
         case TPR_FLOAT32: rsel_load<float, NT, EPT>(key, base, cols, a.largest); break;
@@ -1766,7 +1772,7 @@ __global__ __launch_bounds__(NT) void k_topk_rsel(TopkArgs a, int dtype, int sor
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
             if ((take >> j) & 1u) {
-                if (pos >= r0 && pos < r0 + RND) sh.buf[pos - r0] = CP::make(key[j], (uint32_t)(j * NT + tid));
+                if (pos >= r0 && pos < r0 + RND) sh.buf[pos - r0] = CP::make(key[j], (uint32_t)(lo + j * NT + tid));
                 ++pos;
             }
         }
@@ -1780,6 +1786,13 @@ __global__ __launch_bounds__(NT) void k_topk_rsel(TopkArgs a, int dtype, int sor
         __syncthreads();
     }
     reg_sort_desc<NT, P>(x, sh.buf, sort_n);
+    if (a.nseg > 1) {
+        unsigned long long* dst = a.part + ((long long)row * a.nseg + seg) * k;
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+            if (tid * P + p < k) dst[tid * P + p] = x[p];
+        return;
+    }
     if (dtype == TPR_FLOAT32 && a.sample) {
         const int first = tid * P;
 #pragma unroll
@@ -1806,22 +1819,104 @@ __global__ __launch_bounds__(NT) void k_topk_rsel(TopkArgs a, int dtype, int sor
     }
 }
 
+// Candidate lists longer than this are cut to the k winners by a radix select
+// before ranking (the O(m^2) ranking of 4096 candidates took ~0.9 ms).
+constexpr int kMergeRankMax = 512;
+
 struct MergeShared {
-    unsigned long long cand[kMergeMax];
-    int rank[kMergeMax];
+    unsigned long long cand[kMergeMax];  // also the sort's exchange buffer and rank_select's counts afterwards
+    union {
+        int rank[kMergeRankMax];
+        uint32_t hist[kRadixBins];
+    };
+    unsigned long long surv[kKMax];  // the k winners before ranking
     unsigned long long sel[kKMax];
+    int wtot[kMergeT / 64];
+    int digit, kk, cls, count;
 };
 
-// Pass 2: exact top k of a row's nseg * k segment winners.
-__global__ __launch_bounds__(kMergeT) void k_topk_merge(TopkArgs a) {
+// Pass 2: exact top k of a row's nseg * k segment winners (float32 from the
+// wave / workgroup kernels, any dtype of <= 4 bytes from k_topk_rsel).
+__global__ __launch_bounds__(kMergeT) void k_topk_merge(TopkArgs a, int dtype) {
     __shared__ MergeShared sh;
     const long long row = blockIdx.x;
     const int k = a.k;
     const int m = a.nseg * k;
+    const int tid = threadIdx.x;
     const unsigned long long* src = a.part + row * (long long)m;
-    for (int i = threadIdx.x; i < m; i += kMergeT) sh.cand[i] = src[i];
+    for (int i = tid; i < m; i += kMergeT) sh.cand[i] = src[i];
     __syncthreads();
-    rank_select<kMergeT>(sh.cand, sh.rank, sh.sel, m, k);
+    if (m <= kMergeRankMax) {
+        rank_select<kMergeT>(sh.cand, sh.rank, sh.sel, m, k);
+    } else {
+        // The composites are distinct, so the k-th largest is found exactly by
+        // radix passes over all 64 bits, 11 per pass (2048-bin LDS histogram of
+        // the composites matching the digits found so far), stopping once the
+        // class sharing the found prefix is exactly the number still wanted.
+        constexpr int BPT = kRadixBins / kMergeT;
+        unsigned long long prefix = 0, pmask = 0;
+        int kk = k;
+        bool whole = false;
+        for (int hi = 64; hi > 0 && !whole; hi -= 11) {
+            const int shift = hi > 11 ? hi - 11 : 0;
+            const unsigned long long dmask = (1ull << (hi - shift)) - 1ull;
+#pragma unroll
+            for (int b = 0; b < BPT; ++b) sh.hist[tid * BPT + b] = 0u;
+            __syncthreads();
+            for (int i = tid; i < m; i += kMergeT) {
+                const unsigned long long c = sh.cand[i];
+                if ((c & pmask) == prefix) atomicAdd(&sh.hist[(uint32_t)((c >> shift) & dmask)], 1u);
+            }
+            __syncthreads();
+            uint32_t h[BPT];
+            int own = 0;
+#pragma unroll
+            for (int b = 0; b < BPT; ++b) {
+                h[b] = sh.hist[tid * BPT + b];
+                own += (int)h[b];
+            }
+            const int suf = block_suffix_incl<kMergeT>(own, sh.wtot);
+            if (suf >= kk && suf - own < kk) {
+                int cum = suf - own;
+                int b = BPT - 1;
+                for (; b > 0; --b) {
+                    if (cum + (int)h[b] >= kk) break;
+                    cum += (int)h[b];
+                }
+                sh.digit = tid * BPT + b;
+                sh.kk = kk - cum;
+                sh.cls = (int)h[b];
+            }
+            if (tid == 0) sh.count = 0;
+            __syncthreads();
+            prefix |= (unsigned long long)sh.digit << shift;
+            pmask |= dmask << shift;
+            kk = sh.kk;
+            whole = sh.cls == kk;
+            __syncthreads();
+        }
+        // every composite above the class plus the whole class: exactly k
+        for (int i = tid; i < m; i += kMergeT) {
+            const unsigned long long c = sh.cand[i];
+            if ((c & pmask) >= prefix) sh.surv[atomicAdd(&sh.count, 1)] = c;
+        }
+        __syncthreads();
+        if (k <= 128) {
+            rank_select<kMergeT>(sh.surv, reinterpret_cast<int*>(sh.cand), sh.sel, k, k);
+        } else {
+            // k of 129..1024: bitonic sort, 4 composites per thread, padded with
+            // zeros (below every element) to a power of two
+            const int n = pow2_at_least(k);
+            unsigned long long x[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) x[q] = (tid * 4 + q < k) ? sh.surv[tid * 4 + q] : 0ull;
+            reg_sort_desc<kMergeT, 4>(x, sh.cand, n);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (tid * 4 + q < k) sh.sel[tid * 4 + q] = x[q];
+            __syncthreads();
+        }
+    }
     const float* p = a.in + row * a.row_stride;
     if (a.sample) {
         if (threadIdx.x < 64) sample_from_sel(a, row, p, sh.sel, k);
@@ -1829,8 +1924,17 @@ __global__ __launch_bounds__(kMergeT) void k_topk_merge(TopkArgs a) {
     }
     for (int i = threadIdx.x; i < k; i += kMergeT) {
         const uint32_t idx = comp_index(sh.sel[i]);
-        a.out_v[row * k + i] = selected_value(p, (uint32_t)(sh.sel[i] >> 32), idx, a.largest);
         a.out_i[row * k + i] = (long long)idx;
+        if (dtype == TPR_FLOAT32) {
+            a.out_v[row * k + i] = selected_value(p, (uint32_t)(sh.sel[i] >> 32), idx, a.largest);
+        } else {
+            const char* rb = reinterpret_cast<const char*>(a.in) + row * a.row_stride * dtype_bytes(dtype);
+            switch (dtype_bytes(dtype)) {
+                case 4: reinterpret_cast<uint32_t*>(a.out_v)[row * k + i] = reinterpret_cast<const uint32_t*>(rb)[idx]; break;
+                case 2: reinterpret_cast<uint16_t*>(a.out_v)[row * k + i] = reinterpret_cast<const uint16_t*>(rb)[idx]; break;
+                default: reinterpret_cast<uint8_t*>(a.out_v)[row * k + i] = reinterpret_cast<const uint8_t*>(rb)[idx]; break;
+            }
+        }
     }
 }
 
@@ -1927,10 +2031,24 @@ bool rsel_route(long long cols, int32_t dtype) {
     return dtype_size(dtype) <= 4 && cols <= kRselMaxCols && knobs().topk_radix != 2;
 }
 
+// Longer rows of elements of <= 4 bytes with k <= 1024 and at most kMergeMax
+// segment winners (vocabulary-sized rows: 151936 with k <= 1024): segments of
+// <= 32768 elements through k_topk_rsel, one workgroup each, then the merge
+// pass.  Returns the segment count, 0 when the streaming kernel takes the row.
+// Measured on MI355X against the streaming k_topk_radix (one workgroup per
+// row): [256, 151936] k = 256 1018 us, k = 1000 1053 us; [16, 500000] k = 256
+// 1959 us (the figures after are in the design notes).
+int rsel_segments(long long cols, long long k, int32_t dtype) {
+    if (dtype_size(dtype) > 4 || cols <= kRselMaxCols || k > kKMax || knobs().topk_radix == 2) return 0;
+    const long long nseg = (cols + kRselMaxCols - 1) / kRselMaxCols;
+    return nseg * k <= kMergeMax ? (int)nseg : 0;
+}
+
 // Workspace of the streaming radix kernel: composites sorted outside LDS (8
 // bytes each for elements of at most 4 bytes, 16 for 8-byte elements).
 size_t radix_ws(long long rows, long long cols, long long k, int32_t dtype = TPR_FLOAT32) {
     if (rsel_route(cols, dtype)) return 0;
+    if (const int ns = rsel_segments(cols, k, dtype)) return (size_t)rows * ns * k * sizeof(unsigned long long);
     const long long n2 = pow2_at_least((int)k);
     const bool wide = dtype_size(dtype) == 8;
     const long long lds = wide ? 2048 : kRadixLds;
@@ -2000,7 +2118,7 @@ template <int NT, int EPT>
 int launch_rsel_p(const TopkArgs& a, int32_t dtype, hipStream_t st) {
     const int n = std::max(64, pow2_at_least(a.k));
     const int P = std::min(n / 64, std::max(4, n / NT));
-    const dim3 g((unsigned)a.rows), b(NT);
+    const dim3 g((unsigned)(a.rows * a.nseg)), b(NT);
     if (P == 1) hipLaunchKernelGGL((k_topk_rsel<NT, EPT, 1>), g, b, 0, st, a, (int)dtype, n);
     else if (P == 2) hipLaunchKernelGGL((k_topk_rsel<NT, EPT, 2>), g, b, 0, st, a, (int)dtype, n);
     else if (P == 4) hipLaunchKernelGGL((k_topk_rsel<NT, EPT, 4>), g, b, 0, st, a, (int)dtype, n);
@@ -2014,11 +2132,12 @@ int launch_rsel_p(const TopkArgs& a, int32_t dtype, hipStream_t st) {
 // Workgroup size and keys per thread by row length: NT * EPT >= cols, so
 // pow2(k) / NT <= EPT.
 int launch_rsel(const TopkArgs& a, int32_t dtype, hipStream_t st) {
-    if (a.cols <= 1024) return launch_rsel_p<256, 4>(a, dtype, st);
-    if (a.cols <= 2048) return launch_rsel_p<256, 8>(a, dtype, st);
-    if (a.cols <= 4096) return launch_rsel_p<256, 16>(a, dtype, st);
-    if (a.cols <= 8192) return launch_rsel_p<512, 16>(a, dtype, st);
-    if (a.cols <= 16384) return launch_rsel_p<1024, 16>(a, dtype, st);
+    const int c = a.nseg > 1 ? a.seg_len : a.cols;  // elements per workgroup
+    if (c <= 1024) return launch_rsel_p<256, 4>(a, dtype, st);
+    if (c <= 2048) return launch_rsel_p<256, 8>(a, dtype, st);
+    if (c <= 4096) return launch_rsel_p<256, 16>(a, dtype, st);
+    if (c <= 8192) return launch_rsel_p<512, 16>(a, dtype, st);
+    if (c <= 16384) return launch_rsel_p<1024, 16>(a, dtype, st);
     return launch_rsel_p<1024, 32>(a, dtype, st);
 }
 
@@ -2063,6 +2182,15 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (radix && rsel_route(cols, dtype))
         return launch_rsel(a, dtype, st);
+    if (const int ns = radix ? rsel_segments(cols, k, dtype) : 0) {
+        if (rows * (long long)ns > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: grid too large");
+        a.nseg = ns;
+        a.seg_len = (int)((cols + ns - 1) / ns);
+        const int rc = launch_rsel(a, dtype, st);
+        if (rc != TPR_OK) return rc;
+        hipLaunchKernelGGL(k_topk_merge, dim3((unsigned)rows), dim3(kMergeT), 0, st, a, (int)dtype);
+        return check_launch("k_topk_merge");
+    }
     if (radix) {
         const dim3 g((unsigned)rows), b(kRadixT);
         switch (dtype) {
@@ -2120,7 +2248,7 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     }
     int rc = check_launch("k_topk_seg");
     if (rc != TPR_OK || pl.nseg == 1) return rc;
-    hipLaunchKernelGGL(k_topk_merge, dim3(rows), dim3(kMergeT), 0, st, a);
+    hipLaunchKernelGGL(k_topk_merge, dim3(rows), dim3(kMergeT), 0, st, a, (int)dtype);
     return check_launch("k_topk_merge");
 }
 }  // namespace

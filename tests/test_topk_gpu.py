@@ -219,6 +219,38 @@ def test_short_rows_many():
         check(z, z, k, False)
 
 
+def test_few_long_rows_many_segments():
+    # A few very long rows are cut into up to 4096 / k segments; the merge
+    # pass radix-selects the k winners among nseg * k candidates (> 512) before
+    # ranking them.  Ties across segments, NaN, and winners in the last segment.
+    rng = np.random.default_rng(32)
+    x = rng.standard_normal((2, 3_000_000)).astype(np.float32)
+    x[1] = np.round(x[1] * 2) / 2            # heavy ties across every segment
+    x[0, -5:] = 50.0                         # top values in the last segment
+    x[0, 17] = np.nan
+    for k in (5, 64, 128, 1000):
+        check(x, x, k, True)
+        check(x, x, k, False)
+    y = rng.uniform(-1, 1, (8, 1_000_000)).astype(np.float32)
+    check(y, y, 50)
+
+
+def test_long_rows_large_k_segments():
+    # rows longer than 32768 with k of 129..1024: segments of <= 32768 through
+    # the register radix select, winners merged (radix select over the
+    # nseg * k composites, then a bitonic sort of the k)
+    rng = np.random.default_rng(33)
+    x = (rng.standard_normal((5, 151936)) * 3).astype(np.float32)
+    x[1] = np.round(x[1])                    # heavy ties across segments
+    x[2, ::13] = np.nan
+    x[3] = 1.0                               # all equal: the lowest indices
+    x[4, -300:] = 40.0                       # winners in the last segment
+    for k in (129, 256, 1000, 1024):
+        check(x, x, k, True)
+        check(x, x, k, False)
+    check(x, x[:, 1:100001], 700)            # misaligned rows
+
+
 def test_mid_rows_four_wave_workgroups():
     # >= 4 rows per CU of 4096 .. 16383 elements take 4-wave workgroups of the
     # wave kernel (k <= 128; also k of 65..128 below 8192 elements, which
@@ -312,9 +344,9 @@ def test_other_dtypes(dt):
     t = torch.from_numpy(x).cuda()
     cases = [(t, x, k) for k in (1, 10, 64, 1000, cols)]
     if np.dtype(dt).itemsize <= 4:  # longer rows: 1024-thread workgroups (and the streaming kernel beyond 32768)
-        for n in (20000, 40000):
+        for n in (20000, 40000, 100000):
             y = np.concatenate([x[:3]] * (n // cols + 1), axis=1)[:, :n].copy()
-            cases += [(torch.from_numpy(y).cuda(), y, k) for k in (100, 5000)]
+            cases += [(torch.from_numpy(y).cuda(), y, k) for k in ((100, 300, 5000) if n == 100000 else (100, 5000))]
     for t, x, k in cases:
         for largest in (True, False):
             print(f"case topk dtype={np.dtype(dt).name} shape={x.shape} k={k} largest={largest}", flush=True)
