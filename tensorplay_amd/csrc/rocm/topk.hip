@@ -1647,12 +1647,40 @@ struct RselShared {
     int digit, kk, cls;
 };
 
+// Element of the row held in register j of thread t: groups of four
+// consecutive elements, group g = j / 4 of thread t at element 4 * (g * NT + t),
+// so 4-byte elements load as one 128-bit vector per group.
+template <int NT>
+__device__ __forceinline__ int rsel_idx(int j, int t) {
+    return ((j >> 2) * NT + t) * 4 + (j & 3);
+}
+
 template <class T, int NT, int EPT>
 __device__ __forceinline__ void rsel_load(uint32_t (&key)[EPT], const void* base, int cols, int largest) {
+    static_assert(EPT % 4 == 0, "groups of four");
     const T* p = static_cast<const T*>(base);
+    const int t = (int)threadIdx.x;
+    if constexpr (sizeof(T) == 4) {
+        if ((reinterpret_cast<uintptr_t>(base) & 15u) == 0) {
+            // past the row end the buffer range check returns zeros (masked below)
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                                                                 cols * 4, kBufWord3);
+#pragma unroll
+            for (int g = 0; g < EPT / 4; ++g) {
+                const f32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, (g * NT + t) * 16, 0, kNT);
+                const float f[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int e = (g * NT + t) * 4 + q;
+                    key[4 * g + q] = e < cols ? (uint32_t)SortKey<T>::of(__builtin_bit_cast(T, f[q]), largest) : 0u;
+                }
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
-        const int e = j * NT + (int)threadIdx.x;
+        const int e = rsel_idx<NT>(j, t);
         key[j] = e < cols ? (uint32_t)SortKey<T>::of(p[e], largest) : 0u;
     }
 }
@@ -1694,7 +1722,7 @@ __global__ __launch_bounds__(NT) void k_topk_rsel(TopkArgs a, int dtype, int sor
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < EPT; ++j)
-            if (j * NT + tid < cols && (key[j] & pmask) == prefix) atomicAdd(&sh.hist[(key[j] >> shift) & dmask], 1u);
+            if (rsel_idx<NT>(j, tid) < cols && (key[j] & pmask) == prefix) atomicAdd(&sh.hist[(key[j] >> shift) & dmask], 1u);
         __syncthreads();
         uint32_t h[BPT];
         int own = 0;
@@ -1728,7 +1756,7 @@ __global__ __launch_bounds__(NT) void k_topk_rsel(TopkArgs a, int dtype, int sor
     int nt = 0;
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
-        const bool v = j * NT + tid < cols;
+        const bool v = rsel_idx<NT>(j, tid) < cols;
         const uint32_t hk = key[j] & pmask;
         const bool s = v && (hk > prefix || (whole && hk == prefix));
         take |= (uint32_t)s << j;
@@ -1737,24 +1765,25 @@ __global__ __launch_bounds__(NT) void k_topk_rsel(TopkArgs a, int dtype, int sor
     if (!whole) {
         uint32_t eqm = 0;  // bit j: key[j] is in the class (equal to the k-th key)
 #pragma unroll
-        for (int j = 0; j < EPT; ++j) eqm |= (uint32_t)(j * NT + tid < cols && key[j] == prefix) << j;
-        int run = 0;  // class members in element groups before j
-        const int w = tid / 64;
+        for (int j = 0; j < EPT; ++j) eqm |= (uint32_t)(rsel_idx<NT>(j, tid) < cols && key[j] == prefix) << j;
+        // index order: group by group, in a group thread by thread, in a
+        // thread its four elements in turn
+        int run = 0;  // class members in groups before g
 #pragma unroll 1
-        for (int j = 0; j < EPT; ++j) {
-            const bool eq = (eqm >> j) & 1u;
-            const unsigned long long bal = __ballot(eq);
-            if (__lane_id() == 0) sh.wtot[w] = __popcll(bal);
-            __syncthreads();
-            int before = run + __popcll(bal & lanemask_lt());
-            for (int i = 0; i < NT / 64; ++i) {
-                if (i < w) before += sh.wtot[i];
-                run += sh.wtot[i];
-            }
-            __syncthreads();
-            if (eq && before < kk) {
-                take |= 1u << j;
-                ++nt;
+        for (int g = 0; g < EPT / 4; ++g) {
+            const uint32_t m4 = (eqm >> (4 * g)) & 0xFu;
+            int tot;
+            int before = run + block_prefix_excl<NT>(__popc(m4), sh.wtot, tot);
+            run += tot;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if ((m4 >> q) & 1u) {
+                    if (before < kk) {
+                        take |= 1u << (4 * g + q);
+                        ++nt;
+                    }
+                    ++before;
+                }
             }
         }
     }
@@ -1772,7 +1801,7 @@ __global__ __launch_bounds__(NT) void k_topk_rsel(TopkArgs a, int dtype, int sor
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
             if ((take >> j) & 1u) {
-                if (pos >= r0 && pos < r0 + RND) sh.buf[pos - r0] = CP::make(key[j], (uint32_t)(lo + j * NT + tid));
+                if (pos >= r0 && pos < r0 + RND) sh.buf[pos - r0] = CP::make(key[j], (uint32_t)(lo + rsel_idx<NT>(j, tid)));
                 ++pos;
             }
         }
@@ -2185,7 +2214,7 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     if (const int ns = radix ? rsel_segments(cols, k, dtype) : 0) {
         if (rows * (long long)ns > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: grid too large");
         a.nseg = ns;
-        a.seg_len = (int)((cols + ns - 1) / ns);
+        a.seg_len = (int)((cols + ns - 1) / ns + 3) & ~3;  // segment starts stay 16-byte aligned
         const int rc = launch_rsel(a, dtype, st);
         if (rc != TPR_OK) return rc;
         hipLaunchKernelGGL(k_topk_merge, dim3((unsigned)rows), dim3(kMergeT), 0, st, a, (int)dtype);
