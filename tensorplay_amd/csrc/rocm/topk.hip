@@ -1685,6 +1685,26 @@ __device__ __forceinline__ void rsel_load(uint32_t (&key)[EPT], const void* base
     }
 }
 
+// Raw bits of a selected element of <= 4 bytes, recovered from its sortable
+// key (the inverse of SortKey::of); float32 reads the input only for +-0.0 and
+// NaN, whose keys are canonical.
+__device__ __forceinline__ uint32_t selected_bits(int dtype, uint32_t key, int largest, const void* row, uint32_t idx) {
+    if (dtype == TPR_FLOAT32) return __float_as_uint(selected_value(static_cast<const float*>(row), key, idx, largest));
+    const int bits = 8 * dtype_bytes(dtype);
+    const uint32_t mask = bits == 32 ? 0xffffffffu : ((1u << bits) - 1u);
+    const uint32_t k = (largest ? key : ~key) & mask;
+    const bool sgn = dtype == TPR_INT8 || dtype == TPR_INT16 || dtype == TPR_INT32;
+    return sgn ? (k ^ (1u << (bits - 1))) : k;
+}
+
+__device__ __forceinline__ void store_bits(void* out, long long i, int dtype, uint32_t v) {
+    switch (dtype_bytes(dtype)) {
+        case 4: static_cast<uint32_t*>(out)[i] = v; break;
+        case 2: static_cast<uint16_t*>(out)[i] = (uint16_t)v; break;
+        default: static_cast<uint8_t*>(out)[i] = (uint8_t)v; break;
+    }
+}
+
 template <int NT, int EPT, int P>
 __global__ __launch_bounds__(NT) void k_topk_rsel(TopkArgs a, int dtype, int sort_n) {
     using CP = Comp<uint32_t>;
@@ -1839,11 +1859,7 @@ __global__ __launch_bounds__(NT) void k_topk_rsel(TopkArgs a, int dtype, int sor
         if (r < k) {
             const uint32_t idx = CP::index(x[p]);
             oi[r] = (long long)idx;
-            switch (dtype_bytes(dtype)) {
-                case 4: reinterpret_cast<uint32_t*>(a.out_v)[row * k + r] = reinterpret_cast<const uint32_t*>(base)[idx]; break;
-                case 2: reinterpret_cast<uint16_t*>(a.out_v)[row * k + r] = reinterpret_cast<const uint16_t*>(base)[idx]; break;
-                default: reinterpret_cast<uint8_t*>(a.out_v)[row * k + r] = reinterpret_cast<const uint8_t*>(base)[idx]; break;
-            }
+            store_bits(a.out_v, row * k + r, dtype, selected_bits(dtype, (uint32_t)(x[p] >> 32), a.largest, base, idx));
         }
     }
 }
@@ -1954,16 +1970,8 @@ __global__ __launch_bounds__(kMergeT) void k_topk_merge(TopkArgs a, int dtype) {
     for (int i = threadIdx.x; i < k; i += kMergeT) {
         const uint32_t idx = comp_index(sh.sel[i]);
         a.out_i[row * k + i] = (long long)idx;
-        if (dtype == TPR_FLOAT32) {
-            a.out_v[row * k + i] = selected_value(p, (uint32_t)(sh.sel[i] >> 32), idx, a.largest);
-        } else {
-            const char* rb = reinterpret_cast<const char*>(a.in) + row * a.row_stride * dtype_bytes(dtype);
-            switch (dtype_bytes(dtype)) {
-                case 4: reinterpret_cast<uint32_t*>(a.out_v)[row * k + i] = reinterpret_cast<const uint32_t*>(rb)[idx]; break;
-                case 2: reinterpret_cast<uint16_t*>(a.out_v)[row * k + i] = reinterpret_cast<const uint16_t*>(rb)[idx]; break;
-                default: reinterpret_cast<uint8_t*>(a.out_v)[row * k + i] = reinterpret_cast<const uint8_t*>(rb)[idx]; break;
-            }
-        }
+        const char* rb = reinterpret_cast<const char*>(a.in) + row * a.row_stride * dtype_bytes(dtype);
+        store_bits(a.out_v, row * k + i, dtype, selected_bits(dtype, (uint32_t)(sh.sel[i] >> 32), a.largest, rb, idx));
     }
 }
 
