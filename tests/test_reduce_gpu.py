@@ -453,6 +453,24 @@ def test_median_special_values():
         _capi.reduce(m, "median", [1])
 
 
+def test_median_special_values_float64():
+    # float64 keys: NaN ranks above every number (as numpy's sort places it),
+    # +-inf at the ends, -0.0 == +0.0 with a zero median returned as +0.0
+    x = np.array([np.nan, 1.0, np.nan, -np.inf, 2.0, -0.0, 0.0, np.inf, np.nan, -5e-324, 5e-324], np.float64)
+    rng = np.random.default_rng(24)
+    for k in range(1, len(x) + 1):
+        for v in (np.ascontiguousarray(x[:k]), rng.permutation(x[:k])):
+            print(f"case median float64 special n={k}", flush=True)
+            got = np.asarray(_capi.reduce(torch.from_numpy(v).cuda(), "median", None).cpu().numpy()).reshape(())
+            exp = np.sort(v)[(k - 1) // 2]
+            if np.isnan(exp):
+                assert np.isnan(got)
+            elif exp == 0:
+                assert float(got) == 0.0 and not np.signbit(got)
+            else:
+                assert_bits_equal(got, np.asarray(exp).reshape(()))
+
+
 def test_new_ops_config_shapes():
     # the headline shape through the new ops (sizes the tests run in seconds)
     rng = np.random.default_rng(17)
