@@ -965,6 +965,13 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(6, 8))) void
 constexpr int kShortT = 256;  // threads per short-row workgroup (4 waves)
 constexpr int kShortMaxCols = 4096;
 constexpr int kShortMaxK = 64;
+// Many rows of <= 1024 elements also take k of 65..128 in the lane-group
+// kernel (64 lanes, the exact bit-search path, then a lane sort of the k).
+// MI355X, us, register radix select -> lane groups: [16384, 1024] k = 100
+// 92.9 -> 63.7, k = 65 92.1 -> 63.2; [65536, 256] k = 100 324 -> 176; but
+// [4096, 2048] k = 100 even (36.2 / 35.8), [8192, 3000] k = 128 81 -> 148 and
+// [512, 2000] k = 100 13 -> 24, so rows of <= 1024 and >= 8 rows per CU.
+__host__ inline bool short_exact(long long rows, long long cols, long long k);
 
 template <int L>
 __device__ __forceinline__ int group_sum(int v) {
@@ -1182,13 +1189,16 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
 #pragma unroll
     for (int q = 0; q < E; ++q) mx = max(mx, key[q]);
     const uint32_t srt = group_sort_asc<L>(mx, sl);
-    const uint32_t T = max(__shfl(srt, grp * L + (L - k), 64), 1u);  // k-th largest lane max; valid keys are >= 1
+    // k-th largest lane max (valid keys are >= 1); k > L (64-lane rows, k of
+    // 65..128) has no such bound and takes the exact path below
+    const bool bound_ok = k <= L;
+    const uint32_t T = bound_ok ? max(__shfl(srt, grp * L + (L - min(k, L)), 64), 1u) : 1u;
     const uint32_t gmax = __shfl(srt, grp * L + L - 1, 64);
     int n = 0;
 #pragma unroll
     for (int q = 0; q < E; ++q) n += (key[q] >= T) ? 1 : 0;
     const int incl = group_scan<L>(n, sl);
-    int c = __shfl(incl, grp * L + L - 1, 64);  // candidates of this row
+    int c = bound_ok ? __shfl(incl, grp * L + L - 1, 64) : C + 1;  // candidates of this row
     unsigned long long* list = cl[slot];
     if (c <= C) {
         int pos = incl - n;
@@ -2005,6 +2015,10 @@ bool wave4(long long rows, long long cols, long long k) {
     return cols < 2 * kWaveMinSeg && (rows >= 4LL * device_info().cus || (cols <= kShortMaxCols && k > 32));
 }
 
+__host__ inline bool short_exact(long long rows, long long cols, long long k) {
+    return k > kShortMaxK && k <= kWaveK && cols <= 1024 && rows >= 8LL * device_info().cus;
+}
+
 TopkPlan plan_topk(long long rows, long long cols, long long k) {
     TopkPlan pl{1, (int)cols, false, 8, 0};
     const int cus = device_info().cus;
@@ -2059,7 +2073,7 @@ bool radix_route(long long rows, long long cols, long long k, int32_t dtype = TP
     if (k > kKMax || dtype != TPR_FLOAT32) return true;
     if (knobs().topk_radix < 0 || knobs().topk_fallback) return false;
     if (knobs().topk_radix > 0) return true;
-    return k > kWaveK || (k > kShortMaxK && cols < kWaveMinSeg && !wave4(rows, cols, k));
+    return k > kWaveK || (k > kShortMaxK && cols < kWaveMinSeg && !wave4(rows, cols, k) && !short_exact(rows, cols, k));
 }
 
 // Rows the register-resident kernel takes (elements of <= 4 bytes, rows of
@@ -2251,7 +2265,8 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     // the workgroup kernel ([16384, 3000] k = 64: 124 against 181 us;
     // [8192, 2500] k = 40: 38 against 77 us).
     // (The lane-group kernel addresses up to 4 rows per wave with 32-bit offsets.)
-    const bool short_ok = k <= kShortMaxK && cols <= kShortMaxCols && 3 * row_stride + cols < (1LL << 29);
+    const bool short_ok = (k <= kShortMaxK || short_exact(rows, cols, k)) && cols <= kShortMaxCols &&
+                          3 * row_stride + cols < (1LL << 29);
     const bool short_fit = short_ok && (cols <= 2048 || k <= 32 || !wave4(rows, cols, k));
     if (!smp && (short_fit || (knobs().topk_short > 0 && short_ok)) &&
         knobs().topk_short >= 0 && knobs().topk_fallback == 0 && knobs().splits <= 0)

@@ -212,7 +212,10 @@ def test_short_rows_many():
     check(y, y, 32)
     # 64-lane rows whose candidates (37..128 after the bound) are ranked by a
     # lane sort of one or two composites per lane instead of compares
-    for rows, cols, k in ((2048, 1024, 48), (1024, 2048, 64), (4096, 512, 40), (2048, 1024, 37)):
+    # k of 65..128 on >= 8 rows per CU of <= 1024 elements: exact bit search in
+    # the lane groups, then the lane sort
+    for rows, cols, k in ((2048, 1024, 48), (1024, 2048, 64), (4096, 512, 40), (2048, 1024, 37),
+                          (4096, 1000, 100), (2048, 256, 128), (2048, 1024, 65)):
         z = rng.standard_normal((rows, cols)).astype(np.float32)
         z[::5] = np.round(z[::5] * 4) / 4  # ties among the candidates
         check(z, z, k, True)
