@@ -965,12 +965,13 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(6, 8))) void
 constexpr int kShortT = 256;  // threads per short-row workgroup (4 waves)
 constexpr int kShortMaxCols = 4096;
 constexpr int kShortMaxK = 64;
-// Many rows of <= 1024 elements also take k of 65..128 in the lane-group
-// kernel (64 lanes, the exact bit-search path, then a lane sort of the k).
-// MI355X, us, register radix select -> lane groups: [16384, 1024] k = 100
-// 92.9 -> 63.7, k = 65 92.1 -> 63.2; [65536, 256] k = 100 324 -> 176; but
-// [4096, 2048] k = 100 even (36.2 / 35.8), [8192, 3000] k = 128 81 -> 148 and
-// [512, 2000] k = 100 13 -> 24, so rows of <= 1024 and >= 8 rows per CU.
+// Many rows of <= 2048 elements also take k of 65..128 in the lane-group
+// kernel (64 lanes; the bound is the k-th largest of the lanes' two largest
+// keys).  MI355X, us, register radix select -> lane groups: [16384, 1024]
+// k = 100 94.3 -> 55.8; [65536, 256] k = 100 324 -> 89; [4096, 2048] k = 100
+// 37.5 -> 22.6; [16384, 2048] k = 80 114 -> 38.7; but [8192, 3000] k = 128
+// 83 -> 125 and [512, 2000] k = 100 13.5 -> 15.7, so rows of <= 2048 and >= 8
+// rows per CU.  topk_short = 1 (debug knob) takes every row below 4096.
 __host__ inline bool short_exact(long long rows, long long cols, long long k);
 
 template <int L>
@@ -1185,14 +1186,28 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
         for (int q = 0; q < E; ++q) key[q] = 0u;
     }
 
-    uint32_t mx = 0;
+    uint32_t mx = 0, mx2 = 0;  // the lane's largest and second largest key
 #pragma unroll
-    for (int q = 0; q < E; ++q) mx = max(mx, key[q]);
+    for (int q = 0; q < E; ++q) {
+        mx2 = max(mx2, min(mx, key[q]));
+        mx = max(mx, key[q]);
+    }
     const uint32_t srt = group_sort_asc<L>(mx, sl);
-    // k-th largest lane max (valid keys are >= 1); k > L (64-lane rows, k of
-    // 65..128) has no such bound and takes the exact path below
-    const bool bound_ok = k <= L;
-    const uint32_t T = bound_ok ? max(__shfl(srt, grp * L + (L - min(k, L)), 64), 1u) : 1u;
+    // The bound: the k-th largest lane max (valid keys are >= 1); for k of
+    // 65..128 (64-lane rows) the k-th largest of the lanes' two largest keys,
+    // 128 distinct elements sorted two per lane.
+    uint32_t T;
+    if (L == 64 && k > L) {
+        unsigned long long x2[2] = {mx, mx2};
+        wave_sort_desc<2>(x2);
+        const int r = k - 1;
+        const uint32_t t0 = (uint32_t)__shfl((int)(uint32_t)x2[0], r >> 1, 64);
+        const uint32_t t1 = (uint32_t)__shfl((int)(uint32_t)x2[1], r >> 1, 64);
+        T = max((r & 1) ? t1 : t0, 1u);
+    } else {
+        T = max(__shfl(srt, grp * L + (L - min(k, L)), 64), 1u);
+    }
+    const bool bound_ok = k <= (L == 64 ? 2 * L : L);
     const uint32_t gmax = __shfl(srt, grp * L + L - 1, 64);
     int n = 0;
 #pragma unroll
@@ -2016,7 +2031,9 @@ bool wave4(long long rows, long long cols, long long k) {
 }
 
 __host__ inline bool short_exact(long long rows, long long cols, long long k) {
-    return k > kShortMaxK && k <= kWaveK && cols <= 1024 && rows >= 8LL * device_info().cus;
+    if (k <= kShortMaxK || k > kWaveK) return false;
+    if (knobs().topk_short > 0) return cols < kShortMaxCols;
+    return cols <= 2048 && rows >= 8LL * device_info().cus;
 }
 
 TopkPlan plan_topk(long long rows, long long cols, long long k) {

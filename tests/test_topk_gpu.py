@@ -177,7 +177,8 @@ def test_short_rows(short):
     for rows, cols in [(1, 5), (7, 16), (33, 64), (19, 255), (130, 256), (9, 1000), (5, 2049), (6, 4096),
                        (3, 4093)]:
         x = rng.uniform(-1, 1, (rows, cols)).astype(np.float32)
-        for k in sorted({1, min(cols, 3), min(cols, 8), min(cols, 17), min(cols, 32), min(cols, 64)}):
+        for k in sorted({1, min(cols, 3), min(cols, 8), min(cols, 17), min(cols, 32), min(cols, 64), min(cols, 65),
+                         min(cols, 100), min(cols, 128)}):
             check(x, x, k, True)
             check(x, x, k, False)
     b = rng.standard_normal((40, 1031)).astype(np.float32)
@@ -189,7 +190,7 @@ def test_short_rows(short):
     t[2] = np.round(rng.standard_normal(3000) * 2) / 2
     t[3, 100:2100] = 7.0
     t[4] = np.where(rng.random(3000) < 0.5, -0.0, 0.0)
-    for k in (1, 10, 33, 64):
+    for k in (1, 10, 33, 64, 100, 128):
         check(t, t, k, True)
         check(t, t, k, False)
     s = rng.standard_normal((8, 512)).astype(np.float32)
@@ -198,7 +199,7 @@ def test_short_rows(short):
     s[2, 7] = np.inf
     s[3, :] = np.float32(1e-45)
     s[3, 300] = -np.float32(1e-45)
-    for k in (1, 7, 64):
+    for k in (1, 7, 64, 127):
         check(s, s, k, True)
         check(s, s, k, False)
 
@@ -215,7 +216,7 @@ def test_short_rows_many():
     # k of 65..128 on >= 8 rows per CU of <= 1024 elements: exact bit search in
     # the lane groups, then the lane sort
     for rows, cols, k in ((2048, 1024, 48), (1024, 2048, 64), (4096, 512, 40), (2048, 1024, 37),
-                          (4096, 1000, 100), (2048, 256, 128), (2048, 1024, 65)):
+                          (4096, 1000, 100), (2048, 256, 128), (2048, 1024, 65), (2048, 2048, 90)):
         z = rng.standard_normal((rows, cols)).astype(np.float32)
         z[::5] = np.round(z[::5] * 4) / 4  # ties among the candidates
         check(z, z, k, True)
