@@ -1194,10 +1194,12 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
     }
     const uint32_t srt = group_sort_asc<L>(mx, sl);
     // The bound: the k-th largest lane max (valid keys are >= 1); for k of
-    // 65..128 (64-lane rows) the k-th largest of the lanes' two largest keys,
-    // 128 distinct elements sorted two per lane.
+    // 57..128 (64-lane rows) the k-th largest of the lanes' two largest keys,
+    // 128 distinct elements sorted two per lane (tighter near k = 64: MI355X
+    // [16384, 3000] k = 64 124 -> 90 us, [16384, 2048] 50 -> 39; looser costs
+    // more than the sort below that: k = 40..50 3-12% slower).
     uint32_t T;
-    if (L == 64 && k > L) {
+    if (L == 64 && k > 56) {
         unsigned long long x2[2] = {mx, mx2};
         wave_sort_desc<2>(x2);
         const int r = k - 1;
