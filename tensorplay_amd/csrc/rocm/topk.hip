@@ -2187,7 +2187,9 @@ int launch_short(const TopkArgs& a, bool vec, hipStream_t st) {
 template <int NT, int EPT>
 int launch_rsel_p(const TopkArgs& a, int32_t dtype, hipStream_t st) {
     const int n = std::max(64, pow2_at_least(a.k));
-    const int P = std::min(n / 64, std::max(4, n / NT));
+    int P = std::min(n / 64, std::max(4, n / NT));
+    const long long pv = knobs().topk_variant;  // debug: composites per thread of the sort
+    if (pv >= 1 && pv <= 32 && (pv & (pv - 1)) == 0 && n / pv >= 64 && n / pv <= NT) P = (int)pv;
     const dim3 g((unsigned)(a.rows * a.nseg)), b(NT);
     if (P == 1) hipLaunchKernelGGL((k_topk_rsel<NT, EPT, 1>), g, b, 0, st, a, (int)dtype, n);
     else if (P == 2) hipLaunchKernelGGL((k_topk_rsel<NT, EPT, 2>), g, b, 0, st, a, (int)dtype, n);
