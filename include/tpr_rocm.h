@@ -312,8 +312,15 @@ int32_t tpr_abi_version(void);
  * floats on 512-thread workgroups, 0 = automatic), "smx_res" (-1 = never hold long
  * softmax rows or strided-dim slices on chip: two-pass kernels, 0 = automatic),
  * "topk_variant" (wave kernel prefetch depth: 1 = none, 2 = one slice, 3 = two
- * slices; 0 = automatic), "topk_waves" (8 or 16 waves per wave-kernel
- * workgroup, 0 = automatic).
+ * slices; also, as a power of two 1..32, the register radix select's sort
+ * composites per thread where the sort size allows; 0 = automatic),
+ * "topk_waves" (4, 8 or 16 waves per wave-kernel workgroup, 0 = automatic),
+ * "topk_short" (1 = the lane-group kernel for every row it can hold, -1 =
+ * never), "topk_radix" (1 = the radix-select kernels for every k, 2 = the
+ * streaming one, -1 = never where another kernel can), "topk_dyn" (-1 = static
+ * slice order in the 16-wave kernel), "rowreg" (-1 = no register-row sum
+ * kernel), "nt" (1 / -1 = nontemporal accesses always / never where a kernel
+ * chooses them, 0 = automatic).
  * Process-wide; not synchronised with concurrent launches.  Returns
  * TPR_ERR_INVALID_ARG for an unknown key.  No reference counterpart. */
 int tpr_debug_set(const char* key, int64_t value);
