@@ -1418,8 +1418,8 @@ template <class T>
 struct RadixShared {
     typename Comp<typename SortKey<T>::K>::C cand[radix_lds_count<T>()];
     uint32_t hist[kRadixBins];
-    int wtot[kRadixT / 64];
-    int digit, kk, count, eq_taken;
+    int wtot[kMaxW];
+    int digit, kk, cls, count, eq_taken;
 };
 
 // Inclusive suffix sum over the workgroup's threads (thread t gets the sum of
@@ -1459,7 +1459,8 @@ __device__ void radix_select(RadixShared<T>& sh, typename Comp<typename SortKey<
     const int w = tid / 64;
     K prefix = 0, pmask = 0;
     int kk = k;
-    for (int hi = SortKey<T>::kBits; hi > 0; hi -= 11) {
+    bool whole = false;  // the class sharing the found prefix is exactly the kk still wanted
+    for (int hi = SortKey<T>::kBits; hi > 0 && !whole; hi -= 11) {
         const int shift = hi > 11 ? hi - 11 : 0;
         const K dmask = (K)((1u << (hi - shift)) - 1u);
         for (int i = tid; i < kRadixBins; i += NT) sh.hist[i] = 0u;
@@ -1486,12 +1487,26 @@ __device__ void radix_select(RadixShared<T>& sh, typename Comp<typename SortKey<
             }
             sh.digit = tid * BPT + b;
             sh.kk = kk - cum;
+            sh.cls = (int)h[b];
         }
         __syncthreads();
         prefix |= (K)sh.digit << shift;
         pmask |= dmask << shift;
         kk = sh.kk;
+        whole = sh.cls == kk;
         __syncthreads();
+    }
+    if (whole) {
+        // every key above the class and the whole class: exactly k, no ties to
+        // order (most data: after two or three passes instead of all of them)
+        if (tid == 0) sh.count = 0;
+        __syncthreads();
+        for (int e = tid; e < n; e += NT) {
+            const K key = SortKey<T>::of(p[e], largest);
+            if ((key & pmask) >= prefix) cand[atomicAdd(&sh.count, 1)] = CP::make(key, (uint32_t)e);
+        }
+        __syncthreads();
+        return;
     }
     const K Tk = prefix;  // the k-th key; take kk of the keys equal to it
     if (tid == 0) {
@@ -1530,8 +1545,8 @@ __device__ void radix_select(RadixShared<T>& sh, typename Comp<typename SortKey<
 }
 
 // Values are the selected elements themselves (re-read at their index).
-template <class T>
-__global__ __launch_bounds__(kRadixT) void k_topk_radix(TopkArgs a, void* gcand) {
+template <class T, int NT>
+__global__ __launch_bounds__(NT) void k_topk_radix(TopkArgs a, void* gcand) {
     using C = typename Comp<typename SortKey<T>::K>::C;
     __shared__ RadixShared<T> sh;
     const long long row = blockIdx.x;
@@ -1539,10 +1554,10 @@ __global__ __launch_bounds__(kRadixT) void k_topk_radix(TopkArgs a, void* gcand)
     const int k = a.k;
     const int n2 = pow2_at_least(k);
     C* cand = (n2 <= radix_lds_count<T>()) ? sh.cand : static_cast<C*>(gcand) + row * (long long)n2;
-    radix_select<kRadixT, T>(sh, cand, p, a.cols, k, a.largest);
-    for (int i = k + threadIdx.x; i < n2; i += kRadixT) cand[i] = (C)0;
+    radix_select<NT, T>(sh, cand, p, a.cols, k, a.largest);
+    for (int i = k + threadIdx.x; i < n2; i += NT) cand[i] = (C)0;
     __syncthreads();
-    bitonic_desc<kRadixT, C>(cand, n2);
+    bitonic_desc<NT, C>(cand, n2);
     if constexpr (std::is_same<T, float>::value) {
         if (a.sample) {
             if (threadIdx.x < 64) sample_from_sel(a, row, p, cand, k);
@@ -1550,7 +1565,7 @@ __global__ __launch_bounds__(kRadixT) void k_topk_radix(TopkArgs a, void* gcand)
         }
     }
     T* ov = reinterpret_cast<T*>(a.out_v);
-    for (int i = threadIdx.x; i < k; i += kRadixT) {
+    for (int i = threadIdx.x; i < k; i += NT) {
         const uint32_t idx = Comp<typename SortKey<T>::K>::index(cand[i]);
         ov[row * k + i] = p[idx];
         a.out_i[row * k + i] = (long long)idx;
@@ -2264,19 +2279,26 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
         return check_launch("k_topk_merge");
     }
     if (radix) {
-        const dim3 g((unsigned)rows), b(kRadixT);
+        // few rows: 1024 threads per row (the passes over the row are latency bound)
+        const int nt = rows < 2LL * device_info().cus ? 1024 : kRadixT;
+#define TPR_RADIX(T)                                                                                  \
+    {                                                                                                 \
+        if (nt == 1024) hipLaunchKernelGGL((k_topk_radix<T, 1024>), dim3((unsigned)rows), dim3(1024), 0, st, a, workspace); \
+        else hipLaunchKernelGGL((k_topk_radix<T, kRadixT>), dim3((unsigned)rows), dim3(kRadixT), 0, st, a, workspace); \
+    }
         switch (dtype) {
-            case TPR_FLOAT32: hipLaunchKernelGGL(k_topk_radix<float>, g, b, 0, st, a, workspace); break;
-            case TPR_FLOAT64: hipLaunchKernelGGL(k_topk_radix<double>, g, b, 0, st, a, workspace); break;
-            case TPR_INT8: hipLaunchKernelGGL(k_topk_radix<signed char>, g, b, 0, st, a, workspace); break;
-            case TPR_INT16: hipLaunchKernelGGL(k_topk_radix<short>, g, b, 0, st, a, workspace); break;
-            case TPR_INT32: hipLaunchKernelGGL(k_topk_radix<int>, g, b, 0, st, a, workspace); break;
-            case TPR_INT64: hipLaunchKernelGGL(k_topk_radix<long long>, g, b, 0, st, a, workspace); break;
-            case TPR_UINT16: hipLaunchKernelGGL(k_topk_radix<unsigned short>, g, b, 0, st, a, workspace); break;
-            case TPR_UINT32: hipLaunchKernelGGL(k_topk_radix<unsigned int>, g, b, 0, st, a, workspace); break;
-            case TPR_UINT64: hipLaunchKernelGGL(k_topk_radix<unsigned long long>, g, b, 0, st, a, workspace); break;
-            default: hipLaunchKernelGGL(k_topk_radix<unsigned char>, g, b, 0, st, a, workspace); break;  // UINT8, BOOL
+            case TPR_FLOAT32: TPR_RADIX(float) break;
+            case TPR_FLOAT64: TPR_RADIX(double) break;
+            case TPR_INT8: TPR_RADIX(signed char) break;
+            case TPR_INT16: TPR_RADIX(short) break;
+            case TPR_INT32: TPR_RADIX(int) break;
+            case TPR_INT64: TPR_RADIX(long long) break;
+            case TPR_UINT16: TPR_RADIX(unsigned short) break;
+            case TPR_UINT32: TPR_RADIX(unsigned int) break;
+            case TPR_UINT64: TPR_RADIX(unsigned long long) break;
+            default: TPR_RADIX(unsigned char) break;  // UINT8, BOOL
         }
+#undef TPR_RADIX
         return check_launch("k_topk_radix");
     }
     // Rows of 4096 elements with k > 32 go to the 4-wave wave kernel instead
