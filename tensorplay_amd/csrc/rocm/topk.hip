@@ -1985,7 +1985,10 @@ __global__ __launch_bounds__(kMergeT) void k_topk_merge(TopkArgs a, int dtype) {
         // every composite above the class plus the whole class: exactly k
         for (int i = tid; i < m; i += kMergeT) {
             const unsigned long long c = sh.cand[i];
-            if ((c & pmask) >= prefix) sh.surv[atomicAdd(&sh.count, 1)] = c;
+            if ((c & pmask) >= prefix) {
+                const int pos = atomicAdd(&sh.count, 1);
+                if (pos < kKMax) sh.surv[pos] = c;  // exactly k by construction; the test keeps LDS writes in range
+            }
         }
         __syncthreads();
         if (k <= 128) {
@@ -2010,7 +2013,7 @@ __global__ __launch_bounds__(kMergeT) void k_topk_merge(TopkArgs a, int dtype) {
         return;
     }
     for (int i = threadIdx.x; i < k; i += kMergeT) {
-        const uint32_t idx = comp_index(sh.sel[i]);
+        const uint32_t idx = min(comp_index(sh.sel[i]), (uint32_t)(a.cols - 1));  // in range even for a bad workspace
         a.out_i[row * k + i] = (long long)idx;
         const char* rb = reinterpret_cast<const char*>(a.in) + row * a.row_stride * dtype_bytes(dtype);
         store_bits(a.out_v, row * k + i, dtype, selected_bits(dtype, (uint32_t)(sh.sel[i] >> 32), a.largest, rb, idx));

@@ -239,6 +239,30 @@ def test_few_long_rows_many_segments():
     check(y, y, 50)
 
 
+@pytest.mark.parametrize("dt", [np.float64, np.int64])
+def test_streaming_radix_many_rows_8_byte(dt):
+    # >= 2 rows per CU of 8-byte elements: 256-thread streaming radix
+    # workgroups; the passes stop early unless the k-th key's class needs the
+    # tie order (heavy ties below)
+    rng = np.random.default_rng(34)
+    if dt == np.float64:
+        x = rng.standard_normal((600, 3000))
+        x[1::7] = np.round(x[1::7] * 2)
+        x[3, ::9] = np.nan
+    else:
+        x = rng.integers(-(1 << 40), 1 << 40, size=(600, 3000), dtype=np.int64)
+        x[1::7] %= 5
+    t = torch.from_numpy(x).cuda()
+    for k in (1, 50, 700):
+        for largest in (True, False):
+            print(f"case topk {np.dtype(dt).name} [600, 3000] k={k} largest={largest}", flush=True)
+            gv, gi = _capi.topk(t, k, largest)
+            torch.cuda.synchronize()
+            ev, ei = O.topk_any(x, k, largest)
+            np.testing.assert_array_equal(gi.cpu().numpy(), ei)
+            np.testing.assert_array_equal(gv.cpu().numpy().view(np.uint8), ev.view(np.uint8))
+
+
 def test_long_rows_large_k_segments():
     # rows longer than 32768 with k of 129..1024: segments of <= 32768 through
     # the register radix select, winners merged (radix select over the
