@@ -421,19 +421,22 @@ __global__ __launch_bounds__(kResT) void k_smx_res(SmxArgs p, int vl) {
     f32x4 r[kResVR];
 #pragma unroll
     for (int j = 0; j < kResVR; ++j) r[j] = __builtin_amdgcn_raw_buffer_load_b128(ba, (j * kResT + t) * 16, 0, aux);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the LDS loads have landed
-    __syncthreads();
+    // vmcnt(kResVR): the LDS loads, issued first, have landed while the
+    // register loads may still be in flight.  Each lane reads only the LDS
+    // slots its own load filled, so no workgroup barrier.
+    static_assert(kResVR < 64, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt((kResVR & 15) | ((kResVR >> 4) << 14) | 0x0F70);
 
     auto ldsv = [&](int j) -> f32x4 {
         return ((kResVR + j) * kResT + t < q) ? lds[j * kResT + t] : ninf;
     };
     float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kResVR; ++j) m = fmaxf(fmaxf(m, fmaxf(r[j].x, r[j].y)), fmaxf(r[j].z, r[j].w));
     for (int j = 0; j < vl; ++j) {
         const f32x4 x = ldsv(j);
         m = fmaxf(fmaxf(m, fmaxf(x.x, x.y)), fmaxf(x.z, x.w));
     }
+#pragma unroll
+    for (int j = 0; j < kResVR; ++j) m = fmaxf(fmaxf(m, fmaxf(r[j].x, r[j].y)), fmaxf(r[j].z, r[j].w));
     m = grp<kResT, true>(m, sh[0]);
     // per-lane sum in short chains (groups of 8 vectors, then the groups and
     // the LDS part): ~300 terms per lane, summed sequentially, would cost
