@@ -430,33 +430,67 @@ __global__ __launch_bounds__(kResT) void k_smx_res(SmxArgs p, int vl) {
     auto ldsv = [&](int j) -> f32x4 {
         return ((kResVR + j) * kResT + t < q) ? lds[j * kResT + t] : ninf;
     };
-    float m = -INFINITY;
-    for (int j = 0; j < vl; ++j) {
-        const f32x4 x = ldsv(j);
-        m = fmaxf(fmaxf(m, fmaxf(x.x, x.y)), fmaxf(x.z, x.w));
-    }
-#pragma unroll
-    for (int j = 0; j < kResVR; ++j) m = fmaxf(fmaxf(m, fmaxf(r[j].x, r[j].y)), fmaxf(r[j].z, r[j].w));
-    m = grp<kResT, true>(m, sh[0]);
-    // per-lane sum in short chains (groups of 8 vectors, then the groups and
-    // the LDS part): ~300 terms per lane, summed sequentially, would cost
-    // accuracy next to the two-pass kernel
-    float s = 0.0f;
-    if (m != -INFINITY) {
-        auto vs = [&](f32x4 x) { return (exs(x.x - m) + exs(x.y - m)) + (exs(x.z - m) + exs(x.w - m)); };
-        static_assert(kResVR % 8 == 0, "register vectors come in groups of 8");
-#pragma unroll
-        for (int g = 0; g < kResVR / 8; ++g) {
-            float gs = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 8; j += 2) gs += vs(r[8 * g + j]) + vs(r[8 * g + j + 1]);
-            s += gs;
+    // Online (max, sum exp) per lane, group by group in load order (the LDS
+    // part, then register groups of 8 vectors as their loads land), so the
+    // exponentials run under the remaining loads; one block merge at the end.
+    auto group = [&](auto&& vec, int cnt, float& m, float& s) {
+        float gm = -INFINITY;
+        for (int j = 0; j < cnt; ++j) {
+            const f32x4 x = vec(j);
+            gm = fmaxf(fmaxf(gm, fmaxf(x.x, x.y)), fmaxf(x.z, x.w));
         }
-        float sl = 0.0f;
-        for (int j = 0; j < vl; ++j) sl += vs(ldsv(j));
-        s += sl;
+        float gs = 0.0f;
+        if (gm != -INFINITY) {
+            for (int j = 0; j < cnt; ++j) {
+                const f32x4 x = vec(j);
+                gs += (exs(x.x - gm) + exs(x.y - gm)) + (exs(x.z - gm) + exs(x.w - gm));
+            }
+        } else {
+            for (int j = 0; j < cnt; ++j) {  // only -inf and NaN: NaN stays
+                const f32x4 x = vec(j);
+                gs += ((x.x != x.x ? x.x : 0.0f) + (x.y != x.y ? x.y : 0.0f)) +
+                      ((x.z != x.z ? x.z : 0.0f) + (x.w != x.w ? x.w : 0.0f));
+            }
+        }
+        ms_merge(m, s, gm, gs);
+    };
+    float m = -INFINITY, s = 0.0f;
+    group([&](int j) { return ldsv(j); }, vl, m, s);
+    static_assert(kResVR % 8 == 0, "register vectors come in groups of 8");
+#pragma unroll
+    for (int g = 0; g < kResVR / 8; ++g) {
+        float gm = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) gm = fmaxf(fmaxf(gm, fmaxf(r[8 * g + j].x, r[8 * g + j].y)), fmaxf(r[8 * g + j].z, r[8 * g + j].w));
+        float gs = 0.0f;
+        if (gm != -INFINITY) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const f32x4 x = r[8 * g + j];
+                gs += (exs(x.x - gm) + exs(x.y - gm)) + (exs(x.z - gm) + exs(x.w - gm));
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const f32x4 x = r[8 * g + j];
+                gs += ((x.x != x.x ? x.x : 0.0f) + (x.y != x.y ? x.y : 0.0f)) +
+                      ((x.z != x.z ? x.z : 0.0f) + (x.w != x.w ? x.w : 0.0f));
+            }
+        }
+        ms_merge(m, s, gm, gs);
     }
-    s = grp<kResT, false>(s, sh[1]);
+    // block merge: the wave by lane swaps, then the waves through LDS
+#pragma unroll
+    for (int o = kWave / 2; o >= 1; o >>= 1) ms_merge(m, s, __shfl_xor(m, o, kWave), __shfl_xor(s, o, kWave));
+    if (__lane_id() == 0) {
+        sh[0][t / kWave] = m;
+        sh[1][t / kWave] = s;
+    }
+    __syncthreads();
+    m = sh[0][0];
+    s = sh[1][0];
+#pragma unroll
+    for (int i = 1; i < kResT / kWave; ++i) ms_merge(m, s, sh[0][i], sh[1][i]);
     float st0, st1;
     if (m == -INFINITY) {  // no value above -inf in the slice: NaN, as the reference
         st0 = NAN;
