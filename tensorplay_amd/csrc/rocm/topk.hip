@@ -2061,7 +2061,7 @@ TopkPlan plan_topk(long long rows, long long cols, long long k) {
     const int cus = device_info().cus;
     const bool w4 = wave4(rows, cols, k);
     const bool wave_ok = k <= kWaveK && (cols >= kWaveMinSeg || w4);
-    const int nw = w4 ? 4 : (wave_ok && rows < 2LL * cus && cols >= 2 * kWaveMinSeg) ? 16 : 8;
+    const int nw = w4 ? 4 : (wave_ok && rows <= 2LL * cus && cols >= 2 * kWaveMinSeg) ? 16 : 8;
     const long long unit = wave_ok ? (long long)nw * kSlice : kCH;
     const long long units = (cols + unit - 1) / unit;
     const long long want = (nw == 16) ? cus : 2LL * cus;
@@ -2323,12 +2323,18 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
         // 1024-thread workgroups (few rows): one slice prefetched per wave.
         // (Measured on MI355X at [1024, 32768] k=64 and [256, 151936] k=50.)
         long long var = knobs().topk_variant;
-        if (var == 0) var = pl.nw == 16 ? 2 : (pl.nseg == 1 ? 1 : 2);
+        // 16 waves: one workgroup per CU (<= 1 row per CU) prefetches a slice
+        // per wave; 1..2 rows per CU run two workgroups per CU, 8 waves/SIMD,
+        // no prefetch (MI355X, us: [384, 65536] k = 100 33.5 -> 27.8,
+        // [300, 100000] k = 50 38.8 -> 34.8, [512, 65536] k = 64 31.4 -> 28.1
+        // against the 1-per-CU kernel or 8-wave workgroups)
+        if (var == 0) var = pl.nw == 16 ? (rows > device_info().cus ? 5 : 2) : (pl.nseg == 1 ? 1 : 2);
         const dim3 blk(pl.nw * 64);
         if (pl.nw == 16) {
             if (!vec) hipLaunchKernelGGL((k_topk_wave<false, 4, 4, 1, 16>), dim3(grid), blk, 0, st, a);
             else if (var == 1) hipLaunchKernelGGL((k_topk_wave<true, 4, 4, 0, 16>), dim3(grid), blk, 0, st, a);
             else if (var == 3) hipLaunchKernelGGL((k_topk_wave<true, 4, 4, 2, 16>), dim3(grid), blk, 0, st, a);
+            else if (var == 5) hipLaunchKernelGGL((k_topk_wave<true, 4, 8, 0, 16>), dim3(grid), blk, 0, st, a);
             else hipLaunchKernelGGL((k_topk_wave<true, 4, 4, 1, 16>), dim3(grid), blk, 0, st, a);
         } else if (pl.nw == 4) {
             if (!vec) hipLaunchKernelGGL((k_topk_wave<false, 4, 8, 0, 4>), dim3(grid), blk, 0, st, a);

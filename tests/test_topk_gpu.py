@@ -93,7 +93,7 @@ def test_config5_peaked_logits(dyn):
 
 
 @pytest.mark.parametrize("waves", [4, 8, 16])
-@pytest.mark.parametrize("variant", [1, 2, 3])
+@pytest.mark.parametrize("variant", [1, 2, 3, 5])
 @pytest.mark.parametrize("splits", [0, 1, 2, 3, 5])
 def test_wave_kernel_variants_and_segments(variant, splits, waves):
     # wave-kernel prefetch depths and workgroup sizes, rows cut into 1..5
@@ -277,6 +277,19 @@ def test_long_rows_large_k_segments():
         check(x, x, k, True)
         check(x, x, k, False)
     check(x, x[:, 1:100001], 700)            # misaligned rows
+
+
+def test_one_to_two_rows_per_cu():
+    # between one and two long rows per CU: 16-wave workgroups, two per CU,
+    # no prefetch (the default plan there); adversarial rows included
+    rng = np.random.default_rng(35)
+    x = rng.uniform(-1, 1, (300, 20000)).astype(np.float32)
+    x[4] = 0.5                                # all equal: exact path
+    x[6] = np.round(x[6] * 3) / 3
+    x[8, ::17] = np.nan
+    for k in (1, 50, 128):
+        check(x, x, k, True)
+        check(x, x, k, False)
 
 
 def test_mid_rows_four_wave_workgroups():
