@@ -58,7 +58,8 @@ constexpr int kKMax = 1024;      // largest k of the segment kernels (larger k: 
 constexpr int kMergeT = 256;     // merge workgroup
 constexpr int kMergeMax = 8192;  // candidates a merge workgroup ranks (nseg * k)
 
-constexpr int kWaveK = 128;                   // largest k of the wave kernel
+constexpr int kWaveK = 256;                   // largest k of the wave kernel (129..256: 512-entry lists)
+constexpr int kShortK2 = 128;                 // largest k of the lane-group kernel (64 lanes, two keys each)
 constexpr int kWB = 256;                      // per-wave list capacity
 constexpr int kWaveCompact = 192;             // per-wave list size that always triggers compaction
 constexpr int kSlice = 64 * 16;               // elements per wave slice (4 float4 per lane)
@@ -514,18 +515,19 @@ __device__ __forceinline__ void write_segment(const TopkArgs& a, long long row, 
 // ---------------------------------------------------------------------------
 // Wave-independent segment kernel.
 // ---------------------------------------------------------------------------
-template <int NW>
+template <int NW, int KWB>
 struct WaveShared {
-    unsigned long long wl[NW][kWB];    // per-wave candidate lists (2 KiB per wave)
+    unsigned long long wl[NW][KWB];    // per-wave candidate lists (2 or 4 KiB per wave)
     union {
         uint32_t hist[NW][256];        // per-wave histograms while streaming
-        unsigned long long un[NW * kWB];  // gathered list afterwards
+        unsigned long long un[NW * KWB];  // gathered list afterwards
     };
     BlockScratch bs;
 };
-// After the gather the per-wave list area (NW * kWB composites) is idle: rank
-// (m <= NW * kWB ints) takes its first half and sel (k composites) its second.
-static_assert(kWaveK <= 8 * kWB / 2, "sel fits in the second half of the list area");
+// After the gather the per-wave list area (NW * KWB composites) is idle: rank
+// (m <= NW * KWB ints) takes its first half and sel (k composites) its second;
+// lists of KWB hold k <= KWB / 2 (kWB = 256 for k <= 128, 512 above).
+static_assert(kWaveK <= 4 * 512 / 2, "sel fits in the second half of the list area");
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kBufWord3 = 0x00020000;  // raw buffer resource, 32-bit data (gfx9 family)
@@ -592,13 +594,13 @@ __device__ __forceinline__ void slice_keys(const float4 (&cur)[SV], int base, in
     }
 }
 
-template <bool VEC, int SV, int OCC, int PD, int NW>
+template <bool VEC, int SV, int OCC, int PD, int NW, int KWB = kWB>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8))) void k_topk_wave(TopkArgs a) {
     constexpr int kSl = 256 * SV;  // elements per wave slice
     constexpr int kW = NW;         // waves of this workgroup
     constexpr int kT = NW * 64;
-    constexpr int kB = NW * kWB;   // gathered-list capacity
-    __shared__ WaveShared<NW> sh;
+    constexpr int kB = NW * KWB;   // gathered-list capacity
+    __shared__ WaveShared<NW, KWB> sh;
     BlockScratch& bs = sh.bs;
     const int tid = threadIdx.x;
     const int lane = __lane_id();
@@ -612,7 +614,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
     const int hi = min(a.cols, lo + a.seg_len);
     const int nsl = (hi - lo + kSl - 1) / kSl;
     const int r = (k + kW - 1) / kW;
-    const int compact_at = min(kWaveCompact, max(2 * k, 64));  // per-wave list length that triggers compaction
+    const int compact_at = min(KWB == kWB ? kWaveCompact : KWB - 64, max(2 * k, 64));  // per-wave list length that triggers compaction
     unsigned long long* list = sh.wl[w];
     uint32_t* hist = sh.hist[w];
 
@@ -654,7 +656,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
         int total = 0;
 #pragma unroll
         for (int q = 0; q < 4 * SV; ++q) total += __popcll(__ballot(key[q] >= T));
-        while (total > 0 && cnt + total > kWB) {  // no room: drop stale entries / raise T first
+        while (total > 0 && cnt + total > KWB) {  // no room: drop stale entries / raise T first
             const int before = cnt;
             const uint32_t tn = wave_compact(list, hist, cnt, k, T);
             if (tn > T) {
@@ -778,7 +780,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
             int gbase = 0;
             if (lane == 0 && b) gbase = atomicAdd(&bs.count, __popcll(b));
             gbase = __shfl(gbase, 0, 64);
-            if (keep) sh.un[gbase + __popcll(b & lanemask_lt())] = c;  // sum of lists <= kW * kWB == kB
+            if (keep) sh.un[gbase + __popcll(b & lanemask_lt())] = c;  // sum of lists <= kW * KWB == kB
         }
     }
     __syncthreads();
@@ -2051,7 +2053,7 @@ bool wave4(long long rows, long long cols, long long k) {
 }
 
 __host__ inline bool short_exact(long long rows, long long cols, long long k) {
-    if (k <= kShortMaxK || k > kWaveK) return false;
+    if (k <= kShortMaxK || k > kShortK2) return false;
     if (knobs().topk_short > 0) return cols < kShortMaxCols;
     return cols <= 2048 && rows >= 8LL * device_info().cus;
 }
@@ -2330,7 +2332,20 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
         // against the 1-per-CU kernel or 8-wave workgroups)
         if (var == 0) var = pl.nw == 16 ? (rows > device_info().cus ? 5 : 2) : (pl.nseg == 1 ? 1 : 2);
         const dim3 blk(pl.nw * 64);
-        if (pl.nw == 16) {
+        if (k > 128) {
+            // k of 129..256: 512-entry wave lists (twice the LDS: at most two
+            // 8-wave workgroups per CU: 4 waves per SIMD, a one-slice prefetch)
+            if (pl.nw == 16) {
+                if (!vec) hipLaunchKernelGGL((k_topk_wave<false, 4, 4, 1, 16, 512>), dim3(grid), blk, 0, st, a);
+                else hipLaunchKernelGGL((k_topk_wave<true, 4, 4, 1, 16, 512>), dim3(grid), blk, 0, st, a);
+            } else if (pl.nw == 4) {
+                if (!vec) hipLaunchKernelGGL((k_topk_wave<false, 4, 4, 1, 4, 512>), dim3(grid), blk, 0, st, a);
+                else hipLaunchKernelGGL((k_topk_wave<true, 4, 4, 1, 4, 512>), dim3(grid), blk, 0, st, a);
+            } else {
+                if (!vec) hipLaunchKernelGGL((k_topk_wave<false, 4, 4, 1, 8, 512>), dim3(grid), blk, 0, st, a);
+                else hipLaunchKernelGGL((k_topk_wave<true, 4, 4, 1, 8, 512>), dim3(grid), blk, 0, st, a);
+            }
+        } else if (pl.nw == 16) {
             if (!vec) hipLaunchKernelGGL((k_topk_wave<false, 4, 4, 1, 16>), dim3(grid), blk, 0, st, a);
             else if (var == 1) hipLaunchKernelGGL((k_topk_wave<true, 4, 4, 0, 16>), dim3(grid), blk, 0, st, a);
             else if (var == 3) hipLaunchKernelGGL((k_topk_wave<true, 4, 4, 2, 16>), dim3(grid), blk, 0, st, a);

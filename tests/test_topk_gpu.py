@@ -279,6 +279,33 @@ def test_long_rows_large_k_segments():
     check(x, x[:, 1:100001], 700)            # misaligned rows
 
 
+def test_wave_kernel_k_129_to_256():
+    # k of 129..256 in the wave kernel (512-entry wave lists) on every
+    # workgroup shape: 16 waves (few rows), 8 waves (many), 4 waves (rows of
+    # 4096..16383), split rows with the merge; ties, NaN, all-equal rows (exact
+    # path) and rows whose values rise along the row (repeated compaction)
+    rng = np.random.default_rng(36)
+    n = 40000
+    trend = np.linspace(0, 50, n, dtype=np.float32)
+    a = rng.standard_normal((6, n)).astype(np.float32)
+    a[1] = np.round(a[1] * 3) / 3
+    a[2, ::11] = np.nan
+    a[3] = 1.5
+    a[4] = trend + rng.standard_normal(n).astype(np.float32)
+    for k in (129, 200, 256):
+        check(a, a, k, True)
+        check(a, a, k, False)
+    b = rng.uniform(-1, 1, (1100, 20000)).astype(np.float32)
+    check(b, b, 256)
+    c = rng.standard_normal((1100, 6000)).astype(np.float32)
+    c[::9] = np.round(c[::9] * 2) / 2
+    check(c, c, 150, True)
+    check(c, c, 150, False)
+    d = rng.standard_normal((2, 1_000_000)).astype(np.float32)
+    check(d, d, 256)
+    check(d, d[:, 1:], 200)                  # misaligned rows: scalar loads
+
+
 def test_one_to_two_rows_per_cu():
     # between one and two long rows per CU: 16-wave workgroups, two per CU,
     # no prefetch (the default plan there); adversarial rows included
