@@ -60,6 +60,12 @@ constexpr int kMergeMax = 8192;  // candidates a merge workgroup ranks (nseg * k
 
 constexpr int kWaveK = 256;                   // largest k of the wave kernel (129..256: 512-entry lists)
 constexpr int kShortK2 = 128;                 // largest k of the lane-group kernel (64 lanes, two keys each)
+// Rows shorter than 16384 with k above this take the register radix select:
+// the wave kernel has too few slices per wave there (MI355X, us, k = 256:
+// [1024, 8192] 4 waves 118, 8 waves 42, radix 35; [4096, 4096] 4 waves 155,
+// radix 55), while up to it the 4-wave kernel mostly wins (k = 150:
+// [1024, 8192] 23 against 35, [4096, 8192] 76 against 110).
+constexpr int kWave4K = 192;
 constexpr int kWB = 256;                      // per-wave list capacity
 constexpr int kWaveCompact = 192;             // per-wave list size that always triggers compaction
 constexpr int kSlice = 64 * 16;               // elements per wave slice (4 float4 per lane)
@@ -2047,7 +2053,7 @@ struct TopkPlan {
 // could hold them, is slow there ([512, 4096] k = 64 33 us against 10).
 // topk_waves = 4 (debug knob) forces it on every row of >= 4096 elements.
 bool wave4(long long rows, long long cols, long long k) {
-    if (k > kWaveK || cols < 4 * kSlice) return false;
+    if (k > kWave4K || cols < 4 * kSlice) return false;
     if (knobs().topk_waves != 0) return knobs().topk_waves == 4;
     return cols < 2 * kWaveMinSeg && (rows >= 4LL * device_info().cus || (cols <= kShortMaxCols && k > 32));
 }
@@ -2112,7 +2118,8 @@ bool radix_route(long long rows, long long cols, long long k, int32_t dtype = TP
     if (k > kKMax || dtype != TPR_FLOAT32) return true;
     if (knobs().topk_radix < 0 || knobs().topk_fallback) return false;
     if (knobs().topk_radix > 0) return true;
-    return k > kWaveK || (k > kShortMaxK && cols < kWaveMinSeg && !wave4(rows, cols, k) && !short_exact(rows, cols, k));
+    return k > kWaveK || (k > kWave4K && cols < 2 * kWaveMinSeg) ||
+           (k > kShortMaxK && cols < kWaveMinSeg && !wave4(rows, cols, k) && !short_exact(rows, cols, k));
 }
 
 // Rows the register-resident kernel takes (elements of <= 4 bytes, rows of
