@@ -2048,14 +2048,14 @@ struct TopkPlan {
 // 4 waves): [4096, 4096] k = 64 47.7 -> 29.2, [4096, 6000] k = 16 41.5 -> 26.0,
 // k = 100 105 -> 50, [4096, 8192] k = 64 44.0 -> 37.0, [2048, 12288] k = 64
 // 31.6 -> 26.6; [2048, 16384] even (32.7 / 32.0) and [512, 8192] slower (11.1 /
-// 12.0), so rows >= 4 per CU and rows shorter than 16384.  Rows of exactly
-// 4096 with k > 32 take it at any row count: the lane-group kernel, which
-// could hold them, is slow there ([512, 4096] k = 64 33 us against 10).
-// topk_waves = 4 (debug knob) forces it on every row of >= 4096 elements.
+// 12.0), so rows >= 4 per CU and rows shorter than 16384.  Rows the
+// lane-group kernel can hold (<= 4096) go there first (U(-1, 1) data:
+// [2048, 4096] k = 64 14.0 against 17.7 us, [16384, 4096] k = 64 81 against
+// 99).  topk_waves = 4 (debug knob) forces it on every row of >= 4096 elements.
 bool wave4(long long rows, long long cols, long long k) {
     if (k > kWave4K || cols < 4 * kSlice) return false;
     if (knobs().topk_waves != 0) return knobs().topk_waves == 4;
-    return cols < 2 * kWaveMinSeg && (rows >= 4LL * device_info().cus || (cols <= kShortMaxCols && k > 32));
+    return cols < 2 * kWaveMinSeg && rows >= 4LL * device_info().cus;
 }
 
 __host__ inline bool short_exact(long long rows, long long cols, long long k) {
@@ -2069,7 +2069,12 @@ TopkPlan plan_topk(long long rows, long long cols, long long k) {
     const int cus = device_info().cus;
     const bool w4 = wave4(rows, cols, k);
     const bool wave_ok = k <= kWaveK && (cols >= kWaveMinSeg || w4);
-    const int nw = w4 ? 4 : (wave_ok && rows <= 2LL * cus && cols >= 2 * kWaveMinSeg) ? 16 : 8;
+    // 16 waves: rows <= 1 per CU from 16384 elements, 1..2 per CU from 32768
+    // (at 16384 the 8-wave kernel wins there: [512, 16384] k = 64 13.6 against
+    // 15.5 us)
+    const int nw = w4 ? 4
+                      : (wave_ok && cols >= 2 * kWaveMinSeg && (rows <= cus || (rows <= 2LL * cus && cols >= 4 * kWaveMinSeg)))
+                            ? 16 : 8;
     const long long unit = wave_ok ? (long long)nw * kSlice : kCH;
     const long long units = (cols + unit - 1) / unit;
     const long long want = (nw == 16) ? cus : 2LL * cus;
@@ -2313,16 +2318,14 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
 #undef TPR_RADIX
         return check_launch("k_topk_radix");
     }
-    // Rows of 4096 elements with k > 32 go to the 4-wave wave kernel instead
-    // (MI355X, [16384, 4096] k = 64: 98 us against 117; [2048, 4096]: 18
-    // against 37);
-    // every other row the lane-group kernel can hold is faster there than in
-    // the workgroup kernel ([16384, 3000] k = 64: 124 against 181 us;
-    // [8192, 2500] k = 40: 38 against 77 us).
+    // Every row the lane-group kernel can hold goes there: faster than the
+    // workgroup kernel ([16384, 3000] k = 64: 124 against 181 us; [8192, 2500]
+    // k = 40: 38 against 77 us) and, since its two-key bound, than the 4-wave
+    // kernel on rows of 4096 ([16384, 4096] k = 64: 81 against 99 us).
     // (The lane-group kernel addresses up to 4 rows per wave with 32-bit offsets.)
     const bool short_ok = (k <= kShortMaxK || short_exact(rows, cols, k)) && cols <= kShortMaxCols &&
                           3 * row_stride + cols < (1LL << 29);
-    const bool short_fit = short_ok && (cols <= 2048 || k <= 32 || !wave4(rows, cols, k));
+    const bool short_fit = short_ok;
     if (!smp && (short_fit || (knobs().topk_short > 0 && short_ok)) &&
         knobs().topk_short >= 0 && knobs().topk_fallback == 0 && knobs().splits <= 0)
         return launch_short(a, vec, st);
