@@ -507,9 +507,10 @@ def run_sections(torch, capi, only, stream, steps, warmup, bufs, keep):
         extras["softmax_C2_dim1_64x1024x1024"] = timed(torch, cs, max(steps, 8), warmup, cs[0].bytes)
         del cs
     if "topk_short" in only:
-        # many short rows (lane groups per row) and a large k (rows held in registers), beside the BASELINE top-k configs
+        # many short rows (lane groups per row), a large k (rows held in registers) and k = 256 over C5-sized
+        # vocabulary rows (the wave kernel's 512-entry lists), beside the BASELINE top-k configs
         ets = {}
-        for (rows, cols, k) in ((65536, 256, 8), (16384, 1024, 32), (4096, 2048, 1000)):
+        for (rows, cols, k) in ((65536, 256, 8), (16384, 1024, 32), (4096, 2048, 1000), (256, 151936, 256)):
             nb = max(3, (768 << 20) // (rows * cols * 4))
             bs = [gen(torch, (rows, cols), "uniform", 7000 + i, dev) for i in range(nb)]
             cs = [topk_call(torch, capi, b, k, stream) for b in bs]
