@@ -1,4 +1,5 @@
-// gfx950 top-k along the last dim of a [rows, cols] float32 view.
+// gfx950 top-k along the last dim of a [rows, cols] view (float32 through the
+// filter kernels below; every dtype through the radix-select kernels).
 //
 // TensorPlay has no topk (grep of /root/reference finds no schema, kernel or
 // test); this implements the definition in tpr_rocm.h: order by a 32-bit
@@ -26,16 +27,26 @@
 //     long runs of one value) the workgroup switches to a 4-pass 8-bit radix
 //     select over its segment in global memory, then an index-ordered gather
 //     takes every larger key plus the lowest-index elements equal to the k-th.
-// Two variants of the segment kernel:
-//   k_topk_wave  (k <= 128, segments >= 8192, or >= 4096 with 4-wave
-//     workgroups): every wave streams its own 1024-element slices (w, w+NW,
-//     ...) into a wave-private list with no
-//     workgroup barrier in the loop, so one wave's filtering overlaps the other
-//     waves' loads.  Waves share a monotone threshold through an LDS atomicMax;
-//     a published value always has >= k candidates at or above it in the
-//     publishing wave's list, so it bounds every wave.
-//   k_topk_block (any k <= 1024, any segment): workgroup-wide chunks with one
-//     shared list; used for large k and short rows.
+// Kernels:
+//   k_topk_wave  (k <= 256: 256-entry wave lists up to k = 128, 512 above;
+//     segments >= 8192, or >= 4096 with 4-wave workgroups): every wave streams
+//     its own 1024-element slices (w, w+NW, ... or handed out by an LDS
+//     counter) into a wave-private list with no workgroup barrier in the loop,
+//     so one wave's filtering overlaps the other waves' loads.  Waves share a
+//     monotone threshold through an LDS atomicMax; a published value always
+//     has >= k candidates at or above it in the publishing wave's list, so it
+//     bounds every wave.
+//   k_topk_short (rows <= 4096, k <= 64, or k <= 128 on many rows <= 2048):
+//     16/32/64 lanes per row, the row in registers, no workgroup barrier.
+//   k_topk_rsel  (rows <= 32768 of <= 4-byte elements, large k or any dtype;
+//     longer rows in segments of <= 32768 plus the merge): the row in
+//     registers, an exact radix select, a bitonic sort of the k.
+//   k_topk_radix (8-byte elements, or rows too long for the above): the same
+//     select streaming over the row in memory.
+//   k_topk_block (k <= 1024 on rows the others do not take): workgroup-wide
+//     chunks with one shared list.
+//   k_topk_merge: the k winners of a row's segments (radix cut, then ranking
+//     or a bitonic sort).
 
 #include <hip/hip_runtime.h>
 
