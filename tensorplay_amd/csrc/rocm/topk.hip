@@ -156,7 +156,7 @@ struct TopkArgs {
 // block totals, ballots for the two searches.
 __device__ void sample_from_sel(const TopkArgs& a, long long row, const float* p, const unsigned long long* sel,
                                 int k) {
-    const int lane = threadIdx.x;
+    const int lane = __lane_id();
     if (!(a.temperature > 0.0f)) {
         if (lane == 0) a.ids[row] = (long long)comp_index(sel[0]);
         return;
@@ -1329,24 +1329,58 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
         if (c <= 64) {
             unsigned long long x[1] = {sl < c ? list[sl] : 0ull};
             wave_sort_desc<1>(x);
+            if (a.sample) {  // the sampler: the sorted k in the row's list, then the draw by this wave
+                wave_sync_lds();
+                if (sl < k) list[sl] = x[0];
+                wave_sync_lds();
+                if (live) sample_from_sel(a, row, p, list, k);
+                return;
+            }
             if (sl < k && live) write_ranked(a, row, k, p, largest, sl, x[0]);
         } else {
             unsigned long long x[2] = {2 * sl < c ? list[2 * sl] : 0ull, 2 * sl + 1 < c ? list[2 * sl + 1] : 0ull};
             wave_sort_desc<2>(x);
+            if (a.sample) {
+                wave_sync_lds();
+                if (2 * sl < k) list[2 * sl] = x[0];
+                if (2 * sl + 1 < k) list[2 * sl + 1] = x[1];
+                wave_sync_lds();
+                if (live) sample_from_sel(a, row, p, list, k);
+                return;
+            }
             if (2 * sl < k && live) write_ranked(a, row, k, p, largest, 2 * sl, x[0]);
             if (2 * sl + 1 < k && live) write_ranked(a, row, k, p, largest, 2 * sl + 1, x[1]);
         }
         return;
     }
-    for (int i = sl; i < c; i += L) {
-        const unsigned long long ci = list[i];
-        int r = 0;
-        for (int j = 0; j < c; ++j) r += (list[j] > ci) ? 1 : 0;
-        if (r < k && live) {
-            const uint32_t idx = comp_index(ci);
-            a.out_v[row * k + r] = selected_value(p, (uint32_t)(ci >> 32), idx, largest);
-            a.out_i[row * k + r] = (long long)idx;
+    constexpr int PL = C / L;  // candidates per lane at most
+    int rk[PL];
+    unsigned long long cv[PL];
+#pragma unroll
+    for (int q = 0; q < PL; ++q) {
+        const int i = sl + q * L;
+        rk[q] = k;
+        cv[q] = 0ull;
+        if (i < c) {
+            const unsigned long long ci = list[i];
+            int r = 0;
+            for (int j = 0; j < c; ++j) r += (list[j] > ci) ? 1 : 0;
+            rk[q] = r;
+            cv[q] = ci;
+            if (r < k && live && !a.sample) {
+                const uint32_t idx = comp_index(ci);
+                a.out_v[row * k + r] = selected_value(p, (uint32_t)(ci >> 32), idx, largest);
+                a.out_i[row * k + r] = (long long)idx;
+            }
         }
+    }
+    if (a.sample) {  // L == 64 (one row per wave) when sampling
+        wave_sync_lds();
+#pragma unroll
+        for (int q = 0; q < PL; ++q)
+            if (rk[q] < k) list[rk[q]] = cv[q];
+        wave_sync_lds();
+        if (live) sample_from_sel(a, row, p, list, k);
     }
 }
 
@@ -2216,6 +2250,7 @@ int launch_short(const TopkArgs& a, bool vec, hipStream_t st) {
     // L = 64 15.3; [65536, 256] k = 8: L = 16 19.1, L = 32 21.9.
     int L = 16;
     while (L < 64 && (L < 2 * a.k || L * 16 < a.cols)) L *= 2;
+    if (a.sample) L = 64;  // the draw runs on one wave per row
     if (L == 16) launch_short_l<16>(a, vec, st);
     else if (L == 32) launch_short_l<32>(a, vec, st);
     else launch_short_l<64>(a, vec, st);
@@ -2337,7 +2372,7 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     const bool short_ok = (k <= kShortMaxK || short_exact(rows, cols, k)) && cols <= kShortMaxCols &&
                           3 * row_stride + cols < (1LL << 29);
     const bool short_fit = short_ok;
-    if (!smp && (short_fit || (knobs().topk_short > 0 && short_ok)) &&
+    if ((short_fit || (knobs().topk_short > 0 && short_ok)) &&
         knobs().topk_short >= 0 && knobs().topk_fallback == 0 && knobs().splits <= 0)
         return launch_short(a, vec, st);
     const long long grid = rows * pl.nseg;
