@@ -62,3 +62,25 @@ def test_random_sweep():
         g = gv.cpu().numpy()
         assert g.dtype == ev.dtype
         np.testing.assert_array_equal(g.view(np.uint8), ev.view(np.uint8))
+
+
+def test_random_sweep_many_rows_float32():
+    # float32 with many rows (the routing by rows per CU: lane groups, 4 / 8 /
+    # 16-wave workgroups, two-per-CU 16-wave workgroups, the register and
+    # segmented radix selects) and k up to 256 (512-entry wave lists)
+    rng = np.random.default_rng(20261203)
+    for case in range(40):
+        cols = int(rng.choice([int(rng.integers(200, 4097)), int(rng.integers(4097, 16384)),
+                               int(rng.integers(16384, 70000))]))
+        rows = int(rng.integers(200, max(201, min(5000, 6_000_000 // cols)) + 1))
+        k = int(min(cols, rng.choice([int(rng.integers(1, 65)), int(rng.integers(65, 129)),
+                                      int(rng.integers(129, 257)), int(rng.integers(257, 1025))])))
+        largest = bool(rng.integers(0, 2))
+        x = _row_data(rng, np.float32, rows, cols)
+        print(f"case {case}: float32 rows={rows} cols={cols} k={k} largest={largest}", flush=True)
+        t = torch.from_numpy(x).cuda()
+        gv, gi = _capi.topk(t, k, largest)
+        torch.cuda.synchronize()
+        ev, ei = O.topk(x, k, largest)
+        np.testing.assert_array_equal(gi.cpu().numpy(), ei)
+        np.testing.assert_array_equal(gv.cpu().numpy().view(np.uint32), ev.view(np.uint32))
