@@ -37,7 +37,8 @@
 //     has >= k candidates at or above it in the publishing wave's list, so it
 //     bounds every wave.
 //   k_topk_short (rows <= 4096, k <= 64, or k <= 128 on many rows <= 2048):
-//     16/32/64 lanes per row, the row in registers, no workgroup barrier.
+//     16/32/64 lanes per row, the row in registers, no workgroup barrier;
+//     float32, int32 and uint32.
 //   k_topk_rsel  (rows <= 32768 of <= 4-byte elements, large k or any dtype;
 //     longer rows in segments of <= 32768 plus the merge): the row in
 //     registers, an exact radix select, a bitonic sort of the k.
@@ -113,6 +114,14 @@ __device__ __forceinline__ float selected_value(const float* p, uint32_t key, ui
     return (u == 0u || u == 0x7fc00000u) ? p[idx] : __uint_as_float(u);
 }
 
+// Order-preserving key of a 32-bit integer (its bits in f): int32 flips the
+// sign bit, uint32 is its own key; lmask as for floats.  Unlike float keys an
+// integer key can be 0 (INT_MIN / 0 largest, INT_MAX / UINT_MAX smallest),
+// the key of padding past a row's end.
+__device__ __forceinline__ uint32_t i2key_sel(float f, uint32_t smask, uint32_t lmask) {
+    return __float_as_uint(f) ^ smask ^ lmask;
+}
+
 __device__ __forceinline__ unsigned long long comp_key(uint32_t key, uint32_t idx) {
     return ((unsigned long long)key << 32) | (unsigned long long)(0xffffffffu - idx);
 }
@@ -133,6 +142,7 @@ struct TopkArgs {
     long long row_stride;
     int k;
     int largest;
+    int ikind;  // k_topk_short: 0 float32, 1 int32, 2 uint32 (the elements' bits, loaded as floats)
     int force_fallback;
     int nseg;
     int seg_len;
@@ -1136,7 +1146,7 @@ __device__ __forceinline__ uint32_t group_hist_threshold(const uint32_t* hist, i
 __device__ __forceinline__ void write_ranked(const TopkArgs& a, long long row, int k, const float* p, int largest,
                                              int r, unsigned long long c) {
     const uint32_t idx = comp_index(c);
-    a.out_v[row * k + r] = selected_value(p, (uint32_t)(c >> 32), idx, largest);
+    a.out_v[row * k + r] = a.ikind ? p[idx] : selected_value(p, (uint32_t)(c >> 32), idx, largest);
     a.out_i[row * k + r] = (long long)idx;
 }
 
@@ -1182,7 +1192,17 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
     }
     uint32_t key[E];
     constexpr uint32_t lm = LG ? 0u : 0xffffffffu;
-    if (cols == 4 * E4 * L) {  // every element of every lane is in the row
+    if (a.ikind != 0) {  // 32-bit integers
+        const uint32_t sm = a.ikind == 1 ? 0x80000000u : 0u;
+#pragma unroll
+        for (int j = 0; j < E4; ++j) {
+            const int e = 4 * (j * L + sl);
+            key[4 * j + 0] = (e + 0 < cols) ? i2key_sel(x[j].x, sm, lm) : 0u;
+            key[4 * j + 1] = (e + 1 < cols) ? i2key_sel(x[j].y, sm, lm) : 0u;
+            key[4 * j + 2] = (e + 2 < cols) ? i2key_sel(x[j].z, sm, lm) : 0u;
+            key[4 * j + 3] = (e + 3 < cols) ? i2key_sel(x[j].w, sm, lm) : 0u;
+        }
+    } else if (cols == 4 * E4 * L) {  // every element of every lane is in the row
 #pragma unroll
         for (int j = 0; j < E4; ++j) {
             key[4 * j + 0] = f2key_sel(x[j].x, lm);
@@ -1235,6 +1255,9 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
     for (int q = 0; q < E; ++q) n += (key[q] >= T) ? 1 : 0;
     const int incl = group_scan<L>(n, sl);
     int c = bound_ok ? __shfl(incl, grp * L + L - 1, 64) : C + 1;  // candidates of this row
+    // Fewer than k candidates: the row has keys of 0 (integers only; the
+    // filter keeps keys >= 1), which the exact search below takes.
+    if (c < k) c = C + 1;
     unsigned long long* list = cl[slot];
     if (c <= C) {
         int pos = incl - n;
@@ -1369,7 +1392,7 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
             cv[q] = ci;
             if (r < k && live && !a.sample) {
                 const uint32_t idx = comp_index(ci);
-                a.out_v[row * k + r] = selected_value(p, (uint32_t)(ci >> 32), idx, largest);
+                a.out_v[row * k + r] = a.ikind ? p[idx] : selected_value(p, (uint32_t)(ci >> 32), idx, largest);
                 a.out_i[row * k + r] = (long long)idx;
             }
         }
@@ -2316,6 +2339,7 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     a.row_stride = row_stride;
     a.k = (int)k;
     a.largest = largest ? 1 : 0;
+    a.ikind = dtype == TPR_INT32 ? 1 : dtype == TPR_UINT32 ? 2 : 0;
     a.force_fallback = knobs().topk_fallback ? 1 : 0;
     a.nseg = pl.nseg;
     a.seg_len = pl.seg_len;
@@ -2330,6 +2354,13 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     a.ids = smp ? smp->ids : nullptr;
     const bool vec = ((reinterpret_cast<uintptr_t>(in) & 15u) == 0) && (rows == 1 || row_stride % 4 == 0);
     hipStream_t st = static_cast<hipStream_t>(stream);
+    // (The lane-group kernel addresses up to 4 rows per wave with 32-bit offsets.)
+    const bool short_ok = (k <= kShortMaxK || short_exact(rows, cols, k)) && cols <= kShortMaxCols &&
+                          3 * row_stride + cols < (1LL << 29);
+    const bool short_on = knobs().topk_short >= 0 && knobs().topk_fallback == 0 && knobs().splits <= 0;
+    // 32-bit integer rows the lane-group kernel holds take it rather than the
+    // radix select (the rows fit its registers, so no workspace either way).
+    if (a.ikind != 0 && short_ok && short_on && knobs().topk_radix <= 0) return launch_short(a, vec, st);
     if (radix && rsel_route(cols, dtype))
         return launch_rsel(a, dtype, st);
     if (const int ns = radix ? rsel_segments(cols, k, dtype) : 0) {
@@ -2368,13 +2399,7 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     // workgroup kernel ([16384, 3000] k = 64: 124 against 181 us; [8192, 2500]
     // k = 40: 38 against 77 us) and, since its two-key bound, than the 4-wave
     // kernel on rows of 4096 ([16384, 4096] k = 64: 81 against 99 us).
-    // (The lane-group kernel addresses up to 4 rows per wave with 32-bit offsets.)
-    const bool short_ok = (k <= kShortMaxK || short_exact(rows, cols, k)) && cols <= kShortMaxCols &&
-                          3 * row_stride + cols < (1LL << 29);
-    const bool short_fit = short_ok;
-    if ((short_fit || (knobs().topk_short > 0 && short_ok)) &&
-        knobs().topk_short >= 0 && knobs().topk_fallback == 0 && knobs().splits <= 0)
-        return launch_short(a, vec, st);
+    if (short_ok && short_on) return launch_short(a, vec, st);
     const long long grid = rows * pl.nseg;
     if (pl.wave) {
         // 512-thread workgroups (many rows): 8 waves/SIMD without prefetch.

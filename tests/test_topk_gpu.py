@@ -425,3 +425,47 @@ def test_other_dtypes(dt):
             g = gv.cpu().numpy()
             assert g.dtype == ev.dtype
             np.testing.assert_array_equal(g.view(np.uint8), ev.view(np.uint8))
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.uint32])
+def test_short_rows_32bit_integers(dt):
+    """int32 / uint32 rows of <= 4096 through the lane-group kernel: key 0
+    (INT_MIN / 0 for largest, INT_MAX / UINT_MAX for smallest) is a real
+    element here, so rows with fewer than k other keys take the exact search;
+    also all-extreme rows, heavy ties, k = cols and a strided view."""
+    rng = np.random.default_rng(77)
+    info = np.iinfo(dt)
+    cases = []
+    for rows, cols, ks in [(37, 5, (1, 5)), (300, 100, (1, 7, 64, 100)), (700, 1000, (8, 33, 64)),
+                           (300, 4096, (1, 16, 64)), (2600, 1024, (65, 100, 128)), (2600, 2048, (80, 128))]:
+        x = rng.integers(info.min, info.max, size=(rows, cols), dtype=dt, endpoint=True)
+        x[0] = info.min
+        x[1] = info.max
+        x[2] = np.where(rng.random(cols) < 0.9, info.min, x[2])
+        x[3] = np.where(rng.random(cols) < 0.9, info.max, x[3])
+        x[4] = x[4] % 3
+        x[5, : cols // 2] = info.min
+        x[5, cols // 2:] = info.max
+        cases.append((x, ks))
+    for x, ks in cases:
+        t = torch.from_numpy(x).cuda()
+        for k in ks:
+            for largest in (True, False):
+                print(f"case topk dtype={np.dtype(dt).name} shape={x.shape} k={k} largest={largest}", flush=True)
+                gv, gi = _capi.topk(t, k, largest)
+                torch.cuda.synchronize()
+                ev, ei = O.topk_any(x, k, largest)
+                np.testing.assert_array_equal(gi.cpu().numpy(), ei)
+                np.testing.assert_array_equal(gv.cpu().numpy(), ev)
+    # strided rows (scalar loads): every other row of a wider buffer
+    x = rng.integers(info.min, info.max, size=(64, 3001), dtype=dt, endpoint=True)
+    x[::5, ::2] = info.min
+    t = torch.from_numpy(x).cuda()[:, :2999]
+    for k in (1, 30, 64):
+        for largest in (True, False):
+            print(f"case topk dtype={np.dtype(dt).name} strided k={k} largest={largest}", flush=True)
+            gv, gi = _capi.topk(t, k, largest)
+            torch.cuda.synchronize()
+            ev, ei = O.topk_any(np.ascontiguousarray(x[:, :2999]), k, largest)
+            np.testing.assert_array_equal(gi.cpu().numpy(), ei)
+            np.testing.assert_array_equal(gv.cpu().numpy(), ev)
