@@ -1,5 +1,6 @@
-// gfx950 top-k along the last dim of a [rows, cols] view (float32 through the
-// filter kernels below; every dtype through the radix-select kernels).
+// gfx950 top-k along the last dim of a [rows, cols] view (float32, int32 and
+// uint32 through the filter kernels below; every dtype through the
+// radix-select kernels).
 //
 // TensorPlay has no topk (grep of /root/reference finds no schema, kernel or
 // test); this implements the definition in tpr_rocm.h: order by a 32-bit
@@ -37,8 +38,7 @@
 //     has >= k candidates at or above it in the publishing wave's list, so it
 //     bounds every wave.
 //   k_topk_short (rows <= 4096, k <= 64, or k <= 128 on many rows <= 2048):
-//     16/32/64 lanes per row, the row in registers, no workgroup barrier;
-//     float32, int32 and uint32.
+//     16/32/64 lanes per row, the row in registers, no workgroup barrier.
 //   k_topk_rsel  (rows <= 32768 of <= 4-byte elements, large k or any dtype;
 //     longer rows in segments of <= 32768 plus the merge): the row in
 //     registers, an exact radix select, a bitonic sort of the k.
@@ -120,6 +120,12 @@ __device__ __forceinline__ float selected_value(const float* p, uint32_t key, ui
 // the key of padding past a row's end.
 __device__ __forceinline__ uint32_t i2key_sel(float f, uint32_t smask, uint32_t lmask) {
     return __float_as_uint(f) ^ smask ^ lmask;
+}
+
+// Key of one element of a float32 (ikind 0), int32 (1) or uint32 (2) row.
+__device__ __forceinline__ uint32_t elem_key(float f, int largest, int ikind) {
+    const uint32_t lm = largest ? 0u : 0xffffffffu;
+    return ikind ? i2key_sel(f, ikind == 1 ? 0x80000000u : 0u, lm) : f2key_sel(f, lm);
 }
 
 __device__ __forceinline__ unsigned long long comp_key(uint32_t key, uint32_t idx) {
@@ -463,7 +469,7 @@ __device__ uint32_t wave_kth_bound(const unsigned long long* list, uint32_t* his
 // composites in cand[0..k) (unordered).  hi - lo >= k.
 template <int NT>
 __device__ void exact_select(BlockScratch& bs, unsigned long long* cand, const float* p, int lo, int hi, int k,
-                             int largest) {
+                             int largest, int ikind) {
     constexpr int NW = NT / 64;
     const int tid = threadIdx.x;
     const int lane = __lane_id();
@@ -474,7 +480,7 @@ __device__ void exact_select(BlockScratch& bs, unsigned long long* cand, const f
         if (tid < 256) bs.hist[tid] = 0;
         __syncthreads();
         for (int e = lo + tid; e < hi; e += NT) {
-            const uint32_t key = f2key(p[e], largest);
+            const uint32_t key = elem_key(p[e], largest, ikind);
             if ((key & pmask) == prefix) atomicAdd(&bs.hist[(key >> shift) & 255u], 1u);
         }
         __syncthreads();
@@ -499,7 +505,7 @@ __device__ void exact_select(BlockScratch& bs, unsigned long long* cand, const f
     __syncthreads();
     for (int base = lo; base < hi; base += NT) {
         const int e = base + tid;
-        const uint32_t key = (e < hi) ? f2key(p[e], largest) : 0u;
+        const uint32_t key = (e < hi) ? elem_key(p[e], largest, ikind) : 0u;
         const bool gt = (e < hi) && key > T;
         const bool eq = (e < hi) && key == T;
         if (gt) cand[atomicAdd(&bs.count, 1)] = comp_key(key, (uint32_t)e);
@@ -530,7 +536,7 @@ __device__ __forceinline__ void write_segment(const TopkArgs& a, long long row, 
     } else if (a.nseg == 1) {
         for (int i = threadIdx.x; i < k; i += blockDim.x) {
             const uint32_t idx = comp_index(sel[i]);
-            a.out_v[row * k + i] = selected_value(p, (uint32_t)(sel[i] >> 32), idx, a.largest);
+            a.out_v[row * k + i] = a.ikind ? p[idx] : selected_value(p, (uint32_t)(sel[i] >> 32), idx, a.largest);
             a.out_i[row * k + i] = (long long)idx;
         }
     } else {
@@ -598,8 +604,19 @@ __device__ __forceinline__ void load_slice(float4 (&cur)[SV], __amdgpu_buffer_rs
 // threshold).  A slice wholly inside the segment (every one but the last; the
 // test is wave-uniform) takes no bounds test at all.
 template <int SV>
-__device__ __forceinline__ void slice_keys(const float4 (&cur)[SV], int base, int hi, int largest,
+__device__ __forceinline__ void slice_keys(const float4 (&cur)[SV], int base, int hi, int largest, int ikind,
                                            uint32_t (&key)[4 * SV]) {
+    if (ikind) {  // 32-bit integers (a wave-uniform branch around the float conversion)
+        const int lim = hi - base - 4 * (int)__lane_id();
+#pragma unroll
+        for (int j = 0; j < SV; ++j) {
+            key[4 * j + 0] = (256 * j + 0 < lim) ? elem_key(cur[j].x, largest, ikind) : 0u;
+            key[4 * j + 1] = (256 * j + 1 < lim) ? elem_key(cur[j].y, largest, ikind) : 0u;
+            key[4 * j + 2] = (256 * j + 2 < lim) ? elem_key(cur[j].z, largest, ikind) : 0u;
+            key[4 * j + 3] = (256 * j + 3 < lim) ? elem_key(cur[j].w, largest, ikind) : 0u;
+        }
+        return;
+    }
     if (hi - base >= 256 * SV) {
         const uint32_t lm = largest ? 0u : 0xffffffffu;
 #pragma unroll
@@ -662,7 +679,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
     const __amdgpu_buffer_rsrc_t rs = segment_rsrc(p + lo, hi - lo);
     load_slice<VEC, SV>(bufA, rs, w * kSl);
     if constexpr (PD == 2) load_slice<VEC, SV>(bufB, rs, (w + kW) * kSl);
-    slice_keys(bufA, lo + w * kSl, hi, largest, key);
+    slice_keys(bufA, lo + w * kSl, hi, largest, a.ikind, key);
     if constexpr (PD == 1) load_slice<VEC, SV>(bufA, rs, (w + kW) * kSl);
     if constexpr (PD == 2) load_slice<VEC, SV>(bufA, rs, (w + 2 * kW) * kSl);
     // the first slice of every wave gives the workgroup bound T0
@@ -729,12 +746,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
                 if (!filter(lo + c * kSl)) { over = true; break; }
                 c += kW;
                 if (c >= nsl) break;
-                slice_keys(bufB, lo + c * kSl, hi, largest, key);
+                slice_keys(bufB, lo + c * kSl, hi, largest, a.ikind, key);
                 load_slice<VEC, SV>(bufB, rs, (c + 2 * kW) * kSl);
                 if (!filter(lo + c * kSl)) { over = true; break; }
                 c += kW;
                 if (c >= nsl) break;
-                slice_keys(bufA, lo + c * kSl, hi, largest, key);
+                slice_keys(bufA, lo + c * kSl, hi, largest, a.ikind, key);
                 load_slice<VEC, SV>(bufA, rs, (c + 2 * kW) * kSl);
             }
         } else if (PD == 1 && NW == 16 && a.dyn) {
@@ -752,7 +769,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
             int nx = w + kW;  // already loading into bufA
             while (c < nsl) {
                 if (c != w) {
-                    slice_keys(bufA, lo + c * kSl, hi, largest, key);
+                    slice_keys(bufA, lo + c * kSl, hi, largest, a.ikind, key);
                     nx = grab();
                     load_slice<VEC, SV>(bufA, rs, nx * kSl);  // past the segment: reads 0, no traffic
                 }
@@ -764,7 +781,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
                 const int base = lo + c * kSl;
                 if (c != w) {
                     if constexpr (PD == 0) load_slice<VEC, SV>(bufA, rs, c * kSl);
-                    slice_keys(bufA, base, hi, largest, key);
+                    slice_keys(bufA, base, hi, largest, a.ikind, key);
                     if constexpr (PD == 1) {
                         load_slice<VEC, SV>(bufA, rs, (c + kW) * kSl);
                     }
@@ -814,8 +831,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
     unsigned long long* cand = sh.un;
     unsigned long long* other = &sh.wl[0][0];
     int m = bs.count;
-    if (any_over) {
-        exact_select<kT>(bs, cand, p, lo, hi, k, largest);
+    // fewer than k gathered: the segment has keys of 0 (integers only; the
+    // filter keeps keys >= 1), which the exact select takes
+    if (any_over || m < k) {
+        exact_select<kT>(bs, cand, p, lo, hi, k, largest, a.ikind);
         m = k;
     } else if (m > max(2 * k, 256)) {
         block_compact<kT>(bs, cand, other, m, k, Tf);
@@ -892,7 +911,16 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(6, 8))) void
         float4 cur[kV];
         load_chunk<VEC>(cur, p, cbase, hi);
         uint32_t key[4 * kV];
-        if (cbase + kCH <= hi) {  // whole chunk inside the segment (uniform): no bounds tests
+        if (a.ikind) {  // 32-bit integers
+#pragma unroll
+            for (int j = 0; j < kV; ++j) {
+                const int e = cbase + 4 * (j * kT + tid);
+                key[4 * j + 0] = (e + 0 < hi) ? elem_key(cur[j].x, largest, a.ikind) : 0u;
+                key[4 * j + 1] = (e + 1 < hi) ? elem_key(cur[j].y, largest, a.ikind) : 0u;
+                key[4 * j + 2] = (e + 2 < hi) ? elem_key(cur[j].z, largest, a.ikind) : 0u;
+                key[4 * j + 3] = (e + 3 < hi) ? elem_key(cur[j].w, largest, a.ikind) : 0u;
+            }
+        } else if (cbase + kCH <= hi) {  // whole chunk inside the segment (uniform): no bounds tests
             const uint32_t lm = largest ? 0u : 0xffffffffu;
 #pragma unroll
             for (int j = 0; j < kV; ++j) {
@@ -959,8 +987,8 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(6, 8))) void
     __syncthreads();
 
     int m = bs.count;
-    if (over) {
-        exact_select<kT>(bs, sh.list[0], p, lo, hi, k, largest);
+    if (over || m < k) {  // m < k: keys of 0 in an integer segment (see k_topk_wave)
+        exact_select<kT>(bs, sh.list[0], p, lo, hi, k, largest, a.ikind);
         m = k;
         cur_list = 0;
     }
@@ -2186,9 +2214,9 @@ int dtype_size(int32_t dtype) {
 // Large k takes the radix-select kernel (any k <= cols, any dtype); so does
 // k > 128, k > 64 on rows shorter than the wave kernel's minimum segment
 // (8192, or 4096 where wave4 picks 4-wave workgroups), and every input dtype
-// but float32.
+// but float32, int32 and uint32.
 bool radix_route(long long rows, long long cols, long long k, int32_t dtype = TPR_FLOAT32) {
-    if (k > kKMax || dtype != TPR_FLOAT32) return true;
+    if (k > kKMax || (dtype != TPR_FLOAT32 && dtype != TPR_INT32 && dtype != TPR_UINT32)) return true;
     if (knobs().topk_radix < 0 || knobs().topk_fallback) return false;
     if (knobs().topk_radix > 0) return true;
     return k > kWaveK || (k > kWave4K && cols < 2 * kWaveMinSeg) ||
@@ -2358,9 +2386,6 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     const bool short_ok = (k <= kShortMaxK || short_exact(rows, cols, k)) && cols <= kShortMaxCols &&
                           3 * row_stride + cols < (1LL << 29);
     const bool short_on = knobs().topk_short >= 0 && knobs().topk_fallback == 0 && knobs().splits <= 0;
-    // 32-bit integer rows the lane-group kernel holds take it rather than the
-    // radix select (the rows fit its registers, so no workspace either way).
-    if (a.ikind != 0 && short_ok && short_on && knobs().topk_radix <= 0) return launch_short(a, vec, st);
     if (radix && rsel_route(cols, dtype))
         return launch_rsel(a, dtype, st);
     if (const int ns = radix ? rsel_segments(cols, k, dtype) : 0) {

@@ -469,3 +469,34 @@ def test_short_rows_32bit_integers(dt):
             ev, ei = O.topk_any(np.ascontiguousarray(x[:, :2999]), k, largest)
             np.testing.assert_array_equal(gi.cpu().numpy(), ei)
             np.testing.assert_array_equal(gv.cpu().numpy(), ev)
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.uint32])
+@pytest.mark.parametrize("knob", [("topk_short", 0), ("topk_short", -1), ("topk_fallback", 1)])
+def test_long_rows_32bit_integers(dt, knob):
+    """int32 / uint32 through the wave and workgroup kernels (and the merge of
+    split rows): rows where fewer than k elements have a non-zero key take the
+    exact select; topk_short = -1 sends short rows to the workgroup kernels,
+    topk_fallback = 1 forces the exact select everywhere."""
+    _capi.debug_set(*knob)
+    rng = np.random.default_rng(78)
+    info = np.iinfo(dt)
+    shapes = [(600, 1000, (8, 64)), (1100, 8192, (1, 50, 128)), (300, 20000, (16, 100, 256)),
+              (5, 70000, (10, 200)), (1100, 5000, (64, 200))]
+    for rows, cols, ks in shapes:
+        x = rng.integers(info.min, info.max, size=(rows, cols), dtype=dt, endpoint=True)
+        x[0] = info.min
+        x[1] = info.max
+        x[2] = np.where(rng.random(cols) < 0.995, info.min, x[2])
+        x[3] = np.where(rng.random(cols) < 0.995, info.max, x[3])
+        x[4] = x[4] % 3
+        t = torch.from_numpy(x).cuda()
+        for k in ks:
+            for largest in (True, False):
+                print(f"case topk dtype={np.dtype(dt).name} {knob} shape={x.shape} k={k} largest={largest}",
+                      flush=True)
+                gv, gi = _capi.topk(t, k, largest)
+                torch.cuda.synchronize()
+                ev, ei = O.topk_any(x, k, largest)
+                np.testing.assert_array_equal(gi.cpu().numpy(), ei)
+                np.testing.assert_array_equal(gv.cpu().numpy(), ev)
