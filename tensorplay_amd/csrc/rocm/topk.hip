@@ -1824,6 +1824,30 @@ __device__ __forceinline__ void rsel_load(uint32_t (&key)[EPT], const void* base
             return;
         }
     }
+    if constexpr (sizeof(T) < 4) {
+        if ((reinterpret_cast<uintptr_t>(base) & (4 * sizeof(T) - 1)) == 0) {
+            // a group of four 1- or 2-byte elements is one 32- or 64-bit load;
+            // only the group that straddles the row end loads element-wise
+            using W = typename std::conditional<sizeof(T) == 1, uint32_t, unsigned long long>::type;
+            using U = typename std::make_unsigned<T>::type;
+#pragma unroll
+            for (int g = 0; g < EPT / 4; ++g) {
+                const int e0 = (g * NT + t) * 4;
+                if (e0 + 3 < cols) {
+                    const W wv = *reinterpret_cast<const W*>(p + e0);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const U u = (U)(wv >> (8 * sizeof(T) * q));
+                        key[4 * g + q] = (uint32_t)SortKey<T>::of(__builtin_bit_cast(T, u), largest);
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) key[4 * g + q] = e0 + q < cols ? (uint32_t)SortKey<T>::of(p[e0 + q], largest) : 0u;
+                }
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
         const int e = rsel_idx<NT>(j, t);
@@ -1880,7 +1904,8 @@ __global__ __launch_bounds__(NT) void k_topk_rsel(TopkArgs a, int dtype, int sor
     uint32_t prefix = 0, pmask = 0;
     int kk = k;
     bool whole = false;  // every key of the class is taken
-    for (int hi = 32; hi > 0 && !whole; hi -= 11) {
+    // keys of 1- and 2-byte elements are below 2^8 / 2^16: one / two passes
+    for (int hi = 8 * dtype_bytes(dtype); hi > 0 && !whole; hi -= 11) {
         const int shift = hi > 11 ? hi - 11 : 0;
         const uint32_t dmask = (1u << (hi - shift)) - 1u;
 #pragma unroll

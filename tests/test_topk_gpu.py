@@ -500,3 +500,29 @@ def test_long_rows_32bit_integers(dt, knob):
                 ev, ei = O.topk_any(x, k, largest)
                 np.testing.assert_array_equal(gi.cpu().numpy(), ei)
                 np.testing.assert_array_equal(gv.cpu().numpy(), ev)
+
+
+@pytest.mark.parametrize("dt", [np.int8, np.uint8, np.int16, np.uint16, np.bool_])
+def test_small_integer_rows(dt):
+    """1- and 2-byte elements through the register radix select: one / two
+    radix passes, grouped loads on aligned rows (cols a multiple of 4 or 8 here)
+    and element loads on the others, ties everywhere (few distinct values)."""
+    rng = np.random.default_rng(79)
+    for rows, cols, ks in [(2000, 1024, (1, 8, 100)), (300, 4096, (16, 64, 1000)), (77, 1003, (5, 50)),
+                           (40, 32768, (300,)), (3, 100000, (256,))]:
+        if dt == np.bool_:
+            x = rng.random((rows, cols)) < 0.1
+        else:
+            info = np.iinfo(dt)
+            x = rng.integers(info.min, info.max, size=(rows, cols), dtype=dt, endpoint=True)
+            x[0] = info.min
+            x[1] = info.max
+        t = torch.from_numpy(x).cuda()
+        for k in ks:
+            for largest in (True, False):
+                print(f"case topk dtype={np.dtype(dt).name} shape={x.shape} k={k} largest={largest}", flush=True)
+                gv, gi = _capi.topk(t, k, largest)
+                torch.cuda.synchronize()
+                ev, ei = O.topk_any(x, k, largest)
+                np.testing.assert_array_equal(gi.cpu().numpy(), ei)
+                np.testing.assert_array_equal(gv.cpu().numpy().view(np.uint8), ev.view(np.uint8))
