@@ -92,16 +92,17 @@ def reduce_call(torch, capi, x, op, dims, stream, correction=1):
 
 def topk_call(torch, capi, x, k, stream):
     rows, cols = x.shape
-    vals = torch.empty((rows, k), dtype=torch.float32, device=x.device)
+    dt = capi._torch_dtypes()[x.dtype]
+    vals = torch.empty((rows, k), dtype=x.dtype, device=x.device)
     idx = torch.empty((rows, k), dtype=torch.int64, device=x.device)
     L = capi.lib()
-    wsb = L.tpr_topk_workspace_bytes(capi.FLOAT32, rows, cols, k)
+    wsb = L.tpr_topk_workspace_bytes(dt, rows, cols, k)
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
-    c = Call(L.tpr_topk, (ctypes.c_void_p(x.data_ptr()), capi.FLOAT32, rows, cols, x.stride(0), k, 1, 1,
+    c = Call(L.tpr_topk, (ctypes.c_void_p(x.data_ptr()), dt, rows, cols, x.stride(0), k, 1, 1,
                           ctypes.c_void_p(vals.data_ptr()), ctypes.c_void_p(idx.data_ptr()),
                           ctypes.c_void_p(ws.data_ptr()), wsb, stream))
     c.keep = (vals, idx, ws)
-    c.out_bytes = rows * k * (4 + 8)
+    c.out_bytes = rows * k * (x.element_size() + 8)
     return c
 
 
@@ -508,15 +509,23 @@ def run_sections(torch, capi, only, stream, steps, warmup, bufs, keep):
         del cs
     if "topk_short" in only:
         # many short rows (lane groups per row), a large k (rows held in registers) and k = 256 over C5-sized
-        # vocabulary rows (the wave kernel's 512-entry lists), beside the BASELINE top-k configs
+        # vocabulary rows (the wave kernel's 512-entry lists), beside the BASELINE top-k configs; int32 rows
+        # (full-range values: the float filter kernels on integer keys) and int8 rows (register radix select)
         ets = {}
-        for (rows, cols, k) in ((65536, 256, 8), (16384, 1024, 32), (4096, 2048, 1000), (256, 151936, 256)):
-            nb = max(3, (768 << 20) // (rows * cols * 4))
+        for (rows, cols, k, dt) in ((65536, 256, 8, "f32"), (16384, 1024, 32, "f32"), (4096, 2048, 1000, "f32"),
+                                    (256, 151936, 256, "f32"), (16384, 1024, 32, "i32"), (1024, 32768, 64, "i32"),
+                                    (16384, 1024, 32, "i8")):
+            esz = {"f32": 4, "i32": 4, "i8": 1}[dt]
+            nb = max(3, (768 << 20) // (rows * cols * esz))
             bs = [gen(torch, (rows, cols), "uniform", 7000 + i, dev) for i in range(nb)]
+            if dt == "i32":
+                bs = [(b * 2.0 ** 31).clamp(-2.0 ** 31, 2.0 ** 31 - 1).to(torch.int32) for b in bs]
+            elif dt == "i8":
+                bs = [(b * 127.0).round().to(torch.int8) for b in bs]
             cs = [topk_call(torch, capi, b, k, stream) for b in bs]
-            r = timed(torch, cs, max(steps, 12), warmup, rows * cols * 4 + cs[0].out_bytes)
+            r = timed(torch, cs, max(steps, 12), warmup, rows * cols * esz + cs[0].out_bytes)
             r["rows_per_s"] = round(rows / (r["ms"] * 1e-3), 1)
-            ets[f"topk{k}_{rows}x{cols}"] = r
+            ets[f"topk{k}_{rows}x{cols}" + ("" if dt == "f32" else "_" + ("int32" if dt == "i32" else "int8"))] = r
             del bs, cs
         extras["topk_short_rows"] = ets
     return extras
