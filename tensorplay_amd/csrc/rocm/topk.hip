@@ -1,6 +1,6 @@
 // gfx950 top-k along the last dim of a [rows, cols] view (float32, int32 and
-// uint32 through the filter kernels below; every dtype through the
-// radix-select kernels).
+// uint32 through the filter kernels below, 1- and 2-byte integers through the
+// lane-group one; every dtype through the radix-select kernels).
 //
 // TensorPlay has no topk (grep of /root/reference finds no schema, kernel or
 // test); this implements the definition in tpr_rocm.h: order by a 32-bit
@@ -38,7 +38,8 @@
 //     has >= k candidates at or above it in the publishing wave's list, so it
 //     bounds every wave.
 //   k_topk_short (rows <= 4096, k <= 64, or k <= 128 on many rows <= 2048):
-//     16/32/64 lanes per row, the row in registers, no workgroup barrier.
+//     16/32/64 lanes per row, the row in registers, no workgroup barrier;
+//     also 1- and 2-byte integers and bool on 16-byte aligned rows.
 //   k_topk_rsel  (rows <= 32768 of <= 4-byte elements, large k or any dtype;
 //     longer rows in segments of <= 32768 plus the merge): the row in
 //     registers, an exact radix select, a bitonic sort of the k.
@@ -1170,18 +1171,38 @@ __device__ __forceinline__ uint32_t group_hist_threshold(const uint32_t* hist, i
     return __shfl(tn, grp * L + hl, 64);
 }
 
-// Output r of a row: the value (exact, from the key or the input) and index.
+// Output r of a row: the value (exact, from the key or the input, in the
+// input's dtype of EB bytes) and index.
+template <int EB>
 __device__ __forceinline__ void write_ranked(const TopkArgs& a, long long row, int k, const float* p, int largest,
                                              int r, unsigned long long c) {
     const uint32_t idx = comp_index(c);
-    a.out_v[row * k + r] = a.ikind ? p[idx] : selected_value(p, (uint32_t)(c >> 32), idx, largest);
+    if constexpr (EB == 1) {
+        reinterpret_cast<uint8_t*>(a.out_v)[row * k + r] = reinterpret_cast<const uint8_t*>(p)[idx];
+    } else if constexpr (EB == 2) {
+        reinterpret_cast<uint16_t*>(a.out_v)[row * k + r] = reinterpret_cast<const uint16_t*>(p)[idx];
+    } else {
+        a.out_v[row * k + r] = a.ikind ? p[idx] : selected_value(p, (uint32_t)(c >> 32), idx, largest);
+    }
     a.out_i[row * k + r] = (long long)idx;
 }
 
-template <int L, int E4, bool VEC, bool LG>
+// Element index of key q of lane sl in the lane-group kernel: keys run over the
+// lane's 16-byte vectors j, their dwords c and, for elements of EB < 4 bytes,
+// the 4 / EB elements of a dword (element order inside a lane's vector).
+template <int L, int EB>
+__device__ __forceinline__ int short_elem(int q, int sl) {
+    constexpr int EPW = 4 / EB;
+    const int w = q / EPW;
+    return (4 * ((w >> 2) * L + sl) + (w & 3)) * EPW + q % EPW;
+}
+
+template <int L, int E4, bool VEC, bool LG, int EB = 4>
 __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
+    static_assert(EB == 4 || VEC, "1- and 2-byte rows: 16-byte aligned rows only");
     constexpr int G = 64 / L;
-    constexpr int E = 4 * E4;
+    constexpr int EPW = 4 / EB;     // elements per dword
+    constexpr int E = 4 * E4 * EPW;  // keys per lane
     constexpr int C = 8 * L;  // candidate capacity of one row
     constexpr int RPB = (kShortT / 64) * G;
     __shared__ unsigned long long cl[RPB][C];  // C * 8 >= 1 KiB: also the row's histogram (see below)
@@ -1194,7 +1215,8 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
     const int cols = a.cols;
     const int k = a.k;
     constexpr int largest = LG ? 1 : 0;
-    const float* p = a.in + (live ? row * a.row_stride : 0);
+    const float* p = reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.in) +
+                                                    (live ? row * a.row_stride * EB : 0));
     // One buffer resource per wave (a per-lane resource would make every load
     // a loop over the wave's distinct rows): it spans the wave's live rows, the
     // lane group's row starts at grp * row_stride, and elements past a row's
@@ -1202,9 +1224,15 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
     // (G - 1) * row_stride + cols below 2^29 floats.
     const long long row0 = (long long)blockIdx.x * RPB + __builtin_amdgcn_readfirstlane(threadIdx.x / 64) * G;
     const long long nlive = min((long long)G, max(0LL, a.rows - row0));
-    const __amdgpu_buffer_rsrc_t rs = segment_rsrc(
-        a.in + (nlive > 0 ? row0 * a.row_stride : 0), nlive > 0 ? (int)((nlive - 1) * a.row_stride + cols) : 0);
-    const int rbase = grp * (int)a.row_stride * 4;
+    // (1- and 2-byte rows: the range is rounded up to whole dwords, so the
+    // dword holding a row's last elements is read whole; the rest of it is
+    // masked below, and rows start 16-byte aligned, so it never crosses into
+    // another page.)
+    const char* wbase = reinterpret_cast<const char*>(a.in) + (nlive > 0 ? row0 * a.row_stride * EB : 0);
+    const int nbytes = nlive > 0 ? (int)(((nlive - 1) * a.row_stride + cols) * EB + 3) & ~3 : 0;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wbase), (short)0, nbytes, kBufWord3);
+    const int rbase = grp * (int)a.row_stride * EB;
 
     float4 x[E4];
 #pragma unroll
@@ -1220,7 +1248,24 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
     }
     uint32_t key[E];
     constexpr uint32_t lm = LG ? 0u : 0xffffffffu;
-    if (a.ikind != 0) {  // 32-bit integers
+    if constexpr (EB < 4) {  // 1- and 2-byte integers (ikind 1 signed, 2 unsigned or bool)
+        constexpr uint32_t em = EB == 1 ? 0xffu : 0xffffu;
+        const uint32_t sm = a.ikind == 1 ? (em >> 1) + 1u : 0u;
+#pragma unroll
+        for (int j = 0; j < E4; ++j) {
+            const uint32_t wv[4] = {__float_as_uint(x[j].x), __float_as_uint(x[j].y), __float_as_uint(x[j].z),
+                                    __float_as_uint(x[j].w)};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+#pragma unroll
+                for (int s = 0; s < EPW; ++s) {
+                    const int q = (4 * j + c) * EPW + s;
+                    const uint32_t kv = (((wv[c] >> (8 * EB * s)) & em) ^ sm ^ lm) & em;
+                    key[q] = short_elem<L, EB>(q, sl) < cols ? kv : 0u;
+                }
+            }
+        }
+    } else if (a.ikind != 0) {  // 32-bit integers
         const uint32_t sm = a.ikind == 1 ? 0x80000000u : 0u;
 #pragma unroll
         for (int j = 0; j < E4; ++j) {
@@ -1291,7 +1336,7 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
         int pos = incl - n;
 #pragma unroll
         for (int q = 0; q < E; ++q) {
-            if (key[q] >= T) list[pos++] = comp_key(key[q], (uint32_t)(4 * ((q >> 2) * L + sl) + (q & 3)));
+            if (key[q] >= T) list[pos++] = comp_key(key[q], (uint32_t)short_elem<L, EB>(q, sl));
         }
         if (c * c > 256 * L && c > 2 * k) {
             // Raise the bound with a 256-bin histogram of the candidates over
@@ -1350,21 +1395,22 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
         int pos = gincl - ng;
 #pragma unroll
         for (int q = 0; q < E; ++q) {
-            if (key[q] > pre) list[pos++] = comp_key(key[q], (uint32_t)(4 * ((q >> 2) * L + sl) + (q & 3)));
+            if (key[q] > pre) list[pos++] = comp_key(key[q], (uint32_t)short_elem<L, EB>(q, sl));
         }
-        // keys == pre in index order (vector j, lane, component) until k are taken
+        // keys == pre in index order (vector j, lane, dword, element) until k are taken
         int taken = cgt;
+        constexpr int KV = 4 * EPW;  // keys per vector
 #pragma unroll
         for (int j = 0; j < E4; ++j) {
             int ne = 0;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) ne += (key[4 * j + q] == pre) ? 1 : 0;
+            for (int q = 0; q < KV; ++q) ne += (key[KV * j + q] == pre) ? 1 : 0;
             const int einc = group_scan<L>(ne, sl);
             int at = taken + einc - ne;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                if (key[4 * j + q] == pre) {
-                    if (at < k) list[at] = comp_key(pre, (uint32_t)(4 * (j * L + sl) + q));
+            for (int q = 0; q < KV; ++q) {
+                if (key[KV * j + q] == pre) {
+                    if (at < k) list[at] = comp_key(pre, (uint32_t)short_elem<L, EB>(KV * j + q, sl));
                     ++at;
                 }
             }
@@ -1387,7 +1433,7 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
                 if (live) sample_from_sel(a, row, p, list, k);
                 return;
             }
-            if (sl < k && live) write_ranked(a, row, k, p, largest, sl, x[0]);
+            if (sl < k && live) write_ranked<EB>(a, row, k, p, largest, sl, x[0]);
         } else {
             unsigned long long x[2] = {2 * sl < c ? list[2 * sl] : 0ull, 2 * sl + 1 < c ? list[2 * sl + 1] : 0ull};
             wave_sort_desc<2>(x);
@@ -1399,8 +1445,8 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
                 if (live) sample_from_sel(a, row, p, list, k);
                 return;
             }
-            if (2 * sl < k && live) write_ranked(a, row, k, p, largest, 2 * sl, x[0]);
-            if (2 * sl + 1 < k && live) write_ranked(a, row, k, p, largest, 2 * sl + 1, x[1]);
+            if (2 * sl < k && live) write_ranked<EB>(a, row, k, p, largest, 2 * sl, x[0]);
+            if (2 * sl + 1 < k && live) write_ranked<EB>(a, row, k, p, largest, 2 * sl + 1, x[1]);
         }
         return;
     }
@@ -1418,11 +1464,7 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
             for (int j = 0; j < c; ++j) r += (list[j] > ci) ? 1 : 0;
             rk[q] = r;
             cv[q] = ci;
-            if (r < k && live && !a.sample) {
-                const uint32_t idx = comp_index(ci);
-                a.out_v[row * k + r] = a.ikind ? p[idx] : selected_value(p, (uint32_t)(ci >> 32), idx, largest);
-                a.out_i[row * k + r] = (long long)idx;
-            }
+            if (r < k && live && !a.sample) write_ranked<EB>(a, row, k, p, largest, r, ci);
         }
     }
     if (a.sample) {  // L == 64 (one row per wave) when sampling
@@ -2317,6 +2359,41 @@ void launch_short_l(const TopkArgs& a, bool vec, hipStream_t st) {
     else launch_short_le<L, 16>(a, vec, st);
 }
 
+// 1- and 2-byte integer rows (16-byte aligned): E4 vectors of 16 / EB
+// elements per lane.
+template <int L, int E4, int EB>
+void launch_short_small_le(const TopkArgs& a, hipStream_t st) {
+    constexpr int RPB = (kShortT / 64) * (64 / L);
+    const dim3 grid((unsigned)((a.rows + RPB - 1) / RPB));
+    if (a.largest) hipLaunchKernelGGL((k_topk_short<L, E4, true, true, EB>), grid, dim3(kShortT), 0, st, a);
+    else hipLaunchKernelGGL((k_topk_short<L, E4, true, false, EB>), grid, dim3(kShortT), 0, st, a);
+}
+
+template <int L, int EB>
+void launch_short_small_l(const TopkArgs& a, hipStream_t st) {
+    constexpr int per = 16 / EB * L;  // elements of one vector round of the L lanes
+    const int e4 = (a.cols + per - 1) / per;  // <= 4 * EB (cols <= 4096, L >= cols / 16 below 64 lanes)
+    if (e4 <= 1) launch_short_small_le<L, 1, EB>(a, st);
+    else if (e4 <= 2) launch_short_small_le<L, 2, EB>(a, st);
+    else if (EB == 1 || e4 <= 4) launch_short_small_le<L, 4, EB>(a, st);
+    else if constexpr (EB == 2) launch_short_small_le<L, 8, EB>(a, st);
+}
+
+int launch_short_small(const TopkArgs& a, int eb, hipStream_t st) {
+    int L = 16;  // as launch_short: L >= 2k, and L >= cols / 16 up to 64 lanes
+    while (L < 64 && (L < 2 * a.k || L * 16 < a.cols)) L *= 2;
+    if (eb == 1) {
+        if (L == 16) launch_short_small_l<16, 1>(a, st);
+        else if (L == 32) launch_short_small_l<32, 1>(a, st);
+        else launch_short_small_l<64, 1>(a, st);
+    } else {
+        if (L == 16) launch_short_small_l<16, 2>(a, st);
+        else if (L == 32) launch_short_small_l<32, 2>(a, st);
+        else launch_short_small_l<64, 2>(a, st);
+    }
+    return check_launch("k_topk_short");
+}
+
 int launch_short(const TopkArgs& a, bool vec, hipStream_t st) {
     // L >= 2k where possible: the bound is then the k-th largest of at least
     // 2k lane maxima, well above their minimum, so fewer candidates reach the
@@ -2392,7 +2469,8 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     a.row_stride = row_stride;
     a.k = (int)k;
     a.largest = largest ? 1 : 0;
-    a.ikind = dtype == TPR_INT32 ? 1 : dtype == TPR_UINT32 ? 2 : 0;
+    a.ikind = (dtype == TPR_INT32 || dtype == TPR_INT16 || dtype == TPR_INT8) ? 1
+              : (dtype == TPR_UINT32 || dtype == TPR_UINT16 || dtype == TPR_UINT8 || dtype == TPR_BOOL) ? 2 : 0;
     a.force_fallback = knobs().topk_fallback ? 1 : 0;
     a.nseg = pl.nseg;
     a.seg_len = pl.seg_len;
@@ -2411,6 +2489,12 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     const bool short_ok = (k <= kShortMaxK || short_exact(rows, cols, k)) && cols <= kShortMaxCols &&
                           3 * row_stride + cols < (1LL << 29);
     const bool short_on = knobs().topk_short >= 0 && knobs().topk_fallback == 0 && knobs().splits <= 0;
+    // 1- and 2-byte integer rows the lane-group kernel can hold, 16-byte
+    // aligned: that kernel on integer keys (else the register radix select)
+    const int eb = dtype_size(dtype);
+    if (eb < 4 && short_ok && short_on && knobs().topk_radix <= 0 &&
+        (reinterpret_cast<uintptr_t>(in) & 15u) == 0 && (rows == 1 || (row_stride * eb) % 16 == 0))
+        return launch_short_small(a, eb, st);
     if (radix && rsel_route(cols, dtype))
         return launch_rsel(a, dtype, st);
     if (const int ns = radix ? rsel_segments(cols, k, dtype) : 0) {

@@ -526,3 +526,36 @@ def test_small_integer_rows(dt):
                 ev, ei = O.topk_any(x, k, largest)
                 np.testing.assert_array_equal(gi.cpu().numpy(), ei)
                 np.testing.assert_array_equal(gv.cpu().numpy().view(np.uint8), ev.view(np.uint8))
+
+
+@pytest.mark.parametrize("dt", [np.int8, np.uint8, np.int16, np.uint16, np.bool_])
+def test_small_integer_short_rows(dt):
+    """1- and 2-byte rows of <= 4096 with 16-byte aligned rows through the
+    lane-group kernel (16 or 8 elements per lane vector): views of a wider
+    buffer give odd column counts (a row's last dword partly past its end),
+    k = cols, extreme-value rows (keys of 0) and heavy ties."""
+    rng = np.random.default_rng(80)
+    for rows, width, cols, ks in [(300, 1024, 1024, (1, 8, 32, 64)), (300, 1024, 1001, (1, 37, 64)),
+                                  (97, 16, 5, (1, 5)), (64, 64, 63, (63,)), (200, 4096, 4096, (1, 16, 64)),
+                                  (500, 256, 200, (8, 50)), (3000, 2048, 2047, (65, 128))]:
+        if dt == np.bool_:
+            x = rng.random((rows, width)) < 0.2
+        else:
+            info = np.iinfo(dt)
+            x = rng.integers(info.min, info.max, size=(rows, width), dtype=dt, endpoint=True)
+            x[0] = info.min
+            x[1] = info.max
+            x[2] = np.where(rng.random(width) < 0.95, info.min, x[2])
+            x[3] = np.where(rng.random(width) < 0.95, info.max, x[3])
+            x[4] = x[4] % 3
+        t = torch.from_numpy(x).cuda()[:, :cols]
+        xc = np.ascontiguousarray(x[:, :cols])
+        for k in ks:
+            for largest in (True, False):
+                print(f"case topk dtype={np.dtype(dt).name} rows={rows} width={width} cols={cols} k={k} "
+                      f"largest={largest}", flush=True)
+                gv, gi = _capi.topk(t, k, largest)
+                torch.cuda.synchronize()
+                ev, ei = O.topk_any(xc, k, largest)
+                np.testing.assert_array_equal(gi.cpu().numpy(), ei)
+                np.testing.assert_array_equal(gv.cpu().numpy().view(np.uint8), ev.view(np.uint8))
