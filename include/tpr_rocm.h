@@ -298,7 +298,10 @@ const char* tpr_last_error(void);
 /* ABI version (major << 16 | minor); 1.4 accepts UINT16/32/64 reduction inputs. */
 int32_t tpr_abi_version(void);
 
-/* Tuning / test hook: force plan choices.  Keys: "splits" (row/full/column
+/* Tuning / test hook, exported by the test build libtpr_rocm_dev.so only (built
+ * with -DTPR_DEBUG_KNOBS); the shipped libtpr_rocm.so does not export it and
+ * plans every launch from its arguments and the device alone.  Forces plan
+ * choices.  Keys: "splits" (row/full/column
  * split count, 0 = automatic), "lanes" (threads per row in the row kernel, 16..1024,
  * 0 = automatic), "general" (1 = always use the generic strided kernel),
  * "topk_fallback" (1 = always take top-k's exact multi-pass path), "tx" (64, 128
@@ -321,7 +324,7 @@ int32_t tpr_abi_version(void);
  * slice order in the 16-wave kernel), "rowreg" (-1 = no register-row sum
  * kernel), "nt" (1 / -1 = nontemporal accesses always / never where a kernel
  * chooses them, 0 = automatic).
- * Process-wide; not synchronised with concurrent launches.  Returns
+ * Process-wide in the test build; not synchronised with concurrent launches.  Returns
  * TPR_ERR_INVALID_ARG for an unknown key.  No reference counterpart. */
 int tpr_debug_set(const char* key, int64_t value);
 

@@ -6,13 +6,17 @@ the same entry points directly.  Device memory and streams come from PyTorch
 (plumbing only): tensors are passed as raw device pointers + element strides.
 
 The library must have been built (python tensorplay_amd/build.py); loading
-fails loudly otherwise -- there is no CPU fallback.
+fails loudly otherwise -- there is no CPU fallback.  With TPR_ROCM_DEV=1 in the
+environment (the test suite sets it) this loads the test build
+libtpr_rocm_dev.so instead, the same kernels plus the plan-override hook
+tpr_debug_set; the shipped libtpr_rocm.so has no such hook.
 """
 import ctypes
 import os
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "libtpr_rocm.so")
+DEV_LIB_PATH = os.path.join(PKG, "libtpr_rocm_dev.so")
 
 MAX_DIMS = 8
 
@@ -88,12 +92,18 @@ class SoftmaxDesc(ctypes.Structure):
 _lib = None
 
 
+def lib_path():
+    """The library lib() loads: the test build when TPR_ROCM_DEV=1."""
+    return DEV_LIB_PATH if os.environ.get("TPR_ROCM_DEV") == "1" else LIB_PATH
+
+
 def lib():
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            raise ImportError(f"{LIB_PATH} is not built; run `python tensorplay_amd/build.py`")
-        L = ctypes.CDLL(LIB_PATH)
+        path = lib_path()
+        if not os.path.exists(path):
+            raise ImportError(f"{path} is not built; run `python tensorplay_amd/build.py`")
+        L = ctypes.CDLL(path)
         vp, sz, i32, i64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_int64
         dp = ctypes.POINTER(ReduceDesc)
         i64p = ctypes.POINTER(ctypes.c_int64)
@@ -118,8 +128,9 @@ def lib():
         L.tpr_last_error.restype = ctypes.c_char_p
         L.tpr_abi_version.argtypes = []
         L.tpr_abi_version.restype = i32
-        L.tpr_debug_set.argtypes = [ctypes.c_char_p, i64]
-        L.tpr_debug_set.restype = ctypes.c_int
+        if hasattr(L, "tpr_debug_set"):  # test build only
+            L.tpr_debug_set.argtypes = [ctypes.c_char_p, i64]
+            L.tpr_debug_set.restype = ctypes.c_int
         L.tpr_softmax.argtypes = [ctypes.POINTER(SoftmaxDesc), vp, vp, vp, vp, sz, vp]
         L.tpr_reduce_backward_workspace_bytes.argtypes = [dp]
         L.tpr_reduce_backward_workspace_bytes.restype = sz
@@ -148,7 +159,10 @@ def _check(rc):
 
 
 def debug_set(key, value):
-    _check(lib().tpr_debug_set(key.encode(), int(value)))
+    L = lib()
+    if not hasattr(L, "tpr_debug_set"):
+        raise RuntimeError("plan overrides need the test build: set TPR_ROCM_DEV=1 before the library loads")
+    _check(L.tpr_debug_set(key.encode(), int(value)))
 
 
 def make_desc(op, shape, strides, reduce_dims, out_dtype, correction=1, count_override=0,

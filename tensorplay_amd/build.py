@@ -1,6 +1,9 @@
 """Build the native parts of tensorplay_amd in-tree for gfx950.
 
   libtpr_rocm.so   HIP kernels + the C-ABI launch layer (include/tpr_rocm.h)
+  libtpr_rocm_dev.so  the same with the plan-override hook tpr_debug_set
+                   (-DTPR_DEBUG_KNOBS): the test build, loaded by the tests
+                   that force plans; the shipped library has no mutable plan state
   _C<ext>          host core (tensor, dispatcher with the ROCm key, caching
                    allocator, reduction adapters) + Python bindings; links
                    libtpr_rocm.so
@@ -29,6 +32,7 @@ HIP_FLAGS = [
 ROCM_SOURCES = ["rocm/capi.cpp", "rocm/reduce.hip", "rocm/topk.hip", "rocm/copy.hip",
                 "rocm/softmax.hip", "rocm/loss.hip", "rocm/reduce_bwd.hip"]
 LIB_TPR = os.path.join(PKG, "libtpr_rocm.so")
+LIB_TPR_DEV = os.path.join(PKG, "libtpr_rocm_dev.so")
 
 
 def _run(cmd):
@@ -52,20 +56,33 @@ def _newer(target, deps):
     return any(os.path.getmtime(d) > t for d in deps)
 
 
-def build_tpr(force=True):
-    os.makedirs(BUILD, exist_ok=True)
+def _tpr_compiles(force, dev):
+    """(compile commands, objects) of one flavour of libtpr_rocm."""
+    bdir = os.path.join(BUILD, "dev") if dev else BUILD
+    os.makedirs(bdir, exist_ok=True)
     inc = ["-I", os.path.join(ROOT, "include"), "-I", os.path.join(CSRC, "rocm")]
     headers = [os.path.join(ROOT, "include", "tpr_rocm.h"), os.path.join(CSRC, "rocm", "common.h")]
+    extra = ["-DTPR_DEBUG_KNOBS"] if dev else []
     objs, cmds = [], []
     for src in ROCM_SOURCES:
         s = os.path.join(CSRC, src)
-        o = os.path.join(BUILD, os.path.basename(src) + ".o")
+        o = os.path.join(bdir, os.path.basename(src) + ".o")
         if force or _newer(o, [s] + headers):
             lang = ["-x", "hip"] if src.endswith(".cpp") else []
-            cmds.append([HIPCC] + HIP_FLAGS + inc + lang + ["-c", s, "-o", o])
+            cmds.append([HIPCC] + HIP_FLAGS + extra + inc + lang + ["-c", s, "-o", o])
         objs.append(o)
-    _run_all(cmds)
+    return cmds, objs
+
+
+def build_tpr(force=True, dev=True):
+    """libtpr_rocm.so and (dev=True) the test build libtpr_rocm_dev.so, compiled together."""
+    cmds, objs = _tpr_compiles(force, False)
+    dcmds, dobjs = _tpr_compiles(force, True) if dev else ([], [])
+    # the longest compiles first, so the pool drains evenly
+    _run_all(sorted(cmds + dcmds, key=lambda c: ("topk" not in c[-3], "reduce.hip" not in c[-3])))
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", LIB_TPR] + objs)
+    if dev:
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", LIB_TPR_DEV] + dobjs)
     return LIB_TPR
 
 

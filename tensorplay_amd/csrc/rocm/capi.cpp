@@ -43,10 +43,12 @@ DeviceInfo device_info() {
     return DeviceInfo{cus};
 }
 
+#ifdef TPR_DEBUG_KNOBS
 DebugKnobs& knobs() {
     static DebugKnobs k;
     return k;
 }
+#endif
 
 }  // namespace tpr
 
@@ -56,29 +58,16 @@ const char* tpr_last_error(void) { return tpr::g_last_error.c_str(); }
 
 int32_t tpr_abi_version(void) { return (1 << 16) | 4; }
 
+#ifdef TPR_DEBUG_KNOBS
+// Test builds only (libtpr_rocm_dev.so).
 int tpr_debug_set(const char* key, int64_t value) {
     if (!key) return tpr::fail(TPR_ERR_INVALID_ARG, "tpr_debug_set: null key");
     auto& k = tpr::knobs();
-    if (!std::strcmp(key, "splits")) k.splits = value;
-    else if (!std::strcmp(key, "lanes")) k.lanes = value;
-    else if (!std::strcmp(key, "general")) k.general = value;
-    else if (!std::strcmp(key, "topk_fallback")) k.topk_fallback = value;
-    else if (!std::strcmp(key, "tx")) k.tx = value;
-    else if (!std::strcmp(key, "topk_variant")) k.topk_variant = value;
-    else if (!std::strcmp(key, "topk_waves")) k.topk_waves = value;
-    else if (!std::strcmp(key, "unroll")) k.unroll = value;
-    else if (!std::strcmp(key, "colblock")) k.colblock = value;
-    else if (!std::strcmp(key, "nt")) k.nt = value;
-    else if (!std::strcmp(key, "smx_two_pass")) k.smx_two_pass = value;
-    else if (!std::strcmp(key, "smx_lanes")) k.smx_lanes = value;
-    else if (!std::strcmp(key, "smx_split")) k.smx_split = value;
-    else if (!std::strcmp(key, "smx_res")) k.smx_res = value;
-    else if (!std::strcmp(key, "rowreg")) k.rowreg = value;
-    else if (!std::strcmp(key, "topk_short")) k.topk_short = value;
-    else if (!std::strcmp(key, "topk_radix")) k.topk_radix = value;
-    else if (!std::strcmp(key, "topk_dyn")) k.topk_dyn = value;
-    else return tpr::fail(TPR_ERR_INVALID_ARG, std::string("tpr_debug_set: unknown key ") + key);
-    return TPR_OK;
+#define TPR_KNOB_SET(name) if (!std::strcmp(key, #name)) { k.name = value; return TPR_OK; }
+    TPR_KNOB_LIST(TPR_KNOB_SET)
+#undef TPR_KNOB_SET
+    return tpr::fail(TPR_ERR_INVALID_ARG, std::string("tpr_debug_set: unknown key ") + key);
 }
+#endif
 
 }  // extern "C"

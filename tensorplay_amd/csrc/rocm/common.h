@@ -24,33 +24,32 @@ struct DeviceInfo {
 };
 DeviceInfo device_info();
 
-// Process-wide plan overrides for tests and tuning sweeps (tpr_debug_set).
-// All zero in normal use.  Each knob is an atomic, so a thread that sets one
-// while another plans a launch is not a data race; a launch reads each knob
-// once, but a sweep that changes knobs while other threads launch gets plans
-// that mix old and new values, so sweeps run single-threaded.
+// Plan overrides for tests and tuning sweeps.  The shipped library is built
+// without TPR_DEBUG_KNOBS: every knob is then the constant 0, the planners fold
+// it away, and the library holds no mutable plan state at all.  The test build
+// (libtpr_rocm_dev.so, -DTPR_DEBUG_KNOBS) exports tpr_debug_set, which writes
+// these process-wide atomics; a launch reads each knob once, but a sweep that
+// changes knobs while other threads launch gets plans that mix old and new
+// values, so sweeps run single-threaded.
+#define TPR_KNOB_LIST(X) X(splits) X(lanes) X(general) X(topk_fallback) X(tx) X(topk_variant) X(topk_waves) \
+    X(unroll) X(colblock) X(nt) X(smx_two_pass) X(smx_lanes) X(smx_split) X(smx_res) X(rowreg) X(topk_short) \
+    X(topk_radix) X(topk_dyn)
+#ifdef TPR_DEBUG_KNOBS
 using Knob = std::atomic<int64_t>;
 struct DebugKnobs {
-    Knob splits{0};
-    Knob lanes{0};
-    Knob general{0};
-    Knob topk_fallback{0};
-    Knob tx{0};
-    Knob topk_variant{0};
-    Knob topk_waves{0};
-    Knob unroll{0};
-    Knob colblock{0};
-    Knob nt{0};
-    Knob smx_two_pass{0};
-    Knob smx_lanes{0};
-    Knob smx_split{0};
-    Knob smx_res{0};
-    Knob rowreg{0};
-    Knob topk_short{0};
-    Knob topk_radix{0};
-    Knob topk_dyn{0};
+#define TPR_KNOB_FIELD(name) Knob name{0};
+    TPR_KNOB_LIST(TPR_KNOB_FIELD)
+#undef TPR_KNOB_FIELD
 };
 DebugKnobs& knobs();
+#else
+struct DebugKnobs {
+#define TPR_KNOB_FIELD(name) static constexpr int64_t name = 0;
+    TPR_KNOB_LIST(TPR_KNOB_FIELD)
+#undef TPR_KNOB_FIELD
+};
+constexpr DebugKnobs knobs() { return DebugKnobs{}; }
+#endif
 
 // ---- device helpers ----------------------------------------------------------
 __device__ __forceinline__ int lane_id() { return __lane_id(); }

@@ -23,11 +23,28 @@ def _declared_functions():
 
 
 def test_library_exports_every_declared_symbol():
-    L = _capi.lib()
     declared = _declared_functions()
     assert declared == set(_capi.EXPORTED)
+    dev = ctypes.CDLL(_capi.DEV_LIB_PATH)
     for name in declared:
-        assert hasattr(L, name), name
+        assert hasattr(dev, name), name
+    # the shipped library: every entry point but the test build's plan-override hook
+    rel = ctypes.CDLL(_capi.LIB_PATH)
+    for name in declared - {"tpr_debug_set"}:
+        assert hasattr(rel, name), name
+    assert not hasattr(rel, "tpr_debug_set")
+
+
+def test_release_build_has_no_plan_state():
+    """The shipped library exports no tpr_debug_set and no knob symbols."""
+    import subprocess
+    syms = subprocess.run(["nm", "-D", "--defined-only", _capi.LIB_PATH], capture_output=True, text=True,
+                          check=True).stdout
+    assert "tpr_debug_set" not in syms
+    assert "knobs" not in syms
+    dsyms = subprocess.run(["nm", "-D", "--defined-only", _capi.DEV_LIB_PATH], capture_output=True, text=True,
+                           check=True).stdout
+    assert "tpr_debug_set" in dsyms
 
 
 def test_abi_version():
