@@ -2,15 +2,15 @@
 """Benchmark of the MI355X reduction + top-k path (one GPU).
 
 A "step" is one pass of the hot path over one batch of the headline workload,
-a contiguous fp32 [64, 1024, 1024] N(0,1) tensor reduced
-five ways -- mean over dim=1, amax and argmax over dim=0, var and std
-(unbiased) over dim=-1.  `value` is the step's algorithmic HBM bytes (input read
-once + output written once, per op) divided by the step time: GB/s.
+BASELINE configs[3] (the largest single-GPU config): a flat fp32 tensor of 2^28
+N(0.5, 2) elements (1 GiB) reduced to a scalar six ways -- sum, mean, amax,
+argmax, var and std (unbiased).  `value` is the step's algorithmic HBM bytes
+(input read once + output written once, per op) divided by the step time: GB/s.
 
-Inputs are resident in HBM before the timed region; consecutive steps rotate
-over 3 input buffers (768 MiB > the 256 MB Infinity Cache) so every step reads
-from HBM.  Times come from HIP events on the stream the kernels run on.
-The other BASELINE configs (C1 sum, C3 topk, C4 full-tensor, C5 logits topk /
+Inputs are resident in HBM before the timed region; consecutive ops rotate over
+3 input buffers (3 GiB > the 256 MB Infinity Cache) so every op reads from HBM.
+Times come from HIP events on the stream the kernels run on.  The other
+BASELINE configs (C1 sum, C2 strided reductions, C3 topk, C5 logits topk /
 argmax) are measured the same way and reported under "configs".
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--vs-torch]
@@ -26,10 +26,14 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
-# kernel each headline op launches (single-kernel plans at this shape)
-DOMINANT_KERNEL = {"mean_dim1": "k_cols<SumOp,4,64,4,512>",
-                   "amax_dim0": "k_cols<ArgOp<true>,4,256,2,256>", "argmax_dim0": "k_cols<ArgOp<true>,4,256,2,256>",
-                   "var_dim-1": "k_rows_reg_var<4,1,256>", "std_dim-1": "k_rows_reg_var<4,1,256>"}
+# kernel each headline op launches (one launch per op: the split rows finish in the same launch)
+DOMINANT_KERNEL = {"sum": "k_rows<SumOp,4,256,4>", "mean": "k_rows<SumOp,4,256,4>",
+                   "amax": "k_rows<ArgOp<true>,4,256,4>", "argmax": "k_rows<ArgOp<true>,4,256,4>",
+                   "var": "k_rows<WelfordOp,4,256,4>", "std": "k_rows<WelfordOp,4,256,4>"}
+# the C2 strided ops
+C2_KERNEL = {"mean_dim1": "k_cols<SumOp,4,64,4,512>",
+             "amax_dim0": "k_cols<ArgOp<true>,4,256,2,256>", "argmax_dim0": "k_cols<ArgOp<true>,4,256,2,256>",
+             "var_dim-1": "k_rows_reg_var<4,1,256>", "std_dim-1": "k_rows_reg_var<4,1,256>"}
 METRIC = "achieved HBM GB/s (% of MI355X peak) for sum/argmax/topk; rows/s topk"
 
 
@@ -53,7 +57,7 @@ def parse():
     return ap.parse_args()
 
 
-SECTIONS = ["C1", "C3", "C4", "C4f64", "C5", "softmax", "copy", "reduce_backward", "softmax_cols", "topk_short"]
+SECTIONS = ["C1", "C2", "C3", "C4f64", "C5", "softmax", "copy", "reduce_backward", "softmax_cols", "topk_short"]
 
 
 class Call:
@@ -240,31 +244,31 @@ def main():
     if bad:
         sys.exit(f"bench.py: unknown sections {sorted(bad)}; choose from {SECTIONS}")
 
-    # ---------------- headline: configs[1] --------------------------------------
-    shape2 = (64, 1024, 1024)
+    # ---------------- headline: configs[3] --------------------------------------
+    n4 = 1 << 28
     nbuf = 3
-    bufs = [gen(torch, shape2, "normal", 1000 + i, dev) for i in range(nbuf)]
-    in_bytes = 64 * 1024 * 1024 * 4
-    ops2 = [("mean", [1]), ("amax", [0]), ("argmax", [0]), ("var", [-1]), ("std", [-1])]
-    calls = [[reduce_call(torch, capi, b, op, dims, stream) for (op, dims) in ops2] for b in bufs]
+    bufs = [gen(torch, (n4,), "normal", 4000 + i, dev) * 2.0 + 0.5 for i in range(nbuf)]
+    in_bytes = n4 * 4
+    ops4 = ["sum", "mean", "amax", "argmax", "var", "std"]
+    calls = [[reduce_call(torch, capi, b, op, None, stream) for op in ops4] for b in bufs]
     op_bytes = [in_bytes + c.out_bytes for c in calls[0]]
     step_bytes = sum(op_bytes)
     result = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
               "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-              "data": "synthetic: torch.randn N(0,1) seeded on device, 3 rotating 256 MiB buffers "
+              "data": "synthetic: torch.randn seeded on device, scaled to N(0.5, 2), 3 rotating 1 GiB buffers "
                       "(each op reads a different buffer than the op before it)",
-              "config": {"workload": "configs[1]: fp32 [64,1024,1024]; mean dim=1, amax+argmax dim=0, "
-                                     "var+std dim=-1 (unbiased). configs[1] is the configuration the metric's "
-                                     "strided-reduction bandwidth is quoted on and covers five of the path's "
-                                     "ops in one step; configs[3] (the largest, 1 GiB full reductions) is "
-                                     "measured below under configs.C4_full_2^28",
+              "config": {"workload": "configs[3]: flat fp32 tensor of 268,435,456 elements (1 GiB), N(0.5, 2); "
+                                     "sum, mean, amax, argmax, var, std (unbiased) to a scalar. configs[3] is the "
+                                     "largest single-GPU configuration; configs[0,1,2,4] are measured below under "
+                                     "configs",
                          "step_alg_bytes": step_bytes}}
+    step_fns = []
 
     if not args.no_headline:
-        # Op j of step i reads buffer (5i + j) % 3, so consecutive ops never read the
+        # Op j of step i reads buffer (6i + j) % 3, so consecutive ops never read the
         # buffer the previous op just streamed (no reuse through the 256 MB MALL).
         def make_step(i):
-            seq = [calls[(len(ops2) * i + j) % nbuf][j] for j in range(len(ops2))]
+            seq = [calls[(len(ops4) * i + j) % nbuf][j] for j in range(len(ops4))]
 
             def f():
                 for c in seq:
@@ -276,15 +280,14 @@ def main():
         value = step_bytes / (ms_step * 1e-3) / 1e9
 
         breakdown = {}
-        for j, (op, dims) in enumerate(ops2):
+        for j, op in enumerate(ops4):
             fns = [calls[i][j] for i in range(nbuf)]
             ms = time_calls(torch, fns, steps, warmup)
             gbs = op_bytes[j] / (ms * 1e-3) / 1e9
-            breakdown[f"{op}_dim{dims[0]}"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1),
-                                               "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
-                                               "alg_bytes": op_bytes[j], "kernel": DOMINANT_KERNEL[f"{op}_dim{dims[0]}"]}
+            breakdown[op] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+                             "alg_bytes": op_bytes[j], "kernel": DOMINANT_KERNEL[op]}
         dom_name, dom = max(breakdown.items(), key=lambda kv: kv[1]["ms"])
-        dom_j = [f"{op}_dim{dims[0]}" for (op, dims) in ops2].index(dom_name)
+        dom_j = ops4.index(dom_name)
         dom_ms = dom["ms"]  # average launch duration over the timed loop of that op alone
         dom_gbs = op_bytes[dom_j] / (dom_ms * 1e-3) / 1e9
 
@@ -292,7 +295,7 @@ def main():
         if os.path.exists(args.traffic_file):
             try:
                 tf = json.load(open(args.traffic_file))
-                traffic = tf.get(dom_name, {}).get("hbm_bytes_per_launch")
+                traffic = tf.get("C4_" + dom_name, {}).get("hbm_bytes_per_launch")
             except Exception:
                 traffic = None
         result.update({"value": round(value, 1), "ms_per_step": round(ms_step, 5)})
@@ -304,8 +307,8 @@ def main():
                               "timing": "HIP events on the launch stream, average over the op's own timed loop"}
         result["breakdown"] = breakdown
 
-    keep = {"C2": bufs[0]}
-    result["configs"] = run_sections(torch, capi, only, stream, steps, warmup, bufs, keep)
+    keep = {"C4": bufs[0]}
+    result["configs"] = run_sections(torch, capi, only, stream, steps, warmup, keep)
     if args.calibrate_copy:
         xc = gen(torch, (64 << 20,), "normal", 6000, dev)
         for _ in range(3):
@@ -314,23 +317,23 @@ def main():
 
     # ---------------- CPU baseline and accuracy (rank 0, N = 1) -------------------
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(bufs[0], ops2, op_bytes)
-        if "C3" in keep and "C5" in keep:
-            result["cpu_baseline"]["configs"] = cpu_extras(keep["C3"], keep["C5"])
+        result["cpu_baseline"] = cpu_baseline(bufs[0], ops4, op_bytes)
+        result["cpu_baseline"]["configs"] = cpu_extras(keep.get("C2"), keep.get("C3"), keep.get("C5"))
     else:
         result["cpu_baseline"] = None
     if not args.no_accuracy:
         result["accuracy"] = accuracy(torch, capi, keep)
     if args.vs_torch:
-        del keep
-        result["torch_rocm"] = torch_rocm_times(torch, bufs, steps, warmup)
+        del keep, bufs, calls, step_fns
+        result["torch_rocm"] = torch_rocm_times(torch, steps, warmup)
     print(json.dumps(result), flush=True)
 
 
-def torch_rocm_times(torch, bufs, steps, warmup):
+def torch_rocm_times(torch, steps, warmup):
     """PyTorch-ROCm's own kernels on the same shapes and rotating inputs, timed
     the same way (HIP events; `GB/s` = the same algorithmic bytes as ours)."""
-    dev = bufs[0].device
+    dev = torch.device("cuda:0")
+    bufs = [gen(torch, (64, 1024, 1024), "normal", 1000 + i, dev) for i in range(3)]
     out = {}
 
     def t(name, fns, by):
@@ -352,9 +355,10 @@ def torch_rocm_times(torch, bufs, steps, warmup):
     t("C3_topk64", [lambda b=b: torch.topk(b, 64, dim=1) for b in b3], 1024 * 32768 * 4 + 1024 * 64 * 12)
     t("C3_softmax", [lambda b=b: torch.softmax(b, -1) for b in b3[:4]], 2 * 1024 * 32768 * 4)
     del b3
-    x4 = gen(torch, (1 << 28,), "normal", 4000, dev)
+    del bufs
+    x4 = [gen(torch, (1 << 28,), "normal", 4000 + i, dev) * 2.0 + 0.5 for i in range(3)]
     for op in ("sum", "amax", "argmax", "var"):
-        t(f"C4_{op}", [lambda op=op: getattr(x4, op)()], (1 << 28) * 4 + 8)
+        t(f"C4_{op}", [lambda b=b, op=op: getattr(b, op)() for b in x4], (1 << 28) * 4 + 8)
     del x4
     b5 = [gen(torch, (256, 151936), "normal", 5000 + i, dev) * 3.0 for i in range(5)]
     n5 = 256 * 151936 * 4
@@ -374,12 +378,38 @@ def timed(torch, calls, steps, warmup, by, **extra):
     return dict(rate(ms, by), **extra)
 
 
-def run_sections(torch, capi, only, stream, steps, warmup, bufs, keep):
+def run_sections(torch, capi, only, stream, steps, warmup, keep):
     """The other BASELINE configs and the widened rows, each timed the same way
     (HIP events, inputs rotated so each launch reads HBM)."""
-    dev = bufs[0].device
-    nbuf = len(bufs)
+    dev = keep["C4"].device
     extras = {}
+    nbuf = 3
+    need_c2 = only & {"C2", "copy", "reduce_backward", "softmax_cols"}
+    bufs = [gen(torch, (64, 1024, 1024), "normal", 1000 + i, dev) for i in range(nbuf)] if need_c2 else []
+    if bufs:
+        keep["C2"] = bufs[0]
+    if "C2" in only:
+        # C2: strided reductions of [64,1024,1024] N(0,1): mean dim=1, amax+argmax dim=0, var+std dim=-1
+        ops2 = [("mean", [1]), ("amax", [0]), ("argmax", [0]), ("var", [-1]), ("std", [-1])]
+        c2 = [[reduce_call(torch, capi, b, op, dims, stream) for (op, dims) in ops2] for b in bufs]
+        ob = [64 * 1024 * 1024 * 4 + c.out_bytes for c in c2[0]]
+
+        def make_step(i):
+            seq = [c2[(len(ops2) * i + j) % nbuf][j] for j in range(len(ops2))]
+
+            def f():
+                for c in seq:
+                    c()
+            return f
+
+        ms = time_calls(torch, [make_step(i) for i in range(nbuf)], steps, warmup)
+        e2 = {"step": rate(ms, sum(ob))}
+        for j, (op, dims) in enumerate(ops2):
+            name = f"{op}_dim{dims[0]}"
+            e2[name] = timed(torch, [c2[i][j] for i in range(nbuf)], steps, warmup, ob[j], kernel=C2_KERNEL[name])
+        extras["C2_strided_64x1024x1024"] = e2
+        del c2
+
     if "C1" in only:
         # C1: sum dim=-1 of [4096,4096] (12 rotating 64 MiB buffers)
         b1 = [gen(torch, (4096, 4096), "normal", 2000 + i, dev) for i in range(12)]
@@ -409,16 +439,6 @@ def run_sections(torch, capi, only, stream, steps, warmup, bufs, keep):
                 del cs
             extras["softmax_C3_1024x32768"] = esm3
         del b3
-    if "C4" in only:
-        # C4: full-tensor reductions of 2^28 N(0.5, 2)
-        x4 = gen(torch, (1 << 28,), "normal", 4000, dev) * 2.0 + 0.5
-        c4 = {}
-        for op in ("sum", "mean", "amax", "argmax", "var", "std"):
-            c = reduce_call(torch, capi, x4, op, None, stream)
-            c4[op] = timed(torch, [c], max(steps // 2, 5), 2, (1 << 28) * 4 + c.out_bytes)
-        extras["C4_full_2^28"] = c4
-        keep["C4"] = x4
-        del x4
     if "C4f64" in only:
         # the same 1 GiB as float64 (2^27 elements): reductions computed in double
         x4d = gen(torch, (1 << 27,), "normal", 4001, dev).double() * 2.0 + 0.5
@@ -567,17 +587,18 @@ def accuracy(torch, capi, keep):
         ref, asum = x64.sum(1), np.abs(x64).sum(1)
         acc["C1_sum_dim-1"] = {"gpu": _err_stats(gpu(keep["C1"], "sum", [-1]), ref, asum),
                                "cpu_path": _err_stats(O.sum(x, [-1]), ref, asum)}
-    x = keep["C2"].cpu().numpy()
-    x64 = x.astype(np.float64)
-    ref, asum = x64.mean(1), np.abs(x64).mean(1)
-    c2 = {"mean_dim1": {"gpu": _err_stats(gpu(keep["C2"], "mean", [1]), ref, asum),
-                        "cpu_path": _err_stats(O.mean(x, [1]), ref, asum)}}
-    v = x64.var(2, ddof=1)
-    c2["var_dim-1"] = {"gpu": _err_stats(gpu(keep["C2"], "var", [-1]), v), "cpu_path": _err_stats(O.var(x, [-1]), v)}
-    c2["std_dim-1"] = {"gpu": _err_stats(gpu(keep["C2"], "std", [-1]), np.sqrt(v)),
-                       "cpu_path": _err_stats(O.std(x, [-1]), np.sqrt(v))}
-    acc["C2"] = c2
-    del x, x64
+    if "C2" in keep:
+        x = keep["C2"].cpu().numpy()
+        x64 = x.astype(np.float64)
+        ref, asum = x64.mean(1), np.abs(x64).mean(1)
+        c2 = {"mean_dim1": {"gpu": _err_stats(gpu(keep["C2"], "mean", [1]), ref, asum),
+                            "cpu_path": _err_stats(O.mean(x, [1]), ref, asum)}}
+        v = x64.var(2, ddof=1)
+        c2["var_dim-1"] = {"gpu": _err_stats(gpu(keep["C2"], "var", [-1]), v), "cpu_path": _err_stats(O.var(x, [-1]), v)}
+        c2["std_dim-1"] = {"gpu": _err_stats(gpu(keep["C2"], "std", [-1]), np.sqrt(v)),
+                           "cpu_path": _err_stats(O.std(x, [-1]), np.sqrt(v))}
+        acc["C2"] = c2
+        del x, x64
     if "C4" in keep:
         x = keep["C4"].cpu().numpy()
         x64 = x.astype(np.float64)
@@ -596,44 +617,54 @@ def accuracy(torch, capi, keep):
     return acc
 
 
-def cpu_baseline(x_dev, ops2, op_bytes, budget_s=10.0):
+def cpu_baseline(x_dev, ops4, op_bytes, budget_s=12.0):
     """Time the C restatement of TensorPlay's CPU reduction path (single-threaded,
-    as ReductionKernels.cpp is) on the headline step: the same five reductions of
-    one [64,1024,1024] buffer copied to host memory, repeated until ~budget_s."""
+    as ReductionKernels.cpp is) on the headline step: the same six full
+    reductions of one 1 GiB buffer copied to host memory, repeated until
+    ~budget_s (at least one whole step)."""
     from oracle import oracle as O
 
     x = x_dev.cpu().numpy()
-    fns = {"mean": lambda d: O.mean(x, d), "amax": lambda d: O.amax(x, d),
-           "argmax": lambda d: O.argmax(x, d[0]), "var": lambda d: O.var(x, d), "std": lambda d: O.std(x, d)}
-    per = {f"{op}_dim{dims[0]}": 0.0 for (op, dims) in ops2}
+    fns = {"sum": lambda: O.sum(x), "mean": lambda: O.mean(x), "amax": lambda: O.amax(x),
+           "argmax": lambda: O.argmax(x, None), "var": lambda: O.var(x), "std": lambda: O.std(x)}
+    per = {op: 0.0 for op in ops4}
     reps = 0
     t0 = time.perf_counter()
     while reps == 0 or time.perf_counter() - t0 < budget_s:
-        for (op, dims) in ops2:
+        for op in ops4:
             t = time.perf_counter()
-            fns[op](dims)
-            per[f"{op}_dim{dims[0]}"] += time.perf_counter() - t
+            fns[op]()
+            per[op] += time.perf_counter() - t
         reps += 1
     dt = (time.perf_counter() - t0) / reps
     total = float(sum(op_bytes))
     return {"value": round(total / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{reps} full headline steps (mean dim1, amax+argmax dim0, var+std dim-1 of one "
-                      "[64,1024,1024] buffer) through oracle/tp_cpu_reduce.c, 1 thread",
+            "sample": f"{reps} full headline steps (sum, mean, amax, argmax, var, std of one 2^28-element "
+                      "buffer) through oracle/tp_cpu_reduce.c, 1 thread",
             "seconds_per_step": round(dt, 4),
             "per_op_s": {k: round(v / reps, 4) for k, v in per.items()}, "host_cpus": os.cpu_count()}
 
 
-def cpu_extras(c3_dev, c5_dev):
+def cpu_extras(c2_dev, c3_dev, c5_dev):
     """CPU figures for the other configs on bounded samples (1 thread unless noted)."""
     import numpy as np
     from oracle import oracle as O
 
     out = {}
+    if c2_dev is not None:
+        x2 = c2_dev.cpu().numpy()
+        t = time.perf_counter()
+        O.mean(x2, [1]), O.amax(x2, [0]), O.argmax(x2, 0), O.var(x2, [-1]), O.std(x2, [-1])
+        dt = time.perf_counter() - t
+        out["C2_strided_step"] = {"GB/s": round(5 * x2.nbytes / dt / 1e9, 3), "cores": 1,
+                                  "sample": "one step: mean dim1, amax+argmax dim0, var+std dim-1 of one buffer"}
     x1 = np.random.default_rng(1).standard_normal((4096, 4096), dtype=np.float32)
     t = time.perf_counter()
     O.sum(x1, [-1])
     dt = time.perf_counter() - t
     out["C1_sum_dim-1_4096x4096"] = {"GB/s": round(x1.nbytes / dt / 1e9, 3), "sample": "full config", "cores": 1}
+    if c3_dev is None or c5_dev is None:
+        return out
     x3 = c3_dev[:256].cpu().numpy()
     t = time.perf_counter()
     O.topk(x3, 64)

@@ -114,7 +114,14 @@ size_t tpr_reduce_workspace_bytes(const tpr_reduce_desc* desc);
  * Replaces: DispatchStub<...>::call("sum" | "sum.dim_IntList" | "mean" |
  * "mean.dim" | "max" | "max.dim" | "min" | "min.dim" | "argmax" | "argmin" |
  * "var" | "var.dim" | "std" | "std.dim", DispatchKey::CUDA, ...)
- * (/root/reference/p10/src/backend/cuda/ReductionKernels.cu:385-418). */
+ * (/root/reference/p10/src/backend/cuda/ReductionKernels.cu:385-418).
+ * Reductions split over several workgroups per output (few long rows, the
+ * full tensor) finish in the same launch: the last workgroup of an output
+ * combines the partial states held in the workspace, counted by per-stream
+ * ticket counters inside the library (zero at load, left at zero by every
+ * launch).  Under graph capture, on the per-thread default stream and beyond
+ * 64 streams per device they take a second, finalize launch instead; results
+ * are identical either way. */
 int tpr_reduce(const tpr_reduce_desc* desc, const void* in, void* out,
                void* workspace, size_t workspace_bytes, void* stream);
 
@@ -170,6 +177,19 @@ size_t tpr_topk_workspace_bytes(int32_t dtype, int64_t rows, int64_t cols, int64
 int tpr_topk(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t row_stride,
              int64_t k, int32_t largest, int32_t sorted, void* out_values, void* out_indices,
              void* workspace, size_t workspace_bytes, void* stream);
+
+/* The plan tpr_topk would run for this call, host only, launches nothing (a
+ * test hook with no reference counterpart): out[0] = kernel family (1 lane-group
+ * kernel on 1- / 2-byte elements, 2 register radix select, 3 register radix
+ * select per segment + merge, 4 streaming radix select, 5 lane-group kernel,
+ * 6 wave kernel, 7 workgroup kernel; 6 and 7 add the merge when out[1] > 1),
+ * out[1] = segments per row, out[2] = segment length (segment s covers
+ * [s * out[2], min(cols, (s + 1) * out[2]))), out[3] = waves per wave-kernel
+ * workgroup, out[4] = workspace bytes.  `aligned`: the input and every row
+ * start are 16-byte aligned.  Every segment of a split row holds >= k
+ * elements: each writes exactly k composites that the merge ranks. */
+int tpr_topk_plan(int32_t dtype, int64_t rows, int64_t cols, int64_t k, int64_t row_stride, int32_t aligned,
+                  int64_t* out);
 
 /* Top-k / top-p (nucleus) sampling of one token id per row of float32 logits
  * (a consumer of tpr_topk; TensorPlay has no sampler, so the definition is
@@ -318,6 +338,7 @@ int32_t tpr_abi_version(void);
  * slices; also, as a power of two 1..32, the register radix select's sort
  * composites per thread where the sort size allows; 0 = automatic),
  * "topk_waves" (4, 8 or 16 waves per wave-kernel workgroup, 0 = automatic),
+ * "split_fin" (-1 = split reductions always take the separate finalize launch),
  * "topk_short" (1 = the lane-group kernel for every row it can hold, -1 =
  * never), "topk_radix" (1 = the radix-select kernels for every k, 2 = the
  * streaming one, -1 = never where another kernel can), "topk_dyn" (-1 = static

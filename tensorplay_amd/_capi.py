@@ -34,7 +34,7 @@ EXPORTED = ["tpr_reduce_workspace_bytes", "tpr_reduce", "tpr_topk_workspace_byte
             "tpr_copy", "tpr_copy_plan", "tpr_copy_strided", "tpr_last_error", "tpr_abi_version",
             "tpr_debug_set", "tpr_softmax", "tpr_softmax_workspace_bytes", "tpr_nll_loss_workspace_bytes", "tpr_nll_loss",
             "tpr_nll_loss_backward", "tpr_reduce_backward_workspace_bytes", "tpr_reduce_backward",
-            "tpr_sample_workspace_bytes", "tpr_sample", "tpr_reduce_noalloc"]
+            "tpr_sample_workspace_bytes", "tpr_sample", "tpr_reduce_noalloc", "tpr_topk_plan"]
 REDUCE_SCRATCH_BYTES = 8 << 20  # TPR_REDUCE_SCRATCH_BYTES
 # enum tpr_softmax_mode
 SOFTMAX_FWD, LOG_SOFTMAX_FWD, SOFTMAX_BWD, LOG_SOFTMAX_BWD = range(4)
@@ -117,6 +117,8 @@ def lib():
         L.tpr_topk_workspace_bytes.restype = sz
         L.tpr_topk.argtypes = [vp, i32, i64, i64, i64, i64, i32, i32, vp, vp, vp, sz, vp]
         L.tpr_topk.restype = ctypes.c_int
+        L.tpr_topk_plan.argtypes = [i32, i64, i64, i64, i64, i32, i64p]
+        L.tpr_topk_plan.restype = ctypes.c_int
         cdp = ctypes.POINTER(CopyDesc)
         L.tpr_copy.argtypes = [cdp, vp, vp, vp]
         L.tpr_copy.restype = ctypes.c_int
@@ -163,6 +165,18 @@ def debug_set(key, value):
     if not hasattr(L, "tpr_debug_set"):
         raise RuntimeError("plan overrides need the test build: set TPR_ROCM_DEV=1 before the library loads")
     _check(L.tpr_debug_set(key.encode(), int(value)))
+
+
+TOPK_KINDS = {1: "short_small", 2: "rsel", 3: "rsel_seg", 4: "radix", 5: "short", 6: "wave", 7: "block"}
+
+
+def topk_plan(dtype, rows, cols, k, row_stride=None, aligned=True):
+    """(kernel family, segments per row, segment length, waves, workspace bytes)
+    that tpr_topk plans for this call; launches nothing."""
+    out = (ctypes.c_int64 * 5)()
+    _check(lib().tpr_topk_plan(dtype, rows, cols, k, cols if row_stride is None else row_stride,
+                               1 if aligned else 0, out))
+    return TOPK_KINDS[out[0]], out[1], out[2], out[3], out[4]
 
 
 def make_desc(op, shape, strides, reduce_dims, out_dtype, correction=1, count_override=0,

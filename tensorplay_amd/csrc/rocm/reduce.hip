@@ -39,6 +39,10 @@ namespace {
 
 constexpr long long kSentinel = 0x7fffffffffffffffLL;
 constexpr int kBlock = 256;
+// Ticket counters of split plans that finish in their own launch: one block
+// of kTicketsPerStream counters for each of up to kTicketStreams streams.
+constexpr int kTicketStreams = 64;
+constexpr int kTicketsPerStream = 1024;
 
 // ---------------------------------------------------------------------------
 // Operator policies.  Acc = per-thread running state, State = mergeable state.
@@ -269,6 +273,79 @@ __device__ __forceinline__ typename Op::State block_reduce(typename Op::State st
     return r;  // valid in every thread
 }
 
+template <class Op, int BLK>
+__device__ __forceinline__ typename Op::State block_reduce_n(typename Op::State st) {
+    using State = typename Op::State;
+    __shared__ State sh[BLK / kWave];
+    st = group_reduce_sub_wave<Op, kWave>(st);
+    if (__lane_id() == 0) sh[threadIdx.x / kWave] = st;
+    __syncthreads();
+    State r = sh[0];
+#pragma unroll
+    for (int i = 1; i < BLK / kWave; ++i) r = Op::comb(r, sh[i]);
+    return r;  // valid in every thread
+}
+
+// ---------------------------------------------------------------------------
+// Split plans finished inside the same launch.  Every workgroup of a split
+// output stores its partial state, then draws a ticket from the output's
+// counter; the workgroup that draws ticket S-1 combines the S partials in
+// split order (as k_finalize_block does: thread t takes partials t, t+BLK, ...,
+// then the fixed workgroup tree) and writes the output, then sets the counter
+// back to 0 for the next launch.  The state words are written with
+// device-scope atomic exchanges and read back with device-scope atomic ors of
+// 0, and the ticket is a device-scope atomic add: read-modify-write atomics are
+// performed at the device's point of coherence, so no L2 writeback or
+// invalidate is needed (such fences cost microseconds per workgroup), and the
+// wait for the exchanges to complete (vmcnt(0)) orders them before the ticket.
+// ---------------------------------------------------------------------------
+template <class State>
+__device__ __forceinline__ void publish_state(State* dst, const State& v) {
+    static_assert(sizeof(State) % 4 == 0, "states are whole 32-bit words");
+    unsigned w[sizeof(State) / 4];
+    __builtin_memcpy(w, &v, sizeof(State));
+    unsigned* d = reinterpret_cast<unsigned*>(dst);
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(State) / 4); ++i)
+        __hip_atomic_exchange(d + i, w[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <class State>
+__device__ __forceinline__ State fetch_state(State* src) {
+    unsigned w[sizeof(State) / 4];
+    unsigned* p = reinterpret_cast<unsigned*>(src);
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(State) / 4); ++i)
+        w[i] = __hip_atomic_fetch_or(p + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    State v;
+    __builtin_memcpy(&v, w, sizeof(State));
+    return v;
+}
+
+// st: the workgroup's partial state of output o (valid in thread 0); partial s
+// of output o lives at part[s * stride + o].
+template <class Op, int BLK, class Fn>
+__device__ void split_finish(typename Op::State st, typename Op::State* part, unsigned* ticket, int S, int s,
+                             long long stride, long long o, Fn&& write) {
+    using State = typename Op::State;
+    __shared__ int last;
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        publish_state(part + (long long)s * stride + o, st);
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
+    }
+    __syncthreads();
+    if (!last) return;
+    State r = Op::identity();
+    for (int i = tid; i < S; i += BLK) r = Op::comb(r, fetch_state(part + (long long)i * stride + o));
+    r = block_reduce_n<Op, BLK>(r);
+    if (tid == 0) {
+        write(r);
+        __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // Streaming 128-bit load; `nt` marks it nontemporal (read once, do not keep in cache).
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float4 ld4(const float4* p, int nt) {
@@ -311,6 +388,7 @@ struct RowArgs {
     Fin fin;
     long long idx_off;  // index of this launch's first reduced element (chunked runs)
     int partial;        // 1: write states to `part` (S > 1 or a chunk of a longer run)
+    unsigned* tickets;  // S > 1, one row per workgroup: per-row counters of split_finish (else null)
 };
 
 template <class Op, int VEC, int LANES, int U>
@@ -416,6 +494,13 @@ __global__ __launch_bounds__(LANES > kBlock ? LANES : kBlock) void k_rows(RowArg
 #pragma unroll
             for (int i = 1; i < WPG; ++i) r = Op::comb(r, sh[g * WPG + i]);
             st = r;
+        }
+    }
+    if constexpr (GROUPS == 1) {
+        if (a.tickets) {
+            split_finish<Op, BLK>(st, reinterpret_cast<State*>(a.part), a.tickets + row, a.S, s, a.rows, row,
+                                  [&](const State& r) { fin_write(r, a.fin, a.out, row); });
+            return;
         }
     }
     if (l == 0 && row < a.rows) {
@@ -571,6 +656,7 @@ struct ColArgs {
     Fin fin;
     long long idx_off;  // as RowArgs
     int partial;
+    unsigned* tickets;  // as RowArgs (rows only)
 };
 
 template <class Op, int VEC, int TX, int U, int BLK>
@@ -1136,7 +1222,8 @@ int launch_rows_reg_var(const Plan& p, const float* in, void* out, Fin fin, hipS
 }
 
 template <class Op>
-int launch_rows(const Plan& p, const float* in, void* out, void* ws, Fin fin, hipStream_t st) {
+int launch_rows(const Plan& p, const float* in, void* out, void* ws, Fin fin, hipStream_t st,
+                unsigned* tickets = nullptr) {
     if constexpr (std::is_same<Op, WelfordOp>::value) {
         if (p.var_nv > 0) return launch_rows_reg_var(p, in, out, fin, st);
     }
@@ -1145,7 +1232,8 @@ int launch_rows(const Plan& p, const float* in, void* out, void* ws, Fin fin, hi
     } else {
         if (p.reg_wpr > 0) return fail(TPR_ERR_INVALID_ARG, "tpr_reduce: register-row plan for an op without a zero identity");
     }
-    RowArgs a{in, p.rows, p.R, p.row_stride, (int)p.S, p.nt, out, ws, fin, p.idx_off, p.partial || p.S > 1};
+    RowArgs a{in, p.rows, p.R, p.row_stride, (int)p.S, p.nt, out, ws, fin, p.idx_off, p.partial || p.S > 1,
+              tickets};
     const long long groups = (p.lanes >= kBlock) ? 1 : kBlock / p.lanes;
     const long long grid = ceil_div(p.rows, groups) * p.S;
 #define TPR_ROWS_CASE(L)                                                                             \
@@ -1256,6 +1344,18 @@ int run_chunks(const Plan& p, const void* in, size_t esize, void* out, void* ws,
     return launch_finalize<Op>(pf, out, ws, fin, st);
 }
 
+unsigned* stream_tickets(hipStream_t st);
+
+// Counters for a split plan that finishes in its own launch (split_finish):
+// row plans with S > 1 and one row per workgroup, on a stream that has a
+// counter block.  Null: the plan takes the separate finalize launch.
+unsigned* fused_split_tickets(const Plan& p, hipStream_t st) {
+    if (p.kind != P_ROWS || p.S <= 1 || p.nchunk > 1 || p.partial || p.lanes < kBlock || p.reg_wpr > 0 ||
+        p.var_nv > 0 || p.rows > kTicketsPerStream)
+        return nullptr;
+    return stream_tickets(st);
+}
+
 template <class Op>
 int run(const Plan& p, const float* in, void* out, void* ws, Fin fin, hipStream_t st) {
     if (p.nchunk > 1)
@@ -1264,11 +1364,12 @@ int run(const Plan& p, const float* in, void* out, void* ws, Fin fin, hipStream_
             return pc.kind == P_ROWS ? launch_rows<Op>(pc, x, out, wc, fin, st) : launch_cols<Op>(pc, x, out, wc, fin, st);
         });
     int rc = TPR_OK;
-    if (p.kind == P_ROWS) rc = launch_rows<Op>(p, in, out, ws, fin, st);
+    unsigned* tk = fused_split_tickets(p, st);
+    if (p.kind == P_ROWS) rc = launch_rows<Op>(p, in, out, ws, fin, st, tk);
     else if (p.kind == P_COLS) rc = launch_cols<Op>(p, in, out, ws, fin, st);
     else rc = launch_general<Op>(p, in, out, ws, fin, st);
     if (rc != TPR_OK) return rc;
-    if (p.S > 1) rc = launch_finalize<Op>(p, out, ws, fin, st);
+    if (p.S > 1 && !tk) rc = launch_finalize<Op>(p, out, ws, fin, st);
     return rc;
 }
 
@@ -1424,6 +1525,7 @@ struct ArgsI {
     Fin fin;
     long long idx_off;  // as RowArgs
     int partial;
+    unsigned* tickets;  // as RowArgs (rows only)
 };
 
 template <class T, int NV>
@@ -1514,7 +1616,15 @@ __global__ __launch_bounds__(LANES > kBlock ? LANES : kBlock) void k_rows_i(Args
         }
         for (int e = tail + s * LANES + l; e < R; e += a.S * LANES) Op::acc(acc, p[e], e, prm);
     }
-    typename Op::State st = combine_lanes<Op, LANES>(Op::state(acc), tid);
+    using State = typename Op::State;
+    State st = combine_lanes<Op, LANES>(Op::state(acc), tid);
+    if constexpr (GROUPS == 1) {
+        if (a.tickets) {
+            split_finish<Op, BLK>(st, reinterpret_cast<State*>(a.part), a.tickets + row, a.S, s, a.rows, row,
+                                  [&](const State& r) { fin_write(r, a.fin, a.out, row); });
+            return;
+        }
+    }
     if (l == 0 && row < a.rows) {
         if (!a.partial) fin_write(st, a.fin, a.out, row);
         else reinterpret_cast<typename Op::State*>(a.part)[(long long)s * a.rows + row] = shift_index(st, a.idx_off, 0);
@@ -1824,13 +1934,15 @@ void adapt_plan_int(Plan& p, const tpr_reduce_desc* d, const void* in, int es) {
 }
 
 template <class Op, class T>
-int launch_int_layout(const Plan& p, const void* in, void* out, void* ws, Fin fin, hipStream_t st) {
+int launch_int_layout(const Plan& p, const void* in, void* out, void* ws, Fin fin, hipStream_t st,
+                      unsigned* tickets = nullptr) {
     constexpr int NV = 16 / (int)sizeof(T);
     if (p.kind == P_ROWS) {
         ArgsI a{};
         a.in = in; a.rows = p.rows; a.R = p.R; a.row_stride = p.row_stride;
         a.S = (int)p.S; a.out = out; a.part = ws; a.fin = fin;
         a.idx_off = p.idx_off; a.partial = p.partial || p.S > 1;
+        a.tickets = tickets;
         const long long groups = (p.lanes >= kBlock) ? 1 : kBlock / p.lanes;
         const dim3 grid(ceil_div(p.rows, groups) * p.S);
         const dim3 blk(p.lanes > kBlock ? p.lanes : kBlock);
@@ -1885,9 +1997,10 @@ int run_int_op(const Plan& p, const void* in, void* out, void* ws, Fin fin, hipS
         return run_chunks<Op>(p, in, sizeof(T), out, ws, fin, st, [&](const Plan& pc, const void* ic, void* wc) {
             return launch_int_layout<Op, T>(pc, ic, out, wc, fin, st);
         });
-    int rc = launch_int_layout<Op, T>(p, in, out, ws, fin, st);
+    unsigned* tk = fused_split_tickets(p, st);
+    int rc = launch_int_layout<Op, T>(p, in, out, ws, fin, st, tk);
     if (rc != TPR_OK) return rc;
-    if (p.S > 1) rc = launch_finalize<Op>(p, out, ws, fin, st);
+    if (p.S > 1 && !tk) rc = launch_finalize<Op>(p, out, ws, fin, st);
     return rc;
 }
 
@@ -2325,6 +2438,60 @@ int tpr_reduce(const tpr_reduce_desc* desc, const void* in, void* out, void* wor
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Ticket counters of split plans finished in one launch (split_finish).  Zero
+// when the library loads; every launch that draws tickets leaves its counters
+// at 0 again.  Each stream gets its own block of counters, so launches that can
+// run at the same time never share a counter: launches on one stream run one
+// after another.  Streams beyond kTicketStreams, the per-thread default stream
+// (one handle for many streams) and streams under graph capture (a captured
+// launch may replay on another stream) take the separate finalize launch.
+// ---------------------------------------------------------------------------
+static __device__ unsigned int split_tickets[tpr::kTicketStreams * tpr::kTicketsPerStream];
+
+namespace tpr {
+namespace {
+unsigned* stream_tickets(hipStream_t st) {
+    if (knobs().split_fin < 0) return nullptr;
+    if (st == hipStreamPerThread) return nullptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+        (void)hipGetLastError();  // not an error of this call: take the finalize launch
+        return nullptr;
+    }
+    if (cs != hipStreamCaptureStatusNone) return nullptr;
+    static constexpr int kMaxDev = 64;
+    struct DevTickets {
+        unsigned* base = nullptr;
+        int n = 0;
+        hipStream_t streams[kTicketStreams];
+    };
+    static std::mutex mu;
+    static DevTickets devs[kMaxDev];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> g(mu);
+    DevTickets& d = devs[dev];
+    if (!d.base) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(split_tickets)) != hipSuccess || !ptr) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        d.base = static_cast<unsigned*>(ptr);
+    }
+    for (int i = 0; i < d.n; ++i)
+        if (d.streams[i] == st) return d.base + (size_t)i * kTicketsPerStream;
+    if (d.n == kTicketStreams) return nullptr;
+    d.streams[d.n] = st;
+    return d.base + (size_t)(d.n++) * kTicketsPerStream;
+}
+}  // namespace
+}  // namespace tpr
 
 // ---------------------------------------------------------------------------
 // Workspace-free entry point.  The partial states of split plans (and the

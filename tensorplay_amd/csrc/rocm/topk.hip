@@ -2320,6 +2320,56 @@ size_t radix_ws(long long rows, long long cols, long long k, int32_t dtype = TPR
     return n2 > lds ? (size_t)rows * (size_t)n2 * (wide ? 16 : 8) : 0;
 }
 
+// Which kernels serve a top-k call, and how rows are cut into segments.
+enum TopkKind {
+    TK_SHORT_SMALL = 1,  // k_topk_short on 1- / 2-byte elements
+    TK_RSEL = 2,         // k_topk_rsel, one workgroup per row
+    TK_RSEL_SEG = 3,     // k_topk_rsel per segment, then k_topk_merge
+    TK_RADIX = 4,        // k_topk_radix (streaming)
+    TK_SHORT = 5,        // k_topk_short on 4-byte elements
+    TK_WAVE = 6,         // k_topk_wave (then k_topk_merge when nseg > 1)
+    TK_BLOCK = 7,        // k_topk_block (then k_topk_merge when nseg > 1)
+};
+struct TopkRoute {
+    int kind;
+    int nseg;     // segments per row (1: no merge pass)
+    int seg_len;  // elements per segment (the last one may be shorter)
+    int nw;       // waves per k_topk_wave workgroup
+    size_t ws;    // workspace bytes
+};
+
+// The planner of tpr_topk / tpr_sample, host only.  `aligned`: the input is
+// 16-byte aligned and every row start stays so (rows == 1 or the row stride in
+// bytes is a multiple of 16).  Segment contract of TK_RSEL_SEG, TK_WAVE and
+// TK_BLOCK with nseg > 1: segment s covers [s * seg_len, min(cols, (s + 1) *
+// seg_len)), every one of the nseg segments holds >= k elements (each writes
+// exactly k composites for the merge), and nseg * k <= kMergeMax.
+TopkRoute route_topk(long long rows, long long cols, long long k, int32_t dtype, long long row_stride, bool aligned) {
+    const bool radix = radix_route(rows, cols, k, dtype);
+    // (The lane-group kernel addresses up to 4 rows per wave with 32-bit offsets.)
+    const bool short_ok = (k <= kShortMaxK || short_exact(rows, cols, k)) && cols <= kShortMaxCols &&
+                          3 * row_stride + cols < (1LL << 29);
+    const bool short_on = knobs().topk_short >= 0 && knobs().topk_fallback == 0 && knobs().splits <= 0;
+    // 1- and 2-byte integer rows the lane-group kernel can hold, 16-byte
+    // aligned: that kernel on integer keys (else the register radix select)
+    const int eb = dtype_size(dtype);
+    if (eb < 4 && short_ok && short_on && knobs().topk_radix <= 0 && aligned)
+        return TopkRoute{TK_SHORT_SMALL, 1, (int)cols, 0, 0};
+    if (radix && rsel_route(cols, dtype)) return TopkRoute{TK_RSEL, 1, (int)cols, 0, 0};
+    if (const int ns = radix ? rsel_segments(cols, k, dtype) : 0) {
+        const int seg_len = (int)((cols + ns - 1) / ns + 3) & ~3;  // segment starts stay 16-byte aligned
+        return TopkRoute{TK_RSEL_SEG, ns, seg_len, 0, radix_ws(rows, cols, k, dtype)};
+    }
+    if (radix) return TopkRoute{TK_RADIX, 1, (int)cols, 0, radix_ws(rows, cols, k, dtype)};
+    // Every row the lane-group kernel can hold goes there: faster than the
+    // workgroup kernel ([16384, 3000] k = 64: 124 against 181 us; [8192, 2500]
+    // k = 40: 38 against 77 us) and, since its two-key bound, than the 4-wave
+    // kernel on rows of 4096 ([16384, 4096] k = 64: 81 against 99 us).
+    if (short_ok && short_on) return TopkRoute{TK_SHORT, 1, (int)cols, 0, 0};
+    const TopkPlan pl = plan_topk(rows, cols, k);
+    return TopkRoute{pl.wave ? TK_WAVE : TK_BLOCK, pl.nseg, pl.seg_len, pl.nw, pl.ws};
+}
+
 }  // namespace
 }  // namespace tpr
 
@@ -2327,8 +2377,7 @@ extern "C" {
 
 size_t tpr_topk_workspace_bytes(int32_t dtype, int64_t rows, int64_t cols, int64_t k) {
     if (rows <= 0 || cols <= 0 || k <= 0 || k > cols || cols > 0x7fffffffLL || tpr::dtype_size(dtype) == 0) return 0;
-    if (tpr::radix_route(rows, cols, k, dtype)) return tpr::radix_ws(rows, cols, k, dtype);
-    return tpr::plan_topk(rows, cols, k).ws;
+    return tpr::route_topk(rows, cols, k, dtype, cols, true).ws;
 }
 
 }  // extern "C"
@@ -2457,11 +2506,12 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     if (cols > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: rows longer than 2^31-1");
     if (!in || (!smp && (!out_values || !out_indices))) return fail(TPR_ERR_INVALID_ARG, "tpr_topk: null pointer");
     if (rows > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: more than 2^31-1 rows");
-    const bool radix = radix_route(rows, cols, k, dtype);
-    const TopkPlan pl = radix ? TopkPlan{1, (int)cols, false, 8, radix_ws(rows, cols, k, dtype)} : plan_topk(rows, cols, k);
-    if (rows * (long long)pl.nseg > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: grid too large");
-    if (pl.ws > 0 && (workspace == nullptr || workspace_bytes < pl.ws))
-        return fail(TPR_ERR_WORKSPACE, "tpr_topk: workspace too small (need " + std::to_string(pl.ws) + " bytes)");
+    const bool aligned = ((reinterpret_cast<uintptr_t>(in) & 15u) == 0) &&
+                         (rows == 1 || (row_stride * dtype_size(dtype)) % 16 == 0);
+    const TopkRoute rt = route_topk(rows, cols, k, dtype, row_stride, aligned);
+    if (rows * (long long)rt.nseg > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: grid too large");
+    if (rt.ws > 0 && (workspace == nullptr || workspace_bytes < rt.ws))
+        return fail(TPR_ERR_WORKSPACE, "tpr_topk: workspace too small (need " + std::to_string(rt.ws) + " bytes)");
     TopkArgs a;
     a.in = static_cast<const float*>(in);
     a.rows = rows;
@@ -2472,8 +2522,8 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     a.ikind = (dtype == TPR_INT32 || dtype == TPR_INT16 || dtype == TPR_INT8) ? 1
               : (dtype == TPR_UINT32 || dtype == TPR_UINT16 || dtype == TPR_UINT8 || dtype == TPR_BOOL) ? 2 : 0;
     a.force_fallback = knobs().topk_fallback ? 1 : 0;
-    a.nseg = pl.nseg;
-    a.seg_len = pl.seg_len;
+    a.nseg = rt.nseg;
+    a.seg_len = rt.seg_len;
     a.part = static_cast<unsigned long long*>(workspace);
     a.out_v = static_cast<float*>(out_values);
     a.out_i = static_cast<long long*>(out_indices);
@@ -2485,28 +2535,15 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     a.ids = smp ? smp->ids : nullptr;
     const bool vec = ((reinterpret_cast<uintptr_t>(in) & 15u) == 0) && (rows == 1 || row_stride % 4 == 0);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    // (The lane-group kernel addresses up to 4 rows per wave with 32-bit offsets.)
-    const bool short_ok = (k <= kShortMaxK || short_exact(rows, cols, k)) && cols <= kShortMaxCols &&
-                          3 * row_stride + cols < (1LL << 29);
-    const bool short_on = knobs().topk_short >= 0 && knobs().topk_fallback == 0 && knobs().splits <= 0;
-    // 1- and 2-byte integer rows the lane-group kernel can hold, 16-byte
-    // aligned: that kernel on integer keys (else the register radix select)
-    const int eb = dtype_size(dtype);
-    if (eb < 4 && short_ok && short_on && knobs().topk_radix <= 0 &&
-        (reinterpret_cast<uintptr_t>(in) & 15u) == 0 && (rows == 1 || (row_stride * eb) % 16 == 0))
-        return launch_short_small(a, eb, st);
-    if (radix && rsel_route(cols, dtype))
-        return launch_rsel(a, dtype, st);
-    if (const int ns = radix ? rsel_segments(cols, k, dtype) : 0) {
-        if (rows * (long long)ns > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_topk: grid too large");
-        a.nseg = ns;
-        a.seg_len = (int)((cols + ns - 1) / ns + 3) & ~3;  // segment starts stay 16-byte aligned
+    if (rt.kind == TK_SHORT_SMALL) return launch_short_small(a, dtype_size(dtype), st);
+    if (rt.kind == TK_RSEL) return launch_rsel(a, dtype, st);
+    if (rt.kind == TK_RSEL_SEG) {
         const int rc = launch_rsel(a, dtype, st);
         if (rc != TPR_OK) return rc;
         hipLaunchKernelGGL(k_topk_merge, dim3((unsigned)rows), dim3(kMergeT), 0, st, a, (int)dtype);
         return check_launch("k_topk_merge");
     }
-    if (radix) {
+    if (rt.kind == TK_RADIX) {
         // few rows: 1024 threads per row (the passes over the row are latency bound)
         const int nt = rows < 2LL * device_info().cus ? 1024 : kRadixT;
 #define TPR_RADIX(T)                                                                                  \
@@ -2529,11 +2566,8 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
 #undef TPR_RADIX
         return check_launch("k_topk_radix");
     }
-    // Every row the lane-group kernel can hold goes there: faster than the
-    // workgroup kernel ([16384, 3000] k = 64: 124 against 181 us; [8192, 2500]
-    // k = 40: 38 against 77 us) and, since its two-key bound, than the 4-wave
-    // kernel on rows of 4096 ([16384, 4096] k = 64: 81 against 99 us).
-    if (short_ok && short_on) return launch_short(a, vec, st);
+    if (rt.kind == TK_SHORT) return launch_short(a, vec, st);
+    const TopkPlan pl{rt.nseg, rt.seg_len, rt.kind == TK_WAVE, rt.nw, rt.ws};
     const long long grid = rows * pl.nseg;
     if (pl.wave) {
         // 512-thread workgroups (many rows): 8 waves/SIMD without prefetch.
@@ -2589,6 +2623,21 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
 }  // namespace tpr
 
 extern "C" {
+
+int tpr_topk_plan(int32_t dtype, int64_t rows, int64_t cols, int64_t k, int64_t row_stride, int32_t aligned,
+                  int64_t* out) {
+    if (!out) return tpr::fail(TPR_ERR_INVALID_ARG, "tpr_topk_plan: null output");
+    if (tpr::dtype_size(dtype) == 0) return tpr::fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_topk_plan: unknown dtype");
+    if (rows <= 0 || cols <= 0 || k <= 0 || k > cols || cols > 0x7fffffffLL || rows > 0x7fffffffLL)
+        return tpr::fail(TPR_ERR_INVALID_ARG, "tpr_topk_plan: no kernel runs for this shape");
+    const tpr::TopkRoute rt = tpr::route_topk(rows, cols, k, dtype, row_stride, aligned != 0);
+    out[0] = rt.kind;
+    out[1] = rt.nseg;
+    out[2] = rt.seg_len;
+    out[3] = rt.nw;
+    out[4] = (int64_t)rt.ws;
+    return TPR_OK;
+}
 
 int tpr_topk(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t row_stride,
              int64_t k, int32_t largest, int32_t sorted, void* out_values, void* out_indices,
