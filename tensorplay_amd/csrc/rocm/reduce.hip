@@ -525,6 +525,27 @@ __global__ __launch_bounds__(LANES > kBlock ? LANES : kBlock) void k_rows(RowArg
 constexpr int kBufWord3 = 0x00020000;  // raw buffer resource, 32-bit data (gfx9 family)
 constexpr int kAuxNT = 2;              // buffer-load cache policy: nontemporal
 
+// fp64 sum over the 64 lanes of a wave with DPP lane moves (no LDS round
+// trips): quad swaps, half-row and row mirrors leave every lane of a 16-lane
+// row with the row's sum, then two row broadcasts carry the rows into lane 63.
+// The result is valid in lane 63 only.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const unsigned long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)b, CTRL, ROW_MASK, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), CTRL, ROW_MASK, 0xf, false);
+    return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+__device__ __forceinline__ double wave_sum_f64_lane63(double v) {
+    v += dpp_f64<0xB1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f64<0x4E, 0xf>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f64<0x141, 0xf>(v);  // row_half_mirror
+    v += dpp_f64<0x140, 0xf>(v);  // row_mirror
+    v += dpp_f64<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_f64<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
 template <class Op, int NV, int WPR, int BLK>
 __global__ __launch_bounds__(BLK) void k_rows_reg(RowArgs a) {
     using State = typename Op::State;
@@ -558,17 +579,22 @@ __global__ __launch_bounds__(BLK) void k_rows_reg(RowArgs a) {
         Op::acc(q[3], t[u].w, 0, prm);
     }
     State st = Op::comb(Op::comb(Op::state(q[0]), Op::state(q[1])), Op::comb(Op::state(q[2]), Op::state(q[3])));
-    st = group_reduce_sub_wave<Op, kWave>(st);
+    // the wave's total ends in lane 63 (sums: DPP moves) or every lane (the butterfly)
+    constexpr bool kDpp = std::is_same<State, SumS>::value && std::is_same<typename Op::Acc, double>::value &&
+                          !std::is_same<Op, ProdOp>::value;
+    constexpr int kLead = kDpp ? kWave - 1 : 0;
+    if constexpr (kDpp) st.s = wave_sum_f64_lane63(st.s);
+    else st = group_reduce_sub_wave<Op, kWave>(st);
     if constexpr (WPR > 1) {
         __shared__ State sh[BLK / kWave];
-        if (l == 0) sh[w] = st;
+        if (l == kLead) sh[w] = st;
         __syncthreads();
-        if (sub == 0 && l == 0) {
+        if (sub == 0 && l == kLead) {
 #pragma unroll
             for (int i = 1; i < WPR; ++i) st = Op::comb(st, sh[w + i]);
         }
     }
-    if (sub == 0 && l == 0 && live) fin_write(st, a.fin, a.out, row);
+    if (sub == 0 && l == kLead && live) fin_write(st, a.fin, a.out, row);
 }
 
 // ---------------------------------------------------------------------------

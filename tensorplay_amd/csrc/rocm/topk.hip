@@ -129,6 +129,16 @@ __device__ __forceinline__ uint32_t elem_key(float f, int largest, int ikind) {
     return ikind ? i2key_sel(f, ikind == 1 ? 0x80000000u : 0u, lm) : f2key_sel(f, lm);
 }
 
+// Bits of an integer element (ikind 1 signed, 2 unsigned / bool; em = the
+// element's mask) from its sortable key: the key is the element with the sign
+// bit flipped (signed) and complemented for largest = 0, so this is exact and
+// the selected values need no second read of the input (which the row's
+// nontemporal loads have not left in the cache).
+__device__ __forceinline__ uint32_t int_key_bits(uint32_t key, int ikind, int largest, uint32_t em) {
+    const uint32_t sm = ikind == 1 ? (em >> 1) + 1u : 0u;
+    return (key ^ (largest ? 0u : 0xffffffffu) ^ sm) & em;
+}
+
 __device__ __forceinline__ unsigned long long comp_key(uint32_t key, uint32_t idx) {
     return ((unsigned long long)key << 32) | (unsigned long long)(0xffffffffu - idx);
 }
@@ -537,7 +547,9 @@ __device__ __forceinline__ void write_segment(const TopkArgs& a, long long row, 
     } else if (a.nseg == 1) {
         for (int i = threadIdx.x; i < k; i += blockDim.x) {
             const uint32_t idx = comp_index(sel[i]);
-            a.out_v[row * k + i] = a.ikind ? p[idx] : selected_value(p, (uint32_t)(sel[i] >> 32), idx, a.largest);
+            const uint32_t key = (uint32_t)(sel[i] >> 32);
+            a.out_v[row * k + i] = a.ikind ? __uint_as_float(int_key_bits(key, a.ikind, a.largest, 0xffffffffu))
+                                           : selected_value(p, key, idx, a.largest);
             a.out_i[row * k + i] = (long long)idx;
         }
     } else {
@@ -1177,12 +1189,14 @@ template <int EB>
 __device__ __forceinline__ void write_ranked(const TopkArgs& a, long long row, int k, const float* p, int largest,
                                              int r, unsigned long long c) {
     const uint32_t idx = comp_index(c);
+    const uint32_t key = (uint32_t)(c >> 32);
     if constexpr (EB == 1) {
-        reinterpret_cast<uint8_t*>(a.out_v)[row * k + r] = reinterpret_cast<const uint8_t*>(p)[idx];
+        reinterpret_cast<uint8_t*>(a.out_v)[row * k + r] = (uint8_t)int_key_bits(key, a.ikind, largest, 0xffu);
     } else if constexpr (EB == 2) {
-        reinterpret_cast<uint16_t*>(a.out_v)[row * k + r] = reinterpret_cast<const uint16_t*>(p)[idx];
+        reinterpret_cast<uint16_t*>(a.out_v)[row * k + r] = (uint16_t)int_key_bits(key, a.ikind, largest, 0xffffu);
     } else {
-        a.out_v[row * k + r] = a.ikind ? p[idx] : selected_value(p, (uint32_t)(c >> 32), idx, largest);
+        a.out_v[row * k + r] = a.ikind ? __uint_as_float(int_key_bits(key, a.ikind, largest, 0xffffffffu))
+                                       : selected_value(p, key, idx, largest);
     }
     a.out_i[row * k + r] = (long long)idx;
 }
