@@ -18,7 +18,10 @@
 //     stay in registers: read once and written once -- k_smx_rows;
 //   * rows of 16384..153600 floats, at least one per CU, stay on one CU in
 //     registers plus LDS and are also read once -- k_smx_res (forward),
-//     k_smx_res_bwd (gradients: g held, y streamed);
+//     k_smx_res_bwd (log_softmax gradient: g held, y streamed once);
+//   * softmax gradients of rows of 16385..393216 floats are cut into pieces,
+//     one workgroup each holding its g and y, with the partial dots exchanged
+//     between the pieces -- k_smx_bwd_pieces (every input read once);
 //   * longer rows stream twice: an online (max, sum-of-exp) pass, then the
 //     output pass -- k_smx_rows2, or split over (row, chunk) workgroups when
 //     the rows are fewer than the CUs -- k_smx_part / k_smx_apply;
@@ -377,6 +380,7 @@ __global__ __launch_bounds__(1024) void k_smx_rows2(SmxArgs p) {
 //   j < kResVR, and lds[(j - kResVR) * 512 + t] after that.
 // ---------------------------------------------------------------------------
 constexpr int kResT = 512;
+constexpr int kBufWord3 = 0x00020000;  // raw buffer resource, 32-bit data (gfx9 family)
 constexpr int kResLdsMax = 160 * 1024;           // LDS of one gfx950 workgroup
 constexpr int kResVLMax = kResLdsMax / (kResT * 16) - 1;  // float4 per lane in LDS (19; 4 KB spare)
 // VR = float4 per lane in registers: 56 (224 VGPRs), 40, 24 or 8.  A kernel
@@ -385,8 +389,6 @@ constexpr int kResVLMax = kResLdsMax / (kResT * 16) - 1;  // float4 per lane in 
 constexpr long long res_min(int vr) { return (long long)kResT * 4 * vr; }
 constexpr long long res_max(int vr) { return (long long)kResT * 4 * (vr + kResVLMax); }
 constexpr long long kResMax = res_max(56);       // 153600 floats
-
-constexpr int kBufWord3 = 0x00020000;  // raw buffer resource, 32-bit data (gfx9 family)
 
 // Row loads and stores go through buffer resources spanning the row, with
 // 32-bit offsets (no 64-bit address per vector).  The host sends only rows of
@@ -600,6 +602,118 @@ __global__ __launch_bounds__(kResT) void k_smx_res_bwd(SmxArgs p, int vl) {
         const int off = ((kResVR + j) * kResT + t) * 16;
         const f32x4 y = __builtin_amdgcn_raw_buffer_load_b128(bb, off, z0, aux);
         __builtin_amdgcn_raw_buffer_store_b128(outq(lds[j * kResT + t], y), bo, off, 0, aux);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Softmax gradient with g AND y held on chip: gx = (g - sum(g * y)) * y needs
+// the whole row's dot before any output, and a long row's g and y together
+// exceed one CU, so a row is cut into NS pieces of at most kPcVR * 512
+// float4 of each, one 512-thread workgroup per piece holding its g and y in
+// registers: every input crosses HBM once (k_smx_res_bwd streams y twice).
+// The pieces of a row exchange their partial dots through device memory:
+//   * each piece's workgroup writes (epoch << 32 | partial bits) to its slot
+//     with a device-scope atomic exchange (epoch: a per-launch tag from the
+//     host, never 0, so no clearing is needed);
+//   * thread 0 polls the other pieces' slots (device-scope atomic ors of 0)
+//     until each carries this launch's epoch or `spin` ticks of the 100 MHz
+//     real-time counter have passed;
+//   * a piece still missing then is recomputed by this workgroup from HBM
+//     (its g and y read again, summed in the same order, so the bits equal
+//     the owner's): the wait is bounded and the result never depends on
+//     whether a partner was resident.  Pieces of a row are adjacent in the
+//     grid, so they normally run together.
+// The row's dot is the sum of the NS partials in piece order in every
+// workgroup, so all pieces use the same value.
+// ---------------------------------------------------------------------------
+constexpr int kPcMax = 16;                     // most pieces per row
+constexpr int kSmxSlots = 1 << 16;             // exchange slots (rows * NS wrap around)
+
+}  // namespace
+}  // namespace tpr
+
+static __device__ unsigned long long smx_slots[tpr::kSmxSlots];
+
+namespace tpr {
+namespace {
+
+template <int NT, int PT, int kPcVR>
+__global__ __launch_bounds__(PT) void k_smx_bwd_pieces(SmxArgs p, int ns, int pv, unsigned epoch, int spin) {
+    __shared__ float sh[PT / kWave];
+    __shared__ float parts[kPcMax];
+    __shared__ unsigned missing;
+    constexpr int aux = NT ? 2 : 0;
+    const int t = threadIdx.x;
+    const long long row = blockIdx.x / ns;
+    const int pc = (int)(blockIdx.x % ns);
+    const int q = (int)(p.n >> 2);
+    const float* ra = p.a + row * p.sa;
+    const float* rb = p.b + row * p.sb;
+    auto rsrc = [&](const float* base, int i) {
+        const int v0 = i * pv;
+        const int len = max(0, min(q, v0 + pv) - v0);
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base + 4LL * v0), (short)0, len * 16, kBufWord3);
+    };
+    auto vd = [](f32x4 x, f32x4 y) { return (x.x * y.x + x.y * y.y) + (x.z * y.z + x.w * y.w); };
+    const __amdgpu_buffer_rsrc_t bg = rsrc(ra, pc), by = rsrc(rb, pc);
+    f32x4 g[kPcVR], y[kPcVR];
+#pragma unroll
+    for (int j = 0; j < kPcVR; ++j) g[j] = __builtin_amdgcn_raw_buffer_load_b128(bg, (j * PT + t) * 16, 0, aux);
+#pragma unroll
+    for (int j = 0; j < kPcVR; ++j) y[j] = __builtin_amdgcn_raw_buffer_load_b128(by, (j * PT + t) * 16, 0, aux);
+    float s = 0.0f;  // vectors past the piece read 0 (buffer range check) and add nothing
+#pragma unroll
+    for (int j = 0; j < kPcVR; ++j) s += vd(g[j], y[j]);
+    s = grp<PT, false>(s, sh);
+    if (t == 0) {
+        parts[pc] = s;
+        unsigned need = 0;
+        if (ns > 1) {
+            unsigned long long* slot = smx_slots;
+            const long long base = row * ns;
+            __hip_atomic_exchange(slot + ((base + pc) & (kSmxSlots - 1)),
+                                  ((unsigned long long)epoch << 32) | __float_as_uint(s), __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+            need = ((1u << ns) - 1u) & ~(1u << pc);
+            const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+            for (;;) {
+                for (int i = 0; i < ns; ++i) {
+                    if (!((need >> i) & 1u)) continue;
+                    const unsigned long long v = __hip_atomic_fetch_or(slot + ((base + i) & (kSmxSlots - 1)), 0ull,
+                                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if ((unsigned)(v >> 32) == epoch) {
+                        parts[i] = __uint_as_float((unsigned)v);
+                        need &= ~(1u << i);
+                    }
+                }
+                if (need == 0 || __builtin_amdgcn_s_memrealtime() - t0 > (unsigned long long)spin) break;
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        missing = need;
+    }
+    __syncthreads();
+    const unsigned miss = missing;
+    for (int i = 0; i < ns; ++i) {
+        if (!((miss >> i) & 1u)) continue;  // uniform
+        const __amdgpu_buffer_rsrc_t mg = rsrc(ra, i), my = rsrc(rb, i);
+        float s2 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kPcVR; ++j)
+            s2 += vd(__builtin_amdgcn_raw_buffer_load_b128(mg, (j * PT + t) * 16, 0, 0),
+                     __builtin_amdgcn_raw_buffer_load_b128(my, (j * PT + t) * 16, 0, 0));
+        s2 = grp<PT, false>(s2, sh);
+        if (t == 0) parts[i] = s2;
+        __syncthreads();
+    }
+    float dot = parts[0];
+    for (int i = 1; i < ns; ++i) dot += parts[i];
+    const __amdgpu_buffer_rsrc_t bo = rsrc(p.out + row * p.n, pc);
+#pragma unroll
+    for (int j = 0; j < kPcVR; ++j) {
+        const f32x4 r = {outv<BWD>(g[j].x, y[j].x, dot, 0.0f), outv<BWD>(g[j].y, y[j].y, dot, 0.0f),
+                         outv<BWD>(g[j].z, y[j].z, dot, 0.0f), outv<BWD>(g[j].w, y[j].w, dot, 0.0f)};
+        __builtin_amdgcn_raw_buffer_store_b128(r, bo, (j * PT + t) * 16, 0, aux);  // past the piece: dropped
     }
 }
 
@@ -1294,10 +1408,47 @@ int launch_res(const SmxArgs& a, int vr, hipStream_t st) {
 #undef TPR_RES
 }
 
+// Pieces per row for k_smx_bwd_pieces with PT-thread workgroups (0: not
+// taken): softmax gradients of rows of 16384 .. kPcMax * PT * kPcVR * 4
+// floats, 16-byte vectors.
+int bwd_pieces(long long n, int vw, int pt, int vr) {
+    if (vw != 4 || n <= 16384 || knobs().smx_pieces < 0 || knobs().smx_two_pass) return 0;
+    const long long q = n / 4;
+    const long long per = (long long)pt * vr;
+    const long long ns = (q + per - 1) / per;
+    return ns <= kPcMax ? (int)ns : 0;
+}
+
+template <int PT, int VR>
+int launch_bwd_pieces(const SmxArgs& a, int ns, hipStream_t st) {
+    const long long grid = a.rows * ns;
+    if (grid > 0x7fffffffLL) return fail(TPR_ERR_INVALID_ARG, "tpr_softmax: too many row pieces");
+    const long long q = a.n / 4;
+    const int pv = (int)((q + ns - 1) / ns);
+    // per-launch tag of the partial-dot slots: never 0 (the slots' initial value)
+    static std::atomic<unsigned> epoch_ctr{0};
+    unsigned ep = epoch_ctr.fetch_add(1, std::memory_order_relaxed) + 1u;
+    if (ep == 0) ep = epoch_ctr.fetch_add(1, std::memory_order_relaxed) + 1u;
+    // wait for the row's other pieces up to 40 us (100 MHz ticks); the test
+    // knob smx_spin = -1 makes every piece recompute the others instead
+    const int spin = knobs().smx_spin < 0 ? 0 : 4000;
+    if (a.nt) hipLaunchKernelGGL((k_smx_bwd_pieces<1, PT, VR>), dim3((unsigned)grid), dim3(PT), 0, st, a, ns, pv, ep, spin);
+    else hipLaunchKernelGGL((k_smx_bwd_pieces<0, PT, VR>), dim3((unsigned)grid), dim3(PT), 0, st, a, ns, pv, ep, spin);
+    return check_launch("tpr_softmax (gradient, row pieces)");
+}
+
 template <int MODE>
 int run_rows(const SmxArgs& a0, int vw, hipStream_t st) {
     SmxArgs a = a0;
     const int two_pass = knobs().smx_two_pass;
+    // softmax gradient: g and y both held (row pieces over workgroups), each read once
+    if constexpr (MODE == BWD) {
+        // 512-thread pieces of 24 float4 per lane; measured on MI355X (us):
+        // [256, 151936] 84.8 against 90.4 (256-thread pieces), 90.9 (12 float4
+        // per lane, two workgroups per CU) and 96.0 (g held, y read twice);
+        // [1024, 32768] 67.2 against 74.2 (g held)
+        if (const int ns = bwd_pieces(a.n, vw, 512, 24)) return launch_bwd_pieces<512, 24>(a, ns, st);
+    }
     // rows of 16384..153600 floats, at least one per CU: one row per CU in
     // registers + LDS (forward: x held; gradients: g held, y streamed).
     // Measured on MI355X at [1024, 32768] against the register-only kernels:

@@ -26,7 +26,7 @@ torch = pytest.importorskip("torch")
 @pytest.fixture(autouse=True)
 def _reset_knobs():
     yield
-    for k in ("smx_two_pass", "smx_split", "smx_lanes", "smx_res", "general", "nt"):
+    for k in ("smx_two_pass", "smx_split", "smx_lanes", "smx_res", "general", "nt", "smx_pieces", "smx_spin"):
         _capi.debug_set(k, 0)
 
 
@@ -298,14 +298,51 @@ def test_backward_rows(log, plan):
 
 @pytest.mark.parametrize("log", [False, True])
 @pytest.mark.parametrize("res", [0, -1])
-def test_backward_long_rows(log, res):
-    # softmax / log_softmax gradients over rows of 16384..153600: g held in
-    # registers + LDS while y streams (res=0; once for log_softmax, twice for
-    # softmax), or the two-pass kernel (res=-1)
+@pytest.mark.parametrize("pieces", [0, -1])
+def test_backward_long_rows(log, res, pieces):
+    # softmax / log_softmax gradients over rows of 16384..153600: softmax by
+    # row pieces holding g and y (pieces=0), else g held in registers + LDS
+    # while y streams (res=0; once for log_softmax, twice for softmax), or the
+    # two-pass kernel (res=-1)
     _capi.debug_set("smx_split", -1)
     _capi.debug_set("smx_res", res)
-    for i, n in enumerate([16384, 20000, 32772, 50260, 114688, 151936, 153600]):
+    _capi.debug_set("smx_pieces", pieces)
+    for i, n in enumerate([16384, 20000, 32772, 49152, 49156, 50260, 114688, 151936, 153600]):
         check_bwd((3, n), 1, log, 400 + i)
+
+
+@pytest.mark.parametrize("spin", [0, -1])
+def test_backward_row_pieces(spin):
+    """Softmax gradients by row pieces (g and y held, partial dots exchanged
+    between the pieces' workgroups), with the exchange (spin=0) and with every
+    piece recomputing the others' partials from memory (spin=-1, the path a
+    piece takes when a partner is not resident in time): rows of 1..8 pieces,
+    ragged last pieces, more rows than CUs."""
+    _capi.debug_set("smx_spin", spin)
+    for i, (rows, n) in enumerate([(3, 49152), (2, 49156), (5, 98308), (3, 151936), (2, 200000), (2, 393216),
+                                   (300, 20000)]):
+        check_bwd((rows, n), 1, False, 600 + i)
+
+
+def test_backward_row_pieces_exchange_equals_recompute():
+    """The exchanged partial dots and the recomputed ones are the same bits, so
+    the gradient does not depend on whether the pieces met: C5-shaped rows."""
+    rng = np.random.default_rng(31)
+    g = torch.from_numpy(rng.standard_normal((256, 151936)).astype(np.float32)).cuda()
+    y = torch.softmax(torch.from_numpy((rng.standard_normal((256, 151936)) * 3).astype(np.float32)), -1).cuda()
+    a = _capi.softmax(g, -1, grad_of=y)
+    _capi.debug_set("smx_spin", -1)
+    b = _capi.softmax(g, -1, grad_of=y)
+    _capi.debug_set("smx_spin", 0)
+    c = _capi.softmax(g, -1, grad_of=y)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    assert torch.equal(a.view(torch.int32), c.view(torch.int32))
+    # against fp64 on a sample of rows
+    g64, y64 = g[:8].double().cpu().numpy(), y[:8].double().cpu().numpy()
+    ref = (g64 - (g64 * y64).sum(1, keepdims=True)) * y64
+    tol = 1e-5 * (np.abs(g64) + np.abs(g64 * y64).sum(1, keepdims=True)) * np.abs(y64) + 1e-30
+    assert np.all(np.abs(a[:8].double().cpu().numpy() - ref) <= tol)
 
 
 @pytest.mark.parametrize("log", [False, True])
