@@ -118,12 +118,15 @@ AllocatorStats allocatorStats(int device_index) {
     s.pending_bytes = c.pending_bytes;
     s.device_allocs = c.device_allocs;
     s.requests = c.requests;
+    s.leaked_bytes = c.leaked_bytes;
     return s;
 }
 
 void emptyCache() {
     for (DeviceCache* c : rocm_allocators().all()) c->release_all();
 }
+
+void releaseStreamBlocks(int device_index, void* stream) { rocm_allocators().of(device_index).release_stream(stream); }
 
 int rocmDeviceCount() {
     int n = 0;

@@ -24,6 +24,17 @@
 //   bool  Backend::done(Event)               true once it has completed
 //   void  Backend::destroy(Event)
 //   void  Backend::wait_all()                every queued kernel has finished
+//
+// free() runs inside a tensor's deleter, possibly while the process exits, so
+// it never throws: if recording an event fails it waits for the whole device
+// instead (the block is then idle and goes straight to its free list), and if
+// that fails too the block is dropped (kept out of every list, counted in
+// leaked_bytes) rather than handed out again unsafely.
+//
+// Free lists are keyed by the stream handle.  A runtime may give a destroyed
+// stream's handle to a new stream, so before destroying a stream that
+// allocated blocks, call release_stream(s): it drains the device and returns
+// every block owned by `s` to the runtime.
 #pragma once
 
 #include <cstddef>
@@ -42,6 +53,7 @@ struct CacheStats {
     int64_t pending_bytes = 0;    // freed, waiting for other streams' events
     int64_t device_allocs = 0;    // raw_alloc calls that succeeded
     int64_t requests = 0;         // allocate() calls
+    int64_t leaked_bytes = 0;     // dropped by free() after the runtime failed (never reused)
 };
 
 template <class Backend>
@@ -108,9 +120,43 @@ public:
             return;
         }
         Pending pd{p, b.size, b.stream, {}};
-        for (Stream s : b.uses) pd.events.push_back(be_.record(s));
+        try {
+            for (Stream s : b.uses) pd.events.push_back(be_.record(s));
+        } catch (...) {
+            for (const Event& e : pd.events) destroy_quietly(e);
+            try {
+                be_.wait_all();  // nothing queued anywhere still uses the block
+                free_[{b.stream, b.size}].push_back(p);
+                stats_.cached_bytes += (int64_t)b.size;
+            } catch (...) {
+                stats_.leaked_bytes += (int64_t)b.size;
+            }
+            return;
+        }
         pending_.push_back(std::move(pd));
         stats_.pending_bytes += (int64_t)b.size;
+    }
+
+    // Returns every block owned by `stream` (free or pending) to the runtime,
+    // after draining the device.  Call it before destroying a stream that
+    // allocated blocks: its handle may be reused by a later stream.
+    void release_stream(Stream stream) {
+        be_.wait_all();
+        std::vector<void*> blocks;
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            collect_pending_locked();  // all events have completed
+            for (auto it = free_.begin(); it != free_.end();) {
+                if (it->first.first != stream) {
+                    ++it;
+                    continue;
+                }
+                for (void* q : it->second) blocks.push_back(q);
+                stats_.cached_bytes -= (int64_t)(it->first.second * it->second.size());
+                it = free_.erase(it);
+            }
+        }
+        for (void* q : blocks) be_.raw_free(q);
     }
 
     // Returns every cached block to the runtime (pending ones after their
@@ -142,6 +188,13 @@ public:
     Backend& backend() { return be_; }
 
 private:
+    void destroy_quietly(const Event& e) {
+        try {
+            be_.destroy(e);
+        } catch (...) {
+        }
+    }
+
     struct Live {
         size_t size;
         Stream stream;              // allocation stream: the block's owner

@@ -305,6 +305,8 @@ PYBIND11_MODULE(_C, m) {
     r.def("current_stream", [](int dev) { return reinterpret_cast<uintptr_t>(currentStream(dev)); },
           py::arg("device") = 0);
     r.def("empty_cache", &emptyCache);
+    r.def("release_stream_blocks", [](uintptr_t s, int dev) { releaseStreamBlocks(dev, reinterpret_cast<void*>(s)); },
+          py::arg("stream"), py::arg("device") = 0);
     r.def("memory_stats", [](int dev) {
         AllocatorStats s = allocatorStats(dev);
         py::dict d;
@@ -313,6 +315,7 @@ PYBIND11_MODULE(_C, m) {
         d["pending_bytes"] = s.pending_bytes;
         d["device_allocs"] = s.device_allocs;
         d["requests"] = s.requests;
+        d["leaked_bytes"] = s.leaked_bytes;
         return d;
     }, py::arg("device") = 0);
     r.def("abi_version", [] { return tpr_abi_version(); });

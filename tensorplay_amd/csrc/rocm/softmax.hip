@@ -1031,8 +1031,10 @@ __global__ __launch_bounds__(kWave * BY) void k_smx_cols4r(SmxColArgs p) {
     constexpr bool BW = MODE >= BWD;
     constexpr int RW = kWave / CW;  // rows per wave step
     constexpr int RS = RW * BY;      // rows per workgroup step
-    __shared__ float shm[BY][CW][4];
-    __shared__ float shs[BY][CW][4];
+    // per-wave (max, sum) of each column as whole float4 per lane: one 16-byte
+    // LDS store / load per lane, consecutive lanes on consecutive banks
+    __shared__ f32x4 shm[BY][CW];
+    __shared__ f32x4 shs[BY][CW];
     const int lane = threadIdx.x % kWave;
     const int w = threadIdx.x / kWave;
     const int cl = lane % CW, rl = lane / CW;
@@ -1097,22 +1099,31 @@ __global__ __launch_bounds__(kWave * BY) void k_smx_cols4r(SmxColArgs p) {
         }
     }
     if (rl == 0) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            shm[w][cl][q] = m[q];
-            shs[w][cl][q] = sm[q];
-        }
+        shm[w][cl] = f32x4{m[0], m[1], m[2], m[3]};
+        shs[w][cl] = f32x4{sm[0], sm[1], sm[2], sm[3]};
     }
     __syncthreads();
+    // merge the waves one float4 pair at a time (few live registers: the
+    // slice values are still held)
+    f32x4 Mv = shm[0][cl], Sv = shs[0][cl];
+    for (int k = 1; k < BY; ++k) {
+        const f32x4 mk = shm[k][cl], sk = shs[k][cl];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if constexpr (!BW) {
+                float M = Mv[q], S = Sv[q];
+                ms_merge(M, S, mk[q], sk[q]);
+                Mv[q] = M;
+                Sv[q] = S;
+            } else {
+                Sv[q] += sk[q];
+            }
+        }
+    }
     float st0[4], st1[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        float M = shm[0][cl][q], S = shs[0][cl][q];
-#pragma unroll
-        for (int k = 1; k < BY; ++k) {
-            if constexpr (!BW) ms_merge(M, S, shm[k][cl][q], shs[k][cl][q]);
-            else S += shs[k][cl][q];
-        }
+        const float M = Mv[q], S = Sv[q];
         if constexpr (!BW) {
             if (M == -INFINITY) {
                 st0[q] = NAN;

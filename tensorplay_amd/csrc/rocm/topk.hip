@@ -2433,28 +2433,31 @@ void launch_short_small_le(const TopkArgs& a, hipStream_t st) {
 }
 
 template <int L, int EB>
-void launch_short_small_l(const TopkArgs& a, hipStream_t st) {
+int launch_short_small_l(const TopkArgs& a, hipStream_t st) {
     constexpr int per = 16 / EB * L;  // elements of one vector round of the L lanes
     const int e4 = (a.cols + per - 1) / per;  // <= 4 * EB (cols <= 4096, L >= cols / 16 below 64 lanes)
     if (e4 <= 1) launch_short_small_le<L, 1, EB>(a, st);
     else if (e4 <= 2) launch_short_small_le<L, 2, EB>(a, st);
-    else if (EB == 1 || e4 <= 4) launch_short_small_le<L, 4, EB>(a, st);
-    else if constexpr (EB == 2) launch_short_small_le<L, 8, EB>(a, st);
+    else if (e4 <= 4) launch_short_small_le<L, 4, EB>(a, st);
+    else if (EB == 2 && e4 <= 8) launch_short_small_le<L, EB == 2 ? 8 : 4, EB>(a, st);
+    else return fail(TPR_ERR_INVALID_ARG, "tpr_topk: row too long for the lane-group kernel on 1- / 2-byte elements");
+    return TPR_OK;
 }
 
 int launch_short_small(const TopkArgs& a, int eb, hipStream_t st) {
     int L = 16;  // as launch_short: L >= 2k, and L >= cols / 16 up to 64 lanes
     while (L < 64 && (L < 2 * a.k || L * 16 < a.cols)) L *= 2;
+    int rc;
     if (eb == 1) {
-        if (L == 16) launch_short_small_l<16, 1>(a, st);
-        else if (L == 32) launch_short_small_l<32, 1>(a, st);
-        else launch_short_small_l<64, 1>(a, st);
+        if (L == 16) rc = launch_short_small_l<16, 1>(a, st);
+        else if (L == 32) rc = launch_short_small_l<32, 1>(a, st);
+        else rc = launch_short_small_l<64, 1>(a, st);
     } else {
-        if (L == 16) launch_short_small_l<16, 2>(a, st);
-        else if (L == 32) launch_short_small_l<32, 2>(a, st);
-        else launch_short_small_l<64, 2>(a, st);
+        if (L == 16) rc = launch_short_small_l<16, 2>(a, st);
+        else if (L == 32) rc = launch_short_small_l<32, 2>(a, st);
+        else rc = launch_short_small_l<64, 2>(a, st);
     }
-    return check_launch("k_topk_short");
+    return rc != TPR_OK ? rc : check_launch("k_topk_short");
 }
 
 int launch_short(const TopkArgs& a, bool vec, hipStream_t st) {

@@ -4,6 +4,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <set>
+#include <stdexcept>
 #include <vector>
 
 #include "CachingAllocatorCore.h"
@@ -17,6 +18,8 @@ struct MockBackend {
     size_t* budget;                     // bytes raw_alloc may still hand out
     std::set<void*>* raw_live;
     int* waits;
+    bool* fail_record;  // record() throws (a failing runtime)
+    bool* fail_wait;    // wait_all() throws too
 
     void* raw_alloc(size_t n) {
         if (n > *budget) return nullptr;
@@ -30,6 +33,7 @@ struct MockBackend {
         std::free(p);
     }
     Event record(void* s) {
+        if (*fail_record) throw std::runtime_error("record failed");
         ev_done->push_back(false);
         stream_of_ev->push_back(s);
         return (int)ev_done->size() - 1;
@@ -37,6 +41,7 @@ struct MockBackend {
     bool done(Event e) { return (*ev_done)[e]; }
     void destroy(Event) {}
     void wait_all() {
+        if (*fail_wait) throw std::runtime_error("wait failed");
         ++*waits;
         for (size_t i = 0; i < ev_done->size(); ++i) (*ev_done)[i] = true;
     }
@@ -57,7 +62,8 @@ int main() {
     size_t budget = 1 << 30;
     std::set<void*> raw;
     int waits = 0;
-    CachingAllocatorCore<MockBackend> a(MockBackend{&ev, &ev_stream, &budget, &raw, &waits});
+    bool fail_record = false, fail_wait = false;
+    CachingAllocatorCore<MockBackend> a(MockBackend{&ev, &ev_stream, &budget, &raw, &waits, &fail_record, &fail_wait});
     void* A = (void*)0xA;
     void* B = (void*)0xB;
 
@@ -123,6 +129,51 @@ int main() {
     a.release_all();
     CHECK(raw.empty());
     CHECK(a.stats().allocated_bytes == 0);
+
+    // 5. free() never throws: a failing event record falls back to draining the
+    // device (the block becomes reusable on its owner stream) ...
+    size_t s5 = 1000;
+    void* r5 = a.allocate(s5, A);
+    a.record_stream(r5, B);
+    fail_record = true;
+    const int w0 = waits;
+    a.free(r5);  // must not throw
+    CHECK(waits == w0 + 1);
+    CHECK(a.stats().pending_bytes == 0 && a.stats().cached_bytes == 1024);
+    fail_record = false;
+    size_t s6 = 1000;
+    CHECK(a.allocate(s6, A) == r5);
+    // ... and when draining fails too, the block is dropped, never reused
+    a.record_stream(r5, B);
+    fail_record = fail_wait = true;
+    a.free(r5);
+    fail_record = fail_wait = false;
+    CHECK(a.stats().leaked_bytes == 1024);
+    size_t s7 = 1000;
+    CHECK(a.allocate(s7, A) != r5);
+
+    // 6. release_stream returns one stream's blocks (free and pending) to the
+    // runtime and keeps the other streams' cache
+    a.release_all();
+    size_t s8 = 1000, s9 = 1000, s10 = 1000;
+    void* xa = a.allocate(s8, A);
+    void* xb = a.allocate(s9, B);
+    void* xa2 = a.allocate(s10, A);
+    a.record_stream(xa2, B);
+    a.free(xa);
+    a.free(xb);
+    a.free(xa2);  // pending on B's event
+    CHECK(a.stats().pending_bytes == 1024);
+    a.release_stream(A);
+    CHECK(raw.count(xa) == 0 && raw.count(xa2) == 0 && raw.count(xb) == 1);
+    CHECK(a.stats().cached_bytes == 1024 && a.stats().pending_bytes == 0);
+    size_t s11 = 1000;
+    CHECK(a.allocate(s11, B) == xb);
+    // the test's own cleanup: blocks still handed out, and the dropped one
+    for (void* p : std::vector<void*>(raw.begin(), raw.end())) {
+        raw.erase(p);
+        std::free(p);
+    }
 
     std::printf(failures ? "FAILED %d\n" : "OK\n", failures);
     return failures ? 1 : 0;

@@ -503,10 +503,15 @@ def test_long_rows_32bit_integers(dt, knob):
 
 
 @pytest.mark.parametrize("dt", [np.int8, np.uint8, np.int16, np.uint16, np.bool_])
-def test_small_integer_rows(dt):
-    """1- and 2-byte elements through the register radix select: one / two
-    radix passes, grouped loads on aligned rows (cols a multiple of 4 or 8 here)
-    and element loads on the others, ties everywhere (few distinct values)."""
+@pytest.mark.parametrize("short", [0, -1])
+def test_small_integer_rows(dt, short):
+    """1- and 2-byte elements, ties everywhere (few distinct values).  With
+    short=0 aligned rows of <= 4096 elements and k <= 64 take the lane-group
+    kernel and the rest the register radix select; with short=-1 (the lane-group
+    kernel off) every row takes the radix select: one / two radix passes,
+    grouped loads on aligned rows (cols a multiple of 4 or 8 here) and element
+    loads on the others."""
+    _capi.debug_set("topk_short", short)
     rng = np.random.default_rng(79)
     for rows, cols, ks in [(2000, 1024, (1, 8, 100)), (300, 4096, (16, 64, 1000)), (77, 1003, (5, 50)),
                            (40, 32768, (300,)), (3, 100000, (256,))]:
