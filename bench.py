@@ -534,7 +534,7 @@ def run_sections(torch, capi, only, stream, steps, warmup, keep):
         ets = {}
         for (rows, cols, k, dt) in ((65536, 256, 8, "f32"), (16384, 1024, 32, "f32"), (4096, 2048, 1000, "f32"),
                                     (256, 151936, 256, "f32"), (16384, 1024, 32, "i32"), (1024, 32768, 64, "i32"),
-                                    (16384, 1024, 32, "i8")):
+                                    (16384, 1024, 32, "i8"), (256, 151936, 50, "i8")):
             esz = {"f32": 4, "i32": 4, "i8": 1}[dt]
             nb = max(3, (768 << 20) // (rows * cols * esz))
             bs = [gen(torch, (rows, cols), "uniform", 7000 + i, dev) for i in range(nb)]

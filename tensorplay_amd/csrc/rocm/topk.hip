@@ -79,6 +79,7 @@ constexpr int kShortK2 = 128;                 // largest k of the lane-group ker
 // radix 55), while up to it the 4-wave kernel mostly wins (k = 150:
 // [1024, 8192] 23 against 35, [4096, 8192] 76 against 110).
 constexpr int kWave4K = 192;
+constexpr int kWaveSmallK = 128;              // largest k of the wave kernel on 1- / 2-byte rows
 constexpr int kWB = 256;                      // per-wave list capacity
 constexpr int kWaveCompact = 192;             // per-wave list size that always triggers compaction
 constexpr int kSlice = 64 * 16;               // elements per wave slice (4 float4 per lane)
@@ -478,8 +479,24 @@ __device__ uint32_t wave_kth_bound(const unsigned long long* list, uint32_t* his
 
 // Exact multi-pass path over p[lo, hi) (any data): leaves the k selected
 // composites in cand[0..k) (unordered).  hi - lo >= k.
-template <int NT>
-__device__ void exact_select(BlockScratch& bs, unsigned long long* cand, const float* p, int lo, int hi, int k,
+// Sortable 32-bit key of element e of a row of EB-byte elements (EB = 4:
+// float32 / int32 / uint32 by ikind; EB = 1, 2: 8- and 16-bit integers and
+// bool, key = the element with its sign bit flipped when signed, complemented
+// for largest = 0: the lane-group kernel's key).
+template <int EB>
+__device__ __forceinline__ uint32_t row_key(const void* p, int e, int largest, int ikind) {
+    if constexpr (EB == 4) {
+        return elem_key(static_cast<const float*>(p)[e], largest, ikind);
+    } else {
+        constexpr uint32_t em = EB == 1 ? 0xffu : 0xffffu;
+        const uint32_t v = EB == 1 ? static_cast<const uint8_t*>(p)[e] : static_cast<const uint16_t*>(p)[e];
+        const uint32_t sm = ikind == 1 ? (em >> 1) + 1u : 0u;
+        return (v ^ sm ^ (largest ? 0u : 0xffffffffu)) & em;
+    }
+}
+
+template <int NT, int EB = 4>
+__device__ void exact_select(BlockScratch& bs, unsigned long long* cand, const void* p, int lo, int hi, int k,
                              int largest, int ikind) {
     constexpr int NW = NT / 64;
     const int tid = threadIdx.x;
@@ -491,7 +508,7 @@ __device__ void exact_select(BlockScratch& bs, unsigned long long* cand, const f
         if (tid < 256) bs.hist[tid] = 0;
         __syncthreads();
         for (int e = lo + tid; e < hi; e += NT) {
-            const uint32_t key = elem_key(p[e], largest, ikind);
+            const uint32_t key = row_key<EB>(p, e, largest, ikind);
             if ((key & pmask) == prefix) atomicAdd(&bs.hist[(key >> shift) & 255u], 1u);
         }
         __syncthreads();
@@ -516,7 +533,7 @@ __device__ void exact_select(BlockScratch& bs, unsigned long long* cand, const f
     __syncthreads();
     for (int base = lo; base < hi; base += NT) {
         const int e = base + tid;
-        const uint32_t key = (e < hi) ? elem_key(p[e], largest, ikind) : 0u;
+        const uint32_t key = (e < hi) ? row_key<EB>(p, e, largest, ikind) : 0u;
         const bool gt = (e < hi) && key > T;
         const bool eq = (e < hi) && key == T;
         if (gt) cand[atomicAdd(&bs.count, 1)] = comp_key(key, (uint32_t)e);
@@ -540,6 +557,7 @@ __device__ void exact_select(BlockScratch& bs, unsigned long long* cand, const f
 
 // Writes the ranked top k of one segment: the final values/indices when the row
 // is not split, else the k composites for the merge pass.
+template <int EB = 4>
 __device__ __forceinline__ void write_segment(const TopkArgs& a, long long row, int seg, const float* p,
                                               const unsigned long long* sel, int k) {
     if (a.nseg == 1 && a.sample) {
@@ -548,8 +566,15 @@ __device__ __forceinline__ void write_segment(const TopkArgs& a, long long row, 
         for (int i = threadIdx.x; i < k; i += blockDim.x) {
             const uint32_t idx = comp_index(sel[i]);
             const uint32_t key = (uint32_t)(sel[i] >> 32);
-            a.out_v[row * k + i] = a.ikind ? __uint_as_float(int_key_bits(key, a.ikind, a.largest, 0xffffffffu))
-                                           : selected_value(p, key, idx, a.largest);
+            if constexpr (EB == 1) {
+                reinterpret_cast<uint8_t*>(a.out_v)[row * k + i] = (uint8_t)int_key_bits(key, a.ikind, a.largest, 0xffu);
+            } else if constexpr (EB == 2) {
+                reinterpret_cast<uint16_t*>(a.out_v)[row * k + i] =
+                    (uint16_t)int_key_bits(key, a.ikind, a.largest, 0xffffu);
+            } else {
+                a.out_v[row * k + i] = a.ikind ? __uint_as_float(int_key_bits(key, a.ikind, a.largest, 0xffffffffu))
+                                               : selected_value(p, key, idx, a.largest);
+            }
             a.out_i[row * k + i] = (long long)idx;
         }
     } else {
@@ -651,9 +676,46 @@ __device__ __forceinline__ void slice_keys(const float4 (&cur)[SV], int base, in
     }
 }
 
-template <bool VEC, int SV, int OCC, int PD, int NW, int KWB = kWB>
+// Keys of one slice of EB-byte elements: slice_keys for 4-byte rows; for 1-
+// and 2-byte integer rows each lane's SV = EB vectors hold 16 elements (lane
+// l, vector j: elements (j*64 + l)*(16/EB) .. +16/EB-1 of the slice, byte order
+// inside a vector = element order), keyed as the lane-group kernel does.
+template <int EB, int SV>
+__device__ __forceinline__ void slice_keys_eb(const float4 (&cur)[SV], int base, int hi, int largest, int ikind,
+                                              uint32_t (&key)[16 * SV / EB]) {
+    if constexpr (EB == 4) {
+        slice_keys(cur, base, hi, largest, ikind, key);
+    } else {
+        constexpr int EPV = 16 / EB, EPW = 4 / EB;
+        constexpr uint32_t em = EB == 1 ? 0xffu : 0xffffu;
+        const uint32_t sm = ikind == 1 ? (em >> 1) + 1u : 0u;
+        const uint32_t lm = largest ? 0u : 0xffffffffu;
+        const int lim = hi - base;
+        const int lane = __lane_id();
+#pragma unroll
+        for (int j = 0; j < SV; ++j) {
+            const uint32_t wv[4] = {__float_as_uint(cur[j].x), __float_as_uint(cur[j].y), __float_as_uint(cur[j].z),
+                                    __float_as_uint(cur[j].w)};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+#pragma unroll
+                for (int t = 0; t < EPW; ++t) {
+                    const int q = j * EPV + c * EPW + t;
+                    const uint32_t kv = (((wv[c] >> (8 * EB * t)) & em) ^ sm ^ lm) & em;
+                    key[q] = ((j * 64 + lane) * EPV + c * EPW + t < lim) ? kv : 0u;
+                }
+            }
+        }
+    }
+}
+
+template <bool VEC, int SV, int OCC, int PD, int NW, int KWB = kWB, int EB = 4>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8))) void k_topk_wave(TopkArgs a) {
-    constexpr int kSl = 256 * SV;  // elements per wave slice
+    static_assert(EB == 4 || (SV == EB && VEC), "1- / 2-byte rows: SV = EB float4 per lane, 16-byte aligned");
+    constexpr int kSlF = 256 * SV;         // 4-byte words per wave slice
+    constexpr int kSl = kSlF * 4 / EB;     // elements per wave slice (1024)
+    constexpr int kNK = 16 * SV / EB;      // keys per lane per slice (16)
+    constexpr int kEPV = 16 / EB;          // elements per 16-byte vector
     constexpr int kW = NW;         // waves of this workgroup
     constexpr int kT = NW * 64;
     constexpr int kB = NW * KWB;   // gathered-list capacity
@@ -664,7 +726,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave-uniform: scalar loop control
     const long long row = blockIdx.x / a.nseg;
     const int seg = blockIdx.x % a.nseg;
-    const float* p = a.in + row * a.row_stride;
+    const char* pr = reinterpret_cast<const char*>(a.in) + row * a.row_stride * EB;
+    const float* p = reinterpret_cast<const float*>(pr);
     const int k = a.k;
     const int largest = a.largest;
     const int lo = seg * a.seg_len;
@@ -688,15 +751,20 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
     // register buffers alternate, so two slices are in flight).
     float4 bufA[SV];
     float4 bufB[PD == 2 ? SV : 1];
-    uint32_t key[4 * SV];
-    const __amdgpu_buffer_rsrc_t rs = segment_rsrc(p + lo, hi - lo);
-    load_slice<VEC, SV>(bufA, rs, w * kSl);
-    if constexpr (PD == 2) load_slice<VEC, SV>(bufB, rs, (w + kW) * kSl);
-    slice_keys(bufA, lo + w * kSl, hi, largest, a.ikind, key);
-    if constexpr (PD == 1) load_slice<VEC, SV>(bufA, rs, (w + kW) * kSl);
-    if constexpr (PD == 2) load_slice<VEC, SV>(bufA, rs, (w + 2 * kW) * kSl);
+    uint32_t key[kNK];
+    // (1- / 2-byte rows: the range is rounded up to whole dwords; elements past
+    // the segment's end inside the last dword are masked in the keys)
+    const __amdgpu_buffer_rsrc_t rs =
+        EB == 4 ? segment_rsrc(p + lo, hi - lo)
+                : __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(pr + (long long)lo * EB), (short)0,
+                                                    ((hi - lo) * EB + 3) & ~3, kBufWord3);
+    load_slice<VEC, SV>(bufA, rs, w * kSlF);
+    if constexpr (PD == 2) load_slice<VEC, SV>(bufB, rs, (w + kW) * kSlF);
+    slice_keys_eb<EB>(bufA, lo + w * kSl, hi, largest, a.ikind, key);
+    if constexpr (PD == 1) load_slice<VEC, SV>(bufA, rs, (w + kW) * kSlF);
+    if constexpr (PD == 2) load_slice<VEC, SV>(bufA, rs, (w + 2 * kW) * kSlF);
     // the first slice of every wave gives the workgroup bound T0
-    const uint32_t rth = wave_rth_of_lane_max(key, 4 * SV, r);
+    const uint32_t rth = wave_rth_of_lane_max(key, kNK, r);
     if (lane == 0) bs.wave_val[w] = rth;
     __syncthreads();
     uint32_t T = 0xffffffffu;
@@ -712,7 +780,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
         T = max(T, __atomic_load_n(&bs.tshared, __ATOMIC_RELAXED));
         int total = 0;
 #pragma unroll
-        for (int q = 0; q < 4 * SV; ++q) total += __popcll(__ballot(key[q] >= T));
+        for (int q = 0; q < kNK; ++q) total += __popcll(__ballot(key[q] >= T));
         while (total > 0 && cnt + total > KWB) {  // no room: drop stale entries / raise T first
             const int before = cnt;
             const uint32_t tn = wave_compact(list, hist, cnt, k, T);
@@ -721,7 +789,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
                 T = tn;
                 total = 0;
 #pragma unroll
-                for (int q = 0; q < 4 * SV; ++q) total += __popcll(__ballot(key[q] >= T));
+                for (int q = 0; q < kNK; ++q) total += __popcll(__ballot(key[q] >= T));
             } else if (cnt == before) {
                 return false;  // nothing could be dropped
             }
@@ -730,13 +798,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
             const unsigned long long lt = lanemask_lt();
             int pos = cnt;
 #pragma unroll
-            for (int q = 0; q < 4 * SV; ++q) {
+            for (int q = 0; q < kNK; ++q) {
                 const bool pass = key[q] >= T;
                 const unsigned long long b = __ballot(pass);
                 if (b == 0ull) continue;  // uniform: most slots hold no candidate
                 if (pass)
                     list[pos + __popcll(b & lt)] =
-                        comp_key(key[q], (uint32_t)(base + 4 * ((q >> 2) * 64 + lane) + (q & 3)));
+                        comp_key(key[q], (uint32_t)(base + ((q / kEPV) * 64 + lane) * kEPV + (q % kEPV)));
                 pos += __popcll(b);
             }
             cnt = pos;
@@ -759,13 +827,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
                 if (!filter(lo + c * kSl)) { over = true; break; }
                 c += kW;
                 if (c >= nsl) break;
-                slice_keys(bufB, lo + c * kSl, hi, largest, a.ikind, key);
-                load_slice<VEC, SV>(bufB, rs, (c + 2 * kW) * kSl);
+                slice_keys_eb<EB>(bufB, lo + c * kSl, hi, largest, a.ikind, key);
+                load_slice<VEC, SV>(bufB, rs, (c + 2 * kW) * kSlF);
                 if (!filter(lo + c * kSl)) { over = true; break; }
                 c += kW;
                 if (c >= nsl) break;
-                slice_keys(bufA, lo + c * kSl, hi, largest, a.ikind, key);
-                load_slice<VEC, SV>(bufA, rs, (c + 2 * kW) * kSl);
+                slice_keys_eb<EB>(bufA, lo + c * kSl, hi, largest, a.ikind, key);
+                load_slice<VEC, SV>(bufA, rs, (c + 2 * kW) * kSlF);
             }
         } else if (PD == 1 && NW == 16 && a.dyn) {
             // Slices past the first two of each wave go to whichever wave asks
@@ -782,9 +850,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
             int nx = w + kW;  // already loading into bufA
             while (c < nsl) {
                 if (c != w) {
-                    slice_keys(bufA, lo + c * kSl, hi, largest, a.ikind, key);
+                    slice_keys_eb<EB>(bufA, lo + c * kSl, hi, largest, a.ikind, key);
                     nx = grab();
-                    load_slice<VEC, SV>(bufA, rs, nx * kSl);  // past the segment: reads 0, no traffic
+                    load_slice<VEC, SV>(bufA, rs, nx * kSlF);  // past the segment: reads 0, no traffic
                 }
                 if (!filter(lo + c * kSl)) { over = true; break; }
                 c = nx;
@@ -793,10 +861,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
             for (; c < nsl; c += kW) {
                 const int base = lo + c * kSl;
                 if (c != w) {
-                    if constexpr (PD == 0) load_slice<VEC, SV>(bufA, rs, c * kSl);
-                    slice_keys(bufA, base, hi, largest, a.ikind, key);
+                    if constexpr (PD == 0) load_slice<VEC, SV>(bufA, rs, c * kSlF);
+                    slice_keys_eb<EB>(bufA, base, hi, largest, a.ikind, key);
                     if constexpr (PD == 1) {
-                        load_slice<VEC, SV>(bufA, rs, (c + kW) * kSl);
+                        load_slice<VEC, SV>(bufA, rs, (c + kW) * kSlF);
                     }
                 }
                 if (!filter(base)) { over = true; break; }
@@ -847,7 +915,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
     // fewer than k gathered: the segment has keys of 0 (integers only; the
     // filter keeps keys >= 1), which the exact select takes
     if (any_over || m < k) {
-        exact_select<kT>(bs, cand, p, lo, hi, k, largest, a.ikind);
+        exact_select<kT, EB>(bs, cand, pr, lo, hi, k, largest, a.ikind);
         m = k;
     } else if (m > max(2 * k, 256)) {
         block_compact<kT>(bs, cand, other, m, k, Tf);
@@ -859,7 +927,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
     int* rank = reinterpret_cast<int*>(other);
     unsigned long long* sel = other + kB / 2;
     rank_select<kT>(cand, rank, sel, m, k);
-    write_segment(a, row, seg, p, sel, k);
+    write_segment<EB>(a, row, seg, p, sel, k);
 }
 
 // ---------------------------------------------------------------------------
@@ -2369,6 +2437,13 @@ TopkRoute route_topk(long long rows, long long cols, long long k, int32_t dtype,
     const int eb = dtype_size(dtype);
     if (eb < 4 && short_ok && short_on && knobs().topk_radix <= 0 && aligned)
         return TopkRoute{TK_SHORT_SMALL, 1, (int)cols, 0, 0};
+    // Longer 1- and 2-byte rows, 16-byte aligned, k <= 128: the wave kernel on
+    // their integer keys wherever it takes a float32 row of the same shape
+    if (eb < 4 && aligned && k <= kWaveSmallK && knobs().topk_radix <= 0 && !radix_route(rows, cols, k, TPR_FLOAT32) &&
+        !(short_ok && short_on)) {
+        const TopkPlan pl = plan_topk(rows, cols, k);
+        if (pl.wave) return TopkRoute{TK_WAVE, pl.nseg, pl.seg_len, pl.nw, pl.ws};
+    }
     if (radix && rsel_route(cols, dtype)) return TopkRoute{TK_RSEL, 1, (int)cols, 0, 0};
     if (const int ns = radix ? rsel_segments(cols, k, dtype) : 0) {
         const int seg_len = (int)((cols + ns - 1) / ns + 3) & ~3;  // segment starts stay 16-byte aligned
@@ -2391,7 +2466,10 @@ extern "C" {
 
 size_t tpr_topk_workspace_bytes(int32_t dtype, int64_t rows, int64_t cols, int64_t k) {
     if (rows <= 0 || cols <= 0 || k <= 0 || k > cols || cols > 0x7fffffffLL || tpr::dtype_size(dtype) == 0) return 0;
-    return tpr::route_topk(rows, cols, k, dtype, cols, true).ws;
+    // the plan can depend on the input's alignment (1- / 2-byte rows take the
+    // wave kernel only when 16-byte aligned): enough for either
+    return std::max(tpr::route_topk(rows, cols, k, dtype, cols, true).ws,
+                    tpr::route_topk(rows, cols, k, dtype, cols, false).ws);
 }
 
 }  // extern "C"
@@ -2585,6 +2663,26 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     }
     if (rt.kind == TK_SHORT) return launch_short(a, vec, st);
     const TopkPlan pl{rt.nseg, rt.seg_len, rt.kind == TK_WAVE, rt.nw, rt.ws};
+    if (rt.kind == TK_WAVE && dtype_size(dtype) < 4) {
+        // 1- / 2-byte rows (16-byte aligned, k <= 128): one or two 16-byte
+        // vectors per lane hold a 1024-element slice
+        const long long grid = rows * pl.nseg;
+        const dim3 blk(pl.nw * 64);
+#define TPR_WAVE_EB(EBV)                                                                                          \
+        if (pl.nw == 16) hipLaunchKernelGGL((k_topk_wave<true, EBV, 4, 1, 16, kWB, EBV>), dim3(grid), blk, 0, st, a); \
+        else if (pl.nw == 4) hipLaunchKernelGGL((k_topk_wave<true, EBV, 8, 0, 4, kWB, EBV>), dim3(grid), blk, 0, st, a); \
+        else hipLaunchKernelGGL((k_topk_wave<true, EBV, 8, 0, 8, kWB, EBV>), dim3(grid), blk, 0, st, a);
+        if (dtype_size(dtype) == 1) {
+            TPR_WAVE_EB(1)
+        } else {
+            TPR_WAVE_EB(2)
+        }
+#undef TPR_WAVE_EB
+        const int rc = check_launch("k_topk_wave");
+        if (rc != TPR_OK || pl.nseg == 1) return rc;
+        hipLaunchKernelGGL(k_topk_merge, dim3(rows), dim3(kMergeT), 0, st, a, (int)dtype);
+        return check_launch("k_topk_merge");
+    }
     const long long grid = rows * pl.nseg;
     if (pl.wave) {
         // 512-thread workgroups (many rows): 8 waves/SIMD without prefetch.

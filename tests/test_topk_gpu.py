@@ -564,3 +564,39 @@ def test_small_integer_short_rows(dt):
                 ev, ei = O.topk_any(xc, k, largest)
                 np.testing.assert_array_equal(gi.cpu().numpy(), ei)
                 np.testing.assert_array_equal(gv.cpu().numpy().view(np.uint8), ev.view(np.uint8))
+
+
+@pytest.mark.parametrize("dt", [np.int8, np.uint8, np.int16, np.uint16, np.bool_])
+@pytest.mark.parametrize("fallback", [0, 1])
+def test_small_integer_long_rows_wave_kernel(dt, fallback):
+    """1- and 2-byte rows longer than the lane-group kernel takes, 16-byte
+    aligned, k <= 128: the wave kernel on their integer keys (one or two
+    16-byte vectors per lane per slice), with 8 / 16 / 4-wave workgroups, split
+    rows merged, heavy ties (few distinct values: most rows take the exact
+    path at some point), and the forced exact path (fallback=1)."""
+    _capi.debug_set("topk_fallback", fallback)
+    rng = np.random.default_rng(97)
+    esz = np.dtype(dt).itemsize
+    for rows, cols, ks in [(1024, 16384, (64,)), (128, 151936, (50,)), (2048, 12288, (100,)),
+                           (16, 500000, (128, 1)), (300, 40000, (33,))]:
+        if dt == np.bool_:
+            x = rng.random((rows, cols)) < 0.01
+        else:
+            info = np.iinfo(dt)
+            x = rng.integers(info.min, info.max, size=(rows, cols), dtype=dt, endpoint=True)
+            x[0] = info.min
+            x[1, ::3] = info.max
+        t = torch.from_numpy(x).cuda()
+        for k in ks:
+            kind = _capi.topk_plan(_capi._torch_dtypes()[t.dtype], rows, cols, k)[0]
+            assert kind == "wave", (dt, rows, cols, k, kind)
+            for largest in (True, False):
+                print(f"case topk-wave dtype={np.dtype(dt).name} shape={x.shape} k={k} largest={largest} "
+                      f"fallback={fallback}", flush=True)
+                gv, gi = _capi.topk(t, k, largest)
+                torch.cuda.synchronize()
+                ev, ei = O.topk_any(x, k, largest)
+                np.testing.assert_array_equal(gi.cpu().numpy(), ei)
+                np.testing.assert_array_equal(gv.cpu().numpy().view(np.uint8), ev.view(np.uint8))
+        del t
+    assert esz in (1, 2)

@@ -90,3 +90,22 @@ def test_benchmark_shapes_plan():
     assert _capi.topk_plan(_capi.FLOAT32, 256, 151936, 50)[0] == "wave"
     assert _capi.topk_plan(_capi.FLOAT32, 16384, 1024, 32)[0] == "short"
     assert _capi.topk_plan(_capi.FLOAT32, 4096, 2048, 1000)[0] == "rsel"
+
+
+def test_workspace_query_covers_every_alignment():
+    """tpr_topk_workspace_bytes does not see the input pointer or stride, so it
+    must cover the plan of an aligned and of an unaligned input alike (1- and
+    2-byte rows take the wave kernel only when 16-byte aligned)."""
+    import ctypes
+    L = _capi.lib()
+    rng = np.random.default_rng(5)
+    for dtype in (_capi.INT8, _capi.UINT16, _capi.FLOAT32, _capi.INT32, _capi.FLOAT64):
+        for _ in range(400):
+            rows = int(rng.choice([1, 7, 42, 256, 1000]))
+            cols = int(rng.integers(4000, 600000))
+            k = int(rng.integers(1, 1025))
+            k = min(k, cols)
+            ws = L.tpr_topk_workspace_bytes(dtype, rows, cols, k)
+            for aligned in (True, False):
+                plan_ws = _capi.topk_plan(dtype, rows, cols, k, cols + (0 if aligned else 1), aligned)[4]
+                assert ws >= plan_ws, (dtype, rows, cols, k, aligned, ws, plan_ws)
