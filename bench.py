@@ -534,18 +534,20 @@ def run_sections(torch, capi, only, stream, steps, warmup, keep):
         ets = {}
         for (rows, cols, k, dt) in ((65536, 256, 8, "f32"), (16384, 1024, 32, "f32"), (4096, 2048, 1000, "f32"),
                                     (256, 151936, 256, "f32"), (16384, 1024, 32, "i32"), (1024, 32768, 64, "i32"),
-                                    (16384, 1024, 32, "i8"), (256, 151936, 50, "i8")):
-            esz = {"f32": 4, "i32": 4, "i8": 1}[dt]
+                                    (16384, 1024, 32, "i8"), (256, 151936, 50, "i8"), (256, 151936, 50, "f64")):
+            esz = {"f32": 4, "i32": 4, "i8": 1, "f64": 8}[dt]
             nb = max(3, (768 << 20) // (rows * cols * esz))
             bs = [gen(torch, (rows, cols), "uniform", 7000 + i, dev) for i in range(nb)]
             if dt == "i32":
                 bs = [(b * 2.0 ** 31).clamp(-2.0 ** 31, 2.0 ** 31 - 1).to(torch.int32) for b in bs]
             elif dt == "i8":
                 bs = [(b * 127.0).round().to(torch.int8) for b in bs]
+            elif dt == "f64":
+                bs = [b.double() for b in bs]
             cs = [topk_call(torch, capi, b, k, stream) for b in bs]
             r = timed(torch, cs, max(steps, 12), warmup, rows * cols * esz + cs[0].out_bytes)
             r["rows_per_s"] = round(rows / (r["ms"] * 1e-3), 1)
-            ets[f"topk{k}_{rows}x{cols}" + ("" if dt == "f32" else "_" + ("int32" if dt == "i32" else "int8"))] = r
+            ets[f"topk{k}_{rows}x{cols}" + ("" if dt == "f32" else "_" + {"i32": "int32", "i8": "int8", "f64": "float64"}[dt])] = r
             del bs, cs
         extras["topk_short_rows"] = ets
     return extras

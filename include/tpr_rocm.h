@@ -182,7 +182,8 @@ int tpr_topk(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t 
  * test hook with no reference counterpart): out[0] = kernel family (1 lane-group
  * kernel on 1- / 2-byte elements, 2 register radix select, 3 register radix
  * select per segment + merge, 4 streaming radix select, 5 lane-group kernel,
- * 6 wave kernel, 7 workgroup kernel; 6 and 7 add the merge when out[1] > 1),
+ * 6 wave kernel, 7 workgroup kernel; 6 and 7 add the merge when out[1] > 1; 8 wave kernel on
+ * 8-byte rows, then the streaming radix select for the rows it flags),
  * out[1] = segments per row, out[2] = segment length (segment s covers
  * [s * out[2], min(cols, (s + 1) * out[2]))), out[3] = waves per wave-kernel
  * workgroup, out[4] = workspace bytes.  `aligned`: the input and every row

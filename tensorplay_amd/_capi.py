@@ -167,7 +167,7 @@ def debug_set(key, value):
     _check(L.tpr_debug_set(key.encode(), int(value)))
 
 
-TOPK_KINDS = {1: "short_small", 2: "rsel", 3: "rsel_seg", 4: "radix", 5: "short", 6: "wave", 7: "block"}
+TOPK_KINDS = {1: "short_small", 2: "rsel", 3: "rsel_seg", 4: "radix", 5: "short", 6: "wave", 7: "block", 8: "wave8"}
 
 
 def topk_plan(dtype, rows, cols, k, row_stride=None, aligned=True):

@@ -130,6 +130,36 @@ __device__ __forceinline__ uint32_t elem_key(float f, int largest, int ikind) {
     return ikind ? i2key_sel(f, ikind == 1 ? 0x80000000u : 0u, lm) : f2key_sel(f, lm);
 }
 
+// Ascending sortable key of an element of any dtype, as an unsigned integer of
+// the element's width (32 bits for elements of at most 4 bytes): floats as
+// f2key (-0.0 == +0.0, every NaN above +inf), signed integers with the sign
+// bit flipped, unsigned integers and bool as they are; inverted for
+// largest = 0.
+template <class T>
+struct SortKey {
+    using K = typename std::conditional<(sizeof(T) > 4), unsigned long long, uint32_t>::type;
+    static constexpr int kBits = 8 * (int)sizeof(T);
+    __device__ static K of(T x, int largest) {
+        K k;
+        if constexpr (std::is_same<T, float>::value) {
+            return f2key(x, largest);
+        } else if constexpr (std::is_same<T, double>::value) {
+            const unsigned long long b = (unsigned long long)__double_as_longlong(x);
+            const unsigned long long u =
+                ((b & 0x7fffffffffffffffull) > 0x7ff0000000000000ull) ? 0x7ff8000000000000ull : b;
+            const unsigned long long m = (unsigned long long)((long long)u >> 63);
+            k = (u ^ (m | 0x8000000000000000ull)) - m;
+        } else if constexpr (std::is_signed<T>::value) {
+            using U = typename std::make_unsigned<T>::type;
+            k = (K)(U)((U)x ^ (U)((U)1 << (kBits - 1)));
+        } else {
+            k = (K)x;
+        }
+        if (!largest) k = ~k & (kBits == 64 ? ~(K)0 : (K)(((unsigned long long)1 << kBits) - 1));
+        return k;
+    }
+};
+
 // Bits of an integer element (ikind 1 signed, 2 unsigned / bool; em = the
 // element's mask) from its sortable key: the key is the element with the sign
 // bit flipped (signed) and complemented for largest = 0, so this is exact and
@@ -138,6 +168,14 @@ __device__ __forceinline__ uint32_t elem_key(float f, int largest, int ikind) {
 __device__ __forceinline__ uint32_t int_key_bits(uint32_t key, int ikind, int largest, uint32_t em) {
     const uint32_t sm = ikind == 1 ? (em >> 1) + 1u : 0u;
     return (key ^ (largest ? 0u : 0xffffffffu) ^ sm) & em;
+}
+
+// 64-bit sortable key of an 8-byte element given by its bits: float64 (ikind
+// 0), int64 (1) or uint64 (2), as SortKey.
+__device__ __forceinline__ unsigned long long key64_of(unsigned long long bits, int largest, int ikind) {
+    if (ikind == 0) return SortKey<double>::of(__longlong_as_double((long long)bits), largest);
+    if (ikind == 1) return SortKey<long long>::of((long long)bits, largest);
+    return SortKey<unsigned long long>::of(bits, largest);
 }
 
 __device__ __forceinline__ unsigned long long comp_key(uint32_t key, uint32_t idx) {
@@ -171,6 +209,7 @@ struct TopkArgs {
     // per row from the sorted top k (see sample_from_sel)
     int sample;
     int dyn;  // wave kernel: slices after the first ones handed out by an LDS counter
+    int* flags;  // 8-byte rows in the wave kernel: per row, 1 = finish in k_topk_radix (else null)
     float temperature, top_p;
     const float* u;
     long long* ids;
@@ -289,8 +328,11 @@ __device__ __forceinline__ uint32_t wave_rth_of_lane_max(const uint32_t* key, in
 // Exact top-k of cand[0..m) into sel[0..k) (sorted).  m >= k.  Candidate i is
 // counted by `groups` threads, each over a slice of the list; partial counts
 // are summed in rank[i] with LDS atomics.
-template <int NT>
-__device__ void rank_select(const unsigned long long* cand, int* rank, unsigned long long* sel, int m, int k) {
+// W8: the composites carry the high half of 64-bit keys; lo[i] is the low
+// half of candidate i's key, which orders equal high halves before the index.
+template <int NT, bool W8 = false>
+__device__ void rank_select(const unsigned long long* cand, int* rank, unsigned long long* sel, int m, int k,
+                            const uint32_t* lo = nullptr) {
     const int tid = threadIdx.x;
     for (int i = tid; i < m; i += NT) rank[i] = 0;
     __syncthreads();
@@ -305,14 +347,25 @@ __device__ void rank_select(const unsigned long long* cand, int* rank, unsigned 
         const int j1 = min(m, j0 + slice);
         int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
         int j = j0;
-        for (; j + 4 <= j1; j += 4) {
-            const unsigned long long c0 = cand[j], c1 = cand[j + 1], c2 = cand[j + 2], c3 = cand[j + 3];
-            r0 += (c0 > ci) ? 1 : 0;
-            r1 += (c1 > ci) ? 1 : 0;
-            r2 += (c2 > ci) ? 1 : 0;
-            r3 += (c3 > ci) ? 1 : 0;
+        if constexpr (W8) {
+            // d ranks above c: larger high half, or equal high halves and a
+            // larger low half, or both equal and a lower index
+            const uint32_t chi = (uint32_t)(ci >> 32), clo = lo[i];
+            for (; j < j1; ++j) {
+                const unsigned long long d = cand[j];
+                const uint32_t dhi = (uint32_t)(d >> 32), dlo = lo[j];
+                r0 += (dhi > chi || (dhi == chi && (dlo > clo || (dlo == clo && d > ci)))) ? 1 : 0;
+            }
+        } else {
+            for (; j + 4 <= j1; j += 4) {
+                const unsigned long long c0 = cand[j], c1 = cand[j + 1], c2 = cand[j + 2], c3 = cand[j + 3];
+                r0 += (c0 > ci) ? 1 : 0;
+                r1 += (c1 > ci) ? 1 : 0;
+                r2 += (c2 > ci) ? 1 : 0;
+                r3 += (c3 > ci) ? 1 : 0;
+            }
+            for (; j < j1; ++j) r0 += (cand[j] > ci) ? 1 : 0;
         }
-        for (; j < j1; ++j) r0 += (cand[j] > ci) ? 1 : 0;
         const int r = r0 + r1 + r2 + r3;
         if (groups == 1) rank[i] = r;
         else if (r) atomicAdd(&rank[i], r);
@@ -566,7 +619,10 @@ __device__ __forceinline__ void write_segment(const TopkArgs& a, long long row, 
         for (int i = threadIdx.x; i < k; i += blockDim.x) {
             const uint32_t idx = comp_index(sel[i]);
             const uint32_t key = (uint32_t)(sel[i] >> 32);
-            if constexpr (EB == 1) {
+            if constexpr (EB == 8) {  // the element itself (the composite carries half its key)
+                reinterpret_cast<unsigned long long*>(a.out_v)[row * k + i] =
+                    reinterpret_cast<const unsigned long long*>(p)[idx];
+            } else if constexpr (EB == 1) {
                 reinterpret_cast<uint8_t*>(a.out_v)[row * k + i] = (uint8_t)int_key_bits(key, a.ikind, a.largest, 0xffu);
             } else if constexpr (EB == 2) {
                 reinterpret_cast<uint16_t*>(a.out_v)[row * k + i] =
@@ -685,6 +741,20 @@ __device__ __forceinline__ void slice_keys_eb(const float4 (&cur)[SV], int base,
                                               uint32_t (&key)[16 * SV / EB]) {
     if constexpr (EB == 4) {
         slice_keys(cur, base, hi, largest, ikind, key);
+    } else if constexpr (EB == 8) {
+        // the high 32 bits of each element's 64-bit key (two elements per vector)
+        const int lim = hi - base;
+        const int lane = __lane_id();
+#pragma unroll
+        for (int j = 0; j < SV; ++j) {
+            const unsigned long long b0 =
+                ((unsigned long long)__float_as_uint(cur[j].y) << 32) | __float_as_uint(cur[j].x);
+            const unsigned long long b1 =
+                ((unsigned long long)__float_as_uint(cur[j].w) << 32) | __float_as_uint(cur[j].z);
+            const int e = (j * 64 + lane) * 2;
+            key[2 * j] = e < lim ? (uint32_t)(key64_of(b0, largest, ikind) >> 32) : 0u;
+            key[2 * j + 1] = e + 1 < lim ? (uint32_t)(key64_of(b1, largest, ikind) >> 32) : 0u;
+        }
     } else {
         constexpr int EPV = 16 / EB, EPW = 4 / EB;
         constexpr uint32_t em = EB == 1 ? 0xffu : 0xffffu;
@@ -711,7 +781,8 @@ __device__ __forceinline__ void slice_keys_eb(const float4 (&cur)[SV], int base,
 
 template <bool VEC, int SV, int OCC, int PD, int NW, int KWB = kWB, int EB = 4>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8))) void k_topk_wave(TopkArgs a) {
-    static_assert(EB == 4 || (SV == EB && VEC), "1- / 2-byte rows: SV = EB float4 per lane, 16-byte aligned");
+    static_assert(EB == 4 || (EB == 8 && SV == 4 && VEC) || (SV == EB && VEC),
+                  "1- / 2-byte rows: SV = EB float4 per lane; 8-byte rows: SV = 4; both 16-byte aligned");
     constexpr int kSlF = 256 * SV;         // 4-byte words per wave slice
     constexpr int kSl = kSlF * 4 / EB;     // elements per wave slice (1024)
     constexpr int kNK = 16 * SV / EB;      // keys per lane per slice (16)
@@ -915,8 +986,14 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
     // fewer than k gathered: the segment has keys of 0 (integers only; the
     // filter keeps keys >= 1), which the exact select takes
     if (any_over || m < k) {
-        exact_select<kT, EB>(bs, cand, pr, lo, hi, k, largest, a.ikind);
-        m = k;
+        if constexpr (EB == 8) {
+            // no 64-bit exact path here: the row is finished by k_topk_radix
+            if (threadIdx.x == 0) a.flags[row] = 1;
+            return;
+        } else {
+            exact_select<kT, EB>(bs, cand, pr, lo, hi, k, largest, a.ikind);
+            m = k;
+        }
     } else if (m > max(2 * k, 256)) {
         block_compact<kT>(bs, cand, other, m, k, Tf);
         m = bs.count2;
@@ -926,7 +1003,24 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
     }
     int* rank = reinterpret_cast<int*>(other);
     unsigned long long* sel = other + kB / 2;
-    rank_select<kT>(cand, rank, sel, m, k);
+    if constexpr (EB == 8) {
+        // The candidates hold every element whose key's high half reaches Tf, a
+        // superset of the top k; ties of the high half are ordered by the low
+        // half, read back for each candidate (rank and low halves fit below sel
+        // while m <= kB / 2, else k_topk_radix finishes the row).
+        if (m > kB / 2) {
+            if (threadIdx.x == 0) a.flags[row] = 1;
+            return;
+        }
+        uint32_t* lo32 = reinterpret_cast<uint32_t*>(rank + m);
+        const unsigned long long* p8 = reinterpret_cast<const unsigned long long*>(pr);
+        for (int i = threadIdx.x; i < m; i += kT)
+            lo32[i] = (uint32_t)key64_of(p8[comp_index(cand[i])], largest, a.ikind);
+        rank_select<kT, true>(cand, rank, sel, m, k, lo32);
+        if (threadIdx.x == 0) a.flags[row] = 0;
+    } else {
+        rank_select<kT>(cand, rank, sel, m, k);
+    }
     write_segment<EB>(a, row, seg, p, sel, k);
 }
 
@@ -1579,35 +1673,6 @@ __host__ __device__ inline int pow2_at_least(int v) {
 }
 
 
-// Ascending sortable key of an element of any dtype, as an unsigned integer of
-// the element's width (32 bits for elements of at most 4 bytes): floats as
-// f2key (-0.0 == +0.0, every NaN above +inf), signed integers with the sign
-// bit flipped, unsigned integers and bool as they are; inverted for
-// largest = 0.
-template <class T>
-struct SortKey {
-    using K = typename std::conditional<(sizeof(T) > 4), unsigned long long, uint32_t>::type;
-    static constexpr int kBits = 8 * (int)sizeof(T);
-    __device__ static K of(T x, int largest) {
-        K k;
-        if constexpr (std::is_same<T, float>::value) {
-            return f2key(x, largest);
-        } else if constexpr (std::is_same<T, double>::value) {
-            const unsigned long long b = (unsigned long long)__double_as_longlong(x);
-            const unsigned long long u =
-                ((b & 0x7fffffffffffffffull) > 0x7ff0000000000000ull) ? 0x7ff8000000000000ull : b;
-            const unsigned long long m = (unsigned long long)((long long)u >> 63);
-            k = (u ^ (m | 0x8000000000000000ull)) - m;
-        } else if constexpr (std::is_signed<T>::value) {
-            using U = typename std::make_unsigned<T>::type;
-            k = (K)(U)((U)x ^ (U)((U)1 << (kBits - 1)));
-        } else {
-            k = (K)x;
-        }
-        if (!largest) k = ~k & (kBits == 64 ? ~(K)0 : (K)(((unsigned long long)1 << kBits) - 1));
-        return k;
-    }
-};
 
 // Composite (key, index) ordered by key, then by lowest index; never 0 for an
 // element (0 pads the bitonic sort).
@@ -1778,6 +1843,7 @@ __global__ __launch_bounds__(NT) void k_topk_radix(TopkArgs a, void* gcand) {
     using C = typename Comp<typename SortKey<T>::K>::C;
     __shared__ RadixShared<T> sh;
     const long long row = blockIdx.x;
+    if (a.flags && a.flags[row] == 0) return;  // finished by the wave kernel
     const T* p = reinterpret_cast<const T*>(a.in) + row * a.row_stride;
     const int k = a.k;
     const int n2 = pow2_at_least(k);
@@ -2411,6 +2477,7 @@ enum TopkKind {
     TK_SHORT = 5,        // k_topk_short on 4-byte elements
     TK_WAVE = 6,         // k_topk_wave (then k_topk_merge when nseg > 1)
     TK_BLOCK = 7,        // k_topk_block (then k_topk_merge when nseg > 1)
+    TK_WAVE8 = 8,        // k_topk_wave on 8-byte rows, then k_topk_radix for the rows it flags
 };
 struct TopkRoute {
     int kind;
@@ -2443,6 +2510,15 @@ TopkRoute route_topk(long long rows, long long cols, long long k, int32_t dtype,
         !(short_ok && short_on)) {
         const TopkPlan pl = plan_topk(rows, cols, k);
         if (pl.wave) return TopkRoute{TK_WAVE, pl.nseg, pl.seg_len, pl.nw, pl.ws};
+    }
+    // 8-byte rows (float64, int64, uint64), 16-byte aligned, k <= 128, where the
+    // wave kernel takes a float32 row of the same shape in one segment: the
+    // filter on the high halves of the keys, the ranking with the low halves;
+    // rows it cannot finish (overflowing lists, keys of 0, too many candidates)
+    // are flagged in the workspace and finished by the streaming radix select.
+    if (eb == 8 && aligned && k <= kWaveSmallK && knobs().topk_radix <= 0 && !radix_route(rows, cols, k, TPR_FLOAT32)) {
+        const TopkPlan pl = plan_topk(rows, cols, k);
+        if (pl.wave && pl.nseg == 1) return TopkRoute{TK_WAVE8, 1, (int)cols, pl.nw, (size_t)rows * sizeof(int)};
     }
     if (radix && rsel_route(cols, dtype)) return TopkRoute{TK_RSEL, 1, (int)cols, 0, 0};
     if (const int ns = radix ? rsel_segments(cols, k, dtype) : 0) {
@@ -2614,8 +2690,9 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     a.row_stride = row_stride;
     a.k = (int)k;
     a.largest = largest ? 1 : 0;
-    a.ikind = (dtype == TPR_INT32 || dtype == TPR_INT16 || dtype == TPR_INT8) ? 1
-              : (dtype == TPR_UINT32 || dtype == TPR_UINT16 || dtype == TPR_UINT8 || dtype == TPR_BOOL) ? 2 : 0;
+    a.ikind = (dtype == TPR_INT64 || dtype == TPR_INT32 || dtype == TPR_INT16 || dtype == TPR_INT8) ? 1
+              : (dtype == TPR_UINT64 || dtype == TPR_UINT32 || dtype == TPR_UINT16 || dtype == TPR_UINT8 ||
+                 dtype == TPR_BOOL) ? 2 : 0;
     a.force_fallback = knobs().topk_fallback ? 1 : 0;
     a.nseg = rt.nseg;
     a.seg_len = rt.seg_len;
@@ -2624,6 +2701,7 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
     a.out_i = static_cast<long long*>(out_indices);
     a.sample = smp ? 1 : 0;
     a.dyn = knobs().topk_dyn >= 0 ? 1 : 0;
+    a.flags = nullptr;
     a.temperature = smp ? smp->temperature : 0.0f;
     a.top_p = smp ? smp->top_p : 1.0f;
     a.u = smp ? smp->u : nullptr;
@@ -2638,7 +2716,7 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
         hipLaunchKernelGGL(k_topk_merge, dim3((unsigned)rows), dim3(kMergeT), 0, st, a, (int)dtype);
         return check_launch("k_topk_merge");
     }
-    if (rt.kind == TK_RADIX) {
+    auto launch_radix = [&]() {
         // few rows: 1024 threads per row (the passes over the row are latency bound)
         const int nt = rows < 2LL * device_info().cus ? 1024 : kRadixT;
 #define TPR_RADIX(T)                                                                                  \
@@ -2660,6 +2738,18 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
         }
 #undef TPR_RADIX
         return check_launch("k_topk_radix");
+    };
+    if (rt.kind == TK_RADIX) return launch_radix();
+    if (rt.kind == TK_WAVE8) {
+        a.flags = static_cast<int*>(workspace);
+        const dim3 blk(rt.nw * 64);
+        const dim3 grid((unsigned)rows);
+        if (rt.nw == 16) hipLaunchKernelGGL((k_topk_wave<true, 4, 4, 1, 16, kWB, 8>), grid, blk, 0, st, a);
+        else if (rt.nw == 4) hipLaunchKernelGGL((k_topk_wave<true, 4, 8, 0, 4, kWB, 8>), grid, blk, 0, st, a);
+        else hipLaunchKernelGGL((k_topk_wave<true, 4, 8, 0, 8, kWB, 8>), grid, blk, 0, st, a);
+        const int rc = check_launch("k_topk_wave");
+        if (rc != TPR_OK) return rc;
+        return launch_radix();  // runs only the flagged rows
     }
     if (rt.kind == TK_SHORT) return launch_short(a, vec, st);
     const TopkPlan pl{rt.nseg, rt.seg_len, rt.kind == TK_WAVE, rt.nw, rt.ws};

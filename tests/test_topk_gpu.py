@@ -600,3 +600,47 @@ def test_small_integer_long_rows_wave_kernel(dt, fallback):
                 np.testing.assert_array_equal(gv.cpu().numpy().view(np.uint8), ev.view(np.uint8))
         del t
     assert esz in (1, 2)
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.int64, np.uint64])
+@pytest.mark.parametrize("fallback", [0, 1])
+def test_eight_byte_rows_wave_kernel(dt, fallback):
+    """8-byte rows (16-byte aligned, k <= 128) through the wave kernel: the
+    filter on the high 32 bits of each 64-bit key, the ranking with the low
+    halves read back; rows it cannot finish are flagged and finished by the
+    streaming radix select (forced for every row by fallback=1; taken
+    naturally by int64 rows of small values, whose high halves all tie).
+    Values and indices bit-exact against the oracle, NaN / +-0 / inf and
+    high-half ties included."""
+    _capi.debug_set("topk_fallback", fallback)
+    rng = np.random.default_rng(98 + fallback)
+    for rows, cols, ks in [(256, 151936, (50,)), (1024, 16384, (64, 1)), (2048, 12288, (100,)), (300, 40000, (128,))]:
+        if dt == np.float64:
+            x = rng.standard_normal((rows, cols)) * 3
+            x[0, ::7] = np.nan
+            x[1, ::5] = -0.0
+            x[1, 1::5] = 0.0
+            x[2, :100] = np.inf
+            # equal high halves, different low halves (ties of the filter key)
+            x[3] = 1.0 + rng.integers(0, 1 << 20, size=cols) * 2.0 ** -52
+        elif dt == np.int64:
+            x = rng.integers(-(1 << 62), 1 << 62, size=(rows, cols), dtype=np.int64)
+            x[0] = rng.integers(-50, 50, size=cols)           # all high halves equal: flagged rows
+            x[1, ::3] = np.iinfo(np.int64).min
+        else:
+            x = rng.integers(0, np.iinfo(np.uint64).max, size=(rows, cols), dtype=np.uint64, endpoint=True)
+            x[0] = rng.integers(0, 1000, size=cols).astype(np.uint64)
+            x[1, ::4] = np.iinfo(np.uint64).max
+        t = torch.from_numpy(x).cuda()
+        for k in ks:
+            kind = _capi.topk_plan(_capi._torch_dtypes()[t.dtype], rows, cols, k)[0]
+            assert kind == "wave8", (dt, rows, cols, k, kind)
+            for largest in (True, False):
+                print(f"case topk-wave8 dtype={np.dtype(dt).name} shape={x.shape} k={k} largest={largest} "
+                      f"fallback={fallback}", flush=True)
+                gv, gi = _capi.topk(t, k, largest)
+                torch.cuda.synchronize()
+                ev, ei = O.topk_any(x, k, largest)
+                np.testing.assert_array_equal(gi.cpu().numpy(), ei)
+                np.testing.assert_array_equal(gv.cpu().numpy().view(np.uint8), ev.view(np.uint8))
+        del t

@@ -38,6 +38,8 @@ def _check(dtype, rows, cols, k):
             assert (seg_len * esize) % 16 == 0  # segment starts stay 16-byte aligned
     else:
         assert nseg == 1
+    if kind == "wave8":  # per-row flags in the workspace, one segment
+        assert nseg == 1 and ws >= rows * 4 and esize == 8
     if kind == "wave":
         last = cols - (nseg - 1) * seg_len
         assert min(seg_len, last) >= nw * SLICE, ("wave without a full first slice", rows, cols, k, nw)
