@@ -994,7 +994,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
             exact_select<kT, EB>(bs, cand, pr, lo, hi, k, largest, a.ikind);
             m = k;
         }
-    } else if (m > max(2 * k, 256)) {
+    } else if (m > (k >= 128 ? k + max(k / 4, 32) : max(2 * k, 256))) {
+        // (large k: cut close to k before the O(m^2) ranking; MI355X, us:
+        // [256, 151936] k = 256 40.9 -> 37.4, [1024, 32768] k = 200 53.9 -> 47.9,
+        // [4096, 8192] k = 128 55.4 -> 54.6; at k = 64 the cut cost more than it
+        // saved, C3 29.5 -> 30.7)
         block_compact<kT>(bs, cand, other, m, k, Tf);
         m = bs.count2;
         unsigned long long* t = cand;
