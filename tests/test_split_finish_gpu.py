@@ -112,3 +112,34 @@ def test_two_streams_at_once():
     torch.cuda.synchronize()
     for j in range(2):
         assert all(int(r) == ref[j] for r in res[j])
+
+
+def test_graph_capture_takes_the_finalize_launch():
+    """Under HIP graph capture a split reduction takes the separate finalize
+    launch (a captured launch may replay on another stream, so it does not use
+    the capturing stream's ticket counters).  The graph is replayed several
+    times with eager work between the replays; every replay must equal the
+    eager result."""
+    x = torch.randn(1 << 22, device="cuda")
+    eager = {op: _capi.reduce(x, op, None).clone() for op in ("sum", "argmax", "var")}
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        _capi.reduce(x, "sum", None)  # warm the allocator on the capture stream
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            outs = {op: _capi.reduce(x, op, None) for op in ("sum", "argmax", "var")}
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(4):
+        for o in outs.values():
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for op in outs:
+            assert torch.equal(outs[op], eager[op]), (rep, op, outs[op], eager[op])
+        # eager split reductions between the replays (they use the ticket counters)
+        y = _capi.reduce(x, "sum", None)
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager["sum"])
