@@ -1210,6 +1210,20 @@ constexpr int kShortMaxK = 64;
 // rows per CU.  topk_short = 1 (debug knob) takes every row below 4096.
 __host__ inline bool short_exact(long long rows, long long cols, long long k);
 
+// Float max / min of three without the canonicalising moves the compiler adds
+// to fmaxf / fminf in IEEE mode: v_max3_f32 / v_min3_f32 return the largest /
+// smallest non-NaN operand (NaN only when all three are NaN).
+__device__ __forceinline__ float max3_f32(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float min3_f32(float a, float b, float c) {
+    float r;
+    asm("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 template <int L>
 __device__ __forceinline__ int group_sum(int v) {
 #pragma unroll
@@ -1217,25 +1231,64 @@ __device__ __forceinline__ int group_sum(int v) {
     return v;
 }
 
-// Inclusive prefix sum over the lanes of an L-lane group (sl = lane in group).
+// Inclusive prefix sum over the lanes of an L-lane group (L = 16, 32 or 64;
+// sl = lane in group): DPP row shifts by 1, 2, 4, 8 inside each 16-lane row
+// (lanes whose source is outside the row add the 0 passed as `old`), then
+// row_bcast:15 carries row 0's total into row 1 and row 2's into row 3, and
+// row_bcast:31 the total of rows 0-1 into rows 2-3.  No LDS round trips.
 template <int L>
 __device__ __forceinline__ int group_scan(int v, int sl) {
-#pragma unroll
-    for (int o = 1; o < L; o <<= 1) {
-        const int t = __shfl_up(v, o, 64);
-        if (sl >= o) v += t;
-    }
+    static_assert(L == 16 || L == 32 || L == 64, "lane groups of 16, 32 or 64");
+    (void)sl;
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+    if constexpr (L >= 32) v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    if constexpr (L == 64) v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
     return v;
 }
 
-// Lane lane ^ M's value: DPP quad permutes for M = 1, 2, ds_swizzle (xor
-// mask inside 32-lane halves) for M = 4 .. 16, ds_bpermute for M = 32.
+// Lane lane ^ M's value, without LDS-pipe permutes: DPP quad permutes for
+// M = 1, 2; for M = 4 quad_perm [3,2,1,0] (xor 3) then row_half_mirror
+// (i -> 7 - i = i ^ 7 inside 8 lanes); row_ror:8 for M = 8 (rotating a
+// 16-lane row by 8 is xor 8); for M = 16 and 32 the gfx950 permlane swaps of
+// the value with itself (v_permlane16_swap: odd rows of the first operand
+// with even rows of the second; v_permlane32_swap: upper half of the first
+// with lower half of the second), each lane taking the copy that holds its
+// partner's value.  Every lane of the wave must be active.
 template <int M>
 __device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
-    if constexpr (M == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // [1,0,3,2]
-    else if constexpr (M == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // [2,3,0,1]
-    else if constexpr (M < 32) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (M << 10) | 0x1F);
-    else return (uint32_t)__builtin_amdgcn_ds_bpermute((int)((__lane_id() ^ M) << 2), (int)v);
+    if constexpr (M == 1) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    } else if constexpr (M == 2) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    } else if constexpr (M == 4) {
+        const int t = __builtin_amdgcn_mov_dpp((int)v, 0x1B, 0xF, 0xF, false);  // quad_perm [3,2,1,0]
+        return (uint32_t)__builtin_amdgcn_mov_dpp(t, 0x141, 0xF, 0xF, false);   // row_half_mirror
+    } else if constexpr (M == 8) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
+    } else if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (__lane_id() & 16) ? r[0] : r[1];
+    } else {
+        static_assert(M == 32, "lane distance 1 .. 32");
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (__lane_id() & 32) ? r[0] : r[1];
+    }
+}
+
+// Largest value over the lanes of an L-lane group (every lane of the group
+// active; groups are whole 16-lane rows, so the exchanges stay inside them).
+template <int L>
+__device__ __forceinline__ uint32_t group_max(uint32_t v) {
+    v = max(v, xor_lane<1>(v));
+    v = max(v, xor_lane<2>(v));
+    v = max(v, xor_lane<4>(v));
+    v = max(v, xor_lane<8>(v));
+    if constexpr (L >= 32) v = max(v, xor_lane<16>(v));
+    if constexpr (L == 64) v = max(v, xor_lane<32>(v));
+    return v;
 }
 
 template <int M, int P>
@@ -1297,13 +1350,38 @@ __device__ __forceinline__ uint32_t group_sort_asc(uint32_t m, int sl) {
     for (int size = 2; size <= L; size <<= 1) {
 #pragma unroll
         for (int stride = size / 2; stride > 0; stride >>= 1) {
-            const uint32_t o = __shfl_xor(v, stride, 64);
+            uint32_t o;
+            switch (stride) {
+                case 1: o = xor_lane<1>(v); break;
+                case 2: o = xor_lane<2>(v); break;
+                case 4: o = xor_lane<4>(v); break;
+                case 8: o = xor_lane<8>(v); break;
+                case 16: o = xor_lane<16>(v); break;
+                default: o = xor_lane<32>(v); break;
+            }
             const bool asc = (sl & size) == 0;
             const bool lower = (sl & stride) == 0;
             v = (lower == asc) ? min(v, o) : max(v, o);
         }
     }
     return v;
+}
+
+// The r-th largest (r >= 1) of the wave's 64 * NV values v[] (the multiset
+// over every lane): a 32-step bit search, one compare per value and a ballot
+// count per step (the prefix stays in scalar registers).
+template <int NV>
+__device__ __forceinline__ uint32_t wave_rth_largest(const uint32_t (&v)[NV], int r) {
+    uint32_t pre = 0;
+#pragma unroll 4
+    for (int b = 31; b >= 0; --b) {
+        const uint32_t cand = pre | (1u << b);
+        int cnt = 0;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) cnt += __popcll(__ballot(v[i] >= cand));
+        if (cnt >= r) pre = cand;
+    }
+    return pre;
 }
 
 __device__ __forceinline__ void wave_sync_lds() {
@@ -1428,6 +1506,37 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
     }
     uint32_t key[E];
     constexpr uint32_t lm = LG ? 0u : 0xffffffffu;
+    // Full float32 rows filter on the floats themselves: the bound T (a key)
+    // becomes the float Tf it encodes, an element is a candidate when
+    // !(x < Tf) (largest: NaN, whose key is above every other, passes) or
+    // x <= Tf (smallest: NaN, below every other, fails), and keys are made
+    // only for the listed candidates.  The lane maxima come from float max3,
+    // which skips NaN: that can only lower the bound, which stays valid.
+    const bool ffast = EB == 4 && a.ikind == 0 && cols == 4 * E4 * L;
+    auto float_keys = [&]() {
+#pragma unroll
+        for (int j = 0; j < E4; ++j) {
+            key[4 * j + 0] = live ? f2key_sel(x[j].x, lm) : 0u;
+            key[4 * j + 1] = live ? f2key_sel(x[j].y, lm) : 0u;
+            key[4 * j + 2] = live ? f2key_sel(x[j].z, lm) : 0u;
+            key[4 * j + 3] = live ? f2key_sel(x[j].w, lm) : 0u;
+        }
+    };
+    uint32_t mx = 0;  // the lane's largest key
+    if (ffast) {
+        float m = LG ? -__builtin_inff() : __builtin_inff();
+#pragma unroll
+        for (int j = 0; j < E4; ++j) {
+            if constexpr (LG) {
+                m = max3_f32(m, x[j].x, x[j].y);
+                m = max3_f32(m, x[j].z, x[j].w);
+            } else {
+                m = min3_f32(m, x[j].x, x[j].y);
+                m = min3_f32(m, x[j].z, x[j].w);
+            }
+        }
+        mx = live ? f2key_sel(m, lm) : 0u;
+    } else {
     if constexpr (EB < 4) {  // 1- and 2-byte integers (ikind 1 signed, 2 unsigned or bool)
         constexpr uint32_t em = EB == 1 ? 0xffu : 0xffffu;
         const uint32_t sm = a.ikind == 1 ? (em >> 1) + 1u : 0u;
@@ -1477,35 +1586,52 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
 #pragma unroll
         for (int q = 0; q < E; ++q) key[q] = 0u;
     }
-
-    uint32_t mx = 0, mx2 = 0;  // the lane's largest and second largest key
 #pragma unroll
-    for (int q = 0; q < E; ++q) {
-        mx2 = max(mx2, min(mx, key[q]));
-        mx = max(mx, key[q]);
+    for (int q = 0; q < E; ++q) mx = max(mx, key[q]);
     }
-    const uint32_t srt = group_sort_asc<L>(mx, sl);
     // The bound: the k-th largest lane max (valid keys are >= 1); for k of
-    // 57..128 (64-lane rows) the k-th largest of the lanes' two largest keys,
-    // 128 distinct elements sorted two per lane (tighter near k = 64: MI355X
-    // [16384, 3000] k = 64 124 -> 90 us, [16384, 2048] 50 -> 39; looser costs
-    // more than the sort below that: k = 40..50 3-12% slower).
-    uint32_t T;
-    if (L == 64 && k > 56) {
-        unsigned long long x2[2] = {mx, mx2};
-        wave_sort_desc<2>(x2);
-        const int r = k - 1;
-        const uint32_t t0 = (uint32_t)__shfl((int)(uint32_t)x2[0], r >> 1, 64);
-        const uint32_t t1 = (uint32_t)__shfl((int)(uint32_t)x2[1], r >> 1, 64);
-        T = max((r & 1) ? t1 : t0, 1u);
+    // 57..128 (64-lane rows) the k-th largest of the lanes' two largest keys
+    // (tighter near k = 64: MI355X [16384, 3000] k = 64 124 -> 90 us,
+    // [16384, 2048] 50 -> 39; looser costs more than that below: k = 40..50
+    // 3-12% slower).  One row per wave: a bit search with ballots; lane groups
+    // of several rows: a bitonic sort of the group's lane maxima.
+    uint32_t T, gmax = 0;
+    if constexpr (L == 64) {
+        if (k > 56) {
+            if (ffast) float_keys();
+            uint32_t mx2 = 0;  // the lane's second largest key
+#pragma unroll
+            for (int q = 0; q < E; ++q) mx2 = max(mx2, min(mx, key[q]));
+            const uint32_t v2[2] = {mx, mx2};
+            T = max(wave_rth_largest<2>(v2, k), 1u);
+        } else {
+            const uint32_t v1[1] = {mx};
+            T = max(wave_rth_largest<1>(v1, min(k, L)), 1u);
+        }
     } else {
+        const uint32_t srt = group_sort_asc<L>(mx, sl);
         T = max(__shfl(srt, grp * L + (L - min(k, L)), 64), 1u);
+        gmax = __shfl(srt, grp * L + L - 1, 64);
     }
     const bool bound_ok = k <= (L == 64 ? 2 * L : L);
-    const uint32_t gmax = __shfl(srt, grp * L + L - 1, 64);
+    const bool fkeys = ffast && !(L == 64 && k > 56);  // filter on the floats
+    const float Tf = __uint_as_float(key2bits(T, largest));
+    auto xval = [&](int q) -> float {
+        const float4& v = x[q >> 2];
+        return (q & 3) == 0 ? v.x : (q & 3) == 1 ? v.y : (q & 3) == 2 ? v.z : v.w;
+    };
+    auto fcand = [&](int q) -> bool {
+        const float f = xval(q);
+        return LG ? !(f < Tf) : (f <= Tf);
+    };
     int n = 0;
+    if (fkeys) {
 #pragma unroll
-    for (int q = 0; q < E; ++q) n += (key[q] >= T) ? 1 : 0;
+        for (int q = 0; q < E; ++q) n += fcand(q) ? 1 : 0;
+    } else {
+#pragma unroll
+        for (int q = 0; q < E; ++q) n += (key[q] >= T) ? 1 : 0;
+    }
     const int incl = group_scan<L>(n, sl);
     int c = bound_ok ? __shfl(incl, grp * L + L - 1, 64) : C + 1;  // candidates of this row
     // Fewer than k candidates: the row has keys of 0 (integers only; the
@@ -1514,9 +1640,24 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
     unsigned long long* list = cl[slot];
     if (c <= C) {
         int pos = incl - n;
+        if (fkeys) {
+            // the floats' bits in the keys' place, then the keys in place
 #pragma unroll
-        for (int q = 0; q < E; ++q) {
-            if (key[q] >= T) list[pos++] = comp_key(key[q], (uint32_t)short_elem<L, EB>(q, sl));
+            for (int q = 0; q < E; ++q) {
+                if (fcand(q))
+                    list[pos++] = comp_key(__float_as_uint(xval(q)), (uint32_t)short_elem<L, EB>(q, sl));
+            }
+            wave_sync_lds();
+            for (int i = sl; i < c; i += L) {
+                const unsigned long long e = list[i];
+                list[i] = ((unsigned long long)f2key_sel(__uint_as_float((uint32_t)(e >> 32)), lm) << 32) |
+                          (e & 0xffffffffull);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < E; ++q) {
+                if (key[q] >= T) list[pos++] = comp_key(key[q], (uint32_t)short_elem<L, EB>(q, sl));
+            }
         }
         if (c * c > 256 * L && c > 2 * k) {
             // Raise the bound with a 256-bin histogram of the candidates over
@@ -1539,6 +1680,14 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
             wave_sync_lds();  // every lane has its candidates before the area is cleared
 #pragma unroll
             for (int b = 0; b < 256 / L; ++b) hist[sl * (256 / L) + b] = 0u;
+            if (fkeys) {  // the row's largest key from its candidates (NaN included)
+                uint32_t lmx = 0;
+#pragma unroll
+                for (int r = 0; r < PER; ++r) lmx = max(lmx, (uint32_t)(mine[r] >> 32));
+                gmax = group_max<L>(lmx);
+            } else if constexpr (L == 64) {
+                gmax = wave_max_u32(mx);
+            }
             const int shift = hist_shift(gmax, T);
             wave_sync_lds();
 #pragma unroll
@@ -1559,6 +1708,7 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
         }
     } else {
         // exact k-th key by bit search over every key of the row
+        if (fkeys) float_keys();
         uint32_t pre = 0;
         for (int b = 31; b >= 0; --b) {
             const uint32_t cand = pre | (1u << b);

@@ -204,6 +204,31 @@ def test_short_rows(short):
         check(s, s, k, False)
 
 
+def test_short_full_rows_special_values():
+    """Full float32 rows of the lane-group kernel (every lane's vectors inside
+    the row: 64 .. 4096 elements) filter on the floats themselves; NaN of
+    every kind (quiet, signalling, negative; whole rows of them), +-0,
+    denormals and +-inf must still select exactly as the key order does."""
+    rng = np.random.default_rng(31)
+    snan = np.array([0x7F800001, 0xFFC00000, 0x7FFFFFFF], np.uint32).view(np.float32)
+    tiny = np.float32(1e-45)
+    for rows, cols in [(70, 64), (130, 256), (40, 512), (33, 1024), (9, 2048), (8, 4096)]:
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        x[0, ::5] = np.nan
+        x[1, :] = np.nan
+        x[2, ::3] = snan[rng.integers(0, 3, len(x[2, ::3]))]
+        x[3, :] = -np.inf
+        x[3, 9] = tiny
+        x[4] = np.where(rng.random(cols) < 0.5, -0.0, 0.0)
+        x[5] = rng.choice(np.array([tiny, -tiny, 0.0, -0.0, 1e-39, -1e-39], np.float32), cols)
+        x[6, 1::2] = np.nan
+        x[7, :] = np.inf
+        for k in (1, 7, 32, 50, 64):
+            if k <= cols:
+                check(x, x, k, True)
+                check(x, x, k, False)
+
+
 def test_short_rows_many():
     # BASELINE-like volumes of short rows: every row and every output checked
     rng = np.random.default_rng(29)
