@@ -18,10 +18,12 @@
 //     stay in registers: read once and written once -- k_smx_rows;
 //   * rows of 16384..153600 floats, at least one per CU, stay on one CU in
 //     registers plus LDS and are also read once -- k_smx_res (forward),
-//     k_smx_res_bwd (log_softmax gradient: g held, y streamed once);
-//   * softmax gradients of rows of 16385..393216 floats are cut into pieces,
-//     one workgroup each holding its g and y, with the partial dots exchanged
-//     between the pieces -- k_smx_bwd_pieces (every input read once);
+//     k_smx_res_bwd (gradients of rows the piece kernel does not take: g
+//     held, y streamed);
+//   * softmax and log_softmax gradients of rows of 16385..393216 floats are
+//     cut into pieces, one workgroup each holding its g and y, with the
+//     partial sums (g . y, or sum g) exchanged between the pieces --
+//     k_smx_bwd_pieces (every input read once);
 //   * longer rows stream twice: an online (max, sum-of-exp) pass, then the
 //     output pass -- k_smx_rows2, or split over (row, chunk) workgroups when
 //     the rows are fewer than the CUs -- k_smx_part / k_smx_apply;
@@ -606,8 +608,9 @@ __global__ __launch_bounds__(kResT) void k_smx_res_bwd(SmxArgs p, int vl) {
 }
 
 // ---------------------------------------------------------------------------
-// Softmax gradient with g AND y held on chip: gx = (g - sum(g * y)) * y needs
-// the whole row's dot before any output, and a long row's g and y together
+// Gradients with g AND y held on chip: softmax gx = (g - sum(g * y)) * y and
+// log_softmax gx = g - exp(y) * sum(g) need the whole row's statistic (the
+// "dot" below: sum(g * y) or sum(g)) before any output, and a long row's g and y together
 // exceed one CU, so a row is cut into NS pieces of at most kPcVR * 512
 // float4 of each, one 512-thread workgroup per piece holding its g and y in
 // registers: every input crosses HBM once (k_smx_res_bwd streams y twice).
@@ -637,8 +640,9 @@ static __device__ unsigned long long smx_slots[tpr::kSmxSlots];
 namespace tpr {
 namespace {
 
-template <int NT, int PT, int kPcVR>
+template <int MODE, int NT, int PT, int kPcVR>
 __global__ __launch_bounds__(PT) void k_smx_bwd_pieces(SmxArgs p, int ns, int pv, unsigned epoch, int spin) {
+    static_assert(MODE == BWD || MODE == BWD_LOG, "gradients only");
     __shared__ float sh[PT / kWave];
     __shared__ float parts[kPcMax];
     __shared__ unsigned missing;
@@ -654,7 +658,11 @@ __global__ __launch_bounds__(PT) void k_smx_bwd_pieces(SmxArgs p, int ns, int pv
         const int len = max(0, min(q, v0 + pv) - v0);
         return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base + 4LL * v0), (short)0, len * 16, kBufWord3);
     };
-    auto vd = [](f32x4 x, f32x4 y) { return (x.x * y.x + x.y * y.y) + (x.z * y.z + x.w * y.w); };
+    // the row statistic's term of one vector pair: softmax g . y, log_softmax sum(g)
+    auto vd = [](f32x4 x, f32x4 y) {
+        if constexpr (MODE == BWD_LOG) return (x.x + x.y) + (x.z + x.w);
+        else return (x.x * y.x + x.y * y.y) + (x.z * y.z + x.w * y.w);
+    };
     const __amdgpu_buffer_rsrc_t bg = rsrc(ra, pc), by = rsrc(rb, pc);
     f32x4 g[kPcVR], y[kPcVR];
 #pragma unroll
@@ -699,9 +707,11 @@ __global__ __launch_bounds__(PT) void k_smx_bwd_pieces(SmxArgs p, int ns, int pv
         const __amdgpu_buffer_rsrc_t mg = rsrc(ra, i), my = rsrc(rb, i);
         float s2 = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kPcVR; ++j)
-            s2 += vd(__builtin_amdgcn_raw_buffer_load_b128(mg, (j * PT + t) * 16, 0, 0),
-                     __builtin_amdgcn_raw_buffer_load_b128(my, (j * PT + t) * 16, 0, 0));
+        for (int j = 0; j < kPcVR; ++j) {
+            const f32x4 gm = __builtin_amdgcn_raw_buffer_load_b128(mg, (j * PT + t) * 16, 0, 0);
+            if constexpr (MODE == BWD_LOG) s2 += vd(gm, gm);
+            else s2 += vd(gm, __builtin_amdgcn_raw_buffer_load_b128(my, (j * PT + t) * 16, 0, 0));
+        }
         s2 = grp<PT, false>(s2, sh);
         if (t == 0) parts[i] = s2;
         __syncthreads();
@@ -711,8 +721,8 @@ __global__ __launch_bounds__(PT) void k_smx_bwd_pieces(SmxArgs p, int ns, int pv
     const __amdgpu_buffer_rsrc_t bo = rsrc(p.out + row * p.n, pc);
 #pragma unroll
     for (int j = 0; j < kPcVR; ++j) {
-        const f32x4 r = {outv<BWD>(g[j].x, y[j].x, dot, 0.0f), outv<BWD>(g[j].y, y[j].y, dot, 0.0f),
-                         outv<BWD>(g[j].z, y[j].z, dot, 0.0f), outv<BWD>(g[j].w, y[j].w, dot, 0.0f)};
+        const f32x4 r = {outv<MODE>(g[j].x, y[j].x, dot, 0.0f), outv<MODE>(g[j].y, y[j].y, dot, 0.0f),
+                         outv<MODE>(g[j].z, y[j].z, dot, 0.0f), outv<MODE>(g[j].w, y[j].w, dot, 0.0f)};
         __builtin_amdgcn_raw_buffer_store_b128(r, bo, (j * PT + t) * 16, 0, aux);  // past the piece: dropped
     }
 }
@@ -1430,21 +1440,24 @@ int bwd_pieces(long long n, int vw, int pt, int vr) {
     return ns <= kPcMax ? (int)ns : 0;
 }
 
-template <int PT, int VR>
+// Per-launch tag of the partial slots, one counter for every instantiation of
+// the piece kernel: they share the slots, so a tag may never repeat across them.
+std::atomic<unsigned> smx_epoch_ctr{0};
+
+template <int MODE, int PT, int VR>
 int launch_bwd_pieces(const SmxArgs& a, int ns, hipStream_t st) {
     const long long grid = a.rows * ns;
     if (grid > 0x7fffffffLL) return fail(TPR_ERR_INVALID_ARG, "tpr_softmax: too many row pieces");
     const long long q = a.n / 4;
     const int pv = (int)((q + ns - 1) / ns);
     // per-launch tag of the partial-dot slots: never 0 (the slots' initial value)
-    static std::atomic<unsigned> epoch_ctr{0};
-    unsigned ep = epoch_ctr.fetch_add(1, std::memory_order_relaxed) + 1u;
-    if (ep == 0) ep = epoch_ctr.fetch_add(1, std::memory_order_relaxed) + 1u;
+    unsigned ep = smx_epoch_ctr.fetch_add(1, std::memory_order_relaxed) + 1u;
+    if (ep == 0) ep = smx_epoch_ctr.fetch_add(1, std::memory_order_relaxed) + 1u;
     // wait for the row's other pieces up to 40 us (100 MHz ticks); the test
     // knob smx_spin = -1 makes every piece recompute the others instead
     const int spin = knobs().smx_spin < 0 ? 0 : 4000;
-    if (a.nt) hipLaunchKernelGGL((k_smx_bwd_pieces<1, PT, VR>), dim3((unsigned)grid), dim3(PT), 0, st, a, ns, pv, ep, spin);
-    else hipLaunchKernelGGL((k_smx_bwd_pieces<0, PT, VR>), dim3((unsigned)grid), dim3(PT), 0, st, a, ns, pv, ep, spin);
+    if (a.nt) hipLaunchKernelGGL((k_smx_bwd_pieces<MODE, 1, PT, VR>), dim3((unsigned)grid), dim3(PT), 0, st, a, ns, pv, ep, spin);
+    else hipLaunchKernelGGL((k_smx_bwd_pieces<MODE, 0, PT, VR>), dim3((unsigned)grid), dim3(PT), 0, st, a, ns, pv, ep, spin);
     return check_launch("tpr_softmax (gradient, row pieces)");
 }
 
@@ -1452,13 +1465,13 @@ template <int MODE>
 int run_rows(const SmxArgs& a0, int vw, hipStream_t st) {
     SmxArgs a = a0;
     const int two_pass = knobs().smx_two_pass;
-    // softmax gradient: g and y both held (row pieces over workgroups), each read once
-    if constexpr (MODE == BWD) {
+    // gradients: g and y both held (row pieces over workgroups), each read once
+    if constexpr (MODE >= BWD) {
         // 512-thread pieces of 24 float4 per lane; measured on MI355X (us):
         // [256, 151936] 84.8 against 90.4 (256-thread pieces), 90.9 (12 float4
         // per lane, two workgroups per CU) and 96.0 (g held, y read twice);
         // [1024, 32768] 67.2 against 74.2 (g held)
-        if (const int ns = bwd_pieces(a.n, vw, 512, 24)) return launch_bwd_pieces<512, 24>(a, ns, st);
+        if (const int ns = bwd_pieces(a.n, vw, 512, 24)) return launch_bwd_pieces<MODE, 512, 24>(a, ns, st);
     }
     // rows of 16384..153600 floats, at least one per CU: one row per CU in
     // registers + LDS (forward: x held; gradients: g held, y streamed).

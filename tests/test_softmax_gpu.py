@@ -300,8 +300,8 @@ def test_backward_rows(log, plan):
 @pytest.mark.parametrize("res", [0, -1])
 @pytest.mark.parametrize("pieces", [0, -1])
 def test_backward_long_rows(log, res, pieces):
-    # softmax / log_softmax gradients over rows of 16384..153600: softmax by
-    # row pieces holding g and y (pieces=0), else g held in registers + LDS
+    # softmax / log_softmax gradients over rows of 16384..153600: by row
+    # pieces holding g and y (pieces=0), else g held in registers + LDS
     # while y streams (res=0; once for log_softmax, twice for softmax), or the
     # two-pass kernel (res=-1)
     _capi.debug_set("smx_split", -1)
@@ -311,9 +311,11 @@ def test_backward_long_rows(log, res, pieces):
         check_bwd((3, n), 1, log, 400 + i)
 
 
+@pytest.mark.parametrize("log", [False, True])
 @pytest.mark.parametrize("spin", [0, -1])
-def test_backward_row_pieces(spin):
-    """Softmax gradients by row pieces (g and y held, partial dots exchanged
+def test_backward_row_pieces(spin, log):
+    """Softmax / log_softmax gradients by row pieces (g and y held, partial
+    sums (g . y, or sum g) exchanged
     between the pieces' workgroups), with the exchange (spin=0) and with every
     piece recomputing the others' partials from memory (spin=-1, the path a
     piece takes when a partner is not resident in time): rows of 1..8 pieces,
@@ -321,7 +323,7 @@ def test_backward_row_pieces(spin):
     _capi.debug_set("smx_spin", spin)
     for i, (rows, n) in enumerate([(3, 49152), (2, 49156), (5, 98308), (3, 151936), (2, 200000), (2, 393216),
                                    (300, 20000)]):
-        check_bwd((rows, n), 1, False, 600 + i)
+        check_bwd((rows, n), 1, log, 600 + i)
 
 
 def test_backward_row_pieces_exchange_equals_recompute():
@@ -343,6 +345,14 @@ def test_backward_row_pieces_exchange_equals_recompute():
     ref = (g64 - (g64 * y64).sum(1, keepdims=True)) * y64
     tol = 1e-5 * (np.abs(g64) + np.abs(g64 * y64).sum(1, keepdims=True)) * np.abs(y64) + 1e-30
     assert np.all(np.abs(a[:8].double().cpu().numpy() - ref) <= tol)
+    # log_softmax gradient: the exchanged and recomputed sums of g agree too
+    yl = torch.log_softmax(torch.from_numpy((rng.standard_normal((256, 151936)) * 3).astype(np.float32)), -1).cuda()
+    a = _capi.softmax(g, -1, log=True, grad_of=yl)
+    _capi.debug_set("smx_spin", -1)
+    b = _capi.softmax(g, -1, log=True, grad_of=yl)
+    _capi.debug_set("smx_spin", 0)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
 
 
 @pytest.mark.parametrize("log", [False, True])
