@@ -340,9 +340,11 @@ int32_t tpr_abi_version(void);
  * composites per thread where the sort size allows; 0 = automatic),
  * "topk_waves" (4, 8 or 16 waves per wave-kernel workgroup, 0 = automatic),
  * "split_fin" (-1 = split reductions always take the separate finalize launch),
- * "smx_pieces" (-1 = softmax gradients never take the row-piece kernel),
- * "smx_spin" (-1 = row pieces never wait for each other's partial dots: every
- * piece recomputes them from memory),
+ * "smx_pieces" (-1 = softmax gradients never take the row-piece kernels, nor
+ * does the forward), "smx_fwd_pieces" (1 = the forward row-piece kernel for
+ * every row it can hold, -1 = never, 0 = automatic),
+ * "smx_spin" (-1 = row pieces never wait for each other's partial statistics:
+ * every piece recomputes them from memory),
  * "topk_short" (1 = the lane-group kernel for every row it can hold, -1 =
  * never), "topk_radix" (1 = the radix-select kernels for every k, 2 = the
  * streaming one, -1 = never where another kernel can), "topk_dyn" (-1 = static

@@ -33,7 +33,7 @@ DeviceInfo device_info();
 // values, so sweeps run single-threaded.
 #define TPR_KNOB_LIST(X) X(splits) X(lanes) X(general) X(topk_fallback) X(tx) X(topk_variant) X(topk_waves) \
     X(unroll) X(colblock) X(nt) X(smx_two_pass) X(smx_lanes) X(smx_split) X(smx_res) X(rowreg) X(topk_short) \
-    X(topk_radix) X(topk_dyn) X(split_fin) X(smx_pieces) X(smx_spin)
+    X(topk_radix) X(topk_dyn) X(split_fin) X(smx_pieces) X(smx_spin) X(smx_fwd_pieces)
 #ifdef TPR_DEBUG_KNOBS
 using Knob = std::atomic<int64_t>;
 struct DebugKnobs {

@@ -16,6 +16,9 @@
 // and three temporaries).  Here one kernel does it:
 //   * rows shorter than 16384 floats (or a few long rows, up to 32768)
 //     stay in registers: read once and written once -- k_smx_rows;
+//   * forward rows of 16385..327680 floats, more rows than CUs and two
+//     pieces or more per row, are cut into pieces held in registers by one
+//     workgroup each, (max, sum exp) exchanged -- k_smx_fwd_pieces;
 //   * rows of 16384..153600 floats, at least one per CU, stay on one CU in
 //     registers plus LDS and are also read once -- k_smx_res (forward),
 //     k_smx_res_bwd (gradients of rows the piece kernel does not take: g
@@ -630,6 +633,7 @@ __global__ __launch_bounds__(kResT) void k_smx_res_bwd(SmxArgs p, int vl) {
 // workgroup, so all pieces use the same value.
 // ---------------------------------------------------------------------------
 constexpr int kPcMax = 16;                     // most pieces per row
+constexpr int kFwdPcVR = 20;                   // forward pieces: float4 of x per lane
 constexpr int kSmxSlots = 1 << 16;             // exchange slots (rows * NS wrap around)
 
 }  // namespace
@@ -723,6 +727,173 @@ __global__ __launch_bounds__(PT) void k_smx_bwd_pieces(SmxArgs p, int ns, int pv
     for (int j = 0; j < kPcVR; ++j) {
         const f32x4 r = {outv<MODE>(g[j].x, y[j].x, dot, 0.0f), outv<MODE>(g[j].y, y[j].y, dot, 0.0f),
                          outv<MODE>(g[j].z, y[j].z, dot, 0.0f), outv<MODE>(g[j].w, y[j].w, dot, 0.0f)};
+        __builtin_amdgcn_raw_buffer_store_b128(r, bo, (j * PT + t) * 16, 0, aux);  // past the piece: dropped
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Forward softmax / log_softmax by row pieces: the same cut and exchange as
+// k_smx_bwd_pieces, each 512-thread workgroup holding its piece of x in
+// registers (kPcVR float4 per lane, few enough registers for two workgroups
+// per CU, so one loads while the other writes).  A piece's statistic is its
+// (max, sum of exp(x - max)) pair, two slots of (epoch << 32 | bits) each;
+// a missing piece is recomputed from HBM by the same per-lane code and the
+// same block merge, so its bits equal the owner's.  Every workgroup merges
+// the pieces' pairs in piece order.  NaN and -inf follow k_smx_res: max
+// ignores NaN, a lane or piece with no value above -inf carries its NaNs in
+// the sum, a row with no value above -inf is NaN.
+// ---------------------------------------------------------------------------
+// One lane's (max, sum exp) over its vectors j < nv of a piece, then the block
+// merge.  STREAM (the recompute of another piece): one vector loaded at a
+// time in a rolled loop over j < nv; else the held vectors, unrolled over
+// kPcVR, which the caller has set to -inf past nv.  The two give the same
+// bits: a -inf vector leaves the max alone and adds exp2(-inf) = +0 to a sum
+// that starts at +0.
+template <int PT, int kPcVR, bool STREAM, class V>
+__device__ __forceinline__ void piece_stats(V&& vec, int nv, float (&sh)[2][PT / kWave], float& m, float& s) {
+    const f32x4 ninf = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    (void)ninf;
+    auto at = [&](int j) -> f32x4 { return vec(j); };  // held vectors: -inf past nv already
+    const int n = STREAM ? nv : kPcVR;
+    float gm = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < (STREAM ? 1 : kPcVR); ++j) {
+        for (int jj = j; jj < (STREAM ? n : j + 1); ++jj) {
+            const f32x4 x = at(jj);
+            gm = fmaxf(fmaxf(gm, fmaxf(x.x, x.y)), fmaxf(x.z, x.w));
+        }
+    }
+    float gs = 0.0f;
+    if (gm != -INFINITY) {
+#pragma unroll
+        for (int j = 0; j < (STREAM ? 1 : kPcVR); ++j) {
+            for (int jj = j; jj < (STREAM ? n : j + 1); ++jj) {
+                const f32x4 x = at(jj);
+                gs += (exs(x.x - gm) + exs(x.y - gm)) + (exs(x.z - gm) + exs(x.w - gm));
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < (STREAM ? 1 : kPcVR); ++j) {
+            for (int jj = j; jj < (STREAM ? n : j + 1); ++jj) {  // only -inf and NaN: NaN stays
+                const f32x4 x = at(jj);
+                gs += ((x.x != x.x ? x.x : 0.0f) + (x.y != x.y ? x.y : 0.0f)) +
+                      ((x.z != x.z ? x.z : 0.0f) + (x.w != x.w ? x.w : 0.0f));
+            }
+        }
+    }
+    m = gm;
+    s = gs;
+#pragma unroll
+    for (int o = kWave / 2; o >= 1; o >>= 1) ms_merge(m, s, __shfl_xor(m, o, kWave), __shfl_xor(s, o, kWave));
+    const int t = threadIdx.x;
+    __syncthreads();  // sh may still be read from an earlier merge
+    if (__lane_id() == 0) {
+        sh[0][t / kWave] = m;
+        sh[1][t / kWave] = s;
+    }
+    __syncthreads();
+    m = sh[0][0];
+    s = sh[1][0];
+#pragma unroll
+    for (int i = 1; i < PT / kWave; ++i) ms_merge(m, s, sh[0][i], sh[1][i]);
+}
+
+template <int MODE, int NT, int PT, int kPcVR>
+__global__ __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_smx_fwd_pieces(SmxArgs p, int ns, int pv, unsigned epoch, int spin) {
+    static_assert(MODE == FWD || MODE == FWD_LOG, "forward only");
+    __shared__ float sh[2][PT / kWave];
+    __shared__ float pm[kPcMax], ps[kPcMax];
+    __shared__ unsigned missing;
+    constexpr int aux = NT ? 2 : 0;
+    const int t = threadIdx.x;
+    const long long row = blockIdx.x / ns;
+    const int pc = (int)(blockIdx.x % ns);
+    const int q = (int)(p.n >> 2);
+    const float* ra = p.a + row * p.sa;
+    auto plen = [&](int i) { return max(0, min(q, i * pv + pv) - i * pv); };  // float4 of piece i
+    auto rsrc = [&](const float* base, int i) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base + 4LL * i * pv), (short)0, plen(i) * 16,
+                                                 kBufWord3);
+    };
+    // vectors j of this lane: piece vector j * PT + t, inside the piece for j < nv
+    auto nv_of = [&](int i) { return (plen(i) - t + PT - 1) / PT; };
+    const __amdgpu_buffer_rsrc_t bx = rsrc(ra, pc);
+    f32x4 x[kPcVR];
+#pragma unroll
+    for (int j = 0; j < kPcVR; ++j) x[j] = __builtin_amdgcn_raw_buffer_load_b128(bx, (j * PT + t) * 16, 0, aux);
+    float m, s;
+    {
+        const int nv = nv_of(pc);  // the rest read 0 (buffer range) and are never stored
+        const f32x4 ninf = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+        for (int j = 0; j < kPcVR; ++j) x[j] = j < nv ? x[j] : ninf;
+    }
+    piece_stats<PT, kPcVR, false>([&](int j) { return x[j]; }, kPcVR, sh, m, s);
+    if (t == 0) {
+        pm[pc] = m;
+        ps[pc] = s;
+        unsigned need = 0;
+        if (ns > 1) {
+            unsigned long long* slot = smx_slots;
+            const long long base = 2 * row * ns;
+            const unsigned long long tag = (unsigned long long)epoch << 32;
+            __hip_atomic_exchange(slot + ((base + 2 * pc) & (kSmxSlots - 1)), tag | __float_as_uint(m),
+                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_exchange(slot + ((base + 2 * pc + 1) & (kSmxSlots - 1)), tag | __float_as_uint(s),
+                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            need = ((1u << ns) - 1u) & ~(1u << pc);
+            const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+            for (;;) {
+                for (int i = 0; i < ns; ++i) {
+                    if (!((need >> i) & 1u)) continue;
+                    const unsigned long long vm = __hip_atomic_fetch_or(
+                        slot + ((base + 2 * i) & (kSmxSlots - 1)), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    const unsigned long long vs = __hip_atomic_fetch_or(
+                        slot + ((base + 2 * i + 1) & (kSmxSlots - 1)), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if ((unsigned)(vm >> 32) == epoch && (unsigned)(vs >> 32) == epoch) {
+                        pm[i] = __uint_as_float((unsigned)vm);
+                        ps[i] = __uint_as_float((unsigned)vs);
+                        need &= ~(1u << i);
+                    }
+                }
+                if (need == 0 || __builtin_amdgcn_s_memrealtime() - t0 > (unsigned long long)spin) break;
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        missing = need;
+    }
+    __syncthreads();
+    const unsigned miss = missing;
+    for (int i = 0; i < ns; ++i) {
+        if (!((miss >> i) & 1u)) continue;  // uniform
+        const __amdgpu_buffer_rsrc_t mx = rsrc(ra, i);
+        float m2, s2;
+        piece_stats<PT, kPcVR, true>(
+            [&](int j) { return __builtin_amdgcn_raw_buffer_load_b128(mx, (j * PT + t) * 16, 0, 0); }, nv_of(i), sh,
+            m2, s2);
+        if (t == 0) {
+            pm[i] = m2;
+            ps[i] = s2;
+        }
+    }
+    __syncthreads();
+    float M = pm[0], S = ps[0];
+    for (int i = 1; i < ns; ++i) ms_merge(M, S, pm[i], ps[i]);
+    float st0, st1;
+    if (M == -INFINITY) {  // no value above -inf in the row: NaN, as the reference
+        st0 = NAN;
+        st1 = NAN;
+    } else {
+        st0 = M;
+        st1 = (MODE == FWD) ? 1.0f / S : logf(S);
+    }
+    float* ro = p.out + row * p.n;
+    const __amdgpu_buffer_rsrc_t bo = rsrc(ro, pc);
+#pragma unroll
+    for (int j = 0; j < kPcVR; ++j) {
+        const f32x4 r = {outv<MODE>(x[j].x, 0.0f, st0, st1), outv<MODE>(x[j].y, 0.0f, st0, st1),
+                         outv<MODE>(x[j].z, 0.0f, st0, st1), outv<MODE>(x[j].w, 0.0f, st0, st1)};
         __builtin_amdgcn_raw_buffer_store_b128(r, bo, (j * PT + t) * 16, 0, aux);  // past the piece: dropped
     }
 }
@@ -1461,6 +1632,20 @@ int launch_bwd_pieces(const SmxArgs& a, int ns, hipStream_t st) {
     return check_launch("tpr_softmax (gradient, row pieces)");
 }
 
+template <int MODE, int PT, int VR>
+int launch_fwd_pieces(const SmxArgs& a, int ns, hipStream_t st) {
+    const long long grid = a.rows * ns;
+    if (grid > 0x7fffffffLL) return fail(TPR_ERR_INVALID_ARG, "tpr_softmax: too many row pieces");
+    const long long q = a.n / 4;
+    const int pv = (int)((q + ns - 1) / ns);
+    unsigned ep = smx_epoch_ctr.fetch_add(1, std::memory_order_relaxed) + 1u;
+    if (ep == 0) ep = smx_epoch_ctr.fetch_add(1, std::memory_order_relaxed) + 1u;
+    const int spin = knobs().smx_spin < 0 ? 0 : 4000;
+    if (a.nt) hipLaunchKernelGGL((k_smx_fwd_pieces<MODE, 1, PT, VR>), dim3((unsigned)grid), dim3(PT), 0, st, a, ns, pv, ep, spin);
+    else hipLaunchKernelGGL((k_smx_fwd_pieces<MODE, 0, PT, VR>), dim3((unsigned)grid), dim3(PT), 0, st, a, ns, pv, ep, spin);
+    return check_launch("tpr_softmax (row pieces)");
+}
+
 template <int MODE>
 int run_rows(const SmxArgs& a0, int vw, hipStream_t st) {
     SmxArgs a = a0;
@@ -1472,6 +1657,18 @@ int run_rows(const SmxArgs& a0, int vw, hipStream_t st) {
         // per lane, two workgroups per CU) and 96.0 (g held, y read twice);
         // [1024, 32768] 67.2 against 74.2 (g held)
         if (const int ns = bwd_pieces(a.n, vw, 512, 24)) return launch_bwd_pieces<MODE, 512, 24>(a, ns, st);
+    } else if (knobs().smx_fwd_pieces >= 0) {
+        // forward: x held by row pieces when the one-row-per-CU kernel below
+        // would take more than one round and a row makes two pieces or more;
+        // measured on MI355X (us, resident -> pieces): [512, 65536] 56.7 ->
+        // 48.4 (log 54.5 -> 44.8), [2048, 50260] 165 -> 159 (log 164 -> 151),
+        // [1024, 128256] 197 -> 189, but C5 [256, 151936] 57.1 -> 60.8 (one
+        // round: every CU loads, then every CU writes, at full rate anyway)
+        // and [1024, 32768] (one piece per row) 43.9 -> 48.3.  The test knob
+        // smx_fwd_pieces = 1 takes every row the pieces can hold.
+        const int ns = bwd_pieces(a.n, vw, 512, kFwdPcVR);
+        if (ns > 0 && (knobs().smx_fwd_pieces > 0 || (ns >= 2 && a.rows > device_info().cus)))
+            return launch_fwd_pieces<MODE, 512, kFwdPcVR>(a, ns, st);
     }
     // rows of 16384..153600 floats, at least one per CU: one row per CU in
     // registers + LDS (forward: x held; gradients: g held, y streamed).

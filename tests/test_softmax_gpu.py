@@ -26,7 +26,8 @@ torch = pytest.importorskip("torch")
 @pytest.fixture(autouse=True)
 def _reset_knobs():
     yield
-    for k in ("smx_two_pass", "smx_split", "smx_lanes", "smx_res", "general", "nt", "smx_pieces", "smx_spin"):
+    for k in ("smx_two_pass", "smx_split", "smx_lanes", "smx_res", "general", "nt", "smx_pieces", "smx_spin",
+              "smx_fwd_pieces"):
         _capi.debug_set(k, 0)
 
 
@@ -63,6 +64,47 @@ def test_rows_every_variant(log, plan):
         rows = 5 if n > 4096 else 37
         x = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
         check_fwd(x, x, 1, log)
+
+
+@pytest.mark.parametrize("log", [False, True])
+@pytest.mark.parametrize("spin", [0, -1])
+def test_rows_by_pieces(log, spin):
+    """Forward softmax / log_softmax by row pieces (x held by 1..16 workgroups
+    per row, (max, sum exp) exchanged, spin=0; or every piece recomputing the
+    others from memory, spin=-1), forced onto every row the pieces can hold:
+    ragged last pieces, rows of NaN / -inf / +inf, more rows than CUs."""
+    _capi.debug_set("smx_fwd_pieces", 1)
+    _capi.debug_set("smx_spin", spin)
+    rng = np.random.default_rng(33)
+    for rows, n in [(3, 16388), (2, 40964), (3, 41000), (2, 81924), (3, 151936), (2, 327680), (300, 20000)]:
+        x = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+        if rows <= 3:
+            x[0, n // 3] = np.nan            # a NaN row
+            x[1, :] = -np.inf                # no value above -inf: NaN
+            x[1, n - 1] = np.nan if n % 2 else -np.inf
+            x[-1, 7] = np.inf
+        check_fwd(x, x, 1, log)
+
+
+def test_rows_by_pieces_exchange_equals_recompute():
+    """The exchanged and the recomputed (max, sum exp) pairs are the same bits,
+    so the output does not depend on whether the pieces met; and the planned
+    route (more rows than CUs, two pieces or more per row) runs the pieces."""
+    rng = np.random.default_rng(34)
+    x = torch.from_numpy((rng.standard_normal((600, 65536)) * 3).astype(np.float32)).cuda()
+    for log in (False, True):
+        a = _capi.softmax(x, -1, log=log)
+        _capi.debug_set("smx_spin", -1)
+        b = _capi.softmax(x, -1, log=log)
+        _capi.debug_set("smx_spin", 0)
+        _capi.debug_set("smx_fwd_pieces", -1)
+        c = _capi.softmax(x, -1, log=log)  # the one-row-per-CU kernel
+        _capi.debug_set("smx_fwd_pieces", 0)
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+        r = softmax_error(a[:6].cpu().numpy(), x[:6].double().cpu().numpy(), 1, log)
+        assert r <= 1.0
+        assert softmax_error(c[:6].cpu().numpy(), x[:6].double().cpu().numpy(), 1, log) <= 1.0
 
 
 @pytest.mark.parametrize("log", [False, True])
