@@ -30,6 +30,9 @@
 //   * longer rows stream twice: an online (max, sum-of-exp) pass, then the
 //     output pass -- k_smx_rows2, or split over (row, chunk) workgroups when
 //     the rows are fewer than the CUs -- k_smx_part / k_smx_apply;
+//   * strided forward slices of 513..1024 rows with 16-byte columns: two row
+//     pieces per 64-column group exchanging per-column statistics --
+//     k_smx_cols4p;
 //   * a strided softmax dim (inner extent > 1, or a non-unit dim stride)
 //     keeps one column per lane, thread rows across the dim, an LDS merge of
 //     the per-wave states, and also streams twice -- k_smx_cols.
@@ -634,7 +637,7 @@ __global__ __launch_bounds__(kResT) void k_smx_res_bwd(SmxArgs p, int vl) {
 // ---------------------------------------------------------------------------
 constexpr int kPcMax = 16;                     // most pieces per row
 constexpr int kFwdPcVR = 20;                   // forward pieces: float4 of x per lane
-constexpr int kSmxSlots = 1 << 16;             // exchange slots (rows * NS wrap around)
+constexpr int kSmxSlots = 1 << 18;             // exchange slots (rows * NS wrap around; 2 MiB)
 
 }  // namespace
 }  // namespace tpr
@@ -1332,6 +1335,218 @@ __global__ __launch_bounds__(kWave * BY) void k_smx_cols4r(SmxColArgs p) {
 
 
 // ---------------------------------------------------------------------------
+// Strided forward softmax by row pieces: a 64-column group of a slice of
+// 513..1024 rows is cut into two pieces of <= 512 rows, one 8-wave workgroup
+// each holding its rows in registers (16 per lane, as k_smx_cols4r with 16
+// waves holds the whole slice), so two workgroups share a CU and one loads
+// while the other writes.  The pieces exchange their per-column (max, sum exp)
+// through the slot array with the launch's epoch (lanes of wave 0 with rl = 0
+// own 4 columns each: 8 slots), waiting a bounded time; a piece not seen in
+// time is recomputed from HBM by the same per-lane code (rows streamed in the
+// same order) and the same merges, so its bits equal the owner's.  Every
+// workgroup merges the two pieces in piece order.
+// ---------------------------------------------------------------------------
+template <int BY, int V, bool STREAM, class L>
+__device__ __forceinline__ void col_piece_stats(L&& row, f32x4 (&shm)[BY][16], f32x4 (&shs)[BY][16], f32x4& Mv,
+                                                f32x4& Sv) {
+    constexpr int CW = 16;
+    const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave, cl = lane % CW, rl = lane / CW;
+    float m[4], sm[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) m[q] = -INFINITY;
+    auto max_step = [&](const f32x4 x) {
+        m[0] = fmaxf(m[0], x.x);
+        m[1] = fmaxf(m[1], x.y);
+        m[2] = fmaxf(m[2], x.z);
+        m[3] = fmaxf(m[3], x.w);
+    };
+    // the same steps in the same order either way: the held rows unrolled,
+    // the streamed ones one row at a time (few registers next to the held x);
+    // the -inf test per column outside the row loop (inside it, the selects
+    // kept both results of every element live)
+    if constexpr (STREAM) {
+#pragma nounroll
+        for (int i = 0; i < V; ++i) max_step(row(i));
+    } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) max_step(row(i));
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float acc = 0.0f;
+        if (m[q] != -INFINITY) {
+            if constexpr (STREAM) {
+#pragma nounroll
+                for (int i = 0; i < V; ++i) acc += exs(row(i)[q] - m[q]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < V; ++i) acc += exs(row(i)[q] - m[q]);
+            }
+        } else {  // only -inf and NaN: NaN stays
+            if constexpr (STREAM) {
+#pragma nounroll
+                for (int i = 0; i < V; ++i) {
+                    const float v = row(i)[q];
+                    acc += (v != v) ? v : 0.0f;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < V; ++i) {
+                    const float v = row(i)[q];
+                    acc += (v != v) ? v : 0.0f;
+                }
+            }
+        }
+        sm[q] = acc;
+    }
+#pragma unroll
+    for (int off = CW; off <= 32; off <<= 1) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float m2 = __shfl_xor(m[q], off, kWave), s2 = __shfl_xor(sm[q], off, kWave);
+            ms_merge(m[q], sm[q], m2, s2);
+        }
+    }
+    __syncthreads();  // shm / shs may still be read from an earlier call
+    if (rl == 0) {
+        shm[w][cl] = f32x4{m[0], m[1], m[2], m[3]};
+        shs[w][cl] = f32x4{sm[0], sm[1], sm[2], sm[3]};
+    }
+    __syncthreads();
+    Mv = shm[0][cl];
+    Sv = shs[0][cl];
+    for (int k = 1; k < BY; ++k) {
+        const f32x4 mk = shm[k][cl], sk = shs[k][cl];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float M = Mv[q], S = Sv[q];
+            ms_merge(M, S, mk[q], sk[q]);
+            Mv[q] = M;
+            Sv[q] = S;
+        }
+    }
+}
+
+template <int MODE, int BY, int V, bool NT>
+__global__ __launch_bounds__(kWave * BY) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_smx_cols4p(SmxColArgs p, unsigned epoch, int spin) {
+    static_assert(MODE == FWD || MODE == FWD_LOG, "forward only");
+    constexpr int CW = 16, RW = kWave / CW, RS = RW * BY, PR = RS * V;  // PR rows per piece
+    __shared__ f32x4 shm[BY][CW];
+    __shared__ f32x4 shs[BY][CW];
+    __shared__ f32x4 pm[2][CW], ps[2][CW];
+    __shared__ int missing;
+    const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave, cl = lane % CW, rl = lane / CW;
+    const long long ncg = (p.inner + 4 * CW - 1) / (4 * CW);
+    const long long gi = blockIdx.x / 2;  // column group
+    const int pc = (int)(blockIdx.x % 2);
+    const long long o = gi / ncg;
+    const long long c = (gi - o * ncg) * (4 * CW) + 4 * cl;
+    const bool live = c < p.inner;
+    const float* pa = p.a + o * p.a_so + (live ? c : 0);
+    float* po = p.out + o * p.n * p.inner + (live ? c : 0);
+    const int n = live ? (int)p.n : 0;
+    const f32x4 ninf = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    auto rows_of = [&](int piece, int i) { return piece * PR + rl + RW * w + i * RS; };
+    auto load = [&](int piece, int i) -> f32x4 {
+        const int r = rows_of(piece, i);
+        if (r >= min(n, (piece + 1) * PR)) return ninf;
+        float v[4];
+        vld<4, false>(v, pa + (long long)r * p.a_sn);
+        return f32x4{v[0], v[1], v[2], v[3]};
+    };
+    f32x4 x[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int r = rows_of(pc, i);
+        if (r < min(n, (pc + 1) * PR)) {
+            float v[4];
+            vld<4, NT>(v, pa + (long long)r * p.a_sn);
+            x[i] = f32x4{v[0], v[1], v[2], v[3]};
+        } else {
+            x[i] = ninf;
+        }
+    }
+    f32x4 Mv, Sv;
+    col_piece_stats<BY, V, false>([&](int i) { return x[i]; }, shm, shs, Mv, Sv);
+    const int other = pc ^ 1;
+    if (w == 0 && rl == 0) {
+        pm[pc][cl] = Mv;
+        ps[pc][cl] = Sv;
+        unsigned long long* slot = smx_slots;
+        const unsigned long long tag = (unsigned long long)epoch << 32;
+        const long long mine = ((gi * 2 + pc) * CW + cl) * 8, theirs = ((gi * 2 + other) * CW + cl) * 8;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            __hip_atomic_exchange(slot + ((mine + q) & (kSmxSlots - 1)), tag | __float_as_uint(Mv[q]),
+                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_exchange(slot + ((mine + 4 + q) & (kSmxSlots - 1)), tag | __float_as_uint(Sv[q]),
+                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        unsigned need = 0xffu;  // bit j: slot j of the other piece not seen yet
+        float got[8];
+        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+        for (;;) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (!((need >> j) & 1u)) continue;
+                const unsigned long long v = __hip_atomic_fetch_or(slot + ((theirs + j) & (kSmxSlots - 1)), 0ull,
+                                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if ((unsigned)(v >> 32) == epoch) {
+                    got[j] = __uint_as_float((unsigned)v);
+                    need &= ~(1u << j);
+                }
+            }
+            if (need == 0 || __builtin_amdgcn_s_memrealtime() - t0 > (unsigned long long)spin) break;
+            __builtin_amdgcn_s_sleep(2);
+        }
+        if (need == 0) {
+            pm[other][cl] = f32x4{got[0], got[1], got[2], got[3]};
+            ps[other][cl] = f32x4{got[4], got[5], got[6], got[7]};
+        }
+        // any of the 16 owner lanes short: the whole workgroup recomputes
+        const bool short_any = __ballot(need != 0) != 0ull;
+        if (lane == 0) missing = short_any ? 1 : 0;
+    }
+    __syncthreads();
+    if (missing) {  // uniform
+        f32x4 Mo, So;
+        col_piece_stats<BY, V, true>([&](int i) { return load(other, i); }, shm, shs, Mo, So);
+        if (w == 0 && rl == 0) {
+            pm[other][cl] = Mo;
+            ps[other][cl] = So;
+        }
+        __syncthreads();
+    }
+    float st0[4], st1[4];
+    {
+        const f32x4 m0 = pm[0][cl], s0 = ps[0][cl], m1 = pm[1][cl], s1 = ps[1][cl];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float M = m0[q], S = s0[q];
+            ms_merge(M, S, m1[q], s1[q]);
+            if (M == -INFINITY) {
+                st0[q] = NAN;
+                st1[q] = NAN;
+            } else {
+                st0[q] = M;
+                st1[q] = (MODE == FWD) ? 1.0f / S : logf(S);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int r = rows_of(pc, i);
+        if (r < min(n, (pc + 1) * PR)) {
+            float out[4];
+            const float xv[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) out[q] = outv<MODE>(xv[q], 0.0f, st0[q], st1[q]);
+            vst<4, NT>(po + (long long)r * p.inner, out);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Float64 inputs (the reference's composite runs in the input dtype, so a
 // Float64 tensor gives a Float64 softmax).  Same semantics as the float32
 // kernels, computed in double with exp / log: two passes over a slice.
@@ -1721,6 +1936,20 @@ int run_cols(const SmxColArgs& a, hipStream_t st) {
             // 8 waves 160 us; at [16, 256, 8192] dim 1: 8 waves 70 us, 16 waves 92 us)
             // slices of 65..1024 rows (backward, two inputs: ..256) stay in
             // registers: read once
+            // forward slices of 513..1024 rows: two row pieces per 64-column
+            // group (8-wave workgroups, two per CU) while the grid's slots fit
+            if constexpr (!BW) {
+                const long long gp = 2 * blocks;
+                if (a.n > 512 && a.n <= 1024 && knobs().smx_res >= 0 && knobs().smx_two_pass == 0 &&
+                    knobs().smx_fwd_pieces >= 0 && knobs().smx_pieces >= 0 && gp * 128 <= kSmxSlots) {
+                    unsigned ep = smx_epoch_ctr.fetch_add(1, std::memory_order_relaxed) + 1u;
+                    if (ep == 0) ep = smx_epoch_ctr.fetch_add(1, std::memory_order_relaxed) + 1u;
+                    const int spin = knobs().smx_spin < 0 ? 0 : 4000;
+                    if (a.nt) hipLaunchKernelGGL((k_smx_cols4p<MODE, 8, 16, true>), dim3((unsigned)gp), dim3(kWave * 8), 0, st, a, ep, spin);
+                    else hipLaunchKernelGGL((k_smx_cols4p<MODE, 8, 16, false>), dim3((unsigned)gp), dim3(kWave * 8), 0, st, a, ep, spin);
+                    return check_launch("tpr_softmax (strided dim, row pieces)");
+                }
+            }
             if (a.n > 64 && a.n <= (BW ? 256 : 1024) && knobs().smx_res >= 0 && knobs().smx_two_pass == 0) {
                 // 64-column groups (CW = 16); 32-column groups (CW = 8, two
                 // workgroups per CU) measured slower: 143 vs 131 us at [64, 1024,

@@ -158,6 +158,35 @@ def test_strided_dim_held_in_registers(log, res):
 
 
 @pytest.mark.parametrize("log", [False, True])
+@pytest.mark.parametrize("spin", [0, -1])
+def test_strided_dim_row_pieces(log, spin):
+    """Forward strided slices of 513..1024 rows by two row pieces per 64-column
+    group (per-column (max, sum exp) exchanged, spin=0; or each piece
+    recomputing the other's from memory, spin=-1): ragged column groups, a
+    short second piece, NaN / -inf / +inf columns, and the pieces' results
+    equal bit for bit whether they met or not."""
+    _capi.debug_set("smx_spin", spin)
+    rng = np.random.default_rng(35)
+    for n in (513, 600, 1000, 1024):
+        for inner in (64, 200, 264):
+            x = (rng.standard_normal((3, n, inner)) * 2).astype(np.float32)
+            x[0, n // 2, 1] = np.nan
+            x[0, 3, 9] = np.nan
+            x[1, :, 2] = -np.inf
+            x[1, : n - 1, 6] = -np.inf
+            x[2, n - 1, 3] = np.inf
+            x[2, : n - 1, 5] = -np.inf
+            check_fwd(x, x, 1, log)
+    x = torch.from_numpy((rng.standard_normal((16, 1024, 1024)) * 2).astype(np.float32)).cuda()
+    _capi.debug_set("smx_spin", 0)
+    a = _capi.softmax(x, 1, log=log)
+    _capi.debug_set("smx_spin", -1)
+    b = _capi.softmax(x, 1, log=log)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+@pytest.mark.parametrize("log", [False, True])
 def test_nontemporal_variants(log):
     """The kernels' nontemporal instantiations (chosen from 256 MiB of traffic;
     the nt knob forces them here on small shapes): rows through every plan,
