@@ -637,7 +637,7 @@ __global__ __launch_bounds__(kResT) void k_smx_res_bwd(SmxArgs p, int vl) {
 // ---------------------------------------------------------------------------
 constexpr int kPcMax = 16;                     // most pieces per row
 constexpr int kFwdPcVR = 20;                   // forward pieces: float4 of x per lane
-constexpr int kSmxSlots = 1 << 18;             // exchange slots (rows * NS wrap around; 2 MiB)
+constexpr int kSmxSlots = 1 << 18;             // exchange slots (2 MiB); a launch never needs more
 
 }  // namespace
 }  // namespace tpr
@@ -1871,7 +1871,10 @@ int run_rows(const SmxArgs& a0, int vw, hipStream_t st) {
         // [256, 151936] 84.8 against 90.4 (256-thread pieces), 90.9 (12 float4
         // per lane, two workgroups per CU) and 96.0 (g held, y read twice);
         // [1024, 32768] 67.2 against 74.2 (g held)
-        if (const int ns = bwd_pieces(a.n, vw, 512, 24)) return launch_bwd_pieces<MODE, 512, 24>(a, ns, st);
+        // (one slot per piece: a launch whose pieces outnumber the slots would
+        // reuse a slot under the same epoch, so it takes the kernels below)
+        const int ns = bwd_pieces(a.n, vw, 512, 24);
+        if (ns > 0 && a.rows * ns <= kSmxSlots) return launch_bwd_pieces<MODE, 512, 24>(a, ns, st);
     } else if (knobs().smx_fwd_pieces >= 0) {
         // forward: x held by row pieces when the one-row-per-CU kernel below
         // would take more than one round and a row makes two pieces or more;
@@ -1882,7 +1885,8 @@ int run_rows(const SmxArgs& a0, int vw, hipStream_t st) {
         // and [1024, 32768] (one piece per row) 43.9 -> 48.3.  The test knob
         // smx_fwd_pieces = 1 takes every row the pieces can hold.
         const int ns = bwd_pieces(a.n, vw, 512, kFwdPcVR);
-        if (ns > 0 && (knobs().smx_fwd_pieces > 0 || (ns >= 2 && a.rows > device_info().cus)))
+        if (ns > 0 && a.rows * ns * 2 <= kSmxSlots &&  // two slots per piece, none reused in a launch
+            (knobs().smx_fwd_pieces > 0 || (ns >= 2 && a.rows > device_info().cus)))
             return launch_fwd_pieces<MODE, 512, kFwdPcVR>(a, ns, st);
     }
     // rows of 16384..153600 floats, at least one per CU: one row per CU in
