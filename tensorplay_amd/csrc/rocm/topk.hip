@@ -1368,13 +1368,13 @@ __device__ __forceinline__ uint32_t group_sort_asc(uint32_t m, int sl) {
 }
 
 // The r-th largest (r >= 1) of the wave's 64 * NV values v[] (the multiset
-// over every lane): a 32-step bit search, one compare per value and a ballot
-// count per step (the prefix stays in scalar registers).
-template <int NV>
+// over every lane), all below 2^BITS: a BITS-step bit search, one compare per
+// value and a ballot count per step (the prefix stays in scalar registers).
+template <int NV, int BITS = 32>
 __device__ __forceinline__ uint32_t wave_rth_largest(const uint32_t (&v)[NV], int r) {
     uint32_t pre = 0;
 #pragma unroll 4
-    for (int b = 31; b >= 0; --b) {
+    for (int b = BITS - 1; b >= 0; --b) {
         const uint32_t cand = pre | (1u << b);
         int cnt = 0;
 #pragma unroll
@@ -1603,10 +1603,10 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
 #pragma unroll
             for (int q = 0; q < E; ++q) mx2 = max(mx2, min(mx, key[q]));
             const uint32_t v2[2] = {mx, mx2};
-            T = max(wave_rth_largest<2>(v2, k), 1u);
+            T = max(wave_rth_largest<2, 8 * EB>(v2, k), 1u);
         } else {
             const uint32_t v1[1] = {mx};
-            T = max(wave_rth_largest<1>(v1, min(k, L)), 1u);
+            T = max(wave_rth_largest<1, 8 * EB>(v1, min(k, L)), 1u);
         }
     } else {
         const uint32_t srt = group_sort_asc<L>(mx, sl);
@@ -1707,10 +1707,11 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
                 if (mine[r] && (uint32_t)(mine[r] >> 32) >= T1) list[kpos++] = mine[r];
         }
     } else {
-        // exact k-th key by bit search over every key of the row
+        // exact k-th key by bit search over every key of the row (keys of
+        // EB-byte elements are below 2^(8 EB))
         if (fkeys) float_keys();
         uint32_t pre = 0;
-        for (int b = 31; b >= 0; --b) {
+        for (int b = 8 * EB - 1; b >= 0; --b) {
             const uint32_t cand = pre | (1u << b);
             int cnt = 0;
 #pragma unroll
