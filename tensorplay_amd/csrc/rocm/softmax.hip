@@ -16,9 +16,10 @@
 // and three temporaries).  Here one kernel does it:
 //   * rows shorter than 16384 floats (or a few long rows, up to 32768)
 //     stay in registers: read once and written once -- k_smx_rows;
-//   * forward rows of 16385..327680 floats, more rows than CUs and two
-//     pieces or more per row, are cut into pieces held in registers by one
-//     workgroup each, (max, sum exp) exchanged -- k_smx_fwd_pieces;
+//   * forward rows of 16385..655360 floats with more rows than CUs and two
+//     pieces or more per row, and every forward row of 153601..655360, are
+//     cut into pieces held in registers by one workgroup each, (max, sum
+//     exp) exchanged -- k_smx_fwd_pieces;
 //   * rows of 16384..153600 floats, at least one per CU, stay on one CU in
 //     registers plus LDS and are also read once -- k_smx_res (forward),
 //     k_smx_res_bwd (gradients of rows the piece kernel does not take: g
@@ -1882,11 +1883,15 @@ int run_rows(const SmxArgs& a0, int vw, hipStream_t st) {
         // 48.4 (log 54.5 -> 44.8), [2048, 50260] 165 -> 159 (log 164 -> 151),
         // [1024, 128256] 197 -> 189, but C5 [256, 151936] 57.1 -> 60.8 (one
         // round: every CU loads, then every CU writes, at full rate anyway)
-        // and [1024, 32768] (one piece per row) 43.9 -> 48.3.  The test knob
-        // smx_fwd_pieces = 1 takes every row the pieces can hold.
+        // and [1024, 32768] (one piece per row) 43.9 -> 48.3.  Rows longer than
+        // one CU holds (> 153600 floats) take them at any row count instead of
+        // streaming twice: [64, 262144] 44.4 -> 28.6, [32, 500000] 45.9 ->
+        // 33.9, [512, 163840] 153 -> 120, [8, 655360] 25.0 -> 20.8.  The test
+        // knob smx_fwd_pieces = 1 takes every row the pieces can hold.
         const int ns = bwd_pieces(a.n, vw, 512, kFwdPcVR);
         if (ns > 0 && a.rows * ns * 2 <= kSmxSlots &&  // two slots per piece, none reused in a launch
-            (knobs().smx_fwd_pieces > 0 || (ns >= 2 && a.rows > device_info().cus)))
+            (knobs().smx_fwd_pieces > 0 || (ns >= 2 && a.rows > device_info().cus) ||
+             (a.n > kResMax && knobs().smx_fwd_pieces == 0)))
             return launch_fwd_pieces<MODE, 512, kFwdPcVR>(a, ns, st);
     }
     // rows of 16384..153600 floats, at least one per CU: one row per CU in

@@ -86,6 +86,20 @@ def test_rows_by_pieces(log, spin):
         check_fwd(x, x, 1, log)
 
 
+@pytest.mark.parametrize("log", [False, True])
+def test_long_rows_planned(log):
+    """Rows longer than one CU holds (153601..655360 floats) take the row
+    pieces on the default plan, any row count; longer rows keep the two-pass
+    kernels.  NaN / -inf rows, ragged last pieces."""
+    rng = np.random.default_rng(36)
+    for rows, n in [(3, 153604), (2, 200000), (2, 500001), (2, 655360), (2, 700000)]:
+        x = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+        x[0, n // 5] = np.nan
+        x[1, :] = -np.inf
+        x[1, 3] = 1.0
+        check_fwd(x, x, 1, log)
+
+
 def test_rows_by_pieces_exchange_equals_recompute():
     """The exchanged and the recomputed (max, sum exp) pairs are the same bits,
     so the output does not depend on whether the pieces met; and the planned
