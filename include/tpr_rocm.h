@@ -264,7 +264,12 @@ int tpr_copy_strided(const void* in, int32_t elem_size, int32_t ndim, const int6
  * (computed in double; the reference composite keeps the input dtype).  Workspace:
  * tpr_softmax_workspace_bytes(desc) bytes (0 for most shapes; rows longer than
  * the register-resident kernels hold, when there are few of them, use
- * per-chunk partial statistics). */
+ * per-chunk partial statistics).  Some shapes (long rows, gradients, strided
+ * dims of 513..1024) split a slice over several workgroups that exchange
+ * partial statistics through a fixed per-device array of the library (2 MiB
+ * of device memory, not the workspace), tagged per call: calls on different
+ * streams may run at the same time; a partner that is not seen within about
+ * 40 us is recomputed, so the result never depends on scheduling. */
 enum tpr_softmax_mode {
     TPR_SOFTMAX_FWD = 0,
     TPR_LOG_SOFTMAX_FWD = 1,
