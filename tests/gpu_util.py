@@ -80,11 +80,12 @@ def softmax_reference(x64, dim, log):
     return np.moveaxis(y, -1, dim), np.moveaxis(np.broadcast_to(lse, x.shape), -1, dim)
 
 
-def softmax_error(got, x64, dim, log):
+def softmax_error(got, x64, dim, log, log_abs_floor=0.0):
     """Max error of an fp32 softmax / log_softmax in units of its tolerance:
     softmax 1e-5 relative; log_softmax 1e-5 * (|y| + |log-sum-exp|) absolute
-    (the terms it subtracts).  NaN / +-inf positions must match exactly.
-    Returns the worst ratio (<= 1 passes)."""
+    (the terms it subtracts), plus log_abs_floor (0 unless a caller states
+    one).  NaN / +-inf positions must match exactly.  Returns the worst ratio
+    (<= 1 passes)."""
     ref, lse = softmax_reference(x64, dim, log)
     got = np.asarray(got, np.float64)
     assert got.shape == ref.shape
@@ -96,7 +97,7 @@ def softmax_error(got, x64, dim, log):
     if not ok.any():
         return 0.0
     if log:
-        tol = 1e-5 * (np.abs(ref) + np.abs(lse))
+        tol = 1e-5 * (np.abs(ref) + np.abs(lse)) + log_abs_floor
     else:
         tol = 1e-5 * np.abs(ref)
     with np.errstate(invalid="ignore"):
