@@ -360,6 +360,14 @@ int32_t tpr_abi_version(void);
  * TPR_ERR_INVALID_ARG for an unknown key.  No reference counterpart. */
 int tpr_debug_set(const char* key, int64_t value);
 
+/* Test build only, like tpr_debug_set: reads a device-side check counter into
+ * *value and clears it (synchronous copies on the default stream).  Key
+ * "topk_merge_clamped": outputs of the split-row top-k merge whose row index
+ * lay past the row (a segment that broke the contract of writing k
+ * composites); the merge clamps such an index into the row in every build,
+ * and counts it here.  No reference counterpart. */
+int tpr_debug_get(const char* key, int64_t* value);
+
 #ifdef __cplusplus
 }
 #endif

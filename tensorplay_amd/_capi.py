@@ -34,7 +34,8 @@ EXPORTED = ["tpr_reduce_workspace_bytes", "tpr_reduce", "tpr_topk_workspace_byte
             "tpr_copy", "tpr_copy_plan", "tpr_copy_strided", "tpr_last_error", "tpr_abi_version",
             "tpr_debug_set", "tpr_softmax", "tpr_softmax_workspace_bytes", "tpr_nll_loss_workspace_bytes", "tpr_nll_loss",
             "tpr_nll_loss_backward", "tpr_reduce_backward_workspace_bytes", "tpr_reduce_backward",
-            "tpr_sample_workspace_bytes", "tpr_sample", "tpr_reduce_noalloc", "tpr_topk_plan"]
+            "tpr_sample_workspace_bytes", "tpr_sample", "tpr_reduce_noalloc", "tpr_topk_plan", "tpr_debug_get"]
+TEST_BUILD_ONLY = {"tpr_debug_set", "tpr_debug_get"}  # exported by libtpr_rocm_dev.so alone
 REDUCE_SCRATCH_BYTES = 8 << 20  # TPR_REDUCE_SCRATCH_BYTES
 # enum tpr_softmax_mode
 SOFTMAX_FWD, LOG_SOFTMAX_FWD, SOFTMAX_BWD, LOG_SOFTMAX_BWD = range(4)
@@ -133,6 +134,8 @@ def lib():
         if hasattr(L, "tpr_debug_set"):  # test build only
             L.tpr_debug_set.argtypes = [ctypes.c_char_p, i64]
             L.tpr_debug_set.restype = ctypes.c_int
+            L.tpr_debug_get.argtypes = [ctypes.c_char_p, ctypes.POINTER(i64)]
+            L.tpr_debug_get.restype = ctypes.c_int
         L.tpr_softmax.argtypes = [ctypes.POINTER(SoftmaxDesc), vp, vp, vp, vp, sz, vp]
         L.tpr_reduce_backward_workspace_bytes.argtypes = [dp]
         L.tpr_reduce_backward_workspace_bytes.restype = sz
@@ -165,6 +168,17 @@ def debug_set(key, value):
     if not hasattr(L, "tpr_debug_set"):
         raise RuntimeError("plan overrides need the test build: set TPR_ROCM_DEV=1 before the library loads")
     _check(L.tpr_debug_set(key.encode(), int(value)))
+
+
+def debug_get(key):
+    """A device-side check counter of the test build, read and cleared
+    (tpr_debug_get): "topk_merge_clamped"."""
+    L = lib()
+    if not hasattr(L, "tpr_debug_get"):
+        raise RuntimeError("check counters need the test build: set TPR_ROCM_DEV=1 before the library loads")
+    v = ctypes.c_int64(0)
+    _check(L.tpr_debug_get(key.encode(), ctypes.byref(v)))
+    return v.value
 
 
 TOPK_KINDS = {1: "short_small", 2: "rsel", 3: "rsel_seg", 4: "radix", 5: "short", 6: "wave", 7: "block", 8: "wave8"}

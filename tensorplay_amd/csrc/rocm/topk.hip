@@ -53,10 +53,18 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstring>
 #include <type_traits>
 #include <string>
 
 #include "common.h"
+
+#ifdef TPR_DEBUG_KNOBS
+// Test build only: merge outputs whose row index had to be clamped into the
+// row (a segment that left its workspace slice unwritten, against the segment
+// contract); read and cleared through tpr_debug_get("topk_merge_clamped").
+static __device__ unsigned int topk_merge_clamped;
+#endif
 
 namespace tpr {
 namespace {
@@ -2487,7 +2495,11 @@ __global__ __launch_bounds__(kMergeT) void k_topk_merge(TopkArgs a, int dtype) {
         return;
     }
     for (int i = threadIdx.x; i < k; i += kMergeT) {
-        const uint32_t idx = min(comp_index(sh.sel[i]), (uint32_t)(a.cols - 1));  // in range even for a bad workspace
+        const uint32_t ci = comp_index(sh.sel[i]);
+#ifdef TPR_DEBUG_KNOBS
+        if (ci >= (uint32_t)a.cols) atomicAdd(&topk_merge_clamped, 1u);
+#endif
+        const uint32_t idx = min(ci, (uint32_t)(a.cols - 1));  // in range even for a bad workspace
         a.out_i[row * k + i] = (long long)idx;
         const char* rb = reinterpret_cast<const char*>(a.in) + row * a.row_stride * dtype_bytes(dtype);
         store_bits(a.out_v, row * k + i, dtype, selected_bits(dtype, (uint32_t)(sh.sel[i] >> 32), a.largest, rb, idx));
@@ -2983,6 +2995,22 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
 }  // namespace tpr
 
 extern "C" {
+
+#ifdef TPR_DEBUG_KNOBS
+// Test builds only: reads a device-side check counter and clears it.
+int tpr_debug_get(const char* key, int64_t* value) {
+    if (!key || !value) return tpr::fail(TPR_ERR_INVALID_ARG, "tpr_debug_get: null argument");
+    if (std::strcmp(key, "topk_merge_clamped") != 0)
+        return tpr::fail(TPR_ERR_INVALID_ARG, std::string("tpr_debug_get: unknown key ") + key);
+    unsigned int v = 0;
+    const unsigned int zero = 0;
+    if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(topk_merge_clamped), sizeof(v)) != hipSuccess ||
+        hipMemcpyToSymbol(HIP_SYMBOL(topk_merge_clamped), &zero, sizeof(zero)) != hipSuccess)
+        return tpr::fail(TPR_ERR_HIP, "tpr_debug_get: device counter not readable");
+    *value = (int64_t)v;
+    return TPR_OK;
+}
+#endif
 
 int tpr_topk_plan(int32_t dtype, int64_t rows, int64_t cols, int64_t k, int64_t row_stride, int32_t aligned,
                   int64_t* out) {

@@ -28,11 +28,12 @@ def test_library_exports_every_declared_symbol():
     dev = ctypes.CDLL(_capi.DEV_LIB_PATH)
     for name in declared:
         assert hasattr(dev, name), name
-    # the shipped library: every entry point but the test build's plan-override hook
+    # the shipped library: every entry point but the test build's hooks
     rel = ctypes.CDLL(_capi.LIB_PATH)
-    for name in declared - {"tpr_debug_set"}:
+    for name in declared - _capi.TEST_BUILD_ONLY:
         assert hasattr(rel, name), name
-    assert not hasattr(rel, "tpr_debug_set")
+    for name in _capi.TEST_BUILD_ONLY:
+        assert not hasattr(rel, name), name
 
 
 def test_release_build_has_no_plan_state():
@@ -40,11 +41,11 @@ def test_release_build_has_no_plan_state():
     import subprocess
     syms = subprocess.run(["nm", "-D", "--defined-only", _capi.LIB_PATH], capture_output=True, text=True,
                           check=True).stdout
-    assert "tpr_debug_set" not in syms
+    assert "tpr_debug_set" not in syms and "tpr_debug_get" not in syms
     assert "knobs" not in syms
     dsyms = subprocess.run(["nm", "-D", "--defined-only", _capi.DEV_LIB_PATH], capture_output=True, text=True,
                            check=True).stdout
-    assert "tpr_debug_set" in dsyms
+    assert "tpr_debug_set" in dsyms and "tpr_debug_get" in dsyms
 
 
 def test_abi_version():

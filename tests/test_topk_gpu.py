@@ -13,9 +13,13 @@ torch = pytest.importorskip("torch")
 
 @pytest.fixture(autouse=True)
 def _reset_knobs():
+    _capi.debug_get("topk_merge_clamped")  # clears the test build's merge check counter
     yield
+    clamped = _capi.debug_get("topk_merge_clamped")
     for k in ("topk_fallback", "topk_variant", "topk_waves", "splits", "topk_short", "topk_radix", "topk_dyn"):
         _capi.debug_set(k, 0)
+    # every split row's segments wrote their k composites: no merge output index needed clamping
+    assert clamped == 0, f"{clamped} merge outputs had a row index past the row"
 
 
 def check(base, v, k, largest=True):
