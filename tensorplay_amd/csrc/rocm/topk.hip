@@ -251,14 +251,20 @@ __device__ void sample_from_sel(const TopkArgs& a, long long row, const float* p
             s += pr[q];
         }
     }
+    // inclusive scan of the block totals by DPP (row shifts, then the row
+    // broadcasts), no LDS round trips; lane 63's total read directly
     float incl = s;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const float t = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += t;
-    }
+#define TPR_DPP_ADD(CTRL, ROWS) \
+    incl += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(incl), CTRL, ROWS, 0xf, false))
+    TPR_DPP_ADD(0x111, 0xf);  // row_shr:1
+    TPR_DPP_ADD(0x112, 0xf);  // row_shr:2
+    TPR_DPP_ADD(0x114, 0xf);  // row_shr:4
+    TPR_DPP_ADD(0x118, 0xf);  // row_shr:8
+    TPR_DPP_ADD(0x142, 0xa);  // row_bcast:15
+    TPR_DPP_ADD(0x143, 0xc);  // row_bcast:31
+#undef TPR_DPP_ADD
     const float excl = incl - s;
-    const float cut = a.top_p * __shfl(incl, 63, 64);
+    const float cut = a.top_p * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(incl), 63));
     int mj = 0x7fffffff;
     float c = excl;
 #pragma unroll
@@ -269,8 +275,7 @@ __device__ void sample_from_sel(const TopkArgs& a, long long row, const float* p
             if (c >= cut && mj == 0x7fffffff) mj = j;
         }
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) mj = min(mj, __shfl_xor(mj, o, 64));
+    mj = __ockl_wfred_min_i32(mj);
     const int m = (mj == 0x7fffffff) ? k - 1 : mj;
     float cm_l = 0.0f;
     c = excl;
@@ -282,7 +287,7 @@ __device__ void sample_from_sel(const TopkArgs& a, long long row, const float* p
             if (j == m) cm_l = c;
         }
     }
-    const float thr = a.u[row] * __shfl(cm_l, m / per, 64);
+    const float thr = a.u[row] * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cm_l), m / per));
     int pj = 0x7fffffff;
     c = excl;
 #pragma unroll
@@ -293,8 +298,7 @@ __device__ void sample_from_sel(const TopkArgs& a, long long row, const float* p
             if (c > thr && pj == 0x7fffffff) pj = j;
         }
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) pj = min(pj, __shfl_xor(pj, o, 64));
+    pj = __ockl_wfred_min_i32(pj);
     if (pj > m) pj = m;
     if (lane == 0) a.ids[row] = (long long)comp_index(sel[pj]);
 }
