@@ -397,12 +397,19 @@ __device__ __forceinline__ uint32_t hist_threshold(const uint32_t* hist, int k, 
     const int lane = __lane_id();
     const uint32_t h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2], h3 = hist[4 * lane + 3];
     const int own = (int)(h0 + h1 + h2 + h3);
-    int suf = own;  // inclusive suffix sum over lanes >= lane
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int t = __shfl_down(suf, d, 64);
-        if (lane + d < 64) suf += t;
-    }
+    // inclusive suffix sum over lanes >= lane = total - exclusive prefix: the
+    // prefix by DPP row shifts and row broadcasts (every lane active), the
+    // total read from lane 63, no LDS round trips
+    int pre = own;
+#define TPR_DPP_ADD(CTRL, ROWS) pre += __builtin_amdgcn_update_dpp(0, pre, CTRL, ROWS, 0xf, false)
+    TPR_DPP_ADD(0x111, 0xf);  // row_shr:1
+    TPR_DPP_ADD(0x112, 0xf);  // row_shr:2
+    TPR_DPP_ADD(0x114, 0xf);  // row_shr:4
+    TPR_DPP_ADD(0x118, 0xf);  // row_shr:8
+    TPR_DPP_ADD(0x142, 0xa);  // row_bcast:15
+    TPR_DPP_ADD(0x143, 0xc);  // row_bcast:31
+#undef TPR_DPP_ADD
+    const int suf = __builtin_amdgcn_readlane(pre, 63) - pre + own;
     const unsigned long long ok = __ballot(suf >= k);
     if (ok == 0) return T;                      // fewer than k entries: no raise
     const int L = 63 - __clzll((long long)ok);  // highest lane whose suffix reaches k
@@ -417,7 +424,7 @@ __device__ __forceinline__ uint32_t hist_threshold(const uint32_t* hist, int k, 
         }
         tn = T + ((uint32_t)(4 * lane + b) << shift);
     }
-    return __shfl(tn, L, 64);
+    return (uint32_t)__builtin_amdgcn_readlane((int)tn, L);
 }
 
 __device__ __forceinline__ int hist_shift(uint32_t hi, uint32_t T) {
