@@ -197,6 +197,20 @@ __device__ __forceinline__ uint32_t comp_index(unsigned long long c) {
 // DPP wave reduction from the device library (no LDS round trips).
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) { return __ockl_wfred_max_u32(v); }
 
+// Inclusive prefix sum over the wave's 64 lanes (every lane active): DPP row
+// shifts by 1, 2, 4, 8 (lanes whose source is outside the row add the 0 passed
+// as `old`), then row_bcast:15 and row_bcast:31 carry the row totals upward.
+// No LDS round trips.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return v;
+}
+
 __device__ __forceinline__ unsigned long long lanemask_lt() { return (1ull << __lane_id()) - 1ull; }
 
 struct TopkArgs {
@@ -465,7 +479,7 @@ __device__ uint32_t block_compact(BlockScratch& bs, const unsigned long long* sr
         const unsigned long long bal = __ballot(keep);
         int base = 0;
         if (lane == 0 && bal) base = atomicAdd(&bs.count2, __popcll(bal));
-        base = __shfl(base, 0, 64);
+        base = __builtin_amdgcn_readlane(base, 0);
         if (keep) dst[base + __popcll(bal & lanemask_lt())] = c;
     }
     __syncthreads();
@@ -994,7 +1008,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, 8)
             const unsigned long long b = __ballot(keep);
             int gbase = 0;
             if (lane == 0 && b) gbase = atomicAdd(&bs.count, __popcll(b));
-            gbase = __shfl(gbase, 0, 64);
+            gbase = __builtin_amdgcn_readlane(gbase, 0);
             if (keep) sh.un[gbase + __popcll(b & lanemask_lt())] = c;  // sum of lists <= kW * KWB == kB
         }
     }
@@ -1154,7 +1168,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(6, 8))) void
         if (total) {
             int base = 0;
             if (lane == 0) base = atomicAdd(&bs.count, total);
-            base = __shfl(base, 0, 64);
+            base = __builtin_amdgcn_readlane(base, 0);
             const unsigned long long lt = lanemask_lt();
 #pragma unroll
             for (int q = 0; q < 4 * kV; ++q) {
@@ -1896,13 +1910,10 @@ __device__ int block_suffix_incl(int v, int* wtot) {
     constexpr int NW = NT / 64;
     const int lane = __lane_id();
     const int w = threadIdx.x / 64;
-    int suf = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int t = __shfl_down(suf, o, 64);
-        if (lane + o < 64) suf += t;
-    }
-    if (lane == 0) wtot[w] = suf;
+    const int pre = wave_incl_scan(v);
+    const int wsum = __builtin_amdgcn_readlane(pre, 63);
+    int suf = wsum - pre + v;  // lanes lane .. 63
+    if (lane == 0) wtot[w] = wsum;
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < NW; ++i)
@@ -2065,12 +2076,7 @@ __device__ int block_prefix_excl(int v, int* wtot, int& total) {
     constexpr int NW = NT / 64;
     const int lane = __lane_id();
     const int w = threadIdx.x / 64;
-    int inc = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int t = __shfl_up(inc, o, 64);
-        if (lane >= o) inc += t;
-    }
+    const int inc = wave_incl_scan(v);
     if (lane == 63) wtot[w] = inc;
     __syncthreads();
     int before = 0;
