@@ -100,7 +100,7 @@ __device__ __forceinline__ float grp(float v, float* sh) {
     constexpr int W = G < kWave ? G : kWave;
 #pragma unroll
     for (int o = W / 2; o >= 1; o >>= 1) {
-        const float t = __shfl_xor(v, o, kWave);
+        const float t = xor_lane_f(v, o);
         v = MAX ? fmaxf(v, t) : v + t;
     }
     if constexpr (G > kWave) {
@@ -1161,7 +1161,7 @@ __global__ __launch_bounds__(kWave * BY) void k_smx_cols4(SmxColArgs p) {
     for (int off = 16; off <= 32; off <<= 1) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float m2 = __shfl_xor(m[q], off, kWave), s2 = __shfl_xor(sm[q], off, kWave);
+            const float m2 = xor_lane_f(m[q], off), s2 = xor_lane_f(sm[q], off);
             if constexpr (!BW) ms_merge(m[q], sm[q], m2, s2);
             else sm[q] += s2;
         }
@@ -1278,7 +1278,7 @@ __global__ __launch_bounds__(kWave * BY) void k_smx_cols4r(SmxColArgs p) {
     for (int off = CW; off <= 32; off <<= 1) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float m2 = __shfl_xor(m[q], off, kWave), s2 = __shfl_xor(sm[q], off, kWave);
+            const float m2 = xor_lane_f(m[q], off), s2 = xor_lane_f(sm[q], off);
             if constexpr (!BW) ms_merge(m[q], sm[q], m2, s2);
             else sm[q] += s2;
         }
@@ -1404,7 +1404,7 @@ __device__ __forceinline__ void col_piece_stats(L&& row, f32x4 (&shm)[BY][16], f
     for (int off = CW; off <= 32; off <<= 1) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float m2 = __shfl_xor(m[q], off, kWave), s2 = __shfl_xor(sm[q], off, kWave);
+            const float m2 = xor_lane_f(m[q], off), s2 = xor_lane_f(sm[q], off);
             ms_merge(m[q], sm[q], m2, s2);
         }
     }

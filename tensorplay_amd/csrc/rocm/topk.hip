@@ -1282,35 +1282,6 @@ __device__ __forceinline__ int group_scan(int v, int sl) {
     return v;
 }
 
-// Lane lane ^ M's value, without LDS-pipe permutes: DPP quad permutes for
-// M = 1, 2; for M = 4 quad_perm [3,2,1,0] (xor 3) then row_half_mirror
-// (i -> 7 - i = i ^ 7 inside 8 lanes); row_ror:8 for M = 8 (rotating a
-// 16-lane row by 8 is xor 8); for M = 16 and 32 the gfx950 permlane swaps of
-// the value with itself (v_permlane16_swap: odd rows of the first operand
-// with even rows of the second; v_permlane32_swap: upper half of the first
-// with lower half of the second), each lane taking the copy that holds its
-// partner's value.  Every lane of the wave must be active.
-template <int M>
-__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
-    if constexpr (M == 1) {
-        return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
-    } else if constexpr (M == 2) {
-        return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
-    } else if constexpr (M == 4) {
-        const int t = __builtin_amdgcn_mov_dpp((int)v, 0x1B, 0xF, 0xF, false);  // quad_perm [3,2,1,0]
-        return (uint32_t)__builtin_amdgcn_mov_dpp(t, 0x141, 0xF, 0xF, false);   // row_half_mirror
-    } else if constexpr (M == 8) {
-        return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
-    } else if constexpr (M == 16) {
-        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-        return (__lane_id() & 16) ? r[0] : r[1];
-    } else {
-        static_assert(M == 32, "lane distance 1 .. 32");
-        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-        return (__lane_id() & 32) ? r[0] : r[1];
-    }
-}
-
 // Largest value over the lanes of an L-lane group (every lane of the group
 // active; groups are whole 16-lane rows, so the exchanges stay inside them).
 template <int L>
