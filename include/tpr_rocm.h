@@ -201,9 +201,11 @@ int tpr_topk_plan(int32_t dtype, int64_t rows, int64_t cols, int64_t k, int64_t 
  *   out = the column index of the first j <= m with c_j > u * c_m,
  * with u = uniforms[row] in [0, 1) (device float32 [rows], drawn by the
  * caller).  temperature <= 0 selects v_0 (greedy).  top_p in (0, 1], 1 <= k <=
- * min(cols, 1024).  out_ids: device int64 [rows].  Workspace:
- * tpr_sample_workspace_bytes (tpr_topk's: the draw runs in top-k's last
- * phase, nothing else is written). */
+ * cols (k = cols: top-p alone).  out_ids: device int64 [rows].  Workspace:
+ * tpr_sample_workspace_bytes: for k <= 1024 tpr_topk's (the draw runs in
+ * top-k's last phase, nothing else is written); for k > 1024 tpr_topk's, then
+ * the sorted values (float32 [rows][k]) and indices (int64 [rows][k]) that
+ * tpr_topk writes there and a second kernel draws from. */
 size_t tpr_sample_workspace_bytes(int32_t dtype, int64_t rows, int64_t cols, int64_t k);
 int tpr_sample(const void* logits, int32_t dtype, int64_t rows, int64_t cols, int64_t row_stride, int64_t k,
                float temperature, float top_p, const float* uniforms, int64_t* out_ids, void* workspace,

@@ -317,6 +317,121 @@ __device__ void sample_from_sel(const TopkArgs& a, long long row, const float* p
     if (lane == 0) a.ids[row] = (long long)comp_index(sel[pj]);
 }
 
+// Sampling with k > kKMax: the draw of sample_from_sel over a row's sorted top
+// k that tpr_topk has already written (vals[row][k] in rank order, idx[row][k]
+// their indices), one workgroup of NT threads per row.  Thread t owns the
+// contiguous positions [t*per, (t+1)*per): serial sums inside its block, a
+// workgroup scan of the block totals, workgroup minima for the nucleus end m
+// and the drawn position.  p_j is formed with explicit roundings (no
+// contraction), so the three passes over a block see bit-identical c_j.
+constexpr int kDrawNT = 1024;
+
+__device__ __forceinline__ float draw_weight(float v, float temperature, float z0) {
+    return expf(__fsub_rn(__fdiv_rn(v, temperature), z0));
+}
+
+template <int W>
+__device__ __forceinline__ int block_min_i32(int v, int* sh) {
+    v = __ockl_wfred_min_i32(v);
+    if (__lane_id() == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    int r = sh[0];
+#pragma unroll
+    for (int q = 1; q < W; ++q) r = min(r, sh[q]);
+    return r;
+}
+
+template <int NT>
+__global__ __launch_bounds__(NT) void k_sample_sorted(const float* vals, const long long* idx, int k,
+                                                      float temperature, float top_p, const float* u,
+                                                      long long* ids) {
+    constexpr int W = NT / 64;
+    __shared__ float wsum[W];
+    __shared__ int wmin[2][W];
+    __shared__ float cm_sh;
+    const long long row = blockIdx.x;
+    const float* v = vals + row * k;
+    const int tid = threadIdx.x, w = tid >> 6;
+    if (!(temperature > 0.0f)) {
+        if (tid == 0) ids[row] = idx[row * k];
+        return;
+    }
+    const int per = (k + NT - 1) / NT;
+    const int j0 = min(k, tid * per), j1 = min(k, j0 + per);
+    const float z0 = __fdiv_rn(v[0], temperature);
+    float s = 0.0f;
+    for (int j = j0; j < j1; ++j) s += draw_weight(v[j], temperature, z0);
+    float incl = s;
+#define TPR_DPP_ADD(CTRL, ROWS) \
+    incl += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(incl), CTRL, ROWS, 0xf, false))
+    TPR_DPP_ADD(0x111, 0xf);  // row_shr:1
+    TPR_DPP_ADD(0x112, 0xf);  // row_shr:2
+    TPR_DPP_ADD(0x114, 0xf);  // row_shr:4
+    TPR_DPP_ADD(0x118, 0xf);  // row_shr:8
+    TPR_DPP_ADD(0x142, 0xa);  // row_bcast:15
+    TPR_DPP_ADD(0x143, 0xc);  // row_bcast:31
+#undef TPR_DPP_ADD
+    if (__lane_id() == 63) wsum[w] = incl;
+    __syncthreads();
+    float before = 0.0f, total = 0.0f;
+#pragma unroll
+    for (int q = 0; q < W; ++q) {
+        const float t = wsum[q];
+        if (q < w) before += t;
+        total += t;
+    }
+    const float excl = before + (incl - s);
+    const float cut = top_p * total;
+    int mj = 0x7fffffff;
+    float c = excl;
+    for (int j = j0; j < j1; ++j) {
+        c += draw_weight(v[j], temperature, z0);
+        if (c >= cut) {
+            mj = j;
+            break;
+        }
+    }
+    mj = block_min_i32<W>(mj, wmin[0]);
+    const int m = (mj == 0x7fffffff) ? k - 1 : mj;
+    if (m >= j0 && m < j1) {
+        c = excl;
+        for (int j = j0; j <= m; ++j) c += draw_weight(v[j], temperature, z0);
+        cm_sh = c;
+    }
+    __syncthreads();
+    const float thr = u[row] * cm_sh;
+    int pj = 0x7fffffff;
+    c = excl;
+    for (int j = j0; j < j1 && j <= m; ++j) {
+        c += draw_weight(v[j], temperature, z0);
+        if (c > thr) {
+            pj = j;
+            break;
+        }
+    }
+    pj = block_min_i32<W>(pj, wmin[1]);
+    if (pj > m) pj = m;
+    if (tid == 0) ids[row] = idx[row * k + pj];
+}
+
+// Workspace of tpr_sample with k > kKMax: tpr_topk's own workspace, then the
+// sorted values [rows][k] (float32) and indices [rows][k] (int64), each part
+// starting on a 256-byte boundary.
+struct SampleSortedLayout {
+    size_t topk_ws, vals_off, idx_off, total;
+};
+
+inline size_t round_up_256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+inline SampleSortedLayout sample_sorted_layout(int64_t rows, int64_t cols, int64_t k) {
+    SampleSortedLayout l;
+    l.topk_ws = tpr_topk_workspace_bytes(TPR_FLOAT32, rows, cols, k);
+    l.vals_off = round_up_256(l.topk_ws);
+    l.idx_off = l.vals_off + round_up_256((size_t)rows * (size_t)k * sizeof(float));
+    l.total = l.idx_off + (size_t)rows * (size_t)k * sizeof(long long);
+    return l;
+}
+
 // Small shared state of the workgroup-level helpers.
 struct BlockScratch {
     uint32_t wave_val[kMaxW];
@@ -1823,6 +1938,7 @@ __global__ __launch_bounds__(kShortT) void k_topk_short(TopkArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int kRadixT = 256;    // threads per row (several rows per CU)
 constexpr int kRadixLds = 4096;  // composites sorted in LDS (32 KiB)
+constexpr int kRadixRegChunk = 8192;  // chunk of the global sort held in registers (1024 threads x 8)
 constexpr int kRadixBins = 2048; // 11-bit digits: passes over key bits 31..21, 20..10, 9..0
 
 __host__ __device__ inline int pow2_at_least(int v) {
@@ -1858,6 +1974,175 @@ __device__ void bitonic_desc(C* c, int n) {
                 }
             }
             __syncthreads();
+        }
+    }
+}
+
+// The stages of one bitonic block size `size` with strides from `top` down to
+// 1 on the B-composite chunk held in `lds` whose first element has global
+// position g0 (the direction of a pair follows its global position, as in
+// bitonic_desc).  Ends with a barrier.
+template <int NT, class C, int B>
+__device__ void bitonic_chunk_stages(C* lds, int g0, int size, int top) {
+    for (int stride = top; stride > 0; stride >>= 1) {
+        for (int t = threadIdx.x; t < B / 2; t += NT) {
+            const int i = ((t & ~(stride - 1)) << 1) | (t & (stride - 1));
+            const int j = i + stride;
+            const C ci = lds[i], cj = lds[j];
+            const bool desc = ((g0 + i) & size) == 0;
+            if (desc ? (ci < cj) : (ci > cj)) {
+                lds[i] = cj;
+                lds[j] = ci;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// NST consecutive bitonic stages of block size `size`, strides dl << (NST-1)
+// down to dl, in place in global memory: each thread holds the G = 2^NST
+// elements base + m*dl (m < G) of a group in registers, so one read and one
+// write of the composites serve NST stages.  Ends with a barrier.
+template <int NT, class C, int NST>
+__device__ void bitonic_global_stages(C* c, int n, int size, int dl) {
+    constexpr int G = 1 << NST;
+    const int sh = __builtin_ctz((unsigned)dl);
+    for (int t = threadIdx.x; t < n / G; t += NT) {
+        const int base = ((t >> sh) << (sh + NST)) | (t & (dl - 1));
+        C v[G];
+#pragma unroll
+        for (int m = 0; m < G; ++m) v[m] = c[base + m * dl];
+        const bool desc = (base & size) == 0;
+#pragma unroll
+        for (int s = G / 2; s >= 1; s >>= 1) {
+#pragma unroll
+            for (int m = 0; m < G; ++m) {
+                if (m & s) continue;
+                const C x = v[m], y = v[m + s];
+                const bool sw = desc ? (x < y) : (x > y);
+                v[m] = sw ? y : x;
+                v[m + s] = sw ? x : y;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < G; ++m) c[base + m * dl] = v[m];
+    }
+    __syncthreads();
+}
+
+// The bitonic block sizes s_lo .. s_hi (powers of two) over an n-composite
+// chunk held P per thread (thread t: positions t*P .. t*P+P-1, every thread of
+// the workgroup active, n = NT*P) whose first element has global position g0:
+// the direction of a pair follows its global position, strides start at
+// min(s, n) / 2.  As reg_sort_desc: strides below P in registers, below 64*P
+// by lane permutes, the rest through xb (LDS, NT*min(P, 4) composites) with
+// barriers.
+template <int NT, int P>
+__device__ void reg_bitonic_range(unsigned long long (&x)[P], unsigned long long* xb, int n, int s_lo, int s_hi,
+                                  int g0) {
+    constexpr int Q = P < 4 ? P : 4;
+    const int t = threadIdx.x;
+    for (int s = s_lo; s <= s_hi; s <<= 1) {
+        for (int d = min(s, n) >> 1; d >= P; d >>= 1) {
+            const int m = d / P;  // partner thread t ^ m
+            const bool desc = ((g0 + t * P) & s) == 0;
+            const bool keep_max = ((t & m) == 0) == desc;
+            switch (m) {
+                case 1: sort_lane_stage<1, P>(x, keep_max); break;
+                case 2: sort_lane_stage<2, P>(x, keep_max); break;
+                case 4: sort_lane_stage<4, P>(x, keep_max); break;
+                case 8: sort_lane_stage<8, P>(x, keep_max); break;
+                case 16: sort_lane_stage<16, P>(x, keep_max); break;
+                case 32: sort_lane_stage<32, P>(x, keep_max); break;
+                default:
+#pragma unroll
+                    for (int p0 = 0; p0 < P; p0 += Q) {
+#pragma unroll
+                        for (int q = 0; q < Q; ++q) xb[q * NT + t] = x[p0 + q];
+                        __syncthreads();
+#pragma unroll
+                        for (int q = 0; q < Q; ++q) {
+                            const unsigned long long y = xb[q * NT + (t ^ m)];
+                            x[p0 + q] = ((x[p0 + q] > y) == keep_max) ? x[p0 + q] : y;
+                        }
+                        __syncthreads();
+                    }
+            }
+        }
+#pragma unroll
+        for (int dd = P / 2; dd >= 1; dd >>= 1) {
+            if (dd < s) {
+#pragma unroll
+                for (int p = 0; p < P; ++p) {
+                    if ((p & dd) == 0) {
+                        const bool desc = ((g0 + t * P + p) & s) == 0;
+                        const unsigned long long u = x[p], v = x[p + dd];
+                        const bool sw = (u > v) != desc;
+                        x[p] = sw ? v : u;
+                        x[p + dd] = sw ? u : v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// bitonic_desc for n > B composites in global memory, with the B-composite
+// LDS buffer `lds`: every stage of stride < B runs on B-element chunks staged
+// in LDS (one load and one store per chunk for all of a block size's short
+// strides; 64-bit composites held in registers, reg_bitonic_range); the
+// strides >= B run in global memory, up to three per pass
+// (bitonic_global_stages).  At n = 2^18: 9 global passes and 7 chunk passes
+// with B = 4096, 5 and 5 with B = 16384, against 171 global stages.
+template <int NT, class C, int B>
+__device__ void bitonic_desc_blocked(C* c, int n, C* lds) {
+    for (int size = 2; size <= n; size <<= 1) {
+        if (size > B) {
+            int cur = size / 2;
+            while (cur >= B) {
+                if ((cur >> 2) >= B) {
+                    bitonic_global_stages<NT, C, 3>(c, n, size, cur >> 2);
+                    cur >>= 3;
+                } else if ((cur >> 1) >= B) {
+                    bitonic_global_stages<NT, C, 2>(c, n, size, cur >> 1);
+                    cur >>= 2;
+                } else {
+                    bitonic_global_stages<NT, C, 1>(c, n, size, cur);
+                    cur >>= 1;
+                }
+            }
+        }
+        // the block sizes up to B all run in one visit per chunk
+        if (size > B || size == 2) {
+            if constexpr (std::is_same<C, unsigned long long>::value && B % NT == 0 && NT == 1024) {
+                // 64-bit composites, 1024 threads: the chunk in registers, B / NT
+                // per thread (the 256-thread kernel keeps the LDS stages: 16 per
+                // thread would cost it occupancy in the select phase)
+                constexpr int P = B / NT;
+                const int t = threadIdx.x;
+                for (int g0 = 0; g0 < n; g0 += B) {
+                    unsigned long long x[P];
+#pragma unroll
+                    for (int p = 0; p < P; ++p) x[p] = c[g0 + t * P + p];
+                    if (size > B) reg_bitonic_range<NT, P>(x, lds, B, size, size, g0);
+                    else reg_bitonic_range<NT, P>(x, lds, B, 2, B, g0);
+#pragma unroll
+                    for (int p = 0; p < P; ++p) c[g0 + t * P + p] = x[p];
+                }
+                __syncthreads();
+            } else {
+                for (int g0 = 0; g0 < n; g0 += B) {
+                    for (int e = threadIdx.x; e < B; e += NT) lds[e] = c[g0 + e];
+                    __syncthreads();
+                    if (size > B) {
+                        bitonic_chunk_stages<NT, C, B>(lds, g0, size, B / 2);
+                    } else {
+                        for (int s = 2; s <= B; s <<= 1) bitonic_chunk_stages<NT, C, B>(lds, g0, s, s / 2);
+                    }
+                    for (int e = threadIdx.x; e < B; e += NT) c[g0 + e] = lds[e];
+                    __syncthreads();
+                }
+            }
         }
     }
 }
@@ -1994,7 +2279,9 @@ __device__ void radix_select(RadixShared<T>& sh, typename Comp<typename SortKey<
 }
 
 // Values are the selected elements themselves (re-read at their index).
-template <class T, int NT>
+// GSORT: k's composites are sorted in the workspace (pow2(k) > the LDS count);
+// only those launches carry the global sort's code and registers.
+template <class T, int NT, bool GSORT>
 __global__ __launch_bounds__(NT) void k_topk_radix(TopkArgs a, void* gcand) {
     using C = typename Comp<typename SortKey<T>::K>::C;
     __shared__ RadixShared<T> sh;
@@ -2007,7 +2294,14 @@ __global__ __launch_bounds__(NT) void k_topk_radix(TopkArgs a, void* gcand) {
     radix_select<NT, T>(sh, cand, p, a.cols, k, a.largest);
     for (int i = k + threadIdx.x; i < n2; i += NT) cand[i] = (C)0;
     __syncthreads();
-    bitonic_desc<NT, C>(cand, n2);
+    if constexpr (!GSORT) {
+        bitonic_desc<NT, C>(cand, n2);
+    } else {
+        if (NT == 1024 && sizeof(C) == 8 && n2 > kRadixRegChunk)
+            bitonic_desc_blocked<NT, C, kRadixRegChunk>(cand, n2, sh.cand);  // 8 composites per thread
+        else
+            bitonic_desc_blocked<NT, C, radix_lds_count<T>()>(cand, n2, sh.cand);
+    }
     if constexpr (std::is_same<T, float>::value) {
         if (a.sample) {
             if (threadIdx.x < 64) sample_from_sel(a, row, p, cand, k);
@@ -2876,8 +3170,15 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
         const int nt = rows < 2LL * device_info().cus ? 1024 : kRadixT;
 #define TPR_RADIX(T)                                                                                  \
     {                                                                                                 \
-        if (nt == 1024) hipLaunchKernelGGL((k_topk_radix<T, 1024>), dim3((unsigned)rows), dim3(1024), 0, st, a, workspace); \
-        else hipLaunchKernelGGL((k_topk_radix<T, kRadixT>), dim3((unsigned)rows), dim3(kRadixT), 0, st, a, workspace); \
+        const bool gs = pow2_at_least((int)k) > radix_lds_count<T>();                                 \
+        const dim3 g((unsigned)rows);                                                                 \
+        if (nt == 1024) {                                                                             \
+            if (gs) hipLaunchKernelGGL((k_topk_radix<T, 1024, true>), g, dim3(1024), 0, st, a, workspace); \
+            else hipLaunchKernelGGL((k_topk_radix<T, 1024, false>), g, dim3(1024), 0, st, a, workspace); \
+        } else {                                                                                      \
+            if (gs) hipLaunchKernelGGL((k_topk_radix<T, kRadixT, true>), g, dim3(kRadixT), 0, st, a, workspace); \
+            else hipLaunchKernelGGL((k_topk_radix<T, kRadixT, false>), g, dim3(kRadixT), 0, st, a, workspace); \
+        }                                                                                             \
     }
         switch (dtype) {
             case TPR_FLOAT32: TPR_RADIX(float) break;
@@ -3024,6 +3325,8 @@ int tpr_topk(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64_t 
 }
 
 size_t tpr_sample_workspace_bytes(int32_t dtype, int64_t rows, int64_t cols, int64_t k) {
+    if (dtype == TPR_FLOAT32 && k > tpr::kKMax && k <= cols && rows > 0 && cols <= 0x7fffffffLL)
+        return tpr::sample_sorted_layout(rows, cols, k).total;
     return tpr_topk_workspace_bytes(dtype, rows, cols, k);
 }
 
@@ -3034,7 +3337,6 @@ int tpr_sample(const void* logits, int32_t dtype, int64_t rows, int64_t cols, in
     if (dtype != TPR_FLOAT32) return fail(TPR_ERR_UNSUPPORTED_DTYPE, "tpr_sample: float32 logits only");
     if (rows < 0 || cols < 0) return fail(TPR_ERR_INVALID_ARG, "tpr_sample: negative shape");
     if (k < 1 || k > cols) return fail(TPR_ERR_INVALID_ARG, "tpr_sample: k must be in [1, cols]");
-    if (k > kKMax) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_sample: k > 1024 is not implemented");
     if (!(top_p > 0.0f) || top_p > 1.0f) return fail(TPR_ERR_INVALID_ARG, "tpr_sample: top_p must be in (0, 1]");
     if (rows == 0) return TPR_OK;
     if (!logits || !uniforms || !out_ids) return fail(TPR_ERR_INVALID_ARG, "tpr_sample: null pointer");
@@ -3043,6 +3345,25 @@ int tpr_sample(const void* logits, int32_t dtype, int64_t rows, int64_t cols, in
     smp.top_p = top_p;
     smp.u = uniforms;
     smp.ids = reinterpret_cast<long long*>(out_ids);
+    if (k > kKMax) {
+        // the sorted top k through tpr_topk into the workspace, then the draw
+        // by one workgroup per row
+        if (cols > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_sample: rows longer than 2^31-1");
+        if (rows > 0x7fffffffLL) return fail(TPR_ERR_NOT_IMPLEMENTED, "tpr_sample: more than 2^31-1 rows");
+        const SampleSortedLayout l = sample_sorted_layout(rows, cols, k);
+        if (workspace == nullptr || workspace_bytes < l.total)
+            return fail(TPR_ERR_WORKSPACE, "tpr_sample: workspace too small (need " + std::to_string(l.total) +
+                                               " bytes)");
+        char* ws = static_cast<char*>(workspace);
+        float* vals = reinterpret_cast<float*>(ws + l.vals_off);
+        long long* idx = reinterpret_cast<long long*>(ws + l.idx_off);
+        const int rc = topk_launch(logits, dtype, rows, cols, row_stride, k, 1, vals, idx,
+                                   l.topk_ws ? workspace : nullptr, l.topk_ws, stream, nullptr);
+        if (rc != TPR_OK) return rc;
+        hipLaunchKernelGGL((k_sample_sorted<kDrawNT>), dim3((unsigned)rows), dim3(kDrawNT), 0,
+                           static_cast<hipStream_t>(stream), vals, idx, (int)k, temperature, top_p, uniforms, smp.ids);
+        return check_launch("tpr_sample");
+    }
     return topk_launch(logits, dtype, rows, cols, row_stride, k, 1, nullptr, nullptr, workspace, workspace_bytes,
                        stream, &smp);
 }

@@ -105,6 +105,14 @@ def test_argument_validation_without_gpu():
     assert L.tpr_topk_workspace_bytes(_capi.FLOAT32, 4, 32768, 20000) == 0       # rows held in registers
     assert L.tpr_topk_workspace_bytes(_capi.INT32, 4, 40000, 3000) == 0          # streaming: 4096 in LDS
     assert L.tpr_topk_workspace_bytes(_capi.INT32, 4, 40000, 5000) == 4 * 8192 * 8  # streaming: workspace sort
+    # sampling: k <= 1024 draws inside top-k; larger k adds the sorted values
+    # and indices after top-k's own workspace (256-byte aligned parts)
+    assert L.tpr_sample_workspace_bytes(_capi.FLOAT32, 4, 40000, 1024) == L.tpr_topk_workspace_bytes(
+        _capi.FLOAT32, 4, 40000, 1024)
+    tws = L.tpr_topk_workspace_bytes(_capi.FLOAT32, 4, 40000, 5000)
+    assert tws == 4 * 8192 * 8
+    assert L.tpr_sample_workspace_bytes(_capi.FLOAT32, 4, 40000, 5000) == tws + 80128 + 4 * 5000 * 8
+    assert L.tpr_sample_workspace_bytes(_capi.FLOAT32, 3, 2000, 2000) == 24064 + 3 * 2000 * 8  # top-k needs none here
     with pytest.raises(_capi.TprError):
         _capi.debug_set("no_such_knob", 1)
     d = _capi.make_desc("sum", [4], [1], [0], _capi.FLOAT32)

@@ -94,3 +94,67 @@ def test_dispatcher_op():
     assert np.array_equal(got[margin > 1e-5], exp[margin > 1e-5])
     with pytest.raises(RuntimeError):
         tp.topk_topp_sample(tp.tensor(x, device="rocm"), tp.tensor(u, device="rocm"), 20, 1.0, 1.5)
+
+
+def check_large_k(x, u, k, T, top_p, tol=1e-5):
+    """k > 1024 (the sorted top k drawn by a second kernel).  Long tails hold
+    many positions whose p_j lies below float32 rounding of the cumulative
+    sums, so a boundary draw may land several positions from the oracle's;
+    the rule: the GPU's position pos must satisfy the draw's inequalities on
+    the oracle's float64 sums up to tol * c_{k-1}, i.e. pos <= m_hi (the last
+    nucleus end the cut allows within tol), c_pos > u*c_m - tol and
+    c_{pos-1} <= u*c_m + tol; rows with margin > tol must match exactly."""
+    print(f"case sample_large shape={x.shape} k={k} T={T} top_p={top_p}", flush=True)
+    got = _capi.sample(torch.from_numpy(x).cuda(), torch.from_numpy(u).cuda(), k, T, top_p).cpu().numpy()
+    exp, margin, m, _, _ = O.sample(x, u, k, T, top_p, details=True)
+    sure = margin > tol
+    np.testing.assert_array_equal(got[sure], exp[sure])
+    if not T > 0:
+        np.testing.assert_array_equal(got, exp)
+        return
+    vals, idx = O.topk(x, k)
+    for r in np.nonzero(~sure)[0]:
+        c = np.cumsum(np.exp(vals[r].astype(np.float64) / T - vals[r, 0] / T))
+        e = tol * c[-1]
+        hit = np.nonzero(c >= top_p * c[-1] + e)[0]
+        m_hi = int(hit[0]) if hit.size else k - 1
+        pos = np.nonzero(idx[r] == got[r])[0]
+        assert pos.size == 1, (r, got[r])
+        p = int(pos[0])
+        thr = float(u[r]) * c[m[r]]
+        assert p <= m_hi, (r, p, m_hi)
+        assert c[p] > thr - e or p == m_hi, (r, p)
+        assert p == 0 or c[p - 1] <= thr + e, (r, p)
+
+
+def test_large_k_and_top_p_alone():
+    rng = np.random.default_rng(34)
+    for rows, cols, ks in [(33, 5000, (1025, 2000, 5000)), (5, 40000, (1025, 4096, 40000)), (2, 1025, (1025,))]:
+        x = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
+        u = rng.random(rows).astype(np.float32)
+        for k in ks:
+            for T, top_p in ((1.0, 1.0), (0.7, 0.9), (1.5, 0.5), (0.0, 0.9), (1.0, 1e-6)):
+                check_large_k(x, u, k, T, top_p)
+
+
+def test_large_k_llm_logits_c5_shape():
+    # top-p alone over the whole vocabulary of C5-shaped logits (k = cols)
+    rng = np.random.default_rng(35)
+    rows, cols = 16, 151936
+    x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    for r in range(rows):
+        x[r, rng.choice(cols, 8, replace=False)] += 15.0
+    u = rng.random(rows).astype(np.float32)
+    for T, top_p in ((1.0, 0.9), (0.7, 0.95), (1.3, 1.0)):
+        check_large_k(x, u, cols, T, top_p)
+    check_large_k(x, u, 2048, 1.0, 0.9)
+
+
+def test_large_k_ties():
+    # equal logits: ranks fall to the lowest index, the draw splits evenly
+    x = np.zeros((4, 3000), np.float32)
+    u = np.array([0.0, 0.25, 0.5, 0.999], np.float32)
+    got = _capi.sample(torch.from_numpy(x).cuda(), torch.from_numpy(u).cuda(), 2000, 1.0, 1.0).cpu().numpy()
+    exp, margin = O.sample(x, u, 2000, 1.0, 1.0)
+    np.testing.assert_array_equal(got[margin > 1e-5], exp[margin > 1e-5])
+    assert got[0] == 0 and np.all(got < 2000)
