@@ -407,6 +407,47 @@ def test_register_rows_large_k(cols):
             check(x, v, k, False)
 
 
+def test_workspace_sort_paths():
+    """k whose pow2 exceeds the LDS sort (the streaming kernel sorts in the
+    workspace): 1024-thread workgroups (fewer rows than 2 per CU) with chunks
+    of 4096 and 8192 composites in registers and up to three global stages per
+    pass; 256-thread workgroups (more rows) with 4096-composite chunks in LDS;
+    8-byte dtypes (128-bit composites, 2048-composite LDS chunks).  Ties, equal
+    rows, NaN / +-0 and k = cols included."""
+    _capi.debug_set("topk_radix", 2)  # every row through the streaming kernel
+    rng = np.random.default_rng(36)
+    x = rng.standard_normal((6, 70000)).astype(np.float32)
+    x[1] = np.round(x[1] * 4) / 4
+    x[2] = 0.5
+    x[3, ::3] = np.nan
+    x[4] = np.where(rng.random(70000) < 0.5, -0.0, 0.0)
+    for k in (4097, 8192, 8193, 20000, 65537, 70000):  # pow2: 8192 .. 131072
+        check(x, x, k, True)
+    check(x, x, 8193, False)
+    check(x, x, 70000, False)
+    many = rng.standard_normal((600, 9000)).astype(np.float32)  # 256-thread workgroups
+    many[::7] = np.round(many[::7])
+    check(many, many, 5000, True)
+    check(many, many, 9000, False)
+    for dt in (np.float64, np.int64, np.uint64):
+        if dt == np.float64:
+            y = rng.standard_normal((5, 12000))
+            y[0, ::5] = np.nan
+            y[1] = np.round(y[1])
+        else:
+            info = np.iinfo(dt)
+            y = rng.integers(info.min, info.max, size=(5, 12000), dtype=dt, endpoint=True)
+            y[1] = y[1] % 7
+        yt = torch.from_numpy(y).cuda()
+        for k, largest in ((2049, True), (9000, False), (12000, True)):
+            print(f"case topk dtype={np.dtype(dt).name} shape={y.shape} k={k} largest={largest}", flush=True)
+            gv, gi = _capi.topk(yt, k, largest)
+            torch.cuda.synchronize()
+            ev, ei = O.topk_any(y, k, largest)
+            np.testing.assert_array_equal(gi.cpu().numpy(), ei)
+            np.testing.assert_array_equal(gv.cpu().numpy().view(np.uint8), ev.view(np.uint8))
+
+
 def test_large_k_configs():
     rng = np.random.default_rng(31)
     x = rng.uniform(-1, 1, (4096, 2048)).astype(np.float32)
