@@ -2182,7 +2182,8 @@ __device__ int block_suffix_incl(int v, int* wtot) {
 // by radix passes over the key bits from the top, 11 bits per pass (each pass
 // counts the keys that match the digits found so far in a 2048-bin LDS
 // histogram), then every key > T and the lowest-index keys == T.
-template <int NT, class T>
+// GB: the gather keeps several loads in flight per thread (more registers).
+template <int NT, class T, bool GB = true>
 __device__ void radix_select(RadixShared<T>& sh, typename Comp<typename SortKey<T>::K>::C* cand, const T* p, int n,
                              int k, int largest) {
     using K = typename SortKey<T>::K;
@@ -2199,7 +2200,17 @@ __device__ void radix_select(RadixShared<T>& sh, typename Comp<typename SortKey<
         const K dmask = (K)((1u << (hi - shift)) - 1u);
         for (int i = tid; i < kRadixBins; i += NT) sh.hist[i] = 0u;
         __syncthreads();
-        for (int e = tid; e < n; e += NT) {
+        // eight loads in flight per thread before their histogram updates
+        int e0 = tid;
+        for (; e0 + 7 * NT < n; e0 += 8 * NT) {
+            K key[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) key[u] = SortKey<T>::of(p[e0 + u * NT], largest);
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if ((key[u] & pmask) == prefix) atomicAdd(&sh.hist[(uint32_t)((key[u] >> shift) & dmask)], 1u);
+        }
+        for (int e = e0; e < n; e += NT) {
             const K key = SortKey<T>::of(p[e], largest);
             if ((key & pmask) == prefix) atomicAdd(&sh.hist[(uint32_t)((key >> shift) & dmask)], 1u);
         }
@@ -2235,7 +2246,20 @@ __device__ void radix_select(RadixShared<T>& sh, typename Comp<typename SortKey<
         // order (most data: after two or three passes instead of all of them)
         if (tid == 0) sh.count = 0;
         __syncthreads();
-        for (int e = tid; e < n; e += NT) {
+        // GB: GU loads in flight per thread (8 in the 1024-thread kernel, which
+        // runs one workgroup per CU anyway; 4 in the 256-thread one)
+        constexpr int GU = NT == 1024 ? 8 : 4;
+        int e0 = tid;
+        for (; GB && e0 + (GU - 1) * NT < n; e0 += GU * NT) {
+            K key[GU];
+#pragma unroll
+            for (int u = 0; u < GU; ++u) key[u] = SortKey<T>::of(p[e0 + u * NT], largest);
+#pragma unroll
+            for (int u = 0; u < GU; ++u)
+                if ((key[u] & pmask) >= prefix)
+                    cand[atomicAdd(&sh.count, 1)] = CP::make(key[u], (uint32_t)(e0 + u * NT));
+        }
+        for (int e = e0; e < n; e += NT) {
             const K key = SortKey<T>::of(p[e], largest);
             if ((key & pmask) >= prefix) cand[atomicAdd(&sh.count, 1)] = CP::make(key, (uint32_t)e);
         }
@@ -2280,8 +2304,9 @@ __device__ void radix_select(RadixShared<T>& sh, typename Comp<typename SortKey<
 
 // Values are the selected elements themselves (re-read at their index).
 // GSORT: k's composites are sorted in the workspace (pow2(k) > the LDS count);
-// only those launches carry the global sort's code and registers.
-template <class T, int NT, bool GSORT>
+// only those launches carry the global sort's code and registers.  GB: see
+// radix_select (off where two 1024-thread workgroups per CU must fit).
+template <class T, int NT, bool GSORT, bool GB>
 __global__ __launch_bounds__(NT) void k_topk_radix(TopkArgs a, void* gcand) {
     using C = typename Comp<typename SortKey<T>::K>::C;
     __shared__ RadixShared<T> sh;
@@ -2291,7 +2316,7 @@ __global__ __launch_bounds__(NT) void k_topk_radix(TopkArgs a, void* gcand) {
     const int k = a.k;
     const int n2 = pow2_at_least(k);
     C* cand = (n2 <= radix_lds_count<T>()) ? sh.cand : static_cast<C*>(gcand) + row * (long long)n2;
-    radix_select<NT, T>(sh, cand, p, a.cols, k, a.largest);
+    radix_select<NT, T, GB>(sh, cand, p, a.cols, k, a.largest);
     for (int i = k + threadIdx.x; i < n2; i += NT) cand[i] = (C)0;
     __syncthreads();
     if constexpr (!GSORT) {
@@ -3173,11 +3198,13 @@ int topk_launch(const void* in, int32_t dtype, int64_t rows, int64_t cols, int64
         const bool gs = pow2_at_least((int)k) > radix_lds_count<T>();                                 \
         const dim3 g((unsigned)rows);                                                                 \
         if (nt == 1024) {                                                                             \
-            if (gs) hipLaunchKernelGGL((k_topk_radix<T, 1024, true>), g, dim3(1024), 0, st, a, workspace); \
-            else hipLaunchKernelGGL((k_topk_radix<T, 1024, false>), g, dim3(1024), 0, st, a, workspace); \
+            if (gs) hipLaunchKernelGGL((k_topk_radix<T, 1024, true, true>), g, dim3(1024), 0, st, a, workspace); \
+            else if (rows > device_info().cus)                                                        \
+                hipLaunchKernelGGL((k_topk_radix<T, 1024, false, false>), g, dim3(1024), 0, st, a, workspace); \
+            else hipLaunchKernelGGL((k_topk_radix<T, 1024, false, true>), g, dim3(1024), 0, st, a, workspace); \
         } else {                                                                                      \
-            if (gs) hipLaunchKernelGGL((k_topk_radix<T, kRadixT, true>), g, dim3(kRadixT), 0, st, a, workspace); \
-            else hipLaunchKernelGGL((k_topk_radix<T, kRadixT, false>), g, dim3(kRadixT), 0, st, a, workspace); \
+            if (gs) hipLaunchKernelGGL((k_topk_radix<T, kRadixT, true, true>), g, dim3(kRadixT), 0, st, a, workspace); \
+            else hipLaunchKernelGGL((k_topk_radix<T, kRadixT, false, true>), g, dim3(kRadixT), 0, st, a, workspace); \
         }                                                                                             \
     }
         switch (dtype) {
