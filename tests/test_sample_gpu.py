@@ -158,3 +158,24 @@ def test_large_k_ties():
     exp, margin = O.sample(x, u, 2000, 1.0, 1.0)
     np.testing.assert_array_equal(got[margin > 1e-5], exp[margin > 1e-5])
     assert got[0] == 0 and np.all(got < 2000)
+
+
+def test_random_sweep():
+    """Fixed-seed sweep over row counts, row lengths, k on both sides of 1024
+    (the draw inside top-k, and the sorted top-k plus the draw kernel),
+    temperatures (greedy included) and top_p, with logits of three spreads."""
+    rng = np.random.default_rng(20261202)
+    for case in range(36):
+        rows = int(rng.choice([1, 3, 17, 64, 300]))
+        cols = int(rng.choice([50, 1000, 1500, 5000, 32768, 70000]))
+        k = int(min(cols, rng.choice([1, 8, 50, 256, 1024, 1025, 3000, cols])))
+        T = float(rng.choice([0.0, 0.5, 1.0, 1.7]))
+        top_p = float(rng.choice([0.05, 0.5, 0.9, 0.99, 1.0]))
+        scale = float(rng.choice([0.5, 2.0, 6.0]))
+        x = (rng.standard_normal((rows, cols)) * scale).astype(np.float32)
+        u = rng.random(rows).astype(np.float32)
+        print(f"sweep case {case}", flush=True)
+        if k > 1024:
+            check_large_k(x, u, k, T, top_p)
+        else:
+            check(x, u, k, T, top_p)
