@@ -2919,14 +2919,18 @@ bool rsel_route(long long cols, int32_t dtype) {
 }
 
 // Longer rows of elements of <= 4 bytes with k <= 1024 and at most kMergeMax
-// segment winners (vocabulary-sized rows: 151936 with k <= 1024): segments of
-// <= 32768 elements through k_topk_rsel, one workgroup each, then the merge
-// pass.  Returns the segment count, 0 when the streaming kernel takes the row.
-// Measured on MI355X against the streaming k_topk_radix (one workgroup per
-// row): [256, 151936] k = 256 1018 us, k = 1000 1053 us; [16, 500000] k = 256
-// 1959 us (the figures after are in the design notes).
-int rsel_segments(long long cols, long long k, int32_t dtype) {
-    if (dtype_size(dtype) > 4 || cols <= kRselMaxCols || k > kKMax || knobs().topk_radix == 2) return 0;
+// segment winners, fewer than kSegMaxRows rows: segments of <= 32768 elements
+// through k_topk_rsel, one workgroup each, then the merge pass.  Returns the
+// segment count, 0 when the streaming kernel takes the row.  Few rows need
+// the segments to fill the chip; from 64 rows on the streaming kernel (one
+// workgroup per row, several loads in flight) is faster.  MI355X, us,
+// segments against streaming: [16, 500000] k = 300 65 / 153; [64, 100000]
+// k = 600 69 / 59, k = 1024 78 / 62; [256, 151936] k = 1000 229 / 105;
+// [2048, 65536] k = 500 677 / 373.
+constexpr long long kSegMaxRows = 64;
+int rsel_segments(long long rows, long long cols, long long k, int32_t dtype) {
+    if (dtype_size(dtype) > 4 || cols <= kRselMaxCols || k > kKMax || knobs().topk_radix == 2 || rows >= kSegMaxRows)
+        return 0;
     const long long nseg = (cols + kRselMaxCols - 1) / kRselMaxCols;
     return nseg * k <= kMergeMax ? (int)nseg : 0;
 }
@@ -2935,7 +2939,7 @@ int rsel_segments(long long cols, long long k, int32_t dtype) {
 // bytes each for elements of at most 4 bytes, 16 for 8-byte elements).
 size_t radix_ws(long long rows, long long cols, long long k, int32_t dtype = TPR_FLOAT32) {
     if (rsel_route(cols, dtype)) return 0;
-    if (const int ns = rsel_segments(cols, k, dtype)) return (size_t)rows * ns * k * sizeof(unsigned long long);
+    if (const int ns = rsel_segments(rows, cols, k, dtype)) return (size_t)rows * ns * k * sizeof(unsigned long long);
     const long long n2 = pow2_at_least((int)k);
     const bool wide = dtype_size(dtype) == 8;
     const long long lds = wide ? 2048 : kRadixLds;
@@ -2995,7 +2999,7 @@ TopkRoute route_topk(long long rows, long long cols, long long k, int32_t dtype,
         if (pl.wave && pl.nseg == 1) return TopkRoute{TK_WAVE8, 1, (int)cols, pl.nw, (size_t)rows * sizeof(int)};
     }
     if (radix && rsel_route(cols, dtype)) return TopkRoute{TK_RSEL, 1, (int)cols, 0, 0};
-    if (const int ns = radix ? rsel_segments(cols, k, dtype) : 0) {
+    if (const int ns = radix ? rsel_segments(rows, cols, k, dtype) : 0) {
         const int seg_len = (int)((cols + ns - 1) / ns + 3) & ~3;  // segment starts stay 16-byte aligned
         return TopkRoute{TK_RSEL_SEG, ns, seg_len, 0, radix_ws(rows, cols, k, dtype)};
     }
