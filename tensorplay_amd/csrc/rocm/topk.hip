@@ -2913,8 +2913,15 @@ bool radix_route(long long rows, long long cols, long long k, int32_t dtype = TP
 }
 
 // Rows the register-resident kernel takes (elements of <= 4 bytes, rows of
-// <= 32768); topk_radix = 2 forces the streaming kernel for them.
-bool rsel_route(long long cols, int32_t dtype) {
+// <= 32768); topk_radix = 2 forces the streaming kernel for them.  4-byte
+// rows longer than 16384 with k <= 1024 stream instead: there the register
+// kernel runs 32 keys per thread, and the streaming kernel's passes (several
+// loads in flight) and LDS sort of <= 1024 are faster.  MI355X, us, register
+// / streaming: [1024, 24000] k = 300 139 / 102, k = 1000 156 / 142; [1024,
+// 32768] k = 1000 165 / 159; [200, 32768] k = 700 44 / 36; but [1024, 16384]
+// k = 1000 97 / 106 and [1024, 32768] k = 1500 185 / 226.
+bool rsel_route(long long cols, long long k, int32_t dtype) {
+    if (dtype_size(dtype) == 4 && cols > 16384 && k <= kKMax) return false;
     return dtype_size(dtype) <= 4 && cols <= kRselMaxCols && knobs().topk_radix != 2;
 }
 
@@ -2938,7 +2945,7 @@ int rsel_segments(long long rows, long long cols, long long k, int32_t dtype) {
 // Workspace of the streaming radix kernel: composites sorted outside LDS (8
 // bytes each for elements of at most 4 bytes, 16 for 8-byte elements).
 size_t radix_ws(long long rows, long long cols, long long k, int32_t dtype = TPR_FLOAT32) {
-    if (rsel_route(cols, dtype)) return 0;
+    if (rsel_route(cols, k, dtype)) return 0;
     if (const int ns = rsel_segments(rows, cols, k, dtype)) return (size_t)rows * ns * k * sizeof(unsigned long long);
     const long long n2 = pow2_at_least((int)k);
     const bool wide = dtype_size(dtype) == 8;
@@ -2998,7 +3005,7 @@ TopkRoute route_topk(long long rows, long long cols, long long k, int32_t dtype,
         const TopkPlan pl = plan_topk(rows, cols, k);
         if (pl.wave && pl.nseg == 1) return TopkRoute{TK_WAVE8, 1, (int)cols, pl.nw, (size_t)rows * sizeof(int)};
     }
-    if (radix && rsel_route(cols, dtype)) return TopkRoute{TK_RSEL, 1, (int)cols, 0, 0};
+    if (radix && rsel_route(cols, k, dtype)) return TopkRoute{TK_RSEL, 1, (int)cols, 0, 0};
     if (const int ns = radix ? rsel_segments(rows, cols, k, dtype) : 0) {
         const int seg_len = (int)((cols + ns - 1) / ns + 3) & ~3;  // segment starts stay 16-byte aligned
         return TopkRoute{TK_RSEL_SEG, ns, seg_len, 0, radix_ws(rows, cols, k, dtype)};
